@@ -1,0 +1,270 @@
+"""ctypes bindings of the CPU twin (oracle/libtwin.so): the checker of every parity test.
+
+Test infrastructure only: the product package (perseus_amd) never imports this module.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(ROOT, "oracle", "libtwin.so")
+
+u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (or make -C oracle)")
+    lib = C.CDLL(LIB_PATH)
+    sig = {
+        "or_is_prime": (C.c_int, [C.c_uint64]),
+        "or_first_prime": (C.c_uint64, [C.c_uint32, C.c_uint64]),
+        "or_last_prime": (C.c_uint64, [C.c_uint32, C.c_uint64]),
+        "or_previous_prime": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "or_root_of_unity": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "or_invmod": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "or_powmod": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
+        "or_descending_primes": (C.c_int, [C.c_uint32, C.c_uint64, C.c_int, u64p]),
+        "or_prime_const": (None, [C.c_uint64, C.c_uint32, C.c_void_p]),
+        "or_chacha_block": (None, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, u32p]),
+        "or_kska_expand_row": (None, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, u32p]),
+        "or_kska_expand": (C.c_uint32, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
+        "or_kskb_expand_row": (None, [u32p, C.c_uint32, C.c_uint64, C.c_uint32, u64p]),
+        "or_prng_new": (C.c_void_p, [u32p, C.c_uint32]),
+        "or_prng_free": (None, [C.c_void_p]),
+        "or_prng_next_u32": (C.c_uint32, [C.c_void_p]),
+        "or_prng_next_u64": (C.c_uint64, [C.c_void_p]),
+        "or_prng_uniform_below": (C.c_uint64, [C.c_void_p, C.c_uint64]),
+        "or_prng_uniform_f64": (C.c_double, [C.c_void_p]),
+        "or_prng_ksk_seed": (None, [C.c_void_p, u32p]),
+        "or_sample_sparse_ternary": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, i8p]),
+        "or_sample_gaussian": (None, [C.c_void_p, C.c_double, C.c_uint32, i64p]),
+        "or_automorph_slot": (C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32]),
+        "or_rotation_galois": (C.c_uint64, [C.c_int64, C.c_uint32]),
+        "or_galois_inverse": (C.c_uint64, [C.c_uint64, C.c_uint32]),
+        "or_ctx_new": (C.c_void_p, [C.c_uint32, u64p, C.c_int, C.c_int, C.c_int]),
+        "or_ctx_free": (None, [C.c_void_p]),
+        "or_set_threads": (None, [C.c_int]),
+        "or_get_threads": (C.c_int, []),
+        "or_ctx_twiddles": (None, [C.c_void_p, C.c_int, u32p, u32p, u32p, u32p]),
+        "or_ctx_root": (C.c_uint64, [C.c_void_p, C.c_int]),
+        "or_ntt_fwd_rows": (None, [C.c_void_p, u32p, i32p, C.c_int]),
+        "or_ntt_inv_rows": (None, [C.c_void_p, u32p, i32p, C.c_int]),
+        "or_bconv": (None, [C.c_void_p, C.c_void_p, i32p, C.c_int, C.c_void_p, i32p, C.c_int, C.c_int]),
+        "or_live_digits": (C.c_int, [C.c_void_p, C.c_int]),
+        "or_digit_of": (C.c_int, [C.c_void_p, C.c_int]),
+        "or_modup": (None, [C.c_void_p, u32p, C.c_int, u32p]),
+        "or_ks_dot": (None, [C.c_void_p, u32p, u32p, C.c_int, u32p, u32p, C.c_uint32, u32p]),
+        "or_moddown": (None, [C.c_void_p, u32p, C.c_int, u32p]),
+        "or_rotate": (None, [C.c_void_p, u32p, C.c_int, u32p, u32p, C.c_uint64, u32p]),
+        "or_rotate_hoisted": (None, [C.c_void_p, u32p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p]),
+        "or_ksk_gen": (None, [C.c_void_p, u32p, u32p, u32p, u32p, u32p]),
+        "or_rotation_key": (None, [C.c_void_p, C.c_void_p, u32p, C.c_uint64, u32p, u32p]),
+        "or_secret_eval": (None, [C.c_void_p, i8p, u32p]),
+        "or_automorph_rows": (None, [C.c_void_p, u32p, C.c_uint32, C.c_int, u32p]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+LIB = _load()
+
+
+def ptr_array(arrs):
+    """A C array of pointers to the numpy arrays `arrs` (kept alive by the caller)."""
+    return (C.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+
+
+def set_threads(n):
+    LIB.or_set_threads(int(n))
+
+
+def descending_primes(bits, m, n):
+    out = np.zeros(n, np.uint64)
+    if LIB.or_descending_primes(bits, m, n, out) != 0:
+        raise ValueError("not enough primes")
+    return [int(x) for x in out]
+
+
+class Prng:
+    """The sampler DRBG (ChaCha20, stream id, "DRBG" tag)."""
+
+    def __init__(self, key, stream=0):
+        self.h = LIB.or_prng_new(np.asarray(key, np.uint32), stream)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.or_prng_free(self.h)
+
+    def u32(self):
+        return LIB.or_prng_next_u32(self.h)
+
+    def u64(self):
+        return LIB.or_prng_next_u64(self.h)
+
+    def below(self, q):
+        return LIB.or_prng_uniform_below(self.h, q)
+
+    def f64(self):
+        return LIB.or_prng_uniform_f64(self.h)
+
+    def ksk_seed(self):
+        s = np.zeros(8, np.uint32)
+        LIB.or_prng_ksk_seed(self.h, s)
+        return s
+
+    def sparse_ternary(self, n, h):
+        out = np.zeros(n, np.int8)
+        if LIB.or_sample_sparse_ternary(self.h, n, h, out) != 0:
+            raise ValueError("h > n")
+        return out
+
+    def gaussian(self, n, sigma=3.19):
+        out = np.zeros(n, np.int64)
+        LIB.or_sample_gaussian(self.h, sigma, n, out)
+        return out
+
+
+class Ctx:
+    """A chain of nq Q primes then kp special primes at N = 2^logn with dnum hybrid digits."""
+
+    def __init__(self, logn, q, p, dnum):
+        self.logn, self.n = logn, 1 << logn
+        self.q, self.p = list(q), list(p)
+        self.nq, self.kp, self.dnum = len(q), len(p), dnum
+        self.primes = self.q + self.p
+        self.rows = self.nq + self.kp
+        arr = np.array(self.primes, np.uint64)
+        self.h = LIB.or_ctx_new(logn, arr, self.nq, self.kp, dnum)
+        if not self.h:
+            raise ValueError("invalid chain")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.or_ctx_free(self.h)
+
+    def twiddles(self, pid):
+        n = self.n
+        t = [np.zeros(n, np.uint32) for _ in range(4)]
+        LIB.or_ctx_twiddles(self.h, pid, *t)
+        return t
+
+    def root(self, pid):
+        return LIB.or_ctx_root(self.h, pid)
+
+    def ntt_fwd(self, rows, ids):
+        rows = np.ascontiguousarray(rows, np.uint32)
+        LIB.or_ntt_fwd_rows(self.h, rows, np.asarray(ids, np.int32), len(ids))
+        return rows
+
+    def ntt_inv(self, rows, ids):
+        rows = np.ascontiguousarray(rows, np.uint32)
+        LIB.or_ntt_inv_rows(self.h, rows, np.asarray(ids, np.int32), len(ids))
+        return rows
+
+    def bconv(self, src_rows, src_ids, tgt_ids, prescaled=False):
+        src = [np.ascontiguousarray(r, np.uint32) for r in src_rows]
+        dst = [np.zeros(self.n, np.uint32) for _ in tgt_ids]
+        LIB.or_bconv(self.h, ptr_array(src), np.asarray(src_ids, np.int32), len(src), ptr_array(dst),
+                     np.asarray(tgt_ids, np.int32), len(dst), int(prescaled))
+        return dst
+
+    def live_digits(self, top):
+        return LIB.or_live_digits(self.h, top)
+
+    def digit_of(self, pid):
+        return LIB.or_digit_of(self.h, pid)
+
+    def ct_zeros(self):
+        return np.zeros((2, self.rows, self.n), np.uint32)
+
+    def modup(self, c1, top):
+        digits = np.zeros((self.dnum, self.rows, self.n), np.uint32)
+        LIB.or_modup(self.h, np.ascontiguousarray(c1, np.uint32), top, digits)
+        return digits
+
+    def ks_dot(self, ct, digits, top, seed, b, autok):
+        ext = self.ct_zeros()
+        LIB.or_ks_dot(self.h, np.ascontiguousarray(ct, np.uint32), np.ascontiguousarray(digits, np.uint32), top,
+                      np.asarray(seed, np.uint32), np.ascontiguousarray(b, np.uint32), autok, ext)
+        return ext
+
+    def moddown(self, ext, top):
+        out = self.ct_zeros()
+        LIB.or_moddown(self.h, np.ascontiguousarray(ext, np.uint32), top, out)
+        return out
+
+    def rotate(self, ct, top, seed, b, g):
+        out = self.ct_zeros()
+        LIB.or_rotate(self.h, np.ascontiguousarray(ct, np.uint32), top, np.asarray(seed, np.uint32),
+                      np.ascontiguousarray(b, np.uint32), g, out)
+        return out
+
+    def rotate_hoisted(self, ct, top, seeds, bs, gs):
+        outs = [self.ct_zeros() for _ in gs]
+        bs = [np.ascontiguousarray(b, np.uint32) for b in bs]
+        LIB.or_rotate_hoisted(self.h, np.ascontiguousarray(ct, np.uint32), top, len(gs),
+                              np.ascontiguousarray(seeds, np.uint32).reshape(-1), ptr_array(bs),
+                              np.asarray(gs, np.uint64), ptr_array(outs))
+        return outs
+
+    def ksk_gen(self, s_new, s_old, seed, e):
+        b = np.zeros((self.dnum, self.rows, self.n), np.uint32)
+        LIB.or_ksk_gen(self.h, np.ascontiguousarray(s_new, np.uint32), np.ascontiguousarray(s_old, np.uint32),
+                       np.asarray(seed, np.uint32), np.ascontiguousarray(e, np.uint32), b)
+        return b
+
+    def rotation_key(self, prng, s_eval, g):
+        seed = np.zeros(8, np.uint32)
+        b = np.zeros((self.dnum, self.rows, self.n), np.uint32)
+        LIB.or_rotation_key(self.h, prng.h, np.ascontiguousarray(s_eval, np.uint32), g, seed, b)
+        return seed, b
+
+    def secret_eval(self, s):
+        out = np.zeros((self.rows, self.n), np.uint32)
+        LIB.or_secret_eval(self.h, np.ascontiguousarray(s, np.int8), out)
+        return out
+
+    def automorph_rows(self, rows, k):
+        rows = np.ascontiguousarray(rows, np.uint32)
+        out = np.zeros_like(rows)
+        LIB.or_automorph_rows(self.h, rows, k, rows.shape[0], out)
+        return out
+
+
+def kska_row(seed, digit, p, n):
+    out = np.zeros(n, np.uint32)
+    LIB.or_kska_expand_row(np.asarray(seed, np.uint32), digit, p, n, out)
+    return out
+
+
+def kskb_row(seed, digit, p, n):
+    out = np.zeros(n, np.uint64)
+    LIB.or_kskb_expand_row(np.asarray(seed, np.uint32), digit, p, n, out)
+    return out
+
+
+def chacha_block(key, w12, w13, w14, w15, rounds):
+    out = np.zeros(16, np.uint32)
+    LIB.or_chacha_block(np.asarray(key, np.uint32), w12, w13, w14, w15, rounds, out)
+    return out
+
+
+def automorph_slot(k, slot, logn):
+    return LIB.or_automorph_slot(k, slot, logn)
+
+
+def rotation_galois(r, n):
+    return LIB.or_rotation_galois(r, n)
+
+
+def galois_inverse(g, n):
+    return LIB.or_galois_inverse(g, n)

@@ -1,0 +1,447 @@
+/* pc-hip: the MI355X (gfx950) kernels of the CKKS key-switch / NTT path behind the reference's kernel ABI.
+ *
+ * Three layers, all plain C ABI (no HIP or torch types in a signature; a stream is a hipStream_t passed as void*):
+ *
+ *  1. The kernel table. Byte-identical mirrors of the reference's ABI-30 launch-argument structs
+ *     (crates/pc-kernels/kernels/args.cuh) and its KernelTable of 52 launchers
+ *     (args.cuh:1037-1097). pc_table_u32_barrett64() replaces the CUDA build's export of the same name
+ *     (crates/pc-kernels/kernels/inst/instantiate.inc:32-91, looked up by crates/pc-kernels/src/table.rs:101-112).
+ *     Every launcher reads *args, enqueues on the stream and returns 0, -1/-2/-3 for an argument outside the
+ *     kernel's range (args.cuh:1036; crates/pc-cuda/src/error.rs:47-54) or a positive HIP error code. Launchers never
+ *     allocate, free or synchronise, so they may be captured into a HIP graph.
+ *  2. The runtime FFI (pc_hip_*), the HIP replacement of crates/pc-cuda's cudart bindings (ffi.rs:18-50, mem.rs:19-24):
+ *     device, memory, streams, events, graphs.
+ *  3. The key-switching driver (pcx_*), the launch sequences of crates/pc-gpu (ks.rs, rotate.rs, ntt.rs, keygen.rs)
+ *     restated in C++ over the table: a context of one chain, setup-time plans per limb top, key groups, rotations.
+ */
+#ifndef PC_HIP_H
+#define PC_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#define PC_STATIC_ASSERT(c, m) static_assert(c, m)
+#else
+#define PC_STATIC_ASSERT(c, m) _Static_assert(c, m)
+#endif
+
+#define PC_KERNELS_ABI 30u
+
+typedef void* pc_stream_t; /* a hipStream_t */
+
+/* ------------------------------------------------------------------------------------------ ABI-30 structs */
+/* args.cuh:38-49 */
+typedef struct PrimeConst {
+    uint64_t p;
+    uint64_t mu_lo;
+    uint64_t mu_hi;
+    uint64_t neal_mu;
+    uint32_t bits;
+    uint32_t word_bits;
+    uint64_t mont_pinv;
+    uint64_t mont_r2;
+    uint64_t split;
+} PrimeConst;
+PC_STATIC_ASSERT(sizeof(PrimeConst) == 64, "PrimeConst layout");
+
+/* args.cuh:54-57 */
+typedef struct RowSet {
+    int32_t nq, np, qmax, pad;
+} RowSet;
+PC_STATIC_ASSERT(sizeof(RowSet) == 16, "RowSet layout");
+
+/* args.cuh:60-64 */
+typedef struct PolyRef {
+    void* base;
+    uint64_t ct_stride, part_stride;
+} PolyRef;
+PC_STATIC_ASSERT(sizeof(PolyRef) == 24, "PolyRef layout");
+
+/* args.cuh:66-107: in-place negacyclic NTT of nrows rows (row i at base + roff[i]*N, prime id rprime[i]), OpenFHE
+ * order; soff: out-of-place first pass summing snum source rows; epi 1/2/3: forward epilogues; es/ess: the inverse's
+ * per-row scale */
+typedef struct NttArgs {
+    void* base;
+    const uint32_t* roff;
+    const int32_t* rprime;
+    const void* fw;
+    const void* fws;
+    const void* iw;
+    const void* iws;
+    const void* ninv;
+    const void* ninvs;
+    const PrimeConst* pr;
+    int32_t nrows, chunk;
+    const void* src;
+    const uint32_t* soff;
+    void* eout;
+    const void* ex;
+    const void* es;
+    const void* ess;
+    int32_t epi, snum;
+    uint64_t sstride;
+    int32_t xnum, lazy;
+    uint64_t xstride;
+    const void* ed;
+} NttArgs;
+PC_STATIC_ASSERT(sizeof(NttArgs) == 176, "NttArgs layout");
+
+/* args.cuh:120-141: one fast base-conversion job; pool at pool_off: src_row[ns], src_prime[ns], pre[ns],
+ * tgt_row[nt], tgt_prime[nt], M[ns][nt] (u32 words) */
+typedef struct BconvJob {
+    uint32_t src_off, dst_off;
+    uint32_t nsrc, ntgt;
+    uint32_t pool_off;
+    uint32_t exact;
+    uint32_t prescaled;
+    uint32_t split;
+} BconvJob;
+PC_STATIC_ASSERT(sizeof(BconvJob) == 32, "BconvJob layout");
+
+typedef struct BconvArgs {
+    const void* src;
+    void* dst;
+    const BconvJob* jobs;
+    const void* pool;
+    const PrimeConst* pr;
+    int32_t njobs, max_tgt;
+    int32_t kind, pad;
+} BconvArgs;
+PC_STATIC_ASSERT(sizeof(BconvArgs) == 56, "BconvArgs layout");
+
+/* args.cuh:149-160: element-wise row-set kernels */
+typedef struct EwArgs {
+    PolyRef out, a, b;
+    RowSet rs;
+    const void* sc;
+    const void* scs;
+    const PrimeConst* pr;
+    int32_t K, nparts, sub, zero_p;
+} EwArgs;
+PC_STATIC_ASSERT(sizeof(EwArgs) == 128, "EwArgs layout");
+
+/* args.cuh:203-228: hybrid key-switch inner product */
+#define PC_KS_ACC 4
+#define PC_KS_SUM 8
+typedef struct KsArgs {
+    const void* c1;
+    const void* modup;
+    const void* c0;
+    void* out0;
+    void* out1;
+    const void* const* kb;
+    const void* const* ka;
+    const uint32_t* autok;
+    const uint32_t* rows;
+    const int32_t* digit_of;
+    const void* pmod;
+    const void* pmods;
+    const PrimeConst* pr;
+    uint64_t ct_stride, mu_ct_stride, mu_digit_stride, out_ct_stride, out_rot_stride, key_digit_stride;
+    int32_t K, R, ndig, c0_mode, nq, nrows;
+} KsArgs;
+PC_STATIC_ASSERT(sizeof(KsArgs) == 176, "KsArgs layout");
+
+/* args.cuh:267-281 */
+typedef struct EpiArgs {
+    void* dst;
+    const void* conv;
+    const void* binv;
+    const void* binvs;
+    const void* k;
+    uint64_t part_stride;
+    int32_t dbl, pad;
+    const void* alpha;
+    const void* alphas;
+} EpiArgs;
+PC_STATIC_ASSERT(sizeof(EpiArgs) == 72, "EpiArgs layout");
+
+/* args.cuh:284-294: switching keys read in their stored form, `a` regenerated from each key's KSKA seed */
+typedef struct KeyTab {
+    const void* const* kb;
+    const uint32_t* const* seed;
+    uint64_t row_words;
+    int32_t bits;
+    int32_t q_top;
+    int32_t srows;
+    int32_t nregen;
+} KeyTab;
+PC_STATIC_ASSERT(sizeof(KeyTab) == 40, "KeyTab layout");
+
+/* args.cuh:299-307 */
+typedef struct KsRegenArgs {
+    KsArgs ks;
+    const uint32_t* seed;
+    EpiArgs epi;
+    int32_t use_epi, pad;
+    KeyTab key;
+    const void* add;
+} KsRegenArgs;
+PC_STATIC_ASSERT(sizeof(KsRegenArgs) == 312, "KsRegenArgs layout");
+
+/* args.cuh:317-325: KSKA rows out[d - d0][m][N] */
+typedef struct KskExpandArgs {
+    void* out;
+    const uint32_t* seed;
+    const int32_t* prime_ids;
+    const PrimeConst* pr;
+    int32_t nmod, dnum;
+    int32_t d0, pad;
+} KskExpandArgs;
+PC_STATIC_ASSERT(sizeof(KskExpandArgs) == 48, "KskExpandArgs layout");
+
+/* args.cuh:754-768: sigma_k gather in the bit-reversed evaluation order */
+typedef struct AutomorphArgs {
+    PolyRef out, in, add;
+    RowSet rs;
+    const PrimeConst* pr;
+    uint32_t k;
+    int32_t K, nparts, has_add;
+} AutomorphArgs;
+PC_STATIC_ASSERT(sizeof(AutomorphArgs) == 112, "AutomorphArgs layout");
+
+/* args.cuh:790-807: secret-key encryption, a from the "ENCA" expander lane */
+typedef struct EncryptArgs {
+    void* c0;
+    void* c1;
+    const void* s;
+    const void* e;
+    const void* m;
+    const uint32_t* seed;
+    const PrimeConst* pr;
+    uint32_t nonce;
+    int32_t nl;
+} EncryptArgs;
+PC_STATIC_ASSERT(sizeof(EncryptArgs) == 64, "EncryptArgs layout");
+
+/* args.cuh:817-833: one hybrid switching key (OpenFHE KeySwitchGenInternal relation), dense or bit-packed b */
+typedef struct KskGenArgs {
+    void* b;
+    void* a;
+    const void* e;
+    const void* s_new;
+    const void* s_old;
+    const uint32_t* seed;
+    const int32_t* ids;
+    const int32_t* digit_of;
+    const void* pmod;
+    const void* pmods;
+    const PrimeConst* pr;
+    uint64_t row_words;
+    int32_t nrows, ndig, nq, bits, sq, pad;
+} KskGenArgs;
+PC_STATIC_ASSERT(sizeof(KskGenArgs) == 120, "KskGenArgs layout");
+
+/* args.cuh:836-842 */
+typedef struct KskUnpackArgs {
+    void* out;
+    const uint32_t* in;
+    uint64_t row_words;
+    int32_t nrows, bits;
+} KskUnpackArgs;
+PC_STATIC_ASSERT(sizeof(KskUnpackArgs) == 32, "KskUnpackArgs layout");
+
+/* args.cuh:997-1003 */
+typedef struct KsKeyArgs {
+    KsArgs ks;
+    KeyTab key;
+} KsKeyArgs;
+PC_STATIC_ASSERT(sizeof(KsKeyArgs) == 216, "KsKeyArgs layout");
+
+/* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
+struct PtDotArgs;
+struct CtsArgs;
+struct TensorArgs;
+struct MdEpiArgs;
+struct WsumArgs;
+struct AddConstArgs;
+struct MulTableArgs;
+struct RescaleArgs;
+struct RescaleCombineArgs;
+struct EncodeArgs;
+struct ModRaiseArgs;
+struct SmallIntArgs;
+struct SpruExtractArgs;
+struct SpruFftArgs;
+struct SpruScatterArgs;
+struct CtsRegenArgs;
+struct PcmmArgs;
+struct CcmmArgs;
+struct WsumKArgs;
+struct RescaleCombineToArgs;
+struct MdEpiToArgs;
+struct SmallInt1Args;
+struct CoeffArgs;
+struct MulAddArgs;
+struct RescaleNttArgs;
+struct MulAddNArgs;
+struct TensorYArgs;
+struct WsumMultiArgs;
+struct TfheArgs;
+struct TensorSumArgs;
+struct TensorMultiArgs;
+struct TensorSeededArgs;
+struct EwManyArgs;
+struct SubMulManyArgs;
+struct PackSplitArgs;
+struct PackDotArgs;
+
+/* args.cuh:1037-1097 */
+typedef struct KernelTable {
+    uint32_t abi;
+    uint32_t word_bytes;
+    uint32_t mm;
+    uint32_t log_n;
+    int (*ntt_fwd)(const NttArgs*, pc_stream_t);
+    int (*ntt_inv)(const NttArgs*, pc_stream_t);
+    int (*bconv)(const BconvArgs*, pc_stream_t);
+    int (*ew_add)(const EwArgs*, pc_stream_t);
+    int (*ew_scale)(const EwArgs*, pc_stream_t);
+    int (*ew_sub_mul)(const EwArgs*, pc_stream_t);
+    int (*ew_copy)(const EwArgs*, pc_stream_t);
+    int (*pt_dot)(const struct PtDotArgs*, pc_stream_t);
+    int (*ks_dot)(const KsArgs*, pc_stream_t);
+    int (*ks_dot_regen)(const KsRegenArgs*, pc_stream_t);
+    int (*ksk_expand)(const KskExpandArgs*, pc_stream_t);
+    int (*cts_fused)(const struct CtsArgs*, pc_stream_t);
+    int (*tensor)(const struct TensorArgs*, pc_stream_t);
+    int (*md_epilogue)(const struct MdEpiArgs*, pc_stream_t);
+    int (*wsum)(const struct WsumArgs*, pc_stream_t);
+    int (*add_const)(const struct AddConstArgs*, pc_stream_t);
+    int (*mul_table)(const struct MulTableArgs*, pc_stream_t);
+    int (*rescale_coef)(const struct RescaleArgs*, pc_stream_t);
+    int (*rescale_combine)(const struct RescaleCombineArgs*, pc_stream_t);
+    int (*automorph)(const AutomorphArgs*, pc_stream_t);
+    int (*encode)(const struct EncodeArgs*, pc_stream_t);
+    int (*encrypt)(const EncryptArgs*, pc_stream_t);
+    int (*ksk_gen)(const KskGenArgs*, pc_stream_t);
+    int (*ksk_unpack)(const KskUnpackArgs*, pc_stream_t);
+    int (*mod_raise)(const struct ModRaiseArgs*, pc_stream_t);
+    int (*small_int)(const struct SmallIntArgs*, pc_stream_t);
+    int (*spru_extract)(const struct SpruExtractArgs*, pc_stream_t);
+    int (*spru_fft_pass)(const struct SpruFftArgs*, pc_stream_t);
+    int (*spru_scatter)(const struct SpruScatterArgs*, pc_stream_t);
+    int (*cts_fused_regen)(const struct CtsRegenArgs*, pc_stream_t);
+    int (*ks_dot_key)(const KsKeyArgs*, pc_stream_t);
+    int (*pcmm)(const struct PcmmArgs*, pc_stream_t);
+    int (*ccmm)(const struct CcmmArgs*, pc_stream_t);
+    int (*wsum_k)(const struct WsumKArgs*, pc_stream_t);
+    int (*rescale_combine_to)(const struct RescaleCombineToArgs*, pc_stream_t);
+    int (*md_epilogue_to)(const struct MdEpiToArgs*, pc_stream_t);
+    int (*small_int1)(const struct SmallInt1Args*, pc_stream_t);
+    int (*coeff_sum)(const struct CoeffArgs*, pc_stream_t);
+    int (*mul_add)(const struct MulAddArgs*, pc_stream_t);
+    int (*rescale_fwd)(const struct RescaleNttArgs*, pc_stream_t);
+    int (*mul_add_n)(const struct MulAddNArgs*, pc_stream_t);
+    int (*tensor_y)(const struct TensorYArgs*, pc_stream_t);
+    int (*wsum_multi)(const struct WsumMultiArgs*, pc_stream_t);
+    int (*bconv_wide)(const BconvArgs*, pc_stream_t);
+    int (*tfhe)(const struct TfheArgs*, pc_stream_t);
+    int (*tensor_sum)(const struct TensorSumArgs*, pc_stream_t);
+    int (*tensor_multi)(const struct TensorMultiArgs*, pc_stream_t);
+    int (*tensor_seeded)(const struct TensorSeededArgs*, pc_stream_t);
+    int (*ew_many)(const struct EwManyArgs*, pc_stream_t);
+    int (*submul_many)(const struct SubMulManyArgs*, pc_stream_t);
+    int (*pack_split)(const struct PackSplitArgs*, pc_stream_t);
+    int (*pack_dot)(const struct PackDotArgs*, pc_stream_t);
+} KernelTable;
+PC_STATIC_ASSERT(sizeof(KernelTable) == 16 + 52 * 8, "KernelTable layout");
+
+/* The u32 x Barrett64 table at N = 2^16 (instantiate.inc:32-91; header {abi 30, word_bytes 4, mm 0, log_n 16}). */
+const KernelTable* pc_table_u32_barrett64(void);
+/* The same kernels at N = 2^log_n, log_n in [10, 17] (the header's log_n field says which). No counterpart in the
+ * reference, whose table is fixed at 2^16 (args.cuh:14-18): it exists for ring degrees such as 2^14. NULL outside
+ * the range. */
+const KernelTable* pc_table_u32_logn(uint32_t log_n);
+
+/* ------------------------------------------------------------------------------------------ runtime FFI */
+/* crates/pc-cuda/src/ffi.rs:18-50 and mem.rs:19-24: each returns 0 or a positive HIP error code */
+int pc_hip_device_count(int* n);
+int pc_hip_set_device(int dev);
+int pc_hip_device_name(int dev, char* out, int len);
+int pc_hip_malloc(void** p, size_t bytes);
+int pc_hip_free(void* p);
+int pc_hip_malloc_host(void** p, size_t bytes);
+int pc_hip_free_host(void* p);
+int pc_hip_memcpy_htod(void* dst, const void* src, size_t bytes, pc_stream_t s);
+int pc_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes, pc_stream_t s);
+int pc_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, pc_stream_t s);
+int pc_hip_memset(void* dst, int value, size_t bytes, pc_stream_t s);
+int pc_hip_stream_create(pc_stream_t* s);
+int pc_hip_stream_destroy(pc_stream_t s);
+int pc_hip_stream_sync(pc_stream_t s);
+int pc_hip_stream_wait_event(pc_stream_t s, void* ev);
+int pc_hip_device_sync(void);
+int pc_hip_event_create(void** ev);
+int pc_hip_event_destroy(void* ev);
+int pc_hip_event_record(void* ev, pc_stream_t s);
+int pc_hip_event_sync(void* ev);
+int pc_hip_event_elapsed_ms(float* ms, void* start, void* stop);
+int pc_hip_graph_begin_capture(pc_stream_t s);
+int pc_hip_graph_end_capture(pc_stream_t s, void** graph);
+int pc_hip_graph_instantiate(void** exec, void* graph);
+int pc_hip_graph_launch(void* exec, pc_stream_t s);
+int pc_hip_graph_destroy(void* graph);
+int pc_hip_graph_exec_destroy(void* exec);
+const char* pc_hip_error_string(int code);
+/* the last launch error of the calling thread (hipGetLastError), 0 if none */
+int pc_hip_last_error(void);
+
+/* ------------------------------------------------------------------------------------------ driver (pc-gpu) */
+/* A context: one chain (nq Q primes then kp special primes, all < 2^31 and = 1 mod 2N), N = 2^log_n, dnum hybrid
+ * digits of ceil(nq / dnum) limbs (crates/pc-core/src/params.rs:500-510), and device tables: prime constants, twiddles
+ * (crates/pc-gpu/src/context.rs:169-261), key-switching plans of every limb top (crates/pc-gpu/src/ks.rs:521-828) and
+ * a workspace for up to k_rot extended ciphertexts per hoisted chunk. Errors: NULL, with *err set. */
+typedef struct pcx_ctx pcx_ctx;
+pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int* err);
+void pcx_ctx_free(pcx_ctx* c);
+const KernelTable* pcx_ctx_table(const pcx_ctx* c);
+const PrimeConst* pcx_ctx_primes(const pcx_ctx* c); /* device table by prime id */
+/* device twiddle tables [prime id][N]: fw, fws, iw, iws, then ninv, ninvs [prime id] */
+const void* pcx_ctx_twiddle(const pcx_ctx* c, int which);
+uint64_t pcx_ctx_root(const pcx_ctx* c, int prime_id);
+size_t pcx_ctx_workspace_bytes(const pcx_ctx* c);
+
+/* Batched NTT of nrows rows of one buffer: row i at base + roff[i]*N (prime id ids[i]); host row tables are uploaded
+ * into a device row list made once (crates/pc-gpu/src/ntt.rs:293-326 transform_rows over a RowList). dir: 1 forward,
+ * -1 inverse (scaled by N^-1). */
+typedef struct pcx_rows pcx_rows;
+pcx_rows* pcx_rows_new(pcx_ctx* c, const uint32_t* roff, const int32_t* ids, int nrows);
+void pcx_rows_free(pcx_rows* r);
+int pcx_ntt(pcx_ctx* c, int dir, void* base, const pcx_rows* rows, pc_stream_t s);
+
+/* A key group: R rotation keys (galois elements g_r), each a 256-bit KSKA seed of `a` plus its stored `b`
+ * [dnum][nq + kp][N] (full layout: slot = prime id), dense (bits = 0) or bit-packed at `bits` per value
+ * (crates/pc-gpu/src/keys.rs:24-70). The host b arrays are uploaded (and packed) once. */
+typedef struct pcx_keys pcx_keys;
+pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
+                       const uint32_t* const* b_host, int bits, int* err);
+/* Keys generated on the device (crates/pc-gpu/src/keygen.rs:172-262): secret s (ternary coefficients), per key the
+ * seed of a and the Gaussian errors e[dnum][N] (signed coefficients, the same error on every limb of a digit). */
+pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret,
+                            const uint32_t* seeds, const int64_t* errors, int bits, int* err);
+void pcx_keys_free(pcx_keys* k);
+/* download key r's stored b as dense [dnum][nq + kp][N] words */
+int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host);
+
+/* Ciphertexts are device buffers in the context layout [part][row = prime id over Q u P][N] words (2 (nq+kp) N words;
+ * crates/pc-gpu/src/poly.rs:1-53), Q rows 0..top live. */
+size_t pcx_ct_words(const pcx_ctx* c);
+/* out = rot(ct) by key r of the group (g = 1: a copy): ModUp, key dot, ModDown (crates/pc-gpu/src/rotate.rs:179-204) */
+int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* out, pc_stream_t s);
+/* hoisted rotations (crates/pc-gpu/src/rotate.rs:456-507): one ModUp, then the keys idx[0..n) in chunks of at most
+ * k_rot, output j at out + j * ct_words (words) */
+int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
+                       pc_stream_t s);
+/* the stages alone, for tests and profiles: ModUp of ct's c1 into the context's digit workspace; the dot of key r
+ * into ext (one extended ciphertext); ModDown of ext into out */
+int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);
+const void* pcx_modup_digits(const pcx_ctx* c); /* [dnum][nq + kp][N] */
+int pcx_dot(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ext, pc_stream_t s);
+int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

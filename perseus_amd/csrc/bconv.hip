@@ -1,0 +1,173 @@
+// Batched fast base conversion (crates/pc-kernels/kernels/args.cuh:109-141; host twin crates/pc-host/src/bconv.rs):
+//   y_i = x_i pre_i mod s_i (prescaled jobs: y_i = x_i as stored), out_t = sum_i y_i M[i][t] mod t;
+//   exact jobs: v = sum_i y_i rb_i (double FMA in source order), u = floor(v + 0.5) (centred: the lift's mean),
+//   out_t -= u (B mod t).
+// One launch for every job of a plan: grid (N / 1024, njobs), 256 threads of 4 consecutive coefficients.
+//
+// 31-bit primes break the reference's lazy bound nsrc (p - 1)^2 < 2^64 past 4 sources, so the sum of products is
+// carried in 96 bits (a 64-bit sum and a count of its wraps) and reduced once: the exact integer formula, whatever
+// the width of the primes.
+#include "common.h"
+
+namespace pch {
+namespace bconv {
+
+constexpr int BX = 256, V = 4, PER_WG = BX * V;
+constexpr int MAX_REG_SRC = 16;
+
+struct Pool {
+    const uint32_t* w;
+    int ns, nt;
+    __device__ uint32_t src_row(int i) const { return w[i]; }
+    __device__ uint32_t src_prime(int i) const { return w[ns + i]; }
+    __device__ uint32_t pre(int i) const { return w[2 * ns + i]; }
+    __device__ uint32_t tgt_row(int t) const { return w[3 * ns + t]; }
+    __device__ uint32_t tgt_prime(int t) const { return w[3 * ns + nt + t]; }
+    __device__ uint32_t m(int i, int t) const { return w[3 * ns + 2 * nt + i * nt + t]; }
+};
+
+// the exact jobs' tables after M (build_tables, crates/pc-gpu/src/bconv.rs:94-121): rb[ns] doubles at the first
+// 8-byte aligned word, then bmod[nt]
+__device__ __forceinline__ const double* exact_rb(const uint32_t* pool_base, const BconvJob& j) {
+    size_t w = (size_t)j.pool_off + 3 * j.nsrc + 2 * j.ntgt + (size_t)j.nsrc * j.ntgt;
+    if (w & 1) ++w;  // the pool is 8-byte aligned: word parity is byte alignment
+    return (const double*)(pool_base + w);
+}
+
+__device__ __forceinline__ uint64_t exact_u(const BconvJob& j, const double* rb, const uint32_t* y, int stride,
+                                            uint32_t coef) {
+    if (j.exact == 2) {
+        // the mean-centred job (crates/pc-host/src/bconv.rs:70-76): ns / 2, odd ns rounded by a hash of the index
+        const uint64_t ns = j.nsrc;
+        return (ns >> 1) + ((ns & 1) & ((coef * 0x9E3779B1u) >> 31));
+    }
+    double v = 0.0;
+    for (uint32_t i = 0; i < j.nsrc; ++i) v = __fma_rn((double)y[i * stride], rb[i], v);
+    return (uint64_t)floor(v + 0.5);
+}
+
+// One workgroup = one job x 1024 coefficients (4 per thread). A job's record lives in device memory, so the source
+// count is read here: jobs of at most 16 sources keep the y of their 4 coefficients in registers, wider jobs
+// (bconv_wide, up to 48 at u32 words) re-read their sources per target (L1/L2 resident).
+__device__ __forceinline__ void job_reg(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
+                                        uint32_t* dst, uint32_t c0, int logn) {
+    uint32_t y[MAX_REG_SRC * V];
+    for (int i = 0; i < P.ns; ++i) {
+        const uint4 x = *(const uint4*)(src + ((size_t)P.src_row(i) << logn) + c0);
+        uint32_t v[V] = {x.x, x.y, x.z, x.w};
+        if (!j.prescaled) {
+            const Red red(A.pr[P.src_prime(i)]);
+            const uint32_t pre = P.pre(i);
+#pragma unroll
+            for (int k = 0; k < V; ++k) v[k] = red.mul(v[k], pre);
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
+    }
+    uint64_t u[V] = {0, 0, 0, 0};
+    const uint32_t* bmod = nullptr;
+    if (j.exact) {
+        const double* rb = exact_rb((const uint32_t*)A.pool, j);
+        bmod = (const uint32_t*)(rb + j.nsrc);
+#pragma unroll
+        for (int k = 0; k < V; ++k) u[k] = exact_u(j, rb, y + k, V, c0 + k);
+    }
+    for (int t = 0; t < P.nt; ++t) {
+        const Red red(A.pr[P.tgt_prime(t)]);
+        uint64_t acc[V] = {0, 0, 0, 0};
+        uint32_t wraps[V] = {0, 0, 0, 0};
+        for (int i = 0; i < P.ns; ++i) {
+            const uint32_t m = P.m(i, t);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const uint64_t pr = (uint64_t)y[i * V + k] * m;
+                acc[k] += pr;
+                wraps[k] += acc[k] < pr;
+            }
+        }
+        uint32_t r[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            r[k] = red.red96(acc[k], wraps[k]);
+            if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * bmod[t]), red.p);
+        }
+        *(uint4*)(dst + ((size_t)P.tgt_row(t) << logn) + c0) = make_uint4(r[0], r[1], r[2], r[3]);
+    }
+}
+
+__device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
+                                         uint32_t* dst, uint32_t c, int logn) {
+    auto yv = [&](int i) {
+        uint32_t v = src[((size_t)P.src_row(i) << logn) + c];
+        if (!j.prescaled) v = Red(A.pr[P.src_prime(i)]).mul(v, P.pre(i));
+        return v;
+    };
+    uint64_t u = 0;
+    const uint32_t* bmod = nullptr;
+    if (j.exact) {
+        const double* rb = exact_rb((const uint32_t*)A.pool, j);
+        bmod = (const uint32_t*)(rb + j.nsrc);
+        if (j.exact == 2) {
+            const uint64_t ns = j.nsrc;
+            u = (ns >> 1) + ((ns & 1) & ((c * 0x9E3779B1u) >> 31));
+        } else {
+            double v = 0.0;
+            for (int i = 0; i < P.ns; ++i) v = __fma_rn((double)yv(i), rb[i], v);
+            u = (uint64_t)floor(v + 0.5);
+        }
+    }
+    for (int t = 0; t < P.nt; ++t) {
+        const Red red(A.pr[P.tgt_prime(t)]);
+        uint64_t acc = 0;
+        uint32_t wraps = 0;
+        for (int i = 0; i < P.ns; ++i) {
+            const uint64_t pr = (uint64_t)yv(i) * P.m(i, t);
+            acc += pr;
+            wraps += acc < pr;
+        }
+        uint32_t r = red.red96(acc, wraps);
+        if (j.exact) r = subm(r, red((uint64_t)u * bmod[t]), red.p);
+        dst[((size_t)P.tgt_row(t) << logn) + c] = r;
+    }
+}
+
+__global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
+    const BconvJob j = A.jobs[blockIdx.y];
+    const Pool P{(const uint32_t*)A.pool + j.pool_off, (int)j.nsrc, (int)j.ntgt};
+    const uint32_t c0 = blockIdx.x * PER_WG + threadIdx.x * V;
+    if (c0 >= (1u << logn) || P.ns < 1) return;
+    const uint32_t* src = (const uint32_t*)A.src + ((size_t)j.src_off << logn);
+    uint32_t* dst = (uint32_t*)A.dst + ((size_t)j.dst_off << logn);
+    if (P.ns <= MAX_REG_SRC) {
+        job_reg(A, j, P, src, dst, c0, logn);
+    } else {
+        for (int k = 0; k < V; ++k) job_wide(A, j, P, src, dst, c0 + k, logn);
+    }
+}
+
+inline int check(const BconvArgs* a) {
+    if (!a || !a->src || !a->dst || !a->jobs || !a->pool || !a->pr || a->njobs < 0) return -1;
+    return 0;
+}
+
+template <int LOGN>
+int launch(const BconvArgs* a, pc_stream_t s) {
+    if (int rc = check(a)) return rc;
+    if (a->njobs == 0) return 0;
+    const int gx = ((1 << LOGN) + PER_WG - 1) / PER_WG;
+    hipLaunchKernelGGL(bconv_k, dim3(gx, a->njobs), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    return launch_rc();
+}
+
+}  // namespace bconv
+}  // namespace pch
+
+namespace pch {
+#define PCH_BCONV_INST(L) \
+    int bconv_##L(const BconvArgs* a, pc_stream_t s) { return bconv::launch<L>(a, s); }
+PCH_BCONV_INST(12)
+PCH_BCONV_INST(13)
+PCH_BCONV_INST(14)
+PCH_BCONV_INST(15)
+PCH_BCONV_INST(16)
+}  // namespace pch

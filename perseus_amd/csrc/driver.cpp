@@ -1,0 +1,934 @@
+// The key-switching driver: the launch sequences of crates/pc-gpu restated in C++ over the kernel table.
+//  - context: prime constants, twiddles and gadget scalars of one chain (crates/pc-gpu/src/context.rs:169-261);
+//  - per limb top a plan (crates/pc-gpu/src/ks.rs:521-676 LevelPlan / level_specs_with): the ModUp INTT rows and their
+//    N^-1 pre_t scales, the ModUp conversion jobs and NTT rows, the dot's row list, the ModDown conversion jobs, INTT
+//    rows and scales, NTT rows; every table ordered [ciphertext][...] so a launch over the first m ciphertexts is a
+//    prefix;
+//  - key groups (crates/pc-gpu/src/ks.rs:330-400 KeyGroup; keys.rs:24-160): seeds, stored b, inverse automorphism
+//    exponents;
+//  - rotate (rotate.rs:179-204) and rotate_hoisted (rotate.rs:456-507).
+// All device memory is allocated at setup; the per-call paths only enqueue launches on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "pc_hip.h"
+
+typedef unsigned __int128 u128;
+
+namespace {
+
+uint64_t mulmod(uint64_t a, uint64_t b, uint64_t m) { return (uint64_t)((u128)a * b % m); }
+uint64_t powmod(uint64_t b, uint64_t e, uint64_t m) {
+    uint64_t r = 1 % m;
+    b %= m;
+    while (e) {
+        if (e & 1) r = mulmod(r, b, m);
+        b = mulmod(b, b, m);
+        e >>= 1;
+    }
+    return r;
+}
+uint64_t invmod(uint64_t a, uint64_t p) { return powmod(a % p, p - 2, p); }
+uint32_t shoup_c(uint32_t w, uint32_t p) { return (uint32_t)(((uint64_t)w << 32) / p); }
+uint32_t brev(uint32_t x, int bits) {
+    uint32_t r = 0;
+    for (int i = 0; i < bits; ++i) r |= ((x >> i) & 1u) << (bits - 1 - i);
+    return r;
+}
+bool is_prime(uint64_t n) {
+    if (n < 2) return false;
+    static const uint64_t sp[] = {2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37};
+    for (uint64_t s : sp)
+        if (n % s == 0) return n == s;
+    uint64_t d = n - 1;
+    int s = 0;
+    while (!(d & 1)) d >>= 1, ++s;
+    for (uint64_t a : sp) {
+        uint64_t x = powmod(a, d, n);
+        if (x == 1 || x == n - 1) continue;
+        bool comp = true;
+        for (int i = 1; i < s && comp; ++i) {
+            x = mulmod(x, x, n);
+            if (x == n - 1) comp = false;
+        }
+        if (comp) return false;
+    }
+    return true;
+}
+// the minimal primitive m-th root of unity (crates/pc-core/src/params/nbtheory.rs:104-140)
+uint64_t min_root(uint64_t m, uint64_t p) {
+    uint64_t e = (p - 1) / m, w = 0;
+    for (uint64_t g = 2; g < p; ++g) {
+        uint64_t c = powmod(g, e, p);
+        if (powmod(c, m / 2, p) == p - 1) {
+            w = c;
+            break;
+        }
+    }
+    uint64_t w2 = mulmod(w, w, p), x = w, mn = w;
+    for (uint64_t k = 1; k + 2 < m; k += 2) {
+        x = mulmod(x, w2, p);
+        if (x < mn && x != 1) mn = x;
+    }
+    return mn;
+}
+// crates/pc-core/src/modmul.rs:376-412 (word_bits 32)
+PrimeConst prime_const(uint64_t p) {
+    PrimeConst c;
+    memset(&c, 0, sizeof c);
+    c.p = p;
+    c.mu_lo = (uint64_t)(((u128)1 << 64) / p);
+    c.bits = 64 - __builtin_clzll(p);
+    c.neal_mu = (uint64_t)(((u128)1 << (2 * c.bits + 1)) / p);
+    c.word_bits = 32;
+    uint64_t inv = p;
+    for (int i = 0; i < 6; ++i) inv *= 2 - p * inv;
+    c.mont_pinv = (-inv) & 0xFFFFFFFFull;
+    c.mont_r2 = (uint64_t)(((u128)1 << 64) % p);
+    uint64_t r = (1ull << 32) % p;
+    c.split = r | ((r << 32) / p) << 32;
+    return c;
+}
+// crates/pc-gpu/src/bconv.rs:34-37: pre_i = (B / b_i)^-1 mod b_i
+std::vector<uint32_t> pre_factors(const std::vector<uint64_t>& bp) {
+    std::vector<uint32_t> out(bp.size());
+    for (size_t i = 0; i < bp.size(); ++i) {
+        uint64_t h = 1;
+        for (size_t k = 0; k < bp.size(); ++k)
+            if (k != i) h = mulmod(h, bp[k] % bp[i], bp[i]);
+        out[i] = (uint32_t)invmod(h, bp[i]);
+    }
+    return out;
+}
+
+struct Dev {
+    std::vector<void*> owned;
+    int err = 0;
+    void* alloc(size_t bytes) {
+        void* p = nullptr;
+        if (bytes == 0) bytes = 16;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            err = (int)e;
+            return nullptr;
+        }
+        owned.push_back(p);
+        return p;
+    }
+    template <class T>
+    T* upload(const std::vector<T>& v) {
+        T* p = (T*)alloc(v.size() * sizeof(T));
+        if (p && !v.empty()) {
+            hipError_t e = hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice);
+            if (e != hipSuccess) err = (int)e;
+        }
+        return p;
+    }
+    ~Dev() {
+        for (void* p : owned) (void)hipFree(p);
+    }
+};
+
+// A fast base-conversion plan: device job records and pool (crates/pc-gpu/src/bconv.rs:59-143 build_tables)
+struct JobSpec {
+    uint32_t src_off, dst_off;
+    std::vector<uint32_t> src, tgt;  // rows == prime ids
+};
+struct Bconv {
+    BconvJob* jobs = nullptr;
+    uint32_t* pool = nullptr;
+    int njobs = 0, max_tgt = 0;
+    void build(Dev& dev, const std::vector<uint64_t>& primes, const std::vector<JobSpec>& specs) {
+        std::vector<uint32_t> pool_h;
+        std::vector<BconvJob> jobs_h;
+        for (const JobSpec& j : specs) {
+            const uint32_t ns = (uint32_t)j.src.size(), nt = (uint32_t)j.tgt.size();
+            BconvJob r;
+            memset(&r, 0, sizeof r);
+            r.src_off = j.src_off;
+            r.dst_off = j.dst_off;
+            r.nsrc = ns;
+            r.ntgt = nt;
+            r.pool_off = (uint32_t)pool_h.size();
+            r.exact = 0;
+            r.prescaled = 1;
+            r.split = 0;
+            std::vector<uint64_t> bp;
+            for (uint32_t s : j.src) bp.push_back(primes[s]);
+            for (uint32_t s : j.src) pool_h.push_back(s);
+            for (uint32_t s : j.src) pool_h.push_back(s);
+            for (uint32_t v : pre_factors(bp)) pool_h.push_back(v);
+            for (uint32_t t : j.tgt) pool_h.push_back(t);
+            for (uint32_t t : j.tgt) pool_h.push_back(t);
+            for (uint32_t i = 0; i < ns; ++i)
+                for (uint32_t t : j.tgt) {
+                    uint64_t tp = primes[t], v = 1;
+                    for (uint32_t k = 0; k < ns; ++k)
+                        if (k != i) v = mulmod(v, bp[k] % tp, tp);
+                    pool_h.push_back((uint32_t)v);
+                }
+            if (pool_h.size() & 1) pool_h.push_back(0);
+            jobs_h.push_back(r);
+            max_tgt = std::max(max_tgt, (int)nt);
+        }
+        njobs = (int)jobs_h.size();
+        jobs = dev.upload(jobs_h);
+        pool = dev.upload(pool_h);
+    }
+};
+
+struct Rows {
+    uint32_t* roff = nullptr;
+    int32_t* rprime = nullptr;
+    uint32_t* soff = nullptr;
+    uint32_t* es = nullptr;  // values then Shoup companions (W words)
+    int n = 0;
+};
+
+struct Level {
+    int top = 0, ndig = 0;
+    Rows mu_intt;             // ModUp INTT rows (coef workspace, c1 out of place), es = N^-1 pre_t
+    Bconv mu_bconv;           // per live digit: digit limbs -> the other live Q limbs and P
+    Rows mu_ntt;              // the targets in the digit workspace
+    uint32_t* ks_rows = nullptr;
+    int nks = 0;
+    Rows md_intt;             // [c < k_rot][part][j < kp]: ext P rows, es = N^-1 pre_j
+    Bconv md_bconv;           // [c][part]: P -> Q rows 0..top
+    Rows md_ntt;              // [c][part][t <= top]
+};
+
+}  // namespace
+
+struct pcx_rows {
+    Rows r;
+    Dev dev;
+};
+
+struct pcx_ctx {
+    uint32_t logn = 0, n = 0;
+    int nq = 0, kp = 0, dnum = 0, alpha = 0, k_rot = 1, rows = 0;
+    std::vector<uint64_t> primes, roots;
+    const KernelTable* tab = nullptr;
+    Dev dev;
+    PrimeConst* pr = nullptr;
+    uint32_t *fw = nullptr, *fws = nullptr, *iw = nullptr, *iws = nullptr, *ninv = nullptr, *ninvs = nullptr;
+    uint32_t *pmod = nullptr, *pinv = nullptr;  // values then Shoup companions, by prime id
+    int32_t* digit_of = nullptr;
+    std::vector<Level> levels;
+    uint32_t *coef = nullptr, *digits = nullptr, *ext = nullptr, *conv = nullptr;
+    size_t ws_bytes = 0;
+
+    size_t row_words() const { return n; }
+    size_t ct_words() const { return (size_t)2 * rows * n; }
+    int digit(int id) const { return id < nq ? id / alpha : -1; }
+};
+
+struct pcx_keys {
+    pcx_ctx* c = nullptr;
+    int nkeys = 0, bits = 0;
+    uint64_t row_words = 0;
+    std::vector<uint64_t> galois;
+    std::vector<uint32_t> autok_h;
+    Dev dev;
+    const void** kb = nullptr;        // device array of per-key b pointers
+    const uint32_t** seed = nullptr;  // device array of per-key seed pointers
+    uint32_t* autok = nullptr;        // g^-1 mod 2N per key
+    std::vector<void*> b_ptr;         // device b storage per key
+};
+
+namespace {
+
+int fill_rows(Dev& dev, Rows& r, const std::vector<uint32_t>& roff, const std::vector<int32_t>& rp,
+              const std::vector<uint32_t>* soff, const std::vector<uint32_t>* es) {
+    r.n = (int)roff.size();
+    r.roff = dev.upload(roff);
+    r.rprime = dev.upload(rp);
+    if (soff) r.soff = dev.upload(*soff);
+    if (es) r.es = dev.upload(*es);
+    return dev.err;
+}
+
+// scale tables: v[i] then shoup(v[i]) for rows of prime ids ids[i]
+std::vector<uint32_t> scale_table(const std::vector<uint64_t>& primes, const std::vector<int32_t>& ids,
+                                  const std::vector<uint32_t>& v) {
+    std::vector<uint32_t> out(v);
+    for (size_t i = 0; i < v.size(); ++i) out.push_back(shoup_c(v[i], (uint32_t)primes[ids[i]]));
+    return out;
+}
+
+// the live limbs of digit d at top (crates/pc-gpu/src/ks.rs:576-578)
+std::vector<uint32_t> digit_limbs(const pcx_ctx* c, int d, int top) {
+    std::vector<uint32_t> v;
+    for (int t = d * c->alpha; t < std::min((d + 1) * c->alpha, c->nq); ++t)
+        if (t <= top) v.push_back((uint32_t)t);
+    return v;
+}
+
+int build_level(pcx_ctx* c, int top, Level& L) {
+    const uint32_t n = c->n;
+    L.top = top;
+    std::vector<std::vector<uint32_t>> digs;
+    for (int d = 0; d < c->dnum; ++d) {
+        std::vector<uint32_t> dl = digit_limbs(c, d, top);
+        if (!dl.empty()) digs.push_back(dl);
+    }
+    L.ndig = (int)digs.size();
+    // ModUp INTT: rows 0..top of the coefficient workspace, read out of place from c1, scaled by N^-1 pre_t
+    std::vector<uint32_t> pre_of(top + 1);
+    for (auto& dl : digs) {
+        std::vector<uint64_t> bp;
+        for (uint32_t t : dl) bp.push_back(c->primes[t]);
+        std::vector<uint32_t> pre = pre_factors(bp);
+        for (size_t k = 0; k < dl.size(); ++k) pre_of[dl[k]] = pre[k];
+    }
+    {
+        std::vector<uint32_t> roff, soff, es;
+        std::vector<int32_t> rp;
+        for (int t = 0; t <= top; ++t) {
+            roff.push_back(t);
+            soff.push_back(t);
+            rp.push_back(t);
+            uint64_t p = c->primes[t];
+            es.push_back((uint32_t)mulmod(invmod(n % p, p), pre_of[t], p));
+        }
+        std::vector<uint32_t> est = scale_table(c->primes, rp, es);
+        if (int e = fill_rows(c->dev, L.mu_intt, roff, rp, &soff, &est)) return e;
+    }
+    // ModUp conversions: digit d's limbs -> (0..top minus the digit) then P, into digit d's rows of the workspace
+    {
+        std::vector<JobSpec> specs;
+        std::vector<uint32_t> roff;
+        std::vector<int32_t> rp;
+        for (int d = 0; d < L.ndig; ++d) {
+            JobSpec j;
+            j.src_off = 0;
+            j.dst_off = (uint32_t)(d * c->rows);
+            j.src = digs[d];
+            for (int t = 0; t <= top; ++t)
+                if (std::find(digs[d].begin(), digs[d].end(), (uint32_t)t) == digs[d].end()) j.tgt.push_back(t);
+            for (int k = 0; k < c->kp; ++k) j.tgt.push_back(c->nq + k);
+            for (uint32_t t : j.tgt) {
+                roff.push_back(j.dst_off + t);
+                rp.push_back((int32_t)t);
+            }
+            specs.push_back(j);
+        }
+        L.mu_bconv.build(c->dev, c->primes, specs);
+        if (int e = fill_rows(c->dev, L.mu_ntt, roff, rp, nullptr, nullptr)) return e;
+    }
+    // dot rows: Q 0..top then P
+    {
+        std::vector<uint32_t> ks;
+        for (int t = 0; t <= top; ++t) ks.push_back(t);
+        for (int k = 0; k < c->kp; ++k) ks.push_back(c->nq + k);
+        L.nks = (int)ks.size();
+        L.ks_rows = c->dev.upload(ks);
+    }
+    // ModDown over k_rot extended ciphertexts [c][part]
+    {
+        std::vector<uint64_t> sp;
+        for (int k = 0; k < c->kp; ++k) sp.push_back(c->primes[c->nq + k]);
+        std::vector<uint32_t> pre = pre_factors(sp);
+        std::vector<uint32_t> roff, es, roff2;
+        std::vector<int32_t> rp, rp2;
+        std::vector<JobSpec> specs;
+        for (int ct = 0; ct < c->k_rot; ++ct)
+            for (int part = 0; part < 2; ++part) {
+                const uint32_t base = (uint32_t)((2 * ct + part) * c->rows);
+                JobSpec j;
+                j.src_off = j.dst_off = base;
+                for (int k = 0; k < c->kp; ++k) {
+                    const int id = c->nq + k;
+                    uint64_t p = c->primes[id];
+                    roff.push_back(base + id);
+                    rp.push_back(id);
+                    es.push_back((uint32_t)mulmod(invmod(n % p, p), pre[k], p));
+                    j.src.push_back(id);
+                }
+                for (int t = 0; t <= top; ++t) {
+                    j.tgt.push_back(t);
+                    roff2.push_back(base + t);
+                    rp2.push_back(t);
+                }
+                specs.push_back(j);
+            }
+        std::vector<uint32_t> est = scale_table(c->primes, rp, es);
+        if (int e = fill_rows(c->dev, L.md_intt, roff, rp, nullptr, &est)) return e;
+        L.md_bconv.build(c->dev, c->primes, specs);
+        if (int e = fill_rows(c->dev, L.md_ntt, roff2, rp2, nullptr, nullptr)) return e;
+    }
+    return c->dev.err;
+}
+
+NttArgs ntt_args(const pcx_ctx* c, void* base, const Rows& r, int nrows) {
+    NttArgs a;
+    memset(&a, 0, sizeof a);
+    a.base = base;
+    a.roff = r.roff;
+    a.rprime = r.rprime;
+    a.fw = c->fw;
+    a.fws = c->fws;
+    a.iw = c->iw;
+    a.iws = c->iws;
+    a.ninv = c->ninv;
+    a.ninvs = c->ninvs;
+    a.pr = c->pr;
+    a.nrows = nrows;
+    a.chunk = 0;
+    a.snum = 1;
+    a.xnum = 1;
+    return a;
+}
+
+const Level* level(const pcx_ctx* c, int top) {
+    if (top < 0 || top >= c->nq) return nullptr;
+    return &c->levels[top];
+}
+
+// ModUp (crates/pc-gpu/src/ks.rs:958-1040): INTT of c1 rows 0..top (out of place, N^-1 pre_t), conversion of every
+// live digit, NTT of the targets
+int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
+    const Level* L = level(c, top);
+    if (!L) return -1;
+    NttArgs a = ntt_args(c, c->coef, L->mu_intt, L->mu_intt.n);
+    a.src = (const uint32_t*)ct + (size_t)c->rows * c->n;  // c1
+    a.soff = L->mu_intt.soff;
+    a.snum = 1;
+    a.es = L->mu_intt.es;
+    a.ess = L->mu_intt.es + L->mu_intt.n;
+    if (int e = c->tab->ntt_inv(&a, s)) return e;
+    BconvArgs b;
+    memset(&b, 0, sizeof b);
+    b.src = c->coef;
+    b.dst = c->digits;
+    b.jobs = L->mu_bconv.jobs;
+    b.pool = L->mu_bconv.pool;
+    b.pr = c->pr;
+    b.njobs = L->mu_bconv.njobs;
+    b.max_tgt = L->mu_bconv.max_tgt;
+    if (int e = c->tab->bconv(&b, s)) return e;
+    NttArgs f = ntt_args(c, c->digits, L->mu_ntt, L->mu_ntt.n);
+    return c->tab->ntt_fwd(&f, s);
+}
+
+// the dot of keys [r0, r0 + m) of k into m extended ciphertexts at ext (crates/pc-gpu/src/ks.rs:1225-1308 dot_key)
+int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s) {
+    const Level* L = level(c, top);
+    if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys) return -1;
+    KsKeyArgs g;
+    memset(&g, 0, sizeof g);
+    KsArgs& a = g.ks;
+    a.c1 = (const uint32_t*)ct + (size_t)c->rows * c->n;
+    a.modup = c->digits;
+    a.c0 = ct;
+    a.out0 = ext;
+    a.out1 = (uint32_t*)ext + (size_t)c->rows * c->n;
+    a.kb = nullptr;
+    a.ka = nullptr;
+    a.autok = k->autok + r0;
+    a.rows = L->ks_rows;
+    a.digit_of = c->digit_of;
+    a.pmod = c->pmod;
+    a.pmods = c->pmod + (c->nq + c->kp);
+    a.pr = c->pr;
+    a.ct_stride = c->ct_words();
+    a.mu_ct_stride = (uint64_t)c->dnum * c->rows * c->n;
+    a.mu_digit_stride = (uint64_t)c->rows * c->n;
+    a.out_ct_stride = c->ct_words();
+    a.out_rot_stride = c->ct_words();
+    a.key_digit_stride = 0;
+    a.K = 1;
+    a.R = m;
+    a.ndig = L->ndig;
+    a.c0_mode = 1;
+    a.nq = c->nq;
+    a.nrows = L->nks;
+    KeyTab& t = g.key;
+    t.kb = k->kb + r0;
+    t.seed = k->seed + r0;
+    t.row_words = k->row_words;
+    t.bits = k->bits;
+    t.q_top = -1;
+    t.srows = c->rows;
+    t.nregen = c->dnum;
+    return c->tab->ks_dot_key(&g, s);
+}
+
+// ModDown of m extended ciphertexts at ext into m ciphertexts at out (crates/pc-gpu/src/ks.rs:1620-1649): INTT of the
+// P rows (N^-1 pre_j), conversion P -> Q rows 0..top into conv, NTT of conv with the epilogue (ext - conv) P^-1
+int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
+    const Level* L = level(c, top);
+    if (!L || m < 1 || m > c->k_rot) return -1;
+    NttArgs a = ntt_args(c, ext, L->md_intt, m * 2 * c->kp);
+    a.es = L->md_intt.es;
+    a.ess = L->md_intt.es + L->md_intt.n;
+    if (int e = c->tab->ntt_inv(&a, s)) return e;
+    BconvArgs b;
+    memset(&b, 0, sizeof b);
+    b.src = ext;
+    b.dst = c->conv;
+    b.jobs = L->md_bconv.jobs;
+    b.pool = L->md_bconv.pool;
+    b.pr = c->pr;
+    b.njobs = 2 * m;
+    b.max_tgt = top + 1;
+    if (int e = c->tab->bconv(&b, s)) return e;
+    NttArgs f = ntt_args(c, c->conv, L->md_ntt, m * 2 * (top + 1));
+    f.epi = 1;
+    f.eout = out;
+    f.ex = ext;
+    f.xnum = 1;
+    f.es = c->pinv;
+    f.ess = c->pinv + (c->nq + c->kp);
+    return c->tab->ntt_fwd(&f, s);
+}
+
+int copy_q(pcx_ctx* c, const void* ct, int top, void* out, pc_stream_t s) {
+    const size_t part = (size_t)c->rows * c->n * 4, q = (size_t)(top + 1) * c->n * 4;
+    for (int p = 0; p < 2; ++p) {
+        hipError_t e = hipMemcpyAsync((char*)out + p * part, (const char*)ct + p * part, q, hipMemcpyDeviceToDevice,
+                                      (hipStream_t)s);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
+void pack_row(const uint32_t* v, uint32_t n, int bits, uint32_t* out, uint64_t row_words) {
+    memset(out, 0, row_words * 4);
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint64_t bit = (uint64_t)i * bits;
+        const uint64_t w = bit >> 5, off = bit & 31;
+        const uint64_t x = (uint64_t)v[i] << off;
+        out[w] |= (uint32_t)x;
+        if (off + bits > 32) out[w + 1] |= (uint32_t)(x >> 32);
+    }
+}
+
+uint64_t packed_row_words(uint32_t n, int bits) {
+    // crates/pc-gpu/src/keys.rs:54-58: N bits / 32 words, one zero guard word, padded to 16 bytes
+    return ((uint64_t)n * bits / 32 + 1 + 3) / 4 * 4;
+}
+
+pcx_keys* keys_shell(pcx_ctx* c, int nkeys, const uint64_t* galois, int bits, int* err) {
+    if (nkeys < 1 || bits < 0 || bits > 32 || (bits > 0 && bits < 31 && false)) {
+        *err = -1;
+        return nullptr;
+    }
+    for (int i = 0; i < c->nq + c->kp; ++i)
+        if (bits > 0 && (c->primes[i] >> bits) != 0) {
+            *err = -1;  // a prime wider than the packed width
+            return nullptr;
+        }
+    pcx_keys* k = new (std::nothrow) pcx_keys;
+    if (!k) {
+        *err = -1;
+        return nullptr;
+    }
+    k->c = c;
+    k->nkeys = nkeys;
+    k->bits = bits;
+    k->row_words = bits ? packed_row_words(c->n, bits) : c->n;
+    const uint64_t m = 2ull * c->n;
+    for (int r = 0; r < nkeys; ++r) {
+        uint64_t g = galois[r] % m;
+        if (!(g & 1)) {
+            delete k;
+            *err = -1;
+            return nullptr;
+        }
+        k->galois.push_back(g);
+        k->autok_h.push_back((uint32_t)powmod(g, (m >> 2) - 1, m));  // g^-1 (crates/pc-core/src/galois.rs:50-59)
+    }
+    k->autok = k->dev.upload(k->autok_h);
+    return k;
+}
+
+}  // namespace
+
+extern "C" {
+
+pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int* err) {
+    int dummy;
+    if (!err) err = &dummy;
+    *err = 0;
+    const KernelTable* tab = pc_table_u32_logn(log_n);
+    if (!tab || nq < 1 || kp < 1 || dnum < 1 || dnum > nq || k_rot < 1 || !primes) {
+        *err = -1;
+        return nullptr;
+    }
+    const uint32_t n = 1u << log_n;
+    for (int i = 0; i < nq + kp; ++i) {
+        uint64_t p = primes[i];
+        if (p >= (1ull << 31) || p < 3 || (p - 1) % (2ull * n) || !is_prime(p)) {
+            *err = -1;
+            return nullptr;
+        }
+        for (int k = 0; k < i; ++k)
+            if (primes[k] == p) {
+                *err = -1;
+                return nullptr;
+            }
+    }
+    pcx_ctx* c = new (std::nothrow) pcx_ctx;
+    if (!c) {
+        *err = -1;
+        return nullptr;
+    }
+    c->logn = log_n;
+    c->n = n;
+    c->nq = nq;
+    c->kp = kp;
+    c->dnum = dnum;
+    c->alpha = (nq + dnum - 1) / dnum;
+    c->k_rot = k_rot;
+    c->rows = nq + kp;
+    c->tab = tab;
+    c->primes.assign(primes, primes + nq + kp);
+    const int R = c->rows;
+    // prime constants and twiddles (crates/pc-gpu/src/context.rs:186-230)
+    std::vector<PrimeConst> pc;
+    std::vector<uint32_t> fw((size_t)R * n), fws((size_t)R * n), iw((size_t)R * n), iws((size_t)R * n);
+    std::vector<uint32_t> ninv, ninvs;
+    for (int id = 0; id < R; ++id) {
+        const uint64_t p = c->primes[id];
+        pc.push_back(prime_const(p));
+        const uint64_t psi = min_root(2ull * n, p), ipsi = invmod(psi, p);
+        c->roots.push_back(psi);
+        uint64_t x = 1, y = 1;
+        std::vector<uint32_t> pw(n), ipw(n);
+        for (uint32_t i = 0; i < n; ++i) {
+            pw[i] = (uint32_t)x;
+            ipw[i] = (uint32_t)y;
+            x = mulmod(x, psi, p);
+            y = mulmod(y, ipsi, p);
+        }
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t e = brev(i, log_n);
+            const size_t o = (size_t)id * n + i;
+            fw[o] = pw[e];
+            fws[o] = shoup_c(pw[e], (uint32_t)p);
+            iw[o] = ipw[e];
+            iws[o] = shoup_c(ipw[e], (uint32_t)p);
+        }
+        ninv.push_back((uint32_t)invmod(n % p, p));
+        ninvs.push_back(shoup_c(ninv.back(), (uint32_t)p));
+    }
+    c->pr = c->dev.upload(pc);
+    c->fw = c->dev.upload(fw);
+    c->fws = c->dev.upload(fws);
+    c->iw = c->dev.upload(iw);
+    c->iws = c->dev.upload(iws);
+    c->ninv = c->dev.upload(ninv);
+    c->ninvs = c->dev.upload(ninvs);
+    // P mod q and P^-1 mod q by prime id, then their Shoup companions (crates/pc-gpu/src/context.rs:234-259)
+    std::vector<uint32_t> pm(R, 0), pi(R, 0);
+    for (int t = 0; t < nq; ++t) {
+        uint64_t q = c->primes[t], m = 1;
+        for (int k = 0; k < kp; ++k) m = mulmod(m, c->primes[nq + k] % q, q);
+        pm[t] = (uint32_t)m;
+        pi[t] = (uint32_t)invmod(m, q);
+    }
+    std::vector<uint32_t> pm2(pm), pi2(pi);
+    for (int t = 0; t < R; ++t) {
+        pm2.push_back(shoup_c(pm[t], (uint32_t)c->primes[t]));
+        pi2.push_back(shoup_c(pi[t], (uint32_t)c->primes[t]));
+    }
+    c->pmod = c->dev.upload(pm2);
+    c->pinv = c->dev.upload(pi2);
+    std::vector<int32_t> dof(R);
+    for (int t = 0; t < R; ++t) dof[t] = c->digit(t);
+    c->digit_of = c->dev.upload(dof);
+    c->levels.resize(nq);
+    for (int top = 0; top < nq && !c->dev.err; ++top)
+        if (int e = build_level(c, top, c->levels[top])) {
+            *err = e;
+            delete c;
+            return nullptr;
+        }
+    // workspace: coefficient rows, ModUp digits, k_rot extended ciphertexts and their conversions
+    const size_t rw = (size_t)n * 4;
+    c->coef = (uint32_t*)c->dev.alloc(nq * rw);
+    c->digits = (uint32_t*)c->dev.alloc((size_t)dnum * R * rw);
+    c->ext = (uint32_t*)c->dev.alloc((size_t)k_rot * 2 * R * rw);
+    c->conv = (uint32_t*)c->dev.alloc((size_t)k_rot * 2 * R * rw);
+    c->ws_bytes = nq * rw + (size_t)dnum * R * rw + 2 * (size_t)k_rot * 2 * R * rw;
+    if (c->dev.err) {
+        *err = c->dev.err;
+        delete c;
+        return nullptr;
+    }
+    if (hipMemset(c->digits, 0, (size_t)dnum * R * rw) != hipSuccess) c->dev.err = -1;
+    if (hipDeviceSynchronize() != hipSuccess) {
+        *err = -1;
+        delete c;
+        return nullptr;
+    }
+    return c;
+}
+
+void pcx_ctx_free(pcx_ctx* c) { delete c; }
+const KernelTable* pcx_ctx_table(const pcx_ctx* c) { return c->tab; }
+const PrimeConst* pcx_ctx_primes(const pcx_ctx* c) { return c->pr; }
+const void* pcx_ctx_twiddle(const pcx_ctx* c, int which) {
+    switch (which) {
+        case 0: return c->fw;
+        case 1: return c->fws;
+        case 2: return c->iw;
+        case 3: return c->iws;
+        case 4: return c->ninv;
+        case 5: return c->ninvs;
+        default: return nullptr;
+    }
+}
+uint64_t pcx_ctx_root(const pcx_ctx* c, int id) { return id >= 0 && id < c->rows ? c->roots[id] : 0; }
+size_t pcx_ctx_workspace_bytes(const pcx_ctx* c) { return c->ws_bytes; }
+size_t pcx_ct_words(const pcx_ctx* c) { return c->ct_words(); }
+
+pcx_rows* pcx_rows_new(pcx_ctx* c, const uint32_t* roff, const int32_t* ids, int nrows) {
+    if (nrows < 0) return nullptr;
+    for (int i = 0; i < nrows; ++i)
+        if (ids[i] < 0 || ids[i] >= c->rows) return nullptr;
+    pcx_rows* r = new (std::nothrow) pcx_rows;
+    if (!r) return nullptr;
+    std::vector<uint32_t> ro(roff, roff + nrows);
+    std::vector<int32_t> rp(ids, ids + nrows);
+    if (fill_rows(r->dev, r->r, ro, rp, nullptr, nullptr)) {
+        delete r;
+        return nullptr;
+    }
+    return r;
+}
+void pcx_rows_free(pcx_rows* r) { delete r; }
+
+int pcx_ntt(pcx_ctx* c, int dir, void* base, const pcx_rows* rows, pc_stream_t s) {
+    if (!c || !rows || (dir != 1 && dir != -1)) return -1;
+    NttArgs a = ntt_args(c, base, rows->r, rows->r.n);
+    return dir == 1 ? c->tab->ntt_fwd(&a, s) : c->tab->ntt_inv(&a, s);
+}
+
+pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
+                       const uint32_t* const* b_host, int bits, int* err) {
+    int dummy;
+    if (!err) err = &dummy;
+    *err = 0;
+    pcx_keys* k = keys_shell(c, nkeys, galois, bits, err);
+    if (!k) return nullptr;
+    const uint32_t n = c->n;
+    const size_t nrow = (size_t)c->dnum * c->rows;
+    std::vector<const void*> kb;
+    std::vector<const uint32_t*> sd;
+    for (int r = 0; r < nkeys; ++r) {
+        std::vector<uint32_t> s(seeds + 8 * r, seeds + 8 * r + 8);
+        sd.push_back(k->dev.upload(s));
+        std::vector<uint32_t> st;
+        if (bits == 0) {
+            st.assign(b_host[r], b_host[r] + nrow * n);
+        } else {
+            st.assign(nrow * k->row_words, 0);
+            for (size_t q = 0; q < nrow; ++q) pack_row(b_host[r] + q * n, n, bits, &st[q * k->row_words], k->row_words);
+        }
+        void* p = k->dev.upload(st);
+        k->b_ptr.push_back(p);
+        kb.push_back(p);
+    }
+    k->kb = (const void**)k->dev.upload(kb);
+    k->seed = (const uint32_t**)k->dev.upload(sd);
+    if (k->dev.err) {
+        *err = k->dev.err;
+        delete k;
+        return nullptr;
+    }
+    return k;
+}
+
+// crates/pc-gpu/src/keygen.rs:172-262: the secret's eval rows, per key the Gaussian errors NTT'd, s_new =
+// sigma_{g^-1}(s) by the automorph kernel, then ksk_gen (b dense or packed)
+pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret,
+                            const uint32_t* seeds, const int64_t* errors, int bits, int* err) {
+    int dummy;
+    if (!err) err = &dummy;
+    *err = 0;
+    pcx_keys* k = keys_shell(c, nkeys, galois, bits, err);
+    if (!k) return nullptr;
+    const uint32_t n = c->n;
+    const int R = c->rows;
+    hipStream_t s = nullptr;
+    // secret eval rows [R][N]
+    std::vector<uint32_t> sh((size_t)R * n);
+    for (int t = 0; t < R; ++t) {
+        const uint32_t p = (uint32_t)c->primes[t];
+        for (uint32_t i = 0; i < n; ++i) sh[(size_t)t * n + i] = secret[i] >= 0 ? (uint32_t)secret[i] : p - (uint32_t)(-secret[i]);
+    }
+    Dev tmp;
+    uint32_t* s_eval = tmp.upload(sh);
+    uint32_t* s_new = (uint32_t*)tmp.alloc((size_t)R * n * 4);
+    uint32_t* e = (uint32_t*)tmp.alloc((size_t)c->dnum * R * n * 4);
+    std::vector<uint32_t> all_roff, e_roff;
+    std::vector<int32_t> all_ids, e_ids;
+    for (int t = 0; t < R; ++t) all_roff.push_back(t), all_ids.push_back(t);
+    for (int d = 0; d < c->dnum; ++d)
+        for (int t = 0; t < R; ++t) e_roff.push_back(d * R + t), e_ids.push_back(t);
+    std::vector<int32_t> ids(all_ids);
+    Rows rows_all, rows_e;
+    fill_rows(tmp, rows_all, all_roff, all_ids, nullptr, nullptr);
+    fill_rows(tmp, rows_e, e_roff, e_ids, nullptr, nullptr);
+    int32_t* d_ids = tmp.upload(ids);
+    if (tmp.err) {
+        *err = tmp.err;
+        delete k;
+        return nullptr;
+    }
+    NttArgs a = ntt_args(c, s_eval, rows_all, R);
+    int rc = c->tab->ntt_fwd(&a, s);
+    std::vector<const void*> kb;
+    std::vector<const uint32_t*> sd;
+    for (int r = 0; r < nkeys && !rc; ++r) {
+        std::vector<uint32_t> sv(seeds + 8 * r, seeds + 8 * r + 8);
+        uint32_t* dseed = k->dev.upload(sv);
+        sd.push_back(dseed);
+        // errors: e_d mod q_t for every row of digit d
+        std::vector<uint32_t> eh((size_t)c->dnum * R * n);
+        for (int d = 0; d < c->dnum; ++d)
+            for (int t = 0; t < R; ++t) {
+                const int64_t p = (int64_t)c->primes[t];
+                const int64_t* ev = errors + ((size_t)r * c->dnum + d) * n;
+                uint32_t* o = &eh[((size_t)d * R + t) * n];
+                for (uint32_t i = 0; i < n; ++i) o[i] = (uint32_t)(((ev[i] % p) + p) % p);
+            }
+        if (hipMemcpy(e, eh.data(), eh.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            rc = -1;
+            break;
+        }
+        NttArgs ea = ntt_args(c, e, rows_e, c->dnum * R);
+        if ((rc = c->tab->ntt_fwd(&ea, s))) break;
+        AutomorphArgs au;
+        memset(&au, 0, sizeof au);
+        au.out = PolyRef{s_new, 0, 0};
+        au.in = PolyRef{s_eval, 0, 0};
+        au.rs = RowSet{R, 0, 0, 0};
+        au.pr = c->pr;
+        au.k = k->autok_h[r];
+        au.K = 1;
+        au.nparts = 1;
+        if ((rc = c->tab->automorph(&au, s))) break;
+        const uint64_t words = (uint64_t)c->dnum * R * k->row_words;
+        void* b = k->dev.alloc(words * 4);
+        if (!b) {
+            rc = -1;
+            break;
+        }
+        k->b_ptr.push_back(b);
+        kb.push_back(b);
+        KskGenArgs g;
+        memset(&g, 0, sizeof g);
+        g.b = b;
+        g.a = nullptr;
+        g.e = e;
+        g.s_new = s_new;
+        g.s_old = s_eval;
+        g.seed = dseed;
+        g.ids = d_ids;
+        g.digit_of = c->digit_of;
+        g.pmod = c->pmod;
+        g.pmods = c->pmod + R;
+        g.pr = c->pr;
+        g.row_words = k->row_words;
+        g.nrows = R;
+        g.ndig = c->dnum;
+        g.nq = c->nq;
+        g.bits = bits;
+        g.sq = 0;
+        if ((rc = c->tab->ksk_gen(&g, s))) break;
+        if (hipDeviceSynchronize() != hipSuccess) rc = -1;
+    }
+    if (!rc) {
+        k->kb = (const void**)k->dev.upload(kb);
+        k->seed = (const uint32_t**)k->dev.upload(sd);
+        if (k->dev.err) rc = k->dev.err;
+    }
+    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = -1;
+    if (rc) {
+        *err = rc;
+        delete k;
+        return nullptr;
+    }
+    return k;
+}
+
+void pcx_keys_free(pcx_keys* k) { delete k; }
+
+int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host) {
+    if (!k || r < 0 || r >= k->nkeys) return -1;
+    pcx_ctx* c = k->c;
+    const size_t nrow = (size_t)c->dnum * c->rows;
+    std::vector<uint32_t> st(nrow * k->row_words);
+    if (hipMemcpy(st.data(), k->b_ptr[r], st.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    for (size_t q = 0; q < nrow; ++q) {
+        const uint32_t* w = &st[q * k->row_words];
+        uint32_t* o = b_host + q * c->n;
+        if (k->bits == 0) {
+            memcpy(o, w, (size_t)c->n * 4);
+            continue;
+        }
+        const uint32_t mask = k->bits == 32 ? 0xFFFFFFFFu : (1u << k->bits) - 1u;
+        for (uint32_t i = 0; i < c->n; ++i) {
+            const uint64_t bit = (uint64_t)i * k->bits;
+            const uint64_t v = ((uint64_t)w[(bit >> 5) + 1] << 32 | w[bit >> 5]) >> (bit & 31);
+            o[i] = (uint32_t)v & mask;
+        }
+    }
+    return 0;
+}
+
+int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) { return modup(c, ct, top, s); }
+const void* pcx_modup_digits(const pcx_ctx* c) { return c->digits; }
+int pcx_dot(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ext, pc_stream_t s) {
+    return dot(c, k, r, 1, ct, top, ext, s);
+}
+int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s) { return moddown(c, ext, 1, top, out, s); }
+
+int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* out, pc_stream_t s) {
+    if (!c || !k || r < 0 || r >= k->nkeys || !level(c, top)) return -1;
+    if (k->galois[r] == 1) return copy_q(c, ct, top, out, s);
+    if (int e = modup(c, ct, top, s)) return e;
+    if (int e = dot(c, k, r, 1, ct, top, c->ext, s)) return e;
+    return moddown(c, c->ext, 1, top, out, s);
+}
+
+int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
+                       pc_stream_t s) {
+    if (!c || !k || n < 1 || !level(c, top)) return -1;
+    for (int j = 0; j < n; ++j)
+        if (idx[j] < 0 || idx[j] >= k->nkeys) return -1;
+    const size_t cw = c->ct_words();
+    bool live = false;
+    for (int j = 0; j < n; ++j) {
+        if (k->galois[idx[j]] == 1) {
+            if (int e = copy_q(c, ct, top, (uint32_t*)out + j * cw, s)) return e;
+        } else {
+            live = true;
+        }
+    }
+    if (!live) return 0;
+    if (int e = modup(c, ct, top, s)) return e;
+    int j = 0;
+    while (j < n) {
+        if (k->galois[idx[j]] == 1) {
+            ++j;
+            continue;
+        }
+        // a chunk: consecutive outputs whose keys are consecutive in the group (one dot launch)
+        int m = 1;
+        while (j + m < n && m < c->k_rot && idx[j + m] == idx[j] + m && k->galois[idx[j + m]] != 1) ++m;
+        if (int e = dot(c, k, idx[j], m, ct, top, c->ext, s)) return e;
+        if (int e = moddown(c, c->ext, m, top, (uint32_t*)out + j * cw, s)) return e;
+        j += m;
+    }
+    return 0;
+}
+
+}  // extern "C"

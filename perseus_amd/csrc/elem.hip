@@ -1,0 +1,103 @@
+// Element-wise kernels over polynomial row sets and the eval-form automorphism (crates/pc-kernels/kernels/args.cuh
+// EwArgs :143-160, AutomorphArgs :754-768; host twin crates/pc-host/src/elem.rs). Grid (N / 1024, rows of the row set,
+// K x nparts), 256 threads of 4 consecutive words (16-byte accesses; rows are N-word aligned).
+#include "common.h"
+
+namespace pch {
+namespace elem {
+
+constexpr int BX = 256;
+
+__device__ __forceinline__ int rs_row(const RowSet& rs, int y) { return y < rs.nq ? y : rs.qmax + (y - rs.nq); }
+__device__ __forceinline__ uint32_t* at(const PolyRef& r, int c, int part, int row, int logn) {
+    return (uint32_t*)r.base + c * r.ct_stride + part * r.part_stride + ((size_t)row << logn);
+}
+
+// op 0 add / sub, 1 scale, 2 sub_mul, 3 copy
+template <int OP>
+__global__ void __launch_bounds__(BX) ew_k(EwArgs A, int logn) {
+    const int y = blockIdx.y;
+    const int row = rs_row(A.rs, y);
+    const int c = blockIdx.z / A.nparts, part = blockIdx.z % A.nparts;
+    const uint32_t i = (blockIdx.x * BX + threadIdx.x) * 4;
+    uint32_t* o = at(A.out, c, part, row, logn) + i;
+    if (OP == 3) {
+        *(uint4*)o = *(const uint4*)(at(A.a, c, part, row, logn) + i);
+        return;
+    }
+    const uint32_t p = (uint32_t)A.pr[row].p;
+    if (OP == 1 && A.zero_p && y >= A.rs.nq) {
+        *(uint4*)o = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    const uint4 x4 = *(const uint4*)(at(A.a, c, part, row, logn) + i);
+    uint32_t x[4] = {x4.x, x4.y, x4.z, x4.w}, r[4];
+    if (OP == 0 || OP == 2) {
+        const uint4 y4 = *(const uint4*)(at(A.b, c, part, row, logn) + i);
+        const uint32_t yv[4] = {y4.x, y4.y, y4.z, y4.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = (OP == 0 && !A.sub) ? addm(x[k], yv[k], p) : subm(x[k], yv[k], p);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = x[k];
+    }
+    if (OP == 1 || OP == 2) {
+        const uint32_t s = ((const uint32_t*)A.sc)[row], ss = ((const uint32_t*)A.scs)[row];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = shoup(r[k], s, ss, p);
+    }
+    *(uint4*)o = make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+template <int OP, int LOGN>
+int ew(const EwArgs* a, pc_stream_t s) {
+    if (!a || !a->out.base || !a->a.base || a->K < 0 || a->nparts < 0) return -1;
+    if ((OP == 0 || OP == 2) && !a->b.base) return -1;
+    if ((OP == 1 || OP == 2) && (!a->sc || !a->scs)) return -1;
+    if (OP != 3 && !a->pr) return -1;
+    const int rows = a->rs.nq + a->rs.np;
+    if (rows <= 0 || a->K == 0 || a->nparts == 0) return 0;
+    hipLaunchKernelGGL(ew_k<OP>, dim3((1 << LOGN) / (BX * 4), rows, a->K * a->nparts), dim3(BX), 0, (hipStream_t)s, *a,
+                       LOGN);
+    return launch_rc();
+}
+
+// out[o] = in[automorph_slot(k, o)] (+ add[o]); a gather: every 32-slot aligned block of the output reads one
+// 32-slot aligned block of the input
+template <bool ADD>
+__global__ void __launch_bounds__(BX) automorph_k(AutomorphArgs A, int logn) {
+    const int row = rs_row(A.rs, blockIdx.y);
+    const int c = blockIdx.z / A.nparts, part = blockIdx.z % A.nparts;
+    const uint32_t o = blockIdx.x * BX + threadIdx.x;
+    uint32_t v = at(A.in, c, part, row, logn)[automorph_slot(A.k, o, logn)];
+    if (ADD) v = addm(v, at(A.add, c, part, row, logn)[o], (uint32_t)A.pr[row].p);
+    at(A.out, c, part, row, logn)[o] = v;
+}
+
+template <int LOGN>
+int automorph(const AutomorphArgs* a, pc_stream_t s) {
+    if (!a || (a->k & 1u) == 0 || !a->out.base || !a->in.base) return -1;
+    if (a->has_add && (!a->add.base || !a->pr)) return -1;
+    const int rows = a->rs.nq + a->rs.np;
+    if (rows <= 0 || a->K <= 0 || a->nparts <= 0) return 0;
+    const dim3 grid((1 << LOGN) / BX, rows, a->K * a->nparts);
+    if (a->has_add) hipLaunchKernelGGL(automorph_k<true>, grid, dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    else hipLaunchKernelGGL(automorph_k<false>, grid, dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    return launch_rc();
+}
+
+}  // namespace elem
+
+#define PCH_EW_INST(L)                                                                                \
+    int ew_add_##L(const EwArgs* a, pc_stream_t s) { return elem::ew<0, L>(a, s); }                  \
+    int ew_scale_##L(const EwArgs* a, pc_stream_t s) { return elem::ew<1, L>(a, s); }                \
+    int ew_sub_mul_##L(const EwArgs* a, pc_stream_t s) { return elem::ew<2, L>(a, s); }              \
+    int ew_copy_##L(const EwArgs* a, pc_stream_t s) { return elem::ew<3, L>(a, s); }                 \
+    int automorph_##L(const AutomorphArgs* a, pc_stream_t s) { return elem::automorph<L>(a, s); }
+PCH_EW_INST(12)
+PCH_EW_INST(13)
+PCH_EW_INST(14)
+PCH_EW_INST(15)
+PCH_EW_INST(16)
+
+}  // namespace pch

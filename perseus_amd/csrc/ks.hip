@@ -1,0 +1,365 @@
+// Hybrid key switching on gfx950: the key inner product with the seeded half of each key regenerated in-kernel, the
+// KSKA expander, key generation and packed-key expansion. Semantics: crates/pc-kernels/kernels/args.cuh KsArgs
+// (:197-228), KeyTab (:284-294), KsKeyArgs (:997-1003), KskExpandArgs (:309-325), KskGenArgs (:817-833),
+// KskUnpackArgs (:836-842); host twins crates/pc-host/src/ks.rs, keys.rs.
+//
+// The dot. One workgroup is one wave (64 lanes) on 1024 consecutive slots of one row t of Q u P and one key r; a lane
+// owns 16 consecutive slots, i.e. exactly one ChaCha12 block of the KSKA stream (16 words per block), so the
+// regeneration needs no cross-lane traffic. Per digit d the lane reads its 16 words of D_d (c1 itself on the rows of
+// digit d, else the ModUp output) and of b_d (dense, or unpacked from an LDS-staged copy of the chunk's packed words),
+// regenerates a_d, and accumulates D b and D a in 64 bits. Rejected ChaCha words (v >= floor((2^32-1)/p) p) are
+// retried at block + t N/16 by the lane that owns them. The output is scattered by sigma_k: in the bit-reversed order
+// the high bits of automorph_slot(k, i) depend only on the high bits of i, so the chunk's 1024 slots land in one
+// aligned 1024-slot chunk of the output, permuted; the permutation goes through LDS and the stores stay coalesced.
+#include "common.h"
+
+namespace pch {
+namespace ks {
+
+constexpr int DBX = 64;          // lanes per workgroup (one wave)
+constexpr int DS = 16;           // slots per lane (one ChaCha block)
+constexpr int DCH = DBX * DS;    // slots per workgroup
+
+__device__ __forceinline__ int slot_of(const KeyTab& T, int t, int nq) {
+    return (t < nq || T.q_top < 0) ? t : T.q_top + 1 + (t - nq);
+}
+
+// The 16 KSKA values of slots [s0, s0 + 16) of (seed, digit d, prime p) (crates/pc-core/src/keys.rs:466-498): block
+// s0/16 of the ChaCha12 stream with state words (counter, d, p, "KSKA"); a rejected word is redrawn from block
+// s0/16 + t N/16 (t = 1..15), the 16th attempt kept as is; value v mod p.
+__device__ __forceinline__ void kska16(const uint32_t (&seed)[8], uint32_t s0, uint32_t d, const Expander& ex,
+                                       uint32_t n16, uint32_t (&a)[DS]) {
+    const uint32_t ctr = s0 >> 4;
+    uint32_t o[16];
+    chacha12(seed, ctr, d, ex.p, TAG_KSKA, o);
+    uint32_t rej = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rej |= (uint32_t)(o[j] >= ex.mp) << j;
+    while (rej) {
+        const int j = __builtin_ctz(rej);
+        rej &= rej - 1;
+        uint32_t v = 0;
+        for (int t = 1; t < KSK_T_MAX; ++t) {
+            v = chacha12_word(seed, ctr + (uint32_t)t * n16, d, ex.p, TAG_KSKA, j);
+            if (v < ex.mp) break;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) o[jj] = jj == j ? v : o[jj];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a[j] = ex.red(o[j]);
+}
+
+// Stage the packed words of the workgroup's chunk (and the word after it) into LDS; values of `bits` bits in a
+// little-endian stream (args.cuh:817-833). The row start is 16-byte aligned (packed rows are multiples of 4 words).
+__device__ __forceinline__ void stage_packed(const uint32_t* row, uint32_t chunk0, int bits, uint32_t* lb) {
+    const uint32_t w0 = chunk0 / 32 * (uint32_t)bits;  // chunk0 is a multiple of 1024
+    const int cnt = DCH / 32 * bits;                    // words of the chunk, a multiple of 4
+    const uint4* src = (const uint4*)(row + w0);
+    for (int q = threadIdx.x; q < cnt / 4; q += DBX) {
+        const uint4 v = src[q];
+        lb[4 * q] = v.x;
+        lb[4 * q + 1] = v.y;
+        lb[4 * q + 2] = v.z;
+        lb[4 * q + 3] = v.w;
+    }
+    if (threadIdx.x == 0) lb[cnt] = row[w0 + cnt];
+}
+__device__ __forceinline__ uint32_t unpack_at(const uint32_t* lb, uint32_t bit, int bits) {
+    const uint32_t w = bit >> 5, off = bit & 31;
+    const uint64_t v = ((uint64_t)lb[w + 1] << 32 | lb[w]) >> off;
+    return bits == 32 ? (uint32_t)v : (uint32_t)v & ((1u << bits) - 1u);
+}
+
+// mode 0: ks_dot (dense kb / ka per key, [digit][prime id][N]); mode 1: ks_dot_key (KeyTab)
+__global__ void __launch_bounds__(DBX) dot_k(KsArgs A, KeyTab T, int logn, int mode) {
+    __shared__ uint32_t l0[DCH], l1[DCH];
+    __shared__ uint32_t lb[DCH + 4];
+    const int r = blockIdx.z;
+    const int t = (int)A.rows[blockIdx.y];
+    const PrimeConst& q = A.pr[t];
+    const uint32_t p = (uint32_t)q.p;
+    const Red red(q);
+    const Expander ex(p);
+    const uint32_t n16 = (1u << logn) >> 4;
+    const uint32_t chunk0 = blockIdx.x * DCH;
+    const uint32_t s0 = chunk0 + threadIdx.x * DS;
+    const int dt = t < A.nq ? A.digit_of[t] : -1;
+    const size_t trow = (size_t)t << logn;
+    const int slot = mode == 1 ? slot_of(T, t, A.nq) : t;
+    const bool packed = mode == 1 && T.bits > 0;
+    uint32_t seed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (mode == 1 && T.nregen > 0) {
+        const uint32_t* sp = T.seed[r];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) seed[i] = sp[i];
+    }
+    const uint32_t kexp = A.autok[r];
+    const int m0 = A.c0_mode & 3;
+    const bool acc_out = (A.c0_mode & PC_KS_ACC) != 0;
+    for (int c = 0; c < A.K; ++c) {
+        uint64_t s0a[DS], s1a[DS];
+        uint32_t w0[DS], w1[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) s0a[k] = s1a[k] = 0, w0[k] = w1[k] = 0;
+        for (int d = 0; d < A.ndig; ++d) {
+            const uint32_t* D = d == dt ? (const uint32_t*)A.c1 + c * A.ct_stride + trow
+                                        : (const uint32_t*)A.modup + c * A.mu_ct_stride + d * A.mu_digit_stride + trow;
+            uint32_t x[DS], b[DS], a[DS];
+            ld16(D + s0, x);
+            if (mode == 0) {
+                ld16((const uint32_t*)A.kb[r] + d * A.key_digit_stride + trow + s0, b);
+            } else if (!packed) {
+                ld16((const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words + s0, b);
+            } else {
+                __syncthreads();
+                stage_packed((const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words, chunk0, T.bits, lb);
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < DS; ++k) b[k] = unpack_at(lb, (threadIdx.x * DS + k) * (uint32_t)T.bits, T.bits);
+            }
+            if (mode == 1 && d < T.nregen) kska16(seed, s0, (uint32_t)d, ex, n16, a);
+            else ld16((const uint32_t*)A.ka[r] + d * A.key_digit_stride + trow + s0, a);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) {
+                const uint64_t pb = (uint64_t)x[k] * b[k], pa = (uint64_t)x[k] * a[k];
+                s0a[k] += pb;
+                w0[k] += s0a[k] < pb;
+                s1a[k] += pa;
+                w1[k] += s1a[k] < pa;
+            }
+        }
+        uint32_t r0[DS], r1[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) {
+            r0[k] = red.red96(s0a[k], w0[k]);
+            r1[k] = red.red96(s1a[k], w1[k]);
+        }
+        if (m0 == 1 && t < A.nq) {
+            uint32_t cz[DS];
+            ld16((const uint32_t*)A.c0 + c * A.ct_stride + trow + s0, cz);
+            const uint32_t pm = ((const uint32_t*)A.pmod)[t], pms = ((const uint32_t*)A.pmods)[t];
+#pragma unroll
+            for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], shoup(cz[k], pm, pms, p), p);
+        } else if (m0 == 2) {
+            uint32_t cz[DS];
+            ld16((const uint32_t*)A.c0 + c * A.ct_stride + trow + s0, cz);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], cz[k], p);
+        }
+        uint32_t* o0 = (uint32_t*)A.out0 + c * A.out_ct_stride + r * A.out_rot_stride + trow;
+        uint32_t* o1 = (uint32_t*)A.out1 + c * A.out_ct_stride + r * A.out_rot_stride + trow;
+        if (kexp == 1 && !acc_out) {
+            st16(o0 + s0, r0);
+            st16(o1 + s0, r1);
+            continue;
+        }
+        // scatter by sigma_k inside the chunk through LDS, then coalesced stores of the output chunk
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < DS; ++k) {
+            const uint32_t o = automorph_slot(kexp, s0 + k, logn) & (DCH - 1);
+            l0[o] = r0[k];
+            l1[o] = r1[k];
+        }
+        __syncthreads();
+        const uint32_t ob = (automorph_slot(kexp, chunk0, logn) & ~(uint32_t)(DCH - 1)) + threadIdx.x * DS;
+        uint32_t v0[DS], v1[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) {
+            v0[k] = l0[threadIdx.x * DS + k];
+            v1[k] = l1[threadIdx.x * DS + k];
+        }
+        if (acc_out) {
+            uint32_t e0[DS], e1[DS];
+            ld16(o0 + ob, e0);
+            ld16(o1 + ob, e1);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) {
+                v0[k] = addm(v0[k], e0[k], p);
+                v1[k] = addm(v1[k], e1[k], p);
+            }
+        }
+        st16(o0 + ob, v0);
+        st16(o1 + ob, v1);
+    }
+}
+
+template <int LOGN>
+int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
+    static_assert((1 << LOGN) >= DCH, "ring of at least 1024 slots");
+    if (a.nrows < 0 || a.R < 0 || a.K < 0 || a.ndig < 0) return -1;
+    if (a.nrows == 0 || a.R == 0 || a.K == 0) return 0;
+    if (!a.rows || !a.pr || !a.c1 || !a.out0 || !a.out1 || !a.autok || !a.digit_of) return -1;
+    if (a.ndig > 0 && !a.modup) return -1;
+    if ((a.c0_mode & 3) == 1 && (!a.c0 || !a.pmod || !a.pmods)) return -1;
+    if ((a.c0_mode & 3) == 2 && !a.c0) return -1;
+    if ((a.c0_mode & 3) == 3) return -1;
+    dim3 grid((1 << LOGN) / DCH, a.nrows, a.R);
+    hipLaunchKernelGGL(dot_k, grid, dim3(DBX), 0, (hipStream_t)s, a, key, LOGN, mode);
+    return launch_rc();
+}
+
+// ks_dot: K <= 8 ciphertexts x R keys stored dense (crates/pc-host/src/ks.rs:139-162: KS_SUM -3, K > 8 -1)
+template <int LOGN>
+int ks_dot(const KsArgs* a, pc_stream_t s) {
+    if (!a) return -1;
+    if (a->c0_mode & PC_KS_SUM) return -3;
+    if (a->K > 8) return -1;
+    if (!a->kb || !a->ka) return -1;
+    KeyTab none = {};
+    return dot_launch<LOGN>(*a, none, 0, s);
+}
+
+// ks_dot_key: keys through a KeyTab (crates/pc-host/src/ks.rs:164-200: bits outside 0..=32 -1, K > 4 -2). The summed
+// rotations (KS_SUM) are not implemented in this build: -3.
+template <int LOGN>
+int ks_dot_key(const KsKeyArgs* g, pc_stream_t s) {
+    if (!g) return -1;
+    if (g->key.bits < 0 || g->key.bits > 32) return -1;
+    if (g->ks.K > 4) return -2;
+    if (g->ks.c0_mode & PC_KS_SUM) return -3;
+    if (!g->key.kb || (g->key.nregen > 0 && !g->key.seed)) return -1;
+    if (g->ks.ndig > g->key.nregen && !g->ks.ka) return -1;
+    if (g->key.bits > 0 && (g->key.row_words % 4 != 0)) return -1;
+    return dot_launch<LOGN>(g->ks, g->key, 1, s);
+}
+
+// ------------------------------------------------------------------------------------------------ expander
+__global__ void __launch_bounds__(DBX) expand_k(KskExpandArgs A, int logn) {
+    const int m = blockIdx.y, z = blockIdx.z;
+    const int id = A.prime_ids[m];
+    const uint32_t p = (uint32_t)A.pr[id].p;
+    const Expander ex(p);
+    uint32_t seed[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) seed[i] = A.seed[i];
+    const uint32_t s0 = blockIdx.x * DCH + threadIdx.x * DS;
+    uint32_t a[DS];
+    kska16(seed, s0, (uint32_t)(A.d0 + z), ex, (1u << logn) >> 4, a);
+    st16((uint32_t*)A.out + (((size_t)z * A.nmod + m) << logn) + s0, a);
+}
+
+template <int LOGN>
+int ksk_expand(const KskExpandArgs* a, pc_stream_t s) {
+    if (!a || !a->out || !a->seed || !a->prime_ids || !a->pr) return -1;
+    if (a->d0 < 0 || a->d0 >= a->dnum || a->nmod < 0) return -1;
+    if (a->nmod == 0) return 0;
+    hipLaunchKernelGGL(expand_k, dim3((1 << LOGN) / DCH, a->nmod, a->dnum - a->d0), dim3(DBX), 0, (hipStream_t)s, *a,
+                       LOGN);
+    return launch_rc();
+}
+
+// ------------------------------------------------------------------------------------------------ key generation
+// b = e - a s_new + [id < nq and digit_of[id] == d] (P mod q_id) s_old' (s_old' = s_old^2 when sq), a from the KSKA
+// expander; b dense or bit-packed (the little-endian value stream, the guard words past N bits / 32 zeroed).
+__global__ void __launch_bounds__(DBX) kskgen_k(KskGenArgs A, int logn) {
+    __shared__ uint32_t lv[DCH];
+    const int m = blockIdx.y, d = blockIdx.z;
+    const int id = A.ids[m];
+    const PrimeConst& q = A.pr[id];
+    const uint32_t p = (uint32_t)q.p;
+    const Red red(q);
+    const Expander ex(p);
+    uint32_t seed[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) seed[i] = A.seed[i];
+    const uint32_t n = 1u << logn;
+    const uint32_t chunk0 = blockIdx.x * DCH;
+    const uint32_t s0 = chunk0 + threadIdx.x * DS;
+    uint32_t a[DS], e[DS], sn[DS], r[DS];
+    kska16(seed, s0, (uint32_t)d, ex, n >> 4, a);
+    const size_t row = (size_t)d * A.nrows + m;
+    ld16((const uint32_t*)A.e + (row << logn) + s0, e);
+    ld16((const uint32_t*)A.s_new + ((size_t)id << logn) + s0, sn);
+    const bool in_digit = id < A.nq && A.digit_of[id] == d;
+    uint32_t so[DS];
+    uint32_t pm = 0, pms = 0;
+    if (in_digit) {
+        ld16((const uint32_t*)A.s_old + ((size_t)id << logn) + s0, so);
+        pm = ((const uint32_t*)A.pmod)[id];
+        pms = ((const uint32_t*)A.pmods)[id];
+    }
+#pragma unroll
+    for (int k = 0; k < DS; ++k) {
+        uint32_t x = e[k];
+        if (in_digit) {
+            uint32_t tv = so[k];
+            if (A.sq) tv = red.mul(tv, tv);
+            x = addm(x, shoup(tv, pm, pms, p), p);
+        }
+        r[k] = subm(x, red.mul(a[k], sn[k]), p);
+    }
+    if (A.a) st16((uint32_t*)A.a + (row << logn) + s0, a);
+    if (A.bits == 0) {
+        st16((uint32_t*)A.b + (row << logn) + s0, r);
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < DS; ++k) lv[threadIdx.x * DS + k] = r[k];
+    __syncthreads();
+    const int bits = A.bits;
+    const uint32_t mask = bits == 32 ? 0xFFFFFFFFu : (1u << bits) - 1u;
+    const int nw = DCH / 32 * bits;
+    uint32_t* out = (uint32_t*)A.b + row * A.row_words + chunk0 / 32 * (uint32_t)bits;
+    for (int w = threadIdx.x; w < nw; w += DBX) {
+        const uint32_t bit0 = (uint32_t)w * 32u;
+        uint32_t k = bit0 / bits;
+        const uint32_t o = bit0 - k * bits;
+        uint64_t acc = (uint64_t)(lv[k] & mask) >> o;
+        for (uint32_t filled = bits - o; filled < 32 && k + 1 < (uint32_t)DCH; filled += bits)
+            acc |= (uint64_t)(lv[++k] & mask) << filled;
+        out[w] = (uint32_t)acc;
+    }
+    if (blockIdx.x == gridDim.x - 1) {
+        uint32_t* rowp = (uint32_t*)A.b + row * A.row_words;
+        for (uint64_t g = (uint64_t)n * bits / 32 + threadIdx.x; g < A.row_words; g += DBX) rowp[g] = 0;
+    }
+}
+
+template <int LOGN>
+int ksk_gen(const KskGenArgs* a, pc_stream_t s) {
+    if (!a || !a->b || !a->e || !a->s_new || !a->seed || !a->ids || !a->pr) return -1;
+    if (a->bits < 0 || a->bits > 32 || a->nrows < 0 || a->ndig < 0) return -1;
+    if (a->bits > 0 && (a->row_words < (uint64_t)(1 << LOGN) * a->bits / 32 + 1)) return -1;
+    if (a->nrows == 0 || a->ndig == 0) return 0;
+    if (!a->digit_of || !a->s_old || !a->pmod || !a->pmods) return -1;
+    hipLaunchKernelGGL(kskgen_k, dim3((1 << LOGN) / DCH, a->nrows, a->ndig), dim3(DBX), 0, (hipStream_t)s, *a, LOGN);
+    return launch_rc();
+}
+
+__global__ void unpack_k(KskUnpackArgs A, int logn) {
+    const int r = blockIdx.y;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t* in = A.in + (size_t)r * A.row_words;
+    const uint64_t bit = (uint64_t)i * A.bits;
+    const uint32_t w = (uint32_t)(bit >> 5), off = (uint32_t)(bit & 31);
+    const uint64_t v = ((uint64_t)in[w + 1] << 32 | in[w]) >> off;
+    const uint32_t mask = A.bits == 32 ? 0xFFFFFFFFu : (1u << A.bits) - 1u;
+    ((uint32_t*)A.out)[((size_t)r << logn) + i] = (uint32_t)v & mask;
+}
+
+template <int LOGN>
+int ksk_unpack(const KskUnpackArgs* a, pc_stream_t s) {
+    if (!a || !a->out || !a->in || a->bits < 1 || a->bits > 32 || a->nrows < 0) return -1;
+    if (a->row_words < (uint64_t)(1 << LOGN) * a->bits / 32 + 1) return -1;
+    if (a->nrows == 0) return 0;
+    hipLaunchKernelGGL(unpack_k, dim3((1 << LOGN) / 256, a->nrows), dim3(256), 0, (hipStream_t)s, *a, LOGN);
+    return launch_rc();
+}
+
+}  // namespace ks
+
+#define PCH_KS_INST(L)                                                                                        \
+    int ks_dot_##L(const KsArgs* a, pc_stream_t s) { return ks::ks_dot<L>(a, s); }                          \
+    int ks_dot_key_##L(const KsKeyArgs* a, pc_stream_t s) { return ks::ks_dot_key<L>(a, s); }                \
+    int ksk_expand_##L(const KskExpandArgs* a, pc_stream_t s) { return ks::ksk_expand<L>(a, s); }            \
+    int ksk_gen_##L(const KskGenArgs* a, pc_stream_t s) { return ks::ksk_gen<L>(a, s); }                     \
+    int ksk_unpack_##L(const KskUnpackArgs* a, pc_stream_t s) { return ks::ksk_unpack<L>(a, s); }
+PCH_KS_INST(12)
+PCH_KS_INST(13)
+PCH_KS_INST(14)
+PCH_KS_INST(15)
+PCH_KS_INST(16)
+
+}  // namespace pch

@@ -1,0 +1,64 @@
+// The kernel tables (crates/pc-kernels/kernels/inst/instantiate.inc:32-91): one constant-initialised KernelTable per
+// ring degree, u32 words, Barrett64 (mm 0). Entries this build does not implement return -1 (argument outside the
+// kernel's range), as the reference's table does for an entry a build leaves out.
+#include "pc_hip.h"
+
+namespace pch {
+#define PCH_DECL(L)                                                  \
+    int ntt_fwd_##L(const NttArgs*, pc_stream_t);                    \
+    int ntt_inv_##L(const NttArgs*, pc_stream_t);                    \
+    int bconv_##L(const BconvArgs*, pc_stream_t);                    \
+    int ew_add_##L(const EwArgs*, pc_stream_t);                      \
+    int ew_scale_##L(const EwArgs*, pc_stream_t);                    \
+    int ew_sub_mul_##L(const EwArgs*, pc_stream_t);                  \
+    int ew_copy_##L(const EwArgs*, pc_stream_t);                     \
+    int automorph_##L(const AutomorphArgs*, pc_stream_t);            \
+    int ks_dot_##L(const KsArgs*, pc_stream_t);                      \
+    int ks_dot_key_##L(const KsKeyArgs*, pc_stream_t);               \
+    int ksk_expand_##L(const KskExpandArgs*, pc_stream_t);           \
+    int ksk_gen_##L(const KskGenArgs*, pc_stream_t);                 \
+    int ksk_unpack_##L(const KskUnpackArgs*, pc_stream_t);
+PCH_DECL(12)
+PCH_DECL(13)
+PCH_DECL(14)
+PCH_DECL(15)
+PCH_DECL(16)
+
+template <class A>
+int absent(const A*, pc_stream_t) {
+    return -1;
+}
+
+#define PCH_TABLE(L)                                                                                                 \
+    static const KernelTable TABLE_##L = {                                                                           \
+        PC_KERNELS_ABI, 4, 0, L,                                                                                     \
+        ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
+        absent<PtDotArgs>, ks_dot_##L, absent<KsRegenArgs>, ksk_expand_##L, absent<CtsArgs>, absent<TensorArgs>,     \
+        absent<MdEpiArgs>, absent<WsumArgs>, absent<AddConstArgs>, absent<MulTableArgs>, absent<RescaleArgs>,        \
+        absent<RescaleCombineArgs>, automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L,             \
+        ksk_unpack_##L, absent<ModRaiseArgs>, absent<SmallIntArgs>, absent<SpruExtractArgs>, absent<SpruFftArgs>,    \
+        absent<SpruScatterArgs>, absent<CtsRegenArgs>, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>,           \
+        absent<WsumKArgs>, absent<RescaleCombineToArgs>, absent<MdEpiToArgs>, absent<SmallInt1Args>,                 \
+        absent<CoeffArgs>, absent<MulAddArgs>, absent<RescaleNttArgs>, absent<MulAddNArgs>, absent<TensorYArgs>,     \
+        absent<WsumMultiArgs>, bconv_##L, absent<TfheArgs>, absent<TensorSumArgs>, absent<TensorMultiArgs>,          \
+        absent<TensorSeededArgs>, absent<EwManyArgs>, absent<SubMulManyArgs>, absent<PackSplitArgs>,                 \
+        absent<PackDotArgs>};
+PCH_TABLE(12)
+PCH_TABLE(13)
+PCH_TABLE(14)
+PCH_TABLE(15)
+PCH_TABLE(16)
+}  // namespace pch
+
+extern "C" const KernelTable* pc_table_u32_barrett64(void) { return &pch::TABLE_16; }
+
+extern "C" const KernelTable* pc_table_u32_logn(uint32_t log_n) {
+    switch (log_n) {
+        case 12: return &pch::TABLE_12;
+        case 13: return &pch::TABLE_13;
+        case 14: return &pch::TABLE_14;
+        case 15: return &pch::TABLE_15;
+        case 16: return &pch::TABLE_16;
+        default: return nullptr;
+    }
+}

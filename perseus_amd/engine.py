@@ -1,0 +1,218 @@
+"""Host objects over the C-ABI: device buffers, streams, events, a key-switching context and key groups.
+
+This mirrors the entry points of the reference's runtime ops (crates/pc-gpu/src/rotate.rs rotate /
+rotate_hoisted, crates/pc-gpu/src/ntt.rs transform_rows, crates/pc-gpu/src/keygen.rs) with the same argument meaning;
+the work itself runs in libpchip.so (the driver and the gfx950 kernels).
+"""
+import ctypes as C
+
+import numpy as np
+
+from ._lib import LIB, HipError, check
+from .chains import Chain
+
+
+def device_count():
+    n = C.c_int(0)
+    rc = LIB.pc_hip_device_count(C.byref(n))
+    return n.value if rc == 0 else 0
+
+
+class Stream:
+    def __init__(self):
+        self.h = C.c_void_p()
+        check(LIB.pc_hip_stream_create(C.byref(self.h)), "stream_create")
+
+    def sync(self):
+        check(LIB.pc_hip_stream_sync(self.h), "stream_sync")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pc_hip_stream_destroy(self.h)
+            self.h = None
+
+
+class Event:
+    def __init__(self):
+        self.h = C.c_void_p()
+        check(LIB.pc_hip_event_create(C.byref(self.h)), "event_create")
+
+    def record(self, stream):
+        check(LIB.pc_hip_event_record(self.h, stream.h), "event_record")
+
+    def sync(self):
+        check(LIB.pc_hip_event_sync(self.h), "event_sync")
+
+    def elapsed_ms(self, later):
+        ms = C.c_float()
+        check(LIB.pc_hip_event_elapsed_ms(C.byref(ms), self.h, later.h), "event_elapsed")
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pc_hip_event_destroy(self.h)
+            self.h = None
+
+
+class DevBuf:
+    """A device allocation of u32 words."""
+
+    def __init__(self, words):
+        self.words = int(words)
+        self.ptr = C.c_void_p()
+        check(LIB.pc_hip_malloc(C.byref(self.ptr), max(4 * self.words, 16)), "malloc")
+
+    @classmethod
+    def from_array(cls, a, stream=None):
+        a = np.ascontiguousarray(a, dtype=np.uint32)
+        b = cls(a.size)
+        b.upload(a, stream)
+        return b
+
+    def upload(self, a, stream=None, offset=0):
+        a = np.ascontiguousarray(a, dtype=np.uint32)
+        assert offset + a.size <= self.words
+        s = stream.h if stream else None
+        check(LIB.pc_hip_memcpy_htod(self.addr(offset), a.ctypes.data, 4 * a.size, s), "htod")
+        if stream:
+            stream.sync()
+        else:
+            check(LIB.pc_hip_device_sync(), "sync")
+
+    def download(self, shape=None, stream=None, offset=0, words=None):
+        words = self.words - offset if words is None else words
+        out = np.empty(words, np.uint32)
+        s = stream.h if stream else None
+        check(LIB.pc_hip_memcpy_dtoh(out.ctypes.data, self.addr(offset), 4 * words, s), "dtoh")
+        if stream:
+            stream.sync()
+        else:
+            check(LIB.pc_hip_device_sync(), "sync")
+        return out.reshape(shape) if shape is not None else out
+
+    def zero(self):
+        check(LIB.pc_hip_memset(self.ptr, 0, 4 * self.words, None), "memset")
+        check(LIB.pc_hip_device_sync(), "sync")
+
+    def addr(self, offset=0):
+        return C.c_void_p(self.ptr.value + 4 * int(offset))
+
+    def __del__(self):
+        if getattr(self, "ptr", None) and self.ptr.value:
+            LIB.pc_hip_free(self.ptr)
+            self.ptr = None
+
+
+def _u64(xs):
+    return (C.c_uint64 * len(xs))(*[int(x) for x in xs])
+
+
+class Context:
+    """One chain on the device: tables, per-top plans and a workspace for k_rot extended ciphertexts."""
+
+    def __init__(self, chain: Chain, k_rot=1):
+        self.chain = chain
+        self.n, self.logn = chain.n, chain.logn
+        self.nq, self.kp, self.dnum, self.rows = len(chain.q), len(chain.p), chain.dnum, chain.rows
+        if self.kp < 1:
+            raise ValueError("a key-switching context needs at least one special prime")
+        err = C.c_int(0)
+        self.h = LIB.pcx_ctx_new(chain.logn, _u64(chain.primes), self.nq, self.kp, chain.dnum, k_rot, C.byref(err))
+        if not self.h:
+            raise HipError(f"pcx_ctx_new failed: {err.value}")
+        self.k_rot = k_rot
+        self.ct_words = 2 * self.rows * self.n
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pcx_ctx_free(self.h)
+            self.h = None
+
+    def ct_buf(self, count=1):
+        return DevBuf(count * self.ct_words)
+
+    def modup(self, ct, top, stream):
+        check(LIB.pcx_modup(self.h, ct.addr(), top, stream.h), "modup")
+
+    def modup_digits(self, stream):
+        """The ModUp workspace [dnum][rows][N] (a copy)."""
+        stream.sync()
+        p = LIB.pcx_modup_digits(self.h)
+        out = np.empty(self.dnum * self.rows * self.n, np.uint32)
+        check(LIB.pc_hip_memcpy_dtoh(out.ctypes.data, p, out.nbytes, stream.h), "dtoh")
+        stream.sync()
+        return out.reshape(self.dnum, self.rows, self.n)
+
+    def dot(self, keys, r, ct, top, ext, stream):
+        check(LIB.pcx_dot(self.h, keys.h, r, ct.addr(), top, ext.addr(), stream.h), "dot")
+
+    def moddown(self, ext, top, out, stream):
+        check(LIB.pcx_moddown(self.h, ext.addr(), top, out.addr(), stream.h), "moddown")
+
+    def rotate(self, keys, r, ct, top, out, stream):
+        check(LIB.pcx_rotate(self.h, keys.h, r, ct.addr(), top, out.addr(), stream.h), "rotate")
+
+    def rotate_hoisted(self, keys, idx, ct, top, out, stream):
+        arr = (C.c_int * len(idx))(*idx)
+        check(LIB.pcx_rotate_hoisted(self.h, keys.h, arr, len(idx), ct.addr(), top, out.addr(), stream.h),
+              "rotate_hoisted")
+
+
+class Keys:
+    """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed."""
+
+    def __init__(self, ctx: Context, galois, seeds=None, b=None, bits=0, secret=None, errors=None):
+        self.ctx = ctx
+        self.galois = [int(g) for g in galois]
+        n = len(self.galois)
+        err = C.c_int(0)
+        seeds = np.ascontiguousarray(seeds, np.uint32).reshape(n, 8)
+        sp = seeds.ctypes.data_as(C.POINTER(C.c_uint32))
+        self._keep = [seeds]
+        if b is not None:
+            bs = [np.ascontiguousarray(x, np.uint32) for x in b]
+            self._keep += bs
+            ptrs = (C.c_void_p * n)(*[x.ctypes.data for x in bs])
+            self.h = LIB.pcx_keys_new(ctx.h, n, _u64(self.galois), sp, ptrs, bits, C.byref(err))
+        else:
+            s = np.ascontiguousarray(secret, np.int8)
+            e = np.ascontiguousarray(errors, np.int64).reshape(n, ctx.dnum, ctx.n)
+            self._keep += [s, e]
+            self.h = LIB.pcx_keys_generate(ctx.h, n, _u64(self.galois), s.ctypes.data_as(C.POINTER(C.c_int8)), sp,
+                                           e.ctypes.data_as(C.POINTER(C.c_int64)), bits, C.byref(err))
+        if not self.h:
+            raise HipError(f"key group failed: {err.value}")
+        self._keep = None
+        self.bits = bits
+
+    def download_b(self, r):
+        out = np.empty((self.ctx.dnum, self.ctx.rows, self.ctx.n), np.uint32)
+        check(LIB.pcx_keys_download_b(self.h, r, out.ctypes.data_as(C.POINTER(C.c_uint32))), "download_b")
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pcx_keys_free(self.h)
+            self.h = None
+
+
+class Rows:
+    """A device row list for batched transforms: row i at base + roff[i] N, prime id ids[i]."""
+
+    def __init__(self, ctx, roff, ids):
+        self.ctx = ctx
+        ro = np.ascontiguousarray(roff, np.uint32)
+        ii = np.ascontiguousarray(ids, np.int32)
+        self.n = len(ro)
+        self.h = LIB.pcx_rows_new(ctx.h, ro.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                  ii.ctypes.data_as(C.POINTER(C.c_int32)), self.n)
+        if not self.h:
+            raise HipError("pcx_rows_new failed")
+
+    def ntt(self, base, direction, stream):
+        check(LIB.pcx_ntt(self.ctx.h, direction, base.addr(), self.h, stream.h), "ntt")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pcx_rows_free(self.h)
+            self.h = None

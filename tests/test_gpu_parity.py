@@ -1,0 +1,223 @@
+"""Parity of the gfx950 path with the oracle, word for word, through the C-ABI (driver + kernel table).
+
+Inputs are seeded; keys are the oracle's (seed of a + stored b), so the GPU regenerates a in-kernel from the same
+seeds the twin expands. Each test prints the case it runs before touching the GPU.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import perseus_amd as pa
+from tests import twin
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def stream():
+    assert pa.device_count() >= 1, "no GPU visible"
+    return pa.Stream()
+
+
+_CTX = {}
+
+
+def contexts(name, k_rot=4):
+    key = (name, k_rot)
+    if key not in _CTX:
+        ch = pa.preset(name)
+        _CTX[key] = (ch, pa.Context(ch, k_rot=k_rot), twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum))
+    return _CTX[key]
+
+
+def random_ct(ch, top, seed):
+    rng = np.random.default_rng(seed)
+    ct = np.zeros((2, ch.rows, ch.n), np.uint32)
+    for part in range(2):
+        for t in range(top + 1):
+            ct[part, t] = rng.integers(0, ch.primes[t], ch.n)
+        ct[part, 0, :4] = [0, ch.primes[0] - 1, 1, ch.primes[0] - 1]
+    return ct
+
+
+def oracle_keys(oc, ch, steps, seed=7):
+    g = twin.Prng([seed, 1, 2, 3, 4, 5, 6, 7], 0)
+    s_eval = oc.secret_eval(g.sparse_ternary(ch.n, 192))
+    gals = [twin.rotation_galois(r, ch.n) for r in steps]
+    keys = [oc.rotation_key(g, s_eval, x) for x in gals]
+    return gals, np.stack([k[0] for k in keys]), [k[1] for k in keys]
+
+
+# ----------------------------------------------------------------------------------------------- NTT
+@pytest.mark.parametrize("logn,bits,nrows", [(12, 30, 6), (13, 31, 5), (14, 30, 8), (15, 31, 4), (16, 31, 12)])
+def test_ntt_rows(stream, logn, bits, nrows):
+    say(f"[ntt] logn={logn} bits={bits} rows={nrows}")
+    ps = twin.descending_primes(bits, 2 << logn, nrows)
+    ch = pa.Chain(f"ntt{logn}", logn, ps[:-1], ps[-1:], 1)
+    ctx = pa.Context(ch, k_rot=1)
+    oc = twin.Ctx(logn, ps[:-1], ps[-1:], 1)
+    n = 1 << logn
+    rng = np.random.default_rng(logn)
+    x = np.stack([rng.integers(0, p, n) for p in ps]).astype(np.uint32)
+    x[0, :3] = [ps[0] - 1, 0, ps[0] - 1]
+    x[1] = ps[1] - 1
+    ids = list(range(nrows))
+    rows = pa.Rows(ctx, ids, ids)
+    buf = pa.DevBuf.from_array(x)
+    rows.ntt(buf, 1, stream)
+    stream.sync()
+    y = buf.download((nrows, n))
+    want = oc.ntt_fwd(x.copy(), ids)
+    assert (y == want).all()
+    rows.ntt(buf, -1, stream)
+    stream.sync()
+    assert (buf.download((nrows, n)) == x).all()
+    # inverse of arbitrary words against the twin
+    buf.upload(x)
+    rows.ntt(buf, -1, stream)
+    stream.sync()
+    assert (buf.download((nrows, n)) == oc.ntt_inv(x.copy(), ids)).all()
+
+
+def test_ntt_batch_c2(stream):
+    """The C2 workload: 64 polynomials x 40 limbs at N = 2^16 (2560 row transforms), forward bit-exact against the
+    twin and the round trip exact."""
+    ch = pa.preset("c2")
+    say("[ntt c2] 64 x 40 x 2^16")
+    ctx = pa.Context(pa.Chain("c2k", 16, ch.q[:-1], ch.q[-1:], 1), k_rot=1)
+    oc = twin.Ctx(16, ch.q, [], 1)
+    twin.set_threads(16)
+    npoly, L, n = 64, 40, 1 << 16
+    rng = np.random.default_rng(2)
+    qs = np.array(ch.q, np.uint64)
+    x = (rng.integers(0, 1 << 62, (npoly, L, n), dtype=np.uint64) % qs[None, :, None]).astype(np.uint32)
+    ids = [t for _ in range(npoly) for t in range(L)]
+    rows = pa.Rows(ctx, list(range(npoly * L)), ids)
+    buf = pa.DevBuf.from_array(x)
+    rows.ntt(buf, 1, stream)
+    stream.sync()
+    y = buf.download((npoly, L, n))
+    want = oc.ntt_fwd(x.reshape(-1, n).copy(), ids).reshape(npoly, L, n)
+    assert (y == want).all()
+    rows.ntt(buf, -1, stream)
+    stream.sync()
+    assert (buf.download((npoly, L, n)) == x).all()
+
+
+# ----------------------------------------------------------------------------------------------- key switch stages
+@pytest.mark.parametrize("name,top", [("small", 5), ("small", 2), ("small31", 5), ("c1", 11), ("c1", 6)])
+def test_modup(stream, name, top):
+    say(f"[modup] {name} top={top}")
+    ch, ctx, oc = contexts(name)
+    ct = random_ct(ch, top, 11 + top)
+    dev = pa.DevBuf.from_array(ct)
+    ctx.modup(dev, top, stream)
+    got = ctx.modup_digits(stream)
+    want = oc.modup(ct[1, : top + 1], top)
+    nd = oc.live_digits(top)
+    for d in range(nd):
+        dl = [t for t in range(top + 1) if oc.digit_of(t) == d]
+        tg = [t for t in range(top + 1) if t not in dl] + list(range(ch.rows - len(ch.p), ch.rows))
+        assert (got[d, tg] == want[d, tg]).all(), d
+
+
+@pytest.mark.parametrize("name,top,bits", [("small", 5, 0), ("small", 5, 30), ("small31", 4, 31), ("c1", 11, 0),
+                                           ("c1", 11, 30), ("c1", 3, 30)])
+def test_dot_and_moddown(stream, name, top, bits):
+    say(f"[dot/moddown] {name} top={top} bits={bits}")
+    ch, ctx, oc = contexts(name)
+    gals, seeds, bs = oracle_keys(oc, ch, [1, 5])
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=bits)
+    ct = random_ct(ch, top, 3)
+    dev = pa.DevBuf.from_array(ct)
+    ext = ctx.ct_buf()
+    ext.zero()
+    ctx.modup(dev, top, stream)
+    ctx.dot(keys, 1, dev, top, ext, stream)
+    stream.sync()
+    got = ext.download((2, ch.rows, ch.n))
+    digits = oc.modup(ct[1, : top + 1], top)
+    want = oc.ks_dot(ct, digits, top, seeds[1], bs[1], twin.galois_inverse(gals[1], ch.n))
+    live = list(range(top + 1)) + list(range(len(ch.q), ch.rows))
+    assert (got[:, live] == want[:, live]).all()
+    out = ctx.ct_buf()
+    ctx.moddown(ext, top, out, stream)
+    stream.sync()
+    got_o = out.download((2, ch.rows, ch.n))
+    want_o = oc.moddown(want, top)
+    assert (got_o[:, : top + 1] == want_o[:, : top + 1]).all()
+
+
+# ----------------------------------------------------------------------------------------------- rotations
+def test_rotate_c1(stream):
+    """C1: one rotation (r = 1) at N = 2^14, 12 limbs, dnum 3, 4 special primes, every output residue."""
+    say("[rotate c1]")
+    ch, ctx, oc = contexts("c1")
+    gals, seeds, bs = oracle_keys(oc, ch, [1], seed=42)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=30)
+    top = len(ch.q) - 1
+    ct = random_ct(ch, top, 1)
+    dev = pa.DevBuf.from_array(ct)
+    out = ctx.ct_buf()
+    ctx.rotate(keys, 0, dev, top, out, stream)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.rotate(ct, top, seeds[0], bs[0], gals[0])
+    assert (got[:, : top + 1] == want[:, : top + 1]).all()
+
+
+@pytest.mark.parametrize("name,steps,top", [("small", [1, 2, 3, 0, 7], 5), ("c3", [1, 2, 16, 1 << 15, 64], 29),
+                                            ("c3", [3, 4], 13)])
+def test_hoisted(stream, name, steps, top):
+    say(f"[hoisted] {name} steps={steps} top={top}")
+    ch, ctx, oc = contexts(name, k_rot=4)
+    twin.set_threads(16)
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=5)
+    bits = max(p.bit_length() for p in ch.primes)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=bits)
+    ct = random_ct(ch, top, 9)
+    dev = pa.DevBuf.from_array(ct)
+    outs = ctx.ct_buf(len(steps))
+    ctx.rotate_hoisted(keys, list(range(len(steps))), dev, top, outs, stream)
+    stream.sync()
+    got = outs.download((len(steps), 2, ch.rows, ch.n))
+    want = oc.rotate_hoisted(ct, top, seeds, bs, gals)
+    for j in range(len(steps)):
+        assert (got[j, :, : top + 1] == want[j][:, : top + 1]).all(), steps[j]
+    # the same outputs one rotation at a time (crates/pc-tools/src/word_seam.rs:312-317: hoisted == plain)
+    one = ctx.ct_buf()
+    for j in range(len(steps)):
+        ctx.rotate(keys, j, dev, top, one, stream)
+        stream.sync()
+        assert (one.download((2, ch.rows, ch.n))[:, : top + 1] == got[j, :, : top + 1]).all()
+
+
+# ----------------------------------------------------------------------------------------------- keys
+@pytest.mark.parametrize("name,bits", [("small", 0), ("small", 30), ("c1", 30), ("small31", 31)])
+def test_device_keygen(stream, name, bits):
+    """ksk_gen on the device (a regenerated from the seed, b = e - a s_new + [digit] P s_old, packed) against the
+    twin's ksk_gen on the same secret, errors and seeds."""
+    say(f"[keygen] {name} bits={bits}")
+    ch, ctx, oc = contexts(name)
+    g = twin.Prng([3, 1, 4, 1, 5, 9, 2, 6], 0)
+    s = g.sparse_ternary(ch.n, 64)
+    s_eval = oc.secret_eval(s)
+    gals = [twin.rotation_galois(r, ch.n) for r in (1, 3)]
+    seeds = np.stack([g.ksk_seed() for _ in gals])
+    errs = np.stack([np.stack([g.gaussian(ch.n) for _ in range(ch.dnum)]) for _ in gals])
+    keys = pa.Keys(ctx, gals, seeds=seeds, bits=bits, secret=s, errors=errs)
+    for r, gal in enumerate(gals):
+        e = np.zeros((ch.dnum, ch.rows, ch.n), np.uint32)
+        for d in range(ch.dnum):
+            for t in range(ch.rows):
+                e[d, t] = np.mod(errs[r, d], ch.primes[t])
+        e = oc.ntt_fwd(e.reshape(-1, ch.n), [t for _ in range(ch.dnum) for t in range(ch.rows)]).reshape(e.shape)
+        s_new = oc.automorph_rows(s_eval, twin.galois_inverse(gal, ch.n))
+        want = oc.ksk_gen(s_new, s_eval, seeds[r], e)
+        assert (keys.download_b(r) == want).all(), r

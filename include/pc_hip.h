@@ -350,7 +350,7 @@ PC_STATIC_ASSERT(sizeof(KernelTable) == 16 + 52 * 8, "KernelTable layout");
 
 /* The u32 x Barrett64 table at N = 2^16 (instantiate.inc:32-91; header {abi 30, word_bytes 4, mm 0, log_n 16}). */
 const KernelTable* pc_table_u32_barrett64(void);
-/* The same kernels at N = 2^log_n, log_n in [10, 17] (the header's log_n field says which). No counterpart in the
+/* The same kernels at N = 2^log_n, log_n in [12, 16] (the header's log_n field says which). No counterpart in the
  * reference, whose table is fixed at 2^16 (args.cuh:14-18): it exists for ring degrees such as 2^14. NULL outside
  * the range. */
 const KernelTable* pc_table_u32_logn(uint32_t log_n);
@@ -440,6 +440,14 @@ int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);
 const void* pcx_modup_digits(const pcx_ctx* c); /* [dnum][nq + kp][N] */
 int pcx_dot(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ext, pc_stream_t s);
 int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s);
+
+/* Stage timing, for measurement: while on, the driver records a HIP event pair on the launch stream around each
+ * stage it enqueues (0 ModUp INTT, 1 ModUp conversion, 2 ModUp NTT, 3 key dot, 4 ModDown INTT, 5 ModDown conversion,
+ * 6 ModDown NTT + epilogue). pcx_timing(c, n) turns it on for up to n stages (resetting the record); 0 turns it off.
+ * pcx_timing_read sums the device time of one stage after the stream has synchronised. No counterpart in the
+ * reference (its benches time with CUDA events around whole ops, crates/pc-gpu/benches/ks.rs:80-98). */
+int pcx_timing(pcx_ctx* c, int max_stages);
+int pcx_timing_read(pcx_ctx* c, int stage, double* total_ms, int* count);
 
 #ifdef __cplusplus
 }

@@ -72,6 +72,8 @@ _SIGS = {
     "pcx_modup_digits": (vp, [vp]),
     "pcx_dot": (C.c_int, [vp, vp, C.c_int, vp, C.c_int, vp, vp]),
     "pcx_moddown": (C.c_int, [vp, vp, C.c_int, vp, vp]),
+    "pcx_timing": (C.c_int, [vp, C.c_int]),
+    "pcx_timing_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(LIB, _name)

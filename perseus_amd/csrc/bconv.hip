@@ -2,7 +2,7 @@
 //   y_i = x_i pre_i mod s_i (prescaled jobs: y_i = x_i as stored), out_t = sum_i y_i M[i][t] mod t;
 //   exact jobs: v = sum_i y_i rb_i (double FMA in source order), u = floor(v + 0.5) (centred: the lift's mean),
 //   out_t -= u (B mod t).
-// One launch for every job of a plan: grid (N / 1024, njobs), 256 threads of 4 consecutive coefficients.
+// One launch for every job of a plan: grid (N / 512, njobs), 256 threads of 2 consecutive coefficients.
 //
 // 31-bit primes break the reference's lazy bound nsrc (p - 1)^2 < 2^64 past 4 sources, so the sum of products is
 // carried in 96 bits (a 64-bit sum and a count of its wraps) and reduced once: the exact integer formula, whatever
@@ -12,7 +12,7 @@
 namespace pch {
 namespace bconv {
 
-constexpr int BX = 256, V = 4, PER_WG = BX * V;
+constexpr int BX = 256, V = 2, PER_WG = BX * V;
 constexpr int MAX_REG_SRC = 16;
 
 struct Pool {
@@ -46,43 +46,64 @@ __device__ __forceinline__ uint64_t exact_u(const BconvJob& j, const double* rb,
     return (uint64_t)floor(v + 0.5);
 }
 
-// One workgroup = one job x 1024 coefficients (4 per thread). A job's record lives in device memory, so the source
+// One workgroup = one job x 512 coefficients (2 per thread). A job's record lives in device memory, so the source
 // count is read here: jobs of at most 16 sources keep the y of their 4 coefficients in registers, wider jobs
 // (bconv_wide, up to 48 at u32 words) re-read their sources per target (L1/L2 resident).
 __device__ __forceinline__ void job_reg(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
                                         uint32_t* dst, uint32_t c0, int logn) {
+    // the sources of the 4 coefficients stay in registers: the loops are unrolled to 16 and predicated on ns
     uint32_t y[MAX_REG_SRC * V];
-    for (int i = 0; i < P.ns; ++i) {
-        const uint4 x = *(const uint4*)(src + ((size_t)P.src_row(i) << logn) + c0);
-        uint32_t v[V] = {x.x, x.y, x.z, x.w};
-        if (!j.prescaled) {
-            const Red red(A.pr[P.src_prime(i)]);
-            const uint32_t pre = P.pre(i);
 #pragma unroll
-            for (int k = 0; k < V; ++k) v[k] = red.mul(v[k], pre);
+    for (int i = 0; i < MAX_REG_SRC; ++i) {
+        if (i < P.ns) {
+            const uint2 x = *(const uint2*)(src + ((size_t)P.src_row(i) << logn) + c0);
+            uint32_t v[V] = {x.x, x.y};
+            if (!j.prescaled) {
+                const Red red(A.pr[P.src_prime(i)]);
+                const uint32_t pre = P.pre(i);
+#pragma unroll
+                for (int k = 0; k < V; ++k) v[k] = red.mul(v[k], pre);
+            }
+#pragma unroll
+            for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; ++k) y[i * V + k] = 0;
         }
-#pragma unroll
-        for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
     }
-    uint64_t u[V] = {0, 0, 0, 0};
+    uint64_t u[V] = {0, 0};
     const uint32_t* bmod = nullptr;
     if (j.exact) {
         const double* rb = exact_rb((const uint32_t*)A.pool, j);
         bmod = (const uint32_t*)(rb + j.nsrc);
 #pragma unroll
-        for (int k = 0; k < V; ++k) u[k] = exact_u(j, rb, y + k, V, c0 + k);
+        for (int k = 0; k < V; ++k) {
+            if (j.exact == 2) {
+                const uint64_t ns = j.nsrc;
+                u[k] = (ns >> 1) + ((ns & 1) & (((c0 + k) * 0x9E3779B1u) >> 31));
+            } else {
+                double v = 0.0;
+#pragma unroll
+                for (int i = 0; i < MAX_REG_SRC; ++i)
+                    if (i < P.ns) v = __fma_rn((double)y[i * V + k], rb[i], v);
+                u[k] = (uint64_t)floor(v + 0.5);
+            }
+        }
     }
     for (int t = 0; t < P.nt; ++t) {
         const Red red(A.pr[P.tgt_prime(t)]);
-        uint64_t acc[V] = {0, 0, 0, 0};
-        uint32_t wraps[V] = {0, 0, 0, 0};
-        for (int i = 0; i < P.ns; ++i) {
-            const uint32_t m = P.m(i, t);
+        uint64_t acc[V] = {0, 0};
+        uint32_t wraps[V] = {0, 0};
 #pragma unroll
-            for (int k = 0; k < V; ++k) {
-                const uint64_t pr = (uint64_t)y[i * V + k] * m;
-                acc[k] += pr;
-                wraps[k] += acc[k] < pr;
+        for (int i = 0; i < MAX_REG_SRC; ++i) {
+            if (i < P.ns) {
+                const uint32_t m = P.m(i, t);
+#pragma unroll
+                for (int k = 0; k < V; ++k) {
+                    const uint64_t pr = (uint64_t)y[i * V + k] * m;
+                    acc[k] += pr;
+                    wraps[k] += acc[k] < pr;
+                }
             }
         }
         uint32_t r[V];
@@ -91,7 +112,7 @@ __device__ __forceinline__ void job_reg(const BconvArgs& A, const BconvJob& j, c
             r[k] = red.red96(acc[k], wraps[k]);
             if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * bmod[t]), red.p);
         }
-        *(uint4*)(dst + ((size_t)P.tgt_row(t) << logn) + c0) = make_uint4(r[0], r[1], r[2], r[3]);
+        *(uint2*)(dst + ((size_t)P.tgt_row(t) << logn) + c0) = make_uint2(r[0], r[1]);
     }
 }
 

@@ -221,6 +221,11 @@ struct pcx_ctx {
     std::vector<Level> levels;
     uint32_t *coef = nullptr, *digits = nullptr, *ext = nullptr, *conv = nullptr;
     size_t ws_bytes = 0;
+    // stage timing (pcx_timing): event pairs recorded around each stage's launches on the launch stream
+    bool timing = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<int> ev_stage;  // stage of pair i (events 2i, 2i + 1)
+    size_t ev_used = 0;
 
     size_t row_words() const { return n; }
     size_t ct_words() const { return (size_t)2 * rows * n; }
@@ -241,6 +246,24 @@ struct pcx_keys {
 };
 
 namespace {
+
+// A stage bracket: when timing is on, an event before and after the stage's launches (stream order)
+struct Stage {
+    pcx_ctx* c;
+    int id;
+    pc_stream_t s;
+    size_t slot;
+    Stage(pcx_ctx* c_, int id_, pc_stream_t s_) : c(c_), id(id_), s(s_), slot(SIZE_MAX) {
+        if (c->timing && 2 * (c->ev_used + 1) <= c->ev.size()) {
+            slot = c->ev_used++;
+            c->ev_stage[slot] = id;
+            (void)hipEventRecord(c->ev[2 * slot], (hipStream_t)s);
+        }
+    }
+    ~Stage() {
+        if (slot != SIZE_MAX) (void)hipEventRecord(c->ev[2 * slot + 1], (hipStream_t)s);
+    }
+};
 
 int fill_rows(Dev& dev, Rows& r, const std::vector<uint32_t>& roff, const std::vector<int32_t>& rp,
               const std::vector<uint32_t>* soff, const std::vector<uint32_t>* es) {
@@ -400,7 +423,10 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
     a.snum = 1;
     a.es = L->mu_intt.es;
     a.ess = L->mu_intt.es + L->mu_intt.n;
-    if (int e = c->tab->ntt_inv(&a, s)) return e;
+    {
+        Stage st(c, 0, s);
+        if (int e = c->tab->ntt_inv(&a, s)) return e;
+    }
     BconvArgs b;
     memset(&b, 0, sizeof b);
     b.src = c->coef;
@@ -410,8 +436,12 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
     b.pr = c->pr;
     b.njobs = L->mu_bconv.njobs;
     b.max_tgt = L->mu_bconv.max_tgt;
-    if (int e = c->tab->bconv(&b, s)) return e;
+    {
+        Stage st(c, 1, s);
+        if (int e = c->tab->bconv(&b, s)) return e;
+    }
     NttArgs f = ntt_args(c, c->digits, L->mu_ntt, L->mu_ntt.n);
+    Stage st(c, 2, s);
     return c->tab->ntt_fwd(&f, s);
 }
 
@@ -455,6 +485,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     t.q_top = -1;
     t.srows = c->rows;
     t.nregen = c->dnum;
+    Stage st(c, 3, s);
     return c->tab->ks_dot_key(&g, s);
 }
 
@@ -466,7 +497,10 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
     NttArgs a = ntt_args(c, ext, L->md_intt, m * 2 * c->kp);
     a.es = L->md_intt.es;
     a.ess = L->md_intt.es + L->md_intt.n;
-    if (int e = c->tab->ntt_inv(&a, s)) return e;
+    {
+        Stage st(c, 4, s);
+        if (int e = c->tab->ntt_inv(&a, s)) return e;
+    }
     BconvArgs b;
     memset(&b, 0, sizeof b);
     b.src = ext;
@@ -476,7 +510,10 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
     b.pr = c->pr;
     b.njobs = 2 * m;
     b.max_tgt = top + 1;
-    if (int e = c->tab->bconv(&b, s)) return e;
+    {
+        Stage st(c, 5, s);
+        if (int e = c->tab->bconv(&b, s)) return e;
+    }
     NttArgs f = ntt_args(c, c->conv, L->md_ntt, m * 2 * (top + 1));
     f.epi = 1;
     f.eout = out;
@@ -484,6 +521,7 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
     f.xnum = 1;
     f.es = c->pinv;
     f.ess = c->pinv + (c->nq + c->kp);
+    Stage st(c, 6, s);
     return c->tab->ntt_fwd(&f, s);
 }
 
@@ -670,7 +708,45 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     return c;
 }
 
-void pcx_ctx_free(pcx_ctx* c) { delete c; }
+void pcx_ctx_free(pcx_ctx* c) {
+    if (!c) return;
+    for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+    delete c;
+}
+
+int pcx_timing(pcx_ctx* c, int max_stages) {
+    if (!c || max_stages < 0) return -1;
+    if (max_stages == 0) {
+        c->timing = false;
+        return 0;
+    }
+    while (c->ev.size() < 2 * (size_t)max_stages) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return -1;
+        c->ev.push_back(e);
+    }
+    c->ev_stage.assign(c->ev.size() / 2, -1);
+    c->ev_used = 0;
+    c->timing = true;
+    return 0;
+}
+
+int pcx_timing_read(pcx_ctx* c, int stage, double* total_ms, int* count) {
+    if (!c || !total_ms || !count) return -1;
+    double t = 0;
+    int n = 0;
+    for (size_t i = 0; i < c->ev_used; ++i) {
+        if (c->ev_stage[i] != stage) continue;
+        float ms = 0;
+        hipError_t e = hipEventElapsedTime(&ms, c->ev[2 * i], c->ev[2 * i + 1]);
+        if (e != hipSuccess) return (int)e;
+        t += ms;
+        ++n;
+    }
+    *total_ms = t;
+    *count = n;
+    return 0;
+}
 const KernelTable* pcx_ctx_table(const pcx_ctx* c) { return c->tab; }
 const PrimeConst* pcx_ctx_primes(const pcx_ctx* c) { return c->pr; }
 const void* pcx_ctx_twiddle(const pcx_ctx* c, int which) {

@@ -3,14 +3,17 @@
 // (:197-228), KeyTab (:284-294), KsKeyArgs (:997-1003), KskExpandArgs (:309-325), KskGenArgs (:817-833),
 // KskUnpackArgs (:836-842); host twins crates/pc-host/src/ks.rs, keys.rs.
 //
-// The dot. One workgroup is one wave (64 lanes) on 1024 consecutive slots of one row t of Q u P and one key r; a lane
-// owns 16 consecutive slots, i.e. exactly one ChaCha12 block of the KSKA stream (16 words per block), so the
-// regeneration needs no cross-lane traffic. Per digit d the lane reads its 16 words of D_d (c1 itself on the rows of
-// digit d, else the ModUp output) and of b_d (dense, or unpacked from an LDS-staged copy of the chunk's packed words),
-// regenerates a_d, and accumulates D b and D a in 64 bits. Rejected ChaCha words (v >= floor((2^32-1)/p) p) are
-// retried at block + t N/16 by the lane that owns them. The output is scattered by sigma_k: in the bit-reversed order
-// the high bits of automorph_slot(k, i) depend only on the high bits of i, so the chunk's 1024 slots land in one
-// aligned 1024-slot chunk of the output, permuted; the permutation goes through LDS and the stores stay coalesced.
+// The dot. A workgroup (4 waves) owns 1024 consecutive slots of one row t of Q u P and a group of keys. It stages the
+// chunk's digit operands D_d (c1 itself on the rows of digit d, else the ModUp output) and c0 in LDS once; every key
+// of the group reuses them, so the ModUp output is read once per batch instead of once per key. Each wave takes one
+// key at a time; a lane owns 16 consecutive slots, exactly one ChaCha12 block of the KSKA stream (16 words per
+// block), so the regeneration of a needs no cross-lane traffic. Per digit the lane reads its 16 words of b (dense, or
+// from the bit-packed stream), regenerates a, and accumulates D b and D a in 64 bits (P c0 folded in). Rejected ChaCha
+// words (v >= floor((2^32-1)/p) p, up to a few percent at 31-bit primes) go to a wave-local LDS queue that the whole
+// wave redraws at once, their products added to the slot's sum with 64-bit LDS atomics, so a rare retry does not
+// stall the wave. The output is scattered by sigma_k: in the bit-reversed order the high bits of automorph_slot(k, i)
+// depend only on the high bits of i, so the chunk's 1024 slots land in one aligned 1024-slot chunk of the output,
+// permuted; the permutation goes through LDS and the stores stay coalesced.
 #include "common.h"
 
 namespace pch {
@@ -50,138 +53,245 @@ __device__ __forceinline__ void kska16(const uint32_t (&seed)[8], uint32_t s0, u
     for (int j = 0; j < 16; ++j) a[j] = ex.red(o[j]);
 }
 
-// Stage the packed words of the workgroup's chunk (and the word after it) into LDS; values of `bits` bits in a
-// little-endian stream (args.cuh:817-833). The row start is 16-byte aligned (packed rows are multiples of 4 words).
-__device__ __forceinline__ void stage_packed(const uint32_t* row, uint32_t chunk0, int bits, uint32_t* lb) {
-    const uint32_t w0 = chunk0 / 32 * (uint32_t)bits;  // chunk0 is a multiple of 1024
-    const int cnt = DCH / 32 * bits;                    // words of the chunk, a multiple of 4
-    const uint4* src = (const uint4*)(row + w0);
-    for (int q = threadIdx.x; q < cnt / 4; q += DBX) {
-        const uint4 v = src[q];
-        lb[4 * q] = v.x;
-        lb[4 * q + 1] = v.y;
-        lb[4 * q + 2] = v.z;
-        lb[4 * q + 3] = v.w;
-    }
-    if (threadIdx.x == 0) lb[cnt] = row[w0 + cnt];
-}
-__device__ __forceinline__ uint32_t unpack_at(const uint32_t* lb, uint32_t bit, int bits) {
-    const uint32_t w = bit >> 5, off = bit & 31;
-    const uint64_t v = ((uint64_t)lb[w + 1] << 32 | lb[w]) >> off;
-    return bits == 32 ? (uint32_t)v : (uint32_t)v & ((1u << bits) - 1u);
+// Wave-level ordering of LDS traffic between the lanes of one wave (no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// mode 0: ks_dot (dense kb / ka per key, [digit][prime id][N]); mode 1: ks_dot_key (KeyTab)
-__global__ void __launch_bounds__(DBX) dot_k(KsArgs A, KeyTab T, int logn, int mode) {
-    __shared__ uint32_t l0[DCH], l1[DCH];
-    __shared__ uint32_t lb[DCH + 4];
-    const int r = blockIdx.z;
+constexpr int KW = 4;               // waves per workgroup: each takes one key at a time
+constexpr int KBX = DBX * KW;       // threads per workgroup
+constexpr int MAXD = 3;             // digits staged in LDS (more are read from global memory)
+constexpr int QCAP = 1536;          // rejected-word queue entries per wave (>= 1024 free before every digit)
+
+struct DotLds {
+    uint32_t D[MAXD][DCH];   // the chunk's digit operands D_d (shared by every key)
+    uint32_t c0[DCH];        // the chunk's c0 (mode 1: times P mod q_t; mode 2: added)
+    struct Wave {
+        uint64_t ex[DCH];    // D_d a_d of the redrawn words (64-bit LDS atomics); then the scatter buffers
+        uint32_t q[QCAP];    // rejected words: digit << 16 | slot
+        uint32_t qn;
+    } w[KW];
+};
+
+struct DotCtx {
+    const KsArgs* A;
+    int c, dt, t;
+    size_t trow;
+    uint32_t chunk0;
+    __device__ __forceinline__ const uint32_t* dptr(int d) const {
+        return d == dt ? (const uint32_t*)A->c1 + c * A->ct_stride + trow
+                       : (const uint32_t*)A->modup + c * A->mu_ct_stride + d * A->mu_digit_stride + trow;
+    }
+};
+
+// Redraw the queued words of one wave: item = digit << 16 | slot; each lane takes items and adds D_d a_d (the
+// accepted attempt of the word, attempts t = 1..15 at block + t N/16) to the slot's 64-bit sum.
+__device__ __forceinline__ void drain(DotLds& L, DotLds::Wave& W, const DotCtx& X, int lane, const uint32_t (&seed)[8],
+                                      const Expander& ex, uint32_t n16) {
+    wave_sync();
+    const uint32_t nq = W.qn;
+    for (uint32_t i = lane; i < nq; i += DBX) {
+        const uint32_t it = W.q[i], d = it >> 16, sl = it & 0xFFFF;
+        const uint32_t ctr = (X.chunk0 + sl) >> 4;
+        uint32_t v = 0;
+        for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+            v = chacha12_word(seed, ctr + (uint32_t)tt * n16, d, ex.p, TAG_KSKA, (int)(sl & 15));
+            if (v < ex.mp) break;
+        }
+        const uint32_t xd = d < (uint32_t)MAXD ? L.D[d][sl] : X.dptr((int)d)[X.chunk0 + sl];
+        atomicAdd((unsigned long long*)&W.ex[sl], (unsigned long long)((uint64_t)xd * ex.red(v)));
+    }
+    wave_sync();
+    if (lane == 0) W.qn = 0;
+    wave_sync();
+}
+
+// mode 0: ks_dot (dense kb / ka per key, [digit][prime id][N]); mode 1: ks_dot_key (KeyTab). WIDE: more than 4 digits
+// (the 64-bit sums reduced every 3 digits). grid (N / 1024, rows, key groups), KW waves; each workgroup stages its
+// chunk's D and c0 once, then wave w takes the group's keys w, w + KW, ...
+template <bool WIDE>
+__global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int mode) {
+    __shared__ DotLds L;
+    const int lane = threadIdx.x & (DBX - 1), wv = threadIdx.x / DBX;
     const int t = (int)A.rows[blockIdx.y];
     const PrimeConst& q = A.pr[t];
     const uint32_t p = (uint32_t)q.p;
     const Red red(q);
     const Expander ex(p);
     const uint32_t n16 = (1u << logn) >> 4;
+    const uint32_t mask2n = (2u << logn) - 1;
     const uint32_t chunk0 = blockIdx.x * DCH;
-    const uint32_t s0 = chunk0 + threadIdx.x * DS;
-    const int dt = t < A.nq ? A.digit_of[t] : -1;
-    const size_t trow = (size_t)t << logn;
+    const uint32_t s0 = chunk0 + lane * DS;
     const int slot = mode == 1 ? slot_of(T, t, A.nq) : t;
-    const bool packed = mode == 1 && T.bits > 0;
-    uint32_t seed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (mode == 1 && T.nregen > 0) {
-        const uint32_t* sp = T.seed[r];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) seed[i] = sp[i];
-    }
-    const uint32_t kexp = A.autok[r];
     const int m0 = A.c0_mode & 3;
     const bool acc_out = (A.c0_mode & PC_KS_ACC) != 0;
+    const int ndig = A.ndig;
+    const int kpg = (A.R + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int r_lo = blockIdx.z * kpg, r_hi = min(A.R, r_lo + kpg);
+    const bool pc0 = m0 == 1 && t < A.nq;
+    const bool fold_c0 = pc0 && ndig <= 3;  // ndig + 1 products of (p - 1)^2 < 2^62 stay below 2^64
+    const uint32_t pm = pc0 ? ((const uint32_t*)A.pmod)[t] : 0;
+    const uint32_t pms = pc0 ? ((const uint32_t*)A.pmods)[t] : 0;
+    const uint32_t bs0 = brev_n(s0, logn);
+    DotLds::Wave& W = L.w[wv];
+    DotCtx X{&A, 0, t < A.nq ? A.digit_of[t] : -1, t, (size_t)t << logn, chunk0};
     for (int c = 0; c < A.K; ++c) {
-        uint64_t s0a[DS], s1a[DS];
-        uint32_t w0[DS], w1[DS];
+        X.c = c;
+        __syncthreads();
+        // stage D_d (d < MAXD) and c0 of the chunk: coalesced 16-byte loads by the whole workgroup
+        for (int d = 0; d < min(ndig, MAXD); ++d) {
+            const uint4* D = (const uint4*)(X.dptr(d) + chunk0);
+            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i] = D[i];
+        }
+        if (m0) {
+            const uint4* C0 = (const uint4*)((const uint32_t*)A.c0 + c * A.ct_stride + X.trow + chunk0);
+            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i] = C0[i];
+        }
+        __syncthreads();
+        for (int r = r_lo + wv; r < r_hi; r += KW) {
+            uint32_t seed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (mode == 1 && T.nregen > 0) {
+                const uint32_t* sp = T.seed[r];
 #pragma unroll
-        for (int k = 0; k < DS; ++k) s0a[k] = s1a[k] = 0, w0[k] = w1[k] = 0;
-        for (int d = 0; d < A.ndig; ++d) {
-            const uint32_t* D = d == dt ? (const uint32_t*)A.c1 + c * A.ct_stride + trow
-                                        : (const uint32_t*)A.modup + c * A.mu_ct_stride + d * A.mu_digit_stride + trow;
-            uint32_t x[DS], b[DS], a[DS];
-            ld16(D + s0, x);
-            if (mode == 0) {
-                ld16((const uint32_t*)A.kb[r] + d * A.key_digit_stride + trow + s0, b);
-            } else if (!packed) {
-                ld16((const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words + s0, b);
+                for (int i = 0; i < 8; ++i) seed[i] = sp[i];
+            }
+#pragma unroll
+            for (int k = 0; k < DS; ++k) W.ex[lane * DS + k] = 0;
+            if (lane == 0) W.qn = 0;
+            wave_sync();
+            uint64_t s0a[DS], s1a[DS];
+            uint32_t part0[WIDE ? DS : 1], part1[WIDE ? DS : 1];
+#pragma unroll
+            for (int k = 0; k < (WIDE ? DS : 1); ++k) part0[k] = part1[k] = 0;
+            if (fold_c0) {
+#pragma unroll
+                for (int k = 0; k < DS; ++k) s0a[k] = (uint64_t)L.c0[lane * DS + k] * pm;
             } else {
-                __syncthreads();
-                stage_packed((const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words, chunk0, T.bits, lb);
-                __syncthreads();
 #pragma unroll
-                for (int k = 0; k < DS; ++k) b[k] = unpack_at(lb, (threadIdx.x * DS + k) * (uint32_t)T.bits, T.bits);
+                for (int k = 0; k < DS; ++k) s0a[k] = 0;
             }
-            if (mode == 1 && d < T.nregen) kska16(seed, s0, (uint32_t)d, ex, n16, a);
-            else ld16((const uint32_t*)A.ka[r] + d * A.key_digit_stride + trow + s0, a);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) s1a[k] = 0;
+            for (int d = 0; d < ndig; ++d) {
+                uint32_t b[DS], a[DS];
+                if (mode == 0) {
+                    ld16((const uint32_t*)A.kb[r] + d * A.key_digit_stride + X.trow + s0, b);
+                } else if (T.bits == 0) {
+                    ld16((const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words + s0, b);
+                } else {
+                    // packed b: the lane's 16 values sit in words [bit0 / 32, bit0 / 32 + 16] of the row's stream
+                    const uint32_t* row = (const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words;
+                    const uint32_t bit0 = s0 * (uint32_t)T.bits;
+                    const uint32_t msk = T.bits == 32 ? 0xFFFFFFFFu : (1u << T.bits) - 1u;
+#pragma unroll
+                    for (int k = 0; k < DS; ++k) {
+                        const uint32_t bit = bit0 + k * (uint32_t)T.bits;
+                        const uint32_t w = bit >> 5;
+                        b[k] = __builtin_amdgcn_alignbit(row[w + 1], row[w], bit & 31) & msk;
+                    }
+                }
+                if (mode == 1 && d < T.nregen) {
+                    chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
+                    uint32_t rej = 0;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
+                    if (rej) {
+                        // queued (the slot's sum gets D_d a_d when the wave drains the queue); counts as 0 here
+                        uint32_t m = rej, i = atomicAdd(&W.qn, (uint32_t)__builtin_popcount(rej));
+                        while (m) {
+                            const int j = __builtin_ctz(m);
+                            m &= m - 1;
+                            W.q[i++] = (uint32_t)d << 16 | (lane * DS + j);
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) a[j] = (rej >> j) & 1 ? 0 : ex.red(a[j]);
+                } else {
+                    ld16((const uint32_t*)A.ka[r] + d * A.key_digit_stride + X.trow + s0, a);
+                }
+                uint32_t x[DS];
+                if (d < MAXD) ld16(L.D[d] + lane * DS, x);
+                else ld16(X.dptr(d) + s0, x);
+#pragma unroll
+                for (int k = 0; k < DS; ++k) {
+                    s0a[k] += (uint64_t)x[k] * b[k];
+                    s1a[k] += (uint64_t)x[k] * a[k];
+                }
+                if (WIDE && d % 3 == 2 && d + 1 < ndig) {
+#pragma unroll
+                    for (int k = 0; k < DS; ++k) {
+                        part0[k] = addm(part0[k], red(s0a[k]), p);
+                        part1[k] = addm(part1[k], red(s1a[k]), p);
+                        s0a[k] = s1a[k] = 0;
+                    }
+                }
+                // room for a whole digit's words before the next one (wave-uniform: qn is shared)
+                wave_sync();
+                if (W.qn > (uint32_t)(QCAP - DCH)) drain(L, W, X, lane, seed, ex, n16);
+            }
+            drain(L, W, X, lane, seed, ex, n16);
+            uint32_t r0[DS], r1[DS];
 #pragma unroll
             for (int k = 0; k < DS; ++k) {
-                const uint64_t pb = (uint64_t)x[k] * b[k], pa = (uint64_t)x[k] * a[k];
-                s0a[k] += pb;
-                w0[k] += s0a[k] < pb;
-                s1a[k] += pa;
-                w1[k] += s1a[k] < pa;
+                const uint64_t e = W.ex[lane * DS + k];
+                if (WIDE) {
+                    r0[k] = addm(part0[k], red(s0a[k]), p);
+                    r1[k] = addm(addm(part1[k], red(s1a[k]), p), red(e), p);
+                } else {
+                    r0[k] = red(s0a[k]);
+                    r1[k] = red(s1a[k] + e);  // every (slot, digit) counted once: at most ndig <= 4 products
+                }
             }
-        }
-        uint32_t r0[DS], r1[DS];
+            if ((pc0 && !fold_c0) || m0 == 2) {
 #pragma unroll
-        for (int k = 0; k < DS; ++k) {
-            r0[k] = red.red96(s0a[k], w0[k]);
-            r1[k] = red.red96(s1a[k], w1[k]);
-        }
-        if (m0 == 1 && t < A.nq) {
-            uint32_t cz[DS];
-            ld16((const uint32_t*)A.c0 + c * A.ct_stride + trow + s0, cz);
-            const uint32_t pm = ((const uint32_t*)A.pmod)[t], pms = ((const uint32_t*)A.pmods)[t];
-#pragma unroll
-            for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], shoup(cz[k], pm, pms, p), p);
-        } else if (m0 == 2) {
-            uint32_t cz[DS];
-            ld16((const uint32_t*)A.c0 + c * A.ct_stride + trow + s0, cz);
-#pragma unroll
-            for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], cz[k], p);
-        }
-        uint32_t* o0 = (uint32_t*)A.out0 + c * A.out_ct_stride + r * A.out_rot_stride + trow;
-        uint32_t* o1 = (uint32_t*)A.out1 + c * A.out_ct_stride + r * A.out_rot_stride + trow;
-        if (kexp == 1 && !acc_out) {
-            st16(o0 + s0, r0);
-            st16(o1 + s0, r1);
-            continue;
-        }
-        // scatter by sigma_k inside the chunk through LDS, then coalesced stores of the output chunk
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < DS; ++k) {
-            const uint32_t o = automorph_slot(kexp, s0 + k, logn) & (DCH - 1);
-            l0[o] = r0[k];
-            l1[o] = r1[k];
-        }
-        __syncthreads();
-        const uint32_t ob = (automorph_slot(kexp, chunk0, logn) & ~(uint32_t)(DCH - 1)) + threadIdx.x * DS;
-        uint32_t v0[DS], v1[DS];
-#pragma unroll
-        for (int k = 0; k < DS; ++k) {
-            v0[k] = l0[threadIdx.x * DS + k];
-            v1[k] = l1[threadIdx.x * DS + k];
-        }
-        if (acc_out) {
-            uint32_t e0[DS], e1[DS];
-            ld16(o0 + ob, e0);
-            ld16(o1 + ob, e1);
+                for (int k = 0; k < DS; ++k) {
+                    const uint32_t cz = L.c0[lane * DS + k];
+                    r0[k] = addm(r0[k], m0 == 2 ? cz : shoup(cz, pm, pms, p), p);
+                }
+            }
+            const uint32_t kexp = A.autok[r];
+            uint32_t* o0 = (uint32_t*)A.out0 + c * A.out_ct_stride + r * A.out_rot_stride + X.trow;
+            uint32_t* o1 = (uint32_t*)A.out1 + c * A.out_ct_stride + r * A.out_rot_stride + X.trow;
+            if (kexp == 1 && !acc_out) {
+                st16(o0 + s0, r0);
+                st16(o1 + s0, r1);
+                continue;
+            }
+            // sigma_k: slot s0 + j goes to brev((((2 brev(s0) + 1) + 2 brev(j)) k mod 2N) >> 1); brev(j) of the low 4
+            // bits is brev4(j) 2^(logn - 4), so the 16 targets are one product and 16 uniform offsets apart
+            uint32_t* l0 = (uint32_t*)W.ex;
+            uint32_t* l1 = l0 + DCH;
+            wave_sync();
+            const uint32_t cb = ((2 * bs0 + 1) * kexp) & mask2n;
+            const uint32_t step = (kexp << (logn - 3)) & mask2n;
 #pragma unroll
             for (int k = 0; k < DS; ++k) {
-                v0[k] = addm(v0[k], e0[k], p);
-                v1[k] = addm(v1[k], e1[k], p);
+                const uint32_t b4 = ((k & 1) << 3) | ((k & 2) << 1) | ((k & 4) >> 1) | ((k & 8) >> 3);
+                const uint32_t o = brev_n(((cb + b4 * step) & mask2n) >> 1, logn) & (DCH - 1);
+                l0[o] = r0[k];
+                l1[o] = r1[k];
             }
+            wave_sync();
+            const uint32_t ob = (automorph_slot(kexp, chunk0, logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
+            uint32_t v0[DS], v1[DS];
+            ld16(l0 + lane * DS, v0);
+            ld16(l1 + lane * DS, v1);
+            if (acc_out) {
+                uint32_t e0[DS], e1[DS];
+                ld16(o0 + ob, e0);
+                ld16(o1 + ob, e1);
+#pragma unroll
+                for (int k = 0; k < DS; ++k) {
+                    v0[k] = addm(v0[k], e0[k], p);
+                    v1[k] = addm(v1[k], e1[k], p);
+                }
+            }
+            st16(o0 + ob, v0);
+            st16(o1 + ob, v1);
+            wave_sync();
         }
-        st16(o0 + ob, v0);
-        st16(o1 + ob, v1);
     }
 }
 
@@ -195,8 +305,13 @@ int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     if ((a.c0_mode & 3) == 1 && (!a.c0 || !a.pmod || !a.pmods)) return -1;
     if ((a.c0_mode & 3) == 2 && !a.c0) return -1;
     if ((a.c0_mode & 3) == 3) return -1;
-    dim3 grid((1 << LOGN) / DCH, a.nrows, a.R);
-    hipLaunchKernelGGL(dot_k, grid, dim3(DBX), 0, (hipStream_t)s, a, key, LOGN, mode);
+    // key groups: enough workgroups to fill the chip, each group sharing one staging of D
+    const int chunks = (1 << LOGN) / DCH;
+    int groups = 1;
+    while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
+    dim3 grid(chunks, a.nrows, groups);
+    if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
+    else hipLaunchKernelGGL(dot_k<false>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     return launch_rc();
 }
 

@@ -149,6 +149,21 @@ class Context:
     def moddown(self, ext, top, out, stream):
         check(LIB.pcx_moddown(self.h, ext.addr(), top, out.addr(), stream.h), "moddown")
 
+    STAGES = ("modup_intt", "modup_bconv", "modup_ntt", "dot", "md_intt", "md_bconv", "md_ntt")
+
+    def timing(self, max_stages):
+        """Record device time per stage (0 turns it off)."""
+        check(LIB.pcx_timing(self.h, max_stages), "timing")
+
+    def timing_read(self):
+        """{stage: (total ms, launches)} of the stages recorded since timing() (after a sync)."""
+        out = {}
+        for i, name in enumerate(self.STAGES):
+            ms, n = C.c_double(), C.c_int()
+            check(LIB.pcx_timing_read(self.h, i, C.byref(ms), C.byref(n)), "timing_read")
+            out[name] = (ms.value, n.value)
+        return out
+
     def rotate(self, keys, r, ct, top, out, stream):
         check(LIB.pcx_rotate(self.h, keys.h, r, ct.addr(), top, out.addr(), stream.h), "rotate")
 

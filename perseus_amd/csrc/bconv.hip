@@ -46,76 +46,9 @@ __device__ __forceinline__ uint64_t exact_u(const BconvJob& j, const double* rb,
     return (uint64_t)floor(v + 0.5);
 }
 
-// One workgroup = one job x 512 coefficients (2 per thread). A job's record lives in device memory, so the source
-// count is read here: jobs of at most 16 sources keep the y of their 4 coefficients in registers, wider jobs
-// (bconv_wide, up to 48 at u32 words) re-read their sources per target (L1/L2 resident).
-__device__ __forceinline__ void job_reg(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
-                                        uint32_t* dst, uint32_t c0, int logn) {
-    // the sources of the 4 coefficients stay in registers: the loops are unrolled to 16 and predicated on ns
-    uint32_t y[MAX_REG_SRC * V];
-#pragma unroll
-    for (int i = 0; i < MAX_REG_SRC; ++i) {
-        if (i < P.ns) {
-            const uint2 x = *(const uint2*)(src + ((size_t)P.src_row(i) << logn) + c0);
-            uint32_t v[V] = {x.x, x.y};
-            if (!j.prescaled) {
-                const Red red(A.pr[P.src_prime(i)]);
-                const uint32_t pre = P.pre(i);
-#pragma unroll
-                for (int k = 0; k < V; ++k) v[k] = red.mul(v[k], pre);
-            }
-#pragma unroll
-            for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
-        } else {
-#pragma unroll
-            for (int k = 0; k < V; ++k) y[i * V + k] = 0;
-        }
-    }
-    uint64_t u[V] = {0, 0};
-    const uint32_t* bmod = nullptr;
-    if (j.exact) {
-        const double* rb = exact_rb((const uint32_t*)A.pool, j);
-        bmod = (const uint32_t*)(rb + j.nsrc);
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-            if (j.exact == 2) {
-                const uint64_t ns = j.nsrc;
-                u[k] = (ns >> 1) + ((ns & 1) & (((c0 + k) * 0x9E3779B1u) >> 31));
-            } else {
-                double v = 0.0;
-#pragma unroll
-                for (int i = 0; i < MAX_REG_SRC; ++i)
-                    if (i < P.ns) v = __fma_rn((double)y[i * V + k], rb[i], v);
-                u[k] = (uint64_t)floor(v + 0.5);
-            }
-        }
-    }
-    for (int t = 0; t < P.nt; ++t) {
-        const Red red(A.pr[P.tgt_prime(t)]);
-        uint64_t acc[V] = {0, 0};
-        uint32_t wraps[V] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < MAX_REG_SRC; ++i) {
-            if (i < P.ns) {
-                const uint32_t m = P.m(i, t);
-#pragma unroll
-                for (int k = 0; k < V; ++k) {
-                    const uint64_t pr = (uint64_t)y[i * V + k] * m;
-                    acc[k] += pr;
-                    wraps[k] += acc[k] < pr;
-                }
-            }
-        }
-        uint32_t r[V];
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-            r[k] = red.red96(acc[k], wraps[k]);
-            if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * bmod[t]), red.p);
-        }
-        *(uint2*)(dst + ((size_t)P.tgt_row(t) << logn) + c0) = make_uint2(r[0], r[1]);
-    }
-}
-
+// One workgroup = one job x 512 coefficients (2 per thread). A job's record lives in device memory, so its size is
+// read here: jobs of at most 16 sources keep the sources of their 2 coefficients in registers and the job's tables in
+// LDS; wider jobs (bconv_wide, up to 48 sources at u32 words) re-read their sources per target (L1/L2 resident).
 __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
                                          uint32_t* dst, uint32_t c, int logn) {
     auto yv = [&](int i) {
@@ -152,16 +85,115 @@ __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, 
     }
 }
 
+// The job's tables in LDS (jobs of at most 16 sources and MAXT targets): M transposed and zero-padded to 16 sources,
+// so a target's column is 4 broadcast 16-byte reads; each target's reduction constants; the sources' rows and pre.
+constexpr int MAXT = 64;
+struct JobLds {
+    uint32_t mt[MAXT][MAX_REG_SRC];
+    uint32_t trow[MAXT];
+    uint32_t tc[MAXT][4];  // p, 2^32 mod p, its Shoup companion, floor(2^32 / p)
+    double rb[MAX_REG_SRC];
+    uint32_t bmod[MAXT];
+};
+
+__device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
+                                        const uint32_t* src, uint32_t* dst, uint32_t c0, int logn) {
+    uint32_t y[MAX_REG_SRC * V];
+#pragma unroll
+    for (int i = 0; i < MAX_REG_SRC; ++i) {
+        if (i < P.ns) {
+            const uint2 x = *(const uint2*)(src + ((size_t)P.src_row(i) << logn) + c0);
+            uint32_t v[V] = {x.x, x.y};
+            if (!j.prescaled) {
+                const Red red(A.pr[P.src_prime(i)]);
+                const uint32_t pre = P.pre(i);
+#pragma unroll
+                for (int k = 0; k < V; ++k) v[k] = red.mul(v[k], pre);
+            }
+#pragma unroll
+            for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; ++k) y[i * V + k] = 0;
+        }
+    }
+    uint64_t u[V] = {0, 0};
+    if (j.exact) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            if (j.exact == 2) {
+                const uint64_t ns = j.nsrc;
+                u[k] = (ns >> 1) + ((ns & 1) & (((c0 + k) * 0x9E3779B1u) >> 31));
+            } else {
+                double v = 0.0;
+#pragma unroll
+                for (int i = 0; i < MAX_REG_SRC; ++i)
+                    if (i < P.ns) v = __fma_rn((double)y[i * V + k], S.rb[i], v);
+                u[k] = (uint64_t)floor(v + 0.5);
+            }
+        }
+    }
+    const int ng = (P.ns + 3) >> 2;  // groups of 4 sources (M zero-padded)
+    for (int t = 0; t < P.nt; ++t) {
+        const Red red(S.tc[t][0], S.tc[t][1], S.tc[t][2], S.tc[t][3]);
+        uint64_t acc[V] = {0, 0};
+        uint32_t wraps[V] = {0, 0};
+#pragma unroll
+        for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
+            if (g < ng) {
+                const uint4 m4 = *(const uint4*)&S.mt[t][4 * g];
+                const uint32_t mv[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                    for (int k = 0; k < V; ++k) {
+                        const uint64_t pr = (uint64_t)y[(4 * g + e) * V + k] * mv[e];
+                        acc[k] += pr;
+                        wraps[k] += acc[k] < pr;
+                    }
+                }
+            }
+        }
+        uint32_t r[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            r[k] = red.red96(acc[k], wraps[k]);
+            if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * S.bmod[t]), red.p);
+        }
+        *(uint2*)(dst + ((size_t)S.trow[t] << logn) + c0) = make_uint2(r[0], r[1]);
+    }
+}
+
 __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
+    __shared__ JobLds S;
     const BconvJob j = A.jobs[blockIdx.y];
     const Pool P{(const uint32_t*)A.pool + j.pool_off, (int)j.nsrc, (int)j.ntgt};
     const uint32_t c0 = blockIdx.x * PER_WG + threadIdx.x * V;
-    if (c0 >= (1u << logn) || P.ns < 1) return;
+    if (P.ns < 1) return;
     const uint32_t* src = (const uint32_t*)A.src + ((size_t)j.src_off << logn);
     uint32_t* dst = (uint32_t*)A.dst + ((size_t)j.dst_off << logn);
-    if (P.ns <= MAX_REG_SRC) {
-        job_reg(A, j, P, src, dst, c0, logn);
-    } else {
+    if (P.ns <= MAX_REG_SRC && P.nt <= MAXT) {
+        for (int e = threadIdx.x; e < MAXT * MAX_REG_SRC; e += BX) {
+            const int t = e / MAX_REG_SRC, i = e % MAX_REG_SRC;
+            S.mt[t][i] = (t < P.nt && i < P.ns) ? P.m(i, t) : 0;
+        }
+        for (int t = threadIdx.x; t < P.nt; t += BX) {
+            const PrimeConst& q = A.pr[P.tgt_prime(t)];
+            S.trow[t] = P.tgt_row(t);
+            S.tc[t][0] = (uint32_t)q.p;
+            S.tc[t][1] = (uint32_t)q.split;
+            S.tc[t][2] = (uint32_t)(q.split >> 32);
+            S.tc[t][3] = (uint32_t)(q.mu_lo >> 32);
+        }
+        if (j.exact) {
+            const double* rb = exact_rb((const uint32_t*)A.pool, j);
+            const uint32_t* bmod = (const uint32_t*)(rb + j.nsrc);
+            for (int i = threadIdx.x; i < P.ns; i += BX) S.rb[i] = rb[i];
+            for (int t = threadIdx.x; t < P.nt; t += BX) S.bmod[t] = bmod[t];
+        }
+        __syncthreads();
+        if (c0 < (1u << logn)) job_lds(A, j, P, S, src, dst, c0, logn);
+    } else if (c0 < (1u << logn)) {
         for (int k = 0; k < V; ++k) job_wide(A, j, P, src, dst, c0 + k, logn);
     }
 }

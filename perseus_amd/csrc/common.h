@@ -157,6 +157,14 @@ __device__ __forceinline__ void st16(uint32_t* p, const uint32_t (&v)[16]) {
     for (int i = 0; i < 4; ++i) q[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
 }
 
+// Workgroups of a launch are dispatched round-robin over the 8 XCDs (workgroup i to XCD i mod 8), each XCD with its own
+// L2. Renumbering so that XCD k runs the contiguous range of logical blocks [k q + min(k, r), ...) (q, r = nblocks
+// div / mod 8) keeps neighbouring blocks, which share cache lines and twiddle tables, on one L2.
+__device__ __forceinline__ uint32_t xcd_block(uint32_t bid, uint32_t nblocks) {
+    const uint32_t xcd = bid & 7, slot = bid >> 3, q = nblocks >> 3, r = nblocks & 7;
+    return xcd * q + (xcd < r ? xcd : r) + slot;
+}
+
 inline int launch_rc() {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : (int)e;

@@ -196,9 +196,12 @@ struct Level {
     Rows mu_ntt;              // the targets in the digit workspace
     uint32_t* ks_rows = nullptr;
     int nks = 0;
-    Rows md_intt;             // [c < k_rot][part][j < kp]: ext P rows, es = N^-1 pre_j
-    Bconv md_bconv;           // [c][part]: P -> Q rows 0..top
-    Rows md_ntt;              // [c][part][t <= top]
+    // ModDown tables per chunk size m = 1..k_rot (index m - 1), prime-major so that consecutive rows share one
+    // prime's twiddle table in L2: INTT of the ext P rows [j < kp][c < m][part] (es = N^-1 pre_j) and NTT of the
+    // conversion's Q rows [t <= top][c < m][part]
+    std::vector<Rows> md_intt;
+    Bconv md_bconv;           // [c][part]: P -> Q rows 0..top (a prefix per m)
+    std::vector<Rows> md_ntt;
 };
 
 }  // namespace
@@ -334,12 +337,15 @@ int build_level(pcx_ctx* c, int top, Level& L) {
             for (int t = 0; t <= top; ++t)
                 if (std::find(digs[d].begin(), digs[d].end(), (uint32_t)t) == digs[d].end()) j.tgt.push_back(t);
             for (int k = 0; k < c->kp; ++k) j.tgt.push_back(c->nq + k);
-            for (uint32_t t : j.tgt) {
-                roff.push_back(j.dst_off + t);
-                rp.push_back((int32_t)t);
-            }
             specs.push_back(j);
         }
+        // the targets' NTT rows, prime-major (rows of one prime share its twiddle table)
+        for (int t = 0; t < c->rows; ++t)
+            for (int d = 0; d < L.ndig; ++d)
+                if (std::find(specs[d].tgt.begin(), specs[d].tgt.end(), (uint32_t)t) != specs[d].tgt.end()) {
+                    roff.push_back(specs[d].dst_off + t);
+                    rp.push_back(t);
+                }
         L.mu_bconv.build(c->dev, c->primes, specs);
         if (int e = fill_rows(c->dev, L.mu_ntt, roff, rp, nullptr, nullptr)) return e;
     }
@@ -351,38 +357,48 @@ int build_level(pcx_ctx* c, int top, Level& L) {
         L.nks = (int)ks.size();
         L.ks_rows = c->dev.upload(ks);
     }
-    // ModDown over k_rot extended ciphertexts [c][part]
+    // ModDown over up to k_rot extended ciphertexts
     {
         std::vector<uint64_t> sp;
         for (int k = 0; k < c->kp; ++k) sp.push_back(c->primes[c->nq + k]);
         std::vector<uint32_t> pre = pre_factors(sp);
-        std::vector<uint32_t> roff, es, roff2;
-        std::vector<int32_t> rp, rp2;
         std::vector<JobSpec> specs;
         for (int ct = 0; ct < c->k_rot; ++ct)
             for (int part = 0; part < 2; ++part) {
                 const uint32_t base = (uint32_t)((2 * ct + part) * c->rows);
                 JobSpec j;
                 j.src_off = j.dst_off = base;
-                for (int k = 0; k < c->kp; ++k) {
-                    const int id = c->nq + k;
-                    uint64_t p = c->primes[id];
-                    roff.push_back(base + id);
-                    rp.push_back(id);
-                    es.push_back((uint32_t)mulmod(invmod(n % p, p), pre[k], p));
-                    j.src.push_back(id);
-                }
-                for (int t = 0; t <= top; ++t) {
-                    j.tgt.push_back(t);
-                    roff2.push_back(base + t);
-                    rp2.push_back(t);
-                }
+                for (int k = 0; k < c->kp; ++k) j.src.push_back(c->nq + k);
+                for (int t = 0; t <= top; ++t) j.tgt.push_back(t);
                 specs.push_back(j);
             }
-        std::vector<uint32_t> est = scale_table(c->primes, rp, es);
-        if (int e = fill_rows(c->dev, L.md_intt, roff, rp, nullptr, &est)) return e;
         L.md_bconv.build(c->dev, c->primes, specs);
-        if (int e = fill_rows(c->dev, L.md_ntt, roff2, rp2, nullptr, nullptr)) return e;
+        L.md_intt.resize(c->k_rot);
+        L.md_ntt.resize(c->k_rot);
+        for (int m = 1; m <= c->k_rot; ++m) {
+            std::vector<uint32_t> roff, es, roff2;
+            std::vector<int32_t> rp, rp2;
+            for (int k = 0; k < c->kp; ++k) {
+                const int id = c->nq + k;
+                const uint64_t p = c->primes[id];
+                const uint32_t sc = (uint32_t)mulmod(invmod(n % p, p), pre[k], p);
+                for (int ct = 0; ct < m; ++ct)
+                    for (int part = 0; part < 2; ++part) {
+                        roff.push_back((uint32_t)((2 * ct + part) * c->rows + id));
+                        rp.push_back(id);
+                        es.push_back(sc);
+                    }
+            }
+            for (int t = 0; t <= top; ++t)
+                for (int ct = 0; ct < m; ++ct)
+                    for (int part = 0; part < 2; ++part) {
+                        roff2.push_back((uint32_t)((2 * ct + part) * c->rows + t));
+                        rp2.push_back(t);
+                    }
+            std::vector<uint32_t> est = scale_table(c->primes, rp, es);
+            if (int e = fill_rows(c->dev, L.md_intt[m - 1], roff, rp, nullptr, &est)) return e;
+            if (int e = fill_rows(c->dev, L.md_ntt[m - 1], roff2, rp2, nullptr, nullptr)) return e;
+        }
     }
     return c->dev.err;
 }
@@ -494,9 +510,10 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
 int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
     const Level* L = level(c, top);
     if (!L || m < 1 || m > c->k_rot) return -1;
-    NttArgs a = ntt_args(c, ext, L->md_intt, m * 2 * c->kp);
-    a.es = L->md_intt.es;
-    a.ess = L->md_intt.es + L->md_intt.n;
+    const Rows& ri = L->md_intt[m - 1];
+    NttArgs a = ntt_args(c, ext, ri, ri.n);
+    a.es = ri.es;
+    a.ess = ri.es + ri.n;
     {
         Stage st(c, 4, s);
         if (int e = c->tab->ntt_inv(&a, s)) return e;
@@ -514,7 +531,8 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
         Stage st(c, 5, s);
         if (int e = c->tab->bconv(&b, s)) return e;
     }
-    NttArgs f = ntt_args(c, c->conv, L->md_ntt, m * 2 * (top + 1));
+    const Rows& rn = L->md_ntt[m - 1];
+    NttArgs f = ntt_args(c, c->conv, rn, rn.n);
     f.epi = 1;
     f.eout = out;
     f.ex = ext;

@@ -295,6 +295,205 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
     }
 }
 
+// The hot case of the dot, specialised: one ciphertext, dense b through a KeyTab, every digit's a regenerated, NDIG
+// (<= 3) live digits unrolled. D and c0 are staged once per workgroup as in dot_k. A lane that meets rejected ChaCha
+// words appends them to its wave's queue and keeps the queue position (atomic base) of each digit; the whole wave then
+// redraws the queued words at once, writing each accepted value back into its queue entry, and the owner adds D_d a_d
+// of its words from there. The queue doubles as the scatter buffer of the automorphism, so a wave needs 8 KB of LDS and
+// three workgroups fit on a CU.
+constexpr int FQCAP = 2 * DCH;  // queue entries per wave (= the two 1024-word scatter buffers)
+
+struct FastLds {
+    uint32_t D[MAXD][DCH];
+    uint32_t c0[DCH];
+    struct Wave {
+        uint32_t q[FQCAP];
+        uint32_t qn;
+    } w[KW];
+};
+
+template <int NDIG>
+__global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, int logn) {
+    static_assert(NDIG >= 1 && NDIG <= MAXD, "digits staged in LDS");
+    __shared__ FastLds L;
+    // the wave index is uniform across the wave: in scalar registers, so are its key, seed and row pointers
+    const int lane = threadIdx.x & (DBX - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / DBX);
+    const int t = (int)A.rows[blockIdx.y];
+    const PrimeConst& q = A.pr[t];
+    const uint32_t p = (uint32_t)q.p;
+    const Red red(q);
+    const Expander ex(p);
+    const uint32_t n16 = (1u << logn) >> 4;
+    const uint32_t mask2n = (2u << logn) - 1;
+    const uint32_t chunk0 = blockIdx.x * DCH;
+    const uint32_t s0 = chunk0 + lane * DS;
+    const int slot = slot_of(T, t, A.nq);
+    const int m0 = A.c0_mode & 3;
+    const bool acc_out = (A.c0_mode & PC_KS_ACC) != 0;
+    const int kpg = (A.R + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int r_lo = blockIdx.z * kpg, r_hi = min(A.R, r_lo + kpg);
+    const bool pc0 = m0 == 1 && t < A.nq;
+    const uint32_t pm = pc0 ? ((const uint32_t*)A.pmod)[t] : 0;
+    const uint32_t bs0 = brev_n(s0, logn);
+    auto& W = L.w[wv];
+    DotCtx X{&A, 0, t < A.nq ? A.digit_of[t] : -1, t, (size_t)t << logn, chunk0};
+#pragma unroll
+    for (int d = 0; d < NDIG; ++d) {
+        const uint4* D = (const uint4*)(X.dptr(d) + chunk0);
+        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i] = D[i];
+    }
+    if (m0) {
+        const uint4* C0 = (const uint4*)((const uint32_t*)A.c0 + X.trow + chunk0);
+        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i] = C0[i];
+    }
+    __syncthreads();
+    for (int r = r_lo + wv; r < r_hi; r += KW) {
+        const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)slot * T.row_words + s0;
+        const size_t dstride = (size_t)T.srows * T.row_words;
+        uint32_t seed[8];
+        const uint32_t* sp = T.seed[r];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) seed[i] = sp[i];
+        if (lane == 0) W.qn = 0;
+        wave_sync();
+        // s1 = sum_d D_d a_d, a regenerated (one ChaCha12 block per lane and digit)
+        uint64_t acc[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) acc[k] = 0;
+        uint32_t rejd[NDIG], based[NDIG];
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            uint32_t a[DS];
+            chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
+            uint32_t rej = 0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
+            uint32_t base = 0;
+            if (rej) {
+                const uint32_t cnt = __builtin_popcount(rej);
+                base = atomicAdd(&W.qn, cnt);
+                if (base + cnt <= (uint32_t)FQCAP) {
+                    uint32_t m = rej, i = base;
+                    while (m) {
+                        const int j = __builtin_ctz(m);
+                        m &= m - 1;
+                        W.q[i++] = (uint32_t)d << 16 | (lane * DS + j);
+                    }
+                } else {
+                    // the queue is full (rejection rates far above any prime of this path's): redraw in the lane
+                    uint32_t m = rej;
+                    while (m) {
+                        const int j = __builtin_ctz(m);
+                        m &= m - 1;
+                        uint32_t v = 0;
+                        for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+                            v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * n16, (uint32_t)d, p, TAG_KSKA, j);
+                            if (v < ex.mp) break;
+                        }
+#pragma unroll
+                        for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? v : a[jj];
+                    }
+                    rej = 0;
+                }
+            }
+            rejd[d] = rej;
+            based[d] = base;
+            const uint32_t* x = L.D[d] + lane * DS;
+#pragma unroll
+            for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * ((rej >> k) & 1 ? 0 : ex.red(a[k]));
+            // materialise the sums here: this digit's a words die before the next block is computed
+#pragma unroll
+            for (int k = 0; k < DS; ++k) asm volatile("" : "+v"(acc[k]));
+        }
+        // the key's b rows: they arrive while the queued words are redrawn and are consumed last
+        uint32_t b[NDIG][DS];
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) ld16(kb + d * dstride, b[d]);
+        // redraw the queued words (entry <- accepted value), then each owner adds D_d a_d of its own words
+        wave_sync();
+        const uint32_t nq = min(W.qn, (uint32_t)FQCAP);
+        for (uint32_t i = lane; i < nq; i += DBX) {
+            const uint32_t it = W.q[i], d = it >> 16, sl = it & 0xFFFF;
+            const uint32_t ctr = (chunk0 + sl) >> 4;
+            uint32_t v = 0;
+            for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+                v = chacha12_word(seed, ctr + (uint32_t)tt * n16, d, p, TAG_KSKA, (int)(sl & 15));
+                if (v < ex.mp) break;
+            }
+            W.q[i] = ex.red(v);
+        }
+        wave_sync();
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            const uint32_t rej = rejd[d];
+            if (!rej) continue;
+#pragma unroll
+            for (int k = 0; k < DS; ++k) {
+                if ((rej >> k) & 1) {
+                    const uint32_t idx = based[d] + __builtin_popcount(rej & ((1u << k) - 1));
+                    acc[k] += (uint64_t)L.D[d][lane * DS + k] * W.q[idx];
+                }
+            }
+        }
+        uint32_t r0[DS], r1[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) r1[k] = red(acc[k]);
+        // s0 = sum_d D_d b_d (+ P c0 folded in: ndig + 1 <= 4 products of (p - 1)^2 < 2^62)
+#pragma unroll
+        for (int k = 0; k < DS; ++k) acc[k] = (m0 == 2 || !pc0) ? 0 : (uint64_t)L.c0[lane * DS + k] * pm;
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            const uint32_t* x = L.D[d] + lane * DS;
+#pragma unroll
+            for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * b[d][k];
+        }
+#pragma unroll
+        for (int k = 0; k < DS; ++k) r0[k] = red(acc[k]);
+        if (m0 == 2) {
+#pragma unroll
+            for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], L.c0[lane * DS + k], p);
+        }
+        const uint32_t kexp = A.autok[r];
+        uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + X.trow;
+        uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + X.trow;
+        wave_sync();  // every owner has read its redrawn words before the queue becomes the scatter buffer
+        if (kexp == 1 && !acc_out) {
+            st16(o0 + s0, r0);
+            st16(o1 + s0, r1);
+            continue;
+        }
+        uint32_t* l0 = W.q;
+        uint32_t* l1 = W.q + DCH;
+        const uint32_t cb = ((2 * bs0 + 1) * kexp) & mask2n;
+        const uint32_t step = (kexp << (logn - 3)) & mask2n;
+#pragma unroll
+        for (int k = 0; k < DS; ++k) {
+            const uint32_t b4 = ((k & 1) << 3) | ((k & 2) << 1) | ((k & 4) >> 1) | ((k & 8) >> 3);
+            const uint32_t o = brev_n(((cb + b4 * step) & mask2n) >> 1, logn) & (DCH - 1);
+            l0[o] = r0[k];
+            l1[o] = r1[k];
+        }
+        wave_sync();
+        const uint32_t ob = (automorph_slot(kexp, chunk0, logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
+        uint32_t v0[DS], v1[DS];
+        ld16(l0 + lane * DS, v0);
+        ld16(l1 + lane * DS, v1);
+        if (acc_out) {
+            uint32_t e0[DS], e1[DS];
+            ld16(o0 + ob, e0);
+            ld16(o1 + ob, e1);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) {
+                v0[k] = addm(v0[k], e0[k], p);
+                v1[k] = addm(v1[k], e1[k], p);
+            }
+        }
+        st16(o0 + ob, v0);
+        st16(o1 + ob, v1);
+        wave_sync();
+    }
+}
+
 template <int LOGN>
 int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     static_assert((1 << LOGN) >= DCH, "ring of at least 1024 slots");
@@ -310,7 +509,12 @@ int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     int groups = 1;
     while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
     dim3 grid(chunks, a.nrows, groups);
-    if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
+    const bool fast = mode == 1 && a.K == 1 && key.bits == 0 && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
+    if (fast) {
+        if (a.ndig == 1) hipLaunchKernelGGL(dot_fast<1>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN);
+        if (a.ndig == 2) hipLaunchKernelGGL(dot_fast<2>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN);
+        if (a.ndig == 3) hipLaunchKernelGGL(dot_fast<3>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN);
+    } else if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     else hipLaunchKernelGGL(dot_k<false>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     return launch_rc();
 }

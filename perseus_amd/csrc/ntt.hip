@@ -48,45 +48,87 @@ __device__ __forceinline__ void gs(uint32_t& a, uint32_t& b, uint32_t w, uint32_
     b = shoup(subm(u, v, p), w, ws, p);
 }
 
+// NG consecutive twiddles (and companions) of one stage in one vector load each: a stage's groups are NG = 8 / (h / T)
+// (layout A) or 8 / h (layout B) consecutive table entries, and their first index is a multiple of NG.
+template <int NG>
+__device__ __forceinline__ void ldtw(const uint32_t* p, uint32_t (&v)[8]) {
+    if constexpr (NG == 8) {
+        const uint4 a = ((const uint4*)p)[0], b = ((const uint4*)p)[1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else if constexpr (NG == 4) {
+        const uint4 a = *(const uint4*)p;
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
+    } else if constexpr (NG == 2) {
+        const uint2 a = *(const uint2*)p;
+        v[0] = a.x, v[1] = a.y;
+    } else {
+        v[0] = *p;
+    }
+}
+
 // Butterfly stages of one phase. `base(h)` is the twiddle index of group 0 of the stage of half distance h (in the
 // sub-transform's word units); group g of that stage uses index base(h) + g.
 // Layout A (e = tau + T j), stages h = 8T, 4T, 2T, T: pairs (j, j + h/T), group j / (2 h/T).
+template <bool FWD, int T, int K, class Base>
+__device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p, Base base) {
+    constexpr int hh = 1 << K, NG = 8 >> K;
+    const uint32_t b0 = base(T << K);
+    uint32_t tw[8], tws[8];
+    ldtw<NG>(w + b0, tw);
+    ldtw<NG>(ws + b0, tws);
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        if (j & hh) continue;
+        const int g = j >> (K + 1);
+        if (FWD) ct(x[j], x[j + hh], tw[g], tws[g], p);
+        else gs(x[j], x[j + hh], tw[g], tws[g], p);
+    }
+}
 template <bool FWD, int T, class Base>
 __device__ __forceinline__ void phase_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p, Base base) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int k = FWD ? 3 - s : s;  // h / T = 2^k
-        const int hh = 1 << k;
-        const int h = T << k;
-        const uint32_t b0 = base(h);
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            if (j & hh) continue;
-            const uint32_t idx = b0 + (j >> (k + 1));
-            const uint32_t tw = w[idx], tws = ws[idx];
-            if (FWD) ct(x[j], x[j + hh], tw, tws, p);
-            else gs(x[j], x[j + hh], tw, tws, p);
-        }
+    if (FWD) {
+        stage_a<FWD, T, 3>(x, w, ws, p, base);
+        stage_a<FWD, T, 2>(x, w, ws, p, base);
+        stage_a<FWD, T, 1>(x, w, ws, p, base);
+        stage_a<FWD, T, 0>(x, w, ws, p, base);
+    } else {
+        stage_a<FWD, T, 0>(x, w, ws, p, base);
+        stage_a<FWD, T, 1>(x, w, ws, p, base);
+        stage_a<FWD, T, 2>(x, w, ws, p, base);
+        stage_a<FWD, T, 3>(x, w, ws, p, base);
     }
 }
 // Layout B (e = 16 tau + j), stages h = T/2 .. 1: pairs (j, j + h), group (16 tau + j) / (2h).
+template <bool FWD, int K, class Base>
+__device__ __forceinline__ void stage_b(uint32_t (&x)[E], int tau, const uint32_t* w, const uint32_t* ws, uint32_t p,
+                                        Base base) {
+    constexpr int h = 1 << K, NG = 8 >> K;
+    const uint32_t b0 = base(h) + ((uint32_t)(E * tau) >> (K + 1));
+    uint32_t tw[8], tws[8];
+    ldtw<NG>(w + b0, tw);
+    ldtw<NG>(ws + b0, tws);
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        if (j & h) continue;
+        const int g = j >> (K + 1);
+        if (FWD) ct(x[j], x[j + h], tw[g], tws[g], p);
+        else gs(x[j], x[j + h], tw[g], tws[g], p);
+    }
+}
 template <bool FWD, int T, class Base>
 __device__ __forceinline__ void phase_b(uint32_t (&x)[E], int tau, const uint32_t* w, const uint32_t* ws, uint32_t p,
                                         Base base) {
     constexpr int LT = T == 16 ? 4 : T == 8 ? 3 : T == 4 ? 2 : 1;
-#pragma unroll
-    for (int s = 0; s < LT; ++s) {
-        const int k = FWD ? LT - 1 - s : s;  // h = 2^k
-        const int h = 1 << k;
-        const uint32_t b0 = base(h) + ((uint32_t)(E * tau) >> (k + 1));
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            if (j & h) continue;
-            const uint32_t idx = b0 + (j >> (k + 1));
-            const uint32_t tw = w[idx], tws = ws[idx];
-            if (FWD) ct(x[j], x[j + h], tw, tws, p);
-            else gs(x[j], x[j + h], tw, tws, p);
-        }
+    if (FWD) {
+        if (LT > 3) stage_b<FWD, 3>(x, tau, w, ws, p, base);
+        if (LT > 2) stage_b<FWD, 2>(x, tau, w, ws, p, base);
+        if (LT > 1) stage_b<FWD, 1>(x, tau, w, ws, p, base);
+        stage_b<FWD, 0>(x, tau, w, ws, p, base);
+    } else {
+        stage_b<FWD, 0>(x, tau, w, ws, p, base);
+        if (LT > 1) stage_b<FWD, 1>(x, tau, w, ws, p, base);
+        if (LT > 2) stage_b<FWD, 2>(x, tau, w, ws, p, base);
+        if (LT > 3) stage_b<FWD, 3>(x, tau, w, ws, p, base);
     }
 }
 
@@ -107,19 +149,30 @@ __device__ __forceinline__ uint32_t ld_src(const RowSrc& s, size_t off, uint32_t
     return v;
 }
 
+// the workgroup's logical (block in row, row) after the XCD renumbering of a (gx, rows) grid
+struct Blk {
+    int x, y;
+};
+__device__ __forceinline__ Blk blk_xy() {
+    const uint32_t n = gridDim.x * gridDim.y;
+    const uint32_t l = xcd_block(blockIdx.y * gridDim.x + blockIdx.x, n);
+    return Blk{(int)(l % gridDim.x), (int)(l / gridDim.x)};
+}
+
 // ------------------------------------------------------------------------------------------------ forward
 // Column pass: workgroup (bx, row i) takes columns [bx CC, bx CC + CC) of row i.
 template <int LOGN>
 __global__ void __launch_bounds__(WG) fwd_cols(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::COL_LDS];
-    const int i = row0 + blockIdx.y;
+    const Blk B = blk_xy();
+    const int i = row0 + B.y;
     const int pid = A.rprime[i];
     const uint32_t p = (uint32_t)A.pr[pid].p;
     const uint32_t* w = (const uint32_t*)A.fw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.fws + ((size_t)pid << LOGN);
     const int col = threadIdx.x % G::CC, tau = threadIdx.x / G::CC;
-    const int c = blockIdx.x * G::CC + col;
+    const int c = B.x * G::CC + col;
     const RowSrc src = row_src(A, i, LOGN);
     uint32_t x[E];
 #pragma unroll
@@ -171,13 +224,14 @@ template <int LOGN>
 __global__ void __launch_bounds__(WG) fwd_rows(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::ROW_LDS];
-    const int i = row0 + blockIdx.y;
+    const Blk B = blk_xy();
+    const int i = row0 + B.y;
     const int pid = A.rprime[i];
     const uint32_t p = (uint32_t)A.pr[pid].p;
     const uint32_t* w = (const uint32_t*)A.fw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.fws + ((size_t)pid << LOGN);
     const int lb = threadIdx.x / G::TC, tau = threadIdx.x % G::TC;
-    const int blk = blockIdx.x * G::BB + lb;
+    const int blk = B.x * G::BB + lb;
     uint32_t* row = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
     uint32_t* a = row + (size_t)blk * G::C;
     uint32_t x[E];
@@ -210,13 +264,14 @@ template <int LOGN>
 __global__ void __launch_bounds__(WG) inv_rows(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::ROW_LDS];
-    const int i = row0 + blockIdx.y;
+    const Blk B = blk_xy();
+    const int i = row0 + B.y;
     const int pid = A.rprime[i];
     const uint32_t p = (uint32_t)A.pr[pid].p;
     const uint32_t* w = (const uint32_t*)A.iw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.iws + ((size_t)pid << LOGN);
     const int lb = threadIdx.x / G::TC, tau = threadIdx.x % G::TC;
-    const int blk = blockIdx.x * G::BB + lb;
+    const int blk = B.x * G::BB + lb;
     const RowSrc src = row_src(A, i, LOGN);
     uint32_t x[E];
     const size_t e0 = (size_t)blk * G::C + E * tau;
@@ -251,13 +306,14 @@ template <int LOGN>
 __global__ void __launch_bounds__(WG) inv_cols(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::COL_LDS];
-    const int i = row0 + blockIdx.y;
+    const Blk B = blk_xy();
+    const int i = row0 + B.y;
     const int pid = A.rprime[i];
     const uint32_t p = (uint32_t)A.pr[pid].p;
     const uint32_t* w = (const uint32_t*)A.iw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.iws + ((size_t)pid << LOGN);
     const int col = threadIdx.x % G::CC, tau = threadIdx.x / G::CC;
-    const int c = blockIdx.x * G::CC + col;
+    const int c = B.x * G::CC + col;
     uint32_t* a = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
     uint32_t x[E];
 #pragma unroll

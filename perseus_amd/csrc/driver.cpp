@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -214,6 +215,8 @@ struct pcx_rows {
 struct pcx_ctx {
     uint32_t logn = 0, n = 0;
     int nq = 0, kp = 0, dnum = 0, alpha = 0, k_rot = 1, rows = 0;
+    int lazy = 0;   // NttArgs.lazy: 1 when every prime is below 2^30 (Harvey butterflies)
+    int chunk = 0;  // NttArgs.chunk of the batched transforms: rows per pass pair (0 = all)
     std::vector<uint64_t> primes, roots;
     const KernelTable* tab = nullptr;
     Dev dev;
@@ -417,7 +420,8 @@ NttArgs ntt_args(const pcx_ctx* c, void* base, const Rows& r, int nrows) {
     a.ninvs = c->ninvs;
     a.pr = c->pr;
     a.nrows = nrows;
-    a.chunk = 0;
+    a.chunk = c->chunk;
+    a.lazy = c->lazy;
     a.snum = 1;
     a.xnum = 1;
     return a;
@@ -644,6 +648,10 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     c->rows = nq + kp;
     c->tab = tab;
     c->primes.assign(primes, primes + nq + kp);
+    c->lazy = std::all_of(c->primes.begin(), c->primes.end(), [](uint64_t p) { return p < (1ull << 30); }) ? 1 : 0;
+    // rows per NTT pass pair (0: one pass pair over all rows, measured fastest; PCX_NTT_CHUNK overrides)
+    c->chunk = 0;
+    if (const char* e = getenv("PCX_NTT_CHUNK")) c->chunk = atoi(e);
     const int R = c->rows;
     // prime constants and twiddles (crates/pc-gpu/src/context.rs:186-230)
     std::vector<PrimeConst> pc;

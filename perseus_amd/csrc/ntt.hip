@@ -12,7 +12,12 @@
 // Inside a pass each thread owns 16 words of one sub-transform of S points (T = S / 16 threads per sub-transform,
 // 256 threads per workgroup): 4 butterfly stages on words spaced T apart in registers ("layout A": e = tau + T j),
 // one transpose through LDS, then log2(T) stages on 16 consecutive words ("layout B": e = 16 tau + j). The inverse
-// runs the same two phases in the opposite order. Words stay canonical in [0, p) between stages.
+// runs the same two phases in the opposite order. A row-pass sub-transform lives in one wave, so its transposes need
+// only a wave barrier, and it moves its words with 16-byte accesses (layout B) around one more transpose.
+//
+// Butterflies are lazy. When every prime of the launch is below 2^30 (NttArgs.lazy != 0) they are Harvey's: forward
+// words in [0, 4p), inverse words in [0, 2p). Otherwise (primes up to 2^31, where 4p overflows a word) forward words
+// stay in [0, 2p) and inverse words canonical. Either way a transform returns canonical words.
 #include "common.h"
 
 namespace pch {
@@ -33,23 +38,47 @@ struct Geo {
     static constexpr int CPAD = CC == 16 ? 1 : 0;  // LDS row padding of the column pass
     static constexpr int COL_LDS = R * (CC + CPAD);
     static constexpr int ROW_LDS = BB * (C + C / E);
-    static constexpr int LDS = COL_LDS > ROW_LDS ? COL_LDS : ROW_LDS;
     static_assert(TR >= 2 && TC >= 2 && TR <= E && TC <= E, "sub-transforms of 32 to 256 points");
 };
 
-__device__ __forceinline__ void ct(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p) {
-    const uint32_t t = shoup(b, w, ws, p);
-    b = subm(a, t, p);
-    a = addm(a, t, p);
+// ------------------------------------------------------------------------------------------------ butterflies
+// H: Harvey (every prime < 2^30). p2 = 2p.
+template <bool H>
+__device__ __forceinline__ void ct(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p, uint32_t p2) {
+    uint32_t t = shoup_lz(b, w, ws, p);  // [0, 2p)
+    if (H) {
+        const uint32_t u = min(a, a - p2);  // [0, 4p) -> [0, 2p)
+        a = u + t;
+        b = u - t + p2;
+    } else {
+        const uint32_t u = min(a, a - p);  // [0, 2p) -> [0, p)
+        t = min(t, t - p);
+        a = u + t;
+        b = u - t + p;
+    }
 }
-__device__ __forceinline__ void gs(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p) {
+template <bool H>
+__device__ __forceinline__ void gs(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p, uint32_t p2) {
     const uint32_t u = a, v = b;
-    a = addm(u, v, p);
-    b = shoup(subm(u, v, p), w, ws, p);
+    if (H) {  // [0, 2p) in and out
+        const uint32_t s = u + v;
+        a = min(s, s - p2);
+        b = shoup_lz(u - v + p2, w, ws, p);
+    } else {  // canonical in and out
+        a = addm(u, v, p);
+        const uint32_t d = shoup_lz(u - v + p, w, ws, p);
+        b = min(d, d - p);
+    }
+}
+// a forward lazy word as its residue
+template <bool H>
+__device__ __forceinline__ uint32_t canon(uint32_t a, uint32_t p, uint32_t p2) {
+    if (H) a = min(a, a - p2);
+    return min(a, a - p);
 }
 
-// NG consecutive twiddles (and companions) of one stage in one vector load each: a stage's groups are NG = 8 / (h / T)
-// (layout A) or 8 / h (layout B) consecutive table entries, and their first index is a multiple of NG.
+// NG consecutive twiddles of one stage in one vector load: a stage's groups are NG = 8 / (h / T) (layout A) or 8 / h
+// (layout B) consecutive table entries, and their first index is a multiple of NG.
 template <int NG>
 __device__ __forceinline__ void ldtw(const uint32_t* p, uint32_t (&v)[8]) {
     if constexpr (NG == 8) {
@@ -66,11 +95,10 @@ __device__ __forceinline__ void ldtw(const uint32_t* p, uint32_t (&v)[8]) {
     }
 }
 
-// Butterfly stages of one phase. `base(h)` is the twiddle index of group 0 of the stage of half distance h (in the
-// sub-transform's word units); group g of that stage uses index base(h) + g.
-// Layout A (e = tau + T j), stages h = 8T, 4T, 2T, T: pairs (j, j + h/T), group j / (2 h/T).
-template <bool FWD, int T, int K, class Base>
-__device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p, Base base) {
+// Layout A (e = tau + T j), stage h = T 2^K: pairs (j, j + 2^K), group j / 2^(K+1), index base(h) + group.
+template <bool FWD, bool H, int T, int K, class Base>
+__device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p,
+                                        uint32_t p2, Base base) {
     constexpr int hh = 1 << K, NG = 8 >> K;
     const uint32_t b0 = base(T << K);
     uint32_t tw[8], tws[8];
@@ -80,28 +108,29 @@ __device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, con
     for (int j = 0; j < E; ++j) {
         if (j & hh) continue;
         const int g = j >> (K + 1);
-        if (FWD) ct(x[j], x[j + hh], tw[g], tws[g], p);
-        else gs(x[j], x[j + hh], tw[g], tws[g], p);
+        if (FWD) ct<H>(x[j], x[j + hh], tw[g], tws[g], p, p2);
+        else gs<H>(x[j], x[j + hh], tw[g], tws[g], p, p2);
     }
 }
-template <bool FWD, int T, class Base>
-__device__ __forceinline__ void phase_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p, Base base) {
+template <bool FWD, bool H, int T, class Base>
+__device__ __forceinline__ void phase_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p,
+                                        uint32_t p2, Base base) {
     if (FWD) {
-        stage_a<FWD, T, 3>(x, w, ws, p, base);
-        stage_a<FWD, T, 2>(x, w, ws, p, base);
-        stage_a<FWD, T, 1>(x, w, ws, p, base);
-        stage_a<FWD, T, 0>(x, w, ws, p, base);
+        stage_a<FWD, H, T, 3>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 2>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 1>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 0>(x, w, ws, p, p2, base);
     } else {
-        stage_a<FWD, T, 0>(x, w, ws, p, base);
-        stage_a<FWD, T, 1>(x, w, ws, p, base);
-        stage_a<FWD, T, 2>(x, w, ws, p, base);
-        stage_a<FWD, T, 3>(x, w, ws, p, base);
+        stage_a<FWD, H, T, 0>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 1>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 2>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 3>(x, w, ws, p, p2, base);
     }
 }
-// Layout B (e = 16 tau + j), stages h = T/2 .. 1: pairs (j, j + h), group (16 tau + j) / (2h).
-template <bool FWD, int K, class Base>
+// Layout B (e = 16 tau + j), stage h = 2^K < T: pairs (j, j + h), group (16 tau + j) / (2h).
+template <bool FWD, bool H, int K, class Base>
 __device__ __forceinline__ void stage_b(uint32_t (&x)[E], int tau, const uint32_t* w, const uint32_t* ws, uint32_t p,
-                                        Base base) {
+                                        uint32_t p2, Base base) {
     constexpr int h = 1 << K, NG = 8 >> K;
     const uint32_t b0 = base(h) + ((uint32_t)(E * tau) >> (K + 1));
     uint32_t tw[8], tws[8];
@@ -111,25 +140,59 @@ __device__ __forceinline__ void stage_b(uint32_t (&x)[E], int tau, const uint32_
     for (int j = 0; j < E; ++j) {
         if (j & h) continue;
         const int g = j >> (K + 1);
-        if (FWD) ct(x[j], x[j + h], tw[g], tws[g], p);
-        else gs(x[j], x[j + h], tw[g], tws[g], p);
+        if (FWD) ct<H>(x[j], x[j + h], tw[g], tws[g], p, p2);
+        else gs<H>(x[j], x[j + h], tw[g], tws[g], p, p2);
     }
 }
-template <bool FWD, int T, class Base>
+template <bool FWD, bool H, int T, class Base>
 __device__ __forceinline__ void phase_b(uint32_t (&x)[E], int tau, const uint32_t* w, const uint32_t* ws, uint32_t p,
-                                        Base base) {
+                                        uint32_t p2, Base base) {
     constexpr int LT = T == 16 ? 4 : T == 8 ? 3 : T == 4 ? 2 : 1;
     if (FWD) {
-        if (LT > 3) stage_b<FWD, 3>(x, tau, w, ws, p, base);
-        if (LT > 2) stage_b<FWD, 2>(x, tau, w, ws, p, base);
-        if (LT > 1) stage_b<FWD, 1>(x, tau, w, ws, p, base);
-        stage_b<FWD, 0>(x, tau, w, ws, p, base);
+        if (LT > 3) stage_b<FWD, H, 3>(x, tau, w, ws, p, p2, base);
+        if (LT > 2) stage_b<FWD, H, 2>(x, tau, w, ws, p, p2, base);
+        if (LT > 1) stage_b<FWD, H, 1>(x, tau, w, ws, p, p2, base);
+        stage_b<FWD, H, 0>(x, tau, w, ws, p, p2, base);
     } else {
-        stage_b<FWD, 0>(x, tau, w, ws, p, base);
-        if (LT > 1) stage_b<FWD, 1>(x, tau, w, ws, p, base);
-        if (LT > 2) stage_b<FWD, 2>(x, tau, w, ws, p, base);
-        if (LT > 3) stage_b<FWD, 3>(x, tau, w, ws, p, base);
+        stage_b<FWD, H, 0>(x, tau, w, ws, p, p2, base);
+        if (LT > 1) stage_b<FWD, H, 1>(x, tau, w, ws, p, p2, base);
+        if (LT > 2) stage_b<FWD, H, 2>(x, tau, w, ws, p, p2, base);
+        if (LT > 3) stage_b<FWD, H, 3>(x, tau, w, ws, p, p2, base);
     }
+}
+
+// Wave-level ordering of LDS traffic between the lanes of one wave.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// A row-pass block's 16 words of thread tau through the block's LDS (C + C/16 words, one padding word per 16):
+// layout B (e = 16 tau + j) -> layout A (e = tau + T j) and back. The block lives in one wave.
+template <int T>
+__device__ __forceinline__ void b_to_a(uint32_t (&x)[E], uint32_t* l, int tau) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) l[(E * tau + j) + tau] = x[j];
+    wave_sync();
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int e = tau + T * j;
+        x[j] = l[e + e / E];
+    }
+    wave_sync();
+}
+template <int T>
+__device__ __forceinline__ void a_to_b(uint32_t (&x)[E], uint32_t* l, int tau) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int e = tau + T * j;
+        l[e + e / E] = x[j];
+    }
+    wave_sync();
+#pragma unroll
+    for (int j = 0; j < E; ++j) x[j] = l[(E * tau + j) + tau];
+    wave_sync();
 }
 
 // The first pass's source words of row i: out of place (src + soff[i] N, the sum mod p of snum rows sstride apart)
@@ -148,6 +211,15 @@ __device__ __forceinline__ uint32_t ld_src(const RowSrc& s, size_t off, uint32_t
     for (int k = 1; k < s.n; ++k) v = addm(v, s.p0[off + k * s.stride], p);
     return v;
 }
+__device__ __forceinline__ void ld16_src(const RowSrc& s, size_t off, uint32_t p, uint32_t (&x)[E]) {
+    ld16(s.p0 + off, x);
+    for (int k = 1; k < s.n; ++k) {
+        uint32_t y[E];
+        ld16(s.p0 + off + k * s.stride, y);
+#pragma unroll
+        for (int j = 0; j < E; ++j) x[j] = addm(x[j], y[j], p);
+    }
+}
 
 // the workgroup's logical (block in row, row) after the XCD renumbering of a (gx, rows) grid
 struct Blk {
@@ -160,156 +232,129 @@ __device__ __forceinline__ Blk blk_xy() {
 }
 
 // ------------------------------------------------------------------------------------------------ forward
-// Column pass: workgroup (bx, row i) takes columns [bx CC, bx CC + CC) of row i.
-template <int LOGN>
+// Column pass: workgroup (x, row i) takes columns [x CC, x CC + CC) of row i.
+template <int LOGN, bool H>
 __global__ void __launch_bounds__(WG) fwd_cols(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::COL_LDS];
     const Blk B = blk_xy();
     const int i = row0 + B.y;
     const int pid = A.rprime[i];
-    const uint32_t p = (uint32_t)A.pr[pid].p;
+    const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.fw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.fws + ((size_t)pid << LOGN);
     const int col = threadIdx.x % G::CC, tau = threadIdx.x / G::CC;
     const int c = B.x * G::CC + col;
     const RowSrc src = row_src(A, i, LOGN);
     uint32_t x[E];
+    if (src.n == 1) {
 #pragma unroll
-    for (int j = 0; j < E; ++j) x[j] = ld_src(src, (size_t)(tau + G::TR * j) * G::C + c, p);
+        for (int j = 0; j < E; ++j) x[j] = src.p0[(size_t)(tau + G::TR * j) * G::C + c];
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) x[j] = ld_src(src, (size_t)(tau + G::TR * j) * G::C + c, p);
+    }
     // stages h = R/2 .. TR (rows): index R/(2h) + r/(2h)
-    phase_a<true, G::TR>(x, w, ws, p, [](int h) { return (uint32_t)(G::R / (2 * h)); });
+    auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
+    phase_a<true, H, G::TR>(x, w, ws, p, p2, base);
     constexpr int LS = G::CC + G::CPAD;
 #pragma unroll
     for (int j = 0; j < E; ++j) lds[(tau + G::TR * j) * LS + col] = x[j];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = lds[(E * tau + j) * LS + col];
-    phase_b<true, G::TR>(x, tau, w, ws, p, [](int h) { return (uint32_t)(G::R / (2 * h)); });
+    phase_b<true, H, G::TR>(x, tau, w, ws, p, p2, base);
     uint32_t* out = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
 #pragma unroll
-    for (int j = 0; j < E; ++j) out[(size_t)(E * tau + j) * G::C + c] = x[j];
+    for (int j = 0; j < E; ++j) out[(size_t)(E * tau + j) * G::C + c] = x[j];  // lazy words
 }
 
-// NttArgs.epi on the final words v of row i at word offsets e0 + j (j < 16) (args.cuh:66-80, ntt.cuh:204-222):
-// 1: eout = (x - v) s, 2: eout = d + (x - v) s, 3: eout = x s + v; x = the sum of xnum rows of ex, s = es[prime id].
-__device__ __forceinline__ void epilogue(const NttArgs& A, size_t r0, int pid, uint32_t p, uint32_t (&v)[E]) {
-    const uint32_t s = ((const uint32_t*)A.es)[pid], ss = ((const uint32_t*)A.ess)[pid];
-    const uint32_t* ex = (const uint32_t*)A.ex + r0;
-    uint32_t x[E];
-    ld16(ex, x);
-    for (int k = 1; k < A.xnum; ++k) {
-        uint32_t y[E];
-        ld16(ex + k * A.xstride, y);
-#pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = addm(x[j], y[j], p);
-    }
-    uint32_t* o = (uint32_t*)A.eout + r0;
-    uint32_t d[E];
-    if (A.epi == 2) ld16(A.ed ? (const uint32_t*)A.ed + r0 : o, d);
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        if (A.epi == 3) {
-            v[j] = addm(shoup(x[j], s, ss, p), v[j], p);
-        } else {
-            uint32_t y = shoup(subm(x[j], v[j], p), s, ss, p);
-            v[j] = A.epi == 2 ? addm(d[j], y, p) : y;
-        }
-    }
-    st16(o, v);
-}
-
-// Row pass: workgroup (bx, row i) takes blocks [bx BB, bx BB + BB) of row i (C contiguous words each).
-template <int LOGN>
+// Row pass: workgroup (x, row i) takes blocks [x BB, x BB + BB) of row i (C contiguous words each). EPI: NttArgs.epi
+// (0: in place; 1: eout = (x - v) s, 2: eout = d + (x - v) s, 3: eout = x s + v; x = the sum of xnum rows of ex,
+// s = es[prime id]; args.cuh:66-80).
+template <int LOGN, bool H, int EPI>
 __global__ void __launch_bounds__(WG) fwd_rows(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::ROW_LDS];
     const Blk B = blk_xy();
     const int i = row0 + B.y;
     const int pid = A.rprime[i];
-    const uint32_t p = (uint32_t)A.pr[pid].p;
+    const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.fw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.fws + ((size_t)pid << LOGN);
     const int lb = threadIdx.x / G::TC, tau = threadIdx.x % G::TC;
     const int blk = B.x * G::BB + lb;
-    uint32_t* row = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
-    uint32_t* a = row + (size_t)blk * G::C;
+    const size_t r0 = ((size_t)A.roff[i] << LOGN) + (size_t)blk * G::C + E * tau;
+    uint32_t* a = (uint32_t*)A.base + r0;
     uint32_t x[E];
-#pragma unroll
-    for (int j = 0; j < E; ++j) x[j] = a[tau + G::TC * j];
-    // stage of half distance h (words): index N/(2h) + blk C/(2h) + c/(2h)
-    auto base = [blk](int h) { return (uint32_t)((G::N / (2 * h)) + blk * (G::C / (2 * h))); };
-    phase_a<true, G::TC>(x, w, ws, p, base);
+    ld16(a, x);
     constexpr int LS = G::C + G::C / E;
     uint32_t* l = lds + lb * LS;
+    b_to_a<G::TC>(x, l, tau);
+    // stage of half distance h (words): index N/(2h) + blk C/(2h) + c/(2h)
+    auto base = [blk](int h) { return (uint32_t)((G::N / (2 * h)) + blk * (G::C / (2 * h))); };
+    phase_a<true, H, G::TC>(x, w, ws, p, p2, base);
+    a_to_b<G::TC>(x, l, tau);
+    phase_b<true, H, G::TC>(x, tau, w, ws, p, p2, base);
+#pragma unroll
+    for (int j = 0; j < E; ++j) x[j] = canon<H>(x[j], p, p2);
+    if (EPI == 0) {
+        st16(a, x);
+        return;
+    }
+    const uint32_t s = ((const uint32_t*)A.es)[pid], ss = ((const uint32_t*)A.ess)[pid];
+    uint32_t ex[E];
+    ld16_src(RowSrc{(const uint32_t*)A.ex, A.xnum, A.xstride}, r0, p, ex);
+    uint32_t* o = (uint32_t*)A.eout + r0;
+    uint32_t d[E];
+    if (EPI == 2) ld16(A.ed ? (const uint32_t*)A.ed + r0 : o, d);
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        const int e = tau + G::TC * j;
-        l[e + e / E] = x[j];
+        if (EPI == 3) {
+            x[j] = addm(shoup(ex[j], s, ss, p), x[j], p);
+        } else {
+            const uint32_t y = shoup(ex[j] - x[j] + p, s, ss, p);
+            x[j] = EPI == 2 ? addm(d[j], y, p) : y;
+        }
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int e = E * tau + j;
-        x[j] = l[e + e / E];
-    }
-    phase_b<true, G::TC>(x, tau, w, ws, p, base);
-    const size_t off = ((size_t)A.roff[i] << LOGN) + (size_t)blk * G::C + E * tau;
-    if (A.epi) epilogue(A, off, pid, p, x);
-    else st16(a + E * tau, x);
+    st16(o, x);
 }
 
 // ------------------------------------------------------------------------------------------------ inverse
-template <int LOGN>
+template <int LOGN, bool H>
 __global__ void __launch_bounds__(WG) inv_rows(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::ROW_LDS];
     const Blk B = blk_xy();
     const int i = row0 + B.y;
     const int pid = A.rprime[i];
-    const uint32_t p = (uint32_t)A.pr[pid].p;
+    const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.iw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.iws + ((size_t)pid << LOGN);
     const int lb = threadIdx.x / G::TC, tau = threadIdx.x % G::TC;
     const int blk = B.x * G::BB + lb;
     const RowSrc src = row_src(A, i, LOGN);
-    uint32_t x[E];
     const size_t e0 = (size_t)blk * G::C + E * tau;
-    if (src.n == 1) {
-        ld16(src.p0 + e0, x);
-    } else {
-#pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = ld_src(src, e0 + j, p);
-    }
+    uint32_t x[E];
+    ld16_src(src, e0, p, x);
     auto base = [blk](int h) { return (uint32_t)((G::N / (2 * h)) + blk * (G::C / (2 * h))); };
-    phase_b<false, G::TC>(x, tau, w, ws, p, base);
+    phase_b<false, H, G::TC>(x, tau, w, ws, p, p2, base);
     constexpr int LS = G::C + G::C / E;
     uint32_t* l = lds + lb * LS;
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int e = E * tau + j;
-        l[e + e / E] = x[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int e = tau + G::TC * j;
-        x[j] = l[e + e / E];
-    }
-    phase_a<false, G::TC>(x, w, ws, p, base);
-    uint32_t* a = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN) + (size_t)blk * G::C;
-#pragma unroll
-    for (int j = 0; j < E; ++j) a[tau + G::TC * j] = x[j];
+    b_to_a<G::TC>(x, l, tau);
+    phase_a<false, H, G::TC>(x, w, ws, p, p2, base);
+    a_to_b<G::TC>(x, l, tau);
+    st16((uint32_t*)A.base + ((size_t)A.roff[i] << LOGN) + e0, x);  // [0, 2p) (Harvey) or canonical
 }
 
-template <int LOGN>
+template <int LOGN, bool H>
 __global__ void __launch_bounds__(WG) inv_cols(NttArgs A, int row0) {
     using G = Geo<LOGN>;
     __shared__ uint32_t lds[G::COL_LDS];
     const Blk B = blk_xy();
     const int i = row0 + B.y;
     const int pid = A.rprime[i];
-    const uint32_t p = (uint32_t)A.pr[pid].p;
+    const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.iw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.iws + ((size_t)pid << LOGN);
     const int col = threadIdx.x % G::CC, tau = threadIdx.x / G::CC;
@@ -319,15 +364,15 @@ __global__ void __launch_bounds__(WG) inv_cols(NttArgs A, int row0) {
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = a[(size_t)(E * tau + j) * G::C + c];
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
-    phase_b<false, G::TR>(x, tau, w, ws, p, base);
+    phase_b<false, H, G::TR>(x, tau, w, ws, p, p2, base);
     constexpr int LS = G::CC + G::CPAD;
 #pragma unroll
     for (int j = 0; j < E; ++j) lds[(E * tau + j) * LS + col] = x[j];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = lds[(tau + G::TR * j) * LS + col];
-    phase_a<false, G::TR>(x, w, ws, p, base);
-    // the scale: es[i] per row (NttArgs ABI 17) or N^-1 of the prime
+    phase_a<false, H, G::TR>(x, w, ws, p, p2, base);
+    // the scale: es[i] per row (NttArgs ABI 17) or N^-1 of the prime; Shoup takes the lazy words whole
     uint32_t s, ss;
     if (A.es) {
         s = ((const uint32_t*)A.es)[i];
@@ -354,44 +399,62 @@ inline int check(const NttArgs* a, bool fwd) {
     return 0;
 }
 
+template <int LOGN, bool H>
+void fwd_pair(const NttArgs& A, int r0, int n, hipStream_t st) {
+    using G = Geo<LOGN>;
+    // a first pass out of place, then the row pass in place on base
+    hipLaunchKernelGGL((fwd_cols<LOGN, H>), dim3(G::COL_WGS, n), dim3(WG), 0, st, A, r0);
+    NttArgs B = A;
+    B.soff = nullptr;
+    const dim3 g(G::ROW_WGS, n);
+    switch (A.epi) {
+        case 0: hipLaunchKernelGGL((fwd_rows<LOGN, H, 0>), g, dim3(WG), 0, st, B, r0); break;
+        case 1: hipLaunchKernelGGL((fwd_rows<LOGN, H, 1>), g, dim3(WG), 0, st, B, r0); break;
+        case 2: hipLaunchKernelGGL((fwd_rows<LOGN, H, 2>), g, dim3(WG), 0, st, B, r0); break;
+        default: hipLaunchKernelGGL((fwd_rows<LOGN, H, 3>), g, dim3(WG), 0, st, B, r0); break;
+    }
+}
+
 template <int LOGN>
 int fwd(const NttArgs* a, pc_stream_t s) {
-    using G = Geo<LOGN>;
     if (int rc = check(a, true)) return rc;
     const NttArgs A = *a;
     const int chunk = A.chunk > 0 ? A.chunk : (A.nrows > 0 ? A.nrows : 1);
     hipStream_t st = (hipStream_t)s;
     for (int r0 = 0; r0 < A.nrows; r0 += chunk) {
         const int n = A.nrows - r0 < chunk ? A.nrows - r0 : chunk;
-        // a first pass out of place, then the row pass in place on base
-        hipLaunchKernelGGL(fwd_cols<LOGN>, dim3(G::COL_WGS, n), dim3(WG), 0, st, A, r0);
-        NttArgs B = A;
-        B.soff = nullptr;
-        hipLaunchKernelGGL(fwd_rows<LOGN>, dim3(G::ROW_WGS, n), dim3(WG), 0, st, B, r0);
+        if (A.lazy) fwd_pair<LOGN, true>(A, r0, n, st);
+        else fwd_pair<LOGN, false>(A, r0, n, st);
     }
     return launch_rc();
 }
 
+template <int LOGN, bool H>
+void inv_pair(const NttArgs& A, int r0, int n, hipStream_t st) {
+    using G = Geo<LOGN>;
+    hipLaunchKernelGGL((inv_rows<LOGN, H>), dim3(G::ROW_WGS, n), dim3(WG), 0, st, A, r0);
+    NttArgs B = A;
+    B.soff = nullptr;
+    hipLaunchKernelGGL((inv_cols<LOGN, H>), dim3(G::COL_WGS, n), dim3(WG), 0, st, B, r0);
+}
+
 template <int LOGN>
 int inv(const NttArgs* a, pc_stream_t s) {
-    using G = Geo<LOGN>;
     if (int rc = check(a, false)) return rc;
     const NttArgs A = *a;
     const int chunk = A.chunk > 0 ? A.chunk : (A.nrows > 0 ? A.nrows : 1);
     hipStream_t st = (hipStream_t)s;
     for (int r0 = 0; r0 < A.nrows; r0 += chunk) {
         const int n = A.nrows - r0 < chunk ? A.nrows - r0 : chunk;
-        hipLaunchKernelGGL(inv_rows<LOGN>, dim3(G::ROW_WGS, n), dim3(WG), 0, st, A, r0);
-        NttArgs B = A;
-        B.soff = nullptr;
-        hipLaunchKernelGGL(inv_cols<LOGN>, dim3(G::COL_WGS, n), dim3(WG), 0, st, B, r0);
+        if (A.lazy) inv_pair<LOGN, true>(A, r0, n, st);
+        else inv_pair<LOGN, false>(A, r0, n, st);
     }
     return launch_rc();
 }
 
 }  // namespace ntt
 
-#define PCH_NTT_INST(L)                                              \
+#define PCH_NTT_INST(L)                                                             \
     int ntt_fwd_##L(const NttArgs* a, pc_stream_t s) { return ntt::fwd<L>(a, s); } \
     int ntt_inv_##L(const NttArgs* a, pc_stream_t s) { return ntt::inv<L>(a, s); }
 PCH_NTT_INST(12)

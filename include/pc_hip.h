@@ -449,6 +449,11 @@ int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s);
 int pcx_timing(pcx_ctx* c, int max_stages);
 int pcx_timing_read(pcx_ctx* c, int stage, double* total_ms, int* count);
 
+/* HBM stream-copy probe: copies `bytes` (a multiple of 16 KiB) from src to dst with a plain 16-byte-access kernel, to
+ * state the achievable bandwidth next to the spec figure and to calibrate the FETCH_SIZE / WRITE_SIZE counters. No
+ * counterpart in the reference. */
+int pcx_copy_probe(void* dst, const void* src, size_t bytes, pc_stream_t s);
+
 #ifdef __cplusplus
 }
 #endif

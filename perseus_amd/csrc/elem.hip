@@ -101,3 +101,28 @@ PCH_EW_INST(15)
 PCH_EW_INST(16)
 
 }  // namespace pch
+
+// ------------------------------------------------------------------------------------------------ HBM copy probe
+// A plain stream copy of a known byte count: each 256-thread block moves one contiguous 16 KiB tile, every thread four
+// 16-byte words at stride 4 KiB. It measures the achievable HBM bandwidth and calibrates the FETCH_SIZE / WRITE_SIZE
+// counters (their reading for this kernel over the bytes it must move).
+namespace pch {
+namespace elem {
+__global__ void __launch_bounds__(BX) copy_probe_k(uint4* __restrict__ dst, const uint4* __restrict__ src) {
+    const size_t base = (size_t)blockIdx.x * (BX * 4) + threadIdx.x;
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = src[base + k * BX];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[base + k * BX] = v[k];
+}
+}  // namespace elem
+}  // namespace pch
+
+extern "C" int pcx_copy_probe(void* dst, const void* src, size_t bytes, pc_stream_t s) {
+    constexpr size_t TILE = pch::elem::BX * 4 * 16;
+    if (!dst || !src || bytes == 0 || bytes % TILE || bytes / TILE > 0x7fffffffu) return -1;
+    hipLaunchKernelGGL(pch::elem::copy_probe_k, dim3((unsigned)(bytes / TILE)), dim3(pch::elem::BX), 0,
+                       (hipStream_t)s, (uint4*)dst, (const uint4*)src);
+    return pch::launch_rc();
+}

@@ -297,200 +297,252 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
 
 // The hot case of the dot, specialised: one ciphertext, dense b through a KeyTab, every digit's a regenerated, NDIG
 // (<= 3) live digits unrolled. D and c0 are staged once per workgroup as in dot_k. A lane that meets rejected ChaCha
-// words appends them to its wave's queue and keeps the queue position (atomic base) of each digit; the whole wave then
-// redraws the queued words at once, writing each accepted value back into its queue entry, and the owner adds D_d a_d
-// of its words from there. The queue doubles as the scatter buffer of the automorphism, so a wave needs 8 KB of LDS and
-// three workgroups fit on a CU.
-constexpr int FQCAP = 2 * DCH;  // queue entries per wave (= the two 1024-word scatter buffers)
+// words appends them to its wave's queue (slot and digit; the queue position of each digit's first entry is kept),
+// and leaves their products out of its sums; the whole wave then redraws the queued words at once, writing each
+// accepted value back into its queue entry. The output goes through one 1024-word scatter buffer per wave, one part at
+// a time; each owner adds D_d a_d of its redrawn words into its slots there, after the scatter write of s1. A wave
+// needs 8 KB of LDS, so three workgroups fit on a CU.
+constexpr int FQCAP = DCH;  // queue entries per wave
+
+// D and c0 rows are staged with 4 words of padding after every 16 (a lane's 16 words start 20 words after its
+// neighbour's), so the lanes' 16-byte LDS reads fall on distinct banks.
+constexpr int PADW = DCH + DCH / 4;
+__device__ __forceinline__ int padw(int i) { return i + (i >> 4) * 4; }
 
 struct FastLds {
-    uint32_t D[MAXD][DCH];
-    uint32_t c0[DCH];
+    uint32_t D[MAXD][PADW];
+    uint32_t c0[PADW];
     struct Wave {
-        uint32_t q[FQCAP];
+        uint32_t buf[DCH];  // scatter buffer
+        uint32_t q[FQCAP];  // rejected words: (digit << 16 | slot), then the redrawn value
         uint32_t qn;
     } w[KW];
 };
 
+// Scatter addresses of the automorphism inside a 1024-slot chunk. With V = ((2 brev(s) + 1) k) mod 2N for source slot
+// s, the output slot's offset in its chunk is brev10 of W = the top 10 bits of V, and W is affine in the lane:
+// W = C + k (brev6(lane) + 64 brev4(j)) mod 1024 for the lane's word j. Storing the word at rotr1(W) (a 10-bit rotate
+// right) makes both the 64 lanes' writes of one j and the reads of output offsets 16 lane + j fall on 32 distinct
+// banks per half wave; the offset 16 lane + j is read back from rotr1(64 brev4(j) + brev6(lane)).
+__device__ __forceinline__ uint32_t scat_addr(uint32_t w) { return (w >> 1) | ((w & 1) << 9); }
+__device__ __forceinline__ uint32_t brev4(uint32_t j) { return __brev(j) >> 28; }
+
+// KSKA value of an accepted word v < floor((2^32-1)/p) p. MU2: floor((2^32-1)/p) = 2 (every p > (2^32-1)/3), where
+// v < 2p needs one conditional subtraction.
+template <bool MU2>
+__device__ __forceinline__ uint32_t kska_value(const Expander& ex, uint32_t v) {
+    return MU2 ? min(v, v - ex.p) : ex.red(v);
+}
+
+struct FastCtx {
+    const KsArgs* A;
+    const KeyTab* T;
+    FastLds* L;
+    FastLds::Wave* W;
+    int lane, lp, slot, logn, m0;
+    bool acc_out, pc0;
+    uint32_t p, pm, n16, mask2n, chunk0, s0, bs0, rb;
+    size_t trow;
+};
+
+template <int NDIG, bool MU2>
+__device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, const Expander& ex, int r) {
+    const KsArgs& A = *C.A;
+    const KeyTab& T = *C.T;
+    FastLds& L = *C.L;
+    FastLds::Wave& W = *C.W;
+    const int lane = C.lane, lp = C.lp;
+    const uint32_t p = C.p, s0 = C.s0;
+    const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)C.slot * T.row_words + s0;
+    const size_t dstride = (size_t)T.srows * T.row_words;
+    uint32_t seed[8];
+    const uint32_t* sp = T.seed[r];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) seed[i] = sp[i];
+    if (lane == 0) W.qn = 0;
+    wave_sync();
+    // s1 = sum_d D_d a_d, a regenerated (one ChaCha12 block per lane and digit); rejected words contribute later
+    uint64_t acc[DS];
+#pragma unroll
+    for (int k = 0; k < DS; ++k) acc[k] = 0;
+    uint32_t rejd[NDIG], based[NDIG];
+#pragma unroll
+    for (int d = 0; d < NDIG; ++d) {
+        uint32_t a[DS];
+        chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
+        uint32_t rej = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
+        uint32_t base = 0;
+        if (rej) {
+            const uint32_t cnt = __builtin_popcount(rej);
+            base = atomicAdd(&W.qn, cnt);
+            if (base + cnt <= (uint32_t)FQCAP) {
+                uint32_t m = rej, i = base;
+#pragma unroll 1
+                while (m) {
+                    const int j = __builtin_ctz(m);
+                    m &= m - 1;
+                    W.q[i++] = (uint32_t)d << 16 | (lane * DS + j);
+                }
+            } else {
+                // the queue is full (rejection rates far above any prime of this path's): redraw in the lane
+                uint32_t m = rej;
+                while (m) {
+                    const int j = __builtin_ctz(m);
+                    m &= m - 1;
+                    uint32_t v = 0;
+                    for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+                        v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * C.n16, (uint32_t)d, p, TAG_KSKA, j);
+                        if (v < ex.mp) break;
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? v : a[jj];
+                }
+                rej = 0;
+            }
+        }
+        rejd[d] = rej;
+        based[d] = base;
+        uint32_t x[DS];
+        ld16(L.D[d] + lp, x);
+#pragma unroll
+        for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * ((rej >> k) & 1 ? 0 : kska_value<MU2>(ex, a[k]));
+        // materialise the sums here: this digit's a words die before the next block is computed
+#pragma unroll
+        for (int k = 0; k < DS; ++k) asm volatile("" : "+v"(acc[k]));
+    }
+    // the key's b rows: they arrive while the queued words are redrawn and are consumed last
+    uint32_t b[NDIG][DS];
+#pragma unroll
+    for (int d = 0; d < NDIG; ++d) ld16(kb + d * dstride, b[d]);
+    // redraw the queued words: entry <- accepted value mod p
+    wave_sync();
+    const uint32_t nq = min(W.qn, (uint32_t)FQCAP);
+    for (uint32_t i = lane; i < nq; i += DBX) {
+        const uint32_t it = W.q[i], d = it >> 16, sl = it & 0xFFFF;
+        const uint32_t ctr = (C.chunk0 + sl) >> 4;
+        uint32_t v = 0;
+        for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+            v = chacha12_word(seed, ctr + (uint32_t)tt * C.n16, d, p, TAG_KSKA, (int)(sl & 15));
+            if (v < ex.mp) break;
+        }
+        W.q[i] = ex.red(v);
+    }
+    uint32_t r0[DS], r1[DS];
+#pragma unroll
+    for (int k = 0; k < DS; ++k) r1[k] = red(acc[k]);
+    // s0 = sum_d D_d b_d (+ P c0 folded in: ndig + 1 <= 4 products of (p - 1)^2 < 2^62)
+    uint32_t cw[DS];
+    if (C.m0) ld16(L.c0 + lp, cw);
+#pragma unroll
+    for (int k = 0; k < DS; ++k) acc[k] = (C.m0 == 2 || !C.pc0) ? 0 : (uint64_t)cw[k] * C.pm;
+#pragma unroll
+    for (int d = 0; d < NDIG; ++d) {
+        uint32_t x[DS];
+        ld16(L.D[d] + lp, x);
+#pragma unroll
+        for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * b[d][k];
+    }
+#pragma unroll
+    for (int k = 0; k < DS; ++k) r0[k] = red(acc[k]);
+    if (C.m0 == 2) {
+#pragma unroll
+        for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], cw[k], p);
+    }
+    const uint32_t kexp = A.autok[r];
+    uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + C.trow;
+    uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + C.trow;
+    const uint32_t cb = ((2 * C.bs0 + 1) * kexp) & C.mask2n;
+    const uint32_t step = (kexp << (C.logn - 3)) & C.mask2n;
+    const int sh = C.logn - 9;
+    const uint32_t ob = (automorph_slot(kexp, C.chunk0, C.logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
+    uint32_t* buf = W.buf;
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+        uint32_t(&rv)[DS] = part ? r1 : r0;
+#pragma unroll
+        for (int k = 0; k < DS; ++k) buf[scat_addr(((cb + brev4(k) * step) & C.mask2n) >> sh)] = rv[k];
+        if (part == 1) {
+            // the redrawn words of this lane: add D_d a_d into their slots
+#pragma unroll
+            for (int d = 0; d < NDIG; ++d) {
+                uint32_t m = rejd[d], i = based[d];
+#pragma unroll 1
+                while (m) {
+                    const uint32_t j = __builtin_ctz(m);
+                    m &= m - 1;
+                    const uint32_t add = red.mul(L.D[d][lp + j], W.q[i++]);
+                    const uint32_t o = scat_addr(((cb + brev4(j) * step) & C.mask2n) >> sh);
+                    buf[o] = addm(buf[o], add, p);
+                }
+            }
+        }
+        wave_sync();
+        uint32_t v[DS];
+#pragma unroll
+        for (int j = 0; j < DS; ++j) v[j] = buf[C.rb + 32 * brev4(j)];
+        uint32_t* o = (part ? o1 : o0) + ob;
+        if (C.acc_out) {
+            uint32_t e[DS];
+            ld16(o, e);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) v[k] = addm(v[k], e[k], p);
+        }
+        st16(o, v);
+        wave_sync();
+    }
+}
+
 template <int NDIG>
 __global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, int logn) {
     static_assert(NDIG >= 1 && NDIG <= MAXD, "digits staged in LDS");
+    static_assert(3 * sizeof(FastLds) <= 160 * 1024, "three workgroups per CU");
     __shared__ FastLds L;
     // the wave index is uniform across the wave: in scalar registers, so are its key, seed and row pointers
     const int lane = threadIdx.x & (DBX - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / DBX);
     const int t = (int)A.rows[blockIdx.y];
     const PrimeConst& q = A.pr[t];
-    const uint32_t p = (uint32_t)q.p;
+    FastCtx C;
+    C.A = &A;
+    C.T = &T;
+    C.L = &L;
+    C.W = &L.w[wv];
+    C.lane = lane;
+    C.lp = padw(lane * DS);  // this lane's 16 words in the padded rows
+    C.slot = slot_of(T, t, A.nq);
+    C.logn = logn;
+    C.m0 = A.c0_mode & 3;
+    C.acc_out = (A.c0_mode & PC_KS_ACC) != 0;
+    C.pc0 = C.m0 == 1 && t < A.nq;
+    C.p = (uint32_t)q.p;
+    C.pm = C.pc0 ? ((const uint32_t*)A.pmod)[t] : 0;
+    C.n16 = (1u << logn) >> 4;
+    C.mask2n = (2u << logn) - 1;
+    C.chunk0 = blockIdx.x * DCH;
+    C.s0 = C.chunk0 + lane * DS;
+    C.bs0 = brev_n(C.s0, logn);
+    C.rb = scat_addr(__brev((uint32_t)lane) >> 26);  // read base of output offsets 16 lane + j
+    C.trow = (size_t)t << logn;
     const Red red(q);
-    const Expander ex(p);
-    const uint32_t n16 = (1u << logn) >> 4;
-    const uint32_t mask2n = (2u << logn) - 1;
-    const uint32_t chunk0 = blockIdx.x * DCH;
-    const uint32_t s0 = chunk0 + lane * DS;
-    const int slot = slot_of(T, t, A.nq);
-    const int m0 = A.c0_mode & 3;
-    const bool acc_out = (A.c0_mode & PC_KS_ACC) != 0;
+    const Expander ex(C.p);
     const int kpg = (A.R + (int)gridDim.z - 1) / (int)gridDim.z;
     const int r_lo = blockIdx.z * kpg, r_hi = min(A.R, r_lo + kpg);
-    const bool pc0 = m0 == 1 && t < A.nq;
-    const uint32_t pm = pc0 ? ((const uint32_t*)A.pmod)[t] : 0;
-    const uint32_t bs0 = brev_n(s0, logn);
-    auto& W = L.w[wv];
-    DotCtx X{&A, 0, t < A.nq ? A.digit_of[t] : -1, t, (size_t)t << logn, chunk0};
+    DotCtx X{&A, 0, t < A.nq ? A.digit_of[t] : -1, t, C.trow, C.chunk0};
 #pragma unroll
     for (int d = 0; d < NDIG; ++d) {
-        const uint4* D = (const uint4*)(X.dptr(d) + chunk0);
-        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i] = D[i];
+        const uint4* D = (const uint4*)(X.dptr(d) + C.chunk0);
+        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i + (i >> 2)] = D[i];
     }
-    if (m0) {
-        const uint4* C0 = (const uint4*)((const uint32_t*)A.c0 + X.trow + chunk0);
-        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i] = C0[i];
+    if (C.m0) {
+        const uint4* C0 = (const uint4*)((const uint32_t*)A.c0 + C.trow + C.chunk0);
+        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i + (i >> 2)] = C0[i];
     }
     __syncthreads();
-    for (int r = r_lo + wv; r < r_hi; r += KW) {
-        const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)slot * T.row_words + s0;
-        const size_t dstride = (size_t)T.srows * T.row_words;
-        uint32_t seed[8];
-        const uint32_t* sp = T.seed[r];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) seed[i] = sp[i];
-        if (lane == 0) W.qn = 0;
-        wave_sync();
-        // s1 = sum_d D_d a_d, a regenerated (one ChaCha12 block per lane and digit)
-        uint64_t acc[DS];
-#pragma unroll
-        for (int k = 0; k < DS; ++k) acc[k] = 0;
-        uint32_t rejd[NDIG], based[NDIG];
-#pragma unroll
-        for (int d = 0; d < NDIG; ++d) {
-            uint32_t a[DS];
-            chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
-            uint32_t rej = 0;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
-            uint32_t base = 0;
-            if (rej) {
-                const uint32_t cnt = __builtin_popcount(rej);
-                base = atomicAdd(&W.qn, cnt);
-                if (base + cnt <= (uint32_t)FQCAP) {
-                    uint32_t m = rej, i = base;
-                    while (m) {
-                        const int j = __builtin_ctz(m);
-                        m &= m - 1;
-                        W.q[i++] = (uint32_t)d << 16 | (lane * DS + j);
-                    }
-                } else {
-                    // the queue is full (rejection rates far above any prime of this path's): redraw in the lane
-                    uint32_t m = rej;
-                    while (m) {
-                        const int j = __builtin_ctz(m);
-                        m &= m - 1;
-                        uint32_t v = 0;
-                        for (int tt = 1; tt < KSK_T_MAX; ++tt) {
-                            v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * n16, (uint32_t)d, p, TAG_KSKA, j);
-                            if (v < ex.mp) break;
-                        }
-#pragma unroll
-                        for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? v : a[jj];
-                    }
-                    rej = 0;
-                }
-            }
-            rejd[d] = rej;
-            based[d] = base;
-            const uint32_t* x = L.D[d] + lane * DS;
-#pragma unroll
-            for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * ((rej >> k) & 1 ? 0 : ex.red(a[k]));
-            // materialise the sums here: this digit's a words die before the next block is computed
-#pragma unroll
-            for (int k = 0; k < DS; ++k) asm volatile("" : "+v"(acc[k]));
-        }
-        // the key's b rows: they arrive while the queued words are redrawn and are consumed last
-        uint32_t b[NDIG][DS];
-#pragma unroll
-        for (int d = 0; d < NDIG; ++d) ld16(kb + d * dstride, b[d]);
-        // redraw the queued words (entry <- accepted value), then each owner adds D_d a_d of its own words
-        wave_sync();
-        const uint32_t nq = min(W.qn, (uint32_t)FQCAP);
-        for (uint32_t i = lane; i < nq; i += DBX) {
-            const uint32_t it = W.q[i], d = it >> 16, sl = it & 0xFFFF;
-            const uint32_t ctr = (chunk0 + sl) >> 4;
-            uint32_t v = 0;
-            for (int tt = 1; tt < KSK_T_MAX; ++tt) {
-                v = chacha12_word(seed, ctr + (uint32_t)tt * n16, d, p, TAG_KSKA, (int)(sl & 15));
-                if (v < ex.mp) break;
-            }
-            W.q[i] = ex.red(v);
-        }
-        wave_sync();
-#pragma unroll
-        for (int d = 0; d < NDIG; ++d) {
-            const uint32_t rej = rejd[d];
-            if (!rej) continue;
-#pragma unroll
-            for (int k = 0; k < DS; ++k) {
-                if ((rej >> k) & 1) {
-                    const uint32_t idx = based[d] + __builtin_popcount(rej & ((1u << k) - 1));
-                    acc[k] += (uint64_t)L.D[d][lane * DS + k] * W.q[idx];
-                }
-            }
-        }
-        uint32_t r0[DS], r1[DS];
-#pragma unroll
-        for (int k = 0; k < DS; ++k) r1[k] = red(acc[k]);
-        // s0 = sum_d D_d b_d (+ P c0 folded in: ndig + 1 <= 4 products of (p - 1)^2 < 2^62)
-#pragma unroll
-        for (int k = 0; k < DS; ++k) acc[k] = (m0 == 2 || !pc0) ? 0 : (uint64_t)L.c0[lane * DS + k] * pm;
-#pragma unroll
-        for (int d = 0; d < NDIG; ++d) {
-            const uint32_t* x = L.D[d] + lane * DS;
-#pragma unroll
-            for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * b[d][k];
-        }
-#pragma unroll
-        for (int k = 0; k < DS; ++k) r0[k] = red(acc[k]);
-        if (m0 == 2) {
-#pragma unroll
-            for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], L.c0[lane * DS + k], p);
-        }
-        const uint32_t kexp = A.autok[r];
-        uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + X.trow;
-        uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + X.trow;
-        wave_sync();  // every owner has read its redrawn words before the queue becomes the scatter buffer
-        if (kexp == 1 && !acc_out) {
-            st16(o0 + s0, r0);
-            st16(o1 + s0, r1);
-            continue;
-        }
-        uint32_t* l0 = W.q;
-        uint32_t* l1 = W.q + DCH;
-        const uint32_t cb = ((2 * bs0 + 1) * kexp) & mask2n;
-        const uint32_t step = (kexp << (logn - 3)) & mask2n;
-#pragma unroll
-        for (int k = 0; k < DS; ++k) {
-            const uint32_t b4 = ((k & 1) << 3) | ((k & 2) << 1) | ((k & 4) >> 1) | ((k & 8) >> 3);
-            const uint32_t o = brev_n(((cb + b4 * step) & mask2n) >> 1, logn) & (DCH - 1);
-            l0[o] = r0[k];
-            l1[o] = r1[k];
-        }
-        wave_sync();
-        const uint32_t ob = (automorph_slot(kexp, chunk0, logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
-        uint32_t v0[DS], v1[DS];
-        ld16(l0 + lane * DS, v0);
-        ld16(l1 + lane * DS, v1);
-        if (acc_out) {
-            uint32_t e0[DS], e1[DS];
-            ld16(o0 + ob, e0);
-            ld16(o1 + ob, e1);
-#pragma unroll
-            for (int k = 0; k < DS; ++k) {
-                v0[k] = addm(v0[k], e0[k], p);
-                v1[k] = addm(v1[k], e1[k], p);
-            }
-        }
-        st16(o0 + ob, v0);
-        st16(o1 + ob, v1);
-        wave_sync();
+    if (ex.mu == 2) {
+        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, true>(C, red, ex, r);
+    } else {
+        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, false>(C, red, ex, r);
     }
 }
 

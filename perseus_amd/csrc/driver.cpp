@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "pc_hip.h"
+#include "fused.h"
 
 typedef unsigned __int128 u128;
 
@@ -223,6 +224,9 @@ struct pcx_ctx {
     PrimeConst* pr = nullptr;
     uint32_t *fw = nullptr, *fws = nullptr, *iw = nullptr, *iws = nullptr, *ninv = nullptr, *ninvs = nullptr;
     uint32_t *pmod = nullptr, *pinv = nullptr;  // values then Shoup companions, by prime id
+    uint32_t* mdt = nullptr;  // ModDown conversion matrix M[j][t] = [P / p_j]_{q_t}, j < kp, t < nq
+    int md_fused = 1;         // ModDown conversion inside the NTT column pass (kp <= MDC_MAX_KP)
+    int md_ntg = 5;           // its target rows per workgroup
     int32_t* digit_of = nullptr;
     std::vector<Level> levels;
     uint32_t *coef = nullptr, *digits = nullptr, *ext = nullptr, *conv = nullptr;
@@ -522,6 +526,37 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
         Stage st(c, 4, s);
         if (int e = c->tab->ntt_inv(&a, s)) return e;
     }
+    const Rows& rn = L->md_ntt[m - 1];
+    NttArgs f = ntt_args(c, c->conv, rn, rn.n);
+    f.epi = 1;
+    f.eout = out;
+    f.ex = ext;
+    f.xnum = 1;
+    f.es = c->pinv;
+    f.ess = c->pinv + (c->nq + c->kp);
+    if (c->md_fused) {
+        // the conversion inside the NTT's column pass, then the row pass with the epilogue
+        pch::MdcArgs d;
+        d.ext = (const uint32_t*)ext;
+        d.conv = c->conv;
+        d.mt = c->mdt;
+        d.pr = c->pr;
+        d.fw = c->fw;
+        d.fws = c->fws;
+        d.nq = c->nq;
+        d.kp = c->kp;
+        d.rows = c->rows;
+        d.top = top;
+        d.ntg = c->md_ntg;
+        d.m = m;
+        d.lazy = c->lazy;
+        {
+            Stage st(c, 5, s);
+            if (int e = pch::md_conv_cols((int)c->logn, &d, s)) return e;
+        }
+        Stage st(c, 6, s);
+        return pch::ntt_fwd_rows_only((int)c->logn, &f, s);
+    }
     BconvArgs b;
     memset(&b, 0, sizeof b);
     b.src = ext;
@@ -535,14 +570,6 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
         Stage st(c, 5, s);
         if (int e = c->tab->bconv(&b, s)) return e;
     }
-    const Rows& rn = L->md_ntt[m - 1];
-    NttArgs f = ntt_args(c, c->conv, rn, rn.n);
-    f.epi = 1;
-    f.eout = out;
-    f.ex = ext;
-    f.xnum = 1;
-    f.es = c->pinv;
-    f.ess = c->pinv + (c->nq + c->kp);
     Stage st(c, 6, s);
     return c->tab->ntt_fwd(&f, s);
 }
@@ -652,6 +679,9 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     // rows per NTT pass pair (0: one pass pair over all rows, measured fastest; PCX_NTT_CHUNK overrides)
     c->chunk = 0;
     if (const char* e = getenv("PCX_NTT_CHUNK")) c->chunk = atoi(e);
+    c->md_fused = kp <= pch::MDC_MAX_KP ? 1 : 0;
+    if (const char* e = getenv("PCX_MD_FUSED")) c->md_fused = c->md_fused && atoi(e) != 0;
+    if (const char* e = getenv("PCX_MD_NTG")) c->md_ntg = std::max(1, atoi(e));
     const int R = c->rows;
     // prime constants and twiddles (crates/pc-gpu/src/context.rs:186-230)
     std::vector<PrimeConst> pc;
@@ -703,6 +733,18 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     }
     c->pmod = c->dev.upload(pm2);
     c->pinv = c->dev.upload(pi2);
+    {
+        std::vector<uint32_t> mt((size_t)kp * nq);
+        for (int jj = 0; jj < kp; ++jj)
+            for (int t = 0; t < nq; ++t) {
+                const uint64_t q = c->primes[t];
+                uint64_t v = 1;
+                for (int k = 0; k < kp; ++k)
+                    if (k != jj) v = mulmod(v, c->primes[nq + k] % q, q);
+                mt[(size_t)jj * nq + t] = (uint32_t)v;
+            }
+        c->mdt = c->dev.upload(mt);
+    }
     std::vector<int32_t> dof(R);
     for (int t = 0; t < R; ++t) dof[t] = c->digit(t);
     c->digit_of = c->dev.upload(dof);

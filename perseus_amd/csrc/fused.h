@@ -1,0 +1,33 @@
+// Driver-internal launchers that fuse stages of the key-switching path beyond the kernel-table entries: the ModDown
+// base conversion inside the forward NTT's column pass, and the forward row pass (with its epilogue) on its own.
+// Not part of the C ABI; the driver (driver.cpp) is their only caller.
+#pragma once
+#include <stdint.h>
+
+#include "pc_hip.h"
+
+namespace pch {
+
+// Conversion P -> Q rows 0..top of m extended ciphertexts, each target row then taken through the forward NTT's
+// column pass. ext: [c][part][rows][N] whose P rows (ids nq .. nq + kp - 1) hold y_j = [x_j N^-1 pre_j]_{p_j} in
+// coefficient order (the INTT's output); conv: same layout, receives the column pass of conv_t = sum_j y_j M[j][t]
+// mod q_t in its Q rows (lazy words, as the plain column pass leaves them); mt: M[j][t] = [P / p_j]_{q_t}, row stride
+// nq; ntg: target rows per workgroup.
+struct MdcArgs {
+    const uint32_t* ext;
+    uint32_t* conv;
+    const uint32_t* mt;
+    const PrimeConst* pr;
+    const uint32_t* fw;
+    const uint32_t* fws;
+    int nq, kp, rows, top, ntg, m, lazy;
+};
+constexpr int MDC_MAX_KP = 6;
+// 0, or -1 (bad arguments), -2 (kp outside 1..MDC_MAX_KP or logn outside 12..16), or a HIP error
+int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s);
+
+// The forward transform's row pass alone (grid of every row of a), epilogue a->epi included: completes a forward NTT
+// whose column pass was done by md_conv_cols.
+int ntt_fwd_rows_only(int logn, const NttArgs* a, pc_stream_t s);
+
+}  // namespace pch

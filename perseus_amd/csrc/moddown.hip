@@ -1,0 +1,113 @@
+// ModDown's conversion fused into the forward NTT (crates/pc-gpu/src/ks.rs:1620-1649 moddown_to_j: INTT of the P rows,
+// bconv P -> Q, NTT with the epilogue (x - conv) P^-1; host twin crates/pc-host/src/bconv.rs, ntt.rs).
+//
+// A conversion output row is only ever read by the forward NTT's column pass, and that pass works on whole columns:
+// the words j = r C + c of one column c are a contiguous set of coefficient positions of every row. So one workgroup
+// takes a block of CC columns of one (ciphertext, part): it keeps the kp source words y_j of each of its positions
+// in registers (kp <= 6, loaded once), and for each of its target rows t forms conv_t = sum_j y_j M[j][t] mod q_t and
+// runs the column pass of prime t on it before writing. The conversion rows never reach HBM: per key switch this saves
+// writing and re-reading 2 (top + 1) rows. Targets are split into groups of ntg rows per workgroup so that a launch has
+// several workgroups per CU; the groups of one column block are neighbours in the XCD-aware order, so the second and
+// later reads of the block's sources hit that XCD's L2.
+#include "fused.h"
+#include "ntt_core.h"
+
+namespace pch {
+namespace ntt {
+
+template <int LOGN, bool H, int KP>
+__global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
+    using G = Geo<LOGN>;
+    __shared__ uint32_t lds[2][G::COL_LDS];
+    const Blk B = blk_xy();
+    const int ng = gridDim.x / G::COL_WGS;
+    const int grp = B.x % ng, cbk = B.x / ng;
+    const size_t rb = (size_t)B.y * A.rows;  // row 0 of (ciphertext, part) B.y
+    const int col = threadIdx.x % G::CC, tau = threadIdx.x / G::CC;
+    const int c = cbk * G::CC + col;
+    // the sources at positions (tau + TR e) C + c: the column pass's layout A
+    uint32_t y[KP][E];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        const uint32_t* src = A.ext + ((rb + A.nq + j) << LOGN);
+#pragma unroll
+        for (int e = 0; e < E; ++e) y[j][e] = src[(size_t)(tau + G::TR * e) * G::C + c];
+    }
+    const int t0 = grp * A.ntg, t1 = min(A.top + 1, t0 + A.ntg);
+    auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
+    constexpr int LS = G::CC + G::CPAD;
+    for (int t = t0; t < t1; ++t) {
+        const Red red(A.pr[t]);
+        const uint32_t p = red.p, p2 = 2 * p;
+        uint32_t m[KP];
+#pragma unroll
+        for (int j = 0; j < KP; ++j) m[j] = A.mt[j * A.nq + t];
+        // sum_j y_j M[j][t]: products below 2^62, so three to a 64-bit sum
+        uint32_t x[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            uint64_t a0 = 0, a1 = 0;
+#pragma unroll
+            for (int j = 0; j < KP; ++j) {
+                if (j < 3) a0 += (uint64_t)y[j][e] * m[j];
+                else a1 += (uint64_t)y[j][e] * m[j];
+            }
+            x[e] = KP > 3 ? addm(red(a0), red(a1), p) : red(a0);
+        }
+        const uint32_t* w = A.fw + ((size_t)t << LOGN);
+        const uint32_t* ws = A.fws + ((size_t)t << LOGN);
+        phase_a<true, H, G::TR>(x, w, ws, p, p2, base);
+        // double-buffered transpose: one barrier per target
+        uint32_t* l = lds[t & 1];
+#pragma unroll
+        for (int e = 0; e < E; ++e) l[(tau + G::TR * e) * LS + col] = x[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = l[(E * tau + e) * LS + col];
+        phase_b<true, H, G::TR>(x, tau, w, ws, p, p2, base);
+        uint32_t* out = A.conv + ((rb + t) << LOGN);
+#pragma unroll
+        for (int e = 0; e < E; ++e) out[(size_t)(E * tau + e) * G::C + c] = x[e];  // lazy words
+    }
+}
+
+template <int LOGN, bool H>
+void mdc_launch(const MdcArgs& a, hipStream_t st) {
+    using G = Geo<LOGN>;
+    const int ng = (a.top + 1 + a.ntg - 1) / a.ntg;
+    const dim3 grid(G::COL_WGS * ng, 2 * a.m);
+    switch (a.kp) {
+        case 1: hipLaunchKernelGGL((md_conv_cols_k<LOGN, H, 1>), grid, dim3(WG), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((md_conv_cols_k<LOGN, H, 2>), grid, dim3(WG), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((md_conv_cols_k<LOGN, H, 3>), grid, dim3(WG), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((md_conv_cols_k<LOGN, H, 4>), grid, dim3(WG), 0, st, a); break;
+        case 5: hipLaunchKernelGGL((md_conv_cols_k<LOGN, H, 5>), grid, dim3(WG), 0, st, a); break;
+        default: hipLaunchKernelGGL((md_conv_cols_k<LOGN, H, 6>), grid, dim3(WG), 0, st, a); break;
+    }
+}
+
+template <int LOGN>
+int mdc(const MdcArgs* a, pc_stream_t s) {
+    if (a->lazy) mdc_launch<LOGN, true>(*a, (hipStream_t)s);
+    else mdc_launch<LOGN, false>(*a, (hipStream_t)s);
+    return launch_rc();
+}
+
+}  // namespace ntt
+
+int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s) {
+    if (!a || !a->ext || !a->conv || !a->mt || !a->pr || !a->fw || !a->fws) return -1;
+    if (a->m < 0 || a->top < 0 || a->top >= a->nq || a->ntg < 1 || a->rows < a->nq + a->kp) return -1;
+    if (a->kp < 1 || a->kp > MDC_MAX_KP) return -2;
+    if (a->m == 0) return 0;
+    switch (logn) {
+        case 12: return ntt::mdc<12>(a, s);
+        case 13: return ntt::mdc<13>(a, s);
+        case 14: return ntt::mdc<14>(a, s);
+        case 15: return ntt::mdc<15>(a, s);
+        case 16: return ntt::mdc<16>(a, s);
+        default: return -2;
+    }
+}
+
+}  // namespace pch

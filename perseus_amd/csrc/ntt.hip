@@ -18,218 +18,11 @@
 // Butterflies are lazy. When every prime of the launch is below 2^30 (NttArgs.lazy != 0) they are Harvey's: forward
 // words in [0, 4p), inverse words in [0, 2p). Otherwise (primes up to 2^31, where 4p overflows a word) forward words
 // stay in [0, 2p) and inverse words canonical. Either way a transform returns canonical words.
-#include "common.h"
+#include "fused.h"
+#include "ntt_core.h"
 
 namespace pch {
 namespace ntt {
-
-constexpr int E = 16;     // words per thread
-constexpr int WG = 256;   // threads per workgroup
-
-template <int LOGN>
-struct Geo {
-    static constexpr int LR = LOGN / 2, LC = LOGN - LR;
-    static constexpr int N = 1 << LOGN, R = 1 << LR, C = 1 << LC;
-    static constexpr int TR = R / E, TC = C / E;   // threads per column / row sub-transform
-    static constexpr int CC = WG / TR;             // columns per column-pass workgroup
-    static constexpr int BB = WG / TC;             // blocks per row-pass workgroup
-    static constexpr int COL_WGS = C / CC;         // column-pass workgroups per row
-    static constexpr int ROW_WGS = R / BB;         // row-pass workgroups per row
-    static constexpr int CPAD = CC == 16 ? 1 : 0;  // LDS row padding of the column pass
-    static constexpr int COL_LDS = R * (CC + CPAD);
-    static constexpr int ROW_LDS = BB * (C + C / E);
-    static_assert(TR >= 2 && TC >= 2 && TR <= E && TC <= E, "sub-transforms of 32 to 256 points");
-};
-
-// ------------------------------------------------------------------------------------------------ butterflies
-// H: Harvey (every prime < 2^30). p2 = 2p.
-template <bool H>
-__device__ __forceinline__ void ct(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p, uint32_t p2) {
-    uint32_t t = shoup_lz(b, w, ws, p);  // [0, 2p)
-    if (H) {
-        const uint32_t u = min(a, a - p2);  // [0, 4p) -> [0, 2p)
-        a = u + t;
-        b = u - t + p2;
-    } else {
-        const uint32_t u = min(a, a - p);  // [0, 2p) -> [0, p)
-        t = min(t, t - p);
-        a = u + t;
-        b = u - t + p;
-    }
-}
-template <bool H>
-__device__ __forceinline__ void gs(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p, uint32_t p2) {
-    const uint32_t u = a, v = b;
-    if (H) {  // [0, 2p) in and out
-        const uint32_t s = u + v;
-        a = min(s, s - p2);
-        b = shoup_lz(u - v + p2, w, ws, p);
-    } else {  // canonical in and out
-        a = addm(u, v, p);
-        const uint32_t d = shoup_lz(u - v + p, w, ws, p);
-        b = min(d, d - p);
-    }
-}
-// a forward lazy word as its residue
-template <bool H>
-__device__ __forceinline__ uint32_t canon(uint32_t a, uint32_t p, uint32_t p2) {
-    if (H) a = min(a, a - p2);
-    return min(a, a - p);
-}
-
-// NG consecutive twiddles of one stage in one vector load: a stage's groups are NG = 8 / (h / T) (layout A) or 8 / h
-// (layout B) consecutive table entries, and their first index is a multiple of NG.
-template <int NG>
-__device__ __forceinline__ void ldtw(const uint32_t* p, uint32_t (&v)[8]) {
-    if constexpr (NG == 8) {
-        const uint4 a = ((const uint4*)p)[0], b = ((const uint4*)p)[1];
-        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
-    } else if constexpr (NG == 4) {
-        const uint4 a = *(const uint4*)p;
-        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
-    } else if constexpr (NG == 2) {
-        const uint2 a = *(const uint2*)p;
-        v[0] = a.x, v[1] = a.y;
-    } else {
-        v[0] = *p;
-    }
-}
-
-// Layout A (e = tau + T j), stage h = T 2^K: pairs (j, j + 2^K), group j / 2^(K+1), index base(h) + group.
-template <bool FWD, bool H, int T, int K, class Base>
-__device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p,
-                                        uint32_t p2, Base base) {
-    constexpr int hh = 1 << K, NG = 8 >> K;
-    const uint32_t b0 = base(T << K);
-    uint32_t tw[8], tws[8];
-    ldtw<NG>(w + b0, tw);
-    ldtw<NG>(ws + b0, tws);
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        if (j & hh) continue;
-        const int g = j >> (K + 1);
-        if (FWD) ct<H>(x[j], x[j + hh], tw[g], tws[g], p, p2);
-        else gs<H>(x[j], x[j + hh], tw[g], tws[g], p, p2);
-    }
-}
-template <bool FWD, bool H, int T, class Base>
-__device__ __forceinline__ void phase_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p,
-                                        uint32_t p2, Base base) {
-    if (FWD) {
-        stage_a<FWD, H, T, 3>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 2>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 1>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 0>(x, w, ws, p, p2, base);
-    } else {
-        stage_a<FWD, H, T, 0>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 1>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 2>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 3>(x, w, ws, p, p2, base);
-    }
-}
-// Layout B (e = 16 tau + j), stage h = 2^K < T: pairs (j, j + h), group (16 tau + j) / (2h).
-template <bool FWD, bool H, int K, class Base>
-__device__ __forceinline__ void stage_b(uint32_t (&x)[E], int tau, const uint32_t* w, const uint32_t* ws, uint32_t p,
-                                        uint32_t p2, Base base) {
-    constexpr int h = 1 << K, NG = 8 >> K;
-    const uint32_t b0 = base(h) + ((uint32_t)(E * tau) >> (K + 1));
-    uint32_t tw[8], tws[8];
-    ldtw<NG>(w + b0, tw);
-    ldtw<NG>(ws + b0, tws);
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        if (j & h) continue;
-        const int g = j >> (K + 1);
-        if (FWD) ct<H>(x[j], x[j + h], tw[g], tws[g], p, p2);
-        else gs<H>(x[j], x[j + h], tw[g], tws[g], p, p2);
-    }
-}
-template <bool FWD, bool H, int T, class Base>
-__device__ __forceinline__ void phase_b(uint32_t (&x)[E], int tau, const uint32_t* w, const uint32_t* ws, uint32_t p,
-                                        uint32_t p2, Base base) {
-    constexpr int LT = T == 16 ? 4 : T == 8 ? 3 : T == 4 ? 2 : 1;
-    if (FWD) {
-        if (LT > 3) stage_b<FWD, H, 3>(x, tau, w, ws, p, p2, base);
-        if (LT > 2) stage_b<FWD, H, 2>(x, tau, w, ws, p, p2, base);
-        if (LT > 1) stage_b<FWD, H, 1>(x, tau, w, ws, p, p2, base);
-        stage_b<FWD, H, 0>(x, tau, w, ws, p, p2, base);
-    } else {
-        stage_b<FWD, H, 0>(x, tau, w, ws, p, p2, base);
-        if (LT > 1) stage_b<FWD, H, 1>(x, tau, w, ws, p, p2, base);
-        if (LT > 2) stage_b<FWD, H, 2>(x, tau, w, ws, p, p2, base);
-        if (LT > 3) stage_b<FWD, H, 3>(x, tau, w, ws, p, p2, base);
-    }
-}
-
-// Wave-level ordering of LDS traffic between the lanes of one wave.
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// A row-pass block's 16 words of thread tau through the block's LDS (C + C/16 words, one padding word per 16):
-// layout B (e = 16 tau + j) -> layout A (e = tau + T j) and back. The block lives in one wave.
-template <int T>
-__device__ __forceinline__ void b_to_a(uint32_t (&x)[E], uint32_t* l, int tau) {
-#pragma unroll
-    for (int j = 0; j < E; ++j) l[(E * tau + j) + tau] = x[j];
-    wave_sync();
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int e = tau + T * j;
-        x[j] = l[e + e / E];
-    }
-    wave_sync();
-}
-template <int T>
-__device__ __forceinline__ void a_to_b(uint32_t (&x)[E], uint32_t* l, int tau) {
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int e = tau + T * j;
-        l[e + e / E] = x[j];
-    }
-    wave_sync();
-#pragma unroll
-    for (int j = 0; j < E; ++j) x[j] = l[(E * tau + j) + tau];
-    wave_sync();
-}
-
-// The first pass's source words of row i: out of place (src + soff[i] N, the sum mod p of snum rows sstride apart)
-// or in place (base + roff[i] N).
-struct RowSrc {
-    const uint32_t* p0;
-    int n;
-    uint64_t stride;
-};
-__device__ __forceinline__ RowSrc row_src(const NttArgs& A, int i, int logn) {
-    if (A.soff) return RowSrc{(const uint32_t*)A.src + ((size_t)A.soff[i] << logn), A.snum, A.sstride};
-    return RowSrc{(const uint32_t*)A.base + ((size_t)A.roff[i] << logn), 1, 0};
-}
-__device__ __forceinline__ uint32_t ld_src(const RowSrc& s, size_t off, uint32_t p) {
-    uint32_t v = s.p0[off];
-    for (int k = 1; k < s.n; ++k) v = addm(v, s.p0[off + k * s.stride], p);
-    return v;
-}
-__device__ __forceinline__ void ld16_src(const RowSrc& s, size_t off, uint32_t p, uint32_t (&x)[E]) {
-    ld16(s.p0 + off, x);
-    for (int k = 1; k < s.n; ++k) {
-        uint32_t y[E];
-        ld16(s.p0 + off + k * s.stride, y);
-#pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = addm(x[j], y[j], p);
-    }
-}
-
-// the workgroup's logical (block in row, row) after the XCD renumbering of a (gx, rows) grid
-struct Blk {
-    int x, y;
-};
-__device__ __forceinline__ Blk blk_xy() {
-    const uint32_t n = gridDim.x * gridDim.y;
-    const uint32_t l = xcd_block(blockIdx.y * gridDim.x + blockIdx.x, n);
-    return Blk{(int)(l % gridDim.x), (int)(l / gridDim.x)};
-}
 
 // ------------------------------------------------------------------------------------------------ forward
 // Column pass: workgroup (x, row i) takes columns [x CC, x CC + CC) of row i.
@@ -452,7 +245,44 @@ int inv(const NttArgs* a, pc_stream_t s) {
     return launch_rc();
 }
 
+// the row pass alone over every row of the args (after a column pass done elsewhere)
+template <int LOGN>
+int fwd_rows_only(const NttArgs* a, pc_stream_t s) {
+    if (int rc = check(a, true)) return rc;
+    using G = Geo<LOGN>;
+    if (a->nrows == 0) return 0;
+    NttArgs B = *a;
+    B.soff = nullptr;
+    const dim3 g(G::ROW_WGS, B.nrows);
+    hipStream_t st = (hipStream_t)s;
+#define PCH_ROWS(HH)                                                                               \
+    switch (B.epi) {                                                                               \
+        case 0: hipLaunchKernelGGL((fwd_rows<LOGN, HH, 0>), g, dim3(WG), 0, st, B, 0); break;     \
+        case 1: hipLaunchKernelGGL((fwd_rows<LOGN, HH, 1>), g, dim3(WG), 0, st, B, 0); break;     \
+        case 2: hipLaunchKernelGGL((fwd_rows<LOGN, HH, 2>), g, dim3(WG), 0, st, B, 0); break;     \
+        default: hipLaunchKernelGGL((fwd_rows<LOGN, HH, 3>), g, dim3(WG), 0, st, B, 0); break;    \
+    }
+    if (B.lazy) {
+        PCH_ROWS(true)
+    } else {
+        PCH_ROWS(false)
+    }
+#undef PCH_ROWS
+    return launch_rc();
+}
+
 }  // namespace ntt
+
+int ntt_fwd_rows_only(int logn, const NttArgs* a, pc_stream_t s) {
+    switch (logn) {
+        case 12: return ntt::fwd_rows_only<12>(a, s);
+        case 13: return ntt::fwd_rows_only<13>(a, s);
+        case 14: return ntt::fwd_rows_only<14>(a, s);
+        case 15: return ntt::fwd_rows_only<15>(a, s);
+        case 16: return ntt::fwd_rows_only<16>(a, s);
+        default: return -2;
+    }
+}
 
 #define PCH_NTT_INST(L)                                                             \
     int ntt_fwd_##L(const NttArgs* a, pc_stream_t s) { return ntt::fwd<L>(a, s); } \

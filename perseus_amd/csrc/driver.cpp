@@ -515,7 +515,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
 
 // ModDown of m extended ciphertexts at ext into m ciphertexts at out (crates/pc-gpu/src/ks.rs:1620-1649): INTT of the
 // P rows (N^-1 pre_j), conversion P -> Q rows 0..top into conv, NTT of conv with the epilogue (ext - conv) P^-1
-int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
+int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc_stream_t s) {
     const Level* L = level(c, top);
     if (!L || m < 1 || m > c->k_rot) return -1;
     const Rows& ri = L->md_intt[m - 1];
@@ -527,7 +527,7 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
         if (int e = c->tab->ntt_inv(&a, s)) return e;
     }
     const Rows& rn = L->md_ntt[m - 1];
-    NttArgs f = ntt_args(c, c->conv, rn, rn.n);
+    NttArgs f = ntt_args(c, conv, rn, rn.n);
     f.epi = 1;
     f.eout = out;
     f.ex = ext;
@@ -538,7 +538,7 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
         // the conversion inside the NTT's column pass, then the row pass with the epilogue
         pch::MdcArgs d;
         d.ext = (const uint32_t*)ext;
-        d.conv = c->conv;
+        d.conv = conv;
         d.mt = c->mdt;
         d.pr = c->pr;
         d.fw = c->fw;
@@ -560,7 +560,7 @@ int moddown(pcx_ctx* c, void* ext, int m, int top, void* out, pc_stream_t s) {
     BconvArgs b;
     memset(&b, 0, sizeof b);
     b.src = ext;
-    b.dst = c->conv;
+    b.dst = conv;
     b.jobs = L->md_bconv.jobs;
     b.pool = L->md_bconv.pool;
     b.pr = c->pr;
@@ -1033,14 +1033,16 @@ const void* pcx_modup_digits(const pcx_ctx* c) { return c->digits; }
 int pcx_dot(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ext, pc_stream_t s) {
     return dot(c, k, r, 1, ct, top, ext, s);
 }
-int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s) { return moddown(c, ext, 1, top, out, s); }
+int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s) {
+    return c ? moddown(c, ext, c->conv, 1, top, out, s) : -1;
+}
 
 int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* out, pc_stream_t s) {
     if (!c || !k || r < 0 || r >= k->nkeys || !level(c, top)) return -1;
     if (k->galois[r] == 1) return copy_q(c, ct, top, out, s);
     if (int e = modup(c, ct, top, s)) return e;
     if (int e = dot(c, k, r, 1, ct, top, c->ext, s)) return e;
-    return moddown(c, c->ext, 1, top, out, s);
+    return moddown(c, c->ext, c->conv, 1, top, out, s);
 }
 
 int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
@@ -1069,7 +1071,7 @@ int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const voi
         int m = 1;
         while (j + m < n && m < c->k_rot && idx[j + m] == idx[j] + m && k->galois[idx[j + m]] != 1) ++m;
         if (int e = dot(c, k, idx[j], m, ct, top, c->ext, s)) return e;
-        if (int e = moddown(c, c->ext, m, top, (uint32_t*)out + j * cw, s)) return e;
+        if (int e = moddown(c, c->ext, c->conv, m, top, (uint32_t*)out + j * cw, s)) return e;
         j += m;
     }
     return 0;

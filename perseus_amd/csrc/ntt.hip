@@ -81,14 +81,20 @@ __global__ void __launch_bounds__(WG) fwd_rows(NttArgs A, int row0) {
     uint32_t* a = (uint32_t*)A.base + r0;
     uint32_t x[E];
     ld16(a, x);
+    // the epilogue's operand is loaded with the row: every HBM read of the workgroup is in flight before the butterflies
+    uint32_t ex[E];
+    if (EPI != 0) ld16_src(RowSrc{(const uint32_t*)A.ex, A.xnum, A.xstride}, r0, p, ex);
     constexpr int LS = G::C + G::C / E;
     uint32_t* l = lds + lb * LS;
-    b_to_a<G::TC>(x, l, tau);
     // stage of half distance h (words): index N/(2h) + blk C/(2h) + c/(2h)
     auto base = [blk](int h) { return (uint32_t)((G::N / (2 * h)) + blk * (G::C / (2 * h))); };
-    phase_a<true, H, G::TC>(x, w, ws, p, p2, base);
+    Tw ta, tb;
+    load_tw_a<G::TC>(ta, w, ws, base);
+    load_tw_b<G::TC>(tb, tau, w, ws, base);
+    b_to_a<G::TC>(x, l, tau);
+    phase_a_t<true, H>(x, ta, p, p2);
     a_to_b<G::TC>(x, l, tau);
-    phase_b<true, H, G::TC>(x, tau, w, ws, p, p2, base);
+    phase_b_t<true, H, G::TC>(x, tb, p, p2);
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = canon<H>(x[j], p, p2);
     if (EPI == 0) {
@@ -96,8 +102,6 @@ __global__ void __launch_bounds__(WG) fwd_rows(NttArgs A, int row0) {
         return;
     }
     const uint32_t s = ((const uint32_t*)A.es)[pid], ss = ((const uint32_t*)A.ess)[pid];
-    uint32_t ex[E];
-    ld16_src(RowSrc{(const uint32_t*)A.ex, A.xnum, A.xstride}, r0, p, ex);
     uint32_t* o = (uint32_t*)A.eout + r0;
     uint32_t d[E];
     if (EPI == 2) ld16(A.ed ? (const uint32_t*)A.ed + r0 : o, d);
@@ -131,11 +135,14 @@ __global__ void __launch_bounds__(WG) inv_rows(NttArgs A, int row0) {
     uint32_t x[E];
     ld16_src(src, e0, p, x);
     auto base = [blk](int h) { return (uint32_t)((G::N / (2 * h)) + blk * (G::C / (2 * h))); };
-    phase_b<false, H, G::TC>(x, tau, w, ws, p, p2, base);
+    Tw ta, tb;
+    load_tw_b<G::TC>(tb, tau, w, ws, base);
+    load_tw_a<G::TC>(ta, w, ws, base);
+    phase_b_t<false, H, G::TC>(x, tb, p, p2);
     constexpr int LS = G::C + G::C / E;
     uint32_t* l = lds + lb * LS;
     b_to_a<G::TC>(x, l, tau);
-    phase_a<false, H, G::TC>(x, w, ws, p, p2, base);
+    phase_a_t<false, H>(x, ta, p, p2);
     a_to_b<G::TC>(x, l, tau);
     st16((uint32_t*)A.base + ((size_t)A.roff[i] << LOGN) + e0, x);  // [0, 2p) (Harvey) or canonical
 }

@@ -145,6 +145,86 @@ __device__ __forceinline__ void phase_b(uint32_t (&x)[E], int tau, const uint32_
     }
 }
 
+// A phase's twiddles preloaded into registers (15 values and 15 Shoup companions: the 1 + 2 + 4 + 8 group twiddles of
+// its four stages, stage K's NG = 8 >> K at offset NG - 1), so that every load of a pass can be issued before its
+// first LDS transpose.
+struct Tw {
+    uint32_t w[15], s[15];
+};
+template <int NG>
+__device__ __forceinline__ void ldtw_at(const uint32_t* p, uint32_t* v) {
+    uint32_t t[8];
+    ldtw<NG>(p, t);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) v[i] = t[i];
+}
+// layout A, stages h = T 2^K (K = 0..3)
+template <int T, class Base>
+__device__ __forceinline__ void load_tw_a(Tw& t, const uint32_t* w, const uint32_t* ws, Base base) {
+#define PCH_LA(K)                                                    \
+    {                                                                \
+        const uint32_t b0 = base(T << K);                            \
+        ldtw_at<(8 >> K)>(w + b0, t.w + ((8 >> K) - 1));             \
+        ldtw_at<(8 >> K)>(ws + b0, t.s + ((8 >> K) - 1));            \
+    }
+    PCH_LA(3) PCH_LA(2) PCH_LA(1) PCH_LA(0)
+#undef PCH_LA
+}
+// layout B, stages h = 2^K < T
+template <int T, class Base>
+__device__ __forceinline__ void load_tw_b(Tw& t, int tau, const uint32_t* w, const uint32_t* ws, Base base) {
+    constexpr int LT = T == 16 ? 4 : T == 8 ? 3 : T == 4 ? 2 : 1;
+#define PCH_LB(K)                                                                    \
+    if (LT > K) {                                                                    \
+        const uint32_t b0 = base(1 << K) + ((uint32_t)(E * tau) >> (K + 1));         \
+        ldtw_at<(8 >> K)>(w + b0, t.w + ((8 >> K) - 1));                             \
+        ldtw_at<(8 >> K)>(ws + b0, t.s + ((8 >> K) - 1));                            \
+    }
+    PCH_LB(3) PCH_LB(2) PCH_LB(1) PCH_LB(0)
+#undef PCH_LB
+}
+// one stage of pairs (j, j + 2^K) over preloaded twiddles (both layouts: the group of j is j >> (K + 1))
+template <bool FWD, bool H, int K>
+__device__ __forceinline__ void stage_t(uint32_t (&x)[E], const Tw& t, uint32_t p, uint32_t p2) {
+    constexpr int hh = 1 << K, o = (8 >> K) - 1;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        if (j & hh) continue;
+        const int g = j >> (K + 1);
+        if (FWD) ct<H>(x[j], x[j + hh], t.w[o + g], t.s[o + g], p, p2);
+        else gs<H>(x[j], x[j + hh], t.w[o + g], t.s[o + g], p, p2);
+    }
+}
+template <bool FWD, bool H>
+__device__ __forceinline__ void phase_a_t(uint32_t (&x)[E], const Tw& t, uint32_t p, uint32_t p2) {
+    if (FWD) {
+        stage_t<FWD, H, 3>(x, t, p, p2);
+        stage_t<FWD, H, 2>(x, t, p, p2);
+        stage_t<FWD, H, 1>(x, t, p, p2);
+        stage_t<FWD, H, 0>(x, t, p, p2);
+    } else {
+        stage_t<FWD, H, 0>(x, t, p, p2);
+        stage_t<FWD, H, 1>(x, t, p, p2);
+        stage_t<FWD, H, 2>(x, t, p, p2);
+        stage_t<FWD, H, 3>(x, t, p, p2);
+    }
+}
+template <bool FWD, bool H, int T>
+__device__ __forceinline__ void phase_b_t(uint32_t (&x)[E], const Tw& t, uint32_t p, uint32_t p2) {
+    constexpr int LT = T == 16 ? 4 : T == 8 ? 3 : T == 4 ? 2 : 1;
+    if (FWD) {
+        if (LT > 3) stage_t<FWD, H, 3>(x, t, p, p2);
+        if (LT > 2) stage_t<FWD, H, 2>(x, t, p, p2);
+        if (LT > 1) stage_t<FWD, H, 1>(x, t, p, p2);
+        stage_t<FWD, H, 0>(x, t, p, p2);
+    } else {
+        stage_t<FWD, H, 0>(x, t, p, p2);
+        if (LT > 1) stage_t<FWD, H, 1>(x, t, p, p2);
+        if (LT > 2) stage_t<FWD, H, 2>(x, t, p, p2);
+        if (LT > 3) stage_t<FWD, H, 3>(x, t, p, p2);
+    }
+}
+
 // Wave-level ordering of LDS traffic between the lanes of one wave.
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

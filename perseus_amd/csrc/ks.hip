@@ -453,16 +453,21 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     const uint32_t kexp = A.autok[r];
     uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + C.trow;
     uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + C.trow;
-    const uint32_t cb = ((2 * C.bs0 + 1) * kexp) & C.mask2n;
-    const uint32_t step = (kexp << (C.logn - 3)) & C.mask2n;
+    // W_k = top 10 bits of (cb + brev4(k) step) mod 2N; step's low logn - 3 bits are zero, so the sum's top bits are
+    // (cb >> sh) + brev4(k) (step >> sh) modulo 1024
     const int sh = C.logn - 9;
+    const uint32_t cbh = (((2 * C.bs0 + 1) * kexp) & C.mask2n) >> sh;
+    const uint32_t sth = ((kexp << (C.logn - 3)) & C.mask2n) >> sh;
     const uint32_t ob = (automorph_slot(kexp, C.chunk0, C.logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
     uint32_t* buf = W.buf;
+    uint32_t sa[DS];
+#pragma unroll
+    for (int k = 0; k < DS; ++k) sa[k] = scat_addr((cbh + brev4(k) * sth) & (DCH - 1));
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
         uint32_t(&rv)[DS] = part ? r1 : r0;
 #pragma unroll
-        for (int k = 0; k < DS; ++k) buf[scat_addr(((cb + brev4(k) * step) & C.mask2n) >> sh)] = rv[k];
+        for (int k = 0; k < DS; ++k) buf[sa[k]] = rv[k];
         if (part == 1) {
             // the redrawn words of this lane: add D_d a_d into their slots
 #pragma unroll
@@ -473,7 +478,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
                     const uint32_t j = __builtin_ctz(m);
                     m &= m - 1;
                     const uint32_t add = red.mul(L.D[d][lp + j], W.q[i++]);
-                    const uint32_t o = scat_addr(((cb + brev4(j) * step) & C.mask2n) >> sh);
+                    const uint32_t o = scat_addr((cbh + brev4(j) * sth) & (DCH - 1));
                     buf[o] = addm(buf[o], add, p);
                 }
             }

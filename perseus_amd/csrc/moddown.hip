@@ -39,10 +39,12 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
     for (int t = t0; t < t1; ++t) {
         const Red red(A.pr[t]);
         const uint32_t p = red.p, p2 = 2 * p;
+        const uint32_t r64 = shoup(red.r32, red.r32, red.r32s, p);  // 2^64 mod q_t
         uint32_t m[KP];
 #pragma unroll
         for (int j = 0; j < KP; ++j) m[j] = A.mt[j * A.nq + t];
-        // sum_j y_j M[j][t]: products below 2^62, so three to a 64-bit sum
+        // sum_j y_j M[j][t]: products below 2^62, three to a 64-bit sum; two sums add to 65 bits, the carry folded in
+        // as 2^64 mod q_t, so one reduction per word
         uint32_t x[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -52,7 +54,12 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
                 if (j < 3) a0 += (uint64_t)y[j][e] * m[j];
                 else a1 += (uint64_t)y[j][e] * m[j];
             }
-            x[e] = KP > 3 ? addm(red(a0), red(a1), p) : red(a0);
+            if (KP > 3) {
+                const uint64_t s = a0 + a1;
+                x[e] = addm(red(s), s < a0 ? r64 : 0u, p);
+            } else {
+                x[e] = red(a0);
+            }
         }
         const uint32_t* w = A.fw + ((size_t)t << LOGN);
         const uint32_t* ws = A.fws + ((size_t)t << LOGN);

@@ -157,6 +157,21 @@ __device__ __forceinline__ void st16(uint32_t* p, const uint32_t (&v)[16]) {
     for (int i = 0; i < 4; ++i) q[i] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
 }
 
+// A raw buffer over [base, base + bytes): 32-bit loads and stores at a per-lane byte offset plus a uniform one kept in
+// a scalar register, so a thread's strided accesses need one address register instead of one 64-bit address each;
+// accesses past `bytes` read 0 and write nothing.
+struct Buf {
+    __amdgpu_buffer_rsrc_t r;
+    __device__ __forceinline__ Buf(const void* base, uint32_t bytes)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, 0x00020000)) {}
+    __device__ __forceinline__ uint32_t ld(uint32_t voff, uint32_t soff) const {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+    __device__ __forceinline__ void st(uint32_t v, uint32_t voff, uint32_t soff) const {
+        __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, 0);
+    }
+};
+
 // Workgroups of a launch are dispatched round-robin over the 8 XCDs (workgroup i to XCD i mod 8), each XCD with its own
 // L2. Renumbering so that XCD k runs the contiguous range of logical blocks [k q + min(k, r), ...) (q, r = nblocks
 // div / mod 8) keeps neighbouring blocks, which share cache lines and twiddle tables, on one L2.

@@ -25,14 +25,18 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
     const size_t rb = (size_t)B.y * A.rows;  // row 0 of (ciphertext, part) B.y
     const int col = threadIdx.x % G::CC, tau = threadIdx.x / G::CC;
     const int c = cbk * G::CC + col;
+    // this (ciphertext, part)'s rows through buffer resources: per-lane offsets, the row and the stride uniform
+    const uint32_t span = (uint32_t)A.rows << (LOGN + 2);
+    const Buf bx(A.ext + (rb << LOGN), span), bc(A.conv + (rb << LOGN), span);
     // the sources at positions (tau + TR e) C + c: the column pass's layout A
     uint32_t y[KP][E];
+    const uint32_t vy = (uint32_t)(tau * G::C + c) * 4;
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
-        const uint32_t* src = A.ext + ((rb + A.nq + j) << LOGN);
 #pragma unroll
-        for (int e = 0; e < E; ++e) y[j][e] = src[(size_t)(tau + G::TR * e) * G::C + c];
+        for (int e = 0; e < E; ++e) y[j][e] = bx.ld(vy, (uint32_t)(((A.nq + j) << LOGN) + G::TR * e * G::C) * 4);
     }
+    const uint32_t vo = (uint32_t)(E * tau * G::C + c) * 4;
     const int t0 = grp * A.ntg, t1 = min(A.top + 1, t0 + A.ntg);
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
     constexpr int LS = G::CC + G::CPAD;
@@ -72,9 +76,8 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
 #pragma unroll
         for (int e = 0; e < E; ++e) x[e] = l[(E * tau + e) * LS + col];
         phase_b<true, H, G::TR>(x, tau, w, ws, p, p2, base);
-        uint32_t* out = A.conv + ((rb + t) << LOGN);
 #pragma unroll
-        for (int e = 0; e < E; ++e) out[(size_t)(E * tau + e) * G::C + c] = x[e];  // lazy words
+        for (int e = 0; e < E; ++e) bc.st(x[e], vo, (uint32_t)((t << LOGN) + e * G::C) * 4);  // lazy words
     }
 }
 

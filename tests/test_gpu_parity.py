@@ -154,6 +154,30 @@ def test_dot_and_moddown(stream, name, top, bits):
     assert (got_o[:, : top + 1] == want_o[:, : top + 1]).all()
 
 
+def test_moddown_table_path(stream, monkeypatch):
+    """ModDown through the kernel table's separate stages (INTT, bconv, NTT with epilogue 1), the path the driver takes
+    when the conversion cannot be fused into the NTT column pass (more than 6 special primes): same words as the fused
+    path and the oracle."""
+    say("[moddown table path] c3 top=29")
+    monkeypatch.setenv("PCX_MD_FUSED", "0")
+    ch = pa.preset("c3")
+    ctx = pa.Context(ch, k_rot=1)
+    _, _, oc = contexts("c3")
+    top = len(ch.q) - 1
+    rng = np.random.default_rng(11)
+    ext_h = np.zeros((2, ch.rows, ch.n), np.uint32)
+    for part in range(2):
+        for t in list(range(top + 1)) + list(range(len(ch.q), ch.rows)):
+            ext_h[part, t] = rng.integers(0, ch.primes[t], ch.n)
+    ext = pa.DevBuf.from_array(ext_h)
+    out = ctx.ct_buf()
+    ctx.moddown(ext, top, out, stream)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.moddown(ext_h, top)
+    assert (got[:, : top + 1] == want[:, : top + 1]).all()
+
+
 # ----------------------------------------------------------------------------------------------- rotations
 def test_rotate_c1(stream):
     """C1: one rotation (r = 1) at N = 2^14, 12 limbs, dnum 3, 4 special primes, every output residue."""

@@ -4,6 +4,9 @@ Each check is one the reference itself holds (a golden vector or known answer, c
 (a closed form, an invariant, brute force on small inputs), chosen so that a plausible mistake in the twin (a wrong
 index, sign, stride or dropped term) fails it.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -19,34 +22,29 @@ def fnv(v):
     return h
 
 
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")))
+
+
 # ----------------------------------------------------------------------------------------------- ChaCha / expanders
 def test_chacha20_rfc8439_block():
     # RFC 8439 section 2.3.2: key 00..1f, counter 1, nonce 00:00:00:09:00:00:00:4a:00:00:00:00; the state after the
     # feed-forward add
-    key = [0x03020100, 0x07060504, 0x0B0A0908, 0x0F0E0D0C, 0x13121110, 0x17161514, 0x1B1A1918, 0x1F1E1D1C]
-    out = twin.chacha_block(key, 1, 0x09000000, 0x4A000000, 0x00000000, 20)
-    want = [0xE4E7F110, 0x15593BD1, 0x1FDD0F50, 0xC47120A3, 0xC7F4D1C7, 0x0368C033, 0x9AAA2204, 0x4E6CD4C3,
-            0x466482D2, 0x09AA9F07, 0x05D7C214, 0xA2028BD9, 0xD19C12B5, 0xB94E16DE, 0xE883D0CB, 0x4E3C50A2]
-    assert [int(x) for x in out] == want
+    v = GOLDEN["chacha20_rfc8439_block"]
+    out = twin.chacha_block(v["key"], v["w12"], v["w13"], v["w14"], v["w15"], v["rounds"])
+    assert [int(x) for x in out] == v["out"]
 
 
-KSKB_SEED = [0x01234567, 0x89ABCDEF, 0xDEADBEEF, 0x0BADF00D, 1, 2, 3, 0xFFFFFFFF]
-# crates/pc-core/tests/kskb_frozen.rs:48-52 PINNED: (p, a[0], a[1], a[n-1], FNV-1a of the row), digits 0 / 3 / 6,
+# crates/pc-core/tests/kskb_frozen.rs:46-52 PINNED: (p, a[0], a[1], a[n-1], FNV-1a of the row), digits 0 / 3 / 6,
 # N = 2^16 (the n64 chain, crates/pc-core/src/params.rs:165-168)
-KSKB_PINNED = [
-    (0, 1152921504606584833, 887896118268210575, 381724958222899765, 166443527968165288, 17347891236941834349),
-    (3, 9007199273091073, 3071635100410335, 4572704283048939, 2445311928879128, 6946775773964342884),
-    (6, 1152921504592822273, 229142879966039658, 808485329004953024, 1085433559467732095, 2359252148008581173),
-]
+KSKB = GOLDEN["kskb_frozen"]
 
 
-@pytest.mark.parametrize("digit,p,a0,a1,alast,h", KSKB_PINNED)
+@pytest.mark.parametrize("digit,p,a0,a1,alast,h", [tuple(r) for r in KSKB["pinned"]])
 def test_kskb_frozen_vector(digit, p, a0, a1, alast, h):
     """The u64 lane's pinned keystream: it pins the ChaCha12 core, the (counter, w13, w14, tag) state layout, the block
     and retry-counter machinery (the 2^53 prime rejects ~2^-11 of its words) and the reduction, all of which the u32
     KSKA lane shares."""
-    n = 1 << 16
-    row = twin.kskb_row(KSKB_SEED, digit, p, n)
+    row = twin.kskb_row(KSKB["seed"], digit, p, KSKB["n"])
     assert (int(row[0]), int(row[1]), int(row[-1])) == (a0, a1, alast)
     assert fnv(row) == h
 
@@ -91,12 +89,14 @@ def test_kska_rejection_rule():
 # ----------------------------------------------------------------------------------------------- number theory
 def test_nbtheory_known_answers():
     # crates/pc-core/src/params/nbtheory.rs:170-180
-    m = 1 << 17
-    assert LIB.or_previous_prime(LIB.or_first_prime(28, m), m) == 268042241
-    assert LIB.or_root_of_unity(m, 268042241) == 5274
-    assert LIB.or_is_prime(268042241)
-    assert not LIB.or_is_prime(268042241 * 3)
-    assert not LIB.or_is_prime(3215031751)  # strong pseudoprime to bases 2, 3, 5, 7
+    v = GOLDEN["nbtheory"]
+    m, q = v["m"], v["previous_prime_of_first_prime_28"]
+    assert LIB.or_previous_prime(LIB.or_first_prime(28, m), m) == q
+    assert LIB.or_root_of_unity(m, q) == v["root_of_unity"]
+    assert LIB.or_is_prime(q)
+    assert not LIB.or_is_prime(q * 3)
+    for c in v["not_prime"]:
+        assert not LIB.or_is_prime(c)  # 3215031751: a strong pseudoprime to bases 2, 3, 5, 7
 
 
 def test_is_prime_brute_force():

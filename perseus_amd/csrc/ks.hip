@@ -27,6 +27,14 @@ __device__ __forceinline__ int slot_of(const KeyTab& T, int t, int nq) {
     return (t < nq || T.q_top < 0) ? t : T.q_top + 1 + (t - nq);
 }
 
+// Scatter addresses of the automorphism inside a 1024-slot chunk. With V = ((2 brev(s) + 1) k) mod 2N for source slot
+// s, the output slot's offset in its chunk is brev10 of W = the top 10 bits of V, and W is affine in the lane:
+// W = C + k (brev6(lane) + 64 brev4(j)) mod 1024 for the lane's word j. Storing the word at rotr1(W) (a 10-bit rotate
+// right) makes both the 64 lanes' writes of one j and the reads of output offsets 16 lane + j fall on 32 distinct
+// banks per half wave; the offset 16 lane + j is read back from rotr1(64 brev4(j) + brev6(lane)).
+__device__ __forceinline__ uint32_t scat_addr(uint32_t w) { return (w >> 1) | ((w & 1) << 9); }
+__device__ __forceinline__ uint32_t brev4(uint32_t j) { return __brev(j) >> 28; }
+
 // The 16 KSKA values of slots [s0, s0 + 16) of (seed, digit d, prime p) (crates/pc-core/src/keys.rs:466-498): block
 // s0/16 of the ChaCha12 stream with state words (counter, d, p, "KSKA"); a rejected word is redrawn from block
 // s0/16 + t N/16 (t = 1..15), the 16th attempt kept as is; value v mod p.
@@ -259,25 +267,28 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
                 st16(o1 + s0, r1);
                 continue;
             }
-            // sigma_k: slot s0 + j goes to brev((((2 brev(s0) + 1) + 2 brev(j)) k mod 2N) >> 1); brev(j) of the low 4
-            // bits is brev4(j) 2^(logn - 4), so the 16 targets are one product and 16 uniform offsets apart
+            // sigma_k on the way out, through the conflict-free scatter addresses (scat_addr above)
             uint32_t* l0 = (uint32_t*)W.ex;
             uint32_t* l1 = l0 + DCH;
             wave_sync();
-            const uint32_t cb = ((2 * bs0 + 1) * kexp) & mask2n;
-            const uint32_t step = (kexp << (logn - 3)) & mask2n;
+            const int sh = logn - 9;
+            const uint32_t cbh = (((2 * bs0 + 1) * kexp) & mask2n) >> sh;
+            const uint32_t sth = ((kexp << (logn - 3)) & mask2n) >> sh;
 #pragma unroll
             for (int k = 0; k < DS; ++k) {
-                const uint32_t b4 = ((k & 1) << 3) | ((k & 2) << 1) | ((k & 4) >> 1) | ((k & 8) >> 3);
-                const uint32_t o = brev_n(((cb + b4 * step) & mask2n) >> 1, logn) & (DCH - 1);
+                const uint32_t o = scat_addr((cbh + brev4(k) * sth) & (DCH - 1));
                 l0[o] = r0[k];
                 l1[o] = r1[k];
             }
             wave_sync();
             const uint32_t ob = (automorph_slot(kexp, chunk0, logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
+            const uint32_t rb = scat_addr(__brev((uint32_t)lane) >> 26);
             uint32_t v0[DS], v1[DS];
-            ld16(l0 + lane * DS, v0);
-            ld16(l1 + lane * DS, v1);
+#pragma unroll
+            for (int j = 0; j < DS; ++j) {
+                v0[j] = l0[rb + 32 * brev4(j)];
+                v1[j] = l1[rb + 32 * brev4(j)];
+            }
             if (acc_out) {
                 uint32_t e0[DS], e1[DS];
                 ld16(o0 + ob, e0);
@@ -319,13 +330,6 @@ struct FastLds {
     } w[KW];
 };
 
-// Scatter addresses of the automorphism inside a 1024-slot chunk. With V = ((2 brev(s) + 1) k) mod 2N for source slot
-// s, the output slot's offset in its chunk is brev10 of W = the top 10 bits of V, and W is affine in the lane:
-// W = C + k (brev6(lane) + 64 brev4(j)) mod 1024 for the lane's word j. Storing the word at rotr1(W) (a 10-bit rotate
-// right) makes both the 64 lanes' writes of one j and the reads of output offsets 16 lane + j fall on 32 distinct
-// banks per half wave; the offset 16 lane + j is read back from rotr1(64 brev4(j) + brev6(lane)).
-__device__ __forceinline__ uint32_t scat_addr(uint32_t w) { return (w >> 1) | ((w & 1) << 9); }
-__device__ __forceinline__ uint32_t brev4(uint32_t j) { return __brev(j) >> 28; }
 
 // KSKA value of an accepted word v < floor((2^32-1)/p) p. MU2: floor((2^32-1)/p) = 2 (every p > (2^32-1)/3), where
 // v < 2p needs one conditional subtraction.

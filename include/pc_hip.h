@@ -423,6 +423,10 @@ pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const
                             const uint32_t* seeds, const int64_t* errors, int bits, int* err);
 void pcx_keys_free(pcx_keys* k);
 /* download key r's stored b as dense [dnum][nq + kp][N] words */
+/* bytes of the group's KSKA retry-value table (dense keys: the accepted redraws of the rejected ChaCha words, built
+ * when the keys are made and read by the dot instead of redrawing them; about 1-2% of b at 31-bit primes); 0 if none.
+ * No counterpart in the reference, whose dot redraws in the kernel (as the table entry ks_dot_key does here). */
+size_t pcx_keys_patch_bytes(const pcx_keys* k);
 int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host);
 
 /* Ciphertexts are device buffers in the context layout [part][row = prime id over Q u P][N] words (2 (nq+kp) N words;

@@ -75,6 +75,7 @@ _SIGS = {
     "pcx_timing": (C.c_int, [vp, C.c_int]),
     "pcx_timing_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
     "pcx_copy_probe": (C.c_int, [vp, vp, C.c_size_t, vp]),
+    "pcx_keys_patch_bytes": (C.c_size_t, [vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(LIB, _name)

@@ -95,7 +95,8 @@ def preset(name: str) -> Chain:
     c1: one rotation at N = 2^14, 12 Q primes below 2^30 (lazy butterflies legal), dnum 3, 4 special primes;
     c2: the batched NTT round trip, N = 2^16, 40 primes below 2^31;
     c3: the hoisted rotation batch, N = 2^16, 30 Q primes below 2^31, dnum 3, 6 special primes;
-    small: a quick test chain, N = 2^12, 6 Q + 2 special 30-bit primes, dnum 3.
+    small: a quick test chain, N = 2^12, 6 Q + 2 special 30-bit primes, dnum 3;
+    rej: N = 2^12, 6 Q + 3 special primes just above 2^32 / 3, where a third of the KSKA words are rejected.
     """
     if name == "c1":
         return make("c1", 14, 12, 4, 3, 30)
@@ -107,4 +108,20 @@ def preset(name: str) -> Chain:
         return make("small", 12, 6, 2, 3, 30)
     if name == "small31":
         return make("small31", 12, 6, 3, 3, 31)
+    if name == "rej":
+        return Chain("rej", 12, *_split(ascending_primes(2**32 // 3 + 1, 2 << 12, 9), 6), 3)
     raise KeyError(name)
+
+
+def ascending_primes(lo: int, m: int, n: int) -> List[int]:
+    """n primes q = 1 mod m from lo upwards (a test chain: just above 2^32 / 3 a third of the KSKA words are rejected)."""
+    out, q = [], (lo + m - 2) // m * m + 1
+    while len(out) < n:
+        if is_prime(q):
+            out.append(q)
+        q += m
+    return out
+
+
+def _split(ps, nq):
+    return ps[:nq], ps[nq:]

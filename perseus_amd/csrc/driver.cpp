@@ -253,6 +253,9 @@ struct pcx_keys {
     const uint32_t** seed = nullptr;  // device array of per-key seed pointers
     uint32_t* autok = nullptr;        // g^-1 mod 2N per key
     std::vector<void*> b_ptr;         // device b storage per key
+    // the KSKA retry-value table (dense keys): offsets [key][digit][row][chunk] + 1, values
+    uint32_t *pidx = nullptr, *pval = nullptr;
+    size_t patch_words = 0;
 };
 
 namespace {
@@ -510,6 +513,14 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     t.srows = c->rows;
     t.nregen = c->dnum;
     Stage st(c, 3, s);
+    if (k->pval) {
+        // the retry values from the key group's table (no redraw in the dot)
+        // the table is indexed by the group's key: the launch's key r is the group's r0 + r
+        const size_t per_key = (size_t)c->dnum * c->rows * (c->n / 1024);
+        const pch::PatchTab P = {k->pidx + (size_t)r0 * per_key, k->pval, c->dnum, c->rows};
+        const int rc = pch::ks_dot_patched((int)c->logn, &g, &P, s);
+        if (rc != -2) return rc;
+    }
     return c->tab->ks_dot_key(&g, s);
 }
 
@@ -632,6 +643,37 @@ pcx_keys* keys_shell(pcx_ctx* c, int nkeys, const uint64_t* galois, int bits, in
     }
     k->autok = k->dev.upload(k->autok_h);
     return k;
+}
+
+// The retry-value table of a dense key group (a kernel counts each chunk's rejected KSKA words, the host takes the
+// exclusive prefix, a second kernel writes the redrawn values); skipped when PCX_KS_PATCH=0
+int build_patches(pcx_ctx* c, pcx_keys* k) {
+    if (k->bits != 0) return 0;
+    if (const char* e = getenv("PCX_KS_PATCH"))
+        if (atoi(e) == 0) return 0;
+    const size_t chunks = c->n / 1024, cells = (size_t)k->nkeys * c->dnum * c->rows * chunks;
+    uint32_t* cnt = (uint32_t*)k->dev.alloc(cells * 4);
+    if (!cnt) return k->dev.err;
+    if (int e = pch::kska_patch_count((int)c->logn, k->seed, c->pr, k->nkeys, c->dnum, c->rows, cnt, nullptr)) return e;
+    std::vector<uint32_t> h(cells);
+    if (hipMemcpy(h.data(), cnt, cells * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    std::vector<uint32_t> off(cells + 1);
+    uint64_t acc = 0;
+    for (size_t i = 0; i < cells; ++i) {
+        off[i] = (uint32_t)acc;
+        acc += h[i];
+    }
+    if (acc >= 0xFFFFFFFFull) return -1;
+    off[cells] = (uint32_t)acc;
+    k->pidx = k->dev.upload(off);
+    k->pval = (uint32_t*)k->dev.alloc(std::max<uint64_t>(acc, 1) * 4);
+    if (!k->pidx || !k->pval) return k->dev.err ? k->dev.err : -1;
+    if (int e = pch::kska_patch_fill((int)c->logn, k->seed, c->pr, k->nkeys, c->dnum, c->rows, k->pidx, k->pval,
+                                     nullptr))
+        return e;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    k->patch_words = (cells + 1) + acc;
+    return 0;
 }
 
 }  // namespace
@@ -881,6 +923,9 @@ pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint
     }
     k->kb = (const void**)k->dev.upload(kb);
     k->seed = (const uint32_t**)k->dev.upload(sd);
+    if (!k->dev.err) {
+        if (int e = build_patches(c, k)) k->dev.err = e;
+    }
     if (k->dev.err) {
         *err = k->dev.err;
         delete k;
@@ -994,6 +1039,7 @@ pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const
         k->seed = (const uint32_t**)k->dev.upload(sd);
         if (k->dev.err) rc = k->dev.err;
     }
+    if (!rc) rc = build_patches(c, k);
     if (!rc && hipDeviceSynchronize() != hipSuccess) rc = -1;
     if (rc) {
         *err = rc;
@@ -1004,6 +1050,8 @@ pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const
 }
 
 void pcx_keys_free(pcx_keys* k) { delete k; }
+
+size_t pcx_keys_patch_bytes(const pcx_keys* k) { return k ? k->patch_words * 4 : 0; }
 
 int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host) {
     if (!k || r < 0 || r >= k->nkeys) return -1;

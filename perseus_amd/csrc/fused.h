@@ -30,4 +30,21 @@ int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s);
 // whose column pass was done by md_conv_cols.
 int ntt_fwd_rows_only(int logn, const NttArgs* a, pc_stream_t s);
 
+// The retry values of a key group's KSKA words (the rejected ChaCha words' accepted redraws, in slot order), built
+// once when the keys are made: idx[((r ndig + d) rows + t) chunks + c] is the first value of key r, digit d, row t,
+// 1024-slot chunk c in val (exclusive prefix over that order, one sentinel at the end). With them the fast dot
+// regenerates a and never redraws: a rejected word's value is read from the table.
+struct PatchTab {
+    const uint32_t* idx;
+    const uint32_t* val;
+    int ndig, rows;
+};
+// counts[((r ndig + d) rows + t) chunks + c] for the nkeys seeds (device array of seed pointers) and the context's primes
+int kska_patch_count(int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig, int rows,
+                     uint32_t* counts, pc_stream_t s);
+int kska_patch_fill(int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig, int rows,
+                    const uint32_t* idx, uint32_t* val, pc_stream_t s);
+// the fast dot with the retry values read from P instead of redrawn; -2 where the fast dot does not apply
+int ks_dot_patched(int logn, const KsKeyArgs* g, const PatchTab* P, pc_stream_t s);
+
 }  // namespace pch

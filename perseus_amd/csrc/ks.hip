@@ -15,6 +15,7 @@
 // depend only on the high bits of i, so the chunk's 1024 slots land in one aligned 1024-slot chunk of the output,
 // permuted; the permutation goes through LDS and the stores stay coalesced.
 #include "common.h"
+#include "fused.h"
 
 namespace pch {
 namespace ks {
@@ -349,8 +350,19 @@ struct FastCtx {
     size_t trow;
 };
 
-template <int NDIG, bool MU2>
-__device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, const Expander& ex, int r) {
+// wave-wide exclusive prefix over lanes of a count below 32 (five ballots)
+__device__ __forceinline__ uint32_t lane_prefix(uint32_t cnt, int lane) {
+    const uint64_t below = (1ull << lane) - 1;
+    uint32_t pre = 0;
+#pragma unroll
+    for (int b = 0; b < 5; ++b) pre += (uint32_t)__popcll(__ballot((cnt >> b) & 1) & below) << b;
+    return pre;
+}
+
+// PATCH: the retry values come from the key group's table (P) instead of the wave's redraw
+template <int NDIG, bool MU2, bool PATCH>
+__device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, const Expander& ex, int r,
+                                             const PatchTab& P) {
     const KsArgs& A = *C.A;
     const KeyTab& T = *C.T;
     FastLds& L = *C.L;
@@ -365,11 +377,30 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     for (int i = 0; i < 8; ++i) seed[i] = sp[i];
     if (lane == 0) W.qn = 0;
     wave_sync();
+    // PATCH: this chunk's retry values of each digit, loaded now (two per lane) and stored to the queue after the
+    // ChaCha blocks; a digit whose list would overflow the queue redraws in the lane
+    uint32_t poff[PATCH ? NDIG : 1], pn[PATCH ? NDIG : 1], pv[PATCH ? NDIG : 1][2];
+    if constexpr (PATCH) {
+        const uint32_t chunks = (1u << C.logn) / DCH;
+        uint32_t tot = 0;
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            const size_t ix = (((size_t)r * P.ndig + d) * P.rows + C.slot) * chunks + C.chunk0 / DCH;
+            poff[d] = P.idx[ix];
+            pn[d] = P.idx[ix + 1] - poff[d];
+            if (tot + pn[d] > (uint32_t)FQCAP) pn[d] = 0xFFFFFFFFu;  // redrawn in the lane
+            else tot += pn[d];
+            const bool ok = pn[d] != 0xFFFFFFFFu;
+            pv[d][0] = ok && (uint32_t)lane < pn[d] ? P.val[poff[d] + lane] : 0;
+            pv[d][1] = ok && (uint32_t)lane + DBX < pn[d] ? P.val[poff[d] + lane + DBX] : 0;
+        }
+    }
     // s1 = sum_d D_d a_d, a regenerated (one ChaCha12 block per lane and digit); rejected words contribute later
     uint64_t acc[DS];
 #pragma unroll
     for (int k = 0; k < DS; ++k) acc[k] = 0;
     uint32_t rejd[NDIG], based[NDIG];
+    uint32_t pbase = 0;
 #pragma unroll
     for (int d = 0; d < NDIG; ++d) {
         uint32_t a[DS];
@@ -378,10 +409,14 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 #pragma unroll
         for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
         uint32_t base = 0;
-        if (rej) {
+        if (PATCH && pn[d] != 0xFFFFFFFFu) {
+            // the table lists this chunk's rejected words in slot order: this lane's come after the lower lanes'
+            base = pbase + lane_prefix(__builtin_popcount(rej), lane);
+            pbase += pn[d];
+        } else if (rej) {
             const uint32_t cnt = __builtin_popcount(rej);
-            base = atomicAdd(&W.qn, cnt);
-            if (base + cnt <= (uint32_t)FQCAP) {
+            base = PATCH ? (uint32_t)FQCAP : atomicAdd(&W.qn, cnt);
+            if (!PATCH && base + cnt <= (uint32_t)FQCAP) {
                 uint32_t m = rej, i = base;
 #pragma unroll 1
                 while (m) {
@@ -420,9 +455,22 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     uint32_t b[NDIG][DS];
 #pragma unroll
     for (int d = 0; d < NDIG; ++d) ld16(kb + d * dstride, b[d]);
-    // redraw the queued words: entry <- accepted value mod p
+    // redraw the queued words: entry <- accepted value mod p (PATCH: the table's values into the queue)
     wave_sync();
-    const uint32_t nq = min(W.qn, (uint32_t)FQCAP);
+    uint32_t nq = 0;
+    if constexpr (PATCH) {
+        uint32_t b0 = 0;
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            if (pn[d] == 0xFFFFFFFFu) continue;
+            if ((uint32_t)lane < pn[d]) W.q[b0 + lane] = pv[d][0];
+            if ((uint32_t)lane + DBX < pn[d]) W.q[b0 + lane + DBX] = pv[d][1];
+            for (uint32_t i = lane + 2 * DBX; i < pn[d]; i += DBX) W.q[b0 + i] = P.val[poff[d] + i];
+            b0 += pn[d];
+        }
+    } else {
+        nq = min(W.qn, (uint32_t)FQCAP);
+    }
     for (uint32_t i = lane; i < nq; i += DBX) {
         const uint32_t it = W.q[i], d = it >> 16, sl = it & 0xFFFF;
         const uint32_t ctr = (C.chunk0 + sl) >> 4;
@@ -503,8 +551,8 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     }
 }
 
-template <int NDIG>
-__global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, int logn) {
+template <int NDIG, bool PATCH>
+__global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, PatchTab P, int logn) {
     static_assert(NDIG >= 1 && NDIG <= MAXD, "digits staged in LDS");
     static_assert(3 * sizeof(FastLds) <= 160 * 1024, "three workgroups per CU");
     __shared__ FastLds L;
@@ -549,9 +597,9 @@ __global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, int logn)
     }
     __syncthreads();
     if (ex.mu == 2) {
-        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, true>(C, red, ex, r);
+        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, true, PATCH>(C, red, ex, r, P);
     } else {
-        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, false>(C, red, ex, r);
+        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, false, PATCH>(C, red, ex, r, P);
     }
 }
 
@@ -572,12 +620,80 @@ int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     dim3 grid(chunks, a.nrows, groups);
     const bool fast = mode == 1 && a.K == 1 && key.bits == 0 && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
     if (fast) {
-        if (a.ndig == 1) hipLaunchKernelGGL(dot_fast<1>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN);
-        if (a.ndig == 2) hipLaunchKernelGGL(dot_fast<2>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN);
-        if (a.ndig == 3) hipLaunchKernelGGL(dot_fast<3>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN);
+        const PatchTab none = {};
+        if (a.ndig == 1) hipLaunchKernelGGL((dot_fast<1, false>), grid, dim3(KBX), 0, (hipStream_t)s, a, key, none, LOGN);
+        if (a.ndig == 2) hipLaunchKernelGGL((dot_fast<2, false>), grid, dim3(KBX), 0, (hipStream_t)s, a, key, none, LOGN);
+        if (a.ndig == 3) hipLaunchKernelGGL((dot_fast<3, false>), grid, dim3(KBX), 0, (hipStream_t)s, a, key, none, LOGN);
     } else if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     else hipLaunchKernelGGL(dot_k<false>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     return launch_rc();
+}
+
+// the fast dot with a retry-value table (driver-internal; the table entry ks_dot_key redraws)
+template <int LOGN>
+int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
+    if (!g || !P || !P->idx || !P->val) return -1;
+    const KsArgs& a = g->ks;
+    const KeyTab& key = g->key;
+    if (a.K != 1 || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 || (a.c0_mode & 3) == 3 ||
+        a.ndig > P->ndig || key.q_top >= 0 || key.srows != P->rows)
+        return -2;
+    if (a.nrows < 0 || a.R < 0) return -1;
+    if (a.nrows == 0 || a.R == 0) return 0;
+    if (!a.rows || !a.pr || !a.c1 || !a.out0 || !a.out1 || !a.autok || !a.digit_of || !a.modup) return -1;
+    if ((a.c0_mode & 3) == 1 && (!a.c0 || !a.pmod || !a.pmods)) return -1;
+    if ((a.c0_mode & 3) == 2 && !a.c0) return -1;
+    if (!key.kb || !key.seed) return -1;
+    const int chunks = (1 << LOGN) / DCH;
+    int groups = 1;
+    while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
+    const dim3 grid(chunks, a.nrows, groups);
+    hipStream_t st = (hipStream_t)s;
+    if (a.ndig == 1) hipLaunchKernelGGL((dot_fast<1, true>), grid, dim3(KBX), 0, st, a, key, *P, LOGN);
+    if (a.ndig == 2) hipLaunchKernelGGL((dot_fast<2, true>), grid, dim3(KBX), 0, st, a, key, *P, LOGN);
+    if (a.ndig == 3) hipLaunchKernelGGL((dot_fast<3, true>), grid, dim3(KBX), 0, st, a, key, *P, LOGN);
+    return launch_rc();
+}
+
+// The retry table's two passes: one wave per (chunk, row, key x digit) regenerates the chunk's KSKA blocks, counts
+// its rejected words, then (fill) writes their redrawn values in slot order.
+template <bool FILL>
+__global__ void __launch_bounds__(DBX) patch_k(const uint32_t* const* seeds, const PrimeConst* pr, int ndig, int rows,
+                                              int logn, uint32_t* counts, const uint32_t* idx, uint32_t* val) {
+    const int lane = threadIdx.x, t = blockIdx.y, r = blockIdx.z / ndig, d = blockIdx.z % ndig;
+    const uint32_t chunks = (1u << logn) / DCH;
+    const size_t ix = (((size_t)r * ndig + d) * rows + t) * chunks + blockIdx.x;
+    const uint32_t p = (uint32_t)pr[t].p;
+    const Expander ex(p);
+    uint32_t seed[8];
+    const uint32_t* sp = seeds[r];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) seed[i] = sp[i];
+    const uint32_t s0 = blockIdx.x * DCH + lane * DS, n16 = (1u << logn) >> 4;
+    uint32_t a[DS];
+    chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
+    uint32_t rej = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
+    const uint32_t cnt = __builtin_popcount(rej);
+    if (!FILL) {
+        const uint32_t tot = __popcll(__ballot(cnt & 1)) + 2 * __popcll(__ballot(cnt & 2)) +
+                             4 * __popcll(__ballot(cnt & 4)) + 8 * __popcll(__ballot(cnt & 8)) +
+                             16 * __popcll(__ballot(cnt & 16));
+        if (lane == 0) counts[ix] = tot;
+        return;
+    }
+    uint32_t o = idx[ix] + lane_prefix(cnt, lane);
+    while (rej) {
+        const int j = __builtin_ctz(rej);
+        rej &= rej - 1;
+        uint32_t v = 0;
+        for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+            v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * n16, (uint32_t)d, p, TAG_KSKA, j);
+            if (v < ex.mp) break;
+        }
+        val[o++] = ex.red(v);
+    }
 }
 
 // ks_dot: K <= 8 ciphertexts x R keys stored dense (crates/pc-host/src/ks.rs:139-162: KS_SUM -3, K > 8 -1)
@@ -741,5 +857,35 @@ PCH_KS_INST(13)
 PCH_KS_INST(14)
 PCH_KS_INST(15)
 PCH_KS_INST(16)
+
+int ks_dot_patched(int logn, const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
+    switch (logn) {
+        case 12: return ks::dot_patched<12>(g, P, s);
+        case 13: return ks::dot_patched<13>(g, P, s);
+        case 14: return ks::dot_patched<14>(g, P, s);
+        case 15: return ks::dot_patched<15>(g, P, s);
+        case 16: return ks::dot_patched<16>(g, P, s);
+        default: return -2;
+    }
+}
+static int patch_launch(bool fill, int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig,
+                        int rows, uint32_t* counts, const uint32_t* idx, uint32_t* val, pc_stream_t s) {
+    if (!seeds || !pr || nkeys < 1 || ndig < 1 || ndig > 4 || rows < 1 || logn < 10 || logn > 17) return -1;
+    if (fill ? (!idx || !val) : !counts) return -1;
+    const dim3 grid((1u << logn) / ks::DCH, rows, nkeys * ndig);
+    if (fill) hipLaunchKernelGGL(ks::patch_k<true>, grid, dim3(ks::DBX), 0, (hipStream_t)s, seeds, pr, ndig, rows, logn,
+                                 counts, idx, val);
+    else hipLaunchKernelGGL(ks::patch_k<false>, grid, dim3(ks::DBX), 0, (hipStream_t)s, seeds, pr, ndig, rows, logn,
+                            counts, idx, val);
+    return launch_rc();
+}
+int kska_patch_count(int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig, int rows,
+                     uint32_t* counts, pc_stream_t s) {
+    return patch_launch(false, logn, seeds, pr, nkeys, ndig, rows, counts, nullptr, nullptr, s);
+}
+int kska_patch_fill(int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig, int rows,
+                    const uint32_t* idx, uint32_t* val, pc_stream_t s) {
+    return patch_launch(true, logn, seeds, pr, nkeys, ndig, rows, nullptr, idx, val, s);
+}
 
 }  // namespace pch

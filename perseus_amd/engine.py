@@ -200,6 +200,10 @@ class Keys:
         self._keep = None
         self.bits = bits
 
+    def patch_bytes(self):
+        """Bytes of the group's KSKA retry-value table (0 when the dot redraws in the kernel)."""
+        return int(LIB.pcx_keys_patch_bytes(self.h))
+
     def download_b(self, r):
         out = np.empty((self.ctx.dnum, self.ctx.rows, self.ctx.n), np.uint32)
         check(LIB.pcx_keys_download_b(self.h, r, out.ctypes.data_as(C.POINTER(C.c_uint32))), "download_b")

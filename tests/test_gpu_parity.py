@@ -222,6 +222,54 @@ def test_hoisted(stream, name, steps, top):
         assert (one.download((2, ch.rows, ch.n))[:, : top + 1] == got[j, :, : top + 1]).all()
 
 
+def test_hoisted_dense_c3(stream):
+    """The bench's configuration: C3 at the top with dense b, the fast dot reading the retry-value table."""
+    say("[hoisted dense] c3 top=29")
+    ch, ctx, oc = contexts("c3", k_rot=4)
+    twin.set_threads(16)
+    steps = [1, 5, 1 << 15, 256]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=6)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    assert keys.patch_bytes() > 0
+    top = len(ch.q) - 1
+    ct = random_ct(ch, top, 10)
+    dev = pa.DevBuf.from_array(ct)
+    outs = ctx.ct_buf(len(steps))
+    ctx.rotate_hoisted(keys, list(range(len(steps))), dev, top, outs, stream)
+    stream.sync()
+    got = outs.download((len(steps), 2, ch.rows, ch.n))
+    want = oc.rotate_hoisted(ct, top, seeds, bs, gals)
+    for j in range(len(steps)):
+        assert (got[j, :, : top + 1] == want[j][:, : top + 1]).all(), steps[j]
+
+
+@pytest.mark.parametrize("mode", ["table", "redraw", "packed"])
+def test_rejection_heavy(stream, monkeypatch, mode):
+    """Primes just above 2^32 / 3, where a third of the KSKA words are rejected: the retry table (dense keys), the
+    wave's redraw (dense keys with the table off) and the general dot (packed b), all against the oracle, including
+    waves whose rejections overflow the queue."""
+    say(f"[rejections] mode={mode}")
+    if mode == "redraw":
+        monkeypatch.setenv("PCX_KS_PATCH", "0")
+    ch = pa.preset("rej")
+    ctx = pa.Context(ch, k_rot=3)
+    oc = twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum)
+    steps = [1, 3, 7]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=8)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=31 if mode == "packed" else 0)
+    assert (keys.patch_bytes() > 0) == (mode == "table")
+    top = len(ch.q) - 1
+    ct = random_ct(ch, top, 12)
+    dev = pa.DevBuf.from_array(ct)
+    outs = ctx.ct_buf(len(steps))
+    ctx.rotate_hoisted(keys, list(range(len(steps))), dev, top, outs, stream)
+    stream.sync()
+    got = outs.download((len(steps), 2, ch.rows, ch.n))
+    want = oc.rotate_hoisted(ct, top, seeds, bs, gals)
+    for j in range(len(steps)):
+        assert (got[j, :, : top + 1] == want[j][:, : top + 1]).all(), steps[j]
+
+
 # ----------------------------------------------------------------------------------------------- keys
 @pytest.mark.parametrize("name,bits", [("small", 0), ("small", 30), ("c1", 30), ("small31", 31)])
 def test_device_keygen(stream, name, bits):

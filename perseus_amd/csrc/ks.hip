@@ -451,7 +451,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 #pragma unroll
         for (int k = 0; k < DS; ++k) asm volatile("" : "+v"(acc[k]));
     }
-    // the key's b rows: they arrive while the queued words are redrawn and are consumed last
+    // the key's b rows: they arrive while the queued words are redrawn and s1 goes out, and are consumed last
     uint32_t b[NDIG][DS];
 #pragma unroll
     for (int d = 0; d < NDIG; ++d) ld16(kb + d * dstride, b[d]);
@@ -481,9 +481,50 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         }
         W.q[i] = ex.red(v);
     }
-    uint32_t r0[DS], r1[DS];
+    const uint32_t kexp = A.autok[r];
+    uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + C.trow;
+    uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + C.trow;
+    // W_k = top 10 bits of (cb + brev4(k) step) mod 2N; step's low logn - 3 bits are zero, so the sum's top bits are
+    // (cb >> sh) + brev4(k) (step >> sh) modulo 1024
+    const int sh = C.logn - 9;
+    const uint32_t cbh = (((2 * C.bs0 + 1) * kexp) & C.mask2n) >> sh;
+    const uint32_t sth = ((kexp << (C.logn - 3)) & C.mask2n) >> sh;
+    const uint32_t ob = (automorph_slot(kexp, C.chunk0, C.logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
+    uint32_t* buf = W.buf;
+    // out one part through the scatter buffer: v[j] = the word of output offset 16 lane + j
+    auto emit = [&](uint32_t (&v)[DS], uint32_t* o) {
+        wave_sync();
 #pragma unroll
-    for (int k = 0; k < DS; ++k) r1[k] = red(acc[k]);
+        for (int j = 0; j < DS; ++j) v[j] = buf[C.rb + 32 * brev4(j)];
+        o += ob;
+        if (C.acc_out) {
+            uint32_t e[DS];
+            ld16(o, e);
+#pragma unroll
+            for (int k = 0; k < DS; ++k) v[k] = addm(v[k], e[k], p);
+        }
+        st16(o, v);
+        wave_sync();
+    };
+    {
+        // s1 first (its registers free before s0's): reduce, scatter, add D_d a_d of this lane's redrawn words
+        uint32_t v[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) buf[scat_addr((cbh + brev4(k) * sth) & (DCH - 1))] = red(acc[k]);
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            uint32_t m = rejd[d], i = based[d];
+#pragma unroll 1
+            while (m) {
+                const uint32_t j = __builtin_ctz(m);
+                m &= m - 1;
+                const uint32_t add = red.mul(L.D[d][lp + j], W.q[i++]);
+                const uint32_t o = scat_addr((cbh + brev4(j) * sth) & (DCH - 1));
+                buf[o] = addm(buf[o], add, p);
+            }
+        }
+        emit(v, o1);
+    }
     // s0 = sum_d D_d b_d (+ P c0 folded in: ndig + 1 <= 4 products of (p - 1)^2 < 2^62)
     uint32_t cw[DS];
     if (C.m0) ld16(L.c0 + lp, cw);
@@ -496,58 +537,15 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 #pragma unroll
         for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * b[d][k];
     }
-#pragma unroll
-    for (int k = 0; k < DS; ++k) r0[k] = red(acc[k]);
-    if (C.m0 == 2) {
-#pragma unroll
-        for (int k = 0; k < DS; ++k) r0[k] = addm(r0[k], cw[k], p);
-    }
-    const uint32_t kexp = A.autok[r];
-    uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + C.trow;
-    uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + C.trow;
-    // W_k = top 10 bits of (cb + brev4(k) step) mod 2N; step's low logn - 3 bits are zero, so the sum's top bits are
-    // (cb >> sh) + brev4(k) (step >> sh) modulo 1024
-    const int sh = C.logn - 9;
-    const uint32_t cbh = (((2 * C.bs0 + 1) * kexp) & C.mask2n) >> sh;
-    const uint32_t sth = ((kexp << (C.logn - 3)) & C.mask2n) >> sh;
-    const uint32_t ob = (automorph_slot(kexp, C.chunk0, C.logn) & ~(uint32_t)(DCH - 1)) + lane * DS;
-    uint32_t* buf = W.buf;
-    uint32_t sa[DS];
-#pragma unroll
-    for (int k = 0; k < DS; ++k) sa[k] = scat_addr((cbh + brev4(k) * sth) & (DCH - 1));
-#pragma unroll
-    for (int part = 0; part < 2; ++part) {
-        uint32_t(&rv)[DS] = part ? r1 : r0;
-#pragma unroll
-        for (int k = 0; k < DS; ++k) buf[sa[k]] = rv[k];
-        if (part == 1) {
-            // the redrawn words of this lane: add D_d a_d into their slots
-#pragma unroll
-            for (int d = 0; d < NDIG; ++d) {
-                uint32_t m = rejd[d], i = based[d];
-#pragma unroll 1
-                while (m) {
-                    const uint32_t j = __builtin_ctz(m);
-                    m &= m - 1;
-                    const uint32_t add = red.mul(L.D[d][lp + j], W.q[i++]);
-                    const uint32_t o = scat_addr((cbh + brev4(j) * sth) & (DCH - 1));
-                    buf[o] = addm(buf[o], add, p);
-                }
-            }
-        }
-        wave_sync();
+    {
         uint32_t v[DS];
 #pragma unroll
-        for (int j = 0; j < DS; ++j) v[j] = buf[C.rb + 32 * brev4(j)];
-        uint32_t* o = (part ? o1 : o0) + ob;
-        if (C.acc_out) {
-            uint32_t e[DS];
-            ld16(o, e);
-#pragma unroll
-            for (int k = 0; k < DS; ++k) v[k] = addm(v[k], e[k], p);
+        for (int k = 0; k < DS; ++k) {
+            uint32_t r0 = red(acc[k]);
+            if (C.m0 == 2) r0 = addm(r0, cw[k], p);
+            buf[scat_addr((cbh + brev4(k) * sth) & (DCH - 1))] = r0;
         }
-        st16(o, v);
-        wave_sync();
+        emit(v, o0);
     }
 }
 

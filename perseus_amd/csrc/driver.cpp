@@ -723,7 +723,7 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     if (const char* e = getenv("PCX_NTT_CHUNK")) c->chunk = atoi(e);
     c->md_fused = kp <= pch::MDC_MAX_KP ? 1 : 0;
     if (const char* e = getenv("PCX_MD_FUSED")) c->md_fused = c->md_fused && atoi(e) != 0;
-    if (const char* e = getenv("PCX_MD_NTG")) c->md_ntg = std::max(1, atoi(e));
+    if (const char* e = getenv("PCX_MD_NTG")) c->md_ntg = std::max(1, std::min(pch::MDC_MAX_NTG, atoi(e)));
     const int R = c->rows;
     // prime constants and twiddles (crates/pc-gpu/src/context.rs:186-230)
     std::vector<PrimeConst> pc;

@@ -23,7 +23,9 @@ struct MdcArgs {
     int nq, kp, rows, top, ntg, m, lazy;
 };
 constexpr int MDC_MAX_KP = 6;
-// 0, or -1 (bad arguments), -2 (kp outside 1..MDC_MAX_KP or logn outside 12..16), or a HIP error
+constexpr int MDC_MAX_NTG = 8;
+// 0, or -1 (bad arguments), -2 (kp outside 1..MDC_MAX_KP, ntg above MDC_MAX_NTG or logn outside 12..16), or a HIP
+// error
 int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s);
 
 // The forward transform's row pass alone (grid of every row of a), epilogue a->epi included: completes a forward NTT

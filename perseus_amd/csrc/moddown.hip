@@ -38,6 +38,15 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
     }
     const uint32_t vo = (uint32_t)(E * tau * G::C + c) * 4;
     const int t0 = grp * A.ntg, t1 = min(A.top + 1, t0 + A.ntg);
+    // the column pass reads twiddle entries below R only: the group's targets' tables (values, then Shoup companions)
+    // staged once in LDS, shared by the workgroup's columns
+    __shared__ uint32_t tw[MDC_MAX_NTG][2 * G::R];
+    for (int i = threadIdx.x; i < (t1 - t0) * 2 * G::R; i += WG) {
+        const int k = i / (2 * G::R), j = i % (2 * G::R);
+        const size_t off = ((size_t)(t0 + k) << LOGN) + (j % G::R);
+        tw[k][j] = j < G::R ? A.fw[off] : A.fws[off];
+    }
+    __syncthreads();
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
     constexpr int LS = G::CC + G::CPAD;
     for (int t = t0; t < t1; ++t) {
@@ -64,9 +73,12 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
             } else {
                 x[e] = red(a0);
             }
+            // one word's conversion at a time: interleaving all 16 would hold 16 double-word sums beside the 6 x 16
+            // source words (2 waves per SIMD instead of 3)
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const uint32_t* w = A.fw + ((size_t)t << LOGN);
-        const uint32_t* ws = A.fws + ((size_t)t << LOGN);
+        const uint32_t* w = tw[t - t0];
+        const uint32_t* ws = tw[t - t0] + G::R;
         phase_a<true, H, G::TR>(x, w, ws, p, p2, base);
         // double-buffered transpose: one barrier per target
         uint32_t* l = lds[t & 1];
@@ -108,7 +120,7 @@ int mdc(const MdcArgs* a, pc_stream_t s) {
 int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s) {
     if (!a || !a->ext || !a->conv || !a->mt || !a->pr || !a->fw || !a->fws) return -1;
     if (a->m < 0 || a->top < 0 || a->top >= a->nq || a->ntg < 1 || a->rows < a->nq + a->kp) return -1;
-    if (a->kp < 1 || a->kp > MDC_MAX_KP) return -2;
+    if (a->kp < 1 || a->kp > MDC_MAX_KP || a->ntg > MDC_MAX_NTG) return -2;
     if (a->m == 0) return 0;
     switch (logn) {
         case 12: return ntt::mdc<12>(a, s);

@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(WG) fwd_cols(NttArgs A, int row0) {
     }
     // stages h = R/2 .. TR (rows): index R/(2h) + r/(2h)
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
-    phase_a<true, H, G::TR>(x, w, ws, p, p2, base);
+    phase_a<true, H, G::TR, decltype(base), true>(x, w, ws, p, p2, base);
     constexpr int LS = G::CC + G::CPAD;
 #pragma unroll
     for (int j = 0; j < E; ++j) lds[(tau + G::TR * j) * LS + col] = x[j];
@@ -171,7 +171,7 @@ __global__ void __launch_bounds__(WG) inv_cols(NttArgs A, int row0) {
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = lds[(tau + G::TR * j) * LS + col];
-    phase_a<false, H, G::TR>(x, w, ws, p, p2, base);
+    phase_a<false, H, G::TR, decltype(base), true>(x, w, ws, p, p2, base);
     // the scale: es[i] per row (NttArgs ABI 17) or N^-1 of the prime; Shoup takes the lazy words whole
     uint32_t s, ss;
     if (A.es) {

@@ -79,15 +79,31 @@ __device__ __forceinline__ void ldtw(const uint32_t* p, uint32_t (&v)[8]) {
     }
 }
 
-// Layout A (e = tau + T j), stage h = T 2^K: pairs (j, j + 2^K), group j / 2^(K+1), index base(h) + group.
-template <bool FWD, bool H, int T, int K, class Base>
+// NG twiddles at a workgroup-uniform address, through the scalar cache into scalar registers (the tables are read-only
+// for the whole launch)
+typedef __attribute__((address_space(4))) const uint32_t* cptr;
+template <int NG>
+__device__ __forceinline__ void ldtw_uniform(const uint32_t* p, uint32_t (&v)[8]) {
+    const cptr q = (cptr)p;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) v[i] = q[i];
+}
+
+// Layout A (e = tau + T j), stage h = T 2^K: pairs (j, j + 2^K), group j / 2^(K+1), index base(h) + group. UNI: base()
+// is the same for every thread of the workgroup (the column passes).
+template <bool FWD, bool H, int T, int K, class Base, bool UNI = false>
 __device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p,
                                         uint32_t p2, Base base) {
     constexpr int hh = 1 << K, NG = 8 >> K;
     const uint32_t b0 = base(T << K);
     uint32_t tw[8], tws[8];
-    ldtw<NG>(w + b0, tw);
-    ldtw<NG>(ws + b0, tws);
+    if constexpr (UNI) {
+        ldtw_uniform<NG>(w + b0, tw);
+        ldtw_uniform<NG>(ws + b0, tws);
+    } else {
+        ldtw<NG>(w + b0, tw);
+        ldtw<NG>(ws + b0, tws);
+    }
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         if (j & hh) continue;
@@ -96,19 +112,19 @@ __device__ __forceinline__ void stage_a(uint32_t (&x)[E], const uint32_t* w, con
         else gs<H>(x[j], x[j + hh], tw[g], tws[g], p, p2);
     }
 }
-template <bool FWD, bool H, int T, class Base>
+template <bool FWD, bool H, int T, class Base, bool UNI = false>
 __device__ __forceinline__ void phase_a(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, uint32_t p,
                                         uint32_t p2, Base base) {
     if (FWD) {
-        stage_a<FWD, H, T, 3>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 2>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 1>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 0>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 3, Base, UNI>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 2, Base, UNI>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 1, Base, UNI>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 0, Base, UNI>(x, w, ws, p, p2, base);
     } else {
-        stage_a<FWD, H, T, 0>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 1>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 2>(x, w, ws, p, p2, base);
-        stage_a<FWD, H, T, 3>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 0, Base, UNI>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 1, Base, UNI>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 2, Base, UNI>(x, w, ws, p, p2, base);
+        stage_a<FWD, H, T, 3, Base, UNI>(x, w, ws, p, p2, base);
     }
 }
 // Layout B (e = 16 tau + j), stage h = 2^K < T: pairs (j, j + h), group (16 tau + j) / (2h).

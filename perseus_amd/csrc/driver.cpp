@@ -585,14 +585,18 @@ int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc
     return c->tab->ntt_fwd(&f, s);
 }
 
+// the identity rotation: Q rows 0..top of both parts, one launch of the table's ew_copy
 int copy_q(pcx_ctx* c, const void* ct, int top, void* out, pc_stream_t s) {
-    const size_t part = (size_t)c->rows * c->n * 4, q = (size_t)(top + 1) * c->n * 4;
-    for (int p = 0; p < 2; ++p) {
-        hipError_t e = hipMemcpyAsync((char*)out + p * part, (const char*)ct + p * part, q, hipMemcpyDeviceToDevice,
-                                      (hipStream_t)s);
-        if (e != hipSuccess) return (int)e;
-    }
-    return 0;
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    EwArgs a;
+    memset(&a, 0, sizeof a);
+    a.out = PolyRef{out, 0, part};
+    a.a = PolyRef{const_cast<void*>(ct), 0, part};
+    a.rs = RowSet{top + 1, 0, 0, 0};
+    a.pr = c->pr;
+    a.K = 1;
+    a.nparts = 2;
+    return c->tab->ew_copy(&a, s);
 }
 
 void pack_row(const uint32_t* v, uint32_t n, int bits, uint32_t* out, uint64_t row_words) {

@@ -293,3 +293,42 @@ def test_device_keygen(stream, name, bits):
         s_new = oc.automorph_rows(s_eval, twin.galois_inverse(gal, ch.n))
         want = oc.ksk_gen(s_new, s_eval, seeds[r], e)
         assert (keys.download_b(r) == want).all(), r
+
+
+# ----------------------------------------------------------------------------------------------- graph capture
+def test_graph_replay(stream):
+    """The hoisted batch captured into a HIP graph (the launchers never allocate, synchronise or read device data on
+    the host) and replayed three times, with eager work and a cleared output between replays: every replay equals the
+    eager result word for word."""
+    import ctypes as C
+
+    say("[graph] small hoisted, 3 replays")
+    ch, ctx, oc = contexts("small", k_rot=4)
+    steps = [1, 2, 0, 5]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=13)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1
+    ct = random_ct(ch, top, 14)
+    dev = pa.DevBuf.from_array(ct)
+    idx = list(range(len(steps)))
+    eager = ctx.ct_buf(len(steps))
+    ctx.rotate_hoisted(keys, idx, dev, top, eager, stream)
+    stream.sync()
+    want = eager.download((len(steps), 2, ch.rows, ch.n))
+    out = ctx.ct_buf(len(steps))
+    graph, exe = C.c_void_p(), C.c_void_p()
+    pa.check(pa.LIB.pc_hip_graph_begin_capture(stream.h), "begin_capture")
+    ctx.rotate_hoisted(keys, idx, dev, top, out, stream)
+    pa.check(pa.LIB.pc_hip_graph_end_capture(stream.h, C.byref(graph)), "end_capture")
+    pa.check(pa.LIB.pc_hip_graph_instantiate(C.byref(exe), graph), "instantiate")
+    try:
+        for rep in range(3):
+            out.zero()
+            ctx.rotate_hoisted(keys, idx[::-1], dev, top, eager, stream)  # eager work between replays
+            pa.check(pa.LIB.pc_hip_graph_launch(exe, stream.h), "graph_launch")
+            stream.sync()
+            got = out.download((len(steps), 2, ch.rows, ch.n))
+            assert (got[:, :, : top + 1] == want[:, :, : top + 1]).all(), rep
+    finally:
+        pa.LIB.pc_hip_graph_exec_destroy(exe)
+        pa.LIB.pc_hip_graph_destroy(graph)

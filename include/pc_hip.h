@@ -249,9 +249,51 @@ typedef struct KsKeyArgs {
 } KsKeyArgs;
 PC_STATIC_ASSERT(sizeof(KsKeyArgs) == 216, "KsKeyArgs layout");
 
+/* args.cuh:325-355: the fused CtS / StC stage core (hoisted baby-step rotations times the BSGS plaintext diagonals
+ * in the extended basis, gather form). For output slot o of row t = rows[y]:
+ *   rot_0[o] = (P c0[o], P c1[o]) on Q rows, 0 on special rows (P = pmod[t], Shoup companion pmods[t]); with x0
+ *              non-null, x0's words as stored (every row);
+ *   rot_i[o] = (P c0[s] + sum_d D_d[s] b_{i,d}[s], sum_d D_d[s] a_{i,d}[s]), s = automorph_slot(kinv[i-1], o),
+ *              D_d = c1 on the rows of digit d (digit_of), else modup's digit d;
+ *   res_j[o] = sum_i rot_i[o] pt_{B j + i}[prow][ptidx(o, enc)], j < G, diagonals >= npts skipped; prow = t on Q rows,
+ *              pt_prow + (t - nq) on special rows; ptidx = o >> (enc & 0xFF) when enc >> 24 == 0x7F, else o & enc.
+ * Ciphertext c at x + c ct_stride (c1 at + part_stride), ModUp at modup + c mu_ct_stride + d mu_digit_stride, baby keys
+ * kb / ka [i-1] + d key_digit_stride + t N; results (c, j) at res + (c G + j) ct_stride, or with pair_cts > 0 (K = 1
+ * regen launches of up to 4 giant steps) at res + ((j >> 1) pair_cts + (j & 1)) ct_stride. Strides in words; rows of
+ * N words, 16-byte aligned. */
+typedef struct CtsArgs {
+    const void* x;
+    const void* modup;
+    void* res;
+    const void* const* kb;
+    const void* const* ka;
+    const uint32_t* kinv;
+    const void* const* pts;
+    const uint32_t* rows;
+    const int32_t* digit_of;
+    const void* pmod;
+    const void* pmods;
+    const PrimeConst* pr;
+    uint64_t ct_stride, part_stride, mu_ct_stride, mu_digit_stride, key_digit_stride;
+    int32_t K, B, G, npts, ndig, nq, nlive, ptw, pt_prow;
+    uint32_t enc;
+    int32_t ngrp;
+    int32_t nrows, kmax;
+    int32_t pair_cts;
+    const void* x0;
+} CtsArgs;
+PC_STATIC_ASSERT(sizeof(CtsArgs) == 200, "CtsArgs layout");
+
+/* args.cuh:752-757: cts_fused with the baby keys through a KeyTab: `b` read in its stored form (dense or packed),
+ * `a` regenerated for digits < key.nregen, else read from cts.ka */
+typedef struct CtsRegenArgs {
+    CtsArgs cts;
+    KeyTab key;
+} CtsRegenArgs;
+PC_STATIC_ASSERT(sizeof(CtsRegenArgs) == 240, "CtsRegenArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct PtDotArgs;
-struct CtsArgs;
 struct TensorArgs;
 struct MdEpiArgs;
 struct WsumArgs;
@@ -265,7 +307,6 @@ struct SmallIntArgs;
 struct SpruExtractArgs;
 struct SpruFftArgs;
 struct SpruScatterArgs;
-struct CtsRegenArgs;
 struct PcmmArgs;
 struct CcmmArgs;
 struct WsumKArgs;
@@ -304,7 +345,7 @@ typedef struct KernelTable {
     int (*ks_dot)(const KsArgs*, pc_stream_t);
     int (*ks_dot_regen)(const KsRegenArgs*, pc_stream_t);
     int (*ksk_expand)(const KskExpandArgs*, pc_stream_t);
-    int (*cts_fused)(const struct CtsArgs*, pc_stream_t);
+    int (*cts_fused)(const CtsArgs*, pc_stream_t);
     int (*tensor)(const struct TensorArgs*, pc_stream_t);
     int (*md_epilogue)(const struct MdEpiArgs*, pc_stream_t);
     int (*wsum)(const struct WsumArgs*, pc_stream_t);
@@ -322,7 +363,7 @@ typedef struct KernelTable {
     int (*spru_extract)(const struct SpruExtractArgs*, pc_stream_t);
     int (*spru_fft_pass)(const struct SpruFftArgs*, pc_stream_t);
     int (*spru_scatter)(const struct SpruScatterArgs*, pc_stream_t);
-    int (*cts_fused_regen)(const struct CtsRegenArgs*, pc_stream_t);
+    int (*cts_fused_regen)(const CtsRegenArgs*, pc_stream_t);
     int (*ks_dot_key)(const KsKeyArgs*, pc_stream_t);
     int (*pcmm)(const struct PcmmArgs*, pc_stream_t);
     int (*ccmm)(const struct CcmmArgs*, pc_stream_t);
@@ -438,6 +479,16 @@ int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ou
  * k_rot, output j at out + j * ct_words (words) */
 int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
                        pc_stream_t s);
+/* One CtS / StC stage's hoisted baby steps and plaintext products (crates/pc-gpu/src/bts/cts.rs:840-960, LtStage::run
+ * steps 1 and 2): ModUp of ct's c1 once, then through the table's cts_fused_regen
+ *   res_j = sum_{i < B} rot_i(ct) pt_{B j + i},  j < G,
+ * in the extended basis (Q rows 0..top and the special rows), rot_0 = P ct and rot_i (i >= 1) the key switch before
+ * ModDown by key r0 + i - 1 of the group, its `a` regenerated in the kernel. pts: a DEVICE array of npts device
+ * pointers to diagonals of top + 1 + kp rows (Q rows 0..top, then the special rows) of ptw words; enc the compact index
+ * map (0xFFFFFFFF: full rows; 0x7F000000 | s: o >> s; else o & enc). res: G extended ciphertexts, res_j at
+ * res + j ct_words. */
+int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
+                  uint32_t enc, const void* ct, int top, void* res, pc_stream_t s);
 /* the stages alone, for tests and profiles: ModUp of ct's c1 into the context's digit workspace; the dot of key r
  * into ext (one extended ciphertext); ModDown of ext into out */
 int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);
@@ -447,9 +498,10 @@ int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s);
 
 /* Stage timing, for measurement: while on, the driver records a HIP event pair on the launch stream around each
  * stage it enqueues (0 ModUp INTT, 1 ModUp conversion, 2 ModUp NTT, 3 key dot, 4 ModDown INTT, 5 ModDown conversion,
- * 6 ModDown NTT + epilogue). pcx_timing(c, n) turns it on for up to n stages (resetting the record); 0 turns it off.
- * pcx_timing_read sums the device time of one stage after the stream has synchronised. No counterpart in the
- * reference (its benches time with CUDA events around whole ops, crates/pc-gpu/benches/ks.rs:80-98). */
+ * 6 ModDown NTT + epilogue, 7 CtS baby steps and plaintext products). pcx_timing(c, n) turns it on for up to n stages
+ * (resetting the record); 0 turns it off. pcx_timing_read sums the device time of one stage after the stream has
+ * synchronised. No counterpart in the reference (its benches time with CUDA events around whole ops,
+ * crates/pc-gpu/benches/ks.rs:80-98). */
 int pcx_timing(pcx_ctx* c, int max_stages);
 int pcx_timing_read(pcx_ctx* c, int stage, double* total_ms, int* count);
 

@@ -168,10 +168,11 @@ constexpr uint32_t KSK_T_MAX = 16;
 
 // keys.rs:478-498 (kska_expand_row): one base block per 16 slots, attempt t reads block b0 + t N/16, accept
 // v < floor((2^32-1)/p) p, the 16th attempt kept as is; value v mod p
-void kska_row(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t* out) {
+// (slots [s0, s0 + cnt), both multiples of 16; out[i] is slot s0 + i)
+void kska_range(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t s0, uint32_t cnt, uint32_t* out) {
     const uint32_t n16 = n >> 4, mp = (0xFFFFFFFFu / p) * p;
     uint32_t base[16], alt[16];
-    for (uint32_t b0 = 0; b0 < n16; ++b0) {
+    for (uint32_t b0 = s0 >> 4; b0 < (s0 + cnt) >> 4; ++b0) {
         chacha_block(seed, b0, digit, p, TAG_KSKA, 12, base);
         for (int w = 0; w < 16; ++w) {
             uint32_t v = base[w];
@@ -179,9 +180,12 @@ void kska_row(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint
                 chacha_block(seed, b0 + t * n16, digit, p, TAG_KSKA, 12, alt);
                 v = alt[w];
             }
-            out[b0 * 16 + w] = v % p;
+            out[b0 * 16 + w - s0] = v % p;
         }
     }
+}
+void kska_row(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t* out) {
+    kska_range(seed, digit, p, n, 0, n, out);
 }
 
 // ------------------------------------------------------------------------------------------------ DRBG
@@ -764,6 +768,104 @@ void or_rotate_hoisted(const or_ctx* c, const uint32_t* ct, int top, int nkeys, 
         or_ks_dot(c, ct, digits.data(), top, seeds + 8 * r, bs[r], autok, ext.data());
         or_moddown(c, ext.data(), top, outs[r]);
     }
+}
+
+// crates/pc-host/src/cts.rs:24-200 (run, fetch_keys): per (row, 2048-slot chunk) task, baby i >= 1 formed at its
+// source slots in source order and gathered to the outputs, baby 0 = P x (or x0), then sum_i rot_i pt_{Bj+i} per giant
+// step. Residues are canonical, so the device's reductions every 8 baby steps leave no trace; here every sum is exact
+// (u128) and reduced once.
+void or_cts_fused(const or_ctx* c, int K, const uint32_t* x, const uint32_t* digits, int top, int B, int G, int npts,
+                  const uint32_t* seeds, const uint32_t* const* bs, const uint32_t* const* as, int nregen,
+                  const uint32_t* kinv, const uint32_t* const* pts, int ptw, int pt_prow, uint32_t enc,
+                  const uint32_t* pmod, const uint32_t* x0, uint32_t* res) {
+    check_top(c, top);
+    const uint32_t n = c->n;
+    const int R = c->rows(), nd = live_digits(c, top);
+    const size_t ctw = (size_t)2 * R * n, pw = (size_t)R * n;
+    std::vector<int> rows;
+    for (int t = 0; t <= top; ++t) rows.push_back(t);
+    for (int j = 0; j < c->kp; ++j) rows.push_back(c->nq + j);
+    const uint32_t CH = std::min<uint32_t>(2048, n), nch = n / CH;
+    auto ptidx = [enc](uint32_t o) { return (enc >> 24) == 0x7Fu ? o >> (enc & 0xFFu) : o & enc; };
+    parallel_for((long)rows.size() * nch, [&](long task) {
+        const int t = rows[task / nch];
+        const uint32_t o0 = (uint32_t)(task % nch) * CH;
+        const uint64_t p = c->primes[t];
+        const bool isq = t < c->nq;
+        const int prow = isq ? t : pt_prow + (t - c->nq);
+        const int dt = isq ? c->digit_of(t) : -1;
+        const uint64_t pm = isq ? (pmod ? pmod[t] : c->pmodq[t]) : 0;
+        const size_t roff = (size_t)t * n;
+        std::vector<u128> acc0((size_t)K * G * CH, 0), acc1((size_t)K * G * CH, 0);
+        std::vector<uint64_t> v0((size_t)K * CH), v1((size_t)K * CH);
+        std::vector<uint32_t> a(n), src(CH);
+        for (int i = 0; i < B; ++i) {
+            if (i == 0) {
+                for (int k = 0; k < K; ++k)
+                    for (uint32_t l = 0; l < CH; ++l) {
+                        const size_t at = (size_t)k * ctw + roff + o0 + l;
+                        if (x0) {
+                            v0[(size_t)k * CH + l] = x0[at];
+                            v1[(size_t)k * CH + l] = x0[at + pw];
+                        } else {
+                            v0[(size_t)k * CH + l] = isq ? mulmod(x[at], pm, p) : 0;
+                            v1[(size_t)k * CH + l] = isq ? mulmod(x[at + pw], pm, p) : 0;
+                        }
+                    }
+            } else {
+                // an aligned chunk's sources form one aligned chunk [sb, sb + CH)
+                for (uint32_t l = 0; l < CH; ++l) src[l] = or_automorph_slot(kinv[i - 1], o0 + l, c->logn);
+                const uint32_t sb = src[0] & ~(CH - 1);
+                std::vector<u128> s0((size_t)K * CH, 0), s1((size_t)K * CH, 0);
+                for (int d = 0; d < nd; ++d) {
+                    const uint32_t* bd = bs[i - 1] + ((size_t)d * R + t) * n;
+                    const uint32_t* ad;
+                    if (d < nregen) {
+                        kska_range(seeds + 8 * (i - 1), (uint32_t)d, (uint32_t)p, n, sb, CH, a.data() + sb);
+                        ad = a.data();
+                    } else {
+                        ad = as[i - 1] + ((size_t)d * R + t) * n;
+                    }
+                    for (int k = 0; k < K; ++k) {
+                        const uint32_t* D = d == dt ? x + (size_t)k * ctw + pw + roff
+                                                    : digits + (size_t)k * c->dnum * pw + (size_t)d * pw + roff;
+                        for (uint32_t l = 0; l < CH; ++l) {
+                            const uint32_t s = src[l];
+                            s0[(size_t)k * CH + l] += (u128)D[s] * bd[s];
+                            s1[(size_t)k * CH + l] += (u128)D[s] * ad[s];
+                        }
+                    }
+                }
+                for (int k = 0; k < K; ++k)
+                    for (uint32_t l = 0; l < CH; ++l) {
+                        u128 z0 = s0[(size_t)k * CH + l];
+                        if (isq) z0 += (u128)mulmod(x[(size_t)k * ctw + roff + src[l]], pm, p);
+                        v0[(size_t)k * CH + l] = (uint64_t)(z0 % p);
+                        v1[(size_t)k * CH + l] = (uint64_t)(s1[(size_t)k * CH + l] % p);
+                    }
+            }
+            for (int j = 0; j < G; ++j) {
+                const int dg = B * j + i;
+                if (dg >= npts) continue;
+                const uint32_t* pr = pts[dg] + (size_t)prow * ptw;
+                for (uint32_t l = 0; l < CH; ++l) {
+                    const uint64_t w = pr[ptidx(o0 + l)];
+                    for (int k = 0; k < K; ++k) {
+                        acc0[((size_t)k * G + j) * CH + l] += (u128)v0[(size_t)k * CH + l] * w;
+                        acc1[((size_t)k * G + j) * CH + l] += (u128)v1[(size_t)k * CH + l] * w;
+                    }
+                }
+            }
+        }
+        for (int k = 0; k < K; ++k)
+            for (int j = 0; j < G; ++j) {
+                uint32_t* r = res + ((size_t)k * G + j) * ctw + roff + o0;
+                for (uint32_t l = 0; l < CH; ++l) {
+                    r[l] = (uint32_t)(acc0[((size_t)k * G + j) * CH + l] % p);
+                    r[pw + l] = (uint32_t)(acc1[((size_t)k * G + j) * CH + l] % p);
+                }
+            }
+    });
 }
 
 void or_ksk_gen(const or_ctx* c, const uint32_t* s_new, const uint32_t* s_old, const uint32_t seed[8],

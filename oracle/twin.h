@@ -94,6 +94,24 @@ void or_rotate(const or_ctx* c, const uint32_t* ct, int top, const uint32_t seed
 void or_rotate_hoisted(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const uint32_t* seeds,
                        const uint32_t* const* bs, const uint64_t* gs, uint32_t* const* outs);
 
+/* fused CtS / StC stage (crates/pc-host/src/cts.rs:24-200 `run`, semantics crates/pc-kernels/kernels/cts.cuh:1-10):
+ * K ciphertexts x (ct c at x + c*2*R*N) at limb top, with their ModUp digits (ct c at digits + c*dnum*R*N).
+ * For every row t of Q 0..top u P and output slot o:
+ *   baby 0:      (P c0[o], P c1[o]) on Q rows and 0 on special rows; with x0 non-null, x0's words as stored
+ *                (ct c at x0 + c*2*R*N, every row);
+ *   baby i >= 1: the key-switch dot of baby key i-1 at the source slot s = automorph_slot(kinv[i-1], o):
+ *                (P c0[s] + sum_d D_d[s] b_d[s], sum_d D_d[s] a_d[s]), P c0 on Q rows only;
+ *   res_j[o]:    sum_{i < B} rot_i[o] pt_{B j + i}[prow][ptidx(o, enc)], diagonals >= npts skipped.
+ * Baby keys: seeds[8 (i-1)], b rows bs[i-1] (full layout [dnum][R][N]). a_d is regenerated from the seed for d < nregen,
+ * else read from as[i-1] (same layout; may be null when nregen covers every digit). pmod: P mod q_t per Q prime id
+ * (null: the context's). Diagonal k is pts[k] ([rows][ptw]); prow = t on Q rows, pt_prow + (t - nq) on special rows;
+ * ptidx (crates/pc-kernels/kernels/arith.cuh:242-244) maps o to o >> (enc & 0xFF) when enc >> 24 == 0x7F, else o & enc.
+ * Writes res ct (c, j) at res + (c*G + j)*2*R*N, rows of Q 0..top u P, both parts. */
+void or_cts_fused(const or_ctx* c, int K, const uint32_t* x, const uint32_t* digits, int top, int B, int G, int npts,
+                  const uint32_t* seeds, const uint32_t* const* bs, const uint32_t* const* as, int nregen,
+                  const uint32_t* kinv, const uint32_t* const* pts, int ptw, int pt_prow, uint32_t enc,
+                  const uint32_t* pmod, const uint32_t* x0, uint32_t* res);
+
 /* switching-key generation (crates/pc-kernels/kernels/keygen.cuh ksk_gen; crates/pc-gpu/src/keygen.rs:172-262):
  * b[d][t] = e[d][t] - a_d[t] s_new[t] + [t in digit d] (P mod q_t) s_old[t], every digit and every row of Q u P
  * (eval form; a from the KSKA expander of seed) */

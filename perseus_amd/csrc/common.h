@@ -66,6 +66,21 @@ __device__ __forceinline__ uint32_t automorph_slot(uint32_t k, uint32_t slot, in
     return brev_n(r, logn);
 }
 
+// Scatter addresses of the automorphism inside a 1024-slot chunk. With V = ((2 brev(s) + 1) k) mod 2N for source slot
+// s, the output slot's offset in its chunk is brev10 of W = the top 10 bits of V, and W is affine in the lane:
+// W = C + k (brev6(lane) + 64 brev4(j)) mod 1024 for the lane's word j. Storing the word at rotr1(W) (a 10-bit rotate
+// right) makes both the 64 lanes' writes of one j and the reads of output offsets 16 lane + j fall on 32 distinct
+// banks per half wave; the offset 16 lane + j is read back from rotr1(64 brev4(j) + brev6(lane)).
+__device__ __forceinline__ uint32_t scat_addr(uint32_t w) { return (w >> 1) | ((w & 1) << 9); }
+__device__ __forceinline__ uint32_t brev4(uint32_t j) { return __brev(j) >> 28; }
+
+// Wave-level ordering of LDS traffic between the lanes of one wave (no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ------------------------------------------------------------------------------------------------ ChaCha12
 constexpr uint32_t TAG_KSKA = 0x4b534b41u;  // "KSKA" (crates/pc-core/src/keys.rs:460)
 constexpr uint32_t TAG_ENCA = 0x454e4341u;  // "ENCA" (args.cuh:790)

@@ -252,6 +252,7 @@ struct pcx_keys {
     const void** kb = nullptr;        // device array of per-key b pointers
     const uint32_t** seed = nullptr;  // device array of per-key seed pointers
     uint32_t* autok = nullptr;        // g^-1 mod 2N per key
+    uint32_t* kinv = nullptr;         // g mod 2N per key (the gather exponent of a CtS baby step)
     std::vector<void*> b_ptr;         // device b storage per key
     // the KSKA retry-value table (dense keys): offsets [key][digit][row][chunk] + 1, values
     uint32_t *pidx = nullptr, *pval = nullptr;
@@ -646,6 +647,13 @@ pcx_keys* keys_shell(pcx_ctx* c, int nkeys, const uint64_t* galois, int bits, in
         k->autok_h.push_back((uint32_t)powmod(g, (m >> 2) - 1, m));  // g^-1 (crates/pc-core/src/galois.rs:50-59)
     }
     k->autok = k->dev.upload(k->autok_h);
+    std::vector<uint32_t> gh(k->galois.begin(), k->galois.end());
+    k->kinv = k->dev.upload(gh);
+    if (!k->autok || !k->kinv) {
+        *err = k->dev.err ? k->dev.err : -1;
+        delete k;
+        return nullptr;
+    }
     return k;
 }
 
@@ -1095,6 +1103,59 @@ int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ou
     if (int e = modup(c, ct, top, s)) return e;
     if (int e = dot(c, k, r, 1, ct, top, c->ext, s)) return e;
     return moddown(c, c->ext, c->conv, 1, top, out, s);
+}
+
+int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
+                  uint32_t enc, const void* ct, int top, void* res, pc_stream_t s) {
+    const Level* L = c ? level(c, top) : nullptr;
+    if (!L || !k || k->c != c || B < 1 || G < 1 || npts < 0 || !pts || !ct || !res) return -1;
+    if (B > 1 && (r0 < 0 || r0 + B - 1 > k->nkeys)) return -1;
+    if (B > 1)
+        if (int e = modup(c, ct, top, s)) return e;
+    CtsRegenArgs ra;
+    memset(&ra, 0, sizeof ra);
+    CtsArgs& a = ra.cts;
+    a.x = ct;
+    a.modup = c->digits;
+    a.kinv = k->kinv + (B > 1 ? r0 : 0);
+    a.rows = L->ks_rows;
+    a.digit_of = c->digit_of;
+    a.pmod = c->pmod;
+    a.pmods = c->pmod + (c->nq + c->kp);
+    a.pr = c->pr;
+    a.ct_stride = c->ct_words();
+    a.part_stride = (uint64_t)c->rows * c->n;
+    a.mu_ct_stride = (uint64_t)c->dnum * c->rows * c->n;
+    a.mu_digit_stride = (uint64_t)c->rows * c->n;
+    a.K = 1;
+    a.B = B;
+    a.ndig = L->ndig;
+    a.nq = c->nq;
+    a.nlive = top + 1;
+    a.ptw = ptw;
+    a.pt_prow = top + 1;
+    a.enc = enc;
+    a.nrows = L->nks;
+    a.kmax = 1;
+    a.pair_cts = 2;  // giant steps 2l, 2l + 1 at res + 2l, 2l + 1 cts: the results contiguous
+    KeyTab& t = ra.key;
+    t.kb = k->kb + (B > 1 ? r0 : 0);
+    t.seed = k->seed + (B > 1 ? r0 : 0);
+    t.row_words = k->row_words;
+    t.bits = k->bits;
+    t.q_top = -1;
+    t.srows = c->rows;
+    t.nregen = c->dnum;
+    Stage st(c, 7, s);
+    for (int j0 = 0; j0 < G; j0 += 4) {
+        // up to four giant steps per launch: the baby keys regenerated once per launch
+        a.G = std::min(4, G - j0);
+        a.pts = pts + (size_t)j0 * B;
+        a.npts = std::max(0, npts - j0 * B);
+        a.res = (uint32_t*)res + (size_t)j0 * c->ct_words();
+        if (int e = c->tab->cts_fused_regen(&ra, s)) return e;
+    }
+    return 0;
 }
 
 int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,

@@ -28,14 +28,6 @@ __device__ __forceinline__ int slot_of(const KeyTab& T, int t, int nq) {
     return (t < nq || T.q_top < 0) ? t : T.q_top + 1 + (t - nq);
 }
 
-// Scatter addresses of the automorphism inside a 1024-slot chunk. With V = ((2 brev(s) + 1) k) mod 2N for source slot
-// s, the output slot's offset in its chunk is brev10 of W = the top 10 bits of V, and W is affine in the lane:
-// W = C + k (brev6(lane) + 64 brev4(j)) mod 1024 for the lane's word j. Storing the word at rotr1(W) (a 10-bit rotate
-// right) makes both the 64 lanes' writes of one j and the reads of output offsets 16 lane + j fall on 32 distinct
-// banks per half wave; the offset 16 lane + j is read back from rotr1(64 brev4(j) + brev6(lane)).
-__device__ __forceinline__ uint32_t scat_addr(uint32_t w) { return (w >> 1) | ((w & 1) << 9); }
-__device__ __forceinline__ uint32_t brev4(uint32_t j) { return __brev(j) >> 28; }
-
 // The 16 KSKA values of slots [s0, s0 + 16) of (seed, digit d, prime p) (crates/pc-core/src/keys.rs:466-498): block
 // s0/16 of the ChaCha12 stream with state words (counter, d, p, "KSKA"); a rejected word is redrawn from block
 // s0/16 + t N/16 (t = 1..15), the 16th attempt kept as is; value v mod p.
@@ -60,13 +52,6 @@ __device__ __forceinline__ void kska16(const uint32_t (&seed)[8], uint32_t s0, u
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) a[j] = ex.red(o[j]);
-}
-
-// Wave-level ordering of LDS traffic between the lanes of one wave (no workgroup barrier).
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 constexpr int KW = 4;               // waves per workgroup: each takes one key at a time
@@ -95,10 +80,11 @@ struct DotCtx {
     }
 };
 
-// Redraw the queued words of one wave: item = digit << 16 | slot; each lane takes items and adds D_d a_d (the
-// accepted attempt of the word, attempts t = 1..15 at block + t N/16) to the slot's 64-bit sum.
+// Redraw the queued words of one wave: item = digit << 16 | slot; each lane takes items and adds D_d a_d mod p (the
+// accepted attempt of the word, attempts t = 1..15 at block + t N/16) to the slot's 64-bit sum. Reduced products keep
+// the sum below ndig 2^31 however many of a slot's digits were redrawn.
 __device__ __forceinline__ void drain(DotLds& L, DotLds::Wave& W, const DotCtx& X, int lane, const uint32_t (&seed)[8],
-                                      const Expander& ex, uint32_t n16) {
+                                      const Expander& ex, const Red& red, uint32_t n16) {
     wave_sync();
     const uint32_t nq = W.qn;
     for (uint32_t i = lane; i < nq; i += DBX) {
@@ -110,7 +96,7 @@ __device__ __forceinline__ void drain(DotLds& L, DotLds::Wave& W, const DotCtx& 
             if (v < ex.mp) break;
         }
         const uint32_t xd = d < (uint32_t)MAXD ? L.D[d][sl] : X.dptr((int)d)[X.chunk0 + sl];
-        atomicAdd((unsigned long long*)&W.ex[sl], (unsigned long long)((uint64_t)xd * ex.red(v)));
+        atomicAdd((unsigned long long*)&W.ex[sl], (unsigned long long)red((uint64_t)xd * ex.red(v)));
     }
     wave_sync();
     if (lane == 0) W.qn = 0;
@@ -238,9 +224,9 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
                 }
                 // room for a whole digit's words before the next one (wave-uniform: qn is shared)
                 wave_sync();
-                if (W.qn > (uint32_t)(QCAP - DCH)) drain(L, W, X, lane, seed, ex, n16);
+                if (W.qn > (uint32_t)(QCAP - DCH)) drain(L, W, X, lane, seed, ex, red, n16);
             }
-            drain(L, W, X, lane, seed, ex, n16);
+            drain(L, W, X, lane, seed, ex, red, n16);
             uint32_t r0[DS], r1[DS];
 #pragma unroll
             for (int k = 0; k < DS; ++k) {
@@ -250,7 +236,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
                     r1[k] = addm(addm(part1[k], red(s1a[k]), p), red(e), p);
                 } else {
                     r0[k] = red(s0a[k]);
-                    r1[k] = red(s1a[k] + e);  // every (slot, digit) counted once: at most ndig <= 4 products
+                    r1[k] = red(s1a[k] + e);  // ndig <= 4 products of (p - 1)^2 plus ndig words below p: < 2^64
                 }
             }
             if ((pc0 && !fold_c0) || m0 == 2) {

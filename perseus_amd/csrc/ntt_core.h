@@ -241,13 +241,6 @@ __device__ __forceinline__ void phase_b_t(uint32_t (&x)[E], const Tw& t, uint32_
     }
 }
 
-// Wave-level ordering of LDS traffic between the lanes of one wave.
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // A row-pass block's 16 words of thread tau through the block's LDS (C + C/16 words, one padding word per 16):
 // layout B (e = 16 tau + j) -> layout A (e = tau + T j) and back. The block lives in one wave.
 template <int T>

@@ -172,6 +172,13 @@ class Context:
         check(LIB.pcx_rotate_hoisted(self.h, keys.h, arr, len(idx), ct.addr(), top, out.addr(), stream.h),
               "rotate_hoisted")
 
+    def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
+        """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}
+        in the extended basis, babies i >= 1 by keys r0 + i - 1. pts: a DevBuf holding npts device pointers (uint64)
+        to the diagonals [top + 1 + kp rows][ptw]; res: G extended ciphertexts."""
+        check(LIB.pcx_cts_stage(self.h, keys.h, r0, B, G, pts.addr(), npts, ptw, enc, ct.addr(), top, res.addr(),
+                                stream.h), "cts_stage")
+
 
 class Keys:
     """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed."""

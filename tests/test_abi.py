@@ -56,3 +56,63 @@ def test_chains_match_the_oracle_primes():
     assert (len(c3.q), len(c3.p), c3.dnum, c3.alpha) == (30, 6, 3, 10)
     c1 = pa.preset("c1")
     assert (len(c1.q), len(c1.p), c1.dnum, c1.alpha, c1.logn) == (12, 4, 3, 4, 14)
+
+
+def test_entry_names_follow_the_header():
+    """perseus_amd.abi.ENTRIES is KernelTable's field order (args.cuh:1037-1097) as include/pc_hip.h declares it."""
+    import re
+    from perseus_amd import abi
+    text = open(pa._lib.HEADER).read()
+    body = text[text.index("typedef struct KernelTable"):text.index("} KernelTable;")]
+    assert re.findall(r"\(\*(\w+)\)", body) == abi.ENTRIES
+
+
+def test_cts_launchers_reject_out_of_range_arguments():
+    """The CtS launchers' argument checks (crates/pc-kernels/kernels/cts.cuh:480-524 launch_any / launch_regen, plus
+    this kernel's own range), all decided before any device call."""
+    from perseus_amd import abi
+    a = abi.CtsArgs()
+    a.K, a.B, a.G, a.ndig, a.nrows, a.kmax, a.npts, a.ptw, a.enc = 1, 3, 2, 3, 4, 1, 6, 4096, 0xFFFFFFFF
+    fused = lambda: abi.call("cts_fused", a, log_n=12)  # noqa: E731
+    a.G = 3
+    assert fused() == -1                       # three giant steps outside the pair form
+    a.G, a.pair_cts = 2, 2
+    assert fused() == -1                       # the pair layout is a regen-form feature
+    a.pair_cts, a.ndig = 0, 7
+    assert fused() == -1                       # more than 6 digits
+    a.ndig, a.x0, a.kmax = 3, 0x1000, 2
+    assert fused() == -1                       # x0 with groups of ciphertexts
+    a.x0, a.kmax, a.K = None, 1, 0
+    assert fused() == 0                        # nothing to do
+    a.K = 1
+    assert fused() == -1                       # null row list
+    r = abi.CtsRegenArgs()
+    r.cts.K, r.cts.B, r.cts.G, r.cts.ndig, r.cts.nrows, r.cts.kmax, r.cts.ptw = 1, 3, 4, 3, 4, 1, 4096
+    r.cts.enc, r.cts.npts = 0xFFFFFFFF, 12
+    regen = lambda: abi.call("cts_fused_regen", r, log_n=12)  # noqa: E731
+    r.key.bits = 33
+    assert regen() == -1                       # packed width above 32
+    r.key.bits = 0
+    assert regen() == -1                       # four giant steps need the pair layout
+    r.cts.pair_cts, r.cts.G = 2, 5
+    assert regen() == -1                       # at most four in it
+    r.cts.G, r.cts.K = 4, 2
+    assert regen() == -1                       # the pair layout is for one ciphertext
+    r.cts.K, r.cts.B = 1, 65
+    assert regen() == -1                       # at most 64 baby steps
+    r.cts.B, r.cts.x0 = 3, 0x1000
+    assert regen() == -1                       # x0 outside the four-giant-step form only
+    r.cts.x0 = None
+    assert regen() == -1                       # null row list
+    b = abi.CtsRegenArgs()
+    c = b.cts
+    c.K, c.B, c.G, c.ndig, c.nrows, c.kmax, c.npts = 1, 2, 2, 3, 4, 1, 2
+    c.rows = c.pr = c.x = c.res = c.digit_of = c.pmod = c.pmods = c.pts = c.kinv = c.modup = 0x1000
+    b.key.kb = b.key.seed = 0x1000
+    b.key.nregen = 3
+    c.enc, c.ptw = 0x7F000003, 511
+    assert abi.call("cts_fused_regen", b, log_n=12) == -1   # a block-constant diagonal needs N >> 3 words
+    c.enc, c.ptw = 0x3FF, 1023
+    assert abi.call("cts_fused_regen", b, log_n=12) == -1   # a periodic one (o & enc) needs enc + 1
+    c.ptw, c.ct_stride = 1024, 2 * 8 * 4096 + 1
+    assert abi.call("cts_fused_regen", b, log_n=12) == -2   # rows of whole 16-byte groups

@@ -67,6 +67,9 @@ def _load():
         "or_rotation_key": (None, [C.c_void_p, C.c_void_p, u32p, C.c_uint64, u32p, u32p]),
         "or_secret_eval": (None, [C.c_void_p, i8p, u32p]),
         "or_automorph_rows": (None, [C.c_void_p, u32p, C.c_uint32, C.c_int, u32p]),
+        "or_cts_fused": (None, [C.c_void_p, C.c_int, u32p, u32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                C.c_void_p, C.c_void_p, C.c_int, u32p, C.c_void_p, C.c_int, C.c_int, C.c_uint32,
+                                C.c_void_p, C.c_void_p, u32p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -146,6 +149,10 @@ class Ctx:
         self.h = LIB.or_ctx_new(logn, arr, self.nq, self.kp, dnum)
         if not self.h:
             raise ValueError("invalid chain")
+        big_p = 1
+        for x in self.p:
+            big_p *= int(x)
+        self.pmodq = [big_p % int(x) for x in self.q]  # P mod q_t
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -215,6 +222,30 @@ class Ctx:
                               np.ascontiguousarray(seeds, np.uint32).reshape(-1), ptr_array(bs),
                               np.asarray(gs, np.uint64), ptr_array(outs))
         return outs
+
+    def cts_fused(self, x, digits, top, B, G, pts, kinv, seeds=None, bs=(), as_=None, nregen=None, pt_prow=None,
+                  enc=0xFFFFFFFF, pmod=None, x0=None):
+        """The fused CtS stage of K = len(x) ciphertexts (or_cts_fused): res[c][j] = sum_i rot_i(x_c) pt_{B j + i}.
+        pts: list of diagonals [prow rows][ptw]; kinv: B-1 gather exponents; seeds [B-1][8], bs / as_ [B-1] full-layout
+        key rows; nregen (default: every digit) digits of a regenerated from the seed, the rest read from as_."""
+        x = np.ascontiguousarray(x, np.uint32)
+        K = x.shape[0]
+        digits = np.ascontiguousarray(digits, np.uint32)
+        nd = self.dnum if nregen is None else nregen
+        bs = [np.ascontiguousarray(b, np.uint32) for b in bs]
+        as_ = [np.ascontiguousarray(a, np.uint32) for a in as_] if as_ is not None else []
+        pts = [np.ascontiguousarray(p, np.uint32) for p in pts]
+        ptw = pts[0].shape[-1]
+        res = np.zeros((K, G, 2, self.rows, self.n), np.uint32)
+        sd = np.ascontiguousarray(seeds if seeds is not None else np.zeros((max(B - 1, 1), 8)), np.uint32)
+        ki = np.ascontiguousarray(np.asarray(kinv, np.uint32).reshape(-1) if B > 1 else np.zeros(1), np.uint32)
+        pm = None if pmod is None else np.ascontiguousarray(pmod, np.uint32)
+        x0a = None if x0 is None else np.ascontiguousarray(x0, np.uint32)
+        LIB.or_cts_fused(self.h, K, x, digits, top, B, G, len(pts), sd.ctypes.data, ptr_array(bs) if bs else None,
+                         ptr_array(as_) if as_ else None, nd, ki, ptr_array(pts), ptw,
+                         top + 1 if pt_prow is None else pt_prow, enc, None if pm is None else pm.ctypes.data,
+                         None if x0a is None else x0a.ctypes.data, res)
+        return res
 
     def ksk_gen(self, s_new, s_old, seed, e):
         b = np.zeros((self.dnum, self.rows, self.n), np.uint32)

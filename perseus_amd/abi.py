@@ -39,7 +39,37 @@ class CtsRegenArgs(C.Structure):
     _fields_ = [("cts", CtsArgs), ("key", KeyTab)]
 
 
+class KsArgs(C.Structure):
+    """args.cuh:211-228: the key-switch inner product (176 bytes)."""
+    _fields_ = [("c1", vp), ("modup", vp), ("c0", vp), ("out0", vp), ("out1", vp), ("kb", vp), ("ka", vp),
+                ("autok", vp), ("rows", vp), ("digit_of", vp), ("pmod", vp), ("pmods", vp), ("pr", vp),
+                ("ct_stride", u64), ("mu_ct_stride", u64), ("mu_digit_stride", u64), ("out_ct_stride", u64),
+                ("out_rot_stride", u64), ("key_digit_stride", u64), ("K", i32), ("R", i32), ("ndig", i32),
+                ("c0_mode", i32), ("nq", i32), ("nrows", i32)]
+
+
+class KsKeyArgs(C.Structure):
+    """args.cuh:997-1003: ks_dot with the keys through a KeyTab (216 bytes)."""
+    _fields_ = [("ks", KsArgs), ("key", KeyTab)]
+
+
+class EpiArgs(C.Structure):
+    """args.cuh:268-281: the fused relinearisation epilogue (72 bytes)."""
+    _fields_ = [("dst", vp), ("conv", vp), ("binv", vp), ("binvs", vp), ("k", vp), ("part_stride", u64),
+                ("dbl", i32), ("pad", i32), ("alpha", vp), ("alphas", vp)]
+
+
+class KsRegenArgs(C.Structure):
+    """args.cuh:299-307: the relinearisation dot with a regenerated key (312 bytes)."""
+    _fields_ = [("ks", KsArgs), ("seed", vp), ("epi", EpiArgs), ("use_epi", i32), ("pad", i32), ("key", KeyTab),
+                ("add", vp)]
+
+
+KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:208-210)
+
 assert C.sizeof(KeyTab) == 40 and C.sizeof(CtsArgs) == 200 and C.sizeof(CtsRegenArgs) == 240
+assert C.sizeof(KsArgs) == 176 and C.sizeof(KsKeyArgs) == 216 and C.sizeof(EpiArgs) == 72
+assert C.sizeof(KsRegenArgs) == 312
 
 _LAUNCHER = C.CFUNCTYPE(C.c_int, vp, vp)
 

@@ -49,4 +49,7 @@ int kska_patch_fill(int logn, const uint32_t* const* seeds, const PrimeConst* pr
 // the fast dot with the retry values read from P instead of redrawn; -2 where the fast dot does not apply
 int ks_dot_patched(int logn, const KsKeyArgs* g, const PatchTab* P, pc_stream_t s);
 
+// ks_dot_key's summed rotations (c0_mode | KS_SUM): out = sum_r sigma_r(dot_r), gathered in output order
+int ks_dot_key_sum(int logn, const KsKeyArgs* g, pc_stream_t s);
+
 }  // namespace pch

@@ -691,14 +691,14 @@ int ks_dot(const KsArgs* a, pc_stream_t s) {
     return dot_launch<LOGN>(*a, none, 0, s);
 }
 
-// ks_dot_key: keys through a KeyTab (crates/pc-host/src/ks.rs:164-200: bits outside 0..=32 -1, K > 4 -2). The summed
-// rotations (KS_SUM) are not implemented in this build: -3.
+// ks_dot_key: keys through a KeyTab (crates/pc-host/src/ks.rs:164-200: bits outside 0..=32 -1, K > 4 -2); the summed
+// rotations (KS_SUM) run the gather-form kernel.
 template <int LOGN>
 int ks_dot_key(const KsKeyArgs* g, pc_stream_t s) {
     if (!g) return -1;
     if (g->key.bits < 0 || g->key.bits > 32) return -1;
     if (g->ks.K > 4) return -2;
-    if (g->ks.c0_mode & PC_KS_SUM) return -3;
+    if (g->ks.c0_mode & PC_KS_SUM) return ks_dot_key_sum(LOGN, g, s);
     if (!g->key.kb || (g->key.nregen > 0 && !g->key.seed)) return -1;
     if (g->ks.ndig > g->key.nregen && !g->ks.ka) return -1;
     if (g->key.bits > 0 && (g->key.row_words % 4 != 0)) return -1;

@@ -19,7 +19,8 @@ namespace pch {
     int ksk_gen_##L(const KskGenArgs*, pc_stream_t);                 \
     int ksk_unpack_##L(const KskUnpackArgs*, pc_stream_t);          \
     int cts_fused_##L(const CtsArgs*, pc_stream_t);                  \
-    int cts_fused_regen_##L(const CtsRegenArgs*, pc_stream_t);
+    int cts_fused_regen_##L(const CtsRegenArgs*, pc_stream_t);       \
+    int ks_dot_regen_##L(const KsRegenArgs*, pc_stream_t);
 PCH_DECL(12)
 PCH_DECL(13)
 PCH_DECL(14)
@@ -35,7 +36,7 @@ int absent(const A*, pc_stream_t) {
     static const KernelTable TABLE_##L = {                                                                           \
         PC_KERNELS_ABI, 4, 0, L,                                                                                     \
         ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
-        absent<PtDotArgs>, ks_dot_##L, absent<KsRegenArgs>, ksk_expand_##L, cts_fused_##L, absent<TensorArgs>,        \
+        absent<PtDotArgs>, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, absent<TensorArgs>,        \
         absent<MdEpiArgs>, absent<WsumArgs>, absent<AddConstArgs>, absent<MulTableArgs>, absent<RescaleArgs>,        \
         absent<RescaleCombineArgs>, automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L,             \
         ksk_unpack_##L, absent<ModRaiseArgs>, absent<SmallIntArgs>, absent<SpruExtractArgs>, absent<SpruFftArgs>,    \

@@ -149,7 +149,7 @@ class Context:
     def moddown(self, ext, top, out, stream):
         check(LIB.pcx_moddown(self.h, ext.addr(), top, out.addr(), stream.h), "moddown")
 
-    STAGES = ("modup_intt", "modup_bconv", "modup_ntt", "dot", "md_intt", "md_bconv", "md_ntt")
+    STAGES = ("modup_intt", "modup_bconv", "modup_ntt", "dot", "md_intt", "md_bconv", "md_ntt", "cts")
 
     def timing(self, max_stages):
         """Record device time per stage (0 turns it off)."""

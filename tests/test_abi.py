@@ -116,3 +116,27 @@ def test_cts_launchers_reject_out_of_range_arguments():
     assert abi.call("cts_fused_regen", b, log_n=12) == -1   # a periodic one (o & enc) needs enc + 1
     c.ptw, c.ct_stride = 1024, 2 * 8 * 4096 + 1
     assert abi.call("cts_fused_regen", b, log_n=12) == -2   # rows of whole 16-byte groups
+
+
+def test_dot_launchers_reject_out_of_range_arguments():
+    """ks_dot_regen's checks (crates/pc-host/src/ks.rs:267-280) and ks_dot's refusal of the summed rotations
+    (KS_SUM: -3, crates/pc-host/src/ks.rs:151-153), decided before any device call."""
+    from perseus_amd import abi
+    g = abi.KsRegenArgs()
+    g.ks.K, g.ks.nrows, g.ks.ndig = 1, 2, 3
+    g.key.kb, g.key.bits = 0x1000, 33
+    assert abi.call("ks_dot_regen", g, log_n=12) == -1     # packed width above 32
+    g.key.bits, g.add = 0, 0x1000
+    assert abi.call("ks_dot_regen", g, log_n=12) == -1     # `add` outside the fused epilogue
+    g.add, g.ks.K = None, 5
+    assert abi.call("ks_dot_regen", g, log_n=12) == -2     # more than 4 ciphertexts
+    g.ks.K = 0
+    assert abi.call("ks_dot_regen", g, log_n=12) == 0      # nothing to do
+    g.ks.K = 1
+    assert abi.call("ks_dot_regen", g, log_n=12) == -1     # null row list
+    k = abi.KsArgs()
+    k.c0_mode, k.K = abi.KS_SUM, 1
+    assert abi.call("ks_dot", k, log_n=12) == -3           # the summed rotations: ks_dot_key only
+    kk = abi.KsKeyArgs()
+    kk.ks.c0_mode, kk.ks.K = abi.KS_SUM, 5
+    assert abi.call("ks_dot_key", kk, log_n=12) == -2      # K > 4

@@ -96,6 +96,7 @@ def preset(name: str) -> Chain:
     c2: the batched NTT round trip, N = 2^16, 40 primes below 2^31;
     c3: the hoisted rotation batch, N = 2^16, 30 Q primes below 2^31, dnum 3, 6 special primes;
     small: a quick test chain, N = 2^12, 6 Q + 2 special 30-bit primes, dnum 3;
+    small28: the same at 28-bit primes (a bootstrapping stage's word size);
     rej: N = 2^12, 6 Q + 3 special primes just above 2^32 / 3, where a third of the KSKA words are rejected.
     """
     if name == "c1":
@@ -106,6 +107,8 @@ def preset(name: str) -> Chain:
         return make("c3", 16, 30, 6, 3, 31)
     if name == "small":
         return make("small", 12, 6, 2, 3, 30)
+    if name == "small28":
+        return make("small28", 12, 6, 2, 3, 28)
     if name == "small31":
         return make("small31", 12, 6, 3, 3, 31)
     if name == "rej":

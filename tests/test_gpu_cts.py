@@ -84,6 +84,7 @@ def oracle_keys(oc, ch, steps, seed):
     ("small31", 5, 3, 15, 0x7FF, 5, 31),      # packed b, periodic diagonals, a second launch for giant step 2
     ("c3", 5, 2, 10, FULL, 29, 0),            # the C3 chain at its full shape
     ("rej", 4, 2, 8, FULL, 5, 0),             # a third of the KSKA words rejected: the wave's redraw queue
+    ("small28", 9, 4, 33, FULL, 5, 28),       # 28-bit primes, more than 8 baby steps: the reference's own regime
 ])
 def test_cts_stage(stream, name, B, G, npts, enc, top, bits):
     say(f"[cts stage] {name} B={B} G={G} npts={npts} enc={enc:#x} top={top} bits={bits}")

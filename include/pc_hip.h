@@ -479,6 +479,18 @@ int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ou
  * k_rot, output j at out + j * ct_words (words) */
 int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
                        pc_stream_t s);
+/* out = onto + sum_j rot(ct, key idx[j]) (crates/pc-gpu/src/rotate.rs:692-776 rotate_sum_core, InModDown form): ModUp
+ * once, the key dots summed in the extended basis (runs of consecutive keys through the table's ks_dot_key with
+ * KS_SUM, later runs added with KS_ACC), then ONE ModDown whose epilogue adds onto `onto` (onto == out: in place;
+ * NULL: out = the sum alone). No key of the sum may be the identity (-1). */
+int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
+                   const void* onto, pc_stream_t s);
+/* The rotate-and-sum ladder (crates/pc-gpu/src/rotate.rs:924-992): out = the sum of x over its rotations by every
+ * multiple of start below stop (start < 0: the negative steps), rung by rung (out += rot(out, gap), gap doubling), or
+ * radix_bits >= 2 rungs at a time through pcx_rotate_sum when the group holds every step of the rung. tmp: a scratch
+ * ciphertext. The group must hold the key of every step the ladder takes (-1 otherwise). */
+int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
+                       void* out, void* tmp, pc_stream_t s);
 /* One CtS / StC stage's hoisted baby steps and plaintext products (crates/pc-gpu/src/bts/cts.rs:840-960, LtStage::run
  * steps 1 and 2): ModUp of ct's c1 once, then through the table's cts_fused_regen
  *   res_j = sum_{i < B} rot_i(ct) pt_{B j + i},  j < G,

@@ -868,6 +868,115 @@ void or_cts_fused(const or_ctx* c, int K, const uint32_t* x, const uint32_t* dig
     });
 }
 
+// crates/pc-gpu/src/rotate.rs:692-776 (rotate_sum_core, InModDown form) with ks.rs:1675-1710 (moddown_sum_to_j): one
+// ModUp, the extended rotations summed word by word, one ModDown, the result added onto `onto` (Q rows 0..top)
+int or_rotate_sum(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const uint32_t* seeds,
+                  const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, uint32_t* out) {
+    check_top(c, top);
+    const uint32_t n = c->n;
+    const int R = c->rows();
+    const size_t ctw = (size_t)2 * R * n;
+    if (nkeys < 1) return -1;
+    for (int r = 0; r < nkeys; ++r)
+        if (gs[r] % (2ull * n) == 1) return -1;  // no step 0 in a sum group
+    std::vector<uint32_t> digits((size_t)c->dnum * R * n, 0), ext(ctw, 0), sum(ctw, 0), res(ctw, 0);
+    or_modup(c, ct + (size_t)R * n, top, digits.data());
+    for (int r = 0; r < nkeys; ++r) {
+        or_ks_dot(c, ct, digits.data(), top, seeds + 8 * r, bs[r], (uint32_t)or_galois_inverse(gs[r], n), ext.data());
+        for (int part = 0; part < 2; ++part)
+            for (int t = 0; t < R; ++t) {
+                if (t > top && t < c->nq) continue;
+                const uint32_t p = (uint32_t)c->primes[t];
+                const size_t o = ((size_t)part * R + t) * n;
+                for (uint32_t i = 0; i < n; ++i) sum[o + i] = addm(sum[o + i], ext[o + i], p);
+            }
+    }
+    or_moddown(c, sum.data(), top, res.data());
+    for (int part = 0; part < 2; ++part)
+        for (int t = 0; t <= top; ++t) {
+            const uint32_t p = (uint32_t)c->primes[t];
+            const size_t o = ((size_t)part * R + t) * n;
+            for (uint32_t i = 0; i < n; ++i) out[o + i] = onto ? addm(onto[o + i], res[o + i], p) : res[o + i];
+        }
+    return 0;
+}
+
+// crates/pc-gpu/src/rotate.rs:924-992 (rotate_and_sum): gaps start, 2 start, ... below stop; radix rungs through
+// or_rotate_sum onto out when the keys hold every step of the rung, else rung by rung: tmp = rot(out or x), out += tmp
+int or_rotate_and_sum(const or_ctx* c, const uint32_t* x, int top, int64_t start, int64_t stop, int radix_bits,
+                      int nkeys, const uint32_t* seeds, const uint32_t* const* bs, const uint64_t* gs, uint32_t* out) {
+    check_top(c, top);
+    const uint32_t n = c->n;
+    const int R = c->rows();
+    const size_t ctw = (size_t)2 * R * n;
+    if (start == 0 || stop <= 0) return -1;
+    auto key_of = [&](int64_t st) {
+        const uint64_t g = or_rotation_galois(st, n);
+        for (int i = 0; i < nkeys; ++i)
+            if (gs[i] % (2ull * n) == g) return i;
+        return -1;
+    };
+    auto copy_q = [&](const uint32_t* src, uint32_t* dst) {
+        for (int part = 0; part < 2; ++part)
+            memcpy(dst + (size_t)part * R * n, src + (size_t)part * R * n, 4ull * (top + 1) * n);
+    };
+    const int64_t sign = start > 0 ? 1 : -1, gap = start > 0 ? start : -start;
+    if (gap >= stop) {
+        copy_q(x, out);
+        return 0;
+    }
+    std::vector<int64_t> gaps;
+    for (int64_t g = gap; g < stop; g *= 2) gaps.push_back(g);
+    const size_t rb = radix_bits >= 2 ? (size_t)radix_bits : 1;
+    std::vector<uint32_t> tmp(ctw, 0), cur(ctw, 0);
+    bool have = false;
+    for (size_t i0 = 0; i0 < gaps.size();) {
+        const size_t m = std::min(rb, gaps.size() - i0);
+        if (rb >= 2 && m > 1) {
+            std::vector<int> idx;
+            for (int64_t j = 1; j < ((int64_t)1 << m); ++j) idx.push_back(key_of(sign * j * gaps[i0]));
+            if (std::find(idx.begin(), idx.end(), -1) == idx.end()) {
+                if (!have) {
+                    copy_q(x, out);
+                    have = true;
+                }
+                std::vector<uint32_t> sd;
+                std::vector<const uint32_t*> bb;
+                std::vector<uint64_t> gg;
+                for (int i : idx) {
+                    sd.insert(sd.end(), seeds + 8 * i, seeds + 8 * i + 8);
+                    bb.push_back(bs[i]);
+                    gg.push_back(gs[i]);
+                }
+                copy_q(out, cur.data());
+                if (int e = or_rotate_sum(c, cur.data(), top, (int)idx.size(), sd.data(), bb.data(), gg.data(),
+                                          cur.data(), out))
+                    return e;
+                i0 += m;
+                continue;
+            }
+        }
+        for (size_t r = 0; r < m; ++r) {
+            const int key = key_of(sign * gaps[i0 + r]);
+            if (key < 0) return -1;
+            copy_q(have ? out : x, cur.data());
+            or_rotate(c, cur.data(), top, seeds + 8 * key, bs[key], gs[key], tmp.data());
+            if (!have) {
+                copy_q(x, out);
+                have = true;
+            }
+            for (int part = 0; part < 2; ++part)
+                for (int t = 0; t <= top; ++t) {
+                    const uint32_t p = (uint32_t)c->primes[t];
+                    const size_t o = ((size_t)part * R + t) * n;
+                    for (uint32_t i = 0; i < n; ++i) out[o + i] = addm(out[o + i], tmp[o + i], p);
+                }
+        }
+        i0 += m;
+    }
+    return 0;
+}
+
 void or_ksk_gen(const or_ctx* c, const uint32_t* s_new, const uint32_t* s_old, const uint32_t seed[8],
                 const uint32_t* e, uint32_t* b) {
     const uint32_t n = c->n;

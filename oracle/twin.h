@@ -94,6 +94,17 @@ void or_rotate(const or_ctx* c, const uint32_t* ct, int top, const uint32_t seed
 void or_rotate_hoisted(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const uint32_t* seeds,
                        const uint32_t* const* bs, const uint64_t* gs, uint32_t* const* outs);
 
+/* summed rotations (crates/pc-gpu/src/rotate.rs:692-776 rotate_sum_core, InModDown form): one ModUp, the extended
+ * rotations by keys (seeds, bs, gs) summed word by word, one ModDown; out (Q rows 0..top) = onto + that (onto may be
+ * NULL, or alias ct / out). -1 for an identity key or no keys. */
+int or_rotate_sum(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const uint32_t* seeds,
+                  const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, uint32_t* out);
+/* the rotate-and-sum ladder (crates/pc-gpu/src/rotate.rs:924-992) over the keys (seeds, bs, gs): out = the sum of x
+ * over its rotations by every multiple of start below stop; radix_bits >= 2 rungs through or_rotate_sum. -1 when a
+ * step's key is missing. */
+int or_rotate_and_sum(const or_ctx* c, const uint32_t* x, int top, int64_t start, int64_t stop, int radix_bits,
+                      int nkeys, const uint32_t* seeds, const uint32_t* const* bs, const uint64_t* gs, uint32_t* out);
+
 /* fused CtS / StC stage (crates/pc-host/src/cts.rs:24-200 `run`, semantics crates/pc-kernels/kernels/cts.cuh:1-10):
  * K ciphertexts x (ct c at x + c*2*R*N) at limb top, with their ModUp digits (ct c at digits + c*dnum*R*N).
  * For every row t of Q 0..top u P and output slot o:

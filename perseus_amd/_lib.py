@@ -68,6 +68,8 @@ _SIGS = {
     "pcx_ct_words": (C.c_size_t, [vp]),
     "pcx_rotate": (C.c_int, [vp, vp, C.c_int, vp, C.c_int, vp, vp]),
     "pcx_rotate_hoisted": (C.c_int, [vp, vp, C.POINTER(C.c_int), C.c_int, vp, C.c_int, vp, vp]),
+    "pcx_rotate_sum": (C.c_int, [vp, vp, C.POINTER(C.c_int), C.c_int, vp, C.c_int, vp, vp, vp]),
+    "pcx_rotate_and_sum": (C.c_int, [vp, vp, vp, C.c_int, C.c_int64, C.c_int64, C.c_int, vp, vp, vp]),
     "pcx_cts_stage": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_uint32, vp, C.c_int, vp,
                                 vp]),
     "pcx_modup": (C.c_int, [vp, vp, C.c_int, vp]),

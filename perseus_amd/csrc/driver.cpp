@@ -473,8 +473,9 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
     return c->tab->ntt_fwd(&f, s);
 }
 
-// the dot of keys [r0, r0 + m) of k into m extended ciphertexts at ext (crates/pc-gpu/src/ks.rs:1225-1308 dot_key)
-int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s) {
+// the dot of keys [r0, r0 + m) of k into m extended ciphertexts at ext (crates/pc-gpu/src/ks.rs:1225-1308 dot_key);
+// sum: 1 sums the m rotations into ext's first ciphertext (KS_SUM), 2 adds that sum onto it (KS_SUM | KS_ACC)
+int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0) {
     const Level* L = level(c, top);
     if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys) return -1;
     KsKeyArgs g;
@@ -502,7 +503,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     a.K = 1;
     a.R = m;
     a.ndig = L->ndig;
-    a.c0_mode = 1;
+    a.c0_mode = 1 | (sum ? PC_KS_SUM : 0) | (sum == 2 ? PC_KS_ACC : 0);
     a.nq = c->nq;
     a.nrows = L->nks;
     KeyTab& t = g.key;
@@ -514,7 +515,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     t.srows = c->rows;
     t.nregen = c->dnum;
     Stage st(c, 3, s);
-    if (k->pval) {
+    if (k->pval && !sum) {
         // the retry values from the key group's table (no redraw in the dot)
         // the table is indexed by the group's key: the launch's key r is the group's r0 + r
         const size_t per_key = (size_t)c->dnum * c->rows * (c->n / 1024);
@@ -526,8 +527,10 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
 }
 
 // ModDown of m extended ciphertexts at ext into m ciphertexts at out (crates/pc-gpu/src/ks.rs:1620-1649): INTT of the
-// P rows (N^-1 pre_j), conversion P -> Q rows 0..top into conv, NTT of conv with the epilogue (ext - conv) P^-1
-int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc_stream_t s) {
+// P rows (N^-1 pre_j), conversion P -> Q rows 0..top into conv, NTT of conv with the epilogue (ext - conv) P^-1;
+// onto non-null: onto + (ext - conv) P^-1 (onto == out: added in place; crates/pc-gpu/src/ks.rs:1675-1710 MdOut)
+int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc_stream_t s,
+            const void* onto = nullptr) {
     const Level* L = level(c, top);
     if (!L || m < 1 || m > c->k_rot) return -1;
     const Rows& ri = L->md_intt[m - 1];
@@ -540,7 +543,8 @@ int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc
     }
     const Rows& rn = L->md_ntt[m - 1];
     NttArgs f = ntt_args(c, conv, rn, rn.n);
-    f.epi = 1;
+    f.epi = onto ? 2 : 1;
+    f.ed = onto == out ? nullptr : onto;
     f.eout = out;
     f.ex = ext;
     f.xnum = 1;
@@ -584,6 +588,21 @@ int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc
     }
     Stage st(c, 6, s);
     return c->tab->ntt_fwd(&f, s);
+}
+
+// out = a + b on Q rows 0..top of both parts (the table's ew_add)
+int add_q(pcx_ctx* c, const void* a, const void* b, int top, void* out, pc_stream_t s) {
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    EwArgs e;
+    memset(&e, 0, sizeof e);
+    e.out = PolyRef{out, 0, part};
+    e.a = PolyRef{const_cast<void*>(a), 0, part};
+    e.b = PolyRef{const_cast<void*>(b), 0, part};
+    e.rs = RowSet{top + 1, 0, 0, 0};
+    e.pr = c->pr;
+    e.K = 1;
+    e.nparts = 2;
+    return c->tab->ew_add(&e, s);
 }
 
 // the identity rotation: Q rows 0..top of both parts, one launch of the table's ew_copy
@@ -1186,6 +1205,74 @@ int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const voi
         if (int e = dot(c, k, idx[j], m, ct, top, c->ext, s)) return e;
         if (int e = moddown(c, c->ext, c->conv, m, top, (uint32_t*)out + j * cw, s)) return e;
         j += m;
+    }
+    return 0;
+}
+
+int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
+                   const void* onto, pc_stream_t s) {
+    if (!c || !k || k->c != c || n < 1 || !idx || !ct || !out || !level(c, top)) return -1;
+    for (int j = 0; j < n; ++j)
+        if (idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;  // no step 0 in a sum group
+    if (int e = modup(c, ct, top, s)) return e;
+    // runs of consecutive keys, one summed dot each, the later runs added onto the first's sum
+    for (int j = 0; j < n;) {
+        int m = 1;
+        while (j + m < n && idx[j + m] == idx[j] + m) ++m;
+        if (int e = dot(c, k, idx[j], m, ct, top, c->ext, s, j == 0 ? 1 : 2)) return e;
+        j += m;
+    }
+    return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
+}
+
+int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
+                       void* out, void* tmp, pc_stream_t s) {
+    if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top)) return -1;
+    if (start == 0 || stop <= 0) return -1;
+    const uint64_t m2 = 2ull * c->n;
+    // the key of a rotation step (g = 5^step mod 2N; negative steps by the inverse), -1 if the group has none
+    auto key_of = [&](int64_t st) {
+        const int64_t h = (int64_t)(c->n / 2);
+        const uint64_t r = (uint64_t)(((st % h) + h) % h);
+        const uint64_t g = powmod(5, r, m2);
+        for (int i = 0; i < k->nkeys; ++i)
+            if (k->galois[i] == g) return i;
+        return -1;
+    };
+    const int64_t sign = start > 0 ? 1 : -1, gap = start > 0 ? start : -start;
+    if (gap >= stop) return copy_q(c, x, top, out, s);
+    std::vector<int64_t> gaps;
+    for (int64_t g = gap; g < stop; g *= 2) gaps.push_back(g);
+    const size_t rb = radix_bits >= 2 ? (size_t)radix_bits : 1;
+    bool have = false;
+    for (size_t i0 = 0; i0 < gaps.size();) {
+        const size_t n = std::min(rb, gaps.size() - i0);
+        if (rb >= 2 && n > 1) {
+            // one rung of radix 2^n: out += sum over j < 2^n of rot(out, j gap) when the group holds every step
+            std::vector<int> idx;
+            for (int64_t j = 1; j < ((int64_t)1 << n); ++j) idx.push_back(key_of(sign * j * gaps[i0]));
+            if (std::find(idx.begin(), idx.end(), -1) == idx.end()) {
+                if (!have) {
+                    if (int e = copy_q(c, x, top, out, s)) return e;
+                    have = true;
+                }
+                if (int e = pcx_rotate_sum(c, k, idx.data(), (int)idx.size(), out, top, out, out, s)) return e;
+                i0 += n;
+                continue;
+            }
+        }
+        for (size_t r = 0; r < n; ++r) {
+            const int key = key_of(sign * gaps[i0 + r]);
+            if (key < 0) return -1;
+            // tmp = rot(out, step) (rot(x, step) on the first rung), then out += tmp
+            if (int e = pcx_rotate(c, k, key, have ? out : x, top, tmp, s)) return e;
+            if (!have) {
+                if (int e = copy_q(c, x, top, out, s)) return e;
+                have = true;
+            }
+            if (int e = add_q(c, out, tmp, top, out, s)) return e;
+        }
+        i0 += n;
     }
     return 0;
 }

@@ -172,6 +172,17 @@ class Context:
         check(LIB.pcx_rotate_hoisted(self.h, keys.h, arr, len(idx), ct.addr(), top, out.addr(), stream.h),
               "rotate_hoisted")
 
+    def rotate_sum(self, keys, idx, ct, top, out, stream, onto=None):
+        """out = onto + sum_j rot(ct, key idx[j]): one ModUp, the dots summed, one ModDown (pcx_rotate_sum)."""
+        arr = (C.c_int * len(idx))(*idx)
+        check(LIB.pcx_rotate_sum(self.h, keys.h, arr, len(idx), ct.addr(), top, out.addr(),
+                                 None if onto is None else onto.addr(), stream.h), "rotate_sum")
+
+    def rotate_and_sum(self, keys, x, top, start, stop, out, tmp, stream, radix_bits=1):
+        """The rotate-and-sum ladder: out = sum of x over its rotations by the multiples of start below stop."""
+        check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(), tmp.addr(),
+                                     stream.h), "rotate_and_sum")
+
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}
         in the extended basis, babies i >= 1 by keys r0 + i - 1. pts: a DevBuf holding npts device pointers (uint64)

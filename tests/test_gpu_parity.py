@@ -295,6 +295,53 @@ def test_device_keygen(stream, name, bits):
         assert (keys.download_b(r) == want).all(), r
 
 
+# ----------------------------------------------------------------------------------------------- summed rotations
+@pytest.mark.parametrize("name,idx,mode", [("small", [0, 1, 2], "onto"), ("small", [2, 0], "plain"),
+                                           ("small", [1, 3, 0, 2], "in_place"), ("c3", [0, 1, 2, 3], "onto")])
+def test_rotate_sum(stream, name, idx, mode):
+    """out = onto + ModDown(sum of the dots): runs of consecutive keys through the KS_SUM dot (later runs added with
+    KS_ACC), one ModDown with the add-onto epilogue."""
+    say(f"[rotate_sum] {name} keys={idx} {mode}")
+    ch, ctx, oc = contexts(name, k_rot=4)
+    twin.set_threads(16)
+    steps = [1, 3, 2, 7]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=17)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1 if name == "c3" else 5
+    ct = random_ct(ch, top, 21)
+    dev = pa.DevBuf.from_array(ct)
+    if mode == "in_place":
+        ctx.rotate_sum(keys, idx, dev, top, dev, stream, onto=dev)
+        out = dev
+    else:
+        out = ctx.ct_buf()
+        ctx.rotate_sum(keys, idx, dev, top, out, stream, onto=dev if mode == "onto" else None)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.rotate_sum(ct, top, seeds[idx], [bs[i] for i in idx], [gals[i] for i in idx],
+                         onto=None if mode == "plain" else ct)
+    assert (got[:, : top + 1] == want[:, : top + 1]).all()
+
+
+@pytest.mark.parametrize("name,radix", [("small", 1), ("small", 2), ("c3", 2)])
+def test_rotate_and_sum(stream, name, radix):
+    say(f"[rotate_and_sum] {name} start=1 stop=16 radix_bits={radix}")
+    ch, ctx, oc = contexts(name, k_rot=4)
+    twin.set_threads(16)
+    steps = [1, 2, 3, 4, 8, 12]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=19)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1 if name == "c3" else 5
+    ct = random_ct(ch, top, 23)
+    dev = pa.DevBuf.from_array(ct)
+    out, tmp = ctx.ct_buf(), ctx.ct_buf()
+    ctx.rotate_and_sum(keys, dev, top, 1, 16, out, tmp, stream, radix_bits=radix)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.rotate_and_sum(ct, top, 1, 16, seeds, bs, gals, radix_bits=radix)
+    assert (got[:, : top + 1] == want[:, : top + 1]).all()
+
+
 # ----------------------------------------------------------------------------------------------- graph capture
 def test_graph_replay(stream):
     """The hoisted batch captured into a HIP graph (the launchers never allocate, synchronise or read device data on

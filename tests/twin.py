@@ -67,6 +67,9 @@ def _load():
         "or_rotation_key": (None, [C.c_void_p, C.c_void_p, u32p, C.c_uint64, u32p, u32p]),
         "or_secret_eval": (None, [C.c_void_p, i8p, u32p]),
         "or_automorph_rows": (None, [C.c_void_p, u32p, C.c_uint32, C.c_int, u32p]),
+        "or_rotate_sum": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p, u32p]),
+        "or_rotate_and_sum": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int64, C.c_int64, C.c_int, C.c_int, u32p,
+                                        C.c_void_p, u64p, u32p]),
         "or_cts_fused": (None, [C.c_void_p, C.c_int, u32p, u32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                 C.c_void_p, C.c_void_p, C.c_int, u32p, C.c_void_p, C.c_int, C.c_int, C.c_uint32,
                                 C.c_void_p, C.c_void_p, u32p]),
@@ -222,6 +225,29 @@ class Ctx:
                               np.ascontiguousarray(seeds, np.uint32).reshape(-1), ptr_array(bs),
                               np.asarray(gs, np.uint64), ptr_array(outs))
         return outs
+
+    def rotate_sum(self, ct, top, seeds, bs, gs, onto=None):
+        """onto + ModDown(sum of the extended rotations of ct by the keys): one ModUp, one ModDown."""
+        out = self.ct_zeros()
+        bs = [np.ascontiguousarray(b, np.uint32) for b in bs]
+        on = None if onto is None else np.ascontiguousarray(onto, np.uint32)
+        rc = LIB.or_rotate_sum(self.h, np.ascontiguousarray(ct, np.uint32), top, len(gs),
+                               np.ascontiguousarray(seeds, np.uint32).reshape(-1), ptr_array(bs),
+                               np.asarray(gs, np.uint64), None if on is None else on.ctypes.data, out)
+        if rc:
+            raise ValueError("rotate_sum: an identity key or no keys")
+        return out
+
+    def rotate_and_sum(self, x, top, start, stop, seeds, bs, gs, radix_bits=1):
+        """The rotate-and-sum ladder over the keys (seeds, bs, gs)."""
+        out = self.ct_zeros()
+        bs = [np.ascontiguousarray(b, np.uint32) for b in bs]
+        rc = LIB.or_rotate_and_sum(self.h, np.ascontiguousarray(x, np.uint32), top, start, stop, radix_bits, len(gs),
+                                   np.ascontiguousarray(seeds, np.uint32).reshape(-1), ptr_array(bs),
+                                   np.asarray(gs, np.uint64), out)
+        if rc:
+            raise ValueError("rotate_and_sum: a step's key is missing")
+        return out
 
     def cts_fused(self, x, digits, top, B, G, pts, kinv, seeds=None, bs=(), as_=None, nregen=None, pt_prow=None,
                   enc=0xFFFFFFFF, pmod=None, x0=None):

@@ -48,7 +48,6 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
     }
     __syncthreads();
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
-    constexpr int LS = G::CC + G::CPAD;
     for (int t = t0; t < t1; ++t) {
         const Red red(A.pr[t]);
         const uint32_t p = red.p, p2 = 2 * p;
@@ -83,10 +82,10 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
         // double-buffered transpose: one barrier per target
         uint32_t* l = lds[t & 1];
 #pragma unroll
-        for (int e = 0; e < E; ++e) l[(tau + G::TR * e) * LS + col] = x[e];
+        for (int e = 0; e < E; ++e) l[tau * G::WT + col + e * G::WS] = x[e];
         __syncthreads();
 #pragma unroll
-        for (int e = 0; e < E; ++e) x[e] = l[(E * tau + e) * LS + col];
+        for (int e = 0; e < E; ++e) x[e] = l[tau * G::RT + col + e * G::RS];
         phase_b<true, H, G::TR>(x, tau, w, ws, p, p2, base);
 #pragma unroll
         for (int e = 0; e < E; ++e) bc.st(x[e], vo, (uint32_t)((t << LOGN) + e * G::C) * 4);  // lazy words

@@ -50,12 +50,11 @@ __global__ void __launch_bounds__(WG) fwd_cols(NttArgs A, int row0) {
     // stages h = R/2 .. TR (rows): index R/(2h) + r/(2h)
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
     phase_a<true, H, G::TR, decltype(base), true>(x, w, ws, p, p2, base);
-    constexpr int LS = G::CC + G::CPAD;
 #pragma unroll
-    for (int j = 0; j < E; ++j) lds[(tau + G::TR * j) * LS + col] = x[j];
+    for (int j = 0; j < E; ++j) lds[tau * G::WT + col + j * G::WS] = x[j];
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < E; ++j) x[j] = lds[(E * tau + j) * LS + col];
+    for (int j = 0; j < E; ++j) x[j] = lds[tau * G::RT + col + j * G::RS];
     phase_b<true, H, G::TR>(x, tau, w, ws, p, p2, base);
     uint32_t* out = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
 #pragma unroll
@@ -165,12 +164,11 @@ __global__ void __launch_bounds__(WG) inv_cols(NttArgs A, int row0) {
     for (int j = 0; j < E; ++j) x[j] = a[(size_t)(E * tau + j) * G::C + c];
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
     phase_b<false, H, G::TR>(x, tau, w, ws, p, p2, base);
-    constexpr int LS = G::CC + G::CPAD;
 #pragma unroll
-    for (int j = 0; j < E; ++j) lds[(E * tau + j) * LS + col] = x[j];
+    for (int j = 0; j < E; ++j) lds[tau * G::RT + col + j * G::RS] = x[j];
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < E; ++j) x[j] = lds[(tau + G::TR * j) * LS + col];
+    for (int j = 0; j < E; ++j) x[j] = lds[tau * G::WT + col + j * G::WS];
     phase_a<false, H, G::TR, decltype(base), true>(x, w, ws, p, p2, base);
     // the scale: es[i] per row (NttArgs ABI 17) or N^-1 of the prime; Shoup takes the lazy words whole
     uint32_t s, ss;

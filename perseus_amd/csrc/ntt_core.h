@@ -19,8 +19,15 @@ struct Geo {
     static constexpr int BB = WG / TC;             // blocks per row-pass workgroup
     static constexpr int COL_WGS = C / CC;         // column-pass workgroups per row
     static constexpr int ROW_WGS = R / BB;         // row-pass workgroups per row
-    static constexpr int CPAD = CC == 16 ? 1 : 0;  // LDS row padding of the column pass
-    static constexpr int COL_LDS = R * (CC + CPAD);
+    // The column pass's transpose writes rows tau + TR j and reads rows E tau + j of a CC-wide tile. At CC = 16 one
+    // padding row after every 16 rows puts the four rows a wave touches at once in four distinct 16-bank blocks on
+    // both sides (a single padding word per row cannot serve both: the writes want an even row stride, the reads an
+    // odd one); at CC >= 32 a wave touches at most two rows of 32 or more words, which unpadded rows serve.
+    // Word j of thread (tau, col) is written at tau WT + col + j WS (row tau + TR j) and read at tau RT + col + j RS
+    // (row E tau + j): with the padding row, row r sits at (r + r / 16) 16.
+    static constexpr int COL_LDS = CC == 16 ? (R + R / 16) * 16 : R * CC;
+    static constexpr int WT = CC == 16 ? 16 : CC, WS = CC == 16 ? 17 * 16 : TR * CC;
+    static constexpr int RT = CC == 16 ? 17 * 16 : E * CC, RS = CC;
     static constexpr int ROW_LDS = BB * (C + C / E);
     static_assert(TR >= 2 && TC >= 2 && TR <= E && TC <= E, "sub-transforms of 32 to 256 points");
 };

@@ -31,7 +31,7 @@ extern "C" {
 typedef void* pc_stream_t; /* a hipStream_t */
 
 /* ------------------------------------------------------------------------------------------ ABI-30 structs */
-/* args.cuh:38-49 */
+/* args.cuh:21-49 */
 typedef struct PrimeConst {
     uint64_t p;
     uint64_t mu_lo;
@@ -45,20 +45,20 @@ typedef struct PrimeConst {
 } PrimeConst;
 PC_STATIC_ASSERT(sizeof(PrimeConst) == 64, "PrimeConst layout");
 
-/* args.cuh:54-57 */
+/* args.cuh:52-57 */
 typedef struct RowSet {
     int32_t nq, np, qmax, pad;
 } RowSet;
 PC_STATIC_ASSERT(sizeof(RowSet) == 16, "RowSet layout");
 
-/* args.cuh:60-64 */
+/* args.cuh:59-64 */
 typedef struct PolyRef {
     void* base;
     uint64_t ct_stride, part_stride;
 } PolyRef;
 PC_STATIC_ASSERT(sizeof(PolyRef) == 24, "PolyRef layout");
 
-/* args.cuh:66-107: in-place negacyclic NTT of nrows rows (row i at base + roff[i]*N, prime id rprime[i]), OpenFHE
+/* args.cuh:67-107: in-place negacyclic NTT of nrows rows (row i at base + roff[i]*N, prime id rprime[i]), OpenFHE
  * order; soff: out-of-place first pass summing snum source rows; epi 1/2/3: forward epilogues; es/ess: the inverse's
  * per-row scale */
 typedef struct NttArgs {
@@ -87,7 +87,7 @@ typedef struct NttArgs {
 } NttArgs;
 PC_STATIC_ASSERT(sizeof(NttArgs) == 176, "NttArgs layout");
 
-/* args.cuh:120-141: one fast base-conversion job; pool at pool_off: src_row[ns], src_prime[ns], pre[ns],
+/* args.cuh:110-128: one fast base-conversion job; pool at pool_off: src_row[ns], src_prime[ns], pre[ns],
  * tgt_row[nt], tgt_prime[nt], M[ns][nt] (u32 words) */
 typedef struct BconvJob {
     uint32_t src_off, dst_off;
@@ -110,7 +110,7 @@ typedef struct BconvArgs {
 } BconvArgs;
 PC_STATIC_ASSERT(sizeof(BconvArgs) == 56, "BconvArgs layout");
 
-/* args.cuh:149-160: element-wise row-set kernels */
+/* args.cuh:144-157: element-wise row-set kernels */
 typedef struct EwArgs {
     PolyRef out, a, b;
     RowSet rs;
@@ -121,7 +121,7 @@ typedef struct EwArgs {
 } EwArgs;
 PC_STATIC_ASSERT(sizeof(EwArgs) == 128, "EwArgs layout");
 
-/* args.cuh:203-228: hybrid key-switch inner product */
+/* args.cuh:211-228: hybrid key-switch inner product */
 #define PC_KS_ACC 4
 #define PC_KS_SUM 8
 typedef struct KsArgs {
@@ -143,7 +143,7 @@ typedef struct KsArgs {
 } KsArgs;
 PC_STATIC_ASSERT(sizeof(KsArgs) == 176, "KsArgs layout");
 
-/* args.cuh:267-281 */
+/* args.cuh:263-277 */
 typedef struct EpiArgs {
     void* dst;
     const void* conv;
@@ -157,7 +157,7 @@ typedef struct EpiArgs {
 } EpiArgs;
 PC_STATIC_ASSERT(sizeof(EpiArgs) == 72, "EpiArgs layout");
 
-/* args.cuh:284-294: switching keys read in their stored form, `a` regenerated from each key's KSKA seed */
+/* args.cuh:279-290: switching keys read in their stored form, `a` regenerated from each key's KSKA seed */
 typedef struct KeyTab {
     const void* const* kb;
     const uint32_t* const* seed;
@@ -169,7 +169,7 @@ typedef struct KeyTab {
 } KeyTab;
 PC_STATIC_ASSERT(sizeof(KeyTab) == 40, "KeyTab layout");
 
-/* args.cuh:299-307 */
+/* args.cuh:292-304 */
 typedef struct KsRegenArgs {
     KsArgs ks;
     const uint32_t* seed;
@@ -180,7 +180,7 @@ typedef struct KsRegenArgs {
 } KsRegenArgs;
 PC_STATIC_ASSERT(sizeof(KsRegenArgs) == 312, "KsRegenArgs layout");
 
-/* args.cuh:317-325: KSKA rows out[d - d0][m][N] */
+/* args.cuh:306-323: KSKA rows out[d - d0][m][N] */
 typedef struct KskExpandArgs {
     void* out;
     const uint32_t* seed;
@@ -191,7 +191,7 @@ typedef struct KskExpandArgs {
 } KskExpandArgs;
 PC_STATIC_ASSERT(sizeof(KskExpandArgs) == 48, "KskExpandArgs layout");
 
-/* args.cuh:754-768: sigma_k gather in the bit-reversed evaluation order */
+/* args.cuh:582-592: sigma_k gather in the bit-reversed evaluation order */
 typedef struct AutomorphArgs {
     PolyRef out, in, add;
     RowSet rs;
@@ -201,7 +201,7 @@ typedef struct AutomorphArgs {
 } AutomorphArgs;
 PC_STATIC_ASSERT(sizeof(AutomorphArgs) == 112, "AutomorphArgs layout");
 
-/* args.cuh:790-807: secret-key encryption, a from the "ENCA" expander lane */
+/* args.cuh:614-628: secret-key encryption, a from the "ENCA" expander lane */
 typedef struct EncryptArgs {
     void* c0;
     void* c1;
@@ -215,7 +215,7 @@ typedef struct EncryptArgs {
 } EncryptArgs;
 PC_STATIC_ASSERT(sizeof(EncryptArgs) == 64, "EncryptArgs layout");
 
-/* args.cuh:817-833: one hybrid switching key (OpenFHE KeySwitchGenInternal relation), dense or bit-packed b */
+/* args.cuh:631-654: one hybrid switching key (OpenFHE KeySwitchGenInternal relation), dense or bit-packed b */
 typedef struct KskGenArgs {
     void* b;
     void* a;
@@ -233,7 +233,7 @@ typedef struct KskGenArgs {
 } KskGenArgs;
 PC_STATIC_ASSERT(sizeof(KskGenArgs) == 120, "KskGenArgs layout");
 
-/* args.cuh:836-842 */
+/* args.cuh:656-663 */
 typedef struct KskUnpackArgs {
     void* out;
     const uint32_t* in;
@@ -242,7 +242,7 @@ typedef struct KskUnpackArgs {
 } KskUnpackArgs;
 PC_STATIC_ASSERT(sizeof(KskUnpackArgs) == 32, "KskUnpackArgs layout");
 
-/* args.cuh:997-1003 */
+/* args.cuh:760-768 */
 typedef struct KsKeyArgs {
     KsArgs ks;
     KeyTab key;
@@ -284,7 +284,7 @@ typedef struct CtsArgs {
 } CtsArgs;
 PC_STATIC_ASSERT(sizeof(CtsArgs) == 200, "CtsArgs layout");
 
-/* args.cuh:752-757: cts_fused with the baby keys through a KeyTab: `b` read in its stored form (dense or packed),
+/* args.cuh:753-758: cts_fused with the baby keys through a KeyTab: `b` read in its stored form (dense or packed),
  * `a` regenerated for digits < key.nregen, else read from cts.ka */
 typedef struct CtsRegenArgs {
     CtsArgs cts;
@@ -292,15 +292,201 @@ typedef struct CtsRegenArgs {
 } CtsRegenArgs;
 PC_STATIC_ASSERT(sizeof(CtsRegenArgs) == 240, "CtsRegenArgs layout");
 
+/* ---- EvalMod / plaintext-product element-wise kernels (em.cuh). Q rows [0, n) of K ciphertexts, row index = prime
+ * id; grid (N/1024, n, K or 2K); every output word a canonical residue. */
+
+/* args.cuh:356-367: (c0, c1, d2) (= | +=) sum_{j < min(npairs, 2)} (a_j0 b_j0, a_j0 b_j1 + a_j1 b_j0, a_j1 b_j1); d2
+ * written to part 1 of `d2` (and to coef + c coef_ct_stride + row N when coef is set); acc: (c0, c1) += the old
+ * words, acc_d2: d2 += its old words; dbl: all three doubled after the adds */
+typedef struct TensorArgs {
+    PolyRef out, d2, a0, b0, a1, b1;
+    void* coef;
+    uint64_t coef_ct_stride;
+    const PrimeConst* pr;
+    int32_t npairs, acc, n, K;
+    int32_t dbl, acc_d2;
+} TensorArgs;
+PC_STATIC_ASSERT(sizeof(TensorArgs) == 192, "TensorArgs layout");
+
+/* args.cuh:369-378: tensor, then (c0, c1) +-= y c[row] (Shoup companion cs) after the doubling; d2 unchanged */
+typedef struct TensorYArgs {
+    TensorArgs t;
+    PolyRef y;
+    const void* c;
+    const void* cs;
+    int32_t sub, pad;
+} TensorYArgs;
+PC_STATIC_ASSERT(sizeof(TensorYArgs) == 240, "TensorYArgs layout");
+
+/* args.cuh:379-389: tensor over up to PC_TSUM_MAX pairs passed by value; acc nonzero: (c0, c1) +=, acc & 2: d2 += */
+#define PC_TSUM_MAX 16
+typedef struct TensorSumArgs {
+    PolyRef out, d2;
+    PolyRef a[PC_TSUM_MAX], b[PC_TSUM_MAX];
+    const PrimeConst* pr;
+    int32_t npairs, acc, n, K;
+} TensorSumArgs;
+PC_STATIC_ASSERT(sizeof(TensorSumArgs) == 2 * 24 + 2 * PC_TSUM_MAX * 24 + 8 + 16, "TensorSumArgs layout");
+
+/* args.cuh:438-447: for parts 0, 1: dst = f (dst + (x - t) binv) [+ k[row] on part 0, reduced once], f = 2 when dbl */
+typedef struct MdEpiArgs {
+    PolyRef dst, x, t;
+    const void* binv;
+    const void* binvs;
+    const void* k;
+    const PrimeConst* pr;
+    int32_t dbl, n, K, pad;
+} MdEpiArgs;
+PC_STATIC_ASSERT(sizeof(MdEpiArgs) == 120, "MdEpiArgs layout");
+
+/* args.cuh:449-456: dst = a +- (x - t) binv, both parts (sub: minus) */
+typedef struct MdEpiToArgs {
+    MdEpiArgs m;
+    PolyRef a;
+    int32_t sub, pad;
+} MdEpiToArgs;
+PC_STATIC_ASSERT(sizeof(MdEpiToArgs) == 152, "MdEpiToArgs layout");
+
+/* args.cuh:458-467: out = sum_{j < nsrc <= 8} w[j rowstride + row] src_j (both parts), Shoup companions ws */
+typedef struct WsumArgs {
+    PolyRef out;
+    PolyRef src[8];
+    const void* w;
+    const void* ws;
+    const PrimeConst* pr;
+    int32_t nsrc, rowstride, n, K;
+} WsumArgs;
+PC_STATIC_ASSERT(sizeof(WsumArgs) == 256, "WsumArgs layout");
+
+/* args.cuh:469-474: wsum, then part 0 += k[row] (reduced once) */
+typedef struct WsumKArgs {
+    WsumArgs w;
+    const void* k;
+} WsumKArgs;
+PC_STATIC_ASSERT(sizeof(WsumKArgs) == 264, "WsumKArgs layout");
+
+/* args.cuh:476-489: nout <= 3 weighted sums of one source list: out[m] = sum_j w[m][j rowstride + row] src_j
+ * [+ k[m][row] on part 0] on rows [0, n[m]); blocks over rows [0, nmax) */
+typedef struct WsumMultiArgs {
+    PolyRef out[3];
+    PolyRef src[8];
+    const void* w[3];
+    const void* ws[3];
+    const void* k[3];
+    const PrimeConst* pr;
+    int32_t nout, nsrc, rowstride, K;
+    int32_t n[3], nmax;
+} WsumMultiArgs;
+PC_STATIC_ASSERT(sizeof(WsumMultiArgs) == 376, "WsumMultiArgs layout");
+
+/* args.cuh:491-498: part 0 += k[row] (reduced once) */
+typedef struct AddConstArgs {
+    PolyRef x;
+    const void* k;
+    const PrimeConst* pr;
+    int32_t n, K;
+} AddConstArgs;
+PC_STATIC_ASSERT(sizeof(AddConstArgs) == 48, "AddConstArgs layout");
+
+/* args.cuh:500-506: out = in t[row][i] (both parts; t one table of rows of N words) */
+typedef struct MulTableArgs {
+    PolyRef out, in;
+    const void* t;
+    const PrimeConst* pr;
+    int32_t n, K;
+} MulTableArgs;
+PC_STATIC_ASSERT(sizeof(MulTableArgs) == 72, "MulTableArgs layout");
+
+/* args.cuh:508-515: out = y + m (sub 0), y - m (1), m - y (2), m = in t as mul_table's; out may alias y or in */
+typedef struct MulAddArgs {
+    MulTableArgs m;
+    PolyRef y;
+    int32_t sub, pad;
+} MulAddArgs;
+PC_STATIC_ASSERT(sizeof(MulAddArgs) == 104, "MulAddArgs layout");
+
+/* args.cuh:517-528: out = y + sum_{j < nterm <= 8} x_j t_j (y.base null: no y), rows [0, n) of K cts, both parts; lazy
+ * only chooses the reference's accumulation (the same canonical words either way) */
+typedef struct MulAddNArgs {
+    PolyRef out, y;
+    PolyRef x[8];
+    const void* t[8];
+    const PrimeConst* pr;
+    int32_t n, K, nterm, lazy;
+} MulAddNArgs;
+PC_STATIC_ASSERT(sizeof(MulAddNArgs) == 328, "MulAddNArgs layout");
+
+/* args.cuh:531-552: the composite one-pass rescale by the top ndrop (1 or 2) primes, a = top, b = top - 1,
+ * lift(y, q) = y - q when y > q/2, reduced mod q_i:
+ *   ndrop 2: y' = qinv_ab y_b + C_ab lift(y_a) mod q_b;  tmp_i = A_i lift(y_a) + B_i lift(y')
+ *   ndrop 1: tmp_i = A_i lift(y_a)
+ * on rows i < nrows, coefficient form; ca (cb): the tops scaled first when ca != 1. qam / qbm: q_a, q_b mod q_i. */
+typedef struct RescaleArgs {
+    PolyRef x, tmp;
+    const void* A;
+    const void* B;
+    const void* As;
+    const void* Bs;
+    const void* qam;
+    const void* qbm;
+    const PrimeConst* pr;
+    uint64_t qinv_ab, C_ab, ca, cb;
+    int32_t top, nrows, K, ndrop;
+} RescaleArgs;
+PC_STATIC_ASSERT(sizeof(RescaleArgs) == 152, "RescaleArgs layout");
+
+/* args.cuh:554-563: rescale_coef (ndrop 2) and the forward NTT of its rows in one pipeline, the correction never
+ * stored: the tops' two sources go to tmp rows top, top - 1, the column pass generates tmp_i from them (the sources
+ * sit top - r and top - 1 - r rows above row r of the same polynomial); ntt's epilogue applies (3: the combine) */
+typedef struct RescaleNttArgs {
+    RescaleArgs rs;
+    NttArgs ntt;
+} RescaleNttArgs;
+PC_STATIC_ASSERT(sizeof(RescaleNttArgs) == 328, "RescaleNttArgs layout");
+
+/* args.cuh:565-572: x_i = alpha_i x_i + tmp_i (NTT domain), both parts */
+typedef struct RescaleCombineArgs {
+    PolyRef x, tmp;
+    const void* alpha;
+    const void* alphas;
+    const PrimeConst* pr;
+    int32_t n, K;
+} RescaleCombineArgs;
+PC_STATIC_ASSERT(sizeof(RescaleCombineArgs) == 80, "RescaleCombineArgs layout");
+
+/* args.cuh:574-579: out_i = alpha_i x_i + tmp_i, x read only */
+typedef struct RescaleCombineToArgs {
+    RescaleCombineArgs a;
+    PolyRef out;
+} RescaleCombineToArgs;
+PC_STATIC_ASSERT(sizeof(RescaleCombineToArgs) == 104, "RescaleCombineToArgs layout");
+
+/* args.cuh:162-170: out[i] = a[i] (+ b[i]) (+ c[i]) for n <= 48 polynomials by pointer (rows [0, nrows), row r at
+ * + r N); a null b / c is skipped */
+#define PC_EWM_MAX 48
+typedef struct EwManyArgs {
+    void* out[PC_EWM_MAX];
+    const void* a[PC_EWM_MAX];
+    const void* b[PC_EWM_MAX];
+    const void* c[PC_EWM_MAX];
+    const PrimeConst* pr;
+    int32_t n, nrows;
+} EwManyArgs;
+PC_STATIC_ASSERT(sizeof(EwManyArgs) == 4 * PC_EWM_MAX * 8 + 16, "EwManyArgs layout");
+
+/* args.cuh:172-182: out[i] = (a[i] - b[i]) t[row] for n <= 48 polynomials by pointer */
+typedef struct SubMulManyArgs {
+    void* out[PC_EWM_MAX];
+    const void* a[PC_EWM_MAX];
+    const void* b[PC_EWM_MAX];
+    const void* t;
+    const PrimeConst* pr;
+    int32_t n, nrows;
+} SubMulManyArgs;
+PC_STATIC_ASSERT(sizeof(SubMulManyArgs) == 3 * PC_EWM_MAX * 8 + 24, "SubMulManyArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct PtDotArgs;
-struct TensorArgs;
-struct MdEpiArgs;
-struct WsumArgs;
-struct AddConstArgs;
-struct MulTableArgs;
-struct RescaleArgs;
-struct RescaleCombineArgs;
 struct EncodeArgs;
 struct ModRaiseArgs;
 struct SmallIntArgs;
@@ -309,26 +495,15 @@ struct SpruFftArgs;
 struct SpruScatterArgs;
 struct PcmmArgs;
 struct CcmmArgs;
-struct WsumKArgs;
-struct RescaleCombineToArgs;
-struct MdEpiToArgs;
 struct SmallInt1Args;
 struct CoeffArgs;
-struct MulAddArgs;
-struct RescaleNttArgs;
-struct MulAddNArgs;
-struct TensorYArgs;
-struct WsumMultiArgs;
 struct TfheArgs;
-struct TensorSumArgs;
 struct TensorMultiArgs;
 struct TensorSeededArgs;
-struct EwManyArgs;
-struct SubMulManyArgs;
 struct PackSplitArgs;
 struct PackDotArgs;
 
-/* args.cuh:1037-1097 */
+/* args.cuh:1035-1097 */
 typedef struct KernelTable {
     uint32_t abi;
     uint32_t word_bytes;

@@ -1,4 +1,4 @@
-"""ctypes mirrors of the ABI-30 argument structs a Python caller fills to call the kernel table's CtS entries directly
+"""ctypes mirrors of the ABI-30 argument structs a Python caller fills to call the kernel table's entries directly
 (include/pc_hip.h; the reference's crates/pc-kernels/src/args.rs mirrors the same C structs field for field), and the
 table's entries by name in args.cuh's order (args.cuh:1037-1097)."""
 import ctypes as C
@@ -19,7 +19,7 @@ assert len(ENTRIES) == 52
 
 
 class KeyTab(C.Structure):
-    """args.cuh:284-294: a key set read in its stored form (40 bytes)."""
+    """args.cuh:279-290: a key set read in its stored form (40 bytes)."""
     _fields_ = [("kb", vp), ("seed", vp), ("row_words", u64), ("bits", i32), ("q_top", i32), ("srows", i32),
                 ("nregen", i32)]
 
@@ -35,7 +35,7 @@ class CtsArgs(C.Structure):
 
 
 class CtsRegenArgs(C.Structure):
-    """args.cuh:752-757: cts_fused with the baby keys through a KeyTab (240 bytes)."""
+    """args.cuh:748-758: cts_fused with the baby keys through a KeyTab (240 bytes)."""
     _fields_ = [("cts", CtsArgs), ("key", KeyTab)]
 
 
@@ -49,27 +49,155 @@ class KsArgs(C.Structure):
 
 
 class KsKeyArgs(C.Structure):
-    """args.cuh:997-1003: ks_dot with the keys through a KeyTab (216 bytes)."""
+    """args.cuh:760-768: ks_dot with the keys through a KeyTab (216 bytes)."""
     _fields_ = [("ks", KsArgs), ("key", KeyTab)]
 
 
 class EpiArgs(C.Structure):
-    """args.cuh:268-281: the fused relinearisation epilogue (72 bytes)."""
+    """args.cuh:263-277: the fused relinearisation epilogue (72 bytes)."""
     _fields_ = [("dst", vp), ("conv", vp), ("binv", vp), ("binvs", vp), ("k", vp), ("part_stride", u64),
                 ("dbl", i32), ("pad", i32), ("alpha", vp), ("alphas", vp)]
 
 
 class KsRegenArgs(C.Structure):
-    """args.cuh:299-307: the relinearisation dot with a regenerated key (312 bytes)."""
+    """args.cuh:292-304: the relinearisation dot with a regenerated key (312 bytes)."""
     _fields_ = [("ks", KsArgs), ("seed", vp), ("epi", EpiArgs), ("use_epi", i32), ("pad", i32), ("key", KeyTab),
                 ("add", vp)]
 
 
-KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:208-210)
+class PolyRef(C.Structure):
+    """args.cuh:59-64: a ciphertext buffer: ct c part k row r at base + c ct_stride + k part_stride + r N words."""
+    _fields_ = [("base", vp), ("ct_stride", u64), ("part_stride", u64)]
+
+
+class NttArgs(C.Structure):
+    """args.cuh:67-107 (176 bytes)."""
+    _fields_ = [("base", vp), ("roff", vp), ("rprime", vp), ("fw", vp), ("fws", vp), ("iw", vp), ("iws", vp),
+                ("ninv", vp), ("ninvs", vp), ("pr", vp), ("nrows", i32), ("chunk", i32), ("src", vp), ("soff", vp),
+                ("eout", vp), ("ex", vp), ("es", vp), ("ess", vp), ("epi", i32), ("snum", i32), ("sstride", u64),
+                ("xnum", i32), ("lazy", i32), ("xstride", u64), ("ed", vp)]
+
+
+class TensorArgs(C.Structure):
+    """args.cuh:356-367 (192 bytes)."""
+    _fields_ = [("out", PolyRef), ("d2", PolyRef), ("a0", PolyRef), ("b0", PolyRef), ("a1", PolyRef),
+                ("b1", PolyRef), ("coef", vp), ("coef_ct_stride", u64), ("pr", vp), ("npairs", i32), ("acc", i32),
+                ("n", i32), ("K", i32), ("dbl", i32), ("acc_d2", i32)]
+
+
+class TensorYArgs(C.Structure):
+    """args.cuh:369-378 (240 bytes)."""
+    _fields_ = [("t", TensorArgs), ("y", PolyRef), ("c", vp), ("cs", vp), ("sub", i32), ("pad", i32)]
+
+
+TSUM_MAX = 16
+
+
+class TensorSumArgs(C.Structure):
+    """args.cuh:379-389."""
+    _fields_ = [("out", PolyRef), ("d2", PolyRef), ("a", PolyRef * TSUM_MAX), ("b", PolyRef * TSUM_MAX), ("pr", vp),
+                ("npairs", i32), ("acc", i32), ("n", i32), ("K", i32)]
+
+
+class MdEpiArgs(C.Structure):
+    """args.cuh:438-447 (120 bytes)."""
+    _fields_ = [("dst", PolyRef), ("x", PolyRef), ("t", PolyRef), ("binv", vp), ("binvs", vp), ("k", vp),
+                ("pr", vp), ("dbl", i32), ("n", i32), ("K", i32), ("pad", i32)]
+
+
+class MdEpiToArgs(C.Structure):
+    """args.cuh:449-456 (152 bytes)."""
+    _fields_ = [("m", MdEpiArgs), ("a", PolyRef), ("sub", i32), ("pad", i32)]
+
+
+class WsumArgs(C.Structure):
+    """args.cuh:458-467 (256 bytes)."""
+    _fields_ = [("out", PolyRef), ("src", PolyRef * 8), ("w", vp), ("ws", vp), ("pr", vp), ("nsrc", i32),
+                ("rowstride", i32), ("n", i32), ("K", i32)]
+
+
+class WsumKArgs(C.Structure):
+    """args.cuh:469-474 (264 bytes)."""
+    _fields_ = [("w", WsumArgs), ("k", vp)]
+
+
+class WsumMultiArgs(C.Structure):
+    """args.cuh:476-489 (376 bytes)."""
+    _fields_ = [("out", PolyRef * 3), ("src", PolyRef * 8), ("w", vp * 3), ("ws", vp * 3), ("k", vp * 3), ("pr", vp),
+                ("nout", i32), ("nsrc", i32), ("rowstride", i32), ("K", i32), ("n", i32 * 3), ("nmax", i32)]
+
+
+class AddConstArgs(C.Structure):
+    """args.cuh:491-498 (48 bytes)."""
+    _fields_ = [("x", PolyRef), ("k", vp), ("pr", vp), ("n", i32), ("K", i32)]
+
+
+class MulTableArgs(C.Structure):
+    """args.cuh:500-506 (72 bytes)."""
+    _fields_ = [("out", PolyRef), ("in_", PolyRef), ("t", vp), ("pr", vp), ("n", i32), ("K", i32)]
+
+
+class MulAddArgs(C.Structure):
+    """args.cuh:508-515 (104 bytes)."""
+    _fields_ = [("m", MulTableArgs), ("y", PolyRef), ("sub", i32), ("pad", i32)]
+
+
+class MulAddNArgs(C.Structure):
+    """args.cuh:517-528 (328 bytes)."""
+    _fields_ = [("out", PolyRef), ("y", PolyRef), ("x", PolyRef * 8), ("t", vp * 8), ("pr", vp), ("n", i32),
+                ("K", i32), ("nterm", i32), ("lazy", i32)]
+
+
+class RescaleArgs(C.Structure):
+    """args.cuh:531-552 (152 bytes)."""
+    _fields_ = [("x", PolyRef), ("tmp", PolyRef), ("A", vp), ("B", vp), ("As", vp), ("Bs", vp), ("qam", vp),
+                ("qbm", vp), ("pr", vp), ("qinv_ab", u64), ("C_ab", u64), ("ca", u64), ("cb", u64), ("top", i32),
+                ("nrows", i32), ("K", i32), ("ndrop", i32)]
+
+
+class RescaleNttArgs(C.Structure):
+    """args.cuh:554-563 (328 bytes)."""
+    _fields_ = [("rs", RescaleArgs), ("ntt", NttArgs)]
+
+
+class RescaleCombineArgs(C.Structure):
+    """args.cuh:565-572 (80 bytes)."""
+    _fields_ = [("x", PolyRef), ("tmp", PolyRef), ("alpha", vp), ("alphas", vp), ("pr", vp), ("n", i32), ("K", i32)]
+
+
+class RescaleCombineToArgs(C.Structure):
+    """args.cuh:574-579 (104 bytes)."""
+    _fields_ = [("a", RescaleCombineArgs), ("out", PolyRef)]
+
+
+EWM_MAX = 48
+
+
+class EwManyArgs(C.Structure):
+    """args.cuh:162-170."""
+    _fields_ = [("out", vp * EWM_MAX), ("a", vp * EWM_MAX), ("b", vp * EWM_MAX), ("c", vp * EWM_MAX), ("pr", vp),
+                ("n", i32), ("nrows", i32)]
+
+
+class SubMulManyArgs(C.Structure):
+    """args.cuh:172-182."""
+    _fields_ = [("out", vp * EWM_MAX), ("a", vp * EWM_MAX), ("b", vp * EWM_MAX), ("t", vp), ("pr", vp), ("n", i32),
+                ("nrows", i32)]
+
+
+KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:207-210)
 
 assert C.sizeof(KeyTab) == 40 and C.sizeof(CtsArgs) == 200 and C.sizeof(CtsRegenArgs) == 240
 assert C.sizeof(KsArgs) == 176 and C.sizeof(KsKeyArgs) == 216 and C.sizeof(EpiArgs) == 72
 assert C.sizeof(KsRegenArgs) == 312
+assert C.sizeof(PolyRef) == 24 and C.sizeof(NttArgs) == 176 and C.sizeof(TensorArgs) == 192
+assert C.sizeof(TensorYArgs) == 240 and C.sizeof(TensorSumArgs) == 2 * 24 + 2 * TSUM_MAX * 24 + 8 + 16
+assert C.sizeof(MdEpiArgs) == 120 and C.sizeof(MdEpiToArgs) == 152 and C.sizeof(WsumArgs) == 256
+assert C.sizeof(WsumKArgs) == 264 and C.sizeof(WsumMultiArgs) == 376 and C.sizeof(AddConstArgs) == 48
+assert C.sizeof(MulTableArgs) == 72 and C.sizeof(MulAddArgs) == 104 and C.sizeof(MulAddNArgs) == 328
+assert C.sizeof(RescaleArgs) == 152 and C.sizeof(RescaleNttArgs) == 328 and C.sizeof(RescaleCombineArgs) == 80
+assert C.sizeof(RescaleCombineToArgs) == 104 and C.sizeof(EwManyArgs) == 4 * EWM_MAX * 8 + 16
+assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
 
 _LAUNCHER = C.CFUNCTYPE(C.c_int, vp, vp)
 

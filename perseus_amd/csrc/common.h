@@ -28,6 +28,12 @@ __device__ __forceinline__ uint32_t shoup(uint32_t a, uint32_t w, uint32_t ws, u
     return r >= p ? r - p : r;
 }
 
+// u mod p for any u < 2^32 with m = floor(2^32 / p): the quotient estimate is low by at most 1
+__device__ __forceinline__ uint32_t red32(uint32_t u, uint32_t p, uint32_t m) {
+    const uint32_t b = u - __umulhi(u, m) * p;
+    return b >= p ? b - p : b;
+}
+
 // Reduction of any 64-bit x mod p (p < 2^31) from 32-bit products: x = hi 2^32 + lo, hi (2^32 mod p) as a Shoup
 // product by the constant r32 = 2^32 mod p (companion r32s), lo mod p by m = floor(2^32 / p); each part below 2p
 // before its guard. PrimeConst.split holds (r32, r32s), the high word of mu_lo is m (args.cuh:38-49).
@@ -83,7 +89,7 @@ __device__ __forceinline__ void wave_sync() {
 
 // ------------------------------------------------------------------------------------------------ ChaCha12
 constexpr uint32_t TAG_KSKA = 0x4b534b41u;  // "KSKA" (crates/pc-core/src/keys.rs:460)
-constexpr uint32_t TAG_ENCA = 0x454e4341u;  // "ENCA" (args.cuh:790)
+constexpr uint32_t TAG_ENCA = 0x454e4341u;  // "ENCA" (args.cuh:615)
 constexpr int KSK_T_MAX = 16;
 
 __device__ __forceinline__ uint32_t rotl(uint32_t x, int r) { return __builtin_rotateleft32(x, r); }

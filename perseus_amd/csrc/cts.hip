@@ -2,11 +2,11 @@
 // group, and the relinearisation dot with a regenerated key.
 //   cts_fused / cts_fused_regen: hoisted baby-step rotations of a ModUp'd ciphertext times the BSGS plaintext
 //     diagonals, summed per giant step in Q u P, the rotations never stored (crates/pc-kernels/kernels/cts.cuh;
-//     args.cuh CtsArgs :325-355, CtsRegenArgs :752-757; host twin crates/pc-host/src/cts.rs);
+//     args.cuh CtsArgs :325-355, CtsRegenArgs :748-758; host twin crates/pc-host/src/cts.rs);
 //   ks_dot_key with KS_SUM: the R rotations of a key group summed into one output (ks.cuh ks_dot_seg /
 //     ks_dot_key_sum; host twin crates/pc-host/src/ks.rs:226-265);
 //   ks_dot_regen: one key, `a` regenerated from the args' seed, no automorphism, optionally through the fused ModDown
-//     epilogue (ks.cuh:129-212; args.cuh KsRegenArgs :299-307, EpiArgs; host twin crates/pc-host/src/ks.rs:267-340).
+//     epilogue (ks.cuh:129-212; args.cuh KsRegenArgs :292-304, EpiArgs; host twin crates/pc-host/src/ks.rs:267-340).
 //
 // One wave per workgroup owns an aligned 512-slot chunk of output slots of one row t and one ciphertext, 8 slots per
 // lane, and keeps its sums in registers across all keys (for the CtS stage: up to four giant steps, both parts), so a

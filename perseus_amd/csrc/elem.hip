@@ -1,5 +1,5 @@
 // Element-wise kernels over polynomial row sets and the eval-form automorphism (crates/pc-kernels/kernels/args.cuh
-// EwArgs :143-160, AutomorphArgs :754-768; host twin crates/pc-host/src/elem.rs). Grid (N / 1024, rows of the row set,
+// EwArgs :143-160, AutomorphArgs :582-592; host twin crates/pc-host/src/elem.rs). Grid (N / 1024, rows of the row set,
 // K x nparts), 256 threads of 4 consecutive words (16-byte accesses; rows are N-word aligned).
 #include "common.h"
 

@@ -1,0 +1,502 @@
+// EvalMod and plaintext-product element-wise kernels: the tensor product of two ciphertexts, the ModDown / rescale
+// epilogues, weighted sums, constants, plaintext-table products and their fused add / sub chains, and the
+// pointer-list sums (semantics: crates/pc-kernels/kernels/args.cuh TensorArgs .. SubMulManyArgs :162-579; kernels
+// em.cuh:12-575, rescale.cuh:63-77; host twin crates/pc-host/src/elem.rs:109-636).
+//
+// Q rows [0, n) of K ciphertexts, row index = prime id. Every kernel streams rows once: grid (N / 1024, rows, K or
+// K x 2 parts), 256 threads, each owning 4 consecutive words of a row (16-byte accesses; rows are N-word aligned). The
+// sums of products are accumulated exactly (a 64-bit sum and its carry count, reduced once), so every output is the
+// canonical residue of the stated formula whatever the number of terms; the reference's lazy 64-bit sums give the same
+// words inside the bounds its callers keep (2 npairs (p - 1)^2 < 2^64, nterm p^2 < 2^64).
+#include "common.h"
+
+namespace pch {
+namespace em {
+
+constexpr int BX = 256;
+
+struct W4 {
+    uint32_t v[4];
+};
+__device__ __forceinline__ W4 ld4(const uint32_t* p) {
+    const uint4 t = *(const uint4*)p;
+    return W4{{t.x, t.y, t.z, t.w}};
+}
+__device__ __forceinline__ void st4(uint32_t* p, const W4& w) { *(uint4*)p = make_uint4(w.v[0], w.v[1], w.v[2], w.v[3]); }
+__device__ __forceinline__ uint32_t* at(const PolyRef& r, int c, int part, int row, int logn) {
+    return (uint32_t*)r.base + c * r.ct_stride + part * r.part_stride + ((size_t)row << logn);
+}
+__device__ __forceinline__ uint32_t lane_word() { return (blockIdx.x * BX + threadIdx.x) * 4; }
+__device__ __forceinline__ uint32_t red_once(uint32_t k, uint32_t p) { return k >= p ? k - p : k; }
+
+// An exact sum of 64-bit products: lo + hi 2^64
+struct Acc {
+    uint64_t lo = 0;
+    uint32_t hi = 0;
+    __device__ __forceinline__ void add(uint64_t v) {
+        lo += v;
+        hi += lo < v;
+    }
+    __device__ __forceinline__ uint32_t red(const Red& r) const { return r.red96(lo, hi); }
+};
+
+// ------------------------------------------------------------------------------------------------ tensor
+// (c0, c1, d2) = sum_j (a_j0 b_j0, a_j0 b_j1 + a_j1 b_j0, a_j1 b_j1) over the pairs (the operands of pair j: A[j], B[j])
+struct Tacc {
+    Acc s0[4], s1[4], s2[4];
+    __device__ __forceinline__ void mac(const W4& x0, const W4& x1, const W4& y0, const W4& y1) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            s0[w].add((uint64_t)x0.v[w] * y0.v[w]);
+            s1[w].add((uint64_t)x0.v[w] * y1.v[w]);
+            s1[w].add((uint64_t)x1.v[w] * y0.v[w]);
+            s2[w].add((uint64_t)x1.v[w] * y1.v[w]);
+        }
+    }
+};
+
+// The tail shared by tensor, tensor_y and tensor_sum: reduce, += the old words (acc; d2 with acc2), double (dbl),
+// +- y c (tensor_y), store; every input word is read before the first store, so outputs may alias inputs.
+__device__ __forceinline__ void tensor_tail(const Tacc& s, const Red& red, uint32_t* o0, uint32_t* o1, uint32_t* o2,
+                                            bool acc, bool acc2, bool dbl, const uint32_t* y0p, const uint32_t* y1p,
+                                            uint32_t yc, uint32_t ycs, bool ysub, uint32_t* coef) {
+    const uint32_t p = red.p;
+    W4 r0, r1, r2;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        r0.v[w] = s.s0[w].red(red);
+        r1.v[w] = s.s1[w].red(red);
+        r2.v[w] = s.s2[w].red(red);
+    }
+    if (acc) {
+        const W4 d0 = ld4(o0), d1 = ld4(o1);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            r0.v[w] = addm(r0.v[w], d0.v[w], p);
+            r1.v[w] = addm(r1.v[w], d1.v[w], p);
+        }
+    }
+    if (acc2) {
+        const W4 d2 = ld4(o2);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) r2.v[w] = addm(r2.v[w], d2.v[w], p);
+    }
+    if (dbl) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            r0.v[w] = addm(r0.v[w], r0.v[w], p);
+            r1.v[w] = addm(r1.v[w], r1.v[w], p);
+            r2.v[w] = addm(r2.v[w], r2.v[w], p);
+        }
+    }
+    if (y0p) {
+        const W4 y0 = ld4(y0p), y1 = ld4(y1p);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t m0 = shoup(y0.v[w], yc, ycs, p), m1 = shoup(y1.v[w], yc, ycs, p);
+            r0.v[w] = ysub ? subm(r0.v[w], m0, p) : addm(r0.v[w], m0, p);
+            r1.v[w] = ysub ? subm(r1.v[w], m1, p) : addm(r1.v[w], m1, p);
+        }
+    }
+    st4(o0, r0);
+    st4(o1, r1);
+    st4(o2, r2);
+    if (coef) st4(coef, r2);
+}
+
+template <bool Y>
+__global__ void __launch_bounds__(BX) tensor_k(TensorArgs A, TensorYArgs B, int logn) {
+    const int row = blockIdx.y, c = blockIdx.z;
+    const uint32_t i = lane_word();
+    const Red red(A.pr[row]);
+    Tacc s;
+    const int np = A.npairs < 2 ? A.npairs : 2;
+    for (int j = 0; j < np; ++j) {
+        const PolyRef& a = j ? A.a1 : A.a0;
+        const PolyRef& b = j ? A.b1 : A.b0;
+        s.mac(ld4(at(a, c, 0, row, logn) + i), ld4(at(a, c, 1, row, logn) + i), ld4(at(b, c, 0, row, logn) + i),
+              ld4(at(b, c, 1, row, logn) + i));
+    }
+    uint32_t* coef = A.coef ? (uint32_t*)A.coef + c * A.coef_ct_stride + ((size_t)row << logn) + i : nullptr;
+    tensor_tail(s, red, at(A.out, c, 0, row, logn) + i, at(A.out, c, 1, row, logn) + i, at(A.d2, c, 1, row, logn) + i,
+                A.acc != 0, A.acc_d2 != 0, A.dbl != 0, Y ? at(B.y, c, 0, row, logn) + i : nullptr,
+                Y ? at(B.y, c, 1, row, logn) + i : nullptr, Y ? ((const uint32_t*)B.c)[row] : 0u,
+                Y ? ((const uint32_t*)B.cs)[row] : 0u, Y && B.sub != 0, coef);
+}
+
+__global__ void __launch_bounds__(BX) tensor_sum_k(TensorSumArgs A, int logn) {
+    const int row = blockIdx.y, c = blockIdx.z;
+    const uint32_t i = lane_word();
+    const Red red(A.pr[row]);
+    Tacc s;
+    for (int j = 0; j < A.npairs; ++j)
+        s.mac(ld4(at(A.a[j], c, 0, row, logn) + i), ld4(at(A.a[j], c, 1, row, logn) + i),
+              ld4(at(A.b[j], c, 0, row, logn) + i), ld4(at(A.b[j], c, 1, row, logn) + i));
+    tensor_tail(s, red, at(A.out, c, 0, row, logn) + i, at(A.out, c, 1, row, logn) + i, at(A.d2, c, 1, row, logn) + i,
+                A.acc != 0, (A.acc & 2) != 0, false, nullptr, nullptr, 0u, 0u, false, nullptr);
+}
+
+// ------------------------------------------------------------------------------------------------ epilogues
+// dst = f (dst + (x - t) binv) [+ k], or (TO) dst = a +- (x - t) binv
+template <bool TO>
+__global__ void __launch_bounds__(BX) md_epi_k(MdEpiToArgs B, int logn) {
+    const MdEpiArgs& A = B.m;
+    const int row = blockIdx.y, c = blockIdx.z >> 1, part = blockIdx.z & 1;
+    const uint32_t i = lane_word();
+    const uint32_t p = (uint32_t)A.pr[row].p;
+    const uint32_t bi = ((const uint32_t*)A.binv)[row], bis = ((const uint32_t*)A.binvs)[row];
+    uint32_t* d = at(A.dst, c, part, row, logn) + i;
+    const W4 x = ld4(at(A.x, c, part, row, logn) + i), t = ld4(at(A.t, c, part, row, logn) + i);
+    const W4 base = ld4(TO ? at(B.a, c, part, row, logn) + i : d);
+    const bool addk = !TO && A.k && part == 0;
+    const uint32_t kk = addk ? red_once(((const uint32_t*)A.k)[row], p) : 0u;
+    W4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t v = shoup(subm(x.v[w], t.v[w], p), bi, bis, p);
+        if (TO) {
+            r.v[w] = B.sub ? subm(base.v[w], v, p) : addm(base.v[w], v, p);
+        } else {
+            uint32_t u = addm(base.v[w], v, p);
+            if (A.dbl) u = addm(u, u, p);
+            r.v[w] = addk ? addm(u, kk, p) : u;
+        }
+    }
+    st4(d, r);
+}
+
+// ------------------------------------------------------------------------------------------------ weighted sums
+// out[m] = sum_j w[m][j rowstride + row] src_j [+ k[m][row] on part 0] for the outputs m whose row range holds row
+__global__ void __launch_bounds__(BX) wsum_k(WsumMultiArgs A, int logn) {
+    const int row = blockIdx.y, c = blockIdx.z;
+    const uint32_t i = lane_word();
+    const uint32_t p = (uint32_t)A.pr[row].p;
+    W4 r[3][2] = {};
+    bool on[3];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) on[m] = m < A.nout && row < A.n[m];
+    for (int j = 0; j < A.nsrc; ++j) {
+        const W4 x0 = ld4(at(A.src[j], c, 0, row, logn) + i), x1 = ld4(at(A.src[j], c, 1, row, logn) + i);
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            if (!on[m]) continue;
+            const uint32_t w = ((const uint32_t*)A.w[m])[j * A.rowstride + row];
+            const uint32_t ws = ((const uint32_t*)A.ws[m])[j * A.rowstride + row];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                r[m][0].v[u] = addm(r[m][0].v[u], shoup(x0.v[u], w, ws, p), p);
+                r[m][1].v[u] = addm(r[m][1].v[u], shoup(x1.v[u], w, ws, p), p);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        if (!on[m]) continue;
+        if (A.k[m]) {
+            const uint32_t kr = red_once(((const uint32_t*)A.k[m])[row], p);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) r[m][0].v[u] = addm(r[m][0].v[u], kr, p);
+        }
+        st4(at(A.out[m], c, 0, row, logn) + i, r[m][0]);
+        st4(at(A.out[m], c, 1, row, logn) + i, r[m][1]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ constants, tables
+__global__ void __launch_bounds__(BX) add_const_k(AddConstArgs A, int logn) {
+    const int row = blockIdx.y, c = blockIdx.z;
+    const uint32_t p = (uint32_t)A.pr[row].p;
+    uint32_t* d = at(A.x, c, 0, row, logn) + lane_word();
+    const uint32_t kr = red_once(((const uint32_t*)A.k)[row], p);
+    W4 x = ld4(d);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) x.v[w] = addm(x.v[w], kr, p);
+    st4(d, x);
+}
+
+// out = y op sum_j x_j t_j (MODE 0: y + s, 1: y - s, 2: s - y; Y: whether y is read); one term is mul_table / mul_add
+template <int MODE, bool Y>
+__global__ void __launch_bounds__(BX) mul_k(MulAddNArgs A, int logn) {
+    const int row = blockIdx.y, part = blockIdx.z & 1, c = blockIdx.z >> 1;
+    const uint32_t i = lane_word();
+    const Red red(A.pr[row]);
+    const uint32_t p = red.p;
+    Acc s[4];
+    for (int j = 0; j < A.nterm; ++j) {
+        const W4 x = ld4(at(A.x[j], c, part, row, logn) + i);
+        const W4 t = ld4((const uint32_t*)A.t[j] + ((size_t)row << logn) + i);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) s[w].add((uint64_t)x.v[w] * t.v[w]);
+    }
+    W4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r.v[w] = s[w].red(red);
+    if (Y) {
+        const W4 y = ld4(at(A.y, c, part, row, logn) + i);
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            r.v[w] = MODE == 0 ? addm(y.v[w], r.v[w], p) : MODE == 1 ? subm(y.v[w], r.v[w], p) : subm(r.v[w], y.v[w], p);
+    }
+    st4(at(A.out, c, part, row, logn) + i, r);
+}
+
+// x_i = alpha_i x_i + tmp_i (rescale_combine), or out_i = alpha_i x_i + tmp_i (rescale_combine_to)
+__global__ void __launch_bounds__(BX) combine_k(RescaleCombineToArgs R, int logn) {
+    const RescaleCombineArgs& A = R.a;
+    const int row = blockIdx.y, c = blockIdx.z >> 1, part = blockIdx.z & 1;
+    const uint32_t i = lane_word();
+    const uint32_t p = (uint32_t)A.pr[row].p;
+    const uint32_t al = ((const uint32_t*)A.alpha)[row], als = ((const uint32_t*)A.alphas)[row];
+    const W4 x = ld4(at(A.x, c, part, row, logn) + i), t = ld4(at(A.tmp, c, part, row, logn) + i);
+    W4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r.v[w] = addm(shoup(x.v[w], al, als, p), t.v[w], p);
+    st4(at(R.out, c, part, row, logn) + i, r);
+}
+
+// ------------------------------------------------------------------------------------------------ pointer lists
+__global__ void __launch_bounds__(BX) ew_many_k(EwManyArgs A, int logn) {
+    const int row = blockIdx.y, j = blockIdx.z;
+    const size_t o = ((size_t)row << logn) + lane_word();
+    const uint32_t p = (uint32_t)A.pr[row].p;
+    W4 r = ld4((const uint32_t*)A.a[j] + o);
+    if (A.b[j]) {
+        const W4 y = ld4((const uint32_t*)A.b[j] + o);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) r.v[w] = addm(r.v[w], y.v[w], p);
+    }
+    if (A.c[j]) {
+        const W4 y = ld4((const uint32_t*)A.c[j] + o);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) r.v[w] = addm(r.v[w], y.v[w], p);
+    }
+    st4((uint32_t*)A.out[j] + o, r);
+}
+
+__global__ void __launch_bounds__(BX) submul_many_k(SubMulManyArgs A, int logn) {
+    const int row = blockIdx.y, j = blockIdx.z;
+    const size_t o = ((size_t)row << logn) + lane_word();
+    const Red red(A.pr[row]);
+    const W4 x = ld4((const uint32_t*)A.a[j] + o), y = ld4((const uint32_t*)A.b[j] + o);
+    const W4 t = ld4((const uint32_t*)A.t + o);
+    W4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r.v[w] = red.mul(subm(x.v[w], y.v[w], red.p), t.v[w]);
+    st4((uint32_t*)A.out[j] + o, r);
+}
+
+// ------------------------------------------------------------------------------------------------ launchers
+// The reference's launchers check only the counts below (em.cuh:580-692); these also refuse null operands that the
+// kernel would read (-1) and return 0 without a launch when there is no work.
+template <int LOGN>
+dim3 grid(int rows, int z) {
+    return dim3((1u << LOGN) / (BX * 4), (unsigned)rows, (unsigned)z);
+}
+#define PCH_LAUNCH(kern, g, ...)                                                   \
+    do {                                                                           \
+        hipLaunchKernelGGL(kern, g, dim3(BX), 0, (hipStream_t)s, __VA_ARGS__);     \
+        return launch_rc();                                                        \
+    } while (0)
+
+inline bool ref_ok(const PolyRef& r) { return r.base != nullptr; }
+
+template <int LOGN>
+int tensor(const TensorArgs* a, pc_stream_t s) {
+    if (!a || !a->pr || !ref_ok(a->out) || !ref_ok(a->d2) || a->n < 0 || a->K < 0) return -1;
+    if (a->npairs >= 1 && (!ref_ok(a->a0) || !ref_ok(a->b0))) return -1;
+    if (a->npairs >= 2 && (!ref_ok(a->a1) || !ref_ok(a->b1))) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(tensor_k<false>, grid<LOGN>(a->n, a->K), *a, TensorYArgs{}, LOGN);
+}
+template <int LOGN>
+int tensor_y(const TensorYArgs* a, pc_stream_t s) {
+    if (!a || !a->c || !a->cs || !ref_ok(a->y)) return -1;
+    const TensorArgs& t = a->t;
+    if (!t.pr || !ref_ok(t.out) || !ref_ok(t.d2) || t.n < 0 || t.K < 0) return -1;
+    if (t.npairs >= 1 && (!ref_ok(t.a0) || !ref_ok(t.b0))) return -1;
+    if (t.npairs >= 2 && (!ref_ok(t.a1) || !ref_ok(t.b1))) return -1;
+    if (t.n == 0 || t.K == 0) return 0;
+    PCH_LAUNCH(tensor_k<true>, grid<LOGN>(t.n, t.K), t, *a, LOGN);
+}
+template <int LOGN>
+int tensor_sum(const TensorSumArgs* a, pc_stream_t s) {
+    if (!a || a->npairs < 1 || a->npairs > PC_TSUM_MAX) return -1;
+    if (!a->pr || !ref_ok(a->out) || !ref_ok(a->d2) || a->n < 0 || a->K < 0) return -1;
+    for (int j = 0; j < a->npairs; ++j)
+        if (!ref_ok(a->a[j]) || !ref_ok(a->b[j])) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(tensor_sum_k, grid<LOGN>(a->n, a->K), *a, LOGN);
+}
+inline bool epi_ok(const MdEpiArgs& m) {
+    return m.pr && m.binv && m.binvs && ref_ok(m.dst) && ref_ok(m.x) && ref_ok(m.t) && m.n >= 0 && m.K >= 0;
+}
+template <int LOGN>
+int md_epilogue(const MdEpiArgs* a, pc_stream_t s) {
+    if (!a || !epi_ok(*a)) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    MdEpiToArgs b{};
+    b.m = *a;
+    PCH_LAUNCH(md_epi_k<false>, grid<LOGN>(a->n, 2 * a->K), b, LOGN);
+}
+template <int LOGN>
+int md_epilogue_to(const MdEpiToArgs* a, pc_stream_t s) {
+    if (!a || !epi_ok(a->m) || !ref_ok(a->a)) return -1;
+    if (a->m.n == 0 || a->m.K == 0) return 0;
+    PCH_LAUNCH(md_epi_k<true>, grid<LOGN>(a->m.n, 2 * a->m.K), *a, LOGN);
+}
+inline int wsum_check(const WsumArgs& w) {
+    if (w.nsrc < 0 || w.nsrc > 8 || !w.pr || !ref_ok(w.out) || w.n < 0 || w.K < 0) return -1;
+    if (w.nsrc > 0 && (!w.w || !w.ws)) return -1;
+    for (int j = 0; j < w.nsrc; ++j)
+        if (!ref_ok(w.src[j])) return -1;
+    return 0;
+}
+inline WsumMultiArgs wsum_one(const WsumArgs& w, const void* k) {
+    WsumMultiArgs m{};
+    m.out[0] = w.out;
+    for (int j = 0; j < 8; ++j) m.src[j] = w.src[j];
+    m.w[0] = w.w;
+    m.ws[0] = w.ws;
+    m.k[0] = k;
+    m.pr = w.pr;
+    m.nout = 1;
+    m.nsrc = w.nsrc;
+    m.rowstride = w.rowstride;
+    m.K = w.K;
+    m.n[0] = m.nmax = w.n;
+    return m;
+}
+template <int LOGN>
+int wsum(const WsumArgs* a, pc_stream_t s) {
+    if (!a || wsum_check(*a)) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(wsum_k, grid<LOGN>(a->n, a->K), wsum_one(*a, nullptr), LOGN);
+}
+template <int LOGN>
+int wsum_kc(const WsumKArgs* a, pc_stream_t s) {
+    if (!a || !a->k || wsum_check(a->w)) return -1;
+    if (a->w.n == 0 || a->w.K == 0) return 0;
+    PCH_LAUNCH(wsum_k, grid<LOGN>(a->w.n, a->w.K), wsum_one(a->w, a->k), LOGN);
+}
+template <int LOGN>
+int wsum_multi(const WsumMultiArgs* a, pc_stream_t s) {
+    if (!a || a->nsrc < 1 || a->nsrc > 8 || a->nout < 1 || a->nout > 3) return -1;
+    if (!a->pr || a->K < 0 || a->nmax < 0) return -1;
+    for (int m = 0; m < a->nout; ++m)
+        if (!ref_ok(a->out[m]) || !a->w[m] || !a->ws[m] || a->n[m] > a->nmax) return -1;
+    for (int j = 0; j < a->nsrc; ++j)
+        if (!ref_ok(a->src[j])) return -1;
+    if (a->nmax == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(wsum_k, grid<LOGN>(a->nmax, a->K), *a, LOGN);
+}
+template <int LOGN>
+int add_const(const AddConstArgs* a, pc_stream_t s) {
+    if (!a || !a->pr || !a->k || !ref_ok(a->x) || a->n < 0 || a->K < 0) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(add_const_k, grid<LOGN>(a->n, a->K), *a, LOGN);
+}
+inline MulAddNArgs mul_one(const MulTableArgs& m, const PolyRef* y) {
+    MulAddNArgs n{};
+    n.out = m.out;
+    if (y) n.y = *y;
+    n.x[0] = m.in;
+    n.t[0] = m.t;
+    n.pr = m.pr;
+    n.n = m.n;
+    n.K = m.K;
+    n.nterm = 1;
+    return n;
+}
+inline bool mul_ok(const MulTableArgs& m) {
+    return m.pr && m.t && ref_ok(m.out) && ref_ok(m.in) && m.n >= 0 && m.K >= 0;
+}
+template <int LOGN>
+int mul_table(const MulTableArgs* a, pc_stream_t s) {
+    if (!a || !mul_ok(*a)) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH((mul_k<0, false>), grid<LOGN>(a->n, 2 * a->K), mul_one(*a, nullptr), LOGN);
+}
+template <int LOGN>
+int mul_add(const MulAddArgs* a, pc_stream_t s) {
+    if (!a || a->sub < 0 || a->sub > 2 || !mul_ok(a->m) || !ref_ok(a->y)) return -1;
+    if (a->m.n == 0 || a->m.K == 0) return 0;
+    const dim3 g = grid<LOGN>(a->m.n, 2 * a->m.K);
+    const MulAddNArgs n = mul_one(a->m, &a->y);
+    if (a->sub == 0) PCH_LAUNCH((mul_k<0, true>), g, n, LOGN);
+    if (a->sub == 1) PCH_LAUNCH((mul_k<1, true>), g, n, LOGN);
+    PCH_LAUNCH((mul_k<2, true>), g, n, LOGN);
+}
+template <int LOGN>
+int mul_add_n(const MulAddNArgs* a, pc_stream_t s) {
+    if (!a || a->nterm < 1 || a->nterm > 8 || !a->pr || !ref_ok(a->out) || a->n < 0 || a->K < 0) return -1;
+    for (int j = 0; j < a->nterm; ++j)
+        if (!ref_ok(a->x[j]) || !a->t[j]) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    const dim3 g = grid<LOGN>(a->n, 2 * a->K);
+    if (a->y.base) PCH_LAUNCH((mul_k<0, true>), g, *a, LOGN);
+    PCH_LAUNCH((mul_k<0, false>), g, *a, LOGN);
+}
+inline bool comb_ok(const RescaleCombineArgs& c) {
+    return c.pr && c.alpha && c.alphas && ref_ok(c.x) && ref_ok(c.tmp) && c.n >= 0 && c.K >= 0;
+}
+template <int LOGN>
+int rescale_combine(const RescaleCombineArgs* a, pc_stream_t s) {
+    if (!a || !comb_ok(*a)) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    RescaleCombineToArgs r{};
+    r.a = *a;
+    r.out = a->x;
+    PCH_LAUNCH(combine_k, grid<LOGN>(a->n, 2 * a->K), r, LOGN);
+}
+template <int LOGN>
+int rescale_combine_to(const RescaleCombineToArgs* a, pc_stream_t s) {
+    if (!a || !comb_ok(a->a) || !ref_ok(a->out)) return -1;
+    if (a->a.n == 0 || a->a.K == 0) return 0;
+    PCH_LAUNCH(combine_k, grid<LOGN>(a->a.n, 2 * a->a.K), *a, LOGN);
+}
+template <int LOGN>
+int ew_many(const EwManyArgs* a, pc_stream_t s) {
+    if (!a || a->n < 1 || a->n > PC_EWM_MAX || !a->pr || a->nrows < 0) return -1;
+    for (int j = 0; j < a->n; ++j)
+        if (!a->out[j] || !a->a[j]) return -1;
+    if (a->nrows == 0) return 0;
+    PCH_LAUNCH(ew_many_k, grid<LOGN>(a->nrows, a->n), *a, LOGN);
+}
+template <int LOGN>
+int submul_many(const SubMulManyArgs* a, pc_stream_t s) {
+    if (!a || a->n < 1 || a->n > PC_EWM_MAX || !a->pr || !a->t || a->nrows < 0) return -1;
+    for (int j = 0; j < a->n; ++j)
+        if (!a->out[j] || !a->a[j] || !a->b[j]) return -1;
+    if (a->nrows == 0) return 0;
+    PCH_LAUNCH(submul_many_k, grid<LOGN>(a->nrows, a->n), *a, LOGN);
+}
+#undef PCH_LAUNCH
+
+}  // namespace em
+
+#define PCH_EM_INST(L)                                                                                               \
+    int tensor_##L(const TensorArgs* a, pc_stream_t s) { return em::tensor<L>(a, s); }                               \
+    int tensor_y_##L(const TensorYArgs* a, pc_stream_t s) { return em::tensor_y<L>(a, s); }                          \
+    int tensor_sum_##L(const TensorSumArgs* a, pc_stream_t s) { return em::tensor_sum<L>(a, s); }                    \
+    int md_epilogue_##L(const MdEpiArgs* a, pc_stream_t s) { return em::md_epilogue<L>(a, s); }                      \
+    int md_epilogue_to_##L(const MdEpiToArgs* a, pc_stream_t s) { return em::md_epilogue_to<L>(a, s); }              \
+    int wsum_##L(const WsumArgs* a, pc_stream_t s) { return em::wsum<L>(a, s); }                                     \
+    int wsum_k_##L(const WsumKArgs* a, pc_stream_t s) { return em::wsum_kc<L>(a, s); }                               \
+    int wsum_multi_##L(const WsumMultiArgs* a, pc_stream_t s) { return em::wsum_multi<L>(a, s); }                    \
+    int add_const_##L(const AddConstArgs* a, pc_stream_t s) { return em::add_const<L>(a, s); }                       \
+    int mul_table_##L(const MulTableArgs* a, pc_stream_t s) { return em::mul_table<L>(a, s); }                       \
+    int mul_add_##L(const MulAddArgs* a, pc_stream_t s) { return em::mul_add<L>(a, s); }                             \
+    int mul_add_n_##L(const MulAddNArgs* a, pc_stream_t s) { return em::mul_add_n<L>(a, s); }                        \
+    int rescale_combine_##L(const RescaleCombineArgs* a, pc_stream_t s) { return em::rescale_combine<L>(a, s); }     \
+    int rescale_combine_to_##L(const RescaleCombineToArgs* a, pc_stream_t s) {                                       \
+        return em::rescale_combine_to<L>(a, s);                                                                      \
+    }                                                                                                                \
+    int ew_many_##L(const EwManyArgs* a, pc_stream_t s) { return em::ew_many<L>(a, s); }                             \
+    int submul_many_##L(const SubMulManyArgs* a, pc_stream_t s) { return em::submul_many<L>(a, s); }
+PCH_EM_INST(12)
+PCH_EM_INST(13)
+PCH_EM_INST(14)
+PCH_EM_INST(15)
+PCH_EM_INST(16)
+
+}  // namespace pch

@@ -49,6 +49,10 @@ int kska_patch_fill(int logn, const uint32_t* const* seeds, const PrimeConst* pr
 // the fast dot with the retry values read from P instead of redrawn; -2 where the fast dot does not apply
 int ks_dot_patched(int logn, const KsKeyArgs* g, const PatchTab* P, pc_stream_t s);
 
+// The forward NTT of composite-rescale corrections (rescale_fwd): row i's input generated in the column pass from the
+// two sources r (ndrop 2) names, top - rprime[i] and top - 1 - rprime[i] rows above row i; a's epilogue applies
+int ntt_fwd_rescale(int logn, const NttArgs* a, const RescaleArgs* r, pc_stream_t s);
+
 // ks_dot_key's summed rotations (c0_mode | KS_SUM): out = sum_r sigma_r(dot_r), gathered in output order
 int ks_dot_key_sum(int logn, const KsKeyArgs* g, pc_stream_t s);
 

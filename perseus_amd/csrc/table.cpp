@@ -20,7 +20,25 @@ namespace pch {
     int ksk_unpack_##L(const KskUnpackArgs*, pc_stream_t);          \
     int cts_fused_##L(const CtsArgs*, pc_stream_t);                  \
     int cts_fused_regen_##L(const CtsRegenArgs*, pc_stream_t);       \
-    int ks_dot_regen_##L(const KsRegenArgs*, pc_stream_t);
+    int ks_dot_regen_##L(const KsRegenArgs*, pc_stream_t);           \
+    int tensor_##L(const TensorArgs*, pc_stream_t);                  \
+    int tensor_y_##L(const TensorYArgs*, pc_stream_t);               \
+    int tensor_sum_##L(const TensorSumArgs*, pc_stream_t);           \
+    int md_epilogue_##L(const MdEpiArgs*, pc_stream_t);              \
+    int md_epilogue_to_##L(const MdEpiToArgs*, pc_stream_t);         \
+    int wsum_##L(const WsumArgs*, pc_stream_t);                      \
+    int wsum_k_##L(const WsumKArgs*, pc_stream_t);                   \
+    int wsum_multi_##L(const WsumMultiArgs*, pc_stream_t);           \
+    int add_const_##L(const AddConstArgs*, pc_stream_t);             \
+    int mul_table_##L(const MulTableArgs*, pc_stream_t);             \
+    int mul_add_##L(const MulAddArgs*, pc_stream_t);                 \
+    int mul_add_n_##L(const MulAddNArgs*, pc_stream_t);              \
+    int rescale_combine_##L(const RescaleCombineArgs*, pc_stream_t); \
+    int rescale_combine_to_##L(const RescaleCombineToArgs*, pc_stream_t); \
+    int ew_many_##L(const EwManyArgs*, pc_stream_t);                 \
+    int submul_many_##L(const SubMulManyArgs*, pc_stream_t);         \
+    int rescale_coef_##L(const RescaleArgs*, pc_stream_t);           \
+    int rescale_fwd_##L(const RescaleNttArgs*, pc_stream_t);
 PCH_DECL(12)
 PCH_DECL(13)
 PCH_DECL(14)
@@ -36,15 +54,14 @@ int absent(const A*, pc_stream_t) {
     static const KernelTable TABLE_##L = {                                                                           \
         PC_KERNELS_ABI, 4, 0, L,                                                                                     \
         ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
-        absent<PtDotArgs>, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, absent<TensorArgs>,        \
-        absent<MdEpiArgs>, absent<WsumArgs>, absent<AddConstArgs>, absent<MulTableArgs>, absent<RescaleArgs>,        \
-        absent<RescaleCombineArgs>, automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L,             \
-        ksk_unpack_##L, absent<ModRaiseArgs>, absent<SmallIntArgs>, absent<SpruExtractArgs>, absent<SpruFftArgs>,    \
-        absent<SpruScatterArgs>, cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>,          \
-        absent<WsumKArgs>, absent<RescaleCombineToArgs>, absent<MdEpiToArgs>, absent<SmallInt1Args>,                 \
-        absent<CoeffArgs>, absent<MulAddArgs>, absent<RescaleNttArgs>, absent<MulAddNArgs>, absent<TensorYArgs>,     \
-        absent<WsumMultiArgs>, bconv_##L, absent<TfheArgs>, absent<TensorSumArgs>, absent<TensorMultiArgs>,          \
-        absent<TensorSeededArgs>, absent<EwManyArgs>, absent<SubMulManyArgs>, absent<PackSplitArgs>,                 \
+        absent<PtDotArgs>, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
+        md_epilogue_##L, wsum_##L, add_const_##L, mul_table_##L, rescale_coef_##L, rescale_combine_##L,            \
+        automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L, ksk_unpack_##L, absent<ModRaiseArgs>,   \
+        absent<SmallIntArgs>, absent<SpruExtractArgs>, absent<SpruFftArgs>, absent<SpruScatterArgs>,                 \
+        cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>, wsum_k_##L, rescale_combine_to_##L, \
+        md_epilogue_to_##L, absent<SmallInt1Args>, absent<CoeffArgs>, mul_add_##L, rescale_fwd_##L,          \
+        mul_add_n_##L, tensor_y_##L, wsum_multi_##L, bconv_##L, absent<TfheArgs>, tensor_sum_##L,                    \
+        absent<TensorMultiArgs>, absent<TensorSeededArgs>, ew_many_##L, submul_many_##L, absent<PackSplitArgs>,      \
         absent<PackDotArgs>};
 PCH_TABLE(12)
 PCH_TABLE(13)

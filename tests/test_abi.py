@@ -140,3 +140,33 @@ def test_dot_launchers_reject_out_of_range_arguments():
     kk = abi.KsKeyArgs()
     kk.ks.c0_mode, kk.ks.K = abi.KS_SUM, 5
     assert abi.call("ks_dot_key", kk, log_n=12) == -2      # K > 4
+
+
+def test_em_launchers_reject_out_of_range_arguments():
+    """The EvalMod / rescale launchers' count checks (crates/pc-kernels/kernels/em.cuh:580-692, rescale.cuh:211-263)
+    and null operands, all decided before any device call."""
+    from perseus_amd import abi
+    assert abi.call("wsum_multi", abi.WsumMultiArgs(), log_n=12) == -1      # nout 0
+    m = abi.MulAddArgs()
+    m.sub = 3
+    assert abi.call("mul_add", m, log_n=12) == -1                           # sub outside 0..2
+    n = abi.MulAddNArgs()
+    n.nterm = 9
+    assert abi.call("mul_add_n", n, log_n=12) == -1                         # more than 8 terms
+    s = abi.TensorSumArgs()
+    s.npairs = 17
+    assert abi.call("tensor_sum", s, log_n=12) == -1                        # more than 16 pairs
+    r = abi.RescaleArgs()
+    r.ndrop = 3
+    assert abi.call("rescale_coef", r, log_n=12) == -1                      # one or two primes only
+    rf = abi.RescaleNttArgs()
+    rf.rs.ndrop = 1
+    assert abi.call("rescale_fwd", rf, log_n=12) == -1                      # the pipeline drops two
+    assert abi.call("ew_many", abi.EwManyArgs(), log_n=12) == -1            # n 0
+    assert abi.call("tensor_y", abi.TensorYArgs(), log_n=12) == -1          # no y constant
+    assert abi.call("md_epilogue", abi.MdEpiArgs(), log_n=12) == -1         # null operands
+    w = abi.WsumArgs()
+    w.nsrc = 9
+    assert abi.call("wsum", w, log_n=12) == -1                              # more than 8 sources
+    t = abi.TensorArgs()
+    assert abi.call("tensor", t, log_n=12) == -1                            # null outputs

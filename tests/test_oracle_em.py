@@ -1,0 +1,266 @@
+"""Pins of the oracle's EvalMod / plaintext-product kernels and composite rescale (oracle/em.py), each against what the
+mathematics fixes rather than against the formula restated:
+
+- tensor / tensor_y / tensor_sum: decryption: c0 + c1 s + d2 s^2 = (a0 + a1 s)(b0 + b1 s) word by word in the
+  evaluation domain (summed over the pairs), with the old words, the doubling and +- c y entering as the documented
+  order says (a dropped cross term, a transposed operand or the doubling before the add fails it);
+- mul_table: the evaluation-domain product is the negacyclic convolution of the coefficient rows (schoolbook, N = 64);
+  mul_add / mul_add_n decrypt to y +- in t and y + sum_j x_j t_j;
+- md_epilogue: with x = t + v b and binv = b^-1 the epilogue adds exactly v (then doubles, then adds k on part 0);
+- wsum / add_const: decryption is linear: Dec(out) = sum_j w_j Dec(src_j) + k;
+- ew_many / submul_many: the inverse operations undo them;
+- composite rescale: in coefficient form each output coefficient is the exact integer (X - [X]_{q_a}) / q_a of the CRT
+  value X (Python integers), twice for two primes; the fold equals scaling first.
+"""
+import numpy as np
+import pytest
+
+from oracle import em
+from tests import twin
+from tests.test_oracle_ks import small_chain
+
+RNG = np.random.default_rng(2024)
+
+
+def rand_ct(q, K, n, N, rng=RNG):
+    x = np.zeros((K, 2, n, N), np.uint32)
+    for r in range(n):
+        x[:, :, r] = rng.integers(0, q[r], (K, 2, N))
+    return x
+
+
+def dec(q, c0, c1, s, d2=None):
+    """c0 + c1 s (+ d2 s^2) per row, as Python-exact uint64 arithmetic mod q"""
+    n = c0.shape[-2]
+    qq = np.asarray(q[:n], np.uint64).reshape(n, 1)
+    s = s.astype(np.uint64)
+    v = (c0.astype(np.uint64) + (c1.astype(np.uint64) * s) % qq) % qq
+    if d2 is not None:
+        v = (v + (((d2.astype(np.uint64) * s) % qq) * s) % qq) % qq
+    return v
+
+
+def mulq(a, b, q):
+    n = a.shape[-2]
+    qq = np.asarray(q[:n], np.uint64).reshape(n, 1)
+    return (a.astype(np.uint64) * b.astype(np.uint64)) % qq
+
+
+def addq(a, b, q):
+    n = a.shape[-2]
+    qq = np.asarray(q[:n], np.uint64).reshape(n, 1)
+    return (a.astype(np.uint64) + b.astype(np.uint64)) % qq
+
+
+Q = twin.descending_primes(31, 1 << 13, 5)
+N = 256
+
+
+def secret(q, n, N):
+    return np.stack([RNG.integers(0, q[r], N) for r in range(n)]).astype(np.uint64)
+
+
+@pytest.mark.parametrize("npairs,acc,acc_d2,dbl,ysub", [(1, 0, 0, 0, None), (2, 1, 1, 1, None), (2, 0, 0, 1, 0),
+                                                         (2, 1, 0, 0, 1), (7, 1, 1, 0, None)])
+def test_tensor_decrypts_to_the_product(npairs, acc, acc_d2, dbl, ysub):
+    K, n = 2, 4
+    s = secret(Q, n, N)
+    pairs = [(rand_ct(Q, K, n, N), rand_ct(Q, K, n, N)) for _ in range(npairs)]
+    old, old_d2 = rand_ct(Q, K, n, N), rand_ct(Q, K, n, N)[:, 1]
+    y, yc = rand_ct(Q, K, n, N), [int(RNG.integers(0, q)) for q in Q[:n]]
+    c0, c1, d2 = em.tensor(Q, pairs, old, old_d2, acc, acc_d2, dbl, None if ysub is None else y, yc, bool(ysub))
+    for k in range(K):
+        want = np.zeros((n, N), np.uint64)
+        for a, b in pairs:
+            want = addq(want, mulq(dec(Q, a[k, 0], a[k, 1], s), dec(Q, b[k, 0], b[k, 1], s), Q), Q)
+        if acc:
+            want = addq(want, dec(Q, old[k, 0], old[k, 1], s), Q)
+        if acc_d2:
+            want = addq(want, mulq(mulq(old_d2[k], s, Q), s, Q), Q)
+        if dbl:
+            want = addq(want, want, Q)
+        if ysub is not None:
+            cy = mulq(dec(Q, y[k, 0], y[k, 1], s), np.array(yc, np.uint64).reshape(n, 1).repeat(N, 1), Q)
+            qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+            want = (want + qq - cy) % qq if ysub else addq(want, cy, Q)
+        assert (dec(Q, c0[k], c1[k], s, d2[k]) == want).all()
+
+
+def test_mul_table_is_the_negacyclic_product():
+    ctx = small_chain(logn=6, nq=3, kp=1, dnum=1, bits=30)
+    n, N6 = 3, ctx.n
+    q = ctx.q
+    a = np.stack([RNG.integers(0, q[r], N6) for r in range(n)]).astype(np.uint32)
+    t = np.stack([RNG.integers(0, q[r], N6) for r in range(n)]).astype(np.uint32)
+    ids = list(range(n))
+    ae, te = ctx.ntt_fwd(a.copy(), ids), ctx.ntt_fwd(t.copy(), ids)
+    x = np.zeros((1, 2, n, N6), np.uint32)
+    x[0, 0], x[0, 1] = ae, ae
+    prod = em.mul_add_n(q, [(x, te)])
+    got = ctx.ntt_inv(prod[0, 0], ids)
+    for r in range(n):
+        p = int(q[r])
+        want = [0] * N6
+        for i in range(N6):
+            for j in range(N6):
+                v = int(a[r, i]) * int(t[r, j])
+                if i + j < N6:
+                    want[i + j] += v
+                else:
+                    want[i + j - N6] -= v
+        assert [w % p for w in want] == [int(v) for v in got[r]]
+
+
+@pytest.mark.parametrize("mode", [None, 0, 1, 2])
+def test_mul_add_decrypts(mode):
+    K, n = 2, 3
+    s = secret(Q, n, N)
+    x, y = rand_ct(Q, K, n, N), rand_ct(Q, K, n, N)
+    t = np.stack([RNG.integers(0, Q[r], N) for r in range(n)]).astype(np.uint32)
+    out = em.mul_add_n(Q, [(x, t)], None if mode is None else y, mode or 0)
+    qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+    for k in range(K):
+        m = mulq(dec(Q, x[k, 0], x[k, 1], s), t, Q)
+        dy = dec(Q, y[k, 0], y[k, 1], s)
+        want = m if mode is None else addq(dy, m, Q) if mode == 0 else (dy + qq - m) % qq if mode == 1 else (m + qq - dy) % qq
+        assert (dec(Q, out[k, 0], out[k, 1], s) == want).all()
+
+
+def test_mul_add_n_decrypts_to_the_sum():
+    K, n, T = 1, 3, 8
+    s = secret(Q, n, N)
+    y = rand_ct(Q, K, n, N)
+    terms = [(rand_ct(Q, K, n, N), np.stack([RNG.integers(0, Q[r], N) for r in range(n)]).astype(np.uint32))
+             for _ in range(T)]
+    out = em.mul_add_n(Q, terms, y, 0)
+    want = dec(Q, y[0, 0], y[0, 1], s)
+    for x, t in terms:
+        want = addq(want, mulq(dec(Q, x[0, 0], x[0, 1], s), t, Q), Q)
+    assert (dec(Q, out[0, 0], out[0, 1], s) == want).all()
+
+
+@pytest.mark.parametrize("dbl,withk", [(0, 0), (1, 1), (0, 1)])
+def test_md_epilogue_adds_v(dbl, withk):
+    K, n = 2, 4
+    dst, t, v = rand_ct(Q, K, n, N), rand_ct(Q, K, n, N), rand_ct(Q, K, n, N)
+    b = [int(RNG.integers(1, q)) for q in Q[:n]]
+    binv = [pow(bb, -1, int(q)) for bb, q in zip(b, Q)]
+    qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+    x = ((t.astype(np.uint64) + mulq(v, np.array(b, np.uint64).reshape(n, 1).repeat(N, 1), Q)) % qq).astype(np.uint32)
+    k = [int(q) + 5 if i % 2 else int(RNG.integers(0, q)) for i, q in enumerate(Q[:n])]  # raw constants, some >= p
+    got = em.md_epilogue(Q, dst, x, t, binv, k if withk else None, bool(dbl))
+    want = addq(dst, v, Q)
+    if dbl:
+        want = addq(want, want, Q)
+    if withk:
+        want[:, 0] = addq(want[:, 0], np.array(k, np.uint64).reshape(n, 1) % qq, Q)
+    assert (got == want).all()
+    got_to = em.md_epilogue_to(Q, dst, x, t, binv, sub=True)
+    assert (addq(got_to, v, Q) == dst).all()
+
+
+def test_wsum_and_add_const_are_linear():
+    K, n = 2, 4
+    s = secret(Q, n, N)
+    srcs = [rand_ct(Q, K, n, N) for _ in range(5)]
+    w = [[int(RNG.integers(0, q)) for q in Q[:n]] for _ in srcs]
+    k = [int(RNG.integers(0, 2 * q)) for q in Q[:n]]
+    out = em.wsum(Q, srcs, w, k)
+    qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+    for c in range(K):
+        want = np.array(k, np.uint64).reshape(n, 1) % qq + np.zeros((n, N), np.uint64)
+        for j, x in enumerate(srcs):
+            want = addq(want, mulq(dec(Q, x[c, 0], x[c, 1], s), np.array(w[j], np.uint64).reshape(n, 1).repeat(N, 1),
+                                   Q), Q)
+        assert (dec(Q, out[c, 0], out[c, 1], s) == want).all()
+    x = srcs[0]
+    got = em.add_const(Q, x, k)
+    for c in range(K):
+        want = addq(dec(Q, x[c, 0], x[c, 1], s), np.array(k, np.uint64).reshape(n, 1) % qq + np.zeros((n, N), np.uint64),
+                    Q)
+        assert (dec(Q, got[c, 0], got[c, 1], s) == want).all()
+
+
+def test_ew_many_and_submul_many_invert():
+    n = 4
+    a, b, c = (rand_ct(Q, 1, n, N)[0, 0] for _ in range(3))
+    t = np.stack([RNG.integers(1, Q[r], N) for r in range(n)]).astype(np.uint32)
+    qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+    s3 = em.ew_many(Q, a, b, c)
+    assert (((s3.astype(np.uint64) + 2 * qq - b - c) % qq) == a).all()
+    assert (em.ew_many(Q, a) == a).all()
+    sm = em.submul_many(Q, a, b, t)
+    tinv = np.vectorize(lambda v, p: pow(int(v), -1, int(p)), otypes=[object])(t, np.asarray(Q[:n]).reshape(n, 1))
+    back = np.array([[(int(sm[r, i]) * int(tinv[r, i]) + int(b[r, i])) % int(Q[r]) for i in range(N)]
+                     for r in range(n)], np.uint64)
+    assert (back == a).all()
+
+
+# ----------------------------------------------------------------------------------------------- composite rescale
+def crt_values(q, rows):
+    """the integers X in [0, prod q) of the coefficient rows [len(q)][N]"""
+    big = 1
+    for p in q:
+        big *= int(p)
+    out = []
+    for i in range(rows.shape[1]):
+        x = 0
+        for r, p in enumerate(q):
+            p = int(p)
+            m = big // p
+            x += int(rows[r, i]) * m * pow(m % p, -1, p)
+        out.append(x % big)
+    return out
+
+
+def exact_rescale(vals, q_drop):
+    out = []
+    for x in vals:
+        c = x % q_drop
+        if c > q_drop // 2:
+            c -= q_drop
+        assert (x - c) % q_drop == 0
+        out.append((x - c) // q_drop)
+    return out
+
+
+@pytest.mark.parametrize("ndrop", [1, 2])
+def test_rescale_is_the_exact_division(ndrop):
+    ctx = small_chain(logn=8, nq=6, kp=1, dnum=2, bits=30)
+    q = ctx.q
+    top = 5
+    K = 2
+    coef = np.zeros((K, 2, top + 1, ctx.n), np.uint32)
+    for r in range(top + 1):
+        coef[:, :, r] = RNG.integers(0, q[r], (K, 2, ctx.n))
+    x = np.zeros_like(coef)
+    for k in range(K):
+        for part in range(2):
+            x[k, part] = ctx.ntt_fwd(coef[k, part].copy(), list(range(top + 1)))
+    out = em.rescale(ctx, q, x, top, ndrop)
+    rows = top + 1 - ndrop
+    for k in range(K):
+        for part in range(2):
+            got = ctx.ntt_inv(out[k, part], list(range(rows)))
+            vals = crt_values(q[:top + 1], coef[k, part])
+            vals = exact_rescale(vals, int(q[top]))
+            if ndrop == 2:
+                vals = exact_rescale(vals, int(q[top - 1]))
+            want = np.array([[v % int(q[r]) for v in vals] for r in range(rows)], np.uint64)
+            assert (got == want).all()
+
+
+def test_composite_equals_two_single_drops_and_the_fold():
+    ctx = small_chain(logn=8, nq=6, kp=1, dnum=2, bits=30)
+    q = ctx.q
+    top = 4
+    x = rand_ct(q, 2, top + 1, ctx.n)
+    two = em.rescale(ctx, q, x, top, 2)
+    one = em.rescale(ctx, q, em.rescale(ctx, q, x, top, 1), top - 1, 1)
+    assert (two == one).all()
+    # fold c: rescale(c x) with the tops scaled and alpha_i c_i equals scaling every row first
+    c = [int(RNG.integers(2, p)) for p in q]
+    cx = x.copy()
+    for r in range(top + 1):
+        cx[:, :, r] = (x[:, :, r].astype(np.uint64) * c[r] % int(q[r])).astype(np.uint32)
+    assert (em.rescale(ctx, q, x, top, 2, fold=c) == em.rescale(ctx, q, cx, top, 2)).all()

@@ -485,17 +485,69 @@ typedef struct SubMulManyArgs {
 } SubMulManyArgs;
 PC_STATIC_ASSERT(sizeof(SubMulManyArgs) == 3 * PC_EWM_MAX * 8 + 24, "SubMulManyArgs layout");
 
+/* args.cuh:665-676: composite ModRaise, coefficient form: for rows t in [r0, r1) of K ciphertexts (nparts polynomials
+ * from part 0), x[t] = sum_{k < d} centred([x_k qhatinv_k]_{q_k}) qhat[k][t] mod q_t, the sources x_k = rows 0..d-1
+ * of the same polynomial (each term centred on its own prime; not written) */
+typedef struct ModRaiseArgs {
+    void* x;
+    const PrimeConst* pr;
+    uint64_t ct_stride, part_stride;
+    uint64_t qhatinv[4];
+    uint64_t qhat[4][64];
+    int32_t K, d, r0, r1, nparts, pad;
+} ModRaiseArgs;
+PC_STATIC_ASSERT(sizeof(ModRaiseArgs) == 2136, "ModRaiseArgs layout");
+
+/* args.cuh:678-697: exact small-integer scaling: per coefficient, Garner from the k source rows, centre against Q_k / 2,
+ * optionally q = floor((|x| R + 2^191) / 2^192) (R = round(2^192 / D)), reduce modulo every output row orow[o] (prime
+ * ids; pow32[o][w] = (2^32)^w mod p), restore the sign. Source primes below 2^31. */
+#define PC_SI_MAXK 4
+#define PC_SI_MAXW 8
+#define PC_SI_MAXR 8
+#define PC_SI_SHIFT 192
+#define PC_SI_MAXOUT 64
+typedef struct SmallIntTab {
+    int32_t k, nout, nw, nr, divide, pad;
+    uint32_t q[PC_SI_MAXK];
+    uint32_t qinv[PC_SI_MAXK][PC_SI_MAXK]; /* qinv[i][j] = q_j^-1 mod q_i, j < i */
+    uint32_t Qk[PC_SI_MAXW], Qkh[PC_SI_MAXW];
+    uint32_t R[PC_SI_MAXR];
+    int32_t orow[PC_SI_MAXOUT];
+    uint32_t pow32[PC_SI_MAXOUT][PC_SI_MAXW + PC_SI_MAXR];
+} SmallIntTab;
+PC_STATIC_ASSERT(sizeof(SmallIntTab) == 4552, "SmallIntTab layout");
+
+/* args.cuh:698-709: source row i of (c, part) at src + c src_ct_stride + part src_part_stride + i N; output row
+ * orow[o] at out + c ct_stride + part part_stride + orow[o] N; tab in device memory */
+typedef struct SmallIntArgs {
+    const void* src;
+    void* out;
+    const SmallIntTab* tab;
+    const PrimeConst* pr;
+    uint64_t src_ct_stride, src_part_stride, ct_stride, part_stride;
+    int32_t K, nparts;
+} SmallIntArgs;
+PC_STATIC_ASSERT(sizeof(SmallIntArgs) == 72, "SmallIntArgs layout");
+
+/* args.cuh:890-907: the scaling from one source prime: x = row 0 centred against q0, q = floor((|x| mc + 2^(sh-1)) /
+ * 2^sh), row t := sign(x) q mod q_t for t < nrows, in place (row 0 read first); 1 <= sh <= 127, q < 2^64 */
+typedef struct SmallInt1Args {
+    void* x;
+    const PrimeConst* pr;
+    uint64_t ct_stride, part_stride;
+    uint64_t mc;
+    int32_t sh, nrows, K, nparts;
+} SmallInt1Args;
+PC_STATIC_ASSERT(sizeof(SmallInt1Args) == 56, "SmallInt1Args layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct PtDotArgs;
 struct EncodeArgs;
-struct ModRaiseArgs;
-struct SmallIntArgs;
 struct SpruExtractArgs;
 struct SpruFftArgs;
 struct SpruScatterArgs;
 struct PcmmArgs;
 struct CcmmArgs;
-struct SmallInt1Args;
 struct CoeffArgs;
 struct TfheArgs;
 struct TensorMultiArgs;

@@ -185,6 +185,32 @@ class SubMulManyArgs(C.Structure):
                 ("nrows", i32)]
 
 
+class ModRaiseArgs(C.Structure):
+    """args.cuh:665-676 (2136 bytes)."""
+    _fields_ = [("x", vp), ("pr", vp), ("ct_stride", u64), ("part_stride", u64), ("qhatinv", u64 * 4),
+                ("qhat", (u64 * 64) * 4), ("K", i32), ("d", i32), ("r0", i32), ("r1", i32), ("nparts", i32),
+                ("pad", i32)]
+
+
+class SmallIntTab(C.Structure):
+    """args.cuh:678-697 (4552 bytes; lives in device memory)."""
+    _fields_ = [("k", i32), ("nout", i32), ("nw", i32), ("nr", i32), ("divide", i32), ("pad", i32), ("q", u32 * 4),
+                ("qinv", (u32 * 4) * 4), ("Qk", u32 * 8), ("Qkh", u32 * 8), ("R", u32 * 8), ("orow", i32 * 64),
+                ("pow32", (u32 * 16) * 64)]
+
+
+class SmallIntArgs(C.Structure):
+    """args.cuh:698-709 (72 bytes)."""
+    _fields_ = [("src", vp), ("out", vp), ("tab", vp), ("pr", vp), ("src_ct_stride", u64), ("src_part_stride", u64),
+                ("ct_stride", u64), ("part_stride", u64), ("K", i32), ("nparts", i32)]
+
+
+class SmallInt1Args(C.Structure):
+    """args.cuh:890-907 (56 bytes)."""
+    _fields_ = [("x", vp), ("pr", vp), ("ct_stride", u64), ("part_stride", u64), ("mc", u64), ("sh", i32),
+                ("nrows", i32), ("K", i32), ("nparts", i32)]
+
+
 KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:207-210)
 
 assert C.sizeof(KeyTab) == 40 and C.sizeof(CtsArgs) == 200 and C.sizeof(CtsRegenArgs) == 240
@@ -198,6 +224,8 @@ assert C.sizeof(MulTableArgs) == 72 and C.sizeof(MulAddArgs) == 104 and C.sizeof
 assert C.sizeof(RescaleArgs) == 152 and C.sizeof(RescaleNttArgs) == 328 and C.sizeof(RescaleCombineArgs) == 80
 assert C.sizeof(RescaleCombineToArgs) == 104 and C.sizeof(EwManyArgs) == 4 * EWM_MAX * 8 + 16
 assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
+assert C.sizeof(ModRaiseArgs) == 2136 and C.sizeof(SmallIntTab) == 4552 and C.sizeof(SmallIntArgs) == 72
+assert C.sizeof(SmallInt1Args) == 56
 
 _LAUNCHER = C.CFUNCTYPE(C.c_int, vp, vp)
 

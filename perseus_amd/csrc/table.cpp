@@ -38,7 +38,10 @@ namespace pch {
     int ew_many_##L(const EwManyArgs*, pc_stream_t);                 \
     int submul_many_##L(const SubMulManyArgs*, pc_stream_t);         \
     int rescale_coef_##L(const RescaleArgs*, pc_stream_t);           \
-    int rescale_fwd_##L(const RescaleNttArgs*, pc_stream_t);
+    int rescale_fwd_##L(const RescaleNttArgs*, pc_stream_t);         \
+    int mod_raise_##L(const ModRaiseArgs*, pc_stream_t);             \
+    int small_int_##L(const SmallIntArgs*, pc_stream_t);             \
+    int small_int1_##L(const SmallInt1Args*, pc_stream_t);
 PCH_DECL(12)
 PCH_DECL(13)
 PCH_DECL(14)
@@ -56,10 +59,10 @@ int absent(const A*, pc_stream_t) {
         ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
         absent<PtDotArgs>, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
         md_epilogue_##L, wsum_##L, add_const_##L, mul_table_##L, rescale_coef_##L, rescale_combine_##L,            \
-        automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L, ksk_unpack_##L, absent<ModRaiseArgs>,   \
-        absent<SmallIntArgs>, absent<SpruExtractArgs>, absent<SpruFftArgs>, absent<SpruScatterArgs>,                 \
+        automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
+        small_int_##L, absent<SpruExtractArgs>, absent<SpruFftArgs>, absent<SpruScatterArgs>,                 \
         cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>, wsum_k_##L, rescale_combine_to_##L, \
-        md_epilogue_to_##L, absent<SmallInt1Args>, absent<CoeffArgs>, mul_add_##L, rescale_fwd_##L,          \
+        md_epilogue_to_##L, small_int1_##L, absent<CoeffArgs>, mul_add_##L, rescale_fwd_##L,          \
         mul_add_n_##L, tensor_y_##L, wsum_multi_##L, bconv_##L, absent<TfheArgs>, tensor_sum_##L,                    \
         absent<TensorMultiArgs>, absent<TensorSeededArgs>, ew_many_##L, submul_many_##L, absent<PackSplitArgs>,      \
         absent<PackDotArgs>};

@@ -170,3 +170,23 @@ def test_em_launchers_reject_out_of_range_arguments():
     assert abi.call("wsum", w, log_n=12) == -1                              # more than 8 sources
     t = abi.TensorArgs()
     assert abi.call("tensor", t, log_n=12) == -1                            # null outputs
+
+
+def test_raise_launchers_reject_out_of_range_arguments():
+    """The raise launchers' checks (crates/pc-kernels/kernels/bts.cuh:192-218), decided before any device call."""
+    from perseus_amd import abi
+    m = abi.ModRaiseArgs()
+    m.d, m.r0, m.r1, m.nparts, m.K = 5, 5, 8, 1, 1
+    assert abi.call("mod_raise", m, log_n=12) == -1      # more than four sources
+    m.d, m.r0 = 2, 1
+    assert abi.call("mod_raise", m, log_n=12) == -1      # a target row among the sources
+    m.r0, m.r1 = 2, 65
+    assert abi.call("mod_raise", m, log_n=12) == -1      # past 64 rows
+    s = abi.SmallIntArgs()
+    s.nparts, s.K = 3, 1
+    assert abi.call("small_int", s, log_n=12) == -1      # three parts
+    s1 = abi.SmallInt1Args()
+    s1.sh, s1.nrows, s1.K, s1.nparts = 0, 1, 1, 1
+    assert abi.call("small_int1", s1, log_n=12) == -1    # shift 0
+    s1.sh, s1.nrows = 3, 65
+    assert abi.call("small_int1", s1, log_n=12) == -1    # past 64 rows

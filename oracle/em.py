@@ -244,3 +244,13 @@ def rescale(oc, q, x, top, ndrop, fold=None):
             tmp = oc.ntt_fwd(tmp, list(range(rows)))
             out[k, part] = combine(q, x[k:k + 1, part:part + 1, :rows], tmp[None, None], alpha)[0, 0]
     return out
+
+
+# ----------------------------------------------------------------------------------------------- encryption
+def encrypt(q, a, s, e, m=None):
+    """encrypt (args.cuh:613-628; encrypt.cuh:10-31): limb l (prime id l) of c0 = e + m - a s, with a the "ENCA"
+    expander rows (twin.expand_row with w13 = the nonce), all [nl][N] in the evaluation domain."""
+    n = a.shape[0]
+    qq = _q(q, n)
+    em_ = _u(e) if m is None else _add(e, m, qq)
+    return _out(_sub(em_, _mul(a, s, qq), qq))

@@ -169,15 +169,18 @@ constexpr uint32_t KSK_T_MAX = 16;
 // keys.rs:478-498 (kska_expand_row): one base block per 16 slots, attempt t reads block b0 + t N/16, accept
 // v < floor((2^32-1)/p) p, the 16th attempt kept as is; value v mod p
 // (slots [s0, s0 + cnt), both multiples of 16; out[i] is slot s0 + i)
-void kska_range(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t s0, uint32_t cnt, uint32_t* out) {
+// (tag: "KSKA" for switching keys; the same rule with "ENCA" and w13 = the nonce expands an encryption's a,
+// args.cuh:614-617)
+void kska_range(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t s0, uint32_t cnt, uint32_t* out,
+                uint32_t tag = TAG_KSKA) {
     const uint32_t n16 = n >> 4, mp = (0xFFFFFFFFu / p) * p;
     uint32_t base[16], alt[16];
     for (uint32_t b0 = s0 >> 4; b0 < (s0 + cnt) >> 4; ++b0) {
-        chacha_block(seed, b0, digit, p, TAG_KSKA, 12, base);
+        chacha_block(seed, b0, digit, p, tag, 12, base);
         for (int w = 0; w < 16; ++w) {
             uint32_t v = base[w];
             for (uint32_t t = 1; v >= mp && t < KSK_T_MAX; ++t) {
-                chacha_block(seed, b0 + t * n16, digit, p, TAG_KSKA, 12, alt);
+                chacha_block(seed, b0 + t * n16, digit, p, tag, 12, alt);
                 v = alt[w];
             }
             out[b0 * 16 + w - s0] = v % p;
@@ -442,6 +445,9 @@ void or_chacha_block(const uint32_t key[8], uint32_t w12, uint32_t w13, uint32_t
 }
 void or_kska_expand_row(const uint32_t seed[8], uint32_t digit, uint32_t p, uint32_t n, uint32_t* out) {
     kska_row(seed, digit, p, n, out);
+}
+void or_expand_row(const uint32_t seed[8], uint32_t w13, uint32_t p, uint32_t n, uint32_t tag, uint32_t* out) {
+    kska_range(seed, w13, p, n, 0, n, out, tag);
 }
 // keys.rs:466-481 kska_expand (one slot, random access)
 uint32_t or_kska_expand(const uint32_t seed[8], uint32_t digit, uint32_t p, uint32_t slot, uint32_t n) {

@@ -185,6 +185,12 @@ class SubMulManyArgs(C.Structure):
                 ("nrows", i32)]
 
 
+class EncryptArgs(C.Structure):
+    """args.cuh:613-628 (64 bytes)."""
+    _fields_ = [("c0", vp), ("c1", vp), ("s", vp), ("e", vp), ("m", vp), ("seed", vp), ("pr", vp), ("nonce", u32),
+                ("nl", i32)]
+
+
 class ModRaiseArgs(C.Structure):
     """args.cuh:665-676 (2136 bytes)."""
     _fields_ = [("x", vp), ("pr", vp), ("ct_stride", u64), ("part_stride", u64), ("qhatinv", u64 * 4),
@@ -225,7 +231,7 @@ assert C.sizeof(RescaleArgs) == 152 and C.sizeof(RescaleNttArgs) == 328 and C.si
 assert C.sizeof(RescaleCombineToArgs) == 104 and C.sizeof(EwManyArgs) == 4 * EWM_MAX * 8 + 16
 assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
 assert C.sizeof(ModRaiseArgs) == 2136 and C.sizeof(SmallIntTab) == 4552 and C.sizeof(SmallIntArgs) == 72
-assert C.sizeof(SmallInt1Args) == 56
+assert C.sizeof(SmallInt1Args) == 56 and C.sizeof(EncryptArgs) == 64
 
 _LAUNCHER = C.CFUNCTYPE(C.c_int, vp, vp)
 

@@ -29,13 +29,14 @@ __device__ __forceinline__ int slot_of(const KeyTab& T, int t, int nq) {
 }
 
 // The 16 KSKA values of slots [s0, s0 + 16) of (seed, digit d, prime p) (crates/pc-core/src/keys.rs:466-498): block
-// s0/16 of the ChaCha12 stream with state words (counter, d, p, "KSKA"); a rejected word is redrawn from block
-// s0/16 + t N/16 (t = 1..15), the 16th attempt kept as is; value v mod p.
+// s0/16 of the ChaCha12 stream with state words (counter, d, p, tag); a rejected word is redrawn from block
+// s0/16 + t N/16 (t = 1..15), the 16th attempt kept as is; value v mod p. The tag is "KSKA" for switching keys and
+// "ENCA" (with d = the nonce) for an encryption's a (args.cuh:614-617).
 __device__ __forceinline__ void kska16(const uint32_t (&seed)[8], uint32_t s0, uint32_t d, const Expander& ex,
-                                       uint32_t n16, uint32_t (&a)[DS]) {
+                                       uint32_t n16, uint32_t (&a)[DS], uint32_t tag = TAG_KSKA) {
     const uint32_t ctr = s0 >> 4;
     uint32_t o[16];
-    chacha12(seed, ctr, d, ex.p, TAG_KSKA, o);
+    chacha12(seed, ctr, d, ex.p, tag, o);
     uint32_t rej = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) rej |= (uint32_t)(o[j] >= ex.mp) << j;
@@ -44,7 +45,7 @@ __device__ __forceinline__ void kska16(const uint32_t (&seed)[8], uint32_t s0, u
         rej &= rej - 1;
         uint32_t v = 0;
         for (int t = 1; t < KSK_T_MAX; ++t) {
-            v = chacha12_word(seed, ctr + (uint32_t)t * n16, d, ex.p, TAG_KSKA, j);
+            v = chacha12_word(seed, ctr + (uint32_t)t * n16, d, ex.p, tag, j);
             if (v < ex.mp) break;
         }
 #pragma unroll
@@ -730,6 +731,44 @@ int ksk_expand(const KskExpandArgs* a, pc_stream_t s) {
     return launch_rc();
 }
 
+// ------------------------------------------------------------------------------------------------ encryption
+// Secret-key encryption in the evaluation domain, limb l = prime id l (args.cuh:613-628; encrypt.cuh:10-31): a from the
+// "ENCA" expander lane (w13 = nonce), c0 = e + m - a s, c1 = a when c1 is set. One ChaCha block per lane; e (and m) may
+// alias c0: a lane reads its 16 words before it writes them.
+__global__ void __launch_bounds__(DBX) encrypt_k(EncryptArgs A, int logn) {
+    const int l = blockIdx.y;
+    const Red red(A.pr[l]);
+    const Expander ex(red.p);
+    uint32_t seed[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) seed[i] = A.seed[i];
+    const uint32_t s0 = blockIdx.x * DCH + threadIdx.x * DS;
+    uint32_t a[DS];
+    kska16(seed, s0, A.nonce, ex, (1u << logn) >> 4, a, TAG_ENCA);
+    const size_t off = ((size_t)l << logn) + s0;
+    uint32_t sv[DS], e[DS], m[DS];
+    ld16((const uint32_t*)A.s + off, sv);
+    ld16((const uint32_t*)A.e + off, e);
+    if (A.m) {
+        ld16((const uint32_t*)A.m + off, m);
+    } else {
+#pragma unroll
+        for (int j = 0; j < DS; ++j) m[j] = 0;
+    }
+#pragma unroll
+    for (int j = 0; j < DS; ++j) e[j] = subm(addm(e[j], m[j], red.p), red.mul(a[j], sv[j]), red.p);
+    st16((uint32_t*)A.c0 + off, e);
+    if (A.c1) st16((uint32_t*)A.c1 + off, a);
+}
+
+template <int LOGN>
+int encrypt(const EncryptArgs* a, pc_stream_t s) {
+    if (!a || !a->c0 || !a->s || !a->e || !a->seed || !a->pr || a->nl < 0) return -1;
+    if (a->nl == 0) return 0;
+    hipLaunchKernelGGL(encrypt_k, dim3((1 << LOGN) / DCH, a->nl), dim3(DBX), 0, (hipStream_t)s, *a, LOGN);
+    return launch_rc();
+}
+
 // ------------------------------------------------------------------------------------------------ key generation
 // b = e - a s_new + [id < nq and digit_of[id] == d] (P mod q_id) s_old' (s_old' = s_old^2 when sq), a from the KSKA
 // expander; b dense or bit-packed (the little-endian value stream, the guard words past N bits / 32 zeroed).
@@ -834,6 +873,7 @@ int ksk_unpack(const KskUnpackArgs* a, pc_stream_t s) {
     int ks_dot_##L(const KsArgs* a, pc_stream_t s) { return ks::ks_dot<L>(a, s); }                          \
     int ks_dot_key_##L(const KsKeyArgs* a, pc_stream_t s) { return ks::ks_dot_key<L>(a, s); }                \
     int ksk_expand_##L(const KskExpandArgs* a, pc_stream_t s) { return ks::ksk_expand<L>(a, s); }            \
+    int encrypt_##L(const EncryptArgs* a, pc_stream_t s) { return ks::encrypt<L>(a, s); }                     \
     int ksk_gen_##L(const KskGenArgs* a, pc_stream_t s) { return ks::ksk_gen<L>(a, s); }                     \
     int ksk_unpack_##L(const KskUnpackArgs* a, pc_stream_t s) { return ks::ksk_unpack<L>(a, s); }
 PCH_KS_INST(12)

@@ -41,7 +41,8 @@ namespace pch {
     int rescale_fwd_##L(const RescaleNttArgs*, pc_stream_t);         \
     int mod_raise_##L(const ModRaiseArgs*, pc_stream_t);             \
     int small_int_##L(const SmallIntArgs*, pc_stream_t);             \
-    int small_int1_##L(const SmallInt1Args*, pc_stream_t);
+    int small_int1_##L(const SmallInt1Args*, pc_stream_t);           \
+    int encrypt_##L(const EncryptArgs*, pc_stream_t);
 PCH_DECL(12)
 PCH_DECL(13)
 PCH_DECL(14)
@@ -59,7 +60,7 @@ int absent(const A*, pc_stream_t) {
         ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
         absent<PtDotArgs>, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
         md_epilogue_##L, wsum_##L, add_const_##L, mul_table_##L, rescale_coef_##L, rescale_combine_##L,            \
-        automorph_##L, absent<EncodeArgs>, absent<EncryptArgs>, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
+        automorph_##L, absent<EncodeArgs>, encrypt_##L, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
         small_int_##L, absent<SpruExtractArgs>, absent<SpruFftArgs>, absent<SpruScatterArgs>,                 \
         cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>, wsum_k_##L, rescale_combine_to_##L, \
         md_epilogue_to_##L, small_int1_##L, absent<CoeffArgs>, mul_add_##L, rescale_fwd_##L,          \

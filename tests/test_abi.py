@@ -190,3 +190,10 @@ def test_raise_launchers_reject_out_of_range_arguments():
     assert abi.call("small_int1", s1, log_n=12) == -1    # shift 0
     s1.sh, s1.nrows = 3, 65
     assert abi.call("small_int1", s1, log_n=12) == -1    # past 64 rows
+
+
+def test_encrypt_launcher_rejects_null_operands():
+    from perseus_amd import abi
+    a = abi.EncryptArgs()
+    a.nl = 2
+    assert abi.call("encrypt", a, log_n=12) == -1

@@ -446,3 +446,30 @@ def test_rescale_fwd(stream, name, fold):
     run("rescale_fwd", a, stream, ch.logn)
     got = x.get()
     assert (got[:, :, : top - 1] == want).all()
+
+
+# ----------------------------------------------------------------------------------------------- encryption
+@pytest.mark.parametrize("name,with_m,with_c1,alias_e", [("small31", True, True, False), ("rej", False, True, True),
+                                                        ("small", True, False, True), ("c3", False, True, True)])
+def test_encrypt(stream, name, with_m, with_c1, alias_e):
+    say(f"[encrypt] {name} m={with_m} c1={with_c1} e_in_c0={alias_e}")
+    ch, ctx, _ = contexts(name)
+    rng = np.random.default_rng(len(name) + 2 * with_m + with_c1)
+    nl, n = len(ch.q), ch.n
+    rows = lambda: np.stack([rng.integers(0, ch.primes[r], n) for r in range(nl)]).astype(np.uint32)  # noqa: E731
+    s, e, m = rows(), rows(), rows()
+    seed = [int(v) for v in rng.integers(0, 1 << 32, 8, dtype=np.uint64)]
+    nonce = 12345
+    a_rows = np.stack([twin.expand_row(seed, nonce, ch.primes[r], n, twin.TAG_ENCA) for r in range(nl)])
+    want = em.encrypt(ch.primes, a_rows, s, e, m if with_m else None)
+    bs, bm, bseed = pa.DevBuf.from_array(s), pa.DevBuf.from_array(m), pa.DevBuf.from_array(np.array(seed, np.uint32))
+    c0 = pa.DevBuf.from_array(e if alias_e else np.zeros_like(e))
+    be = c0 if alias_e else pa.DevBuf.from_array(e)
+    c1 = pa.DevBuf(nl * n)
+    a = abi.EncryptArgs()
+    a.c0, a.c1, a.s, a.e = c0.ptr.value, c1.ptr.value if with_c1 else None, bs.ptr.value, be.ptr.value
+    a.m, a.seed, a.pr, a.nonce, a.nl = bm.ptr.value if with_m else None, bseed.ptr.value, pr_of(ctx), nonce, nl
+    run("encrypt", a, stream, ch.logn)
+    assert (c0.download((nl, n)) == want).all()
+    if with_c1:
+        assert (c1.download((nl, n)) == a_rows).all()

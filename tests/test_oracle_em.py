@@ -264,3 +264,33 @@ def test_composite_equals_two_single_drops_and_the_fold():
     for r in range(top + 1):
         cx[:, :, r] = (x[:, :, r].astype(np.uint64) * c[r] % int(q[r])).astype(np.uint32)
     assert (em.rescale(ctx, q, x, top, 2, fold=c) == em.rescale(ctx, q, cx, top, 2)).all()
+
+
+# ----------------------------------------------------------------------------------------------- encryption
+def test_enca_lane_is_the_expander_rule():
+    """The "ENCA" lane is the KSKA rule under another tag: with the KSKA tag it is the pinned KSKA row, and each ENCA
+    word is the first accepted ChaCha12 word of (slot / 16 + t N / 16, nonce, p, "ENCA") at slot % 16, mod p."""
+    n = 1 << 10
+    seed = [int(v) for v in RNG.integers(0, 1 << 32, 8, dtype=np.uint64)]
+    for p in (twin.descending_primes(31, 2 * n, 1)[0], 1431658497):  # the second rejects about a third of the words
+        assert (twin.expand_row(seed, 2, p, n, twin.TAG_KSKA) == twin.kska_row(seed, 2, p, n)).all()
+        row = twin.expand_row(seed, 77, p, n, twin.TAG_ENCA)
+        bound = (0xFFFFFFFF // p) * p
+        for s in range(0, n, 7):
+            v = 0
+            for t in range(16):
+                v = int(twin.chacha_block(seed, s // 16 + t * (n // 16), 77, p, twin.TAG_ENCA, 12)[s % 16])
+                if v < bound:
+                    break
+            assert int(row[s]) == v % p
+
+
+def test_encryption_decrypts_to_e_plus_m():
+    n, nl = 1 << 10, 4
+    q = twin.descending_primes(31, 2 * n, nl)
+    seed = [1, 2, 3, 4, 5, 6, 7, 8]
+    a = np.stack([twin.expand_row(seed, 9, p, n, twin.TAG_ENCA) for p in q])
+    s, e, m = (np.stack([RNG.integers(0, p, n) for p in q]).astype(np.uint32) for _ in range(3))
+    c0 = em.encrypt(q, a, s, e, m)
+    assert (addq(c0, mulq(a, s, q), q) == addq(e, m, q)).all()
+    assert (addq(em.encrypt(q, a, s, e), mulq(a, s, q), q) == e).all()

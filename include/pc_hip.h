@@ -728,6 +728,19 @@ int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t 
  * res + j ct_words. */
 int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
                   uint32_t enc, const void* ct, int top, void* res, pc_stream_t s);
+/* The relinearization key s^2 -> s (crates/pc-gpu/src/keygen.rs:150-170): one key of galois 1 generated as
+ * pcx_keys_generate's, its old secret squared in the kernel (KskGenArgs.sq). */
+pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed, const int64_t* errors, int bits,
+                         int* err);
+/* Rescale by the top ndrop (1 or 2) primes (crates/pc-gpu/src/rescale.rs:318-440 Rescaler::rescale): out's Q rows
+ * 0..top - ndrop = the rescale of ct's rows 0..top, both parts in the evaluation domain, the same words as dropping
+ * the primes one at a time; out's rows above are scratch. Two primes run the table's rescale_fwd (the corrections
+ * generated in the forward NTT), one prime rescale_coef and the NTT. out may be ct. */
+int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_stream_t s);
+/* The relinearized product (crates/pc-gpu/src/relin.rs:248-272 mult): the tensor (c0, c1, d2), then d2 key-switched
+ * by key 0 of k (the relinearization key: galois 1) and added: out = (c0, c1) + ModDown(dot(ModUp(d2))) on Q rows
+ * 0..top (degree 2, rescale pending). out may be a or b. */
+int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);
 /* the stages alone, for tests and profiles: ModUp of ct's c1 into the context's digit workspace; the dot of key r
  * into ext (one extended ciphertext); ModDown of ext into out */
 int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);
@@ -737,7 +750,8 @@ int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s);
 
 /* Stage timing, for measurement: while on, the driver records a HIP event pair on the launch stream around each
  * stage it enqueues (0 ModUp INTT, 1 ModUp conversion, 2 ModUp NTT, 3 key dot, 4 ModDown INTT, 5 ModDown conversion,
- * 6 ModDown NTT + epilogue, 7 CtS baby steps and plaintext products). pcx_timing(c, n) turns it on for up to n stages
+ * 6 ModDown NTT + epilogue, 7 CtS baby steps and plaintext products, 8 tensor, 9 rescale). pcx_timing(c, n) turns it
+ * on for up to n stages
  * (resetting the record); 0 turns it off. pcx_timing_read sums the device time of one stage after the stream has
  * synchronised. No counterpart in the reference (its benches time with CUDA events around whole ops,
  * crates/pc-gpu/benches/ks.rs:80-98). */

@@ -204,6 +204,14 @@ struct Level {
     std::vector<Rows> md_intt;
     Bconv md_bconv;           // [c][part]: P -> Q rows 0..top (a prefix per m)
     std::vector<Rows> md_ntt;
+    // the rescale from this top by one prime (index 0) or two (index 1; crates/pc-gpu/src/rescale.rs:118-160): the
+    // tops' INTT rows of one ciphertext, the correction rows' NTT list (tmp rows 0..top - ndrop, both parts,
+    // prime-major) and the per-prime-id constants [A | As | B | Bs | alpha | alphas | qam | qbm] (rows words each)
+    struct Rescale {
+        Rows intt, ntt;
+        uint32_t* k = nullptr;
+        uint64_t qinv_ab = 0, C_ab = 0;
+    } rs[2];
 };
 
 }  // namespace
@@ -230,6 +238,7 @@ struct pcx_ctx {
     int32_t* digit_of = nullptr;
     std::vector<Level> levels;
     uint32_t *coef = nullptr, *digits = nullptr, *ext = nullptr, *conv = nullptr;
+    uint32_t* tmp = nullptr;  // one ciphertext: the rescale's correction rows, a product's d2 (part 1)
     size_t ws_bytes = 0;
     // stage timing (pcx_timing): event pairs recorded around each stage's launches on the launch stream
     bool timing = false;
@@ -411,6 +420,59 @@ int build_level(pcx_ctx* c, int top, Level& L) {
             if (int e = fill_rows(c->dev, L.md_ntt[m - 1], roff2, rp2, nullptr, nullptr)) return e;
         }
     }
+    // rescale by one or two primes: qlql[l][i] = -q_l^-1 mod q_i, qinv[l][i] = q_l^-1 mod q_i
+    // (crates/pc-core/src/scale.rs:196-208); ndrop 1: A_i = qlql[a][i], alpha_i = qinv[a][i]; ndrop 2 (a = top,
+    // b = top - 1): A_i = qinv[b][i] qlql[a][i], B_i = qlql[b][i], alpha_i = qinv[b][i] qinv[a][i]
+    for (int g = 1; g <= 2; ++g) {
+        if (top < g) continue;
+        Level::Rescale& Z = L.rs[g - 1];
+        const int a = top, b = top - 1, R = c->rows;
+        auto qinv = [&](int l, int i) { return invmod(c->primes[l] % c->primes[i], c->primes[i]); };
+        auto qlql = [&](int l, int i) {
+            const uint64_t v = qinv(l, i);
+            return v ? c->primes[i] - v : 0;
+        };
+        std::vector<uint32_t> k((size_t)8 * R, 0);
+        for (int i = 0; i + g <= top; ++i) {
+            const uint64_t qi = c->primes[i];
+            uint64_t A, B = 0, al;
+            if (g == 1) {
+                A = qlql(a, i);
+                al = qinv(a, i);
+            } else {
+                A = mulmod(qinv(b, i), qlql(a, i), qi);
+                B = qlql(b, i);
+                al = mulmod(qinv(b, i), qinv(a, i), qi);
+            }
+            k[0 * R + i] = (uint32_t)A;
+            k[1 * R + i] = shoup_c((uint32_t)A, (uint32_t)qi);
+            k[2 * R + i] = (uint32_t)B;
+            k[3 * R + i] = shoup_c((uint32_t)B, (uint32_t)qi);
+            k[4 * R + i] = (uint32_t)al;
+            k[5 * R + i] = shoup_c((uint32_t)al, (uint32_t)qi);
+            k[6 * R + i] = (uint32_t)(c->primes[a] % qi);
+            k[7 * R + i] = (uint32_t)(c->primes[b] % qi);
+        }
+        if (g == 2) {
+            Z.qinv_ab = qinv(a, b);
+            Z.C_ab = qlql(a, b);
+        }
+        Z.k = c->dev.upload(k);
+        std::vector<uint32_t> roff, roff2;
+        std::vector<int32_t> rp, rp2;
+        for (int t = top + 1 - g; t <= top; ++t)
+            for (int part = 0; part < 2; ++part) {
+                roff.push_back((uint32_t)(part * R + t));
+                rp.push_back(t);
+            }
+        for (int t = 0; t + g <= top; ++t)
+            for (int part = 0; part < 2; ++part) {
+                roff2.push_back((uint32_t)(part * R + t));
+                rp2.push_back(t);
+            }
+        if (int e = fill_rows(c->dev, Z.intt, roff, rp, nullptr, nullptr)) return e;
+        if (int e = fill_rows(c->dev, Z.ntt, roff2, rp2, nullptr, nullptr)) return e;
+    }
     return c->dev.err;
 }
 
@@ -475,7 +537,8 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
 
 // the dot of keys [r0, r0 + m) of k into m extended ciphertexts at ext (crates/pc-gpu/src/ks.rs:1225-1308 dot_key);
 // sum: 1 sums the m rotations into ext's first ciphertext (KS_SUM), 2 adds that sum onto it (KS_SUM | KS_ACC)
-int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0) {
+int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0,
+        int c0_mode = 1) {
     const Level* L = level(c, top);
     if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys) return -1;
     KsKeyArgs g;
@@ -503,7 +566,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     a.K = 1;
     a.R = m;
     a.ndig = L->ndig;
-    a.c0_mode = 1 | (sum ? PC_KS_SUM : 0) | (sum == 2 ? PC_KS_ACC : 0);
+    a.c0_mode = c0_mode | (sum ? PC_KS_SUM : 0) | (sum == 2 ? PC_KS_ACC : 0);
     a.nq = c->nq;
     a.nrows = L->nks;
     KeyTab& t = g.key;
@@ -834,7 +897,8 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     c->digits = (uint32_t*)c->dev.alloc((size_t)dnum * R * rw);
     c->ext = (uint32_t*)c->dev.alloc((size_t)k_rot * 2 * R * rw);
     c->conv = (uint32_t*)c->dev.alloc((size_t)k_rot * 2 * R * rw);
-    c->ws_bytes = nq * rw + (size_t)dnum * R * rw + 2 * (size_t)k_rot * 2 * R * rw;
+    c->tmp = (uint32_t*)c->dev.alloc((size_t)2 * R * rw);
+    c->ws_bytes = nq * rw + (size_t)dnum * R * rw + 2 * (size_t)k_rot * 2 * R * rw + (size_t)2 * R * rw;
     if (c->dev.err) {
         *err = c->dev.err;
         delete c;
@@ -966,9 +1030,10 @@ pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint
 }
 
 // crates/pc-gpu/src/keygen.rs:172-262: the secret's eval rows, per key the Gaussian errors NTT'd, s_new =
-// sigma_{g^-1}(s) by the automorph kernel, then ksk_gen (b dense or packed)
-pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret,
-                            const uint32_t* seeds, const int64_t* errors, int bits, int* err) {
+// sigma_{g^-1}(s) by the automorph kernel, then ksk_gen (b dense or packed); sq: the old secret squared in the kernel
+// (the relinearization key s^2 -> s, galois 1; keygen.rs:150-170)
+static pcx_keys* keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret, const uint32_t* seeds,
+                        const int64_t* errors, int bits, int sq, int* err) {
     int dummy;
     if (!err) err = &dummy;
     *err = 0;
@@ -1061,7 +1126,7 @@ pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const
         g.ndig = c->dnum;
         g.nq = c->nq;
         g.bits = bits;
-        g.sq = 0;
+        g.sq = sq;
         if ((rc = c->tab->ksk_gen(&g, s))) break;
         if (hipDeviceSynchronize() != hipSuccess) rc = -1;
     }
@@ -1078,6 +1143,17 @@ pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const
         return nullptr;
     }
     return k;
+}
+
+pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret,
+                            const uint32_t* seeds, const int64_t* errors, int bits, int* err) {
+    return keys_generate(c, nkeys, galois, secret, seeds, errors, bits, 0, err);
+}
+
+pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed, const int64_t* errors, int bits,
+                         int* err) {
+    const uint64_t one = 1;
+    return keys_generate(c, 1, &one, secret, seed, errors, bits, 1, err);
 }
 
 void pcx_keys_free(pcx_keys* k) { delete k; }
@@ -1275,6 +1351,82 @@ int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t 
         i0 += n;
     }
     return 0;
+}
+
+
+// Rescale by the top ndrop (1 or 2) primes (crates/pc-gpu/src/rescale.rs:318-440): out's rows 0..top - ndrop become
+// the rescale of ct's rows 0..top (both parts, eval form); out's rows above are left as scratch. Two primes: INTT of
+// the tops, rescale_fwd (the corrections generated in the forward NTT's column pass, out = alpha out + NTT(tmp) in its
+// epilogue); one prime: INTT of the top, rescale_coef, the NTT of the corrections with the same epilogue.
+int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_stream_t s) {
+    if (!c || !ct || !out || (ndrop != 1 && ndrop != 2) || top < ndrop || top >= c->nq) return -1;
+    const Level::Rescale& Z = c->levels[top].rs[ndrop - 1];
+    const int R = c->rows;
+    Stage st(c, 9, s);
+    if (ct != out)
+        if (int e = copy_q(c, ct, top, out, s)) return e;
+    NttArgs in = ntt_args(c, out, Z.intt, Z.intt.n);
+    if (int e = c->tab->ntt_inv(&in, s)) return e;
+    RescaleArgs r;
+    memset(&r, 0, sizeof r);
+    const uint64_t part = (uint64_t)R * c->n;
+    r.x = PolyRef{out, 2 * part, part};
+    r.tmp = PolyRef{c->tmp, 2 * part, part};
+    r.A = Z.k;
+    r.As = Z.k + R;
+    r.B = Z.k + 2 * R;
+    r.Bs = Z.k + 3 * R;
+    r.qam = Z.k + 6 * R;
+    r.qbm = Z.k + 7 * R;
+    r.pr = c->pr;
+    r.qinv_ab = Z.qinv_ab;
+    r.C_ab = Z.C_ab;
+    r.ca = r.cb = 1;
+    r.top = top;
+    r.nrows = top + 1 - ndrop;
+    r.K = 1;
+    r.ndrop = ndrop;
+    NttArgs f = ntt_args(c, c->tmp, Z.ntt, Z.ntt.n);
+    f.epi = 3;
+    f.eout = out;
+    f.ex = out;
+    f.xnum = 1;
+    f.es = Z.k + 4 * R;
+    f.ess = Z.k + 5 * R;
+    if (ndrop == 2) {
+        RescaleNttArgs a;
+        a.rs = r;
+        a.ntt = f;
+        return c->tab->rescale_fwd(&a, s);
+    }
+    if (int e = c->tab->rescale_coef(&r, s)) return e;
+    return c->tab->ntt_fwd(&f, s);
+}
+
+// The relinearized product (crates/pc-gpu/src/relin.rs:248-272 mult, Cached-key form :120-130): (c0, c1, d2) by the
+// tensor kernel (d2 into part 1 of the context's tmp ciphertext), ModUp(d2), the key inner product with the
+// relinearization key (no c0 term, no automorphism), and the ModDown added onto (c0, c1): out = (c0, c1) +
+// (ext - conv) P^-1 on Q rows 0..top. out may be a or b.
+int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
+    if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    TensorArgs t;
+    memset(&t, 0, sizeof t);
+    t.out = PolyRef{out, 2 * part, part};
+    t.d2 = PolyRef{c->tmp, 2 * part, part};
+    t.a0 = t.a1 = PolyRef{const_cast<void*>(a), 2 * part, part};
+    t.b0 = t.b1 = PolyRef{const_cast<void*>(b), 2 * part, part};
+    t.pr = c->pr;
+    t.npairs = 1;
+    t.n = top + 1;
+    t.K = 1;
+    {
+        Stage st(c, 8, s);
+        if (int e = c->tab->tensor(&t, s)) return e;
+    }
+    if (int e = modup(c, c->tmp, top, s)) return e;
+    if (int e = dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, 0)) return e;
+    return moddown(c, c->ext, c->conv, 1, top, out, s, out);
 }
 
 }  // extern "C"

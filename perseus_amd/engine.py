@@ -149,7 +149,8 @@ class Context:
     def moddown(self, ext, top, out, stream):
         check(LIB.pcx_moddown(self.h, ext.addr(), top, out.addr(), stream.h), "moddown")
 
-    STAGES = ("modup_intt", "modup_bconv", "modup_ntt", "dot", "md_intt", "md_bconv", "md_ntt", "cts")
+    STAGES = ("modup_intt", "modup_bconv", "modup_ntt", "dot", "md_intt", "md_bconv", "md_ntt", "cts", "tensor",
+              "rescale")
 
     def timing(self, max_stages):
         """Record device time per stage (0 turns it off)."""
@@ -183,6 +184,14 @@ class Context:
         check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(), tmp.addr(),
                                      stream.h), "rotate_and_sum")
 
+    def rescale(self, ct, top, ndrop, out, stream):
+        """out's rows 0..top - ndrop = the rescale of ct by its top ndrop (1 or 2) primes (pcx_rescale)."""
+        check(LIB.pcx_rescale(self.h, ct.addr(), top, ndrop, out.addr(), stream.h), "rescale")
+
+    def mul_relin(self, keys, a, b, top, out, stream):
+        """out = a b relinearized by key 0 of keys (pcx_mul_relin)."""
+        check(LIB.pcx_mul_relin(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h), "mul_relin")
+
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}
         in the extended basis, babies i >= 1 by keys r0 + i - 1. pts: a DevBuf holding npts device pointers (uint64)
@@ -192,9 +201,10 @@ class Context:
 
 
 class Keys:
-    """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed."""
+    """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed. relin:
+    the relinearization key s^2 -> s (galois 1, generated from secret / errors)."""
 
-    def __init__(self, ctx: Context, galois, seeds=None, b=None, bits=0, secret=None, errors=None):
+    def __init__(self, ctx: Context, galois, seeds=None, b=None, bits=0, secret=None, errors=None, relin=False):
         self.ctx = ctx
         self.galois = [int(g) for g in galois]
         n = len(self.galois)
@@ -202,7 +212,15 @@ class Keys:
         seeds = np.ascontiguousarray(seeds, np.uint32).reshape(n, 8)
         sp = seeds.ctypes.data_as(C.POINTER(C.c_uint32))
         self._keep = [seeds]
-        if b is not None:
+        if relin:
+            if self.galois != [1] or secret is None:
+                raise ValueError("the relinearization key is one key of galois 1 generated from the secret")
+            s = np.ascontiguousarray(secret, np.int8)
+            e = np.ascontiguousarray(errors, np.int64).reshape(1, ctx.dnum, ctx.n)
+            self._keep += [s, e]
+            self.h = LIB.pcx_keys_relin(ctx.h, s.ctypes.data_as(C.POINTER(C.c_int8)), sp,
+                                        e.ctypes.data_as(C.POINTER(C.c_int64)), bits, C.byref(err))
+        elif b is not None:
             bs = [np.ascontiguousarray(x, np.uint32) for x in b]
             self._keep += bs
             ptrs = (C.c_void_p * n)(*[x.ctypes.data for x in bs])

@@ -1,0 +1,137 @@
+"""Parity of the driver's composite operations with the oracle, word for word: the relinearization key (keygen with the
+old secret squared), the relinearized product pcx_mul_relin (tensor, ModUp of d2, key dot, ModDown onto (c0, c1))
+and the rescale pcx_rescale by one or two primes. The oracle composes its pinned pieces (tests/twin.py mul_relin,
+rescale; pinned end to end by tests/test_oracle_em.py's decryption test). Each test prints its case before the GPU
+runs.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import perseus_amd as pa
+from tests import twin
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def stream():
+    assert pa.device_count() >= 1, "no GPU visible"
+    return pa.Stream()
+
+
+_CTX = {}
+
+
+def contexts(name):
+    if name not in _CTX:
+        ch = pa.preset(name)
+        _CTX[name] = (ch, pa.Context(ch, k_rot=2), twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum))
+    return _CTX[name]
+
+
+_KEYS = {}
+
+
+def relin_key(name, bits=0):
+    """the relinearization key on the device, and its b and seed for the oracle"""
+    if (name, bits) not in _KEYS:
+        ch, ctx, oc = contexts(name)
+        g = twin.Prng([1, 4, 1, 4, 2, 1, 3, 5], 0)
+        s = g.sparse_ternary(ch.n, 192)
+        seed = g.ksk_seed()
+        errs = np.stack([g.gaussian(ch.n) for _ in range(ch.dnum)])
+        keys = pa.Keys(ctx, [1], seeds=seed[None], bits=bits, secret=s, errors=errs[None], relin=True)
+        _KEYS[(name, bits)] = (keys, s, seed, errs)
+    return _KEYS[(name, bits)]
+
+
+def random_ct(ch, top, rng):
+    x = np.zeros((2, ch.rows, ch.n), np.uint32)
+    for t in range(top + 1):
+        x[:, t] = rng.integers(0, ch.primes[t], (2, ch.n))
+    return x
+
+
+@pytest.mark.parametrize("name,bits", [("small", 0), ("small31", 31)])
+def test_relin_keygen(stream, name, bits):
+    say(f"[relin keygen] {name} bits={bits}")
+    ch, ctx, oc = contexts(name)
+    keys, s, seed, errs = relin_key(name, bits)
+    s_eval = oc.secret_eval(s)
+    s2 = np.stack([(s_eval[t].astype(np.uint64) ** 2 % ch.primes[t]) for t in range(ch.rows)]).astype(np.uint32)
+    e = np.zeros((ch.dnum, ch.rows, ch.n), np.uint32)
+    for d in range(ch.dnum):
+        for t in range(ch.rows):
+            e[d, t] = np.mod(errs[d], ch.primes[t])
+    e = oc.ntt_fwd(e.reshape(-1, ch.n), [t for _ in range(ch.dnum) for t in range(ch.rows)]).reshape(e.shape)
+    assert (keys.download_b(0) == oc.ksk_gen(s_eval, s2, seed, e)).all()
+
+
+@pytest.mark.parametrize("name,top,alias", [("small", 5, False), ("small", 3, True), ("small31", 5, False),
+                                            ("c3", 29, False), ("c3", 17, True)])
+def test_mul_relin(stream, name, top, alias):
+    say(f"[mul_relin] {name} top={top} out=a:{alias}")
+    ch, ctx, oc = contexts(name)
+    keys, _, seed, _ = relin_key(name)
+    rng = np.random.default_rng(top * 7 + alias)
+    a, b = random_ct(ch, top, rng), random_ct(ch, top, rng)
+    want = oc.mul_relin(a, b, top, seed, keys.download_b(0))
+    ba, bb = pa.DevBuf.from_array(a), pa.DevBuf.from_array(b)
+    out = ba if alias else ctx.ct_buf(1)
+    ctx.mul_relin(keys, ba, bb, top, out, stream)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    assert (got[:, : top + 1] == want[:, : top + 1]).all()
+
+
+@pytest.mark.parametrize("name,top,ndrop,inplace", [("small", 5, 2, False), ("small", 4, 1, True),
+                                                    ("small31", 5, 1, False), ("small31", 3, 2, True),
+                                                    ("c3", 29, 2, False), ("c3", 28, 1, False)])
+def test_rescale(stream, name, top, ndrop, inplace):
+    say(f"[rescale] {name} top={top} ndrop={ndrop} inplace={inplace}")
+    ch, ctx, oc = contexts(name)
+    rng = np.random.default_rng(top * 3 + ndrop)
+    x = random_ct(ch, top, rng)
+    want = oc.rescale(x, top, ndrop)
+    bx = pa.DevBuf.from_array(x)
+    out = bx if inplace else ctx.ct_buf(1)
+    ctx.rescale(bx, top, ndrop, out, stream)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    rows = top + 1 - ndrop
+    assert (got[:, :rows] == want[:, :rows]).all()
+    if not inplace:
+        assert (bx.download((2, ch.rows, ch.n)) == x).all(), "the source is read only"
+
+
+def test_mul_relin_rescale_decrypts(stream):
+    """The device chain encrypt -> mul_relin -> rescale decrypts to the product of the messages divided by the two
+    dropped primes (the oracle's decryption test, on the GPU's words)."""
+    say("[mul_relin + rescale] small decrypt")
+    from tests.test_oracle_em import crt_centred, negacyclic
+    from tests.test_oracle_ks import decrypt, encrypt
+    ch, ctx, oc = contexts("small")
+    keys, s, _, _ = relin_key("small")
+    s_eval = oc.secret_eval(s)
+    rng = np.random.default_rng(11)
+    top = 5
+    delta = 1 << 30
+    ma, mb = np.zeros(ch.n, np.int64), rng.integers(-50, 50, ch.n) * delta
+    ma[rng.choice(ch.n, 48, replace=False)] = rng.integers(-50, 50, 48) * delta  # sparse: the check's product is cheap
+    ca, _ = encrypt(oc, s_eval, ma, rng, top)
+    cb, _ = encrypt(oc, s_eval, mb, rng, top)
+    ba, bb, out = pa.DevBuf.from_array(ca), pa.DevBuf.from_array(cb), ctx.ct_buf(1)
+    ctx.mul_relin(keys, ba, bb, top, out, stream)
+    ctx.rescale(out, top, 2, out, stream)
+    stream.sync()
+    got = crt_centred(decrypt(oc, s_eval, out.download((2, ch.rows, ch.n)), top - 2), ch.primes[: top - 1])
+    div = int(ch.primes[top]) * int(ch.primes[top - 1])
+    prod = negacyclic(ma, mb)
+    assert max(abs(x - round(y / div)) for x, y in zip(got, prod)) < 1 << 8

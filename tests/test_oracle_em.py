@@ -294,3 +294,71 @@ def test_encryption_decrypts_to_e_plus_m():
     c0 = em.encrypt(q, a, s, e, m)
     assert (addq(c0, mulq(a, s, q), q) == addq(e, m, q)).all()
     assert (addq(em.encrypt(q, a, s, e), mulq(a, s, q), q) == e).all()
+
+
+# ----------------------------------------------------------------------------------------------- relinearized product
+def crt_centred(rows, q):
+    """the centred integers of coefficient rows [k][N] over the primes q"""
+    big = 1
+    for p in q:
+        big *= int(p)
+    vals = crt_values(q, rows)
+    return [v - big if v > big // 2 else v for v in vals]
+
+
+def negacyclic(a, b):
+    n = len(a)
+    out = [0] * n
+    for i in range(n):
+        ai = int(a[i])
+        if ai == 0:
+            continue
+        for j in range(n):
+            v = ai * int(b[j])
+            if i + j < n:
+                out[i + j] += v
+            else:
+                out[i + j - n] -= v
+    return out
+
+
+def test_mul_relin_then_rescale_decrypts_to_the_product():
+    """Dec(mul_relin(ct_a, ct_b)) = m_a m_b (negacyclic, exact integers over Q) up to the encryption noise times the
+    messages, with the relinearization key b = e - a s + P s^2 (ksk_gen with s_old = s^2); after a two-prime rescale
+    the decryption is m_a m_b / (q_a q_b) up to a few units."""
+    from tests.test_oracle_ks import decrypt, encrypt
+    ctx = small_chain(logn=8, nq=6, kp=2, dnum=3, bits=30)
+    top, n = 5, ctx.n
+    g = twin.Prng([2, 7, 1, 8, 2, 8, 1, 8], 0)
+    s_eval = ctx.secret_eval(g.sparse_ternary(n, 64))
+    s2 = np.stack([(s_eval[t].astype(np.uint64) ** 2 % ctx.primes[t]) for t in range(ctx.rows)]).astype(np.uint32)
+    seed = g.ksk_seed()
+    e = np.zeros((ctx.dnum, ctx.rows, n), np.uint32)
+    for d in range(ctx.dnum):
+        ed = g.gaussian(n)
+        for t in range(ctx.rows):
+            e[d, t] = np.mod(ed, ctx.primes[t])
+    e = ctx.ntt_fwd(e.reshape(-1, n), [t for _ in range(ctx.dnum) for t in range(ctx.rows)]).reshape(e.shape)
+    bkey = ctx.ksk_gen(s_eval, s2, seed, e)
+    rng = np.random.default_rng(8)
+    delta = 1 << 30
+    ma, mb = rng.integers(-100, 100, n) * delta, rng.integers(-100, 100, n) * delta
+    ca, _ = encrypt(ctx, s_eval, ma, rng, top)
+    cb, _ = encrypt(ctx, s_eval, mb, rng, top)
+    out = ctx.mul_relin(ca, cb, top, seed, bkey)
+    prod = negacyclic(ma, mb)
+    q = ctx.primes[: top + 1]
+    got = crt_centred(decrypt(ctx, s_eval, out, top), q)
+    assert max(abs(x - y) for x, y in zip(got, prod)) < delta << 20  # the product is ~ delta^2 2^20
+    # without the relinearization term the decryption is far off (the key switch carries d2 s^2)
+    plain = ctx.ct_zeros()
+    from oracle import em as em_
+    c0, c1, _ = em_.tensor(ctx.primes, [(ca[None, :, : top + 1], cb[None, :, : top + 1])])
+    plain[0, : top + 1], plain[1, : top + 1] = c0[0], c1[0]
+    bad = crt_centred(decrypt(ctx, s_eval, plain, top), q)
+    assert max(abs(x - y) for x, y in zip(bad, prod)) > delta << 40
+    # the rescale by the two top primes divides by q_4 q_5
+    rs = ctx.rescale(out, top, 2)
+    got = crt_centred(decrypt(ctx, s_eval, rs, top - 2), ctx.primes[: top - 1])
+    div = int(ctx.primes[top]) * int(ctx.primes[top - 1])
+    assert max(abs(x - round(y / div)) for x, y in zip(got, prod)) < 1 << 8

@@ -213,6 +213,29 @@ class Ctx:
         LIB.or_moddown(self.h, np.ascontiguousarray(ext, np.uint32), top, out)
         return out
 
+    def mul_relin(self, a, b, top, seed, bkey):
+        """The relinearized product (crates/pc-gpu/src/relin.rs:248-272) composed from the oracle's pieces: the tensor
+        (oracle/em.py), ModUp(d2), the key dot with no c0 term and no automorphism, ModDown added onto (c0, c1)."""
+        from oracle import em
+        n = top + 1
+        c0, c1, d2 = em.tensor(self.primes, [(a[None, :, :n], b[None, :, :n])])
+        tmp = self.ct_zeros()
+        tmp[1, :n] = d2[0]
+        ext = self.ks_dot(tmp, self.modup(tmp[1], top), top, seed, bkey, 1)
+        md = self.moddown(ext, top)
+        out = self.ct_zeros()
+        q = np.asarray(self.primes[:n], np.uint64).reshape(n, 1)
+        out[0, :n] = ((c0[0].astype(np.uint64) + md[0, :n]) % q).astype(np.uint32)
+        out[1, :n] = ((c1[0].astype(np.uint64) + md[1, :n]) % q).astype(np.uint32)
+        return out
+
+    def rescale(self, x, top, ndrop):
+        """Rows 0..top - ndrop of the rescale of one ciphertext x [2][rows][N] (oracle/em.py rescale)."""
+        from oracle import em
+        out = self.ct_zeros()
+        out[:, : top + 1 - ndrop] = em.rescale(self, self.primes, x[None, :, : top + 1], top, ndrop)[0]
+        return out
+
     def rotate(self, ct, top, seed, b, g):
         out = self.ct_zeros()
         LIB.or_rotate(self.h, np.ascontiguousarray(ct, np.uint32), top, np.asarray(seed, np.uint32),

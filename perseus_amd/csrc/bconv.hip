@@ -2,7 +2,9 @@
 //   y_i = x_i pre_i mod s_i (prescaled jobs: y_i = x_i as stored), out_t = sum_i y_i M[i][t] mod t;
 //   exact jobs: v = sum_i y_i rb_i (double FMA in source order), u = floor(v + 0.5) (centred: the lift's mean),
 //   out_t -= u (B mod t).
-// One launch for every job of a plan: grid (N / 512, njobs), 256 threads of 2 consecutive coefficients.
+// One launch for every job of a plan: grid (N / 512, njobs, target groups), 256 threads of 2 consecutive
+// coefficients; the job's targets are split over ceil(max_tgt / TPG) groups (each re-reads the job's sources, from
+// L2), so that a few wide jobs still put several waves on every SIMD.
 //
 // 31-bit primes break the reference's lazy bound nsrc (p - 1)^2 < 2^64 past 4 sources, so the sum of products is
 // carried in 96 bits (a 64-bit sum and a count of its wraps) and reduced once: the exact integer formula, whatever
@@ -14,6 +16,7 @@ namespace bconv {
 
 constexpr int BX = 256, V = 2, PER_WG = BX * V;
 constexpr int MAX_REG_SRC = 16;
+constexpr int TPG = 8;  // targets per workgroup when BconvArgs.max_tgt gives the grid its target groups
 
 struct Pool {
     const uint32_t* w;
@@ -50,7 +53,7 @@ __device__ __forceinline__ uint64_t exact_u(const BconvJob& j, const double* rb,
 // read here: jobs of at most 16 sources keep the sources of their 2 coefficients in registers and the job's tables in
 // LDS; wider jobs (bconv_wide, up to 48 sources at u32 words) re-read their sources per target (L1/L2 resident).
 __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
-                                         uint32_t* dst, uint32_t c, int logn) {
+                                         uint32_t* dst, uint32_t c, int logn, int t0, int t1) {
     auto yv = [&](int i) {
         uint32_t v = src[((size_t)P.src_row(i) << logn) + c];
         if (!j.prescaled) v = Red(A.pr[P.src_prime(i)]).mul(v, P.pre(i));
@@ -70,7 +73,7 @@ __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, 
             u = (uint64_t)floor(v + 0.5);
         }
     }
-    for (int t = 0; t < P.nt; ++t) {
+    for (int t = t0; t < t1; ++t) {
         const Red red(A.pr[P.tgt_prime(t)]);
         uint64_t acc = 0;
         uint32_t wraps = 0;
@@ -97,7 +100,7 @@ struct JobLds {
 };
 
 __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
-                                        const uint32_t* src, uint32_t* dst, uint32_t c0, int logn) {
+                                        const uint32_t* src, uint32_t* dst, uint32_t c0, int logn, int ntl) {
     uint32_t y[MAX_REG_SRC * V];
 #pragma unroll
     for (int i = 0; i < MAX_REG_SRC; ++i) {
@@ -134,7 +137,7 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
         }
     }
     const int ng = (P.ns + 3) >> 2;  // groups of 4 sources (M zero-padded)
-    for (int t = 0; t < P.nt; ++t) {
+    for (int t = 0; t < ntl; ++t) {
         const Red red(S.tc[t][0], S.tc[t][1], S.tc[t][2], S.tc[t][3]);
         uint64_t acc[V] = {0, 0};
         uint32_t wraps[V] = {0, 0};
@@ -170,16 +173,21 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
     const Pool P{(const uint32_t*)A.pool + j.pool_off, (int)j.nsrc, (int)j.ntgt};
     const uint32_t c0 = blockIdx.x * PER_WG + threadIdx.x * V;
     if (P.ns < 1) return;
+    // this workgroup's targets [t0, t0 + ntl): the job's targets split evenly over the grid's target groups
+    const int tpg = (P.nt + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int t0 = (int)blockIdx.z * tpg;
+    const int ntl = P.nt - t0 < tpg ? P.nt - t0 : tpg;
+    if (ntl <= 0) return;
     const uint32_t* src = (const uint32_t*)A.src + ((size_t)j.src_off << logn);
     uint32_t* dst = (uint32_t*)A.dst + ((size_t)j.dst_off << logn);
-    if (P.ns <= MAX_REG_SRC && P.nt <= MAXT) {
+    if (P.ns <= MAX_REG_SRC && ntl <= MAXT) {
         for (int e = threadIdx.x; e < MAXT * MAX_REG_SRC; e += BX) {
             const int t = e / MAX_REG_SRC, i = e % MAX_REG_SRC;
-            S.mt[t][i] = (t < P.nt && i < P.ns) ? P.m(i, t) : 0;
+            S.mt[t][i] = (t < ntl && i < P.ns) ? P.m(i, t0 + t) : 0;
         }
-        for (int t = threadIdx.x; t < P.nt; t += BX) {
-            const PrimeConst& q = A.pr[P.tgt_prime(t)];
-            S.trow[t] = P.tgt_row(t);
+        for (int t = threadIdx.x; t < ntl; t += BX) {
+            const PrimeConst& q = A.pr[P.tgt_prime(t0 + t)];
+            S.trow[t] = P.tgt_row(t0 + t);
             S.tc[t][0] = (uint32_t)q.p;
             S.tc[t][1] = (uint32_t)q.split;
             S.tc[t][2] = (uint32_t)(q.split >> 32);
@@ -189,12 +197,12 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             const double* rb = exact_rb((const uint32_t*)A.pool, j);
             const uint32_t* bmod = (const uint32_t*)(rb + j.nsrc);
             for (int i = threadIdx.x; i < P.ns; i += BX) S.rb[i] = rb[i];
-            for (int t = threadIdx.x; t < P.nt; t += BX) S.bmod[t] = bmod[t];
+            for (int t = threadIdx.x; t < ntl; t += BX) S.bmod[t] = bmod[t0 + t];
         }
         __syncthreads();
-        if (c0 < (1u << logn)) job_lds(A, j, P, S, src, dst, c0, logn);
+        if (c0 < (1u << logn)) job_lds(A, j, P, S, src, dst, c0, logn, ntl);
     } else if (c0 < (1u << logn)) {
-        for (int k = 0; k < V; ++k) job_wide(A, j, P, src, dst, c0 + k, logn);
+        for (int k = 0; k < V; ++k) job_wide(A, j, P, src, dst, c0 + k, logn, t0, t0 + ntl);
     }
 }
 
@@ -208,7 +216,9 @@ int launch(const BconvArgs* a, pc_stream_t s) {
     if (int rc = check(a)) return rc;
     if (a->njobs == 0) return 0;
     const int gx = ((1 << LOGN) + PER_WG - 1) / PER_WG;
-    hipLaunchKernelGGL(bconv_k, dim3(gx, a->njobs), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    // target groups: every job's targets fit max_tgt (the plan's widest job; 0: one group)
+    const int gz = a->max_tgt > TPG ? std::min((a->max_tgt + TPG - 1) / TPG, 256) : 1;
+    hipLaunchKernelGGL(bconv_k, dim3(gx, a->njobs, gz), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
     return launch_rc();
 }
 

@@ -15,6 +15,8 @@
 // depend only on the high bits of i, so the chunk's 1024 slots land in one aligned 1024-slot chunk of the output,
 // permuted; the permutation goes through LDS and the stores stay coalesced.
 #include "common.h"
+#include <type_traits>
+
 #include "fused.h"
 
 namespace pch {
@@ -308,14 +310,21 @@ constexpr int FQCAP = DCH;  // queue entries per wave
 constexpr int PADW = DCH + DCH / 4;
 __device__ __forceinline__ int padw(int i) { return i + (i >> 4) * 4; }
 
+struct FastWave {
+    uint32_t buf[DCH];  // scatter buffer
+    uint32_t q[FQCAP];  // rejected words: (digit << 16 | slot), then the redrawn value
+    uint32_t qn;
+};
+// KW waves (one key each) share the chunk's D and c0 staged in LDS; a launch with fewer keys than KW runs one-wave
+// workgroups that read D and c0 straight from memory (their LDS holds the wave's buffers only), so the chip keeps
+// enough waves in flight on a single key
 struct FastLds {
     uint32_t D[MAXD][PADW];
     uint32_t c0[PADW];
-    struct Wave {
-        uint32_t buf[DCH];  // scatter buffer
-        uint32_t q[FQCAP];  // rejected words: (digit << 16 | slot), then the redrawn value
-        uint32_t qn;
-    } w[KW];
+    FastWave w[KW];
+};
+struct FastLds1 {
+    FastWave w[1];
 };
 
 
@@ -329,8 +338,9 @@ __device__ __forceinline__ uint32_t kska_value(const Expander& ex, uint32_t v) {
 struct FastCtx {
     const KsArgs* A;
     const KeyTab* T;
-    FastLds* L;
-    FastLds::Wave* W;
+    const uint32_t* D[MAXD];  // the chunk's D_d words (LDS, padded; or memory), this lane's at lp
+    const uint32_t* c0;
+    FastWave* W;
     int lane, lp, slot, logn, m0;
     bool acc_out, pc0;
     uint32_t p, pm, n16, mask2n, chunk0, s0, bs0, rb;
@@ -352,8 +362,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
                                              const PatchTab& P) {
     const KsArgs& A = *C.A;
     const KeyTab& T = *C.T;
-    FastLds& L = *C.L;
-    FastLds::Wave& W = *C.W;
+    FastWave& W = *C.W;
     const int lane = C.lane, lp = C.lp;
     const uint32_t p = C.p, s0 = C.s0;
     const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)C.slot * T.row_words + s0;
@@ -431,7 +440,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         rejd[d] = rej;
         based[d] = base;
         uint32_t x[DS];
-        ld16(L.D[d] + lp, x);
+        ld16(C.D[d] + lp, x);
 #pragma unroll
         for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * ((rej >> k) & 1 ? 0 : kska_value<MU2>(ex, a[k]));
         // materialise the sums here: this digit's a words die before the next block is computed
@@ -505,7 +514,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
             while (m) {
                 const uint32_t j = __builtin_ctz(m);
                 m &= m - 1;
-                const uint32_t add = red.mul(L.D[d][lp + j], W.q[i++]);
+                const uint32_t add = red.mul(C.D[d][lp + j], W.q[i++]);
                 const uint32_t o = scat_addr((cbh + brev4(j) * sth) & (DCH - 1));
                 buf[o] = addm(buf[o], add, p);
             }
@@ -514,13 +523,13 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     }
     // s0 = sum_d D_d b_d (+ P c0 folded in: ndig + 1 <= 4 products of (p - 1)^2 < 2^62)
     uint32_t cw[DS];
-    if (C.m0) ld16(L.c0 + lp, cw);
+    if (C.m0) ld16(C.c0 + lp, cw);
 #pragma unroll
     for (int k = 0; k < DS; ++k) acc[k] = (C.m0 == 2 || !C.pc0) ? 0 : (uint64_t)cw[k] * C.pm;
 #pragma unroll
     for (int d = 0; d < NDIG; ++d) {
         uint32_t x[DS];
-        ld16(L.D[d] + lp, x);
+        ld16(C.D[d] + lp, x);
 #pragma unroll
         for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * b[d][k];
     }
@@ -536,11 +545,14 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     }
 }
 
-template <int NDIG, bool PATCH>
-__global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, PatchTab P, int logn) {
+// NW: waves per workgroup (KW: staged D and c0, one key per wave; 1: read from memory)
+template <int NDIG, bool PATCH, int NW>
+__global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, PatchTab P, int logn) {
     static_assert(NDIG >= 1 && NDIG <= MAXD, "digits staged in LDS");
+    static_assert(NW == KW || NW == 1, "staged (KW waves) or direct (one wave)");
     static_assert(3 * sizeof(FastLds) <= 160 * 1024, "three workgroups per CU");
-    __shared__ FastLds L;
+    using Lds = typename std::conditional<NW == KW, FastLds, FastLds1>::type;
+    __shared__ Lds L;
     // the wave index is uniform across the wave: in scalar registers, so are its key, seed and row pointers
     const int lane = threadIdx.x & (DBX - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / DBX);
     const int t = (int)A.rows[blockIdx.y];
@@ -548,10 +560,8 @@ __global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, PatchTab 
     FastCtx C;
     C.A = &A;
     C.T = &T;
-    C.L = &L;
     C.W = &L.w[wv];
     C.lane = lane;
-    C.lp = padw(lane * DS);  // this lane's 16 words in the padded rows
     C.slot = slot_of(T, t, A.nq);
     C.logn = logn;
     C.m0 = A.c0_mode & 3;
@@ -571,20 +581,42 @@ __global__ void __launch_bounds__(KBX, 3) dot_fast(KsArgs A, KeyTab T, PatchTab 
     const int kpg = (A.R + (int)gridDim.z - 1) / (int)gridDim.z;
     const int r_lo = blockIdx.z * kpg, r_hi = min(A.R, r_lo + kpg);
     DotCtx X{&A, 0, t < A.nq ? A.digit_of[t] : -1, t, C.trow, C.chunk0};
+    const uint32_t* c0row = (const uint32_t*)A.c0 + C.trow + C.chunk0;
+    if constexpr (NW == KW) {
+        C.lp = padw(lane * DS);  // this lane's 16 words in the padded rows
 #pragma unroll
-    for (int d = 0; d < NDIG; ++d) {
-        const uint4* D = (const uint4*)(X.dptr(d) + C.chunk0);
-        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i + (i >> 2)] = D[i];
-    }
-    if (C.m0) {
-        const uint4* C0 = (const uint4*)((const uint32_t*)A.c0 + C.trow + C.chunk0);
-        for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i + (i >> 2)] = C0[i];
-    }
-    __syncthreads();
-    if (ex.mu == 2) {
-        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, true, PATCH>(C, red, ex, r, P);
+        for (int d = 0; d < NDIG; ++d) {
+            const uint4* D = (const uint4*)(X.dptr(d) + C.chunk0);
+            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i + (i >> 2)] = D[i];
+            C.D[d] = L.D[d];
+        }
+        if (C.m0) {
+            const uint4* C0 = (const uint4*)c0row;
+            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i + (i >> 2)] = C0[i];
+        }
+        C.c0 = L.c0;
+        __syncthreads();
     } else {
-        for (int r = r_lo + wv; r < r_hi; r += KW) dot_fast_key<NDIG, false, PATCH>(C, red, ex, r, P);
+        C.lp = lane * DS;
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) C.D[d] = X.dptr(d) + C.chunk0;
+        C.c0 = C.m0 ? c0row : nullptr;
+    }
+    if (ex.mu == 2) {
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH>(C, red, ex, r, P);
+    } else {
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH>(C, red, ex, r, P);
+    }
+}
+
+// the fast dot's launch: one-wave direct workgroups when the launch has fewer keys than a staged workgroup's waves
+template <int NDIG, bool PATCH>
+void dot_fast_launch(dim3 grid, const KsArgs& a, const KeyTab& key, const PatchTab& P, int logn, hipStream_t st) {
+    if (a.R < KW) {
+        grid.z = a.R;
+        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1>), grid, dim3(DBX), 0, st, a, key, P, logn);
+    } else {
+        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW>), grid, dim3(KBX), 0, st, a, key, P, logn);
     }
 }
 
@@ -606,9 +638,9 @@ int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     const bool fast = mode == 1 && a.K == 1 && key.bits == 0 && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
     if (fast) {
         const PatchTab none = {};
-        if (a.ndig == 1) hipLaunchKernelGGL((dot_fast<1, false>), grid, dim3(KBX), 0, (hipStream_t)s, a, key, none, LOGN);
-        if (a.ndig == 2) hipLaunchKernelGGL((dot_fast<2, false>), grid, dim3(KBX), 0, (hipStream_t)s, a, key, none, LOGN);
-        if (a.ndig == 3) hipLaunchKernelGGL((dot_fast<3, false>), grid, dim3(KBX), 0, (hipStream_t)s, a, key, none, LOGN);
+        if (a.ndig == 1) dot_fast_launch<1, false>(grid, a, key, none, LOGN, (hipStream_t)s);
+        if (a.ndig == 2) dot_fast_launch<2, false>(grid, a, key, none, LOGN, (hipStream_t)s);
+        if (a.ndig == 3) dot_fast_launch<3, false>(grid, a, key, none, LOGN, (hipStream_t)s);
     } else if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     else hipLaunchKernelGGL(dot_k<false>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     return launch_rc();
@@ -634,9 +666,9 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
     const dim3 grid(chunks, a.nrows, groups);
     hipStream_t st = (hipStream_t)s;
-    if (a.ndig == 1) hipLaunchKernelGGL((dot_fast<1, true>), grid, dim3(KBX), 0, st, a, key, *P, LOGN);
-    if (a.ndig == 2) hipLaunchKernelGGL((dot_fast<2, true>), grid, dim3(KBX), 0, st, a, key, *P, LOGN);
-    if (a.ndig == 3) hipLaunchKernelGGL((dot_fast<3, true>), grid, dim3(KBX), 0, st, a, key, *P, LOGN);
+    if (a.ndig == 1) dot_fast_launch<1, true>(grid, a, key, *P, LOGN, st);
+    if (a.ndig == 2) dot_fast_launch<2, true>(grid, a, key, *P, LOGN, st);
+    if (a.ndig == 3) dot_fast_launch<3, true>(grid, a, key, *P, LOGN, st);
     return launch_rc();
 }
 

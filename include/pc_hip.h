@@ -728,7 +728,7 @@ int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t 
  * res + j ct_words. */
 int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
                   uint32_t enc, const void* ct, int top, void* res, pc_stream_t s);
-/* The relinearization key s^2 -> s (crates/pc-gpu/src/keygen.rs:150-170): one key of galois 1 generated as
+/* The relinearization key s^2 -> s (crates/pc-gpu/src/keygen.rs:225-226): one key of galois 1 generated as
  * pcx_keys_generate's, its old secret squared in the kernel (KskGenArgs.sq). */
 pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed, const int64_t* errors, int bits,
                          int* err);
@@ -737,7 +737,7 @@ pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed,
  * the primes one at a time; out's rows above are scratch. Two primes run the table's rescale_fwd (the corrections
  * generated in the forward NTT), one prime rescale_coef and the NTT. out may be ct. */
 int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_stream_t s);
-/* The relinearized product (crates/pc-gpu/src/relin.rs:248-272 mult): the tensor (c0, c1, d2), then d2 key-switched
+/* The relinearized product (crates/pc-gpu/src/relin.rs:213-235 mult): the tensor (c0, c1, d2), then d2 key-switched
  * by key 0 of k (the relinearization key: galois 1) and added: out = (c0, c1) + ModDown(dot(ModUp(d2))) on Q rows
  * 0..top (degree 2, rescale pending). out may be a or b. */
 int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);

@@ -1031,7 +1031,7 @@ pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint
 
 // crates/pc-gpu/src/keygen.rs:172-262: the secret's eval rows, per key the Gaussian errors NTT'd, s_new =
 // sigma_{g^-1}(s) by the automorph kernel, then ksk_gen (b dense or packed); sq: the old secret squared in the kernel
-// (the relinearization key s^2 -> s, galois 1; keygen.rs:150-170)
+// (the relinearization key s^2 -> s, galois 1; keygen.rs:225-226)
 static pcx_keys* keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret, const uint32_t* seeds,
                         const int64_t* errors, int bits, int sq, int* err) {
     int dummy;
@@ -1403,7 +1403,7 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
     return c->tab->ntt_fwd(&f, s);
 }
 
-// The relinearized product (crates/pc-gpu/src/relin.rs:248-272 mult, Cached-key form :120-130): (c0, c1, d2) by the
+// The relinearized product (crates/pc-gpu/src/relin.rs:213-235 mult, Cached-key form :119-128): (c0, c1, d2) by the
 // tensor kernel (d2 into part 1 of the context's tmp ciphertext), ModUp(d2), the key inner product with the
 // relinearization key (no c0 term, no automorphism), and the ModDown added onto (c0, c1): out = (c0, c1) +
 // (ext - conv) P^-1 on Q rows 0..top. out may be a or b.

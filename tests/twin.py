@@ -214,7 +214,7 @@ class Ctx:
         return out
 
     def mul_relin(self, a, b, top, seed, bkey):
-        """The relinearized product (crates/pc-gpu/src/relin.rs:248-272) composed from the oracle's pieces: the tensor
+        """The relinearized product (crates/pc-gpu/src/relin.rs:213-235) composed from the oracle's pieces: the tensor
         (oracle/em.py), ModUp(d2), the key dot with no c0 term and no automorphism, ModDown added onto (c0, c1)."""
         from oracle import em
         n = top + 1

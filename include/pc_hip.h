@@ -540,8 +540,25 @@ typedef struct SmallInt1Args {
 } SmallInt1Args;
 PC_STATIC_ASSERT(sizeof(SmallInt1Args) == 56, "SmallInt1Args layout");
 
+/* args.cuh:184-198: the BSGS plaintext dot of a stage in the extended basis, K <= 8 ciphertexts sharing the diagonals:
+ * res[c][j][part] = sum_{i < bstep} rot[c][i][part] pt[bstep j + i] (j < gstep, diagonals >= npts skipped); rot (c, i)
+ * at rot.base + c rot.ct_stride + i rot_stride, res (c, j) at res.base + c res.ct_stride + j res_stride; pts[d]: the
+ * diagonal's rows (ptw words each; Q rows, then the special rows from pt_prow), read at the compact index (enc as
+ * CtsArgs.enc) */
+typedef struct PtDotArgs {
+    PolyRef rot, res;
+    uint64_t rot_stride, res_stride;
+    const void* const* pts;
+    const PrimeConst* pr;
+    RowSet rs;
+    int32_t npts, bstep, gstep, K;
+    int32_t ptw, pt_prow;
+    uint32_t enc;
+    int32_t pad;
+} PtDotArgs;
+PC_STATIC_ASSERT(sizeof(PtDotArgs) == 128, "PtDotArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
-struct PtDotArgs;
 struct EncodeArgs;
 struct SpruExtractArgs;
 struct SpruFftArgs;

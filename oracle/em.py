@@ -254,3 +254,32 @@ def encrypt(q, a, s, e, m=None):
     qq = _q(q, n)
     em_ = _u(e) if m is None else _add(e, m, qq)
     return _out(_sub(em_, _mul(a, s, qq), qq))
+
+
+# ----------------------------------------------------------------------------------------------- BSGS plaintext dot
+def ptidx(o, enc):
+    """a diagonal's compact index of slot o (arith.cuh:242-244): o >> (enc & 0xFF) when enc >> 24 == 0x7F, else o & enc"""
+    o = np.asarray(o, np.uint64)
+    if enc >> 24 == 0x7F:
+        return o >> np.uint64(enc & 0xFF)
+    return o & np.uint64(enc)
+
+
+def pt_dot(q, rot, pts, bstep, gstep, npts, enc, prows):
+    """pt_dot (args.cuh:184-198; elem.cuh:83-118; elem.rs:145-193): rot [K][bstep][2][n][N] over rows with primes q[r],
+    pts[d] [rows][ptw] read at row prows[r] and index ptidx(i, enc) -> res [K][gstep][2][n][N] with
+    res[c][j] = sum_{b < bstep, bstep j + b < npts} rot[c][b] pt_{bstep j + b}."""
+    K, _, _, n, N = rot.shape
+    qq = _q(q, n)
+    idx = ptidx(np.arange(N), enc).astype(np.int64)
+    out = np.zeros((K, gstep, 2, n, N), np.uint32)
+    for j in range(gstep):
+        acc = np.zeros((K, 2, n, N), U64)
+        for b in range(bstep):
+            d = bstep * j + b
+            if d >= npts:
+                break
+            w = np.stack([np.asarray(pts[d][prows[r]], U64)[idx] for r in range(n)])
+            acc = _add(acc, _mul(rot[:, b], w[None, None], qq), qq)
+        out[:, j] = _out(acc)
+    return out

@@ -78,6 +78,18 @@ class NttArgs(C.Structure):
                 ("xnum", i32), ("lazy", i32), ("xstride", u64), ("ed", vp)]
 
 
+class RowSet(C.Structure):
+    """args.cuh:52-57: Q rows [0, nq) then np special rows from prime id qmax."""
+    _fields_ = [("nq", i32), ("np", i32), ("qmax", i32), ("pad", i32)]
+
+
+class PtDotArgs(C.Structure):
+    """args.cuh:184-198 (128 bytes)."""
+    _fields_ = [("rot", PolyRef), ("res", PolyRef), ("rot_stride", u64), ("res_stride", u64), ("pts", vp), ("pr", vp),
+                ("rs", RowSet), ("npts", i32), ("bstep", i32), ("gstep", i32), ("K", i32), ("ptw", i32),
+                ("pt_prow", i32), ("enc", u32), ("pad", i32)]
+
+
 class TensorArgs(C.Structure):
     """args.cuh:356-367 (192 bytes)."""
     _fields_ = [("out", PolyRef), ("d2", PolyRef), ("a0", PolyRef), ("b0", PolyRef), ("a1", PolyRef),
@@ -232,6 +244,7 @@ assert C.sizeof(RescaleCombineToArgs) == 104 and C.sizeof(EwManyArgs) == 4 * EWM
 assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
 assert C.sizeof(ModRaiseArgs) == 2136 and C.sizeof(SmallIntTab) == 4552 and C.sizeof(SmallIntArgs) == 72
 assert C.sizeof(SmallInt1Args) == 56 and C.sizeof(EncryptArgs) == 64
+assert C.sizeof(RowSet) == 16 and C.sizeof(PtDotArgs) == 128
 
 _LAUNCHER = C.CFUNCTYPE(C.c_int, vp, vp)
 

@@ -63,6 +63,11 @@ struct Red {
 };
 
 // ------------------------------------------------------------------------------------------------ bit tricks
+// A BSGS diagonal's compact index of output slot o (crates/pc-kernels/kernels/arith.cuh:242-244): o >> (enc & 0xFF)
+// when enc >> 24 == 0x7F (a block-constant diagonal), else o & enc (0xFFFFFFFF: the full row)
+__device__ __forceinline__ uint32_t ptidx(uint32_t o, uint32_t enc) {
+    return (enc >> 24) == 0x7Fu ? o >> (enc & 0xFFu) : o & enc;
+}
 __device__ __forceinline__ uint32_t brev_n(uint32_t x, int logn) { return __brev(x) >> (32 - logn); }
 // FIDESlib automorph_slot (crates/pc-kernels/kernels/arith.cuh:233-239; crates/pc-core/src/galois.rs:105-112): the
 // slot of sigma_k's source for output `slot` in the bit-reversed evaluation order. Scatter by k = gather by k^-1.

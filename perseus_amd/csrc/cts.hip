@@ -45,11 +45,6 @@ __device__ __forceinline__ uint32_t inv_odd(uint32_t k) {
     return x;
 }
 
-// crates/pc-kernels/kernels/arith.cuh:242-244: a diagonal's compact index of slot o
-__device__ __forceinline__ uint32_t ptidx(uint32_t o, uint32_t enc) {
-    return (enc >> 24) == 0x7Fu ? o >> (enc & 0xFFu) : o & enc;
-}
-
 // the key slot of prime id t (KskShape::slot_of): Q primes at their id, special prime nq + j at q_top + 1 + j
 __device__ __forceinline__ int slot_of(const KeyTab& T, int t, int nq) {
     return (t < nq || T.q_top < 0) ? t : T.q_top + 1 + (t - nq);

@@ -285,6 +285,50 @@ __global__ void __launch_bounds__(BX) submul_many_k(SubMulManyArgs A, int logn) 
     st4((uint32_t*)A.out[j] + o, r);
 }
 
+// ------------------------------------------------------------------------------------------------ BSGS plaintext dot
+// res[c][j] = sum_{b < bstep} rot[c][b] pt_{bstep j + b}[prow][ptidx(i, enc)] on the row set's rows (args.cuh:184-198;
+// elem.cuh:83-118): rotations and results by PolyRef plus the per-rotation / per-result strides, diagonals >= npts
+// skipped; prow = y on Q rows, pt_prow + (y - nq) on special rows. 4 consecutive slots per thread, one ciphertext at a
+// time (the diagonals' words come again from L2), the sums exact.
+__global__ void __launch_bounds__(BX) pt_dot_k(PtDotArgs A, int logn) {
+    const int y = blockIdx.y;
+    const int row = y < A.rs.nq ? y : A.rs.qmax + (y - A.rs.nq);
+    const int prow = y < A.rs.nq ? y : A.pt_prow + (y - A.rs.nq);
+    const Red red(A.pr[row]);
+    const uint32_t i = lane_word();
+    uint32_t pi[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pi[w] = ptidx(i + w, A.enc);
+    const size_t roff = ((size_t)row << logn) + i;
+    for (int c = 0; c < A.K; ++c) {
+        for (int j = 0; j < A.gstep; ++j) {
+            Acc s0[4], s1[4];
+            for (int b = 0; b < A.bstep; ++b) {
+                const int d = A.bstep * j + b;
+                if (d >= A.npts) break;
+                const uint32_t* pt = (const uint32_t*)A.pts[d] + (size_t)prow * A.ptw;
+                const uint32_t* r = (const uint32_t*)A.rot.base + c * A.rot.ct_stride + b * A.rot_stride + roff;
+                const W4 x0 = ld4(r), x1 = ld4(r + A.rot.part_stride);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t pw = pt[pi[w]];
+                    s0[w].add((uint64_t)x0.v[w] * pw);
+                    s1[w].add((uint64_t)x1.v[w] * pw);
+                }
+            }
+            W4 r0, r1;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                r0.v[w] = s0[w].red(red);
+                r1.v[w] = s1[w].red(red);
+            }
+            uint32_t* o = (uint32_t*)A.res.base + c * A.res.ct_stride + j * A.res_stride + roff;
+            st4(o, r0);
+            st4(o + A.res.part_stride, r1);
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
 // The reference's launchers check only the counts below (em.cuh:580-692); these also refuse null operands that the
 // kernel would read (-1) and return 0 without a launch when there is no work.
@@ -470,6 +514,14 @@ int submul_many(const SubMulManyArgs* a, pc_stream_t s) {
     if (a->nrows == 0) return 0;
     PCH_LAUNCH(submul_many_k, grid<LOGN>(a->nrows, a->n), *a, LOGN);
 }
+template <int LOGN>
+int pt_dot(const PtDotArgs* a, pc_stream_t s) {
+    if (!a || a->K > 8) return -1;
+    if (!a->rot.base || !a->res.base || !a->pts || !a->pr || a->K < 0 || a->bstep < 0 || a->gstep < 0) return -1;
+    const int rows = a->rs.nq + a->rs.np;
+    if (rows <= 0 || a->K == 0 || a->gstep == 0) return 0;
+    PCH_LAUNCH(pt_dot_k, grid<LOGN>(rows, 1), *a, LOGN);
+}
 #undef PCH_LAUNCH
 
 }  // namespace em
@@ -492,7 +544,8 @@ int submul_many(const SubMulManyArgs* a, pc_stream_t s) {
         return em::rescale_combine_to<L>(a, s);                                                                      \
     }                                                                                                                \
     int ew_many_##L(const EwManyArgs* a, pc_stream_t s) { return em::ew_many<L>(a, s); }                             \
-    int submul_many_##L(const SubMulManyArgs* a, pc_stream_t s) { return em::submul_many<L>(a, s); }
+    int submul_many_##L(const SubMulManyArgs* a, pc_stream_t s) { return em::submul_many<L>(a, s); }             \
+    int pt_dot_##L(const PtDotArgs* a, pc_stream_t s) { return em::pt_dot<L>(a, s); }
 PCH_EM_INST(12)
 PCH_EM_INST(13)
 PCH_EM_INST(14)

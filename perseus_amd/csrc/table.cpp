@@ -42,7 +42,8 @@ namespace pch {
     int mod_raise_##L(const ModRaiseArgs*, pc_stream_t);             \
     int small_int_##L(const SmallIntArgs*, pc_stream_t);             \
     int small_int1_##L(const SmallInt1Args*, pc_stream_t);           \
-    int encrypt_##L(const EncryptArgs*, pc_stream_t);
+    int encrypt_##L(const EncryptArgs*, pc_stream_t);                \
+    int pt_dot_##L(const PtDotArgs*, pc_stream_t);
 PCH_DECL(12)
 PCH_DECL(13)
 PCH_DECL(14)
@@ -58,7 +59,7 @@ int absent(const A*, pc_stream_t) {
     static const KernelTable TABLE_##L = {                                                                           \
         PC_KERNELS_ABI, 4, 0, L,                                                                                     \
         ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
-        absent<PtDotArgs>, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
+        pt_dot_##L, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
         md_epilogue_##L, wsum_##L, add_const_##L, mul_table_##L, rescale_coef_##L, rescale_combine_##L,            \
         automorph_##L, absent<EncodeArgs>, encrypt_##L, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
         small_int_##L, absent<SpruExtractArgs>, absent<SpruFftArgs>, absent<SpruScatterArgs>,                 \

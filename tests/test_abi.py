@@ -197,3 +197,12 @@ def test_encrypt_launcher_rejects_null_operands():
     a = abi.EncryptArgs()
     a.nl = 2
     assert abi.call("encrypt", a, log_n=12) == -1
+
+
+def test_pt_dot_launcher_checks():
+    from perseus_amd import abi
+    a = abi.PtDotArgs()
+    a.K = 9
+    assert abi.call("pt_dot", a, log_n=12) == -1    # more than 8 ciphertexts
+    a.K = 1
+    assert abi.call("pt_dot", a, log_n=12) == -1    # null operands

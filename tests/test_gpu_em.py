@@ -473,3 +473,39 @@ def test_encrypt(stream, name, with_m, with_c1, alias_e):
     assert (c0.download((nl, n)) == want).all()
     if with_c1:
         assert (c1.download((nl, n)) == a_rows).all()
+
+
+# ----------------------------------------------------------------------------------------------- BSGS plaintext dot
+@pytest.mark.parametrize("name,enc,K", [("small31", 0xFFFFFFFF, 2), ("small31", 0x7F000003, 3), ("small", 0x3FF, 1),
+                                        ("c3", 0xFFFFFFFF, 1)])
+def test_pt_dot(stream, name, enc, K):
+    say(f"[pt_dot] {name} enc={enc:#x} K={K}")
+    ch, ctx, _ = contexts(name)
+    rng = np.random.default_rng(enc % 1000 + K)
+    B, G, npts = 3, 2, 5
+    top = len(ch.q) - 1 if name == "c3" else len(ch.q) - 2
+    rows = list(range(top + 1)) + [len(ch.q) + j for j in range(len(ch.p))]
+    n, R = len(rows), ch.rows
+    # rotations (c, b): K x B extended ciphertexts [2][R][N] (rows of the row set filled); results K x G
+    rot = np.zeros((K, B, 2, R, ch.n), np.uint32)
+    for t in rows:
+        rot[:, :, :, t] = rng.integers(0, ch.primes[t], (K, B, 2, ch.n))
+    ptw = ch.n if enc == 0xFFFFFFFF else (ch.n >> 3 if enc >> 24 == 0x7F else enc + 1)
+    pt_prow = top + 1  # the special rows' diagonal rows follow the Q rows
+    pts = [np.stack([rng.integers(0, ch.primes[t], ptw) for t in rows]).astype(np.uint32) for _ in range(npts)]
+    pbufs = [pa.DevBuf.from_array(p) for p in pts]
+    ptrs = pa.DevBuf.from_array(np.array([b.ptr.value for b in pbufs], np.uint64).view(np.uint32))
+    brot = pa.DevBuf.from_array(rot)
+    res = pa.DevBuf(K * G * 2 * R * ch.n)
+    a = abi.PtDotArgs()
+    a.rot = abi.PolyRef(brot.ptr.value, B * 2 * R * ch.n, R * ch.n)
+    a.res = abi.PolyRef(res.ptr.value, G * 2 * R * ch.n, R * ch.n)
+    a.rot_stride, a.res_stride = 2 * R * ch.n, 2 * R * ch.n
+    a.pts, a.pr = ptrs.ptr.value, pr_of(ctx)
+    a.rs = abi.RowSet(top + 1, len(ch.p), len(ch.q), 0)
+    a.npts, a.bstep, a.gstep, a.K, a.ptw, a.pt_prow, a.enc = npts, B, G, K, ptw, pt_prow, enc
+    run("pt_dot", a, stream, ch.logn)
+    got = res.download((K, G, 2, R, ch.n))
+    q = [ch.primes[t] for t in rows]
+    want = em.pt_dot(q, rot[:, :, :, rows], pts, B, G, npts, enc, list(range(n)))
+    assert (got[:, :, :, rows] == want).all()

@@ -362,3 +362,28 @@ def test_mul_relin_then_rescale_decrypts_to_the_product():
     got = crt_centred(decrypt(ctx, s_eval, rs, top - 2), ctx.primes[: top - 1])
     div = int(ctx.primes[top]) * int(ctx.primes[top - 1])
     assert max(abs(x - round(y / div)) for x, y in zip(got, prod)) < 1 << 8
+
+
+# ----------------------------------------------------------------------------------------------- BSGS plaintext dot
+@pytest.mark.parametrize("enc", [0xFFFFFFFF, 0x7F000003, 0x1F])
+def test_pt_dot_decrypts_to_the_diagonal_products(enc):
+    """Dec(res_j) = sum_b Dec(rot_b) pt_{B j + b} word by word, diagonals past npts skipped; a compact diagonal read
+    through enc equals its expansion to a full row read plainly."""
+    K, B, G, n = 2, 3, 2, 4
+    npts = 5
+    s = secret(Q, n, N)
+    rot = np.stack([np.stack([rand_ct(Q, 1, n, N)[0] for _ in range(B)]) for _ in range(K)])
+    ptw = N if enc == 0xFFFFFFFF else (N >> 3 if enc >> 24 == 0x7F else enc + 1)
+    pts = [np.stack([RNG.integers(0, Q[r], ptw) for r in range(n)]).astype(np.uint32) for _ in range(npts)]
+    res = em.pt_dot(Q, rot, pts, B, G, npts, enc, list(range(n)))
+    idx = em.ptidx(np.arange(N), enc).astype(np.int64)
+    full = [p[:, idx] for p in pts]
+    assert (em.pt_dot(Q, rot, full, B, G, npts, 0xFFFFFFFF, list(range(n))) == res).all()
+    qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+    for c in range(K):
+        for j in range(G):
+            want = np.zeros((n, N), np.uint64)
+            for b in range(B):
+                if B * j + b < npts:
+                    want = addq(want, mulq(dec(Q, rot[c, b, 0], rot[c, b, 1], s), full[B * j + b], Q), Q)
+            assert (dec(Q, res[c, j, 0], res[c, j, 1], s) == want % qq).all()

@@ -328,6 +328,20 @@ typedef struct TensorSumArgs {
 } TensorSumArgs;
 PC_STATIC_ASSERT(sizeof(TensorSumArgs) == 2 * 24 + 2 * PC_TSUM_MAX * 24 + 8 + 16, "TensorSumArgs layout");
 
+/* args.cuh:391-406: nout <= 4 tensor sums in one call, output o = sum_{j < npairs <= 32} a[o][j] b[o][j] (c0, c1 into
+ * out[o], d2 into part 1 of d2[o]; acc as tensor_sum's). Here each output's pairs run as launches of 16, so no
+ * output may alias an operand of the call. */
+#define PC_TMULTI_OUT 4
+#define PC_TMULTI_PAIRS 32
+typedef struct TensorMultiArgs {
+    PolyRef out[PC_TMULTI_OUT], d2[PC_TMULTI_OUT];
+    PolyRef a[PC_TMULTI_OUT][PC_TMULTI_PAIRS], b[PC_TMULTI_OUT][PC_TMULTI_PAIRS];
+    const PrimeConst* pr;
+    int32_t nout, npairs, acc, n, K, pad;
+} TensorMultiArgs;
+PC_STATIC_ASSERT(sizeof(TensorMultiArgs) == (2 * PC_TMULTI_OUT + 2 * PC_TMULTI_OUT * PC_TMULTI_PAIRS) * 24 + 8 + 24,
+                 "TensorMultiArgs layout");
+
 /* args.cuh:438-447: for parts 0, 1: dst = f (dst + (x - t) binv) [+ k[row] on part 0, reduced once], f = 2 when dbl */
 typedef struct MdEpiArgs {
     PolyRef dst, x, t;
@@ -558,6 +572,37 @@ typedef struct PtDotArgs {
 } PtDotArgs;
 PC_STATIC_ASSERT(sizeof(PtDotArgs) == 128, "PtDotArgs layout");
 
+/* args.cuh:230-241: the subring switch's split, coefficient form: row y of polynomial c (q + c q_stride + y N for
+ * y < nq, else p + c p_stride + (y - nq) N) into sub digits, digit j = the coefficients at the exponents = j mod sub
+ * (the rest 0), written at out + c out_stride + (j nrows + y) N */
+typedef struct PackSplitArgs {
+    const void* q;
+    const void* p;
+    void* out;
+    uint64_t q_stride, p_stride, out_stride;
+    int32_t K, sub, nq, nrows;
+} PackSplitArgs;
+PC_STATIC_ASSERT(sizeof(PackSplitArgs) == 64, "PackSplitArgs layout");
+
+/* args.cuh:243-259: the subring switch's dot, evaluation form: s1 = sum_j D_j a_j, s0 = sum_j D_j b_j (+ pmod c0 on
+ * the Q rows y < nq), row y at prime id rows[y]; D as pack_split's out (dig, dig_stride), kb / ka [digit][row y][N];
+ * c0 and the outputs in prime-id rows, polynomial c at + c ct_stride / + c out_ct_stride */
+typedef struct PackDotArgs {
+    const void* dig;
+    const void* kb;
+    const void* ka;
+    const void* c0;
+    void* out0;
+    void* out1;
+    const uint32_t* rows;
+    const void* pmod;
+    const void* pmods;
+    const PrimeConst* pr;
+    uint64_t dig_stride, ct_stride, out_ct_stride;
+    int32_t K, sub, nq, nrows;
+} PackDotArgs;
+PC_STATIC_ASSERT(sizeof(PackDotArgs) == 120, "PackDotArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct EncodeArgs;
 struct SpruExtractArgs;
@@ -567,10 +612,7 @@ struct PcmmArgs;
 struct CcmmArgs;
 struct CoeffArgs;
 struct TfheArgs;
-struct TensorMultiArgs;
 struct TensorSeededArgs;
-struct PackSplitArgs;
-struct PackDotArgs;
 
 /* args.cuh:1035-1097 */
 typedef struct KernelTable {

@@ -283,3 +283,28 @@ def pt_dot(q, rot, pts, bstep, gstep, npts, enc, prows):
             acc = _add(acc, _mul(rot[:, b], w[None, None], qq), qq)
         out[:, j] = _out(acc)
     return out
+
+
+# ----------------------------------------------------------------------------------------------- subring switch
+def pack_split(x, sub):
+    """pack_split (args.cuh:230-241; ks.cuh:909-921; crates/pc-host/src/ks.rs:364-381): rows [nrows][N] of one
+    polynomial -> digits [sub][nrows][N], digit j keeping the coefficients at exponents = j mod sub."""
+    N = x.shape[-1]
+    cls = np.arange(N) % sub
+    return np.stack([np.where(cls == j, x, 0).astype(np.uint32) for j in range(sub)])
+
+
+def pack_dot(q, dig, kb, ka, c0=None, pmod=None, nq=0):
+    """pack_dot (args.cuh:243-259; ks.cuh:923-947; crates/pc-host/src/ks.rs:383-405): digits, key b and key a
+    [sub][n][N] over rows of primes q -> (s0, s1) [n][N]: s1 = sum_j D_j a_j, s0 = sum_j D_j b_j, plus pmod[y] c0 on
+    the first nq rows."""
+    n = dig.shape[1]
+    qq = _q(q, n)
+    s0 = np.zeros(dig.shape[1:], U64)
+    s1 = s0.copy()
+    for j in range(dig.shape[0]):
+        s0 = _add(s0, _mul(dig[j], kb[j], qq), qq)
+        s1 = _add(s1, _mul(dig[j], ka[j], qq), qq)
+    if nq:
+        s0[:nq] = _add(s0[:nq], _mul(c0[:nq], _row(pmod, nq), qq[:nq]), qq[:nq])
+    return _out(s0), _out(s1)

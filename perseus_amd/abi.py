@@ -90,6 +90,19 @@ class PtDotArgs(C.Structure):
                 ("pt_prow", i32), ("enc", u32), ("pad", i32)]
 
 
+class PackSplitArgs(C.Structure):
+    """args.cuh:230-241 (64 bytes)."""
+    _fields_ = [("q", vp), ("p", vp), ("out", vp), ("q_stride", u64), ("p_stride", u64), ("out_stride", u64),
+                ("K", i32), ("sub", i32), ("nq", i32), ("nrows", i32)]
+
+
+class PackDotArgs(C.Structure):
+    """args.cuh:243-259 (120 bytes)."""
+    _fields_ = [("dig", vp), ("kb", vp), ("ka", vp), ("c0", vp), ("out0", vp), ("out1", vp), ("rows", vp),
+                ("pmod", vp), ("pmods", vp), ("pr", vp), ("dig_stride", u64), ("ct_stride", u64),
+                ("out_ct_stride", u64), ("K", i32), ("sub", i32), ("nq", i32), ("nrows", i32)]
+
+
 class TensorArgs(C.Structure):
     """args.cuh:356-367 (192 bytes)."""
     _fields_ = [("out", PolyRef), ("d2", PolyRef), ("a0", PolyRef), ("b0", PolyRef), ("a1", PolyRef),
@@ -109,6 +122,16 @@ class TensorSumArgs(C.Structure):
     """args.cuh:379-389."""
     _fields_ = [("out", PolyRef), ("d2", PolyRef), ("a", PolyRef * TSUM_MAX), ("b", PolyRef * TSUM_MAX), ("pr", vp),
                 ("npairs", i32), ("acc", i32), ("n", i32), ("K", i32)]
+
+
+TMULTI_OUT, TMULTI_PAIRS = 4, 32
+
+
+class TensorMultiArgs(C.Structure):
+    """args.cuh:391-406."""
+    _fields_ = [("out", PolyRef * TMULTI_OUT), ("d2", PolyRef * TMULTI_OUT),
+                ("a", (PolyRef * TMULTI_PAIRS) * TMULTI_OUT), ("b", (PolyRef * TMULTI_PAIRS) * TMULTI_OUT),
+                ("pr", vp), ("nout", i32), ("npairs", i32), ("acc", i32), ("n", i32), ("K", i32), ("pad", i32)]
 
 
 class MdEpiArgs(C.Structure):
@@ -245,6 +268,8 @@ assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
 assert C.sizeof(ModRaiseArgs) == 2136 and C.sizeof(SmallIntTab) == 4552 and C.sizeof(SmallIntArgs) == 72
 assert C.sizeof(SmallInt1Args) == 56 and C.sizeof(EncryptArgs) == 64
 assert C.sizeof(RowSet) == 16 and C.sizeof(PtDotArgs) == 128
+assert C.sizeof(PackSplitArgs) == 64 and C.sizeof(PackDotArgs) == 120
+assert C.sizeof(TensorMultiArgs) == (2 * TMULTI_OUT + 2 * TMULTI_OUT * TMULTI_PAIRS) * 24 + 8 + 24
 
 _LAUNCHER = C.CFUNCTYPE(C.c_int, vp, vp)
 

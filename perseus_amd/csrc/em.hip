@@ -514,6 +514,39 @@ int submul_many(const SubMulManyArgs* a, pc_stream_t s) {
     if (a->nrows == 0) return 0;
     PCH_LAUNCH(submul_many_k, grid<LOGN>(a->nrows, a->n), *a, LOGN);
 }
+// tensor_multi: each output's pair list through the tensor_sum kernel, 16 pairs per launch (a longer list continues
+// with acc 2 onto the first launch's words: the sums are exact, so the words are those of one pass). The reference
+// loads an operand shared by consecutive outputs once (em.cuh:125-197); here each output reads its own.
+template <int LOGN>
+int tensor_multi(const TensorMultiArgs* a, pc_stream_t s) {
+    if (!a || a->nout < 1 || a->nout > PC_TMULTI_OUT || a->npairs < 1 || a->npairs > PC_TMULTI_PAIRS) return -1;
+    if (!a->pr || a->n < 0 || a->K < 0) return -1;
+    for (int o = 0; o < a->nout; ++o) {
+        if (!ref_ok(a->out[o]) || !ref_ok(a->d2[o])) return -1;
+        for (int j = 0; j < a->npairs; ++j)
+            if (!ref_ok(a->a[o][j]) || !ref_ok(a->b[o][j])) return -1;
+    }
+    if (a->n == 0 || a->K == 0) return 0;
+    for (int o = 0; o < a->nout; ++o)
+        for (int j0 = 0; j0 < a->npairs; j0 += PC_TSUM_MAX) {
+            TensorSumArgs t{};
+            t.out = a->out[o];
+            t.d2 = a->d2[o];
+            t.npairs = a->npairs - j0 < PC_TSUM_MAX ? a->npairs - j0 : PC_TSUM_MAX;
+            for (int j = 0; j < t.npairs; ++j) {
+                t.a[j] = a->a[o][j0 + j];
+                t.b[j] = a->b[o][j0 + j];
+            }
+            t.pr = a->pr;
+            t.acc = j0 == 0 ? a->acc : 2;
+            t.n = a->n;
+            t.K = a->K;
+            hipLaunchKernelGGL(tensor_sum_k, grid<LOGN>(a->n, a->K), dim3(BX), 0, (hipStream_t)s, t, LOGN);
+            if (int rc = launch_rc()) return rc;
+        }
+    return 0;
+}
+
 template <int LOGN>
 int pt_dot(const PtDotArgs* a, pc_stream_t s) {
     if (!a || a->K > 8) return -1;
@@ -545,7 +578,8 @@ int pt_dot(const PtDotArgs* a, pc_stream_t s) {
     }                                                                                                                \
     int ew_many_##L(const EwManyArgs* a, pc_stream_t s) { return em::ew_many<L>(a, s); }                             \
     int submul_many_##L(const SubMulManyArgs* a, pc_stream_t s) { return em::submul_many<L>(a, s); }             \
-    int pt_dot_##L(const PtDotArgs* a, pc_stream_t s) { return em::pt_dot<L>(a, s); }
+    int pt_dot_##L(const PtDotArgs* a, pc_stream_t s) { return em::pt_dot<L>(a, s); }                            \
+    int tensor_multi_##L(const TensorMultiArgs* a, pc_stream_t s) { return em::tensor_multi<L>(a, s); }
 PCH_EM_INST(12)
 PCH_EM_INST(13)
 PCH_EM_INST(14)

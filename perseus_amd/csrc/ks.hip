@@ -801,6 +801,94 @@ int encrypt(const EncryptArgs* a, pc_stream_t s) {
     return launch_rc();
 }
 
+// ------------------------------------------------------------------------------------------------ subring switch
+// pack_split / pack_dot (args.cuh:230-259; ks.cuh:909-963; host twin crates/pc-host/src/ks.rs:355-405): the split
+// of c1 into sub coefficient classes (4 consecutive coefficients per thread, one 16-byte store per digit), and the dot
+// of the digits against the pack key with the sum of the sub <= 16 products carried exactly.
+constexpr int PBX = 256;
+
+__global__ void __launch_bounds__(PBX) pack_split_k(PackSplitArgs A, int logn) {
+    const int y = blockIdx.y, c = blockIdx.z;
+    const uint32_t i = (blockIdx.x * PBX + threadIdx.x) * 4;
+    const uint32_t* src = y < A.nq ? (const uint32_t*)A.q + c * A.q_stride + ((size_t)y << logn)
+                                   : (const uint32_t*)A.p + c * A.p_stride + ((size_t)(y - A.nq) << logn);
+    const uint4 v = *(const uint4*)(src + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t* o = (uint32_t*)A.out + c * A.out_stride + ((size_t)y << logn) + i;
+    const size_t js = (size_t)A.nrows << logn;
+    for (int j = 0; j < A.sub; ++j) {
+        uint32_t r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = (int)((i + k) & (A.sub - 1)) == j ? w[k] : 0u;
+        *(uint4*)(o + j * js) = make_uint4(r[0], r[1], r[2], r[3]);
+    }
+}
+
+__global__ void __launch_bounds__(PBX) pack_dot_k(PackDotArgs A, int logn) {
+    const int y = blockIdx.y, c = blockIdx.z;
+    const uint32_t t = A.rows[y];
+    const Red red(A.pr[t]);
+    const uint32_t i = (blockIdx.x * PBX + threadIdx.x) * 4;
+    const size_t koff = ((size_t)y << logn) + i, js = (size_t)A.nrows << logn;
+    const uint32_t* dg = (const uint32_t*)A.dig + c * A.dig_stride + koff;
+    uint64_t l0[4] = {0, 0, 0, 0}, l1[4] = {0, 0, 0, 0};
+    uint32_t h0[4] = {0, 0, 0, 0}, h1[4] = {0, 0, 0, 0};
+    for (int j = 0; j < A.sub; ++j) {
+        const uint4 x = *(const uint4*)(dg + j * js);
+        const uint4 b = *(const uint4*)((const uint32_t*)A.kb + koff + j * js);
+        const uint4 a = *(const uint4*)((const uint32_t*)A.ka + koff + j * js);
+        const uint32_t xv[4] = {x.x, x.y, x.z, x.w}, bv[4] = {b.x, b.y, b.z, b.w}, av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint64_t p0 = (uint64_t)xv[k] * bv[k], p1 = (uint64_t)xv[k] * av[k];
+            l0[k] += p0;
+            h0[k] += l0[k] < p0;
+            l1[k] += p1;
+            h1[k] += l1[k] < p1;
+        }
+    }
+    const size_t roff = ((size_t)t << logn) + i;
+    uint32_t r0[4], r1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        r0[k] = red.red96(l0[k], h0[k]);
+        r1[k] = red.red96(l1[k], h1[k]);
+    }
+    if (y < A.nq) {
+        const uint32_t pm = ((const uint32_t*)A.pmod)[t], pms = ((const uint32_t*)A.pmods)[t];
+        const uint4 z = *(const uint4*)((const uint32_t*)A.c0 + c * A.ct_stride + roff);
+        const uint32_t zv[4] = {z.x, z.y, z.z, z.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r0[k] = addm(r0[k], shoup(zv[k], pm, pms, red.p), red.p);
+    }
+    *(uint4*)((uint32_t*)A.out0 + c * A.out_ct_stride + roff) = make_uint4(r0[0], r0[1], r0[2], r0[3]);
+    *(uint4*)((uint32_t*)A.out1 + c * A.out_ct_stride + roff) = make_uint4(r1[0], r1[1], r1[2], r1[3]);
+}
+
+// the reference's checks (ks.cuh:949-963): sub a power of two in 2..16, 0 <= nq <= nrows, K >= 1
+inline bool pack_ok(int sub, int nq, int nrows, int K) {
+    return sub >= 2 && sub <= 16 && !(sub & (sub - 1)) && nq >= 0 && nq <= nrows && K >= 1;
+}
+template <int LOGN>
+int pack_split(const PackSplitArgs* a, pc_stream_t s) {
+    if (!a || !pack_ok(a->sub, a->nq, a->nrows, a->K)) return -1;
+    if (!a->out || (a->nq > 0 && !a->q) || (a->nrows > a->nq && !a->p)) return -1;
+    if (a->nrows == 0) return 0;
+    hipLaunchKernelGGL(pack_split_k, dim3((1 << LOGN) / (PBX * 4), a->nrows, a->K), dim3(PBX), 0, (hipStream_t)s, *a,
+                       LOGN);
+    return launch_rc();
+}
+template <int LOGN>
+int pack_dot(const PackDotArgs* a, pc_stream_t s) {
+    if (!a || !pack_ok(a->sub, a->nq, a->nrows, a->K)) return -1;
+    if (!a->dig || !a->kb || !a->ka || !a->out0 || !a->out1 || !a->rows || !a->pr) return -1;
+    if (a->nq > 0 && (!a->c0 || !a->pmod || !a->pmods)) return -1;
+    if (a->nrows == 0) return 0;
+    hipLaunchKernelGGL(pack_dot_k, dim3((1 << LOGN) / (PBX * 4), a->nrows, a->K), dim3(PBX), 0, (hipStream_t)s, *a,
+                       LOGN);
+    return launch_rc();
+}
+
 // ------------------------------------------------------------------------------------------------ key generation
 // b = e - a s_new + [id < nq and digit_of[id] == d] (P mod q_id) s_old' (s_old' = s_old^2 when sq), a from the KSKA
 // expander; b dense or bit-packed (the little-endian value stream, the guard words past N bits / 32 zeroed).
@@ -906,6 +994,8 @@ int ksk_unpack(const KskUnpackArgs* a, pc_stream_t s) {
     int ks_dot_key_##L(const KsKeyArgs* a, pc_stream_t s) { return ks::ks_dot_key<L>(a, s); }                \
     int ksk_expand_##L(const KskExpandArgs* a, pc_stream_t s) { return ks::ksk_expand<L>(a, s); }            \
     int encrypt_##L(const EncryptArgs* a, pc_stream_t s) { return ks::encrypt<L>(a, s); }                     \
+    int pack_split_##L(const PackSplitArgs* a, pc_stream_t s) { return ks::pack_split<L>(a, s); }            \
+    int pack_dot_##L(const PackDotArgs* a, pc_stream_t s) { return ks::pack_dot<L>(a, s); }                  \
     int ksk_gen_##L(const KskGenArgs* a, pc_stream_t s) { return ks::ksk_gen<L>(a, s); }                     \
     int ksk_unpack_##L(const KskUnpackArgs* a, pc_stream_t s) { return ks::ksk_unpack<L>(a, s); }
 PCH_KS_INST(12)

@@ -206,3 +206,27 @@ def test_pt_dot_launcher_checks():
     assert abi.call("pt_dot", a, log_n=12) == -1    # more than 8 ciphertexts
     a.K = 1
     assert abi.call("pt_dot", a, log_n=12) == -1    # null operands
+
+
+def test_pack_launcher_checks():
+    """pack_split / pack_dot (crates/pc-kernels/kernels/ks.cuh:949-963): sub a power of two in 2..16, nq <= nrows."""
+    from perseus_amd import abi
+    a = abi.PackSplitArgs()
+    a.K, a.nq, a.nrows = 1, 2, 4
+    for sub in (1, 3, 32):
+        a.sub = sub
+        assert abi.call("pack_split", a, log_n=12) == -1
+    a.sub, a.nq = 4, 5
+    assert abi.call("pack_split", a, log_n=12) == -1
+    d = abi.PackDotArgs()
+    d.K, d.sub, d.nq, d.nrows = 1, 4, 2, 4
+    assert abi.call("pack_dot", d, log_n=12) == -1   # null operands
+
+
+def test_tensor_multi_launcher_checks():
+    from perseus_amd import abi
+    a = abi.TensorMultiArgs()
+    a.nout, a.npairs = 5, 1
+    assert abi.call("tensor_multi", a, log_n=12) == -1   # more than 4 outputs
+    a.nout, a.npairs = 1, 33
+    assert abi.call("tensor_multi", a, log_n=12) == -1   # more than 32 pairs

@@ -509,3 +509,81 @@ def test_pt_dot(stream, name, enc, K):
     q = [ch.primes[t] for t in rows]
     want = em.pt_dot(q, rot[:, :, :, rows], pts, B, G, npts, enc, list(range(n)))
     assert (got[:, :, :, rows] == want).all()
+
+
+# ----------------------------------------------------------------------------------------------- subring switch
+@pytest.mark.parametrize("name,sub,K", [("small31", 4, 2), ("small", 16, 1), ("c3", 2, 1)])
+def test_pack(stream, name, sub, K):
+    say(f"[pack_split / pack_dot] {name} sub={sub} K={K}")
+    ch, ctx, _ = contexts(name)
+    rng = np.random.default_rng(sub * 5 + K)
+    nq = len(ch.q) - 1 if name == "c3" else 4
+    kp = len(ch.p)
+    rows = list(range(nq)) + [len(ch.q) + j for j in range(kp)]
+    n, N = len(rows), ch.n
+    # split: Q rows from one buffer, special rows from another
+    xq = np.stack([np.stack([rng.integers(0, ch.primes[t], N) for t in rows[:nq]]) for _ in range(K)]).astype(np.uint32)
+    xp = np.stack([np.stack([rng.integers(0, ch.primes[t], N) for t in rows[nq:]]) for _ in range(K)]).astype(np.uint32)
+    bq, bp = pa.DevBuf.from_array(xq), pa.DevBuf.from_array(xp)
+    dig = pa.DevBuf(K * sub * n * N)
+    a = abi.PackSplitArgs()
+    a.q, a.p, a.out = bq.ptr.value, bp.ptr.value, dig.ptr.value
+    a.q_stride, a.p_stride, a.out_stride = nq * N, kp * N, sub * n * N
+    a.K, a.sub, a.nq, a.nrows = K, sub, nq, n
+    run("pack_split", a, stream, ch.logn)
+    got = dig.download((K, sub, n, N))
+    for c in range(K):
+        assert (got[c] == em.pack_split(np.concatenate([xq[c], xp[c]]), sub)).all(), c
+    # dot: the digits (taken as evaluation-form words) against a random pack key; c0 and outputs in prime-id rows
+    q = [ch.primes[t] for t in rows]
+    kb = np.stack([np.stack([rng.integers(0, p, N) for p in q]) for _ in range(sub)]).astype(np.uint32)
+    ka = np.stack([np.stack([rng.integers(0, p, N) for p in q]) for _ in range(sub)]).astype(np.uint32)
+    c0 = np.zeros((K, ch.rows, N), np.uint32)
+    for t in range(ch.rows):
+        c0[:, t] = rng.integers(0, ch.primes[t], (K, N))
+    big_p = 1
+    for x in ch.p:
+        big_p *= int(x)
+    pm = [big_p % int(p) for p in ch.primes]
+    pmv, pms = consts(ch, pm)
+    bkb, bka, bc0 = pa.DevBuf.from_array(kb), pa.DevBuf.from_array(ka), pa.DevBuf.from_array(c0)
+    brows = pa.DevBuf.from_array(np.array(rows, np.uint32))
+    o0, o1 = pa.DevBuf(K * ch.rows * N), pa.DevBuf(K * ch.rows * N)
+    d = abi.PackDotArgs()
+    d.dig, d.kb, d.ka, d.c0, d.out0, d.out1 = dig.ptr.value, bkb.ptr.value, bka.ptr.value, bc0.ptr.value, \
+        o0.ptr.value, o1.ptr.value
+    d.rows, d.pmod, d.pmods, d.pr = brows.ptr.value, pmv.ptr.value, pms.ptr.value, pr_of(ctx)
+    d.dig_stride, d.ct_stride, d.out_ct_stride = sub * n * N, ch.rows * N, ch.rows * N
+    d.K, d.sub, d.nq, d.nrows = K, sub, nq, n
+    run("pack_dot", d, stream, ch.logn)
+    g0, g1 = o0.download((K, ch.rows, N)), o1.download((K, ch.rows, N))
+    for c in range(K):
+        w0, w1 = em.pack_dot(q, got[c], kb, ka, c0[c][rows], [pm[t] for t in rows], nq)
+        assert (g0[c][rows] == w0).all() and (g1[c][rows] == w1).all(), c
+
+
+@pytest.mark.parametrize("nout,npairs,acc", [(3, 20, 0), (1, 32, 2), (4, 5, 1)])
+def test_tensor_multi(stream, nout, npairs, acc):
+    name = "small31"
+    say(f"[tensor_multi] {name} nout={nout} npairs={npairs} acc={acc}")
+    ch, ctx, _ = contexts(name)
+    rng = np.random.default_rng(nout * 100 + npairs + acc)
+    K, n, q = 1, 4, ch.primes
+    # a small pool of operands shared across the outputs' lists
+    pool = [Cts(ch, K, n, rng) for _ in range(6)]
+    pick = rng.integers(0, len(pool), (nout, npairs, 2))
+    outs, d2s = [Cts(ch, K, n, rng) for _ in range(nout)], [Cts(ch, K, n, rng) for _ in range(nout)]
+    a = abi.TensorMultiArgs()
+    for o in range(nout):
+        a.out[o], a.d2[o] = outs[o].ref(), d2s[o].ref()
+        for j in range(npairs):
+            a.a[o][j], a.b[o][j] = pool[pick[o, j, 0]].ref(), pool[pick[o, j, 1]].ref()
+    a.pr, a.nout, a.npairs, a.acc, a.n, a.K = pr_of(ctx), nout, npairs, acc, n, K
+    sl = lambda c: c.host[:, :, :n]  # noqa: E731
+    want = [em.tensor(q, [(sl(pool[pick[o, j, 0]]), sl(pool[pick[o, j, 1]])) for j in range(npairs)], sl(outs[o]),
+                      d2s[o].host[:, 1, :n], acc != 0, (acc & 2) != 0) for o in range(nout)]
+    run("tensor_multi", a, stream, ch.logn)
+    for o in range(nout):
+        got, gd2 = outs[o].get(), d2s[o].get()
+        assert (got[:, 0, :n] == want[o][0]).all() and (got[:, 1, :n] == want[o][1]).all(), o
+        assert (gd2[:, 1, :n] == want[o][2]).all(), o

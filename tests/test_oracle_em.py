@@ -387,3 +387,35 @@ def test_pt_dot_decrypts_to_the_diagonal_products(enc):
                 if B * j + b < npts:
                     want = addq(want, mulq(dec(Q, rot[c, b, 0], rot[c, b, 1], s), full[B * j + b], Q), Q)
             assert (dec(Q, res[c, j, 0], res[c, j, 1], s) == want % qq).all()
+
+
+# ----------------------------------------------------------------------------------------------- subring switch
+@pytest.mark.parametrize("sub", [2, 4, 16])
+def test_pack_split_partitions_the_coefficients(sub):
+    """The digits sum back to the row, and digit j vanishes off the exponents = j mod sub."""
+    x = rand_ct(Q, 1, 4, N)[0, 0]
+    d = em.pack_split(x, sub)
+    assert (d.astype(np.uint64).sum(0) == x).all()
+    for j in range(sub):
+        off = (np.arange(N) % sub) != j
+        assert (d[j][:, off] == 0).all()
+
+
+def test_pack_dot_decrypts_to_the_errors():
+    """With a pack key b_j = e_j - a_j s, Dec(s0, s1) = s0 + s1 s = sum_j D_j e_j + pmod c0 on the Q rows (and without
+    the c0 term on the others): a swapped a / b or a dropped digit breaks it."""
+    n, sub, nq = 4, 4, 3
+    s = secret(Q, n, N)
+    qq = np.asarray(Q[:n], np.uint64).reshape(n, 1)
+    dig = np.stack([rand_ct(Q, 1, n, N)[0, 0] for _ in range(sub)])
+    ka = np.stack([rand_ct(Q, 1, n, N)[0, 0] for _ in range(sub)])
+    e = RNG.integers(0, 8, (sub, n, N)).astype(np.uint64)
+    kb = ((e + qq - mulq(ka, s, Q)) % qq).astype(np.uint32)
+    c0 = rand_ct(Q, 1, n, N)[0, 0]
+    pmod = [int(RNG.integers(0, q)) for q in Q[:n]]
+    s0, s1 = em.pack_dot(Q, dig, kb, ka, c0, pmod, nq)
+    want = np.zeros((n, N), np.uint64)
+    for j in range(sub):
+        want = addq(want, mulq(dig[j], e[j], Q), Q)
+    want[:nq] = addq(want[:nq], mulq(c0[:nq], np.array(pmod[:nq], np.uint64).reshape(nq, 1).repeat(N, 1), Q), Q)
+    assert (addq(s0, mulq(s1, s, Q), Q) == want).all()

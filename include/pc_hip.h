@@ -800,6 +800,9 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
  * by key 0 of k (the relinearization key: galois 1) and added: out = (c0, c1) + ModDown(dot(ModUp(d2))) on Q rows
  * 0..top (degree 2, rescale pending). out may be a or b. */
 int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);
+/* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
+ * form rows by prime id (rows 0..top read). out may be ct. */
+int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);
 /* the stages alone, for tests and profiles: ModUp of ct's c1 into the context's digit workspace; the dot of key r
  * into ext (one extended ciphertext); ModDown of ext into out */
 int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);

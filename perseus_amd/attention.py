@@ -1,0 +1,89 @@
+"""Encrypted attention scoring for a GPT-2-small-shaped decode step (12 heads of 64 dimensions, d_model 768, a KV cache
+of 512 tokens): the keys K live encrypted in HBM, the query q is a plaintext, and the scores s[h][t] = sum_d q[h][d]
+K[t][64 h + d] come out encrypted, one per slot. The operation sequence is the reference's scoring recipe
+(crates/pc-gpu/src/ops.rs:927-951 mult_pt, crates/pc-gpu/src/rescale.rs:230-264, crates/pc-gpu/src/rotate.rs:924-992
+rotate_and_sum): per ciphertext a plaintext product, a two-prime rescale back to the ciphertext's scale, and the
+log-step rotate-and-sum over each 64-slot head block.
+
+Packing (complex, two real vectors per ciphertext): N/2 = 2^15 slots hold 512 blocks of 64; ciphertext c carries heads
+2c and 2c + 1, block (hl, t) = 256 hl + t for t < 256, its real part token t and its imaginary part token t + 256, slot
+64 block + d the key's dimension d. The query plaintext repeats q[h] over its head's blocks (a real multiplier, so it
+scales both parts alike). After the sums, slot 64 block holds s[h][t] + i s[h][t + 256]."""
+import numpy as np
+
+HEADS, HEAD_DIM, TOKENS = 12, 64, 512
+BLOCK = HEAD_DIM
+HEADS_PER_CT = 2
+TOK_PER_PART = TOKENS // 2
+
+
+def n_cts():
+    return HEADS // HEADS_PER_CT
+
+
+def key_slots(K, n):
+    """The ciphertexts' slot vectors (N/2 complex each) of the key matrix K [TOKENS][HEADS * HEAD_DIM]."""
+    assert n // 2 == HEADS_PER_CT * TOK_PER_PART * BLOCK, "the packing fills N/2 slots at N = 2^16"
+    out = []
+    for c in range(n_cts()):
+        z = np.zeros(n // 2, np.complex128)
+        for hl in range(HEADS_PER_CT):
+            h = HEADS_PER_CT * c + hl
+            blk = K[:, h * HEAD_DIM:(h + 1) * HEAD_DIM]  # [TOKENS][64]
+            part = blk[:TOK_PER_PART] + 1j * blk[TOK_PER_PART:]
+            z[hl * TOK_PER_PART * BLOCK:(hl + 1) * TOK_PER_PART * BLOCK] = part.reshape(-1)
+        out.append(z)
+    return out
+
+
+def query_slots(q, n):
+    """The plaintexts' slot vectors (real) of the query q [HEADS][HEAD_DIM], one per ciphertext."""
+    out = []
+    for c in range(n_cts()):
+        z = np.zeros(n // 2, np.float64)
+        for hl in range(HEADS_PER_CT):
+            h = HEADS_PER_CT * c + hl
+            z[hl * TOK_PER_PART * BLOCK:(hl + 1) * TOK_PER_PART * BLOCK] = np.tile(q[h], TOK_PER_PART)
+        out.append(z)
+    return out
+
+
+def scores_from_slots(zs):
+    """s [HEADS][TOKENS] from the decrypted, decoded slot vectors of the ciphertexts."""
+    s = np.zeros((HEADS, TOKENS))
+    for c, z in enumerate(zs):
+        for hl in range(HEADS_PER_CT):
+            h = HEADS_PER_CT * c + hl
+            v = z[hl * TOK_PER_PART * BLOCK:(hl + 1) * TOK_PER_PART * BLOCK:BLOCK]
+            s[h, :TOK_PER_PART] = v.real
+            s[h, TOK_PER_PART:] = v.imag
+    return s
+
+
+def score(ctx, keys, ct, pt, top, out, tmp, stream):
+    """One ciphertext's scores: out = rotate_and_sum(rescale(ct pt)) over the head blocks at limb top - 2; keys holds
+    the rotations by 1, 2, ..., 32. ct is left untouched; out and tmp are single ciphertexts (tmp: the ladder's
+    scratch)."""
+    ctx.mul_plain(ct, pt, top, out, stream)
+    ctx.rescale(out, top, 2, out, stream)
+    ctx.rotate_and_sum(keys, out, top - 2, 1, BLOCK, out, tmp, stream)
+
+
+def score_streams(lanes, cts, pts, top, outs, main):
+    """The scorings of independent ciphertexts side by side: lane i = (context, keys, stream, tmp) takes ciphertexts
+    i, i + len(lanes), ...; each lane has its own context (its own workspace), so the lanes' small kernels overlap on
+    the chip. Ordered after the work already on `main`, and `main` waits for every lane."""
+    from .engine import Event
+
+    start = Event()
+    start.record(main)
+    ends = []
+    for i, (ctx, keys, st, tmp) in enumerate(lanes):
+        st.wait(start)
+        for c in range(i, len(cts), len(lanes)):
+            score(ctx, keys, cts[c], pts[c], top, outs[c], tmp, st)
+        e = Event()
+        e.record(st)
+        ends.append(e)
+    for e in ends:
+        main.wait(e)

@@ -1429,4 +1429,20 @@ int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top
     return moddown(c, c->ext, c->conv, 1, top, out, s, out);
 }
 
+// The plaintext product (crates/pc-gpu/src/ops.rs:927-951 mult_pt, the table's mul_table, em.cuh:508-515): out = ct pt
+// on Q rows 0..top of both parts, pt one plaintext of evaluation-form rows by prime id. out may be ct.
+int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s) {
+    if (!c || !ct || !pt || !out || top < 0 || top >= c->nq) return -1;
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    MulTableArgs m;
+    memset(&m, 0, sizeof m);
+    m.out = PolyRef{out, 2 * part, part};
+    m.in = PolyRef{const_cast<void*>(ct), 2 * part, part};
+    m.t = pt;
+    m.pr = c->pr;
+    m.n = top + 1;
+    m.K = 1;
+    return c->tab->mul_table(&m, s);
+}
+
 }  // extern "C"

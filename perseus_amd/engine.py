@@ -26,6 +26,10 @@ class Stream:
     def sync(self):
         check(LIB.pc_hip_stream_sync(self.h), "stream_sync")
 
+    def wait(self, event):
+        """Later work on this stream waits for the event (recorded on another stream)."""
+        check(LIB.pc_hip_stream_wait_event(self.h, event.h), "stream_wait_event")
+
     def __del__(self):
         if getattr(self, "h", None):
             LIB.pc_hip_stream_destroy(self.h)
@@ -52,6 +56,33 @@ class Event:
         if getattr(self, "h", None):
             LIB.pc_hip_event_destroy(self.h)
             self.h = None
+
+
+class Graph:
+    """A HIP graph of the work fn() enqueues on `stream` (stream capture; the launchers and the driver are capture
+    safe: they never allocate, synchronise or read device data on the host), replayed by launch(). Launch-bound
+    sequences of small kernels (a ladder of single key switches at a few limbs) pay their launch costs once."""
+
+    def __init__(self, stream, fn):
+        self.graph, self.exe = C.c_void_p(), C.c_void_p()
+        check(LIB.pc_hip_graph_begin_capture(stream.h), "graph_begin_capture")
+        try:
+            fn()
+        finally:
+            rc = LIB.pc_hip_graph_end_capture(stream.h, C.byref(self.graph))
+        check(rc, "graph_end_capture")
+        check(LIB.pc_hip_graph_instantiate(C.byref(self.exe), self.graph), "graph_instantiate")
+
+    def launch(self, stream):
+        check(LIB.pc_hip_graph_launch(self.exe, stream.h), "graph_launch")
+
+    def __del__(self):
+        if getattr(self, "exe", None) and self.exe.value:
+            LIB.pc_hip_graph_exec_destroy(self.exe)
+            self.exe = None
+        if getattr(self, "graph", None) and self.graph.value:
+            LIB.pc_hip_graph_destroy(self.graph)
+            self.graph = None
 
 
 class DevBuf:
@@ -187,6 +218,10 @@ class Context:
     def rescale(self, ct, top, ndrop, out, stream):
         """out's rows 0..top - ndrop = the rescale of ct by its top ndrop (1 or 2) primes (pcx_rescale)."""
         check(LIB.pcx_rescale(self.h, ct.addr(), top, ndrop, out.addr(), stream.h), "rescale")
+
+    def mul_plain(self, ct, pt, top, out, stream):
+        """out = ct pt on Q rows 0..top (pcx_mul_plain); pt a DevBuf of evaluation-form rows by prime id."""
+        check(LIB.pcx_mul_plain(self.h, ct.addr(), pt.addr(), top, out.addr(), stream.h), "mul_plain")
 
     def mul_relin(self, keys, a, b, top, out, stream):
         """out = a b relinearized by key 0 of keys (pcx_mul_relin)."""

@@ -29,15 +29,12 @@ def stream():
     return pa.Stream()
 
 
-STEPS = [1, 2, 4, 8, 16, 32]
-
-
-def setup(ch, ctx, oc, seed=2025):
+def setup(ch, ctx, oc, seed=2025, radix_bits=attention.RADIX_BITS):
     n, top = ch.n, len(ch.q) - 1
     g = twin.Prng([seed, 1, 2, 3, 4, 5, 6, 7], 0)
     s = g.sparse_ternary(n, 192)
     s_eval = oc.secret_eval(s)
-    gals = [twin.rotation_galois(r, n) for r in STEPS]
+    gals = [twin.rotation_galois(r, n) for r in attention.ladder_steps(radix_bits)]
     seeds = np.stack([g.ksk_seed() for _ in gals])
     errs = np.stack([np.stack([g.gaussian(n) for _ in range(ch.dnum)]) for _ in gals])
     keys = pa.Keys(ctx, gals, seeds=seeds, secret=s, errors=errs)
@@ -61,18 +58,19 @@ def setup(ch, ctx, oc, seed=2025):
     return dict(s_eval=s_eval, gals=gals, seeds=seeds, keys=keys, cts=cts, pts=pts, want=want, delta=delta, top=top)
 
 
-def test_attention_scores_decrypt_and_match_the_oracle(stream):
-    say("[attention] c4: 6 ciphertexts, mul_plain -> rescale -> rotate_and_sum(1..32)")
+@pytest.mark.parametrize("radix_bits", [1, 2, 3])
+def test_attention_scores_decrypt_and_match_the_oracle(stream, radix_bits):
+    say(f"[attention] c4: 6 ciphertexts, mul_plain -> rescale -> rotate_and_sum over 64 slots, radix 2^{radix_bits}")
     ch = pa.preset("c4")
     ctx = pa.Context(ch, k_rot=1)
     oc = twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum)
-    S = setup(ch, ctx, oc)
+    S = setup(ch, ctx, oc, radix_bits=radix_bits)
     top, n = S["top"], ch.n
     outs = []
     tmp = ctx.ct_buf(1)
     for ct, pt in zip(S["cts"], S["pts"]):
         bct, bpt, out = pa.DevBuf.from_array(ct), pa.DevBuf.from_array(pt), ctx.ct_buf(1)
-        attention.score(ctx, S["keys"], bct, bpt, top, out, tmp, stream)
+        attention.score(ctx, S["keys"], bct, bpt, top, out, tmp, stream, radix_bits)
         stream.sync()
         outs.append(out.download((2, ch.rows, n)))
     zs = []
@@ -88,8 +86,8 @@ def test_attention_scores_decrypt_and_match_the_oracle(stream):
     prod = oc.ct_zeros()
     prod[:, : top + 1] = em.mul_add_n(ch.primes, [(x[None, :, : top + 1], S["pts"][0])])[0]
     rs = oc.rescale(prod, top, 2)
-    bs = [S["keys"].download_b(i) for i in range(len(STEPS))]
-    want0 = oc.rotate_and_sum(rs, top - 2, 1, attention.BLOCK, S["seeds"], bs, S["gals"])
+    bs = [S["keys"].download_b(i) for i in range(len(S["gals"]))]
+    want0 = oc.rotate_and_sum(rs, top - 2, 1, attention.BLOCK, S["seeds"], bs, S["gals"], radix_bits)
     assert (outs[0][:, : top - 1] == want0[:, : top - 1]).all()
 
 

@@ -53,6 +53,11 @@ int ks_dot_patched(int logn, const KsKeyArgs* g, const PatchTab* P, pc_stream_t 
 // two sources r (ndrop 2) names, top - rprime[i] and top - 1 - rprime[i] rows above row i; a's epilogue applies
 int ntt_fwd_rescale(int logn, const NttArgs* a, const RescaleArgs* r, pc_stream_t s);
 
+// The one-pass transforms of N = 2^16 (ntt1.hip): one 1024-thread workgroup per row of rows [r0, r0 + n) of a
+// (checked by the caller), the forward with a's epilogue, the inverse with its es / N^-1 scale.
+void ntt1_fwd(const NttArgs& a, int r0, int n, pc_stream_t st);
+void ntt1_inv(const NttArgs& a, int r0, int n, pc_stream_t st);
+
 // ks_dot_key's summed rotations (c0_mode | KS_SUM): out = sum_r sigma_r(dot_r), gathered in output order
 int ks_dot_key_sum(int logn, const KsKeyArgs* g, pc_stream_t s);
 

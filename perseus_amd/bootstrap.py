@@ -1,0 +1,726 @@
+"""Full-slot CKKS bootstrap (N/2 complex slots): ModRaise -> CoeffToSlot -> EvalMod -> SlotToCoeff, the composite of
+the reference's dense route (crates/pc-gpu/src/bts/dense.rs:1-9: mod_raise, CtS x4 as BSGS linear transforms, EvalMod
+as a Chebyshev series plus double angles on the real and imaginary parts, StC x3), built on this engine's device
+operations. The constants are this module's own (host, float64); the linear-transform factors follow the published
+special FFT of CKKS (the decoding map z_j = sum_i w_i zeta^(5^j i) factored into log2(N/2) butterfly layers, the
+factorisation OpenFHE's collapsed FFT also uses: crates/pc-core/src/bts_setup.rs:366-435 CoeffEncodingOneLevel /
+CoeffDecodingOneLevel).
+
+Scale bookkeeping. Every ciphertext carries its scale as a float (the slot values are decode(P) / scale). A linear
+transform level encodes its diagonals at scale q_a q_b g (q_a q_b the two primes the rescale after it drops, g the
+level's gain), so the rescale leaves the values as transformed and multiplies the scale by g exactly. In EvalMod every
+addition joins ciphertexts of the same scale: a term that would arrive at another scale is first multiplied by an
+integer constant chosen for the target scale and rescaled (the targets are propagated top-down through the Chebyshev
+evaluation, as Lattigo's polynomial evaluator does), so no scale mismatch ever enters a sum.
+
+The composite is written against an operations object (`ops`): `GpuOps` below runs it on the device through the
+engine; the tests run the same composite on the oracle's operations and compare the words.
+"""
+import math
+
+import numpy as np
+
+# ----------------------------------------------------------------------------------------------- special FFT layers
+
+
+def rot_group(n):
+    """5^j mod 4n, j < n: slot j sits at the root zeta^(5^j), zeta = exp(2 pi i / 4n)."""
+    g = np.empty(n, np.int64)
+    v = 1
+    for j in range(n):
+        g[j] = v
+        v = v * 5 % (4 * n)
+    return g
+
+
+def _layer_w(n, ln):
+    """The twiddles of the butterfly layer of blocks of 2^ln slots, per slot of the first half of each block."""
+    m, length = 4 * n, 1 << ln
+    lenh, lenq = length >> 1, length << 2
+    k = np.arange(n)
+    pos = k % length
+    first = pos < lenh
+    j = np.where(first, pos, pos - lenh)
+    idx = (rot_group(n)[j] % lenq) * (m // lenq)
+    return first, np.exp(2j * np.pi * idx / m), lenh
+
+
+def layer(n, ln):
+    """Decoding layer (blocks of 2^ln): u, v -> u + w v, u - w v, as diagonals {offset: vector} over n slots
+    (y[k] = sum_d D_d[k] x[(k + d) mod n])."""
+    first, w, lenh = _layer_w(n, ln)
+    return {0: np.where(first, 1.0, -w).astype(complex), lenh: np.where(first, w, 0).astype(complex),
+            -lenh: np.where(first, 0, 1).astype(complex)}
+
+
+def layer_inv(n, ln):
+    """Inverse of `layer`: y_top, y_bot -> (y_top + y_bot) / 2, (y_top - y_bot) / (2 w)."""
+    first, w, lenh = _layer_w(n, ln)
+    iw = 1.0 / (2.0 * w)
+    return {0: np.where(first, 0.5, -iw).astype(complex), lenh: np.where(first, 0.5, 0).astype(complex),
+            -lenh: np.where(first, 0, iw).astype(complex)}
+
+
+def _norm(d, n):
+    d %= n
+    return d - n if d > n // 2 else d
+
+
+def compose(a, b, n):
+    """Diagonals of A o B (B applied first)."""
+    out = {}
+    for da, va in a.items():
+        for db, vb in b.items():
+            d = _norm(da + db, n)
+            t = va * np.roll(vb, -da)
+            out[d] = out[d] + t if d in out else t
+    return out
+
+
+def apply_diags(diags, x):
+    """y = sum_d D_d * rot(x, d) on plain slot vectors (rot(x, d)[k] = x[k + d])."""
+    y = np.zeros_like(x, dtype=complex)
+    for d, v in diags.items():
+        y += v * np.roll(x, -d)
+    return y
+
+
+def bitrev(n):
+    b = n.bit_length() - 1
+    return np.array([int(format(i, f"0{b}b")[::-1], 2) for i in range(n)], np.int64)
+
+
+def cts_levels(n, sizes):
+    """The CoeffToSlot levels: the inverse layers applied from blocks of n down to blocks of 2, grouped `sizes` (sum =
+    log2 n) in order of application; the product of all is the inverse decoding map up to the bit reversal
+    (slots come out bit-reversed)."""
+    assert sum(sizes) == n.bit_length() - 1
+    lns = list(range(n.bit_length() - 1, 0, -1))
+    out, i = [], 0
+    for s in sizes:
+        acc = None
+        for ln in lns[i:i + s]:
+            L = layer_inv(n, ln)
+            acc = L if acc is None else compose(L, acc, n)
+        out.append(acc)
+        i += s
+    return out
+
+
+def stc_levels(n, sizes):
+    """The SlotToCoeff levels: the decoding layers applied from blocks of 2 up to blocks of n, grouped `sizes`; their
+    product takes bit-reversed slots to the decoding of the coefficients."""
+    assert sum(sizes) == n.bit_length() - 1
+    lns = list(range(1, n.bit_length()))
+    out, i = [], 0
+    for s in sizes:
+        acc = None
+        for ln in lns[i:i + s]:
+            L = layer(n, ln)
+            acc = L if acc is None else compose(L, acc, n)
+        out.append(acc)
+        i += s
+    return out
+
+
+class BsgsPlan:
+    """A level y = sum_d D_d rot(x, d), offsets d = k s with k in [k0, k1] (each offset reduced into (-n/2, n/2]), as
+    baby-step giant-step: k - k0 = B j + i, y = sum_j rot(sum_i D'_{j,i} rot(x, i s), g_j s), g_j = B j + k0,
+    D'_{j,i} = rot(D_{(g_j + i) s}, -g_j s)."""
+
+    def __init__(self, diags, n, B=None):
+        offs = [d for d, v in diags.items() if np.abs(v).max() > 0]
+        s = 0
+        for d in offs:
+            s = math.gcd(s, abs(d))
+        s = s or 1
+        ks = sorted(d // s for d in offs)
+        k0, k1 = ks[0], ks[-1]
+        self.n, self.s, self.k0, self.k1 = n, s, k0, k1
+        width = k1 - k0 + 1
+        self.B = B or (1 << max(1, (width.bit_length() + 1) // 2))
+        self.G = -(-width // self.B)
+        self.baby = [i * s for i in range(self.B)]
+        self.giant = [(self.B * j + k0) * s for j in range(self.G)]
+        self.pts = []  # [j][i] the pre-rotated diagonal or None
+        for j in range(self.G):
+            row = []
+            for i in range(self.B):
+                k = self.B * j + k0 + i
+                v = diags.get(k * s) if k <= k1 else None
+                row.append(None if v is None or np.abs(v).max() == 0 else np.roll(v, self.giant[j]))
+            self.pts.append(row)
+
+    def apply(self, x):
+        """plain evaluation in BSGS order (the check of the decomposition)"""
+        rots = [np.roll(x, -b) for b in self.baby]
+        y = np.zeros(self.n, complex)
+        for j in range(self.G):
+            acc = np.zeros(self.n, complex)
+            for i in range(self.B):
+                if self.pts[j][i] is not None:
+                    acc += self.pts[j][i] * rots[i]
+            y += np.roll(acc, -self.giant[j])
+        return y
+
+    def steps(self):
+        """the rotation steps the level takes (babies, then giants), reduced to (0, n)"""
+        out = []
+        for r in self.baby[1:] + self.giant:
+            r %= self.n
+            if r and r not in out:
+                out.append(r)
+        return out
+
+
+# ----------------------------------------------------------------------------------------------- Chebyshev series
+
+
+def cheb_coeffs(f, deg):
+    """Chebyshev interpolant of f on [-1, 1] at the deg + 1 Chebyshev nodes: p(u) = sum_k c_k T_k(u)."""
+    return np.polynomial.chebyshev.chebinterpolate(f, deg)
+
+
+def cheb_split(c, g):
+    """p = q T_g + r for p = sum_k c_k T_k of degree < 2g: T_{g + j} = 2 T_g T_j - T_{g - j}."""
+    c = list(c)
+    r = c[:g] + [0.0] * max(0, g - len(c))
+    q = [0.0] * max(1, len(c) - g)
+    for j in range(len(c) - g):
+        v = c[g + j]
+        if j == 0:
+            q[0] += v
+        else:
+            q[j] += 2 * v
+            r[g - j] -= v
+    return np.array(q), np.array(r)
+
+
+def cheb_eval(c, u):
+    return np.polynomial.chebyshev.chebval(u, c)
+
+
+class EvalModPlan:
+    """y -> sin(2 pi y) / (2 pi)... as cos(2 pi (y - 1/4) / 2^r) on |y| <= K, a Chebyshev series in u = y / K of degree
+    `deg`, then r double angles (cos 2t = 2 cos^2 t - 1): the output is cos(2 pi (y - 1/4)) = sin(2 pi y)."""
+
+    def __init__(self, K=32, deg=63, r=3):
+        self.K, self.deg, self.r = K, deg, r
+        self.c = cheb_coeffs(lambda u: np.cos(2 * np.pi * (K * u - 0.25) / (1 << r)), deg)
+
+    def plain(self, u):
+        h = cheb_eval(self.c, u)
+        for _ in range(self.r):
+            h = 2 * h * h - 1
+        return h
+
+
+# ----------------------------------------------------------------------------------------------- parameters
+
+
+class Params:
+    """Bootstrap shape: slots n = N/2; CtS / StC level sizes (layers per level); EvalMod's K, degree, double angles;
+    the input's message scale; the output scale is whatever the chain leaves (reported)."""
+
+    def __init__(self, logn, cts=None, stc=None, K=32, deg=63, r=3, delta_in=2.0 ** 20, target=2.0 ** 60):
+        self.logn, self.N, self.n = logn, 1 << logn, 1 << (logn - 1)
+        L = logn - 1
+        self.cts = cts or _split(L, 4)
+        self.stc = stc or _split(L, 3)
+        self.K, self.deg, self.r = K, deg, r
+        self.delta_in, self.target = delta_in, target
+
+    def levels_used(self):
+        """composite (two-prime) levels the bootstrap consumes after ModRaise"""
+        return len(self.cts) + 7 + self.r + len(self.stc)
+
+
+def _split(L, k):
+    base, extra = divmod(L, k)
+    return [base + (1 if i < extra else 0) for i in range(k)]
+
+
+def simulate(P, par, em=None):
+    """Plain float simulation of the bootstrap's algorithm on an integer coefficient vector P (= m + q0 I after the raise,
+    here given directly) whose decoding the ciphertext holds: returns the output slot values (the decoding of
+    q0 / (2 pi) sin(2 pi P / q0), i.e. of m when |m| << q0) -- the check that the factors, the BSGS split and the
+    EvalMod series compose to the bootstrap. q0 is taken as 1 (P given as P / q0)."""
+    n = par.n
+    em = em or EvalModPlan(par.K, par.deg, par.r)
+    from .encoding import decode
+
+    z = decode(P, par.N, 1.0)  # slots of P / q0
+    x = z / (2.0 * par.K)
+    for lv in cts_levels(n, par.cts):
+        x = BsgsPlan(lv, n).apply(x)
+    re, im = x + np.conj(x), -1j * (x - np.conj(x))
+    s_re, s_im = em.plain(re.real), em.plain(im.real)
+    w = (s_re + 1j * s_im) / (2 * np.pi)
+    for lv in stc_levels(n, par.stc):
+        w = BsgsPlan(lv, n).apply(w)
+    return w
+
+
+# ----------------------------------------------------------------------------------------------- host encoding
+
+
+def residues(f, primes):
+    """Exact residues [len(primes)][N] (u32) of the integers nearest the float coefficients f (|f| < 2^85): f rounded,
+    split f = a 2^32 + b with both parts exact in float64, then (a mod p) (2^32 mod p) + b mod p in int64."""
+    f = np.rint(np.asarray(f, np.float64))
+    a = np.floor(f / 4294967296.0)
+    b = (f - a * 4294967296.0).astype(np.int64)
+    a = a.astype(np.int64) if np.abs(a).max(initial=0) < 2.0 ** 62 else None
+    assert a is not None, "coefficient beyond 2^85"
+    out = np.empty((len(primes), f.shape[-1]), np.uint32)
+    for r, p in enumerate(primes):
+        p = int(p)
+        out[r] = ((a % p) * ((1 << 32) % p) % p + b % p) % p
+    return out
+
+
+def encode_rows(z, N, scale, primes):
+    """The plaintext of slot vector z (N/2 complex values) at `scale`, as coefficient residue rows over `primes`."""
+    from .encoding import encode
+
+    return residues(encode(z, N, scale), primes)
+
+
+def int_rows(k, primes):
+    """An integer constant (any size, any sign) as residues per prime (Python ints)."""
+    return [int(k) % int(p) for p in primes]
+
+
+# ----------------------------------------------------------------------------------------------- scale-tracked evaluator
+
+
+class Ct:
+    """A ciphertext handle of the operations object, its top limb and its scale (slot values = decode / scale)."""
+    __slots__ = ("h", "top", "scale")
+
+    def __init__(self, h, top, scale):
+        self.h, self.top, self.scale = h, top, scale
+
+
+class Evaluator:
+    def __init__(self, ops, primes):
+        self.ops, self.q = ops, [int(p) for p in primes]
+
+    def qq(self, top):
+        """the two primes the rescale from `top` drops"""
+        return float(self.q[top]) * float(self.q[top - 1])
+
+    def mul(self, a, b):
+        t = min(a.top, b.top)
+        out = self.ops.alloc()
+        self.ops.mul_relin(out, a.h, b.h, t)
+        self.ops.rescale2(out, out, t)
+        return Ct(out, t - 2, a.scale * b.scale / self.qq(t))
+
+    def mul_to(self, a, c, scale, top):
+        """c a landing exactly at (top, scale): a times the integer round(c scale q_a q_b / a.scale), rescaled"""
+        assert a.top - 2 >= top, (a.top, top)
+        k = int(round(c * scale * self.qq(a.top) / a.scale))
+        out = self.ops.alloc()
+        self.ops.mul_const(out, a.h, a.top, k)
+        self.ops.rescale2(out, out, a.top)
+        return Ct(out, top, scale)
+
+    def add(self, a, b, sub=False):
+        assert abs(a.scale / b.scale - 1.0) < 1e-9, (a.scale, b.scale)
+        t = min(a.top, b.top)
+        out = self.ops.alloc()
+        self.ops.add(out, a.h, b.h, t, sub)
+        return Ct(out, t, a.scale)
+
+    def add_const(self, a, c):
+        """in place: the constant c at a's scale added to every slot"""
+        self.ops.add_const(a.h, a.top, int(round(c * a.scale)))
+        return a
+
+    def double(self, a):
+        out = self.ops.alloc()
+        self.ops.add(out, a.h, a.h, a.top, False)
+        return Ct(out, a.top, a.scale)
+
+
+class ChebEval:
+    """p(u) = sum_k c_k T_k(u) of degree <= 63 on the ciphertext u: the power basis T_1..T_8, T_16, T_32 with every
+    T_{a+b} = 2 T_a T_b - T_{|a-b|} formed at one exact scale, then p split by T_32, T_16, T_8 down to leaves of
+    degree < 8 whose terms are each brought to the leaf's target (top, scale) by one constant product."""
+
+    BABY, GIANTS = 8, (8, 16, 32)
+
+    def __init__(self, ev):
+        self.ev = ev
+
+    def basis(self, u):
+        ev = self.ev
+        T = {1: u}
+
+        def make(a, b):
+            P = ev.mul(ev.double(T[a]), T[b])
+            if a == b:
+                return ev.add_const(P, -1.0)
+            return ev.add(P, ev.mul_to(T[a - b], 1.0, P.scale, P.top), sub=True)
+
+        for k, (a, b) in ((2, (1, 1)), (3, (2, 1)), (4, (2, 2)), (5, (3, 2)), (6, (3, 3)), (7, (4, 3)), (8, (4, 4)),
+                          (16, (8, 8)), (32, (16, 16))):
+            T[k] = make(a, b)
+        self.T = T
+        return T
+
+    def out_top(self):
+        """the top the series lands on: the leaves need a product below T_7's top, and three giant products follow"""
+        return self.T[7].top - 2 - 6
+
+    def eval(self, c, top, scale):
+        c = np.trim_zeros(np.asarray(c, np.float64), "b")
+        ev, T = self.ev, self.T
+        if len(c) <= self.BABY:
+            acc = None
+            for k in range(1, len(c)):
+                if c[k] == 0.0:
+                    continue
+                t = ev.mul_to(T[k], float(c[k]), scale, top)
+                acc = t if acc is None else ev.add(acc, t)
+            assert acc is not None, "a leaf with no term of degree >= 1"
+            return ev.add_const(acc, float(c[0]))
+        g = max(x for x in self.GIANTS if x < len(c))
+        q, r = cheb_split(c, g)
+        G = T[g]
+        assert G.top >= top + 2
+        Q = self.eval(q, top + 2, scale * ev.qq(top + 2) / G.scale)
+        P = ev.mul(Q, Ct(G.h, top + 2, G.scale))
+        return ev.add(P, self.eval(r, top, scale))
+
+
+# ----------------------------------------------------------------------------------------------- the composite
+
+
+class Bootstrap:
+    """ModRaise -> CtS (len(par.cts) levels) -> EvalMod (real and imaginary parts) -> StC (len(par.stc) levels) on
+    an operations object. `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
+    scale par.delta_in. Plaintexts (the levels' diagonals, the i monomial) are encoded once by `prepare`."""
+
+    def __init__(self, ops, par, primes):
+        self.ops, self.par = ops, par
+        self.q = [int(p) for p in primes]
+        self.T = len(self.q) - 1
+        n = par.n
+        self.cts = [BsgsPlan(lv, n) for lv in cts_levels(n, par.cts)]
+        self.stc = [BsgsPlan(lv, n) for lv in stc_levels(n, par.stc)]
+        self.em = EvalModPlan(par.K, par.deg, par.r)
+        self.ev = Evaluator(ops, self.q)
+        self.q0 = float(self.q[0])
+        # CtS: the raised ciphertext (values decode(P) / (2 q0 K), P = m + q0 I) is first multiplied by the integer
+        # c = 2^e that lifts its label 2 q0 K near par.target: the baby rotations' key-switch noise is added to
+        # integers that large, not to the raw P (about 2 q0 K); each level then multiplies the label by f so that the
+        # EvalMod input sits at par.target exactly
+        self.lift = 1 << max(0, int(math.floor(math.log2(par.target / (2.0 * self.q0 * par.K)))))
+        self.raise_scale = 2.0 * self.q0 * par.K * self.lift
+        self.cts_f = (par.target / self.raise_scale) ** (1.0 / len(self.cts))
+        self.top_out = self.T - 2 * (len(self.cts) + 7 + par.r + len(self.stc))
+        assert self.top_out >= 0, "the chain is too short for the bootstrap"
+
+    def steps(self):
+        """every rotation step the linear transforms take"""
+        out = []
+        for p in self.cts + self.stc:
+            for s in p.steps():
+                if s not in out:
+                    out.append(s)
+        return out
+
+    def prepare(self):
+        """encode every level's diagonals (at the level's input top, scale q_a q_b f) and the i monomial"""
+        ops, N = self.ops, self.par.N
+        self.pts = []
+        top = self.T
+        for plans, f in ((self.cts, self.cts_f), (self.stc, 1.0)):
+            for p in plans:
+                sc = self.ev.qq(top) * f
+                prim = self.q[: top + 1]
+                row = []
+                for j in range(p.G):
+                    for i in range(p.B):
+                        d = p.pts[j][i]
+                        row.append(None if d is None else ops.plaintext(encode_rows(d, N, sc, prim), top))
+                self.pts.append(row)
+                top -= 2
+                if plans is self.cts and p is self.cts[-1]:
+                    top -= 2 * (7 + self.par.r)
+        mono = np.zeros((len(self.q), N), np.uint32)
+        mono[:, N // 2] = 1  # X^(N/2): i in every slot
+        self.mono_i = ops.plaintext(mono, self.T)
+        mono_m = np.zeros((len(self.q), N), np.uint32)
+        mono_m[:, N // 2] = [p - 1 for p in self.q]  # -X^(N/2): -i
+        self.mono_mi = ops.plaintext(mono_m, self.T)
+
+    def lt(self, x, plan, pts, f):
+        ops, top = self.ops, x.top
+        B, G = plan.B, plan.G
+        rots = ops.alloc(B)
+        ops.copy(ops.item(rots, 0), x.h, top)
+        ops.hoisted(ops.item(rots, 1), x.h, top, [b % self.par.n for b in plan.baby[1:]])
+        res = ops.alloc(G)
+        ops.pt_dot(res, rots, top, pts, B, G)
+        acc = None
+        for j in range(G):
+            g = plan.giant[j] % self.par.n
+            y = ops.item(res, j)
+            if g:
+                t = ops.alloc()
+                ops.rotate(t, y, top, g)
+                y = t
+            if acc is None:
+                acc = y
+            else:
+                s = ops.alloc()
+                ops.add(s, acc, y, top, False)
+                acc = s
+        out = ops.alloc()
+        ops.rescale2(out, acc, top)
+        ops.level_done()
+        return Ct(out, top - 2, x.scale * f)
+
+    def evalmod(self, u):
+        ce = ChebEval(self.ev)
+        ce.basis(u)
+        top = ce.out_top()
+        h = ce.eval(self.em.c, top, self.ev.qq(top))
+        for _ in range(self.par.r):
+            h = self.ev.add_const(self.ev.mul(self.ev.double(h), h), -1.0)
+        return h
+
+    def run(self, x_h):
+        """x_h: the input ciphertext at top 0 (message scale par.delta_in). Returns the output Ct (its top and scale:
+        slot values = the input's message)."""
+        ops, ev, par = self.ops, self.ev, self.par
+        ops.begin()
+        raised = ops.alloc()
+        ops.mod_raise(raised, x_h, self.T)
+        ops.mul_const(raised, raised, self.T, self.lift)
+        x = Ct(raised, self.T, self.raise_scale)
+        k = 0
+        for p in self.cts:
+            x = self.lt(x, p, self.pts[k], self.cts_f)
+            k += 1
+        cj = ops.alloc()
+        ops.rotate(cj, x.h, x.top, "conj")
+        re = Ct(ops.alloc(), x.top, x.scale)
+        ops.add(re.h, x.h, cj, x.top, False)
+        d = ops.alloc()
+        ops.add(d, x.h, cj, x.top, True)
+        im = Ct(ops.alloc(), x.top, x.scale)
+        ops.mul_pt(im.h, d, x.top, self.mono_mi)
+        re, im = self.evalmod(re), self.evalmod(im)
+        ii = ops.alloc()
+        ops.mul_pt(ii, im.h, im.top, self.mono_i)
+        w = ev.add(re, Ct(ii, im.top, im.scale))
+        for p in self.stc:
+            w = self.lt(w, p, self.pts[k], 1.0)
+            k += 1
+        # the slot values are now (2 pi / q0) times the message's at the input's scale: relabel
+        w.scale = w.scale * 2.0 * math.pi * par.delta_in / self.q0
+        return w
+
+
+# ----------------------------------------------------------------------------------------------- device operations
+
+
+class View:
+    """A ciphertext inside a device buffer (word offset), addressable like a DevBuf by the engine's calls."""
+    __slots__ = ("buf", "off")
+
+    def __init__(self, buf, off=0):
+        self.buf, self.off = buf, off
+
+    def addr(self, offset=0):
+        return self.buf.addr(self.off + offset)
+
+
+def key_plan(boot):
+    """The galois elements of the bootstrap's key group, one slot per use: per linear-transform level its babies
+    (consecutive, so that the hoisted rotations batch their ModDowns) then its giants; the conjugation last. Returns
+    (galois list, per level (baby key indices, {giant step: key index}), conj index)."""
+    N, n = boot.par.N, boot.par.n
+    gal, levels = [], []
+    for p in boot.cts + boot.stc:
+        babies = []
+        for b in p.baby[1:]:
+            babies.append(len(gal))
+            gal.append(pow(5, b % n, 2 * N))
+        giants = {}
+        for g in p.giant:
+            g %= n
+            if g and g not in giants:
+                giants[g] = len(gal)
+                gal.append(pow(5, g, 2 * N))
+        levels.append((babies, giants))
+    gal.append(2 * N - 1)
+    return gal, levels, len(gal) - 1
+
+
+class GpuOps:
+    """The composite's operations on the device: the engine's key switches, rescale and products, the kernel table's
+    element-wise entries (ew_add, ew_scale, ew_copy, add_const, mul_table, pt_dot, mod_raise). Buffers come from a
+    pool reused in request order (begin() rewinds it), constants and plaintexts are cached on the device, so that a
+    second run allocates nothing."""
+
+    def __init__(self, ctx, keys, relin, levels, conj, stream):
+        from . import abi, bts, engine
+        from ._lib import LIB
+
+        self.abi, self.eng, self.LIB = abi, engine, LIB
+        self.ctx, self.keys, self.relin, self.st = ctx, keys, relin, stream
+        self.levels, self.conj_key = levels, conj
+        self.N, self.R, self.nq = ctx.n, ctx.rows, ctx.nq
+        self.cw = ctx.ct_words
+        self.primes = [int(p) for p in ctx.chain.primes]
+        self.pr = LIB.pcx_ctx_primes(ctx.h)
+        self.pool, self.cur = [], 0
+        self.cache = {}
+        self.level_i = 0
+        self.zero_pt = None
+        self.mr_consts = bts.mod_raise_consts(self.primes, 1)
+        self.lvl_of_plan = {}
+
+    # -- buffers
+    def begin(self):
+        self.cur = 0
+        self.level_i = 0
+
+    def alloc(self, count=1):
+        if self.cur < len(self.pool) and self.pool[self.cur][1] == count:
+            buf = self.pool[self.cur][0]
+        else:
+            buf = self.eng.DevBuf(count * self.cw)
+            if self.cur < len(self.pool):
+                self.pool[self.cur] = (buf, count)
+            else:
+                self.pool.append((buf, count))
+        self.cur += 1
+        return View(buf, 0)
+
+    def item(self, h, i):
+        return View(h.buf, h.off + i * self.cw)
+
+    def _ref(self, h):
+        return self.abi.PolyRef(h.addr().value, self.cw, self.R * self.N)
+
+    def _call(self, name, a):
+        rc = self.abi.call(name, a, self.st, self.ctx.logn)
+        if rc != 0:
+            raise self.eng.HipError(f"{name} returned {rc}")
+
+    def _ew(self, name, out, a, b, top, sub=0, sc=None):
+        e = self.abi.EwArgs()
+        e.out, e.a = self._ref(out), self._ref(a)
+        if b is not None:
+            e.b = self._ref(b)
+        e.rs = self.abi.RowSet(top + 1, 0, self.nq, 0)
+        if sc is not None:
+            e.sc, e.scs = sc[0].ptr.value, sc[1].ptr.value
+        e.pr, e.K, e.nparts, e.sub = self.pr, 1, 2, sub
+        self._call(name, e)
+
+    # -- element-wise
+    def copy(self, dst, src, top):
+        self._ew("ew_copy", dst, src, None, top)
+
+    def add(self, out, a, b, top, sub):
+        self._ew("ew_add", out, a, b, top, 1 if sub else 0)
+
+    def _const_rows(self, k):
+        key = ("k", k)
+        if key not in self.cache:
+            r = np.array([k % p for p in self.primes], np.uint32)
+            rs = np.array([(int(v) << 32) // p for v, p in zip(r, self.primes)], np.uint64).astype(np.uint32)
+            self.cache[key] = (self.eng.DevBuf.from_array(r), self.eng.DevBuf.from_array(rs))
+        return self.cache[key]
+
+    def mul_const(self, out, x, top, k):
+        self._ew("ew_scale", out, x, None, top, sc=self._const_rows(int(k)))
+
+    def add_const(self, x, top, k):
+        r, _ = self._const_rows(int(k))
+        a = self.abi.AddConstArgs()
+        a.x, a.k, a.pr, a.n, a.K = self._ref(x), r.ptr.value, self.pr, top + 1, 1
+        self._call("add_const", a)
+
+    def mul_pt(self, out, x, top, pt):
+        a = self.abi.MulTableArgs()
+        a.out, a.in_, a.t, a.pr, a.n, a.K = self._ref(out), self._ref(x), pt.ptr.value, self.pr, top + 1, 1
+        self._call("mul_table", a)
+
+    # -- plaintexts
+    def _rows(self, roff, ids):
+        key = ("rows", tuple(roff), tuple(ids))
+        if key not in self.cache:
+            self.cache[key] = self.eng.Rows(self.ctx, roff, ids)
+        return self.cache[key]
+
+    def plaintext(self, coef_rows, top):
+        """coefficient residue rows 0..top -> a device plaintext [top + 1][N] in evaluation form"""
+        buf = self.eng.DevBuf.from_array(np.ascontiguousarray(coef_rows[: top + 1], np.uint32))
+        self._rows(list(range(top + 1)), list(range(top + 1))).ntt(buf, 1, self.st)
+        self.st.sync()
+        return buf
+
+    def pt_dot(self, res, rots, top, pts, B, G):
+        key = ("ptr", tuple(id(p) for p in pts))
+        if key not in self.cache:
+            if any(p is None for p in pts) and self.zero_pt is None:
+                self.zero_pt = self.eng.DevBuf((self.nq) * self.N)
+                self.zero_pt.zero()
+            ptrs = np.array([(self.zero_pt if p is None else p).ptr.value for p in pts], np.uint64)
+            self.cache[key] = self.eng.DevBuf.from_array(ptrs.view(np.uint32))
+        a = self.abi.PtDotArgs()
+        a.rot = self.abi.PolyRef(rots.addr().value, B * self.cw, self.R * self.N)
+        a.res = self.abi.PolyRef(res.addr().value, G * self.cw, self.R * self.N)
+        a.rot_stride, a.res_stride = self.cw, self.cw
+        a.pts, a.pr = self.cache[key].ptr.value, self.pr
+        a.rs = self.abi.RowSet(top + 1, 0, self.nq, 0)
+        a.npts, a.bstep, a.gstep, a.K, a.ptw, a.pt_prow, a.enc = B * G, B, G, 1, self.N, top + 1, 0xFFFFFFFF
+        self._call("pt_dot", a)
+
+    # -- key switches
+    def rotate(self, out, x, top, step):
+        if step == "conj":
+            r = self.conj_key
+        else:
+            r = self.levels[self.level_i][1][step]
+        self.ctx.rotate(self.keys, r, x, top, out, self.st)
+
+    def hoisted(self, outs, x, top, steps):
+        babies = self.levels[self.level_i][0]
+        assert len(babies) == len(steps)
+        self.ctx.rotate_hoisted(self.keys, babies, x, top, outs, self.st)
+
+    def level_done(self):
+        self.level_i += 1
+
+    def mul_relin(self, out, a, b, top):
+        self.ctx.mul_relin(self.relin, a, b, top, out, self.st)
+
+    def rescale2(self, out, x, top):
+        self.ctx.rescale(x, top, 2, out, self.st)
+
+    # -- ModRaise
+    def mod_raise(self, out, x, top):
+        self._ew("ew_copy", out, x, None, 0)
+        R = self.R
+        self._rows([0, R], [0, 0]).ntt(out, -1, self.st)
+        qhatinv, qhat = self.mr_consts
+        a = self.abi.ModRaiseArgs()
+        a.x, a.pr = out.addr().value, self.pr
+        a.ct_stride, a.part_stride = self.cw, R * self.N
+        for k in range(4):
+            a.qhatinv[k] = qhatinv[k]
+            for t in range(64):
+                a.qhat[k][t] = qhat[k][t]
+        a.K, a.d, a.r0, a.r1, a.nparts = 1, 1, 1, top + 1, 2
+        self._call("mod_raise", a)
+        rows = list(range(top + 1))
+        self._rows(rows + [R + t for t in rows], rows + rows).ntt(out, 1, self.st)

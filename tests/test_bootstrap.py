@@ -1,0 +1,149 @@
+"""The bootstrap composite (perseus_amd/bootstrap.py) on the CPU: its host constants against what the mathematics
+fixes (the special-FFT layers against the direct Vandermonde sums of the canonical embedding, the CoeffToSlot /
+SlotToCoeff levels and their baby-step giant-step split against the plain maps, the Chebyshev division identity, the
+EvalMod series against sin(2 pi y)), the float simulation of the whole algorithm, and the homomorphic composite run on
+the oracle's operations at N = 2^12: the decrypted output equals the input's message.
+"""
+import numpy as np
+import pytest
+
+from perseus_amd import bootstrap as B
+from perseus_amd.encoding import decode, encode
+from tests import twin
+from tests.bts_ops import OracleOps
+from tests.test_oracle_ks import decrypt, encrypt
+
+
+def test_layers_compose_to_the_canonical_embedding():
+    logn = 7
+    N, n = 1 << logn, 1 << (logn - 1)
+    rng = np.random.default_rng(1)
+    w = rng.normal(size=n) + 1j * rng.normal(size=n)
+    x = w[B.bitrev(n)]
+    for ln in range(1, logn):
+        x = B.apply_diags(B.layer(n, ln), x)
+    zeta = np.exp(2j * np.pi / (4 * n))
+    g = B.rot_group(n)
+    direct = np.array([np.sum(w * zeta ** ((g[j] * np.arange(n)) % (4 * n))) for j in range(n)])
+    assert np.abs(x - direct).max() < 1e-10
+    # a real coefficient vector m decodes to V (m_lo + i m_hi)
+    m = rng.normal(size=N)
+    want = np.array([np.sum((m[:n] + 1j * m[n:]) * zeta ** ((g[j] * np.arange(n)) % (4 * n))) for j in range(n)])
+    assert np.abs(decode(m, N, 1.0) - want).max() < 1e-10
+
+
+@pytest.mark.parametrize("logn", [6, 9])
+def test_levels_and_bsgs(logn):
+    N, n = 1 << logn, 1 << (logn - 1)
+    par = B.Params(logn)
+    rng = np.random.default_rng(logn)
+    m = rng.normal(size=N)
+    z = decode(m, N, 1.0)
+    y = z
+    for lv in B.cts_levels(n, par.cts):
+        p = B.BsgsPlan(lv, n)
+        y2 = B.apply_diags(lv, y)
+        assert np.abs(p.apply(y) - y2).max() < 1e-9
+        y = y2
+    assert np.abs(y - (m[:n] + 1j * m[n:])[B.bitrev(n)]).max() < 1e-9, "CtS gives the bit-reversed coefficients"
+    for lv in B.stc_levels(n, par.stc):
+        p = B.BsgsPlan(lv, n)
+        y2 = B.apply_diags(lv, y)
+        assert np.abs(p.apply(y) - y2).max() < 1e-9
+        y = y2
+    assert np.abs(y - z).max() < 1e-9, "StC undoes CtS"
+
+
+def test_cheb_split_and_evalmod():
+    em = B.EvalModPlan(32, 63, 3)
+    u = np.linspace(-1, 1, 4001)
+    assert np.abs(em.plain(u) - np.sin(2 * np.pi * 32 * u)).max() < 1e-9
+    for g in (8, 16, 32):
+        c = em.c[: 2 * g]
+        q, r = B.cheb_split(c, g)
+        Tg = np.polynomial.chebyshev.chebval(u, np.eye(g + 1)[g])
+        assert np.abs(B.cheb_eval(q, u) * Tg + B.cheb_eval(r, u) - B.cheb_eval(c, u)).max() < 1e-12
+
+
+def test_residues_exact():
+    rng = np.random.default_rng(3)
+    f = np.concatenate([rng.normal(size=50) * 2.0 ** 70, rng.normal(size=50) * 1e6, [2.0 ** 84, -2.0 ** 84, 0.5, -1.5]])
+    ps = [1073479681, 1073184769, 3]
+    got = B.residues(f, ps)
+    for r, p in enumerate(ps):
+        assert [int(v) for v in got[r]] == [int(round(x)) % p if abs(x) < 2 ** 53 else int(x) % p for x in f]
+
+
+def test_simulated_bootstrap():
+    logn = 10
+    N = 1 << logn
+    par = B.Params(logn)
+    rng = np.random.default_rng(3)
+    m = rng.uniform(-1, 1, N) * 2.0 ** -12
+    out = B.simulate(m + rng.integers(-20, 21, N), par)
+    want = decode(m, N, 1.0)
+    assert np.abs(out - want).max() / np.abs(want).max() < 1e-5
+
+
+def setup_oracle(logn=12, seed=5):
+    """a chain with the bootstrap's levels plus one spare (three limbs out), oracle keys, the composite"""
+    par = B.Params(logn)
+    nq = 1 + 2 * par.levels_used() + 2
+    dnum = 3
+    kp = -(-nq // dnum)
+    ps = [int(p) for p in twin.descending_primes(30, 2 << logn, nq + kp)]
+    q, p = ps[:nq], ps[nq:]
+    oc = twin.Ctx(logn, q, p, dnum)
+    g = twin.Prng([seed, 2, 7, 1, 8, 2, 8, 1], 0)
+    s = g.sparse_ternary(1 << logn, 192)
+    s_eval = oc.secret_eval(s)
+    boot = B.Bootstrap(None, par, q)
+    gal, levels, conj = B.key_plan(boot)
+    keys = [oc.rotation_key(g, s_eval, x) for x in gal]
+    seeds = np.stack([k[0] for k in keys])
+    bs = [k[1] for k in keys]
+    rseed = g.ksk_seed()
+    e = np.zeros((dnum, oc.rows, 1 << logn), np.uint32)
+    errs = [g.gaussian(1 << logn) for _ in range(dnum)]
+    for d in range(dnum):
+        for t in range(oc.rows):
+            e[d, t] = np.mod(errs[d], oc.primes[t])
+    e = oc.ntt_fwd(e.reshape(-1, 1 << logn), [t for _ in range(dnum) for t in range(oc.rows)]).reshape(e.shape)
+    s2 = np.stack([(s_eval[t].astype(np.uint64) ** 2 % oc.primes[t]) for t in range(oc.rows)]).astype(np.uint32)
+    rb = oc.ksk_gen(s_eval, s2, rseed, e)
+    ops = OracleOps(oc, q, seeds, bs, levels, conj, rseed, rb)
+    ops.set_galois(gal)
+    boot.ops = boot.ev.ops = ops
+    return dict(par=par, oc=oc, s=s, s_eval=s_eval, boot=boot, ops=ops, q=q, gal=gal, seeds=seeds, bs=bs,
+                levels=levels, conj=conj, rseed=rseed, rb=rb, errs=errs)
+
+
+def input_ct(S, rng):
+    par, oc = S["par"], S["oc"]
+    z = rng.uniform(-1, 1, par.n) + 1j * rng.uniform(-1, 1, par.n)
+    m = np.rint(encode(z, par.N, par.delta_in)).astype(np.int64)
+    ct, me = encrypt(oc, S["s_eval"], m, rng, 0)
+    return z, ct, me
+
+
+def decrypt_slots(S, ct, top, scale):
+    from perseus_amd.encoding import from_residues
+
+    oc = S["oc"]
+    coef = from_residues(decrypt(oc, S["s_eval"], ct, top), oc.primes[: top + 1])
+    return decode(coef, S["par"].N, scale)
+
+
+def test_bootstrap_on_the_oracle():
+    S = setup_oracle()
+    boot, ops = S["boot"], S["ops"]
+    rng = np.random.default_rng(9)
+    z, ct, me = input_ct(S, rng)
+    boot.prepare()
+    out = boot.run((ct[None], 0))
+    assert out.top == boot.top_out
+    got = decrypt_slots(S, OracleOps.get(out.h), out.top, out.scale)
+    ref = decode(me.astype(np.float64), S["par"].N, S["par"].delta_in)  # the input's message with its noise
+    err = np.abs(got - ref).max()
+    print(f"bootstrap error vs the input's decryption: {err:.3g} (vs the plaintext: {np.abs(got - z).max():.3g})")
+    assert err < 1e-3

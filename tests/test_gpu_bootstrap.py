@@ -1,0 +1,63 @@
+"""The bootstrap composite on the GPU (perseus_amd.bootstrap.GpuOps) at N = 2^12: word for word equal to the same
+composite run on the oracle's operations (tests/bts_ops.py) with the same keys, its decryption equal to the input's
+message, and a second run (the buffer pool and the cached constants reused) giving the same words. Each test prints its
+case before the GPU runs.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import perseus_amd as pa
+from perseus_amd import bootstrap as B
+from tests.bts_ops import OracleOps
+from tests.test_bootstrap import decrypt_slots, input_ct, setup_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def gpu_boot(S):
+    par, q, oc = S["par"], S["q"], S["oc"]
+    ch = pa.Chain("bts12", par.logn, q, [int(p) for p in oc.primes[len(q):]], oc.dnum)
+    ctx = pa.Context(ch, k_rot=8)
+    keys = pa.Keys(ctx, S["gal"], seeds=S["seeds"], b=S["bs"])
+    relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
+    st = pa.Stream()
+    ops = B.GpuOps(ctx, keys, relin, S["levels"], S["conj"], st)
+    boot = B.Bootstrap(ops, par, q)
+    boot.prepare()
+    return ctx, keys, relin, st, ops, boot
+
+
+def test_bootstrap_gpu_matches_the_oracle():
+    say("[bootstrap] N=2^12: GPU composite vs the oracle composite, decryption, rerun")
+    S = setup_oracle()
+    rng = np.random.default_rng(9)
+    z, ct, me = input_ct(S, rng)
+    ctx, keys, relin, st, ops, boot = gpu_boot(S)
+    say(f"[bootstrap] {len(S['gal'])} keys, top {boot.T} -> {boot.top_out}")
+    x = pa.DevBuf.from_array(ct)
+    out = boot.run(B.View(x))
+    st.sync()
+    got = out.h.buf.download((2, ctx.rows, ctx.n), offset=out.h.off, words=ctx.ct_words)
+    S["boot"].prepare()
+    want = S["boot"].run((ct[None], 0))
+    assert out.top == want.top and out.scale == want.scale
+    wh = OracleOps.get(want.h)
+    assert (got[:, : out.top + 1] == wh[:, : out.top + 1]).all(), "GPU == oracle, word for word"
+    from perseus_amd.encoding import decode
+
+    slots = decrypt_slots(S, got, out.top, out.scale)
+    ref = decode(me.astype(np.float64), S["par"].N, S["par"].delta_in)
+    err = np.abs(slots - ref).max()
+    say(f"[bootstrap] max |error| against the input's decryption: {err:.3g}")
+    assert err < 1e-3
+    out2 = boot.run(B.View(x))
+    st.sync()
+    got2 = out2.h.buf.download((2, ctx.rows, ctx.n), offset=out2.h.off, words=ctx.ct_words)
+    assert (got2[:, : out.top + 1] == got[:, : out.top + 1]).all(), "the rerun gives the same words"

@@ -97,6 +97,8 @@ def preset(name: str) -> Chain:
     c3: the hoisted rotation batch, N = 2^16, 30 Q primes below 2^31, dnum 3, 6 special primes;
     c4: attention scoring, N = 2^16, 6 Q + 2 special 30-bit primes, dnum 3 (a ciphertext at scale 2^40 takes one
         plaintext product and a two-prime rescale, then its rotations at 4 limbs);
+    c5: the full-slot bootstrap, N = 2^16, 47 Q primes below 2^30 (q0, 17 two-prime levels the bootstrap consumes,
+        12 limbs left), dnum 3, 16 special primes (as many as a digit's limbs, so key switching adds little noise);
     small: a quick test chain, N = 2^12, 6 Q + 2 special 30-bit primes, dnum 3;
     small28: the same at 28-bit primes (a bootstrapping stage's word size);
     rej: N = 2^12, 6 Q + 3 special primes just above 2^32 / 3, where a third of the KSKA words are rejected.
@@ -109,6 +111,8 @@ def preset(name: str) -> Chain:
         return make("c3", 16, 30, 6, 3, 31)
     if name == "c4":
         return make("c4", 16, 6, 2, 3, 30)
+    if name == "c5":
+        return make("c5", 16, 47, 16, 3, 30)
     if name == "small":
         return make("small", 12, 6, 2, 3, 30)
     if name == "small28":

@@ -326,6 +326,19 @@ class Evaluator:
         self.ops.rescale2(out, out, a.top)
         return Ct(out, top, scale)
 
+    def lincomb(self, terms, c0, top, scale):
+        """c0 + sum c_j a_j landing exactly at (top, scale): each a_j (dropped to top + 2) times the integer
+        round(c_j scale q_a q_b / a_j.scale) in one weighted sum with the constant, then one rescale"""
+        tc = top + 2
+        qq = self.qq(tc)
+        for a, _ in terms:
+            assert a.top >= tc, (a.top, tc)
+        ks = [int(round(c * scale * qq / a.scale)) for a, c in terms]
+        out = self.ops.alloc()
+        self.ops.wsum(out, [a.h for a, _ in terms], tc, ks, int(round(c0 * scale * qq)))
+        self.ops.rescale2(out, out, tc)
+        return Ct(out, top, scale)
+
     def add(self, a, b, sub=False):
         assert abs(a.scale / b.scale - 1.0) < 1e-9, (a.scale, b.scale)
         t = min(a.top, b.top)
@@ -347,7 +360,8 @@ class Evaluator:
 class ChebEval:
     """p(u) = sum_k c_k T_k(u) of degree <= 63 on the ciphertext u: the power basis T_1..T_8, T_16, T_32 with every
     T_{a+b} = 2 T_a T_b - T_{|a-b|} formed at one exact scale, then p split by T_32, T_16, T_8 down to leaves of
-    degree < 8 whose terms are each brought to the leaf's target (top, scale) by one constant product."""
+    degree < 8, each one weighted sum of its T_k with integer constants chosen for the leaf's target (top, scale) and
+    one rescale."""
 
     BABY, GIANTS = 8, (8, 16, 32)
 
@@ -378,14 +392,9 @@ class ChebEval:
         c = np.trim_zeros(np.asarray(c, np.float64), "b")
         ev, T = self.ev, self.T
         if len(c) <= self.BABY:
-            acc = None
-            for k in range(1, len(c)):
-                if c[k] == 0.0:
-                    continue
-                t = ev.mul_to(T[k], float(c[k]), scale, top)
-                acc = t if acc is None else ev.add(acc, t)
-            assert acc is not None, "a leaf with no term of degree >= 1"
-            return ev.add_const(acc, float(c[0]))
+            terms = [(T[k], float(c[k])) for k in range(1, len(c)) if c[k] != 0.0]
+            assert terms, "a leaf with no term of degree >= 1"
+            return ev.lincomb(terms, float(c[0]), top, scale)
         g = max(x for x in self.GIANTS if x < len(c))
         q, r = cheb_split(c, g)
         G = T[g]
@@ -648,6 +657,23 @@ class GpuOps:
         a = self.abi.AddConstArgs()
         a.x, a.k, a.pr, a.n, a.K = self._ref(x), r.ptr.value, self.pr, top + 1, 1
         self._call("add_const", a)
+
+    def wsum(self, out, srcs, top, ks, k0):
+        key = ("w", tuple(ks), k0)
+        if key not in self.cache:
+            w = np.array([[k % p for p in self.primes] for k in ks], np.uint32)
+            ws = np.array([[(int(v) << 32) // p for v, p in zip(r, self.primes)] for r in w], np.uint64)
+            kr = np.array([k0 % p for p in self.primes], np.uint32)
+            self.cache[key] = tuple(self.eng.DevBuf.from_array(v) for v in (w, ws.astype(np.uint32), kr))
+        bw, bws, bk = self.cache[key]
+        a = self.abi.WsumKArgs()
+        a.w.out = self._ref(out)
+        for j, x in enumerate(srcs):
+            a.w.src[j] = self._ref(x)
+        a.w.w, a.w.ws, a.w.pr = bw.ptr.value, bws.ptr.value, self.pr
+        a.w.nsrc, a.w.rowstride, a.w.n, a.w.K = len(srcs), self.R, top + 1, 1
+        a.k = bk.ptr.value
+        self._call("wsum_k", a)
 
     def mul_pt(self, out, x, top, pt):
         a = self.abi.MulTableArgs()

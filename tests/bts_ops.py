@@ -58,6 +58,12 @@ class OracleOps:
         kr = np.array([int(k) % p for p in self.q], np.uint32)
         self.get(x)[:, : top + 1] = em.add_const(self.q[: top + 1], self.get(x)[None, :, : top + 1], kr[: top + 1])[0]
 
+    def wsum(self, out, srcs, top, ks, k0):
+        w = np.array([[k % p for p in self.q[: top + 1]] for k in ks], np.uint64)
+        kr = np.array([k0 % p for p in self.q[: top + 1]], np.uint64)
+        self.get(out)[:, : top + 1] = em.wsum(self.q[: top + 1], [self.get(x)[None, :, : top + 1] for x in srcs], w,
+                                              kr)[0]
+
     def mul_pt(self, out, x, top, pt):
         self.get(out)[:, : top + 1] = (self.get(x)[:, : top + 1].astype(np.uint64) *
                                        pt[None, : top + 1].astype(np.uint64) % self._qq(top)).astype(np.uint32)

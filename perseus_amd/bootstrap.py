@@ -222,7 +222,7 @@ class Params:
     """Bootstrap shape: slots n = N/2; CtS / StC level sizes (layers per level); EvalMod's K, degree, double angles;
     the input's message scale; the output scale is whatever the chain leaves (reported)."""
 
-    def __init__(self, logn, cts=None, stc=None, K=32, deg=63, r=3, delta_in=2.0 ** 20, target=2.0 ** 60):
+    def __init__(self, logn, cts=None, stc=None, K=32, deg=63, r=3, delta_in=2.0 ** 25, target=2.0 ** 60):
         self.logn, self.N, self.n = logn, 1 << logn, 1 << (logn - 1)
         L = logn - 1
         self.cts = cts or _split(L, 4)
@@ -412,8 +412,8 @@ class Bootstrap:
     an operations object. `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
     scale par.delta_in. Plaintexts (the levels' diagonals, the i monomial) are encoded once by `prepare`."""
 
-    def __init__(self, ops, par, primes):
-        self.ops, self.par = ops, par
+    def __init__(self, ops, par, primes, ops2=None):
+        self.ops, self.par, self.ops2 = ops, par, ops2
         self.q = [int(p) for p in primes]
         self.T = len(self.q) - 1
         n = par.n
@@ -493,13 +493,14 @@ class Bootstrap:
         ops.level_done()
         return Ct(out, top - 2, x.scale * f)
 
-    def evalmod(self, u):
-        ce = ChebEval(self.ev)
+    def evalmod(self, u, ev=None):
+        ev = ev or self.ev
+        ce = ChebEval(ev)
         ce.basis(u)
         top = ce.out_top()
-        h = ce.eval(self.em.c, top, self.ev.qq(top))
+        h = ce.eval(self.em.c, top, ev.qq(top))
         for _ in range(self.par.r):
-            h = self.ev.add_const(self.ev.mul(self.ev.double(h), h), -1.0)
+            h = ev.add_const(ev.mul(ev.double(h), h), -1.0)
         return h
 
     def run(self, x_h):
@@ -507,6 +508,8 @@ class Bootstrap:
         slot values = the input's message)."""
         ops, ev, par = self.ops, self.ev, self.par
         ops.begin()
+        if self.ops2 is not None:
+            self.ops2.begin()
         raised = ops.alloc()
         ops.mod_raise(raised, x_h, self.T)
         ops.mul_const(raised, raised, self.T, self.lift)
@@ -523,7 +526,14 @@ class Bootstrap:
         ops.add(d, x.h, cj, x.top, True)
         im = Ct(ops.alloc(), x.top, x.scale)
         ops.mul_pt(im.h, d, x.top, self.mono_mi)
-        re, im = self.evalmod(re), self.evalmod(im)
+        if self.ops2 is None:
+            re, im = self.evalmod(re), self.evalmod(im)
+        else:
+            # the imaginary part's chain on the second lane (its own workspace and stream), beside the real part's
+            ops.fork(self.ops2)
+            im = self.evalmod(im, Evaluator(self.ops2, self.q))
+            re = self.evalmod(re)
+            ops.join(self.ops2)
         ii = ops.alloc()
         ops.mul_pt(ii, im.h, im.top, self.mono_i)
         w = ev.add(re, Ct(ii, im.top, im.scale))
@@ -533,6 +543,9 @@ class Bootstrap:
         # the slot values are now (2 pi / q0) times the message's at the input's scale: relabel
         w.scale = w.scale * 2.0 * math.pi * par.delta_in / self.q0
         return w
+
+    def precision_bits(self, err):
+        return -math.log2(err) if err > 0 else float("inf")
 
 
 # ----------------------------------------------------------------------------------------------- device operations
@@ -726,6 +739,20 @@ class GpuOps:
 
     def level_done(self):
         self.level_i += 1
+
+    def fork(self, other):
+        """other's stream waits for the work queued on this one"""
+        if "fork" not in self.cache:
+            self.cache["fork"] = (self.eng.Event(), self.eng.Event())
+        e = self.cache["fork"][0]
+        e.record(self.st)
+        other.st.wait(e)
+
+    def join(self, other):
+        """this stream waits for the work queued on other's"""
+        e = self.cache["fork"][1]
+        e.record(other.st)
+        self.st.wait(e)
 
     def mul_relin(self, out, a, b, top):
         self.ctx.mul_relin(self.relin, a, b, top, out, self.st)

@@ -21,7 +21,7 @@ def say(*a):
     sys.stdout.flush()
 
 
-def gpu_boot(S):
+def gpu_boot(S, lanes=1):
     par, q, oc = S["par"], S["q"], S["oc"]
     ch = pa.Chain("bts12", par.logn, q, [int(p) for p in oc.primes[len(q):]], oc.dnum)
     ctx = pa.Context(ch, k_rot=8)
@@ -29,17 +29,25 @@ def gpu_boot(S):
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()
     ops = B.GpuOps(ctx, keys, relin, S["levels"], S["conj"], st)
-    boot = B.Bootstrap(ops, par, q)
+    ops2 = None
+    if lanes == 2:
+        ctx2 = pa.Context(ch, k_rot=1)
+        relin2 = pa.Keys(ctx2, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None],
+                         relin=True)
+        ops2 = B.GpuOps(ctx2, None, relin2, S["levels"], S["conj"], pa.Stream())
+        ops2.keep = (ctx2, relin2)
+    boot = B.Bootstrap(ops, par, q, ops2)
     boot.prepare()
     return ctx, keys, relin, st, ops, boot
 
 
-def test_bootstrap_gpu_matches_the_oracle():
-    say("[bootstrap] N=2^12: GPU composite vs the oracle composite, decryption, rerun")
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_bootstrap_gpu_matches_the_oracle(lanes):
+    say(f"[bootstrap] N=2^12, {lanes} EvalMod lane(s): GPU composite vs the oracle composite, decryption, rerun")
     S = setup_oracle()
     rng = np.random.default_rng(9)
     z, ct, me = input_ct(S, rng)
-    ctx, keys, relin, st, ops, boot = gpu_boot(S)
+    ctx, keys, relin, st, ops, boot = gpu_boot(S, lanes)
     say(f"[bootstrap] {len(S['gal'])} keys, top {boot.T} -> {boot.top_out}")
     x = pa.DevBuf.from_array(ct)
     out = boot.run(B.View(x))

@@ -603,6 +603,28 @@ typedef struct PackDotArgs {
 } PackDotArgs;
 PC_STATIC_ASSERT(sizeof(PackDotArgs) == 120, "PackDotArgs layout");
 
+/* args.cuh:906-927 (coeff_sum, ABI 9): streamed-weight inner sum out (+)= sum_{r < n} ct[r] pt_r over Q limbs
+ * 0..L-1 (prime id = limb), pt_r = NTT(round(rows[r] scale) mod p): round half to even, a product of magnitude
+ * 9.2e18 or more clamped to +-2^62 and counted in *overflow (when non-null) once per limb and coefficient. ct[r], out:
+ * part 0 row 0 of a ciphertext (part 1 at + part_stride words, row l at + l N); rows[r]: N float32 coefficients in
+ * device memory; scratch: n L N words (left holding the NTT'd plaintexts). n in [1, MAXT], L in [1, MAXL]. */
+#define PC_COEFF_MAXT 32
+#define PC_COEFF_MAXL 64
+typedef struct CoeffArgs {
+    void* scratch;
+    void* out;
+    const void* fw;
+    const void* fws;
+    const PrimeConst* pr;
+    unsigned long long* overflow;
+    uint64_t part_stride;
+    double scale;
+    int32_t n, L, accumulate, pad;
+    const float* rows[PC_COEFF_MAXT];
+    const void* ct[PC_COEFF_MAXT];
+} CoeffArgs;
+PC_STATIC_ASSERT(sizeof(CoeffArgs) == 80 + 16 * PC_COEFF_MAXT, "CoeffArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct EncodeArgs;
 struct SpruExtractArgs;
@@ -610,7 +632,6 @@ struct SpruFftArgs;
 struct SpruScatterArgs;
 struct PcmmArgs;
 struct CcmmArgs;
-struct CoeffArgs;
 struct TfheArgs;
 struct TensorSeededArgs;
 

@@ -308,3 +308,34 @@ def pack_dot(q, dig, kb, ka, c0=None, pmod=None, nq=0):
     if nq:
         s0[:nq] = _add(s0[:nq], _mul(c0[:nq], _row(pmod, nq), qq[:nq]), qq[:nq])
     return _out(s0), _out(s1)
+
+
+# ----------------------------------------------------------------------------------------------- coeff_sum
+def coeff_residues(rows, scale, q):
+    """round(rows * scale) (float32 rows widened to float64, half to even) as residues [len(q)][n][N]; a product of
+    magnitude 9.2e18 or more becomes +-2^62 and is counted once per limb (args.cuh:906-911;
+    crates/pc-host/src/coeffrows.rs:11-27). Returns (residues, overflow count)."""
+    x = np.asarray(rows, np.float32).astype(np.float64) * float(scale)
+    big = ~(np.abs(x) < 9.2e18)
+    m = np.where(big, np.where(x < 0, -(2.0 ** 62), 2.0 ** 62), np.rint(np.where(big, 0.0, x))).astype(np.int64)
+    mag = np.abs(m).astype(U64)
+    out = []
+    for p in q:
+        v = mag % U64(p)
+        v = np.where((m < 0) & (v != 0), U64(p) - v, v)
+        out.append(v.astype(np.uint32))
+    return np.stack(out), int(big.sum()) * len(q)
+
+
+def coeff_sum(q, rows, scale, cts, ntt, out=None):
+    """coeff_sum (args.cuh:906-927; coeffrows.rs:30-80): out (+)= sum_r ct_r NTT(round(rows_r scale)) over limbs
+    l < len(q) (prime id l). cts [n][2][L][N]; ntt(rows [L][N], ids) the forward transform. Returns (out, overflow)."""
+    res, ovf = coeff_residues(rows, scale, q)
+    L, n, N = res.shape
+    qq = np.asarray(q, U64)[:, None]
+    acc = np.zeros((2, L, N), U64) if out is None else np.asarray(out, U64).copy() % qq
+    for r in range(n):
+        pt = np.asarray(ntt(np.ascontiguousarray(res[:, r]), list(range(L))), U64)
+        for part in range(2):
+            acc[part] = (acc[part] + pt * np.asarray(cts[r][part], U64) % qq) % qq
+    return acc.astype(np.uint32), ovf

@@ -83,6 +83,16 @@ class RowSet(C.Structure):
     _fields_ = [("nq", i32), ("np", i32), ("qmax", i32), ("pad", i32)]
 
 
+COEFF_MAXT = 32
+
+
+class CoeffArgs(C.Structure):
+    """args.cuh:906-927 (592 bytes): coeff_sum."""
+    _fields_ = [("scratch", vp), ("out", vp), ("fw", vp), ("fws", vp), ("pr", vp), ("overflow", vp),
+                ("part_stride", u64), ("scale", C.c_double), ("n", i32), ("L", i32), ("accumulate", i32),
+                ("pad", i32), ("rows", vp * COEFF_MAXT), ("ct", vp * COEFF_MAXT)]
+
+
 class EwArgs(C.Structure):
     """args.cuh:144-157 (128 bytes): element-wise row-set kernels (ew_add / ew_scale / ew_sub_mul / ew_copy)."""
     _fields_ = [("out", PolyRef), ("a", PolyRef), ("b", PolyRef), ("rs", RowSet), ("sc", vp), ("scs", vp),
@@ -263,7 +273,7 @@ KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:207-210)
 assert C.sizeof(KeyTab) == 40 and C.sizeof(CtsArgs) == 200 and C.sizeof(CtsRegenArgs) == 240
 assert C.sizeof(KsArgs) == 176 and C.sizeof(KsKeyArgs) == 216 and C.sizeof(EpiArgs) == 72
 assert C.sizeof(KsRegenArgs) == 312
-assert C.sizeof(EwArgs) == 128
+assert C.sizeof(EwArgs) == 128 and C.sizeof(CoeffArgs) == 592
 assert C.sizeof(PolyRef) == 24 and C.sizeof(NttArgs) == 176 and C.sizeof(TensorArgs) == 192
 assert C.sizeof(TensorYArgs) == 240 and C.sizeof(TensorSumArgs) == 2 * 24 + 2 * TSUM_MAX * 24 + 8 + 16
 assert C.sizeof(MdEpiArgs) == 120 and C.sizeof(MdEpiToArgs) == 152 and C.sizeof(WsumArgs) == 256

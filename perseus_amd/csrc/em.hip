@@ -9,6 +9,7 @@
 // canonical residue of the stated formula whatever the number of terms; the reference's lazy 64-bit sums give the same
 // words inside the bounds its callers keep (2 npairs (p - 1)^2 < 2^64, nterm p^2 < 2^64).
 #include "common.h"
+#include "fused.h"
 
 namespace pch {
 namespace em {
@@ -547,6 +548,70 @@ int tensor_multi(const TensorMultiArgs* a, pc_stream_t s) {
     return 0;
 }
 
+// ------------------------------------------------------------------------------------------------ coeff_sum
+// coeff_sum (args.cuh:906-927; host twin crates/pc-host/src/coeffrows.rs:11-80). Pass 1: scratch row (r, l) = the
+// residues mod p_l of round(rows[r] scale) (half to even; a product of magnitude 9.2e18 or more becomes +-2^62 and is
+// counted once per limb and coefficient). Pass 2: the forward NTT of the n L scratch rows (dense: row r L + l, prime
+// l). Pass 3: out (+)= sum_r scratch(r, l) ct_r, both parts, one exact reduction per word.
+__global__ void __launch_bounds__(BX) coeff_conv_k(CoeffArgs A, int logn) {
+    const int l = blockIdx.y, r = blockIdx.z;
+    const uint32_t k = blockIdx.x * BX + threadIdx.x;
+    const uint32_t p = (uint32_t)A.pr[l].p;
+    const double x = (double)A.rows[r][k] * A.scale;
+    int64_t m;
+    const bool ovf = !(fabs(x) < 9.2e18);
+    if (!ovf) m = (int64_t)rint(x);
+    else m = x < 0.0 ? -(int64_t(1) << 62) : (int64_t(1) << 62);
+    const uint64_t mag = m < 0 ? (uint64_t)0 - (uint64_t)m : (uint64_t)m;
+    uint32_t v = (uint32_t)(mag % p);
+    if (m < 0 && v) v = p - v;
+    ((uint32_t*)A.scratch)[((size_t)(r * A.L + l) << logn) + k] = v;
+    if (ovf && A.overflow) atomicAdd(A.overflow, 1ull);
+}
+
+__global__ void __launch_bounds__(BX) coeff_acc_k(CoeffArgs A, int logn) {
+    const int l = blockIdx.y, part = blockIdx.z;
+    const uint32_t i = lane_word();
+    const Red red(A.pr[l]);
+    const size_t row = ((size_t)l << logn) + i;
+    uint32_t* o = (uint32_t*)A.out + part * A.part_stride + row;
+    Acc s[4];
+    if (A.accumulate) {
+        const W4 y = ld4(o);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) s[w].add(y.v[w]);
+    }
+    for (int r = 0; r < A.n; ++r) {
+        const W4 x = ld4((const uint32_t*)A.scratch + ((size_t)(r * A.L + l) << logn) + i);
+        const W4 c = ld4((const uint32_t*)A.ct[r] + part * A.part_stride + row);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) s[w].add((uint64_t)x.v[w] * c.v[w]);
+    }
+    W4 z;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) z.v[w] = s[w].red(red);
+    st4(o, z);
+}
+
+template <int LOGN>
+int coeff_sum(const CoeffArgs* a, pc_stream_t s) {
+    if (!a || a->n < 1 || a->n > PC_COEFF_MAXT || a->L < 1 || a->L > PC_COEFF_MAXL) return -1;
+    if (!a->scratch || !a->out || !a->fw || !a->fws || !a->pr) return -2;
+    for (int r = 0; r < a->n; ++r)
+        if (!a->rows[r] || !a->ct[r]) return -2;
+    hipLaunchKernelGGL(coeff_conv_k, dim3((1 << LOGN) / BX, a->L, a->n), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    if (int rc = launch_rc()) return rc;
+    NttArgs t{};
+    t.base = a->scratch;
+    t.fw = a->fw;
+    t.fws = a->fws;
+    t.pr = a->pr;
+    t.nrows = a->n * a->L;
+    t.xnum = a->L;
+    if (int rc = ntt_fwd_dense(LOGN, &t, s)) return rc;
+    PCH_LAUNCH(coeff_acc_k, grid<LOGN>(a->L, 2), *a, LOGN);
+}
+
 template <int LOGN>
 int pt_dot(const PtDotArgs* a, pc_stream_t s) {
     if (!a || a->K > 8) return -1;
@@ -579,6 +644,7 @@ int pt_dot(const PtDotArgs* a, pc_stream_t s) {
     int ew_many_##L(const EwManyArgs* a, pc_stream_t s) { return em::ew_many<L>(a, s); }                             \
     int submul_many_##L(const SubMulManyArgs* a, pc_stream_t s) { return em::submul_many<L>(a, s); }             \
     int pt_dot_##L(const PtDotArgs* a, pc_stream_t s) { return em::pt_dot<L>(a, s); }                            \
+    int coeff_sum_##L(const CoeffArgs* a, pc_stream_t s) { return em::coeff_sum<L>(a, s); }                      \
     int tensor_multi_##L(const TensorMultiArgs* a, pc_stream_t s) { return em::tensor_multi<L>(a, s); }
 PCH_EM_INST(12)
 PCH_EM_INST(13)

@@ -147,7 +147,7 @@ template <bool H, int EPI>
 __global__ void __launch_bounds__(T) fwd1(NttArgs A, int row0) {
     __shared__ uint32_t lds[LDSW];
     const int i = row_of(row0);
-    const int pid = A.rprime[i];
+    const int pid = ntt::row_prime(A, i);
     const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.fw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.fws + ((size_t)pid << LOGN);
@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(T) fwd1(NttArgs A, int row0) {
         stage<true, H, 1, 2, false>(x, w, ws, 16384 + 16 * u, p, p2);
         stage<true, H, 0, 2, false>(x, w, ws, 32768 + 32 * u, p, p2);
     }
-    const size_t r0 = ((size_t)A.roff[i] << LOGN) + (size_t)W * t;
+    const size_t r0 = (ntt::row_off(A, i) << LOGN) + (size_t)W * t;
     if (EPI == 0) {
         uint4* o = (uint4*)((uint32_t*)A.base + r0);
 #pragma unroll
@@ -229,7 +229,7 @@ template <bool H>
 __global__ void __launch_bounds__(T) inv1(NttArgs A, int row0) {
     __shared__ uint32_t lds[LDSW];
     const int i = row_of(row0);
-    const int pid = A.rprime[i];
+    const int pid = ntt::row_prime(A, i);
     const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.iw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.iws + ((size_t)pid << LOGN);
@@ -277,7 +277,7 @@ __global__ void __launch_bounds__(T) inv1(NttArgs A, int row0) {
         s = ((const uint32_t*)A.ninv)[pid];
         ss = ((const uint32_t*)A.ninvs)[pid];
     }
-    uint32_t* o = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
+    uint32_t* o = (uint32_t*)A.base + (ntt::row_off(A, i) << LOGN);
 #pragma unroll
     for (int j = 0; j < W; ++j) o[t + T * j] = shoup(x[phys(4, j)], s, ss, p);
 }

@@ -275,6 +275,11 @@ __device__ __forceinline__ void a_to_b(uint32_t (&x)[E], uint32_t* l, int tau) {
     wave_sync();
 }
 
+// Row i's prime id and offset (in rows of N words). Dense launches (roff and rprime both null; internal launchers
+// only, the table entries reject them) take row i at i N with prime id i mod xnum.
+__device__ __forceinline__ int row_prime(const NttArgs& A, int i) { return A.rprime ? A.rprime[i] : i % A.xnum; }
+__device__ __forceinline__ size_t row_off(const NttArgs& A, int i) { return A.roff ? (size_t)A.roff[i] : (size_t)i; }
+
 // The first pass's source words of row i: out of place (src + soff[i] N, the sum mod p of snum rows sstride apart)
 // or in place (base + roff[i] N).
 struct RowSrc {
@@ -284,7 +289,7 @@ struct RowSrc {
 };
 __device__ __forceinline__ RowSrc row_src(const NttArgs& A, int i, int logn) {
     if (A.soff) return RowSrc{(const uint32_t*)A.src + ((size_t)A.soff[i] << logn), A.snum, A.sstride};
-    return RowSrc{(const uint32_t*)A.base + ((size_t)A.roff[i] << logn), 1, 0};
+    return RowSrc{(const uint32_t*)A.base + (row_off(A, i) << logn), 1, 0};
 }
 __device__ __forceinline__ uint32_t ld_src(const RowSrc& s, size_t off, uint32_t p) {
     uint32_t v = s.p0[off];

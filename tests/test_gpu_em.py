@@ -587,3 +587,50 @@ def test_tensor_multi(stream, nout, npairs, acc):
         got, gd2 = outs[o].get(), d2s[o].get()
         assert (got[:, 0, :n] == want[o][0]).all() and (got[:, 1, :n] == want[o][1]).all(), o
         assert (gd2[:, 1, :n] == want[o][2]).all(), o
+
+
+# ----------------------------------------------------------------------------------------------- coeff_sum
+@pytest.mark.parametrize("name,nterm,L,acc,big", [("small", 3, 6, False, True), ("small31", 5, 9, True, False),
+                                                  ("c3", 32, 36, False, False)])
+def test_coeff_sum(stream, name, nterm, L, acc, big):
+    """coeff_sum through the table: float32 weight rows rounded at a scale (ties, clamped values counted), NTT'd in the
+    scratch (dense rows; 32 x 36 = 1152 rows of N = 2^16 take the one-pass transform), summed against the
+    ciphertexts, onto the old output or not"""
+    say(f"[coeff_sum] {name} n={nterm} L={L} acc={acc} clamp={big}")
+    ch, ctx, oc = contexts(name)
+    N, R = ch.n, ch.rows
+    rng = np.random.default_rng(nterm * 7 + L)
+    q = [int(p) for p in ch.primes[:L]]
+    scale = 2.0 ** 20
+    rows = (rng.normal(size=(nterm, N)) * 3e4).astype(np.float32)
+    rows[0, :6] = [0.5 / scale, 1.5 / scale, 2.5 / scale, -0.5 / scale, -2.5 / scale, 7.0]
+    if big:
+        rows[1, :3] = [1e19, -3e30, 2e18]
+    cts = [np.zeros((2, R, N), np.uint32) for _ in range(nterm)]
+    for c in cts:
+        for part in range(2):
+            c[part, :L] = np.stack([rng.integers(0, p, N) for p in q])
+    old = np.zeros((2, R, N), np.uint32)
+    for part in range(2):
+        old[part, :L] = np.stack([rng.integers(0, p, N) for p in q])
+    bct = [pa.DevBuf.from_array(c) for c in cts]
+    brow = [pa.DevBuf.from_array(r.view(np.uint32)) for r in rows]
+    out = pa.DevBuf.from_array(old)
+    scratch = pa.DevBuf(nterm * L * N)
+    ovf = pa.DevBuf.from_array(np.zeros(2, np.uint32))
+    a = abi.CoeffArgs()
+    a.scratch, a.out = scratch.ptr.value, out.ptr.value
+    a.fw, a.fws = LIB.pcx_ctx_twiddle(ctx.h, 0), LIB.pcx_ctx_twiddle(ctx.h, 1)
+    a.pr, a.overflow = pr_of(ctx), ovf.ptr.value
+    a.part_stride, a.scale, a.n, a.L, a.accumulate = R * N, scale, nterm, L, int(acc)
+    for r in range(nterm):
+        a.rows[r], a.ct[r] = brow[r].ptr.value, bct[r].ptr.value
+    run("coeff_sum", a, stream, ch.logn)
+    got = out.download((2, R, N))
+    twin.set_threads(16)
+    want, want_ovf = em.coeff_sum(q, rows, scale, [c[:, :L] for c in cts], oc.ntt_fwd,
+                                  out=old[:, :L] if acc else None)
+    assert (got[:, :L] == want).all()
+    assert int(ovf.download().view(np.uint64)[0]) == want_ovf
+    if not acc:
+        assert (got[:, L:] == old[:, L:]).all(), "rows past L untouched"

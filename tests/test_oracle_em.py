@@ -419,3 +419,49 @@ def test_pack_dot_decrypts_to_the_errors():
         want = addq(want, mulq(dig[j], e[j], Q), Q)
     want[:nq] = addq(want[:nq], mulq(c0[:nq], np.array(pmod[:nq], np.uint64).reshape(nq, 1).repeat(N, 1), Q), Q)
     assert (addq(s0, mulq(s1, s, Q), Q) == want).all()
+
+
+# ----------------------------------------------------------------------------------------------- coeff_sum
+def test_coeff_residues_against_python_integers():
+    """round half to even of float32 * scale in float64, the +-2^62 clamp past 9.2e18 counted per limb, the residue
+    of a negative value p - (|m| mod p)"""
+    q = [1073479681, 2147352577, 97]
+    f = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.0, -7.25, 1e19, -1e19, 123456.78, -0.0], np.float32)
+    rng = np.random.default_rng(4)
+    f = np.concatenate([f, rng.normal(size=200).astype(np.float32) * 1e6])
+    for scale in (1.0, 2.0 ** 20, 3.7):
+        got, ovf = em.coeff_residues(f[None], scale, q)
+        n_big = 0
+        for k, v in enumerate(f):
+            x = float(v) * scale
+            if abs(x) < 9.2e18:
+                m = round(x)
+            else:
+                m = -(1 << 62) if x < 0 else 1 << 62
+                n_big += 1
+            assert [int(got[t, 0, k]) for t in range(len(q))] == [m % p for p in q], (scale, k, v)
+        assert ovf == n_big * len(q)
+
+
+def test_coeff_sum_against_the_schoolbook_product():
+    """INTT(out) = sum_r INTT(ct_r) * m_r (negacyclic, mod p) with m_r = round(rows_r scale), plus the old out"""
+    oc = small_chain(logn=6, nq=3, kp=0, dnum=1)
+    n_terms, N = 3, oc.n
+    q = [int(p) for p in oc.primes]
+    rng = np.random.default_rng(8)
+    rows = (rng.normal(size=(n_terms, N)) * 40).astype(np.float32)
+    cts = [np.stack([np.stack([rng.integers(0, p, N) for p in q]) for _ in range(2)]).astype(np.uint32)
+           for _ in range(n_terms)]
+    old = np.stack([np.stack([rng.integers(0, p, N) for p in q]) for _ in range(2)]).astype(np.uint32)
+    out, ovf = em.coeff_sum(q, rows, 3.0, cts, oc.ntt_fwd, out=old)
+    assert ovf == 0
+    ids = list(range(len(q)))
+    for part in range(2):
+        got = oc.ntt_inv(out[part].copy(), ids)
+        want = oc.ntt_inv(old[part].copy(), ids).astype(object)
+        for r in range(n_terms):
+            c = oc.ntt_inv(cts[r][part].copy(), ids)
+            m = [round(float(v) * 3.0) for v in rows[r]]
+            for t, p in enumerate(q):
+                want[t] = (want[t] + np.array(negacyclic([int(x) for x in c[t]], m), dtype=object)) % p
+        assert (got.astype(object) == want).all(), part

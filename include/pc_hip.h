@@ -625,6 +625,33 @@ typedef struct CoeffArgs {
 } CoeffArgs;
 PC_STATIC_ASSERT(sizeof(CoeffArgs) == 80 + 16 * PC_COEFF_MAXT, "CoeffArgs layout");
 
+/* args.cuh:407-436 (tensor_seeded, ABI 27-28): tensor_multi over seeded first operands that share their second ones,
+ * single ciphertexts, rows [0, n): output q nout + o = sum_{j < npairs} a[o][j] * set q's j-th second operand (set 0:
+ * b[j]; set q > 0: bq[q - 1][j] with b[j]'s strides); c0, c1 into out[], d2 into part 1 of d2[]; acc as
+ * tensor_sum's (nonzero: onto out's c0, c1; bit 1: onto d2). a[o][j] is a seeded ciphertext's c0, row r at r N words
+ * (packed: r PC_PACK_ROW_WORDS words, 28 bits per coefficient, one little-endian bit stream per row); its rows' 8-word
+ * seeds at a[o][j] + seed_off + 8 r; its c1 word (row, slot) is drawn in the kernel by the "CTSA" expander
+ * (crates/pc-core/src/keys.rs:580-630). cout and swords only schedule the reference's blocks; here they are ignored.
+ * Every sum is reduced exactly (no lazy bound on the pairs). u32 words only. */
+#define PC_PACK_BITS 28
+#define PC_TSEED_OUT 16
+#define PC_TSEED_PAIRS 128
+#define PC_TSEED_Q 4
+#define PC_TSEED_QOUT 64
+typedef struct TensorSeededArgs {
+    PolyRef out[PC_TSEED_QOUT], d2[PC_TSEED_QOUT];
+    PolyRef b[PC_TSEED_PAIRS];
+    const void* a[PC_TSEED_OUT][PC_TSEED_PAIRS];
+    const PrimeConst* pr;
+    uint64_t seed_off;
+    int32_t nout, npairs, acc, n, packed, pad;
+    const void* bq[PC_TSEED_Q - 1][PC_TSEED_PAIRS];
+    int32_t nq, cout, swords, qpad;
+} TensorSeededArgs;
+PC_STATIC_ASSERT(sizeof(TensorSeededArgs) == (2 * PC_TSEED_QOUT + PC_TSEED_PAIRS) * 24 + PC_TSEED_OUT * PC_TSEED_PAIRS * 8 +
+                                                 16 + 24 + (PC_TSEED_Q - 1) * PC_TSEED_PAIRS * 8 + 16,
+                 "TensorSeededArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct EncodeArgs;
 struct SpruExtractArgs;
@@ -633,7 +660,6 @@ struct SpruScatterArgs;
 struct PcmmArgs;
 struct CcmmArgs;
 struct TfheArgs;
-struct TensorSeededArgs;
 
 /* args.cuh:1035-1097 */
 typedef struct KernelTable {

@@ -339,3 +339,56 @@ def coeff_sum(q, rows, scale, cts, ntt, out=None):
         for part in range(2):
             acc[part] = (acc[part] + pt * np.asarray(cts[r][part], U64) % qq) % qq
     return acc.astype(np.uint32), ovf
+
+
+# ----------------------------------------------------------------------------------------------- tensor_seeded
+PACK_BITS = 28
+
+
+def pack28(rows):
+    """rows [n][N] of values below 2^28 as little-endian 28-bit streams, (N 28 + 31) / 32 words per row
+    (args.cuh:412-413)"""
+    rows = np.asarray(rows, U64)
+    n, N = rows.shape
+    words = (N * PACK_BITS + 31) // 32
+    out = np.zeros((n, words + 1), U64)
+    for i in range(N):
+        bit = PACK_BITS * i
+        w, sh = bit >> 5, bit & 31
+        v = rows[:, i] << U64(sh)
+        out[:, w] |= v & U64(0xFFFFFFFF)
+        out[:, w + 1] |= v >> U64(32)
+    return out[:, :words].astype(np.uint32)
+
+
+def tensor_seeded(q, c0s, seeds, bsets, acc=0, old=None, old_d2=None, cts_row=None):
+    """tensor_seeded (args.cuh:407-436; crates/pc-host/src/elem.rs:345-404): first operands o < nout, j < npairs given
+    by their c0 rows c0s[o][j] [n][N] (the words as stored) and row seeds seeds[o][j] [n][8], their c1 rows drawn by
+    cts_row(seed, p, N); second-operand sets bsets[q][j] [2][n][N]. Output m = q nout + o: (c0, c1, d2) =
+    sum_j (x0 y0, x0 y1 + x1 y0, x1 y1) mod p; acc nonzero adds the old c0, c1, bit 1 the old d2.
+    Returns (out [M][2][n][N], d2 [M][n][N])."""
+    nout, npairs = len(c0s), len(c0s[0])
+    n, N = np.asarray(c0s[0][0]).shape
+    qq = np.asarray(q[:n], U64)[:, None]
+    outs, d2s = [], []
+    for bs in bsets:
+        for o in range(nout):
+            s0 = np.zeros((n, N), U64)
+            s1 = np.zeros((n, N), U64)
+            s2 = np.zeros((n, N), U64)
+            for j in range(npairs):
+                x0 = np.asarray(c0s[o][j], U64) % qq
+                x1 = np.stack([np.asarray(cts_row(seeds[o][j][r], int(q[r]), N), U64) for r in range(n)])
+                y0, y1 = np.asarray(bs[j][0], U64), np.asarray(bs[j][1], U64)
+                s0 = (s0 + x0 * y0 % qq) % qq
+                s1 = (s1 + x0 * y1 % qq + x1 * y0 % qq) % qq
+                s2 = (s2 + x1 * y1 % qq) % qq
+            m = len(outs)
+            if acc:
+                s0 = (s0 + np.asarray(old[m][0], U64)) % qq
+                s1 = (s1 + np.asarray(old[m][1], U64)) % qq
+            if acc & 2:
+                s2 = (s2 + np.asarray(old_d2[m], U64)) % qq
+            outs.append(np.stack([s0, s1]).astype(np.uint32))
+            d2s.append(s2.astype(np.uint32))
+    return np.stack(outs), np.stack(d2s)

@@ -172,14 +172,14 @@ constexpr uint32_t KSK_T_MAX = 16;
 // (tag: "KSKA" for switching keys; the same rule with "ENCA" and w13 = the nonce expands an encryption's a,
 // args.cuh:614-617)
 void kska_range(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t s0, uint32_t cnt, uint32_t* out,
-                uint32_t tag = TAG_KSKA) {
+                uint32_t tag = TAG_KSKA, uint32_t tmax = KSK_T_MAX) {
     const uint32_t n16 = n >> 4, mp = (0xFFFFFFFFu / p) * p;
     uint32_t base[16], alt[16];
     for (uint32_t b0 = s0 >> 4; b0 < (s0 + cnt) >> 4; ++b0) {
         chacha_block(seed, b0, digit, p, tag, 12, base);
         for (int w = 0; w < 16; ++w) {
             uint32_t v = base[w];
-            for (uint32_t t = 1; v >= mp && t < KSK_T_MAX; ++t) {
+            for (uint32_t t = 1; v >= mp && t < tmax; ++t) {
                 chacha_block(seed, b0 + t * n16, digit, p, tag, 12, alt);
                 v = alt[w];
             }
@@ -445,6 +445,11 @@ void or_chacha_block(const uint32_t key[8], uint32_t w12, uint32_t w13, uint32_t
 }
 void or_kska_expand_row(const uint32_t seed[8], uint32_t digit, uint32_t p, uint32_t n, uint32_t* out) {
     kska_row(seed, digit, p, n, out);
+}
+// keys.rs:580-630 (cts_expand_row): a regenerable ciphertext's c1 row, the KSKA rule with w13 = 0, the "CTSA" tag and
+// 32 attempts
+void or_cts_expand_row(const uint32_t seed[8], uint32_t p, uint32_t n, uint32_t* out) {
+    kska_range(seed, 0, p, n, 0, n, out, 0x43545341u, 32);
 }
 void or_expand_row(const uint32_t seed[8], uint32_t w13, uint32_t p, uint32_t n, uint32_t tag, uint32_t* out) {
     kska_range(seed, w13, p, n, 0, n, out, tag);

@@ -37,6 +37,7 @@ uint32_t or_kska_expand(const uint32_t seed[8], uint32_t digit, uint32_t p, uint
 /* the expander rule of or_kska_expand_row under any tag (w15) and w13: "ENCA" with w13 = the nonce gives secret-key
  * encryption's a (crates/pc-kernels/kernels/args.cuh:614-617) */
 void or_expand_row(const uint32_t seed[8], uint32_t w13, uint32_t p, uint32_t n, uint32_t tag, uint32_t* out);
+void or_cts_expand_row(const uint32_t seed[8], uint32_t p, uint32_t n, uint32_t* out);
 void or_kskb_expand_row(const uint32_t seed[8], uint32_t digit, uint64_t p, uint32_t n, uint64_t* out);
 
 /* ---- sampler DRBG and samplers (crates/pc-core/src/keys.rs:122-325) ---- */

@@ -93,6 +93,17 @@ class CoeffArgs(C.Structure):
                 ("pad", i32), ("rows", vp * COEFF_MAXT), ("ct", vp * COEFF_MAXT)]
 
 
+TSEED_OUT, TSEED_PAIRS, TSEED_Q, TSEED_QOUT = 16, 128, 4, 64
+
+
+class TensorSeededArgs(C.Structure):
+    """args.cuh:407-436 (25656 bytes): tensor_seeded."""
+    _fields_ = [("out", PolyRef * TSEED_QOUT), ("d2", PolyRef * TSEED_QOUT), ("b", PolyRef * TSEED_PAIRS),
+                ("a", (vp * TSEED_PAIRS) * TSEED_OUT), ("pr", vp), ("seed_off", u64), ("nout", i32), ("npairs", i32),
+                ("acc", i32), ("n", i32), ("packed", i32), ("pad", i32), ("bq", (vp * TSEED_PAIRS) * (TSEED_Q - 1)),
+                ("nq", i32), ("cout", i32), ("swords", i32), ("qpad", i32)]
+
+
 class EwArgs(C.Structure):
     """args.cuh:144-157 (128 bytes): element-wise row-set kernels (ew_add / ew_scale / ew_sub_mul / ew_copy)."""
     _fields_ = [("out", PolyRef), ("a", PolyRef), ("b", PolyRef), ("rs", RowSet), ("sc", vp), ("scs", vp),
@@ -273,7 +284,7 @@ KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:207-210)
 assert C.sizeof(KeyTab) == 40 and C.sizeof(CtsArgs) == 200 and C.sizeof(CtsRegenArgs) == 240
 assert C.sizeof(KsArgs) == 176 and C.sizeof(KsKeyArgs) == 216 and C.sizeof(EpiArgs) == 72
 assert C.sizeof(KsRegenArgs) == 312
-assert C.sizeof(EwArgs) == 128 and C.sizeof(CoeffArgs) == 592
+assert C.sizeof(EwArgs) == 128 and C.sizeof(CoeffArgs) == 592 and C.sizeof(TensorSeededArgs) == 25656
 assert C.sizeof(PolyRef) == 24 and C.sizeof(NttArgs) == 176 and C.sizeof(TensorArgs) == 192
 assert C.sizeof(TensorYArgs) == 240 and C.sizeof(TensorSumArgs) == 2 * 24 + 2 * TSUM_MAX * 24 + 8 + 16
 assert C.sizeof(MdEpiArgs) == 120 and C.sizeof(MdEpiToArgs) == 152 and C.sizeof(WsumArgs) == 256

@@ -987,6 +987,160 @@ int ksk_unpack(const KskUnpackArgs* a, pc_stream_t s) {
     return launch_rc();
 }
 
+// ------------------------------------------------------------------------------------------------ tensor_seeded
+// tensor_seeded (args.cuh:407-436; host twin crates/pc-host/src/elem.rs:345-404). The table's argument struct is
+// 25 KiB, beyond a kernel's argument space, so the launcher runs it in chunks of TS_OUT outputs x TS_PAIRS pairs:
+// each chunk reduces its sums exactly and the chunks after a group's first add onto its outputs (acc 3), which gives
+// the words of one sum.
+constexpr int TS_OUT = 4, TS_PAIRS = 32, TS_BX = 64;
+constexpr uint32_t TAG_CTSA = 0x43545341u;  // "CTSA" (keys.rs:580-582)
+constexpr int CTS_T_MAX = 32;               // attempts per word (keys.rs:585-587)
+struct TsChunk {
+    PolyRef out[TS_OUT], d2[TS_OUT];
+    PolyRef b[TS_PAIRS];
+    const uint32_t* a[TS_OUT][TS_PAIRS];
+    const PrimeConst* pr;
+    uint64_t seed_off;
+    int nout, npairs, acc, packed;
+};
+
+// 16 consecutive c1 words (slots s0 .. s0 + 15, s0 a multiple of 16) of a regenerable ciphertext's row with prime p:
+// ChaCha12 block s0 / 16 of (seed, w13 = 0, p, "CTSA"), a rejected word redrawn from block s0 / 16 + t N / 16
+// (t < 32, the last draw kept), then mod p
+__device__ __forceinline__ void cts16(const uint32_t (&seed)[8], uint32_t s0, const Expander& ex, uint32_t n16,
+                                      uint32_t (&a)[16]) {
+    const uint32_t ctr = s0 >> 4;
+    uint32_t o[16];
+    chacha12(seed, ctr, 0, ex.p, TAG_CTSA, o);
+    uint32_t rej = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rej |= (uint32_t)(o[j] >= ex.mp) << j;
+    while (rej) {
+        const int j = __builtin_ctz(rej);
+        rej &= rej - 1;
+        uint32_t v = 0;
+        for (int t = 1; t < CTS_T_MAX; ++t) {
+            v = chacha12_word(seed, ctr + (uint32_t)t * n16, 0, ex.p, TAG_CTSA, j);
+            if (v < ex.mp) break;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) o[jj] = jj == j ? v : o[jj];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a[j] = ex.red(o[j]);
+}
+
+// one thread: 16 slots (one ChaCha block) of one row, every output and pair of the chunk
+__global__ void __launch_bounds__(TS_BX) tseed_k(TsChunk A, int logn) {
+    const int row = blockIdx.y;
+    const uint32_t s0 = (blockIdx.x * TS_BX + threadIdx.x) * 16;
+    const uint32_t n = 1u << logn, n16 = n >> 4;
+    const Red red(A.pr[row]);
+    const Expander ex(red.p);
+    const uint32_t p = red.p;
+    const size_t roff = ((size_t)row << logn) + s0;
+    const uint32_t roww = (n * PC_PACK_BITS + 31) / 32;
+    for (int o = 0; o < A.nout; ++o) {
+        uint32_t s0v[16], s1v[16], s2v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) s0v[k] = s1v[k] = s2v[k] = 0;
+        for (int j = 0; j < A.npairs; ++j) {
+            const uint32_t* base = A.a[o][j];
+            uint32_t x0[16], x1[16], y0[16], y1[16];
+            if (A.packed) {
+                // 16 words of 28 bits = 14 words of the row's bit stream, word-aligned at slot s0
+                const uint32_t* w = base + (size_t)row * roww + (s0 / 16) * 14;
+                uint32_t u[15];
+#pragma unroll
+                for (int k = 0; k < 14; ++k) u[k] = w[k];
+                u[14] = 0;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int bit = 28 * k, wi = bit >> 5, sh = bit & 31;
+                    const uint64_t v = ((uint64_t)u[wi + 1] << 32) | u[wi];
+                    x0[k] = (uint32_t)(v >> sh) & ((1u << PC_PACK_BITS) - 1u);
+                }
+            } else {
+                ld16(base + roff, x0);
+            }
+            uint32_t seed[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) seed[k] = base[A.seed_off + 8 * (size_t)row + k];
+            cts16(seed, s0, ex, n16, x1);
+            const uint32_t* b0 = (const uint32_t*)A.b[j].base + roff;
+            ld16(b0, y0);
+            ld16(b0 + A.b[j].part_stride, y1);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                s0v[k] = red((uint64_t)s0v[k] + (uint64_t)x0[k] * y0[k]);
+                s1v[k] = red((uint64_t)s1v[k] + (uint64_t)x0[k] * y1[k]);
+                s1v[k] = red((uint64_t)s1v[k] + (uint64_t)x1[k] * y0[k]);
+                s2v[k] = red((uint64_t)s2v[k] + (uint64_t)x1[k] * y1[k]);
+            }
+        }
+        uint32_t* o0 = (uint32_t*)A.out[o].base + roff;
+        uint32_t* o1 = o0 + A.out[o].part_stride;
+        uint32_t* d2 = (uint32_t*)A.d2[o].base + A.d2[o].part_stride + roff;
+        if (A.acc) {
+            uint32_t v0[16], v1[16];
+            ld16(o0, v0);
+            ld16(o1, v1);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) s0v[k] = addm(s0v[k], v0[k], p), s1v[k] = addm(s1v[k], v1[k], p);
+        }
+        if (A.acc & 2) {
+            uint32_t v2[16];
+            ld16(d2, v2);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) s2v[k] = addm(s2v[k], v2[k], p);
+        }
+        st16(o0, s0v);
+        st16(o1, s1v);
+        st16(d2, s2v);
+    }
+}
+
+template <int LOGN>
+int tensor_seeded(const TensorSeededArgs* a, pc_stream_t s) {
+    if (!a || !a->pr || a->nq < 1 || a->nq > PC_TSEED_Q || a->nout < 1 || a->nout > PC_TSEED_OUT || a->npairs < 1 ||
+        a->npairs > PC_TSEED_PAIRS || a->nq * a->nout > PC_TSEED_QOUT || a->n < 0)
+        return -1;
+    for (int j = 0; j < a->npairs; ++j) {
+        if (!a->b[j].base) return -1;
+        for (int q = 1; q < a->nq; ++q)
+            if (!a->bq[q - 1][j]) return -1;
+        for (int o = 0; o < a->nout; ++o)
+            if (!a->a[o][j]) return -1;
+    }
+    for (int m = 0; m < a->nq * a->nout; ++m)
+        if (!a->out[m].base || !a->d2[m].base) return -1;
+    if (a->n == 0) return 0;
+    const dim3 grid((1u << LOGN) / 16 / TS_BX, a->n);
+    for (int q = 0; q < a->nq; ++q)
+        for (int o0 = 0; o0 < a->nout; o0 += TS_OUT)
+            for (int j0 = 0; j0 < a->npairs; j0 += TS_PAIRS) {
+                TsChunk c{};
+                c.nout = std::min(TS_OUT, a->nout - o0);
+                c.npairs = std::min(TS_PAIRS, a->npairs - j0);
+                for (int k = 0; k < c.nout; ++k) {
+                    c.out[k] = a->out[q * a->nout + o0 + k];
+                    c.d2[k] = a->d2[q * a->nout + o0 + k];
+                    for (int j = 0; j < c.npairs; ++j) c.a[k][j] = (const uint32_t*)a->a[o0 + k][j0 + j];
+                }
+                for (int j = 0; j < c.npairs; ++j) {
+                    c.b[j] = a->b[j0 + j];
+                    if (q > 0) c.b[j].base = const_cast<void*>(a->bq[q - 1][j0 + j]);
+                }
+                c.pr = a->pr;
+                c.seed_off = a->seed_off;
+                c.acc = j0 == 0 ? a->acc : 3;
+                c.packed = a->packed;
+                hipLaunchKernelGGL(tseed_k, grid, dim3(TS_BX), 0, (hipStream_t)s, c, LOGN);
+                if (int rc = launch_rc()) return rc;
+            }
+    return 0;
+}
+
 }  // namespace ks
 
 #define PCH_KS_INST(L)                                                                                        \
@@ -997,7 +1151,8 @@ int ksk_unpack(const KskUnpackArgs* a, pc_stream_t s) {
     int pack_split_##L(const PackSplitArgs* a, pc_stream_t s) { return ks::pack_split<L>(a, s); }            \
     int pack_dot_##L(const PackDotArgs* a, pc_stream_t s) { return ks::pack_dot<L>(a, s); }                  \
     int ksk_gen_##L(const KskGenArgs* a, pc_stream_t s) { return ks::ksk_gen<L>(a, s); }                     \
-    int ksk_unpack_##L(const KskUnpackArgs* a, pc_stream_t s) { return ks::ksk_unpack<L>(a, s); }
+    int ksk_unpack_##L(const KskUnpackArgs* a, pc_stream_t s) { return ks::ksk_unpack<L>(a, s); }            \
+    int tensor_seeded_##L(const TensorSeededArgs* a, pc_stream_t s) { return ks::tensor_seeded<L>(a, s); }
 PCH_KS_INST(12)
 PCH_KS_INST(13)
 PCH_KS_INST(14)

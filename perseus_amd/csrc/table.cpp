@@ -45,6 +45,7 @@ namespace pch {
     int encrypt_##L(const EncryptArgs*, pc_stream_t);                \
     int pt_dot_##L(const PtDotArgs*, pc_stream_t);                   \
     int coeff_sum_##L(const CoeffArgs*, pc_stream_t);                \
+    int tensor_seeded_##L(const TensorSeededArgs*, pc_stream_t);     \
     int pack_split_##L(const PackSplitArgs*, pc_stream_t);           \
     int pack_dot_##L(const PackDotArgs*, pc_stream_t);               \
     int tensor_multi_##L(const TensorMultiArgs*, pc_stream_t);
@@ -70,7 +71,7 @@ int absent(const A*, pc_stream_t) {
         cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>, wsum_k_##L, rescale_combine_to_##L, \
         md_epilogue_to_##L, small_int1_##L, coeff_sum_##L, mul_add_##L, rescale_fwd_##L,          \
         mul_add_n_##L, tensor_y_##L, wsum_multi_##L, bconv_##L, absent<TfheArgs>, tensor_sum_##L,                    \
-        tensor_multi_##L, absent<TensorSeededArgs>, ew_many_##L, submul_many_##L, pack_split_##L,      \
+        tensor_multi_##L, tensor_seeded_##L, ew_many_##L, submul_many_##L, pack_split_##L,      \
         pack_dot_##L};
 PCH_TABLE(12)
 PCH_TABLE(13)

@@ -634,3 +634,67 @@ def test_coeff_sum(stream, name, nterm, L, acc, big):
     assert int(ovf.download().view(np.uint64)[0]) == want_ovf
     if not acc:
         assert (got[:, L:] == old[:, L:]).all(), "rows past L untouched"
+
+
+# ----------------------------------------------------------------------------------------------- tensor_seeded
+@pytest.mark.parametrize("name,nout,npairs,nq,packed,acc", [("small", 2, 3, 1, False, 0), ("small28", 5, 34, 2, True, 1),
+                                                           ("c3", 1, 2, 1, False, 3)])
+def test_tensor_seeded(stream, name, nout, npairs, nq, packed, acc):
+    """tensor_seeded through the table: seeded first operands (c0 stored plain or as 28-bit streams, c1 drawn by the
+    "CTSA" expander in the kernel), 5 outputs x 34 pairs cross the launcher's 4 x 32 chunks, two second-operand sets,
+    accumulate modes"""
+    say(f"[tensor_seeded] {name} nout={nout} npairs={npairs} nq={nq} packed={packed} acc={acc}")
+    ch, ctx, _ = contexts(name)
+    N, R = ch.n, ch.rows
+    n = 4 if name == "c3" else len(ch.q)
+    q = [int(p) for p in ch.primes]
+    rng = np.random.default_rng(nout * 10 + npairs + acc)
+    roww = (N * 28 + 31) // 32
+    c0s, seeds, abufs = [], [], []
+    for o in range(nout):
+        rc, rs, rb = [], [], []
+        for j in range(npairs):
+            c0 = np.stack([rng.integers(0, min(q[r], 1 << 28), N) for r in range(n)]).astype(np.uint32)
+            sd = rng.integers(0, 1 << 32, (n, 8), dtype=np.uint64).astype(np.uint32)
+            body = em.pack28(c0) if packed else c0
+            buf = np.concatenate([body.reshape(-1), sd.reshape(-1)])
+            rc.append(c0)
+            rs.append(sd)
+            rb.append(pa.DevBuf.from_array(buf))
+        c0s.append(rc)
+        seeds.append(rs)
+        abufs.append(rb)
+    seed_off = n * (roww if packed else N)
+    bsets = [[np.zeros((2, R, N), np.uint32) for _ in range(npairs)] for _ in range(nq)]
+    for bs in bsets:
+        for b in bs:
+            for part in range(2):
+                b[part, :n] = np.stack([rng.integers(0, q[r], N) for r in range(n)])
+    bbufs = [[pa.DevBuf.from_array(b) for b in bs] for bs in bsets]
+    M = nq * nout
+    old = np.zeros((M, 2, R, N), np.uint32)
+    for m in range(M):
+        for part in range(2):
+            old[m, part, :n] = np.stack([rng.integers(0, q[r], N) for r in range(n)])
+    outb = pa.DevBuf.from_array(old)
+    d2b = pa.DevBuf.from_array(old)  # d2 goes to part 1 of each d2 ciphertext
+    a = abi.TensorSeededArgs()
+    cw = 2 * R * N
+    for m in range(M):
+        a.out[m] = abi.PolyRef(outb.ptr.value + 4 * m * cw, cw, R * N)
+        a.d2[m] = abi.PolyRef(d2b.ptr.value + 4 * m * cw, cw, R * N)
+    for j in range(npairs):
+        a.b[j] = abi.PolyRef(bbufs[0][j].ptr.value, cw, R * N)
+        for qs in range(1, nq):
+            a.bq[qs - 1][j] = bbufs[qs][j].ptr.value
+        for o in range(nout):
+            a.a[o][j] = abufs[o][j].ptr.value
+    a.pr, a.seed_off = pr_of(ctx), seed_off
+    a.nout, a.npairs, a.acc, a.n, a.packed, a.nq = nout, npairs, acc, n, int(packed), nq
+    run("tensor_seeded", a, stream, ch.logn)
+    got = outb.download((M, 2, R, N))
+    got_d2 = d2b.download((M, 2, R, N))[:, 1]
+    want, want_d2 = em.tensor_seeded(q, c0s, seeds, [[b[:, :n] for b in bs] for bs in bsets], acc=acc,
+                                     old=old[:, :, :n], old_d2=old[:, 1, :n], cts_row=twin.cts_expand_row)
+    assert (got[:, :, :n] == want).all()
+    assert (got_d2[:, :n] == want_d2).all()

@@ -274,3 +274,30 @@ def test_samplers():
     blk0 = twin.chacha_block(key, 0, 0, 3, 0x47425244, 20)
     blk1 = twin.chacha_block(key, 1, 0, 3, 0x47425244, 20)
     assert [h.u32() for _ in range(32)] == [int(x) for x in np.concatenate([blk0, blk1])]
+
+
+def test_cts_expand_rule():
+    """The regenerable-ciphertext c1 lane (keys.rs:580-630): slot s reads word s & 15 of ChaCha12 block s >> 4 with
+    (w13, w14, w15) = (0, p, "CTSA"); a word at or above floor((2^32 - 1)/p) p is redrawn from block s >> 4 + t N/16,
+    t < 32, the last draw kept; value mod p. The reference's own checks: values below p, rows distinct per seed, per
+    prime and from the KSKA lane (crates/pc-core/tests/cts_expand.rs)."""
+    n = 1 << 10
+    seed = [((i + 1) * 0x9E3779B9 ^ (w * 0x85EBCA6B)) & 0xFFFFFFFF for i, w in [(0, w) for w in range(8)]]
+    for p in (134176769, 268369921, 1431655777):  # the last one just above 2^32 / 3: a third of the words redrawn
+        row = twin.cts_expand_row(seed, p, n)
+        mp = (0xFFFFFFFF // p) * p
+        for s in range(0, n, 37):
+            b0, w = s >> 4, s & 15
+            v = 0
+            for t in range(32):
+                v = int(twin.chacha_block(seed, b0 + t * (n // 16), 0, p, 0x43545341, 12)[w])
+                if v < mp:
+                    break
+            assert int(row[s]) == v % p, (p, s)
+        assert (row < p).all()
+    p = 134176769
+    a = twin.cts_expand_row(seed, p, n)
+    b = twin.cts_expand_row([x ^ 1 for x in seed], p, n)
+    c = twin.cts_expand_row(seed, 132120577, n)
+    k = twin.expand_row(seed, 0, p, n, twin.TAG_KSKA)
+    assert (a == b).sum() < 4 and (a == c).sum() < 4 and (a == k).sum() < 4

@@ -465,3 +465,37 @@ def test_coeff_sum_against_the_schoolbook_product():
             for t, p in enumerate(q):
                 want[t] = (want[t] + np.array(negacyclic([int(x) for x in c[t]], m), dtype=object)) % p
         assert (got.astype(object) == want).all(), part
+
+
+# ----------------------------------------------------------------------------------------------- tensor_seeded
+def test_tensor_seeded_is_the_tensor_of_the_expanded_ciphertexts():
+    """tensor_seeded's oracle equals the (pinned) tensor of full ciphertexts whose c1 rows are the (pinned) CTSA rows
+    of their seeds, for every second-operand set; the 28-bit packing round-trips"""
+    q = [268369921, 268361729, 268271617]
+    n, N = 3, 64
+    rng = np.random.default_rng(12)
+    nout, npairs = 2, 3
+    c0s = [[np.stack([rng.integers(0, p, N) for p in q]).astype(np.uint32) for _ in range(npairs)] for _ in range(nout)]
+    seeds = [[rng.integers(0, 1 << 32, (n, 8), dtype=np.uint64).astype(np.uint32) for _ in range(npairs)]
+             for _ in range(nout)]
+    bsets = [[np.stack([np.stack([rng.integers(0, p, N) for p in q]) for _ in range(2)]).astype(np.uint32)
+              for _ in range(npairs)] for _ in range(2)]
+    old = rng.integers(0, 1 << 27, (4, 2, n, N)).astype(np.uint32)
+    old_d2 = rng.integers(0, 1 << 27, (4, n, N)).astype(np.uint32)
+    out, d2 = em.tensor_seeded(q, c0s, seeds, bsets, acc=3, old=old, old_d2=old_d2, cts_row=twin.cts_expand_row)
+    m = 0
+    for bs in bsets:
+        for o in range(nout):
+            pairs = []
+            for j in range(npairs):
+                c1 = np.stack([twin.cts_expand_row(seeds[o][j][r], q[r], N) for r in range(n)])
+                pairs.append((np.stack([c0s[o][j], c1])[None], bs[j][None]))
+            w0, w1, w2 = em.tensor(q, pairs, old=old[m][None], old_d2=old_d2[m][None], acc=True, acc_d2=True)
+            assert (out[m, 0] == w0[0]).all() and (out[m, 1] == w1[0]).all() and (d2[m] == w2[0]).all()
+            m += 1
+    vals = rng.integers(0, 1 << 28, (2, 40)).astype(np.uint32)
+    pk = em.pack28(vals)
+    assert pk.shape == (2, (40 * 28 + 31) // 32)
+    for r in range(2):
+        stream = int.from_bytes(pk[r].tobytes(), "little")
+        assert [(stream >> (28 * i)) & ((1 << 28) - 1) for i in range(40)] == [int(v) for v in vals[r]]

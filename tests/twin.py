@@ -35,6 +35,7 @@ def _load():
         "or_kska_expand_row": (None, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, u32p]),
         "or_kska_expand": (C.c_uint32, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
         "or_expand_row": (None, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, u32p]),
+        "or_cts_expand_row": (None, [u32p, C.c_uint32, C.c_uint32, u32p]),
         "or_kskb_expand_row": (None, [u32p, C.c_uint32, C.c_uint64, C.c_uint32, u64p]),
         "or_prng_new": (C.c_void_p, [u32p, C.c_uint32]),
         "or_prng_free": (None, [C.c_void_p]),
@@ -333,6 +334,13 @@ TAG_KSKA, TAG_ENCA = 0x4B534B41, 0x454E4341
 def expand_row(seed, w13, p, n, tag):
     out = np.zeros(n, np.uint32)
     LIB.or_expand_row(np.asarray(seed, np.uint32), w13, p, n, tag, out)
+    return out
+
+
+def cts_expand_row(seed, p, n):
+    """a regenerable ciphertext's c1 row (the "CTSA" lane)"""
+    out = np.zeros(n, np.uint32)
+    LIB.or_cts_expand_row(np.asarray(seed, np.uint32), p, n, out)
     return out
 
 

@@ -412,9 +412,12 @@ class Bootstrap:
     an operations object. `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
     scale par.delta_in. Plaintexts (the levels' diagonals, the i monomial) are encoded once by `prepare`."""
 
-    def __init__(self, ops, par, primes, ops2=None):
+    def __init__(self, ops, par, primes, ops2=None, special=None):
         self.ops, self.par, self.ops2 = ops, par, ops2
         self.q = [int(p) for p in primes]
+        # special primes given: the levels' babies run fused in the extended basis (cts: one ModUp, the products of
+        # the key-switched babies before any ModDown, one ModDown per giant step), the diagonals encoded over Q and P
+        self.p = None if special is None else [int(x) for x in special]
         self.T = len(self.q) - 1
         n = par.n
         self.cts = [BsgsPlan(lv, n) for lv in cts_levels(n, par.cts)]
@@ -449,12 +452,17 @@ class Bootstrap:
         for plans, f in ((self.cts, self.cts_f), (self.stc, 1.0)):
             for p in plans:
                 sc = self.ev.qq(top) * f
-                prim = self.q[: top + 1]
+                prim = self.q[: top + 1] + (self.p or [])
                 row = []
                 for j in range(p.G):
                     for i in range(p.B):
                         d = p.pts[j][i]
-                        row.append(None if d is None else ops.plaintext(encode_rows(d, N, sc, prim), top))
+                        if d is None:
+                            row.append(None)
+                        elif self.p is None:
+                            row.append(ops.plaintext(encode_rows(d, N, sc, prim), top))
+                        else:
+                            row.append(ops.plaintext_ext(encode_rows(d, N, sc, prim), top))
                 self.pts.append(row)
                 top -= 2
                 if plans is self.cts and p is self.cts[-1]:
@@ -469,15 +477,22 @@ class Bootstrap:
     def lt(self, x, plan, pts, f):
         ops, top = self.ops, x.top
         B, G = plan.B, plan.G
-        rots = ops.alloc(B)
-        ops.copy(ops.item(rots, 0), x.h, top)
-        ops.hoisted(ops.item(rots, 1), x.h, top, [b % self.par.n for b in plan.baby[1:]])
         res = ops.alloc(G)
-        ops.pt_dot(res, rots, top, pts, B, G)
+        if self.p is None:
+            rots = ops.alloc(B)
+            ops.copy(ops.item(rots, 0), x.h, top)
+            ops.hoisted(ops.item(rots, 1), x.h, top, [b % self.par.n for b in plan.baby[1:]])
+            ops.pt_dot(res, rots, top, pts, B, G)
+        else:
+            ops.cts(res, x.h, top, pts, B, G)
         acc = None
         for j in range(G):
             g = plan.giant[j] % self.par.n
             y = ops.item(res, j)
+            if self.p is not None:
+                t = ops.alloc()
+                ops.moddown(t, y, top)
+                y = t
             if g:
                 t = ops.alloc()
                 ops.rotate(t, y, top, g)
@@ -706,6 +721,35 @@ class GpuOps:
         self._rows(list(range(top + 1)), list(range(top + 1))).ntt(buf, 1, self.st)
         self.st.sync()
         return buf
+
+    def plaintext_ext(self, coef_rows, top):
+        """coefficient residue rows over Q 0..top then the special primes -> a device plaintext [top + 1 + kp][N] in
+        evaluation form (the extended basis of the fused stage)"""
+        kp = self.R - self.nq
+        rows = top + 1 + kp
+        buf = self.eng.DevBuf.from_array(np.ascontiguousarray(coef_rows[:rows], np.uint32))
+        ids = list(range(top + 1)) + [self.nq + j for j in range(kp)]
+        self._rows(list(range(rows)), ids).ntt(buf, 1, self.st)
+        self.st.sync()
+        return buf
+
+    def cts(self, res, x, top, pts, B, G):
+        """res_j = sum_i rot_i(x) pt_{B j + i} in the extended basis (pcx_cts_stage: one ModUp, the babies' key
+        switches before ModDown, keys regenerated in the kernel)"""
+        key = ("cptr", tuple(id(p) for p in pts))
+        if key not in self.cache:
+            if any(p is None for p in pts) and "zero_ext" not in self.cache:
+                z = self.eng.DevBuf(self.R * self.N)
+                z.zero()
+                self.cache["zero_ext"] = z
+            ptrs = np.array([(self.cache["zero_ext"] if p is None else p).ptr.value for p in pts], np.uint64)
+            self.cache[key] = self.eng.DevBuf.from_array(ptrs.view(np.uint32))
+        babies = self.levels[self.level_i][0]
+        self.ctx.cts_stage(self.keys, babies[0] if babies else 0, B, G, self.cache[key], B * G, self.N, 0xFFFFFFFF, x,
+                           top, res, self.st)
+
+    def moddown(self, out, ext, top):
+        self.ctx.moddown(ext, top, out, self.st)
 
     def pt_dot(self, res, rots, top, pts, B, G):
         key = ("ptr", tuple(id(p) for p in pts))

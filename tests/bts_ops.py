@@ -72,6 +72,25 @@ class OracleOps:
         ids = list(range(top + 1))
         return self.oc.ntt_fwd(np.ascontiguousarray(coef_rows[: top + 1], np.uint32).copy(), ids)
 
+    def plaintext_ext(self, coef_rows, top):
+        kp = self.R - len(self.q)
+        ids = list(range(top + 1)) + [len(self.q) + j for j in range(kp)]
+        return self.oc.ntt_fwd(np.ascontiguousarray(coef_rows[: top + 1 + kp], np.uint32).copy(), ids)
+
+    def cts(self, res, x, top, pts, B, G):
+        kp = self.R - len(self.q)
+        zero = np.zeros((top + 1 + kp, self.N), np.uint32)
+        full = [zero if p is None else p for p in pts]
+        babies = self.levels[self.level_i][0]
+        xx = self.get(x)
+        digits = self.oc.modup(xx[1], top)
+        out = self.oc.cts_fused(xx[None], digits[None], top, B, G, full, [self.gal[r] for r in babies],
+                                seeds=self.seeds[babies] if babies else None, bs=[self.bs[r] for r in babies])[0]
+        res[0][res[1]: res[1] + G] = out
+
+    def moddown(self, out, ext, top):
+        self.get(out)[:] = self.oc.moddown(self.get(ext).copy(), top)
+
     def pt_dot(self, res, rots, top, pts, B, G):
         zero = np.zeros((top + 1, self.N), np.uint32)
         full = [zero if p is None else p for p in pts]

@@ -85,8 +85,9 @@ def test_simulated_bootstrap():
     assert np.abs(out - want).max() / np.abs(want).max() < 1e-5
 
 
-def setup_oracle(logn=12, seed=5):
-    """a chain with the bootstrap's levels plus one spare (three limbs out), oracle keys, the composite"""
+def setup_oracle(logn=12, seed=5, fused=True):
+    """a chain with the bootstrap's levels plus one spare (three limbs out), oracle keys, the composite (fused: the
+    levels' babies in the extended basis)"""
     par = B.Params(logn)
     nq = 1 + 2 * par.levels_used() + 2
     dnum = 3
@@ -97,7 +98,7 @@ def setup_oracle(logn=12, seed=5):
     g = twin.Prng([seed, 2, 7, 1, 8, 2, 8, 1], 0)
     s = g.sparse_ternary(1 << logn, 192)
     s_eval = oc.secret_eval(s)
-    boot = B.Bootstrap(None, par, q)
+    boot = B.Bootstrap(None, par, q, special=p if fused else None)
     gal, levels, conj = B.key_plan(boot)
     keys = [oc.rotation_key(g, s_eval, x) for x in gal]
     seeds = np.stack([k[0] for k in keys])
@@ -114,8 +115,8 @@ def setup_oracle(logn=12, seed=5):
     ops = OracleOps(oc, q, seeds, bs, levels, conj, rseed, rb)
     ops.set_galois(gal)
     boot.ops = boot.ev.ops = ops
-    return dict(par=par, oc=oc, s=s, s_eval=s_eval, boot=boot, ops=ops, q=q, gal=gal, seeds=seeds, bs=bs,
-                levels=levels, conj=conj, rseed=rseed, rb=rb, errs=errs)
+    return dict(par=par, oc=oc, s=s, s_eval=s_eval, boot=boot, ops=ops, q=q, p=p, gal=gal, seeds=seeds, bs=bs,
+                levels=levels, conj=conj, rseed=rseed, rb=rb, errs=errs, fused=fused)
 
 
 def input_ct(S, rng):
@@ -134,8 +135,9 @@ def decrypt_slots(S, ct, top, scale):
     return decode(coef, S["par"].N, scale)
 
 
-def test_bootstrap_on_the_oracle():
-    S = setup_oracle()
+@pytest.mark.parametrize("fused", [True, False])
+def test_bootstrap_on_the_oracle(fused):
+    S = setup_oracle(fused=fused)
     boot, ops = S["boot"], S["ops"]
     rng = np.random.default_rng(9)
     z, ct, me = input_ct(S, rng)

@@ -36,15 +36,16 @@ def gpu_boot(S, lanes=1):
                          relin=True)
         ops2 = B.GpuOps(ctx2, None, relin2, S["levels"], S["conj"], pa.Stream())
         ops2.keep = (ctx2, relin2)
-    boot = B.Bootstrap(ops, par, q, ops2)
+    boot = B.Bootstrap(ops, par, q, ops2, special=S["p"] if S["fused"] else None)
     boot.prepare()
     return ctx, keys, relin, st, ops, boot
 
 
-@pytest.mark.parametrize("lanes", [1, 2])
-def test_bootstrap_gpu_matches_the_oracle(lanes):
-    say(f"[bootstrap] N=2^12, {lanes} EvalMod lane(s): GPU composite vs the oracle composite, decryption, rerun")
-    S = setup_oracle()
+@pytest.mark.parametrize("lanes,fused", [(1, False), (2, True), (1, True)])
+def test_bootstrap_gpu_matches_the_oracle(lanes, fused):
+    say(f"[bootstrap] N=2^12, {lanes} EvalMod lane(s), fused babies {fused}: GPU composite vs the oracle composite, "
+        "decryption, rerun")
+    S = setup_oracle(fused=fused)
     rng = np.random.default_rng(9)
     z, ct, me = input_ct(S, rng)
     ctx, keys, relin, st, ops, boot = gpu_boot(S, lanes)

@@ -142,19 +142,24 @@ __device__ __forceinline__ void x1_inv(uint32_t (&x)[W], uint32_t* l, int t) {
 __device__ __forceinline__ int row_of(int row0) { return row0 + (int)xcd_block(blockIdx.x, gridDim.x); }
 
 // Forward transform of one row per workgroup. EPI as ntt.hip's row pass (0: in place; 1: eout = (x - v) s;
-// 2: eout = d + (x - v) s; 3: eout = x s + v; v = the sum of xnum rows of ex, s = es[prime id]).
-template <bool H, int EPI>
+// 2: eout = d + (x - v) s; 3: eout = x s + v; v = the sum of xnum rows of ex, s = es[prime id]). DENSE: row i at
+// base + i N with prime id i mod xnum (no row tables; a compile-time choice, since a run-time one costs the kernel
+// its register allocation).
+template <bool H, int EPI, bool DENSE = false>
 __global__ void __launch_bounds__(T) fwd1(NttArgs A, int row0) {
     __shared__ uint32_t lds[LDSW];
     const int i = row_of(row0);
-    const int pid = ntt::row_prime(A, i);
+    const int pid = DENSE ? i % A.xnum : A.rprime[i];
     const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.fw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.fws + ((size_t)pid << LOGN);
     const int t = threadIdx.x;
     uint32_t x[W];
     {
-        const ntt::RowSrc src = ntt::row_src(A, i, LOGN);
+        const ntt::RowSrc src = DENSE    ? ntt::RowSrc{(const uint32_t*)A.base + ((size_t)i << LOGN), 1, 0}
+                                : A.soff ? ntt::RowSrc{(const uint32_t*)A.src + ((size_t)A.soff[i] << LOGN), A.snum,
+                                                       A.sstride}
+                                         : ntt::RowSrc{(const uint32_t*)A.base + ((size_t)A.roff[i] << LOGN), 1, 0};
         if (src.n == 1) {
 #pragma unroll
             for (int j = 0; j < W; ++j) x[j] = src.p0[t + T * j];
@@ -190,7 +195,7 @@ __global__ void __launch_bounds__(T) fwd1(NttArgs A, int row0) {
         stage<true, H, 1, 2, false>(x, w, ws, 16384 + 16 * u, p, p2);
         stage<true, H, 0, 2, false>(x, w, ws, 32768 + 32 * u, p, p2);
     }
-    const size_t r0 = (ntt::row_off(A, i) << LOGN) + (size_t)W * t;
+    const size_t r0 = ((DENSE ? (size_t)i : (size_t)A.roff[i]) << LOGN) + (size_t)W * t;
     if (EPI == 0) {
         uint4* o = (uint4*)((uint32_t*)A.base + r0);
 #pragma unroll
@@ -229,14 +234,16 @@ template <bool H>
 __global__ void __launch_bounds__(T) inv1(NttArgs A, int row0) {
     __shared__ uint32_t lds[LDSW];
     const int i = row_of(row0);
-    const int pid = ntt::row_prime(A, i);
+    const int pid = A.rprime[i];
     const uint32_t p = (uint32_t)A.pr[pid].p, p2 = 2 * p;
     const uint32_t* w = (const uint32_t*)A.iw + ((size_t)pid << LOGN);
     const uint32_t* ws = (const uint32_t*)A.iws + ((size_t)pid << LOGN);
     const int t = threadIdx.x;
     uint32_t x[W];
     {
-        const ntt::RowSrc src = ntt::row_src(A, i, LOGN);
+        const ntt::RowSrc src = A.soff ? ntt::RowSrc{(const uint32_t*)A.src + ((size_t)A.soff[i] << LOGN), A.snum,
+                                                      A.sstride}
+                                       : ntt::RowSrc{(const uint32_t*)A.base + ((size_t)A.roff[i] << LOGN), 1, 0};
 #pragma unroll
         for (int q = 0; q < W / E; ++q) {
             uint32_t y[E];
@@ -277,7 +284,7 @@ __global__ void __launch_bounds__(T) inv1(NttArgs A, int row0) {
         s = ((const uint32_t*)A.ninv)[pid];
         ss = ((const uint32_t*)A.ninvs)[pid];
     }
-    uint32_t* o = (uint32_t*)A.base + (ntt::row_off(A, i) << LOGN);
+    uint32_t* o = (uint32_t*)A.base + ((size_t)A.roff[i] << LOGN);
 #pragma unroll
     for (int j = 0; j < W; ++j) o[t + T * j] = shoup(x[phys(4, j)], s, ss, p);
 }
@@ -295,7 +302,9 @@ void ntt1_fwd(const NttArgs& A, int r0, int n, pc_stream_t s) {
         case 2: hipLaunchKernelGGL((ntt1::fwd1<HH, 2>), g, b, 0, st, A, r0); break;               \
         default: hipLaunchKernelGGL((ntt1::fwd1<HH, 3>), g, b, 0, st, A, r0); break;              \
     }
-    if (A.lazy) {
+    if (!A.roff) {  // dense rows (internal launches, epilogue 0, non-lazy)
+        hipLaunchKernelGGL((ntt1::fwd1<false, 0, true>), g, b, 0, st, A, r0);
+    } else if (A.lazy) {
         PCH_F1(true)
     } else {
         PCH_F1(false)

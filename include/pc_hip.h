@@ -652,11 +652,39 @@ PC_STATIC_ASSERT(sizeof(TensorSeededArgs) == (2 * PC_TSEED_QOUT + PC_TSEED_PAIRS
                                                  16 + 24 + (PC_TSEED_Q - 1) * PC_TSEED_PAIRS * 8 + 16,
                  "TensorSeededArgs layout");
 
+/* args.cuh:726-734 (spru_fft_pass, ABI 3): one forward Stockham pass of half-size ns over batch size-N complex
+ * transforms (transform e at in/out + e N double2; in and out distinct), twiddle table tw of N/2 double2 with
+ * tw[m] = exp(-i pi m / (N/2)). Output pair (idx, idx + ns), idx = (j / ns) 2 ns + j % ns, for j < N/2:
+ * v0 +- t with t = v1 w, w = tw[(j % ns) (N/2) / ns], as the reference compiles it:
+ * t.x = fma(v1.x, w.x, -(v1.y w.y)), t.y = fma(v1.y, w.x, v1.x w.y), every other product and sum rounded alone.
+ * Replaces crates/pc-host/src/spru.rs:83-107 spru_fft_pass. ns a power of two in [1, N/2] (the reference checks
+ * only the range), batch >= 1. */
+typedef struct SpruFftArgs {
+    const void* in;
+    void* out;
+    const void* tw;
+    int32_t ns, batch;
+} SpruFftArgs;
+PC_STATIC_ASSERT(sizeof(SpruFftArgs) == 32, "SpruFftArgs layout");
+
+/* args.cuh:735-746 (spru_scatter, ABI 3): coefficients of batch FFT outputs y (transform e at y + e N double2):
+ * m_k = rint(fma(y.x, zt.x, -(y.y zt.y)) 2^-logN scale) (round half to even), zt[k] = exp(-i pi k / N), reduced into
+ * limbs l < nl (prime ids 0..nl-1) at out + e out_stride + l N words, coefficient form. Replaces
+ * crates/pc-host/src/spru.rs:110-140 spru_scatter. |m_k| < 2^63 is the caller's guarantee, as in the reference. */
+typedef struct SpruScatterArgs {
+    const void* y;
+    void* out;
+    const void* zt;
+    const PrimeConst* pr;
+    double scale;
+    int32_t nl, batch;
+    uint64_t out_stride;
+} SpruScatterArgs;
+PC_STATIC_ASSERT(sizeof(SpruScatterArgs) == 56, "SpruScatterArgs layout");
+
 /* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
 struct EncodeArgs;
 struct SpruExtractArgs;
-struct SpruFftArgs;
-struct SpruScatterArgs;
 struct PcmmArgs;
 struct CcmmArgs;
 struct TfheArgs;

@@ -1058,4 +1058,52 @@ void or_rotation_key(const or_ctx* c, or_prng* g, const uint32_t* s_eval, uint64
     or_ksk_gen(c, s_new.data(), s_eval, seed, e.data(), b);
 }
 
+// crates/pc-host/src/encode.rs:87-101 (stockham_pass, spru = true) as crates/pc-host/src/spru.rs:83-107 calls it:
+// w = tw[k (n/2) / ns] with k = j % ns; t = (fma(v1.x, w.x, -(v1.y w.y)), fma(v1.y, w.x, v1.x w.y)); out[idx] = v0 + t,
+// out[idx + ns] = v0 - t, idx = (j / ns) 2 ns + k. Only the two fmas contract.
+__attribute__((optimize("fp-contract=off"))) void or_spru_fft_pass(const double* in, double* out, const double* tw,
+                                                                   uint32_t n, uint32_t ns, uint32_t batch) {
+    const uint32_t half = n / 2;
+    for (uint32_t e = 0; e < batch; ++e) {
+        const double* a = in + 2 * (size_t)e * n;
+        double* o = out + 2 * (size_t)e * n;
+        for (uint32_t j = 0; j < half; ++j) {
+            const uint32_t k = j % ns, idx = (j / ns) * ns * 2 + k;
+            const double* w = tw + 2 * (size_t)(k * (half / ns));
+            const double* v0 = a + 2 * (size_t)j;
+            const double* v1 = a + 2 * (size_t)(j + half);
+            const double p1 = v1[1] * w[1];
+            const double tx = std::fma(v1[0], w[0], -p1);
+            const double p2 = v1[0] * w[1];
+            const double ty = std::fma(v1[1], w[0], p2);
+            o[2 * idx] = v0[0] + tx;
+            o[2 * idx + 1] = v0[1] + ty;
+            o[2 * (idx + ns)] = v0[0] - tx;
+            o[2 * (idx + ns) + 1] = v0[1] - ty;
+        }
+    }
+}
+
+// crates/pc-host/src/spru.rs:110-140: re = fma(y.x, z.x, -(y.y z.y)) (1/n); m = round half to even (re scale); row l
+// holds m mod p_l (|m| mod p, negated for m < 0).
+__attribute__((optimize("fp-contract=off"))) void or_spru_scatter(const double* y, const double* zt,
+                                                                  const uint64_t* primes, uint32_t nl, uint32_t n,
+                                                                  uint32_t batch, double scale, uint64_t out_stride,
+                                                                  uint32_t* out) {
+    for (uint32_t e = 0; e < batch; ++e)
+        for (uint32_t k = 0; k < n; ++k) {
+            const double* v = y + 2 * ((size_t)e * n + k);
+            const double* z = zt + 2 * (size_t)k;
+            const double p1 = v[1] * z[1];
+            const double re = std::fma(v[0], z[0], -p1) * (1.0 / (double)n);
+            const int64_t m = (int64_t)std::nearbyint(re * scale);
+            const uint64_t am = m < 0 ? 0ull - (uint64_t)m : (uint64_t)m;
+            for (uint32_t l = 0; l < nl; ++l) {
+                uint64_t r = am % primes[l];
+                if (m < 0 && r != 0) r = primes[l] - r;
+                out[e * out_stride + (size_t)l * n + k] = (uint32_t)r;
+            }
+        }
+}
+
 }  // extern "C"

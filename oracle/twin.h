@@ -142,6 +142,14 @@ void or_secret_eval(const or_ctx* c, const int8_t* s, uint32_t* s_eval);
 /* sigma_k as an eval-form gather out[o] = in[automorph_slot(k, o)] on nrows rows */
 void or_automorph_rows(const or_ctx* c, const uint32_t* in, uint32_t k, int nrows, uint32_t* out);
 
+/* ---- SPRU floating-point stages (crates/pc-host/src/spru.rs:83-140, encode.rs:85-101) ----
+ * complex values as interleaved double pairs. fft_pass: one forward Stockham pass of half-size ns over batch size-n
+ * transforms, tw of n/2 pairs; scatter: batch size-n FFT outputs y, zeta table zt of n pairs, to nl coefficient rows
+ * per transform at out + e out_stride + l n (residues mod primes[l]). */
+void or_spru_fft_pass(const double* in, double* out, const double* tw, uint32_t n, uint32_t ns, uint32_t batch);
+void or_spru_scatter(const double* y, const double* zt, const uint64_t* primes, uint32_t nl, uint32_t n,
+                     uint32_t batch, double scale, uint64_t out_stride, uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

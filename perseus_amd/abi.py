@@ -93,6 +93,17 @@ class CoeffArgs(C.Structure):
                 ("pad", i32), ("rows", vp * COEFF_MAXT), ("ct", vp * COEFF_MAXT)]
 
 
+class SpruFftArgs(C.Structure):
+    """args.cuh:726-734 (32 bytes): spru_fft_pass."""
+    _fields_ = [("inp", vp), ("out", vp), ("tw", vp), ("ns", i32), ("batch", i32)]
+
+
+class SpruScatterArgs(C.Structure):
+    """args.cuh:735-746 (56 bytes): spru_scatter."""
+    _fields_ = [("y", vp), ("out", vp), ("zt", vp), ("pr", vp), ("scale", C.c_double), ("nl", i32), ("batch", i32),
+                ("out_stride", u64)]
+
+
 TSEED_OUT, TSEED_PAIRS, TSEED_Q, TSEED_QOUT = 16, 128, 4, 64
 
 

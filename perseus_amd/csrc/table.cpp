@@ -38,6 +38,8 @@ namespace pch {
     int ew_many_##L(const EwManyArgs*, pc_stream_t);                 \
     int submul_many_##L(const SubMulManyArgs*, pc_stream_t);         \
     int rescale_coef_##L(const RescaleArgs*, pc_stream_t);           \
+    int spru_fft_pass_##L(const SpruFftArgs*, pc_stream_t);          \
+    int spru_scatter_##L(const SpruScatterArgs*, pc_stream_t);       \
     int rescale_fwd_##L(const RescaleNttArgs*, pc_stream_t);         \
     int mod_raise_##L(const ModRaiseArgs*, pc_stream_t);             \
     int small_int_##L(const SmallIntArgs*, pc_stream_t);             \
@@ -67,7 +69,7 @@ int absent(const A*, pc_stream_t) {
         pt_dot_##L, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
         md_epilogue_##L, wsum_##L, add_const_##L, mul_table_##L, rescale_coef_##L, rescale_combine_##L,            \
         automorph_##L, absent<EncodeArgs>, encrypt_##L, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
-        small_int_##L, absent<SpruExtractArgs>, absent<SpruFftArgs>, absent<SpruScatterArgs>,                 \
+        small_int_##L, absent<SpruExtractArgs>, spru_fft_pass_##L, spru_scatter_##L,                 \
         cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>, wsum_k_##L, rescale_combine_to_##L, \
         md_epilogue_to_##L, small_int1_##L, coeff_sum_##L, mul_add_##L, rescale_fwd_##L,          \
         mul_add_n_##L, tensor_y_##L, wsum_multi_##L, bconv_##L, absent<TfheArgs>, tensor_sum_##L,                    \

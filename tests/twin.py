@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(ROOT, "oracle", "libtwin.so")
 
 u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
@@ -36,6 +37,9 @@ def _load():
         "or_kska_expand": (C.c_uint32, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
         "or_expand_row": (None, [u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, u32p]),
         "or_cts_expand_row": (None, [u32p, C.c_uint32, C.c_uint32, u32p]),
+        "or_spru_fft_pass": (None, [f64p, f64p, f64p, C.c_uint32, C.c_uint32, C.c_uint32]),
+        "or_spru_scatter": (None, [f64p, f64p, u64p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_double, C.c_uint64,
+                                   u32p]),
         "or_kskb_expand_row": (None, [u32p, C.c_uint32, C.c_uint64, C.c_uint32, u64p]),
         "or_prng_new": (C.c_void_p, [u32p, C.c_uint32]),
         "or_prng_free": (None, [C.c_void_p]),
@@ -366,3 +370,22 @@ def rotation_galois(r, n):
 
 def galois_inverse(g, n):
     return LIB.or_galois_inverse(g, n)
+
+
+def spru_fft_pass(x, tw, ns):
+    """one forward Stockham pass (half-size ns) of complex128 transforms x [batch][n], twiddles tw [n/2]"""
+    x = np.ascontiguousarray(x, np.complex128)
+    out = np.zeros_like(x)
+    LIB.or_spru_fft_pass(x.view(np.float64), out.view(np.float64),
+                         np.ascontiguousarray(tw, np.complex128).view(np.float64), x.shape[-1], ns, x.shape[0])
+    return out
+
+
+def spru_scatter(y, zt, primes, scale):
+    """coefficient rows [batch][nl][n] of complex128 FFT outputs y [batch][n] with the zeta table zt [n]"""
+    y = np.ascontiguousarray(y, np.complex128)
+    b, n = y.shape
+    out = np.zeros((b, len(primes), n), np.uint32)
+    LIB.or_spru_scatter(y.view(np.float64), np.ascontiguousarray(zt, np.complex128).view(np.float64),
+                        np.array(primes, np.uint64), len(primes), n, b, scale, len(primes) * n, out)
+    return out

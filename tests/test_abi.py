@@ -230,3 +230,12 @@ def test_tensor_multi_launcher_checks():
     assert abi.call("tensor_multi", a, log_n=12) == -1   # more than 4 outputs
     a.nout, a.npairs = 1, 33
     assert abi.call("tensor_multi", a, log_n=12) == -1   # more than 32 pairs
+
+
+def test_struct_mirrors_match_the_header_sizes():
+    """the ctypes mirrors of the argument structs have the sizes include/pc_hip.h asserts (args.cuh's layouts)"""
+    from perseus_amd import abi
+    sizes = {"PolyRef": 24, "EwArgs": 128, "CoeffArgs": 592, "TensorSeededArgs": 25656, "SpruFftArgs": 32,
+             "SpruScatterArgs": 56}
+    for name, size in sizes.items():
+        assert C.sizeof(getattr(abi, name)) == size, name

@@ -216,12 +216,18 @@ uint64_t prng_u64(or_prng* g) {
     uint64_t lo = prng_u32(g);
     return lo | (uint64_t)prng_u32(g) << 32;
 }
-uint64_t prng_below(or_prng* g, uint64_t q) {
+// keys.rs:166-176 uniform_below: a word v is accepted iff v >= 2^64 mod q (the accepted range is then a multiple of
+// q), and gives v mod q
+int below_accept(uint64_t v, uint64_t q, uint64_t* out) {
     uint64_t rem = (UINT64_MAX % q + 1) % q;  // 2^64 mod q
-    for (;;) {
-        uint64_t v = prng_u64(g);
-        if (v >= rem) return v % q;
-    }
+    if (v < rem) return 0;
+    *out = v % q;
+    return 1;
+}
+uint64_t prng_below(or_prng* g, uint64_t q) {
+    uint64_t r;
+    for (;;)
+        if (below_accept(prng_u64(g), q, &r)) return r;
 }
 double prng_f64(or_prng* g) { return (double)(prng_u64(g) >> 11) * (1.0 / (double)(1ull << 53)); }
 
@@ -244,10 +250,13 @@ struct Gauss {
             cdf[k] = acc;
         }
     }
-    int64_t sample(or_prng* g) const {
-        double u = prng_f64(g);
+    // keys.rs:307-318: |x| is the first k with cdf[k] > u (clamped to the bound); a sign word is drawn only for k > 0
+    size_t index(double u) const {
         size_t k = std::partition_point(cdf.begin(), cdf.end(), [&](double c) { return c <= u; }) - cdf.begin();
-        k = std::min(k, cdf.size() - 1);
+        return std::min(k, cdf.size() - 1);
+    }
+    int64_t sample(or_prng* g) const {
+        size_t k = index(prng_f64(g));
         if (k == 0) return 0;
         return (prng_u32(g) & 1) == 0 ? (int64_t)k : -(int64_t)k;
     }
@@ -519,6 +528,14 @@ void or_sample_gaussian(or_prng* g, double sigma, uint32_t n, int64_t* out) {
     Gauss ga(sigma);
     for (uint32_t i = 0; i < n; ++i) out[i] = ga.sample(g);
 }
+int or_below_accept(uint64_t v, uint64_t q, uint64_t* out) { return below_accept(v, q, out); }
+// the CDF table (bound + 1 entries; returns the entry count, writes at most cap)
+int or_gauss_cdf(double sigma, double* out, int cap) {
+    Gauss ga(sigma);
+    for (int k = 0; k < cap && k < (int)ga.cdf.size(); ++k) out[k] = ga.cdf[k];
+    return (int)ga.cdf.size();
+}
+int or_gauss_index(double sigma, double u) { return (int)Gauss(sigma).index(u); }
 
 // crates/pc-kernels/kernels/arith.cuh:233-239 automorph_slot; crates/pc-core/src/galois.rs:105-112
 uint32_t or_automorph_slot(uint32_t k, uint32_t slot, uint32_t logn) {

@@ -51,6 +51,10 @@ double or_prng_uniform_f64(or_prng* g);
 void or_prng_ksk_seed(or_prng* g, uint32_t out[8]);
 int or_sample_sparse_ternary(or_prng* g, uint32_t n, uint32_t h, int8_t* out);
 void or_sample_gaussian(or_prng* g, double sigma, uint32_t n, int64_t* out);
+// the sampler's parts, callable alone: uniform_below's accept rule on one word, the Gaussian's CDF table and inversion
+int or_below_accept(uint64_t v, uint64_t q, uint64_t* out);
+int or_gauss_cdf(double sigma, double* out, int cap);
+int or_gauss_index(double sigma, double u);
 
 /* ---- galois (crates/pc-core/src/galois.rs) ---- */
 uint32_t or_automorph_slot(uint32_t k, uint32_t slot, uint32_t logn);

@@ -50,6 +50,9 @@ def _load():
         "or_prng_ksk_seed": (None, [C.c_void_p, u32p]),
         "or_sample_sparse_ternary": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, i8p]),
         "or_sample_gaussian": (None, [C.c_void_p, C.c_double, C.c_uint32, i64p]),
+        "or_below_accept": (C.c_int, [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64)]),
+        "or_gauss_cdf": (C.c_int, [C.c_double, f64p, C.c_int]),
+        "or_gauss_index": (C.c_int, [C.c_double, C.c_double]),
         "or_automorph_slot": (C.c_uint32, [C.c_uint32, C.c_uint32, C.c_uint32]),
         "or_rotation_galois": (C.c_uint64, [C.c_int64, C.c_uint32]),
         "or_galois_inverse": (C.c_uint64, [C.c_uint64, C.c_uint32]),
@@ -143,6 +146,23 @@ class Prng:
         out = np.zeros(n, np.int64)
         LIB.or_sample_gaussian(self.h, sigma, n, out)
         return out
+
+
+def below_accept(v, q):
+    """uniform_below's rule on one 64-bit word: v mod q if v is accepted, else None."""
+    r = C.c_uint64(0)
+    return int(r.value) if LIB.or_below_accept(v, q, C.byref(r)) else None
+
+
+def gauss_cdf(sigma=3.19):
+    n = LIB.or_gauss_cdf(sigma, np.zeros(1, np.float64), 0)
+    out = np.zeros(n, np.float64)
+    LIB.or_gauss_cdf(sigma, out, n)
+    return out
+
+
+def gauss_index(u, sigma=3.19):
+    return LIB.or_gauss_index(sigma, u)
 
 
 class Ctx:

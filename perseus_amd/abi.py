@@ -290,6 +290,24 @@ class SmallInt1Args(C.Structure):
                 ("nrows", i32), ("K", i32), ("nparts", i32)]
 
 
+class KskExpandArgs(C.Structure):
+    """args.cuh:306-323: KSKA rows out[d - d0][m][N] (48 bytes)."""
+    _fields_ = [("out", vp), ("seed", vp), ("prime_ids", vp), ("pr", vp), ("nmod", i32), ("dnum", i32), ("d0", i32),
+                ("pad", i32)]
+
+
+class KskUnpackArgs(C.Structure):
+    """args.cuh:656-663: packed key rows to dense rows (32 bytes)."""
+    _fields_ = [("out", vp), ("in_", vp), ("row_words", u64), ("nrows", i32), ("bits", i32)]
+
+
+class BconvArgs(C.Structure):
+    """args.cuh:130-141: a batch of fast base-conversion jobs (56 bytes); jobs are 8 u32 words each (BconvJob: src_off,
+    dst_off, nsrc, ntgt, pool_off, exact, prescaled, split)."""
+    _fields_ = [("src", vp), ("dst", vp), ("jobs", vp), ("pool", vp), ("pr", vp), ("njobs", i32), ("max_tgt", i32),
+                ("kind", i32), ("pad", i32)]
+
+
 KS_ACC, KS_SUM = 4, 8  # KsArgs.c0_mode flags (args.cuh:207-210)
 
 assert C.sizeof(KeyTab) == 40 and C.sizeof(CtsArgs) == 200 and C.sizeof(CtsRegenArgs) == 240
@@ -306,6 +324,7 @@ assert C.sizeof(RescaleCombineToArgs) == 104 and C.sizeof(EwManyArgs) == 4 * EWM
 assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
 assert C.sizeof(ModRaiseArgs) == 2136 and C.sizeof(SmallIntTab) == 4552 and C.sizeof(SmallIntArgs) == 72
 assert C.sizeof(SmallInt1Args) == 56 and C.sizeof(EncryptArgs) == 64
+assert C.sizeof(KskExpandArgs) == 48 and C.sizeof(KskUnpackArgs) == 32 and C.sizeof(BconvArgs) == 56
 assert C.sizeof(RowSet) == 16 and C.sizeof(PtDotArgs) == 128
 assert C.sizeof(PackSplitArgs) == 64 and C.sizeof(PackDotArgs) == 120
 assert C.sizeof(TensorMultiArgs) == (2 * TMULTI_OUT + 2 * TMULTI_OUT * TMULTI_PAIRS) * 24 + 8 + 24

@@ -236,6 +236,7 @@ def test_struct_mirrors_match_the_header_sizes():
     """the ctypes mirrors of the argument structs have the sizes include/pc_hip.h asserts (args.cuh's layouts)"""
     from perseus_amd import abi
     sizes = {"PolyRef": 24, "EwArgs": 128, "CoeffArgs": 592, "TensorSeededArgs": 25656, "SpruFftArgs": 32,
-             "SpruScatterArgs": 56}
+             "SpruScatterArgs": 56, "KskExpandArgs": 48, "KskUnpackArgs": 32, "BconvArgs": 56, "KsArgs": 176,
+             "KsKeyArgs": 216, "KsRegenArgs": 312, "KeyTab": 40}
     for name, size in sizes.items():
         assert C.sizeof(getattr(abi, name)) == size, name

@@ -769,6 +769,8 @@ int pc_hip_free_host(void* p);
 int pc_hip_memcpy_htod(void* dst, const void* src, size_t bytes, pc_stream_t s);
 int pc_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes, pc_stream_t s);
 int pc_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, pc_stream_t s);
+/* cudaMemsetAsync (crates/pc-cuda/src/mem.rs:305-331): the low byte of value into bytes bytes from dst, any alignment,
+ * enqueued on s as a fill kernel (so a captured replay holds no memset node) */
 int pc_hip_memset(void* dst, int value, size_t bytes, pc_stream_t s);
 int pc_hip_stream_create(pc_stream_t* s);
 int pc_hip_stream_destroy(pc_stream_t s);

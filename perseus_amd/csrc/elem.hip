@@ -126,3 +126,40 @@ extern "C" int pcx_copy_probe(void* dst, const void* src, size_t bytes, pc_strea
                        (hipStream_t)s, (uint4*)dst, (const uint4*)src);
     return pch::launch_rc();
 }
+
+// ------------------------------------------------------------------------------------------------ byte fill
+// cudaMemsetAsync's replacement (crates/pc-cuda/src/mem.rs:305-331, DBuf::zero / zero_range) as an ordinary kernel, so
+// that a replay captured into a HIP graph holds a kernel node and no memset node. The body between the first and
+// last 16-byte boundaries is written with 16-byte stores (grid-stride); the head and tail bytes (< 16 each) by one
+// thread.
+namespace pch {
+namespace elem {
+__global__ void __launch_bounds__(BX) fill_k(uint8_t* dst, uint32_t pat, size_t head, size_t body16, size_t tail) {
+    const size_t tid = (size_t)blockIdx.x * BX + threadIdx.x, stride = (size_t)gridDim.x * BX;
+    uint4* b = (uint4*)(dst + head);
+    const uint4 v = make_uint4(pat, pat, pat, pat);
+    for (size_t i = tid; i < body16; i += stride) b[i] = v;
+    if (tid == 0) {
+        const uint8_t c = (uint8_t)pat;
+        for (size_t i = 0; i < head; ++i) dst[i] = c;
+        uint8_t* t = dst + head + body16 * 16;
+        for (size_t i = 0; i < tail; ++i) t[i] = c;
+    }
+}
+}  // namespace elem
+
+int fill_bytes(void* dst, int value, size_t bytes, pc_stream_t s) {
+    if (bytes == 0) return 0;
+    if (!dst) return -1;
+    uint8_t* d = (uint8_t*)dst;
+    size_t head = (16 - ((uintptr_t)d & 15)) & 15;
+    if (head > bytes) head = bytes;
+    const size_t body16 = (bytes - head) / 16, tail = bytes - head - body16 * 16;
+    const uint32_t c = (uint32_t)(value & 0xFF);
+    const size_t want = (body16 + elem::BX - 1) / elem::BX;
+    const unsigned grid = (unsigned)(want < 1 ? 1 : want > 4096 ? 4096 : want);
+    hipLaunchKernelGGL(elem::fill_k, dim3(grid), dim3(elem::BX), 0, (hipStream_t)s, d, c * 0x01010101u, head, body16,
+                       tail);
+    return launch_rc();
+}
+}  // namespace pch

@@ -6,6 +6,10 @@
 #include "pc_hip.h"
 
 static inline int rc(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
+
+namespace pch {
+int fill_bytes(void* dst, int value, size_t bytes, pc_stream_t s);  // elem.hip: a fill kernel
+}
 static inline hipStream_t S(pc_stream_t s) { return (hipStream_t)s; }
 
 extern "C" {
@@ -32,9 +36,8 @@ int pc_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes, pc_stream_t s) 
 int pc_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, pc_stream_t s) {
     return rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(s)));
 }
-int pc_hip_memset(void* dst, int value, size_t bytes, pc_stream_t s) {
-    return rc(hipMemsetAsync(dst, value, bytes, S(s)));
-}
+// a fill kernel, not hipMemsetAsync: a replay captured into a graph then holds no memset node
+int pc_hip_memset(void* dst, int value, size_t bytes, pc_stream_t s) { return pch::fill_bytes(dst, value, bytes, s); }
 // non-blocking streams at the default priority (crates/pc-cuda/src/stream.rs:20-28)
 int pc_hip_stream_create(pc_stream_t* s) {
     hipStream_t h;

@@ -85,15 +85,18 @@ def test_simulated_bootstrap():
     assert np.abs(out - want).max() / np.abs(want).max() < 1e-5
 
 
-def setup_oracle(logn=12, seed=5, fused=True):
-    """a chain with the bootstrap's levels plus one spare (three limbs out), oracle keys, the composite (fused: the
-    levels' babies in the extended basis)"""
+def setup_oracle(logn=12, seed=5, fused=True, chain=None):
+    """a chain with the bootstrap's levels plus one spare (three limbs out), or the given chain (q, p, dnum), oracle
+    keys, the composite (fused: the levels' babies in the extended basis)"""
     par = B.Params(logn)
-    nq = 1 + 2 * par.levels_used() + 2
-    dnum = 3
-    kp = -(-nq // dnum)
-    ps = [int(p) for p in twin.descending_primes(30, 2 << logn, nq + kp)]
-    q, p = ps[:nq], ps[nq:]
+    if chain is None:
+        nq = 1 + 2 * par.levels_used() + 2
+        dnum = 3
+        kp = -(-nq // dnum)
+        ps = [int(p) for p in twin.descending_primes(30, 2 << logn, nq + kp)]
+        q, p = ps[:nq], ps[nq:]
+    else:
+        q, p, dnum = [int(x) for x in chain[0]], [int(x) for x in chain[1]], chain[2]
     oc = twin.Ctx(logn, q, p, dnum)
     g = twin.Prng([seed, 2, 7, 1, 8, 2, 8, 1], 0)
     s = g.sparse_ternary(1 << logn, 192)

@@ -854,6 +854,15 @@ int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* c
  * ciphertext. The group must hold the key of every step the ladder takes (-1 otherwise). */
 int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
                        void* out, void* tmp, pc_stream_t s);
+/* No counterpart in the reference: pcx_rotate_and_sum for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). The scratch ciphertext is a file-scope device
+ * array of PCX_NOALLOC_SCRATCH_WORDS u32 words (32 MiB per device, held until the process ends) instead of tmp; the
+ * call allocates nothing. -2 when the context's ciphertext (pcx_ct_words) exceeds the array or radix_bits > 8; other
+ * arguments and errors as pcx_rotate_and_sum. Calls that overlap on one device (another stream, another thread) race
+ * on the shared array. */
+#define PCX_NOALLOC_SCRATCH_WORDS (2u * 64u * 65536u)
+int pcx_rotate_and_sum_noalloc(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop,
+                               int radix_bits, void* out, pc_stream_t s);
 /* One CtS / StC stage's hoisted baby steps and plaintext products (crates/pc-gpu/src/bts/cts.rs:840-960, LtStage::run
  * steps 1 and 2): ModUp of ct's c1 once, then through the table's cts_fused_regen
  *   res_j = sum_{i < B} rot_i(ct) pt_{B j + i},  j < G,

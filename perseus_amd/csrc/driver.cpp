@@ -1317,22 +1317,30 @@ int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t 
     };
     const int64_t sign = start > 0 ? 1 : -1, gap = start > 0 ? start : -start;
     if (gap >= stop) return copy_q(c, x, top, out, s);
-    std::vector<int64_t> gaps;
-    for (int64_t g = gap; g < stop; g *= 2) gaps.push_back(g);
+    // the rungs' gaps (doubling from |start| below stop: at most 63) and, for rungs of up to 8 bits, their key lists in
+    // fixed arrays: the ladder itself allocates nothing on the host or the device
+    int64_t gaps[64];
+    size_t ng = 0;
+    for (int64_t g = gap; g < stop && ng < 64; g *= 2) gaps[ng++] = g;
     const size_t rb = radix_bits >= 2 ? (size_t)radix_bits : 1;
     bool have = false;
-    for (size_t i0 = 0; i0 < gaps.size();) {
-        const size_t n = std::min(rb, gaps.size() - i0);
+    for (size_t i0 = 0; i0 < ng;) {
+        const size_t n = std::min(rb, ng - i0);
         if (rb >= 2 && n > 1) {
             // one rung of radix 2^n: out += sum over j < 2^n of rot(out, j gap) when the group holds every step
-            std::vector<int> idx;
-            for (int64_t j = 1; j < ((int64_t)1 << n); ++j) idx.push_back(key_of(sign * j * gaps[i0]));
-            if (std::find(idx.begin(), idx.end(), -1) == idx.end()) {
+            int small[255];
+            std::vector<int> big;
+            const int64_t cnt = ((int64_t)1 << n) - 1;
+            if (n > 8) big.resize((size_t)cnt);
+            int* idx = n > 8 ? big.data() : small;
+            bool all = true;
+            for (int64_t j = 1; j <= cnt; ++j) all = (idx[j - 1] = key_of(sign * j * gaps[i0])) >= 0 && all;
+            if (all) {
                 if (!have) {
                     if (int e = copy_q(c, x, top, out, s)) return e;
                     have = true;
                 }
-                if (int e = pcx_rotate_sum(c, k, idx.data(), (int)idx.size(), out, top, out, out, s)) return e;
+                if (int e = pcx_rotate_sum(c, k, idx, (int)cnt, out, top, out, out, s)) return e;
                 i0 += n;
                 continue;
             }

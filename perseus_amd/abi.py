@@ -290,6 +290,12 @@ class SmallInt1Args(C.Structure):
                 ("nrows", i32), ("K", i32), ("nparts", i32)]
 
 
+class EncodeArgs(C.Structure):
+    """args.cuh:595-611: device slot encoding (80 bytes)."""
+    _fields_ = [("v", vp), ("a", vp), ("b", vp), ("c", vp), ("cmax", vp), ("out", vp), ("deg_factor", vp), ("pr", vp),
+                ("scale", C.c_double), ("nl", i32), ("pad", i32)]
+
+
 class KskExpandArgs(C.Structure):
     """args.cuh:306-323: KSKA rows out[d - d0][m][N] (48 bytes)."""
     _fields_ = [("out", vp), ("seed", vp), ("prime_ids", vp), ("pr", vp), ("nmod", i32), ("dnum", i32), ("d0", i32),
@@ -324,7 +330,7 @@ assert C.sizeof(RescaleCombineToArgs) == 104 and C.sizeof(EwManyArgs) == 4 * EWM
 assert C.sizeof(SubMulManyArgs) == 3 * EWM_MAX * 8 + 24
 assert C.sizeof(ModRaiseArgs) == 2136 and C.sizeof(SmallIntTab) == 4552 and C.sizeof(SmallIntArgs) == 72
 assert C.sizeof(SmallInt1Args) == 56 and C.sizeof(EncryptArgs) == 64
-assert C.sizeof(KskExpandArgs) == 48 and C.sizeof(KskUnpackArgs) == 32 and C.sizeof(BconvArgs) == 56
+assert C.sizeof(EncodeArgs) == 80 and C.sizeof(KskExpandArgs) == 48 and C.sizeof(KskUnpackArgs) == 32 and C.sizeof(BconvArgs) == 56
 assert C.sizeof(RowSet) == 16 and C.sizeof(PtDotArgs) == 128
 assert C.sizeof(PackSplitArgs) == 64 and C.sizeof(PackDotArgs) == 120
 assert C.sizeof(TensorMultiArgs) == (2 * TMULTI_OUT + 2 * TMULTI_OUT * TMULTI_PAIRS) * 24 + 8 + 24

@@ -7,6 +7,7 @@ namespace pch {
 #define PCH_DECL(L)                                                  \
     int ntt_fwd_##L(const NttArgs*, pc_stream_t);                    \
     int ntt_inv_##L(const NttArgs*, pc_stream_t);                    \
+    int encode_##L(const EncodeArgs*, pc_stream_t);                  \
     int bconv_##L(const BconvArgs*, pc_stream_t);                    \
     int ew_add_##L(const EwArgs*, pc_stream_t);                      \
     int ew_scale_##L(const EwArgs*, pc_stream_t);                    \
@@ -68,7 +69,7 @@ int absent(const A*, pc_stream_t) {
         ntt_fwd_##L, ntt_inv_##L, bconv_##L, ew_add_##L, ew_scale_##L, ew_sub_mul_##L, ew_copy_##L,                  \
         pt_dot_##L, ks_dot_##L, ks_dot_regen_##L, ksk_expand_##L, cts_fused_##L, tensor_##L,                  \
         md_epilogue_##L, wsum_##L, add_const_##L, mul_table_##L, rescale_coef_##L, rescale_combine_##L,            \
-        automorph_##L, absent<EncodeArgs>, encrypt_##L, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
+        automorph_##L, encode_##L, encrypt_##L, ksk_gen_##L, ksk_unpack_##L, mod_raise_##L,   \
         small_int_##L, absent<SpruExtractArgs>, spru_fft_pass_##L, spru_scatter_##L,                 \
         cts_fused_regen_##L, ks_dot_key_##L, absent<PcmmArgs>, absent<CcmmArgs>, wsum_k_##L, rescale_combine_to_##L, \
         md_epilogue_to_##L, small_int1_##L, coeff_sum_##L, mul_add_##L, rescale_fwd_##L,          \

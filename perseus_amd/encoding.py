@@ -4,8 +4,8 @@ zeta^(-5^j), so that rotating the slots left by r is the automorphism X -> X^(5^
 OpenFHE's slot order; crates/pc-core/src/galois.rs:35-60).
 
 encode: coefficients m_i = round(scale Re(sum_k v_k zeta^(-i (2k+1))) / N), with v the slot values placed at the
-odd powers they sit on; decode: the inverse. Both through one N-point FFT. The device table has no counterpart: its
-`encode` entry is not built (its words follow CUDA's sincospi), so plaintexts are encoded here and uploaded.
+odd powers they sit on; decode: the inverse. Both through one N-point FFT. The kernel table's `encode` entry encodes
+on the device by the same mathematics (csrc/encode.hip).
 """
 import numpy as np
 

@@ -64,3 +64,75 @@ def test_bundle_keys_rotate_like_the_oracle():
         got = out.download((2, ch.rows, n))
         want = oc.rotate(ct, top, seed, b, gals[r])
         assert (got[:, : top + 1] == want[:, : top + 1]).all(), r
+
+
+# ----------------------------------------------------------------------------------------------- import / export
+META = {"level": 0, "deg": 1, "nf": 2.0 ** 30, "slots": 2048, "tag": None}
+
+
+def _bytes(h, data):
+    f = io.BytesIO()
+    wire.write_ct(f, h, data)
+    return f.getvalue()
+
+
+def test_import_coefficient_form_frames():
+    say("[wire] small chain: import_ct of a short-c0 DRBG-seeded frame and a subring frame (forward NTT on the device)")
+    ch = pa.preset("small")
+    ctx, oc = pa.Context(ch, k_rot=1), twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum)
+    st = pa.Stream()
+    n, rows = ch.n, 3
+    q = ch.q[:rows]
+    rng = np.random.default_rng(21)
+    # short c0: coefficient rows rounded to their top bits, seeds for c1 (DRBG)
+    coef = np.stack([rng.integers(0, p, n) for p in q]).astype(np.uint32)
+    seeds = rng.integers(0, 1 << 32, (rows, 8), dtype=np.uint64).astype(np.uint32)
+    w, bits = wire.pack_dropped(q, coef, 12)
+    h = wire.ct_header("t", n, 1, rows, META, seeded=True, drop=12, bits=bits, sparse=True)
+    raw = _bytes(h, np.concatenate([w, seeds.reshape(-1)]))
+    with pytest.raises(wire.WireError, match="client"):
+        wire.import_ct(ctx, raw, st)  # as the reference's import_ct: a short-c0 frame is expanded first
+    buf, hh = wire.import_ct(ctx, wire.expand_frame(raw, ch.q), st)
+    assert hh.get("sparse") and hh.get("coeff0")
+    got = buf.download((2, ch.rows, n))
+    want0 = oc.ntt_fwd(wire.unpack_dropped(q, w, 12, n), list(range(rows)))
+    assert (got[0, :rows] == want0).all()
+    for r in range(rows):
+        assert (got[1, r] == wire.drbg_row(seeds[r], q[r], n)).all()
+    # a subring client's frame: both parts in coefficient form over N/2 coefficients, lifted X -> X^2, then NTT'd
+    hs = wire.ct_header("t", n // 2, 1, rows, dict(META, slots=n // 4), coeff0=True, coeff1=True)
+    small = np.stack([np.stack([rng.integers(0, p, n // 2) for p in q]) for _ in range(2)]).astype(np.uint32)
+    buf, hh = wire.import_ct(ctx, _bytes(hs, small), st)
+    got = buf.download((2, ch.rows, n))
+    big = np.zeros((2, rows, n), np.uint32)
+    big[:, :, ::2] = small
+    for part in range(2):
+        assert (got[part, :rows] == oc.ntt_fwd(big[part], list(range(rows)))).all(), part
+    assert hh["n"] == n
+    # a compressed frame is a client's to decrypt
+    hc = wire.ct_header("t", n, 1, 2, META, bits=20)
+    with pytest.raises(wire.WireError, match="client"):
+        wire.import_ct(ctx, _bytes(hc, np.zeros(wire.ct_words(hc), np.uint32)), st)
+
+
+def test_export_full_and_compressed():
+    say("[wire] small chain: export_ct full and compressed (inverse NTT on the device, rounded CRT at 24 bits)")
+    ch = pa.preset("small")
+    ctx, oc = pa.Context(ch, k_rot=1), twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum)
+    st = pa.Stream()
+    n, top = ch.n, 1
+    rng = np.random.default_rng(22)
+    ct = np.zeros((2, ch.rows, n), np.uint32)
+    for part in range(2):
+        for t in range(top + 1):
+            ct[part, t] = rng.integers(0, ch.q[t], n)
+    buf = pa.DevBuf.from_array(ct)
+    h, d = wire.read_ct(io.BytesIO(wire.export_ct(ctx, buf, top, META, "t", st)))
+    assert (d.reshape(2, top + 1, n) == ct[:, : top + 1]).all()
+    h, d = wire.read_ct(io.BytesIO(wire.export_ct(ctx, buf, top, META, "t", st, bits=24)))
+    assert h["bits"] == 24 and (buf.download((2, ch.rows, n)) == ct).all(), "the source is unchanged"
+    q = ch.q[: top + 1]
+    pw = wire.packed_words(n, 24)
+    for part in range(2):
+        coef = oc.ntt_inv(ct[part, : top + 1].copy(), list(range(top + 1)))
+        assert (d[part * pw:(part + 1) * pw] == wire.pack_frame_part(q, coef, 24)).all(), part

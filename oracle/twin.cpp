@@ -11,6 +11,11 @@
 #include <cstring>
 #include <stdexcept>
 #include <thread>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <pthread.h>
+#include <sched.h>
 #include <vector>
 
 typedef unsigned __int128 u128;
@@ -20,7 +25,9 @@ namespace {
 // ------------------------------------------------------------------------------------------------ thread pool
 // The reference host runtime runs launchers on a pool of min(cores, 36) threads (crates/pc-hostrt/src/lib.rs:176-226);
 // here a parallel_for over an index range with a fixed thread count (or_set_threads).
+// Threads may be pinned one per logical CPU of a list (or_set_cpus: the reference pins one thread per physical core).
 int g_threads = 1;
+std::vector<int> g_cpus;
 
 template <class F>
 void parallel_for(long n, F f) {
@@ -32,12 +39,29 @@ void parallel_for(long n, F f) {
     std::atomic<long> next{0};
     std::vector<std::thread> th;
     th.reserve(nt);
-    for (int t = 0; t < nt; ++t)
+    for (int t = 0; t < nt; ++t) {
         th.emplace_back([&] {
             for (long i; (i = next.fetch_add(1)) < n;) f(i);
         });
+        if (!g_cpus.empty()) {
+            cpu_set_t set;
+            CPU_ZERO(&set);
+            CPU_SET(g_cpus[t % g_cpus.size()], &set);
+            (void)pthread_setaffinity_np(th.back().native_handle(), sizeof(set), &set);
+        }
+    }
     for (auto& x : th) x.join();
 }
+
+// The expanded-key cache of the reference's host twin (crates/pc-host/src/expand.rs:56-116, PERSEUS_CPU_KEYCACHE_GB):
+// KSKA rows kept across calls, keyed by (seed, digit, prime, n), up to a byte budget (0: off).
+struct KskaKey {
+    uint32_t w[11];
+    bool operator<(const KskaKey& o) const { return std::lexicographical_compare(w, w + 11, o.w, o.w + 11); }
+};
+std::mutex g_kc_mu;
+std::map<KskaKey, std::shared_ptr<std::vector<uint32_t>>> g_kc;
+size_t g_kc_cap = 0, g_kc_bytes = 0;
 
 // ------------------------------------------------------------------------------------------------ modular helpers
 inline uint64_t mulmod(uint64_t a, uint64_t b, uint64_t m) { return (uint64_t)((u128)a * b % m); }
@@ -189,6 +213,29 @@ void kska_range(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, ui
 }
 void kska_row(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t* out) {
     kska_range(seed, digit, p, n, 0, n, out);
+}
+// kska_row through the expanded-key cache when it is on
+void kska_row_cached(const uint32_t* seed, uint32_t digit, uint32_t p, uint32_t n, uint32_t* out) {
+    if (!g_kc_cap) return kska_row(seed, digit, p, n, out);
+    KskaKey k;
+    for (int i = 0; i < 8; ++i) k.w[i] = seed[i];
+    k.w[8] = digit, k.w[9] = p, k.w[10] = n;
+    std::shared_ptr<std::vector<uint32_t>> hit;
+    {
+        std::lock_guard<std::mutex> lk(g_kc_mu);
+        auto it = g_kc.find(k);
+        if (it != g_kc.end()) hit = it->second;
+    }
+    if (hit) {
+        std::copy(hit->begin(), hit->end(), out);
+        return;
+    }
+    kska_row(seed, digit, p, n, out);
+    std::lock_guard<std::mutex> lk(g_kc_mu);
+    if (g_kc_bytes + 4 * (size_t)n <= g_kc_cap && !g_kc.count(k)) {
+        g_kc[k] = std::make_shared<std::vector<uint32_t>>(out, out + n);
+        g_kc_bytes += 4 * (size_t)n;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ DRBG
@@ -557,6 +604,13 @@ uint64_t or_galois_inverse(uint64_t g, uint32_t n) {
 }
 
 void or_set_threads(int n) { g_threads = std::max(1, n); }
+void or_set_cpus(const int* cpus, int n) { g_cpus.assign(cpus, cpus + std::max(0, n)); }
+void or_set_kska_cache(size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_kc_mu);
+    g_kc.clear();
+    g_kc_bytes = 0;
+    g_kc_cap = bytes;
+}
 int or_get_threads(void) { return g_threads; }
 
 or_ctx* or_ctx_new(uint32_t logn, const uint64_t* primes, int nq, int kp, int dnum) {
@@ -710,7 +764,7 @@ void or_ks_dot(const or_ctx* c, const uint32_t* ct, const uint32_t* digits, int 
         for (int d = 0; d < nd; ++d) {
             const uint32_t* D = d == dt ? c1 + (size_t)t * n : digits + ((size_t)d * R + t) * n;
             const uint32_t* bd = b + ((size_t)d * R + t) * n;
-            kska_row(seed, (uint32_t)d, p, n, a.data());
+            kska_row_cached(seed, (uint32_t)d, p, n, a.data());
             for (uint32_t i = 0; i < n; ++i) {
                 s0[i] += (uint64_t)D[i] * bd[i];  // at most dnum <= 4 products < 2^62: no wrap
                 s1[i] += (uint64_t)D[i] * a[i];

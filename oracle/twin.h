@@ -9,6 +9,7 @@
  * key's b is [digit][slot = prime id][N] (full layout), a ModUp output is [digit][row][N].
  */
 #pragma once
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -66,6 +67,10 @@ typedef struct or_ctx or_ctx;
 or_ctx* or_ctx_new(uint32_t logn, const uint64_t* primes, int nq, int kp, int dnum);
 void or_ctx_free(or_ctx* c);
 void or_set_threads(int n);
+// pin the pool's threads one per logical CPU of the list (empty: unpinned); the expanded-key (KSKA row) cache's byte
+// budget (0: off, cleared)
+void or_set_cpus(const int* cpus, int n);
+void or_set_kska_cache(size_t bytes);
 int or_get_threads(void);
 /* twiddle tables of prime id (crates/pc-gpu/src/context.rs:190-230): fw[i] = psi^brev(i), iw = psi^-brev(i) and the
  * Shoup companions floor(w 2^32 / p) */

@@ -59,6 +59,8 @@ def _load():
         "or_ctx_new": (C.c_void_p, [C.c_uint32, u64p, C.c_int, C.c_int, C.c_int]),
         "or_ctx_free": (None, [C.c_void_p]),
         "or_set_threads": (None, [C.c_int]),
+        "or_set_cpus": (None, [i32p, C.c_int]),
+        "or_set_kska_cache": (None, [C.c_size_t]),
         "or_get_threads": (C.c_int, []),
         "or_ctx_twiddles": (None, [C.c_void_p, C.c_int, u32p, u32p, u32p, u32p]),
         "or_ctx_root": (C.c_uint64, [C.c_void_p, C.c_int]),
@@ -100,6 +102,17 @@ def ptr_array(arrs):
 
 def set_threads(n):
     LIB.or_set_threads(int(n))
+
+
+def set_cpus(cpus):
+    """pin the pool's threads one per logical CPU of the list (empty: unpinned)"""
+    a = np.asarray(list(cpus) or [0], np.int32)
+    LIB.or_set_cpus(a, len(cpus))
+
+
+def set_kska_cache(nbytes):
+    """the expanded-key cache's byte budget (0: off, cleared)"""
+    LIB.or_set_kska_cache(int(nbytes))
 
 
 def descending_primes(bits, m, n):

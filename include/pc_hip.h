@@ -822,6 +822,10 @@ const PrimeConst* pcx_ctx_primes(const pcx_ctx* c); /* device table by prime id 
 const void* pcx_ctx_twiddle(const pcx_ctx* c, int which);
 uint64_t pcx_ctx_root(const pcx_ctx* c, int prime_id);
 size_t pcx_ctx_workspace_bytes(const pcx_ctx* c);
+/* Every launch of the context's operations through the kernel table alone, as crates/pc-gpu issues them (on != 0):
+ * the ModDown conversion as the table's bconv then ntt_fwd with its epilogue, the key dots as ks_dot_key (a key
+ * group's retry-value table unused); off: the driver's fused forms. Returns the previous setting, -1 on NULL. */
+int pcx_ctx_table_only(pcx_ctx* c, int on);
 
 /* Batched NTT of nrows rows of one buffer: row i at base + roff[i]*N (prime id ids[i]); host row tables are uploaded
  * into a device row list made once (crates/pc-gpu/src/ntt.rs:293-326 transform_rows over a RowList). dir: 1 forward,

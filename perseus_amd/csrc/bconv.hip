@@ -77,10 +77,12 @@ __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, 
         const Red red(A.pr[P.tgt_prime(t)]);
         uint64_t acc = 0;
         uint32_t wraps = 0;
-        for (int i = 0; i < P.ns; ++i) {
-            const uint64_t pr = (uint64_t)yv(i) * P.m(i, t);
-            acc += pr;
-            wraps += acc < pr;
+        // groups of four products (below 2^64 for words below 2^31), one carry per group
+        for (int i = 0; i < P.ns; i += 4) {
+            uint64_t cs = 0;
+            for (int e = i; e < i + 4 && e < P.ns; ++e) cs += (uint64_t)yv(e) * P.m(e, t);
+            acc += cs;
+            wraps += acc < cs;
         }
         uint32_t r = red.red96(acc, wraps);
         if (j.exact) r = subm(r, red((uint64_t)u * bmod[t]), red.p);
@@ -97,6 +99,8 @@ struct JobLds {
     uint32_t tc[MAXT][4];  // p, 2^32 mod p, its Shoup companion, floor(2^32 / p)
     double rb[MAX_REG_SRC];
     uint32_t bmod[MAXT];
+    uint32_t lazy[MAXT];   // 1: ns (max source prime - 1) (p_t - 1) < 2^64, the sum needs no carry count
+    uint32_t maxs;         // the job's largest source prime
 };
 
 __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
@@ -140,27 +144,50 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
     for (int t = 0; t < ntl; ++t) {
         const Red red(S.tc[t][0], S.tc[t][1], S.tc[t][2], S.tc[t][3]);
         uint64_t acc[V] = {0, 0};
-        uint32_t wraps[V] = {0, 0};
+        uint32_t r[V];
+        if (S.lazy[t]) {
+            // every partial sum stays below 2^64: one multiply-add per product
 #pragma unroll
-        for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
-            if (g < ng) {
-                const uint4 m4 = *(const uint4*)&S.mt[t][4 * g];
-                const uint32_t mv[4] = {m4.x, m4.y, m4.z, m4.w};
+            for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
+                if (g < ng) {
+                    const uint4 m4 = *(const uint4*)&S.mt[t][4 * g];
+                    const uint32_t mv[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
+                    for (int e = 0; e < 4; ++e) {
 #pragma unroll
-                    for (int k = 0; k < V; ++k) {
-                        const uint64_t pr = (uint64_t)y[(4 * g + e) * V + k] * mv[e];
-                        acc[k] += pr;
-                        wraps[k] += acc[k] < pr;
+                        for (int k = 0; k < V; ++k) acc[k] += (uint64_t)y[(4 * g + e) * V + k] * mv[e];
                     }
                 }
             }
+#pragma unroll
+            for (int k = 0; k < V; ++k) r[k] = red(acc[k]);
+        } else {
+            // four products of words below 2^31 stay below 2^64: each group of four is summed by multiply-adds, and
+            // only the group sums carry into the 96-bit total
+            uint32_t wraps[V] = {0, 0};
+#pragma unroll
+            for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
+                if (g < ng) {
+                    const uint4 m4 = *(const uint4*)&S.mt[t][4 * g];
+                    const uint32_t mv[4] = {m4.x, m4.y, m4.z, m4.w};
+                    uint64_t cs[V] = {0, 0};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                        for (int k = 0; k < V; ++k) cs[k] += (uint64_t)y[(4 * g + e) * V + k] * mv[e];
+                    }
+#pragma unroll
+                    for (int k = 0; k < V; ++k) {
+                        acc[k] += cs[k];
+                        wraps[k] += acc[k] < cs[k];
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < V; ++k) r[k] = red.red96(acc[k], wraps[k]);
         }
-        uint32_t r[V];
 #pragma unroll
         for (int k = 0; k < V; ++k) {
-            r[k] = red.red96(acc[k], wraps[k]);
             if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * S.bmod[t]), red.p);
         }
         *(uint2*)(dst + ((size_t)S.trow[t] << logn) + c0) = make_uint2(r[0], r[1]);
@@ -185,6 +212,12 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             const int t = e / MAX_REG_SRC, i = e % MAX_REG_SRC;
             S.mt[t][i] = (t < ntl && i < P.ns) ? P.m(i, t0 + t) : 0;
         }
+        if (threadIdx.x == 0) {
+            uint32_t mx = 0;
+            for (int i = 0; i < P.ns; ++i) mx = max(mx, (uint32_t)A.pr[P.src_prime(i)].p);
+            S.maxs = mx;
+        }
+        __syncthreads();
         for (int t = threadIdx.x; t < ntl; t += BX) {
             const PrimeConst& q = A.pr[P.tgt_prime(t0 + t)];
             S.trow[t] = P.tgt_row(t0 + t);
@@ -192,6 +225,10 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             S.tc[t][1] = (uint32_t)q.split;
             S.tc[t][2] = (uint32_t)(q.split >> 32);
             S.tc[t][3] = (uint32_t)(q.mu_lo >> 32);
+            // sources are reduced below their prime, M's entries below the target's: ns products of at most
+            // (maxs - 1) (p_t - 1) each
+            const uint64_t b = (uint64_t)(S.maxs - 1) * (uint64_t)((uint32_t)q.p - 1);
+            S.lazy[t] = b <= ~0ull / (uint64_t)P.ns;
         }
         if (j.exact) {
             const double* rb = exact_rb((const uint32_t*)A.pool, j);

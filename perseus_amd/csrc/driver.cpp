@@ -234,6 +234,7 @@ struct pcx_ctx {
     uint32_t *pmod = nullptr, *pinv = nullptr;  // values then Shoup companions, by prime id
     uint32_t* mdt = nullptr;  // ModDown conversion matrix M[j][t] = [P / p_j]_{q_t}, j < kp, t < nq
     int md_fused = 1;         // ModDown conversion inside the NTT column pass (kp <= MDC_MAX_KP)
+    int table_only = 0;       // every launch through the kernel table (pcx_ctx_table_only)
     int md_ntg = 5;           // its target rows per workgroup
     int32_t* digit_of = nullptr;
     std::vector<Level> levels;
@@ -578,7 +579,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     t.srows = c->rows;
     t.nregen = c->dnum;
     Stage st(c, 3, s);
-    if (k->pval && !sum) {
+    if (k->pval && !sum && !c->table_only) {
         // the retry values from the key group's table (no redraw in the dot)
         // the table is indexed by the group's key: the launch's key r is the group's r0 + r
         const size_t per_key = (size_t)c->dnum * c->rows * (c->n / 1024);
@@ -967,6 +968,14 @@ const void* pcx_ctx_twiddle(const pcx_ctx* c, int which) {
 }
 uint64_t pcx_ctx_root(const pcx_ctx* c, int id) { return id >= 0 && id < c->rows ? c->roots[id] : 0; }
 size_t pcx_ctx_workspace_bytes(const pcx_ctx* c) { return c->ws_bytes; }
+
+int pcx_ctx_table_only(pcx_ctx* c, int on) {
+    if (!c) return -1;
+    const int prev = c->table_only;
+    c->table_only = on ? 1 : 0;
+    c->md_fused = on ? 0 : (c->kp <= pch::MDC_MAX_KP ? 1 : 0);
+    return prev;
+}
 size_t pcx_ct_words(const pcx_ctx* c) { return c->ct_words(); }
 
 pcx_rows* pcx_rows_new(pcx_ctx* c, const uint32_t* roff, const int32_t* ids, int nrows) {

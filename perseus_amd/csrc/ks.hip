@@ -356,8 +356,40 @@ __device__ __forceinline__ uint32_t lane_prefix(uint32_t cnt, int lane) {
     return pre;
 }
 
-// PATCH: the retry values come from the key group's table (P) instead of the wave's redraw
-template <int NDIG, bool MU2, bool PATCH>
+// The 16 values of slots [s0, s0 + 16) of a bit-packed key row (value i at bits [i BITS, (i + 1) BITS) of the row's
+// little-endian stream, crates/pc-gpu/src/keys.rs:54-58): the lane's words w0 .. w0 + 16, read as four 16-byte loads
+// and one word (the row's guard word keeps w0 + 16 inside the row). With s0 a multiple of 16 the first value starts
+// at bit 0 of w0 (even BITS) or at bit 0 or 16 (odd BITS, by the lane's parity): the window is realigned by that shift
+// once, so every value's position is a compile-time constant.
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+template <int BITS>
+__device__ __forceinline__ void ldpk16(const uint32_t* row, uint32_t s0, uint32_t (&out)[DS]) {
+    const uint32_t bit0 = s0 * BITS;
+    const uint32_t* p = row + (bit0 >> 5);
+    uint32_t w[17];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x4a4 v = *(const u32x4a4*)(p + 4 * i);
+        w[4 * i] = v.x, w[4 * i + 1] = v.y, w[4 * i + 2] = v.z, w[4 * i + 3] = v.w;
+    }
+    w[16] = p[16];
+    if (BITS & 1) {
+        const uint32_t sh = bit0 & 31;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+    }
+    constexpr uint32_t mask = BITS == 32 ? 0xFFFFFFFFu : (1u << BITS) - 1u;
+#pragma unroll
+    for (int k = 0; k < DS; ++k) {
+        const int pos = k * BITS, wi = pos >> 5, off = pos & 31;
+        const uint32_t v = off + BITS <= 32 ? w[wi] >> off : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], off);
+        out[k] = v & mask;
+    }
+}
+
+// PATCH: the retry values come from the key group's table (P) instead of the wave's redraw. PK: key b bit-packed at
+// PK bits (0: dense words)
+template <int NDIG, bool MU2, bool PATCH, int PK>
 __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, const Expander& ex, int r,
                                              const PatchTab& P) {
     const KsArgs& A = *C.A;
@@ -365,7 +397,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     FastWave& W = *C.W;
     const int lane = C.lane, lp = C.lp;
     const uint32_t p = C.p, s0 = C.s0;
-    const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)C.slot * T.row_words + s0;
+    const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)C.slot * T.row_words + (PK ? 0 : s0);
     const size_t dstride = (size_t)T.srows * T.row_words;
     uint32_t seed[8];
     const uint32_t* sp = T.seed[r];
@@ -450,7 +482,10 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     // the key's b rows: they arrive while the queued words are redrawn and s1 goes out, and are consumed last
     uint32_t b[NDIG][DS];
 #pragma unroll
-    for (int d = 0; d < NDIG; ++d) ld16(kb + d * dstride, b[d]);
+    for (int d = 0; d < NDIG; ++d) {
+        if constexpr (PK == 0) ld16(kb + d * dstride, b[d]);
+        else ldpk16<PK>(kb + d * dstride, s0, b[d]);
+    }
     // redraw the queued words: entry <- accepted value mod p (PATCH: the table's values into the queue)
     wave_sync();
     uint32_t nq = 0;
@@ -546,7 +581,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 }
 
 // NW: waves per workgroup (KW: staged D and c0, one key per wave; 1: read from memory)
-template <int NDIG, bool PATCH, int NW>
+template <int NDIG, bool PATCH, int NW, int PK = 0>
 __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, PatchTab P, int logn) {
     static_assert(NDIG >= 1 && NDIG <= MAXD, "digits staged in LDS");
     static_assert(NW == KW || NW == 1, "staged (KW waves) or direct (one wave)");
@@ -603,21 +638,29 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
         C.c0 = C.m0 ? c0row : nullptr;
     }
     if (ex.mu == 2) {
-        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH>(C, red, ex, r, P);
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH, PK>(C, red, ex, r, P);
     } else {
-        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH>(C, red, ex, r, P);
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH, PK>(C, red, ex, r, P);
     }
 }
 
 // the fast dot's launch: one-wave direct workgroups when the launch has fewer keys than a staged workgroup's waves
-template <int NDIG, bool PATCH>
+template <int NDIG, bool PATCH, int PK = 0>
 void dot_fast_launch(dim3 grid, const KsArgs& a, const KeyTab& key, const PatchTab& P, int logn, hipStream_t st) {
     if (a.R < KW) {
         grid.z = a.R;
-        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1>), grid, dim3(DBX), 0, st, a, key, P, logn);
+        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1, PK>), grid, dim3(DBX), 0, st, a, key, P, logn);
     } else {
-        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW>), grid, dim3(KBX), 0, st, a, key, P, logn);
+        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW, PK>), grid, dim3(KBX), 0, st, a, key, P, logn);
     }
+}
+// the fast dot's packed-b widths (the reference's PackedSeeded keys store b at the widest prime's bits)
+template <int PK>
+void dot_fast_pk(int ndig, dim3 grid, const KsArgs& a, const KeyTab& key, int logn, hipStream_t st) {
+    const PatchTab none = {};
+    if (ndig == 1) dot_fast_launch<1, false, PK>(grid, a, key, none, logn, st);
+    if (ndig == 2) dot_fast_launch<2, false, PK>(grid, a, key, none, logn, st);
+    if (ndig == 3) dot_fast_launch<3, false, PK>(grid, a, key, none, logn, st);
 }
 
 template <int LOGN>
@@ -635,12 +678,12 @@ int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     int groups = 1;
     while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
     dim3 grid(chunks, a.nrows, groups);
-    const bool fast = mode == 1 && a.K == 1 && key.bits == 0 && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
+    const bool pk_fast = key.bits == 0 || key.bits == 30 || key.bits == 31;
+    const bool fast = mode == 1 && a.K == 1 && pk_fast && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
     if (fast) {
-        const PatchTab none = {};
-        if (a.ndig == 1) dot_fast_launch<1, false>(grid, a, key, none, LOGN, (hipStream_t)s);
-        if (a.ndig == 2) dot_fast_launch<2, false>(grid, a, key, none, LOGN, (hipStream_t)s);
-        if (a.ndig == 3) dot_fast_launch<3, false>(grid, a, key, none, LOGN, (hipStream_t)s);
+        if (key.bits == 0) dot_fast_pk<0>(a.ndig, grid, a, key, LOGN, (hipStream_t)s);
+        if (key.bits == 30) dot_fast_pk<30>(a.ndig, grid, a, key, LOGN, (hipStream_t)s);
+        if (key.bits == 31) dot_fast_pk<31>(a.ndig, grid, a, key, LOGN, (hipStream_t)s);
     } else if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     else hipLaunchKernelGGL(dot_k<false>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     return launch_rc();

@@ -162,6 +162,10 @@ class Context:
     def ct_buf(self, count=1):
         return DevBuf(count * self.ct_words)
 
+    def table_only(self, on=True):
+        """Issue every operation through the kernel table alone (pcx_ctx_table_only); returns the previous setting."""
+        return bool(LIB.pcx_ctx_table_only(self.h, int(on)))
+
     def modup(self, ct, top, stream):
         check(LIB.pcx_modup(self.h, ct.addr(), top, stream.h), "modup")
 

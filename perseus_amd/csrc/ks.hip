@@ -62,9 +62,14 @@ constexpr int KBX = DBX * KW;       // threads per workgroup
 constexpr int MAXD = 3;             // digits staged in LDS (more are read from global memory)
 constexpr int QCAP = 1536;          // rejected-word queue entries per wave (>= 1024 free before every digit)
 
+// D and c0 rows are staged with 4 words of padding after every 16 (a lane's 16 words start 20 words after its
+// neighbour's), so the lanes' 16-byte LDS reads fall on distinct banks.
+constexpr int PADW = DCH + DCH / 4;
+__device__ __forceinline__ int padw(int i) { return i + (i >> 4) * 4; }
+
 struct DotLds {
-    uint32_t D[MAXD][DCH];   // the chunk's digit operands D_d (shared by every key)
-    uint32_t c0[DCH];        // the chunk's c0 (mode 1: times P mod q_t; mode 2: added)
+    uint32_t D[MAXD][PADW];  // the chunk's digit operands D_d (shared by every key), padded rows
+    uint32_t c0[PADW];       // the chunk's c0 (mode 1: times P mod q_t; mode 2: added), padded
     struct Wave {
         uint64_t ex[DCH];    // D_d a_d of the redrawn words (64-bit LDS atomics); then the scatter buffers
         uint32_t q[QCAP];    // rejected words: digit << 16 | slot
@@ -83,6 +88,10 @@ struct DotCtx {
     }
 };
 
+// The redraw sums' slot s lives at (s mod 16) 64 + s / 16: a lane's 16 slots are 64 entries apart, so the 64 lanes'
+// clears and reads of one k touch consecutive words (bank-conflict free)
+__device__ __forceinline__ uint32_t ex_slot(uint32_t s) { return (s & 15u) * DBX + (s >> 4); }
+
 // Redraw the queued words of one wave: item = digit << 16 | slot; each lane takes items and adds D_d a_d mod p (the
 // accepted attempt of the word, attempts t = 1..15 at block + t N/16) to the slot's 64-bit sum. Reduced products keep
 // the sum below ndig 2^31 however many of a slot's digits were redrawn.
@@ -98,8 +107,8 @@ __device__ __forceinline__ void drain(DotLds& L, DotLds::Wave& W, const DotCtx& 
             v = chacha12_word(seed, ctr + (uint32_t)tt * n16, d, ex.p, TAG_KSKA, (int)(sl & 15));
             if (v < ex.mp) break;
         }
-        const uint32_t xd = d < (uint32_t)MAXD ? L.D[d][sl] : X.dptr((int)d)[X.chunk0 + sl];
-        atomicAdd((unsigned long long*)&W.ex[sl], (unsigned long long)red((uint64_t)xd * ex.red(v)));
+        const uint32_t xd = d < (uint32_t)MAXD ? L.D[d][padw(sl)] : X.dptr((int)d)[X.chunk0 + sl];
+        atomicAdd((unsigned long long*)&W.ex[ex_slot(sl)], (unsigned long long)red((uint64_t)xd * ex.red(v)));
     }
     wave_sync();
     if (lane == 0) W.qn = 0;
@@ -141,11 +150,11 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
         // stage D_d (d < MAXD) and c0 of the chunk: coalesced 16-byte loads by the whole workgroup
         for (int d = 0; d < min(ndig, MAXD); ++d) {
             const uint4* D = (const uint4*)(X.dptr(d) + chunk0);
-            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i] = D[i];
+            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.D[d])[i + (i >> 2)] = D[i];
         }
         if (m0) {
             const uint4* C0 = (const uint4*)((const uint32_t*)A.c0 + c * A.ct_stride + X.trow + chunk0);
-            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i] = C0[i];
+            for (int i = threadIdx.x; i < DCH / 4; i += KBX) ((uint4*)L.c0)[i + (i >> 2)] = C0[i];
         }
         __syncthreads();
         for (int r = r_lo + wv; r < r_hi; r += KW) {
@@ -156,7 +165,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
                 for (int i = 0; i < 8; ++i) seed[i] = sp[i];
             }
 #pragma unroll
-            for (int k = 0; k < DS; ++k) W.ex[lane * DS + k] = 0;
+            for (int k = 0; k < DS; ++k) W.ex[k * DBX + lane] = 0;
             if (lane == 0) W.qn = 0;
             wave_sync();
             uint64_t s0a[DS], s1a[DS];
@@ -165,7 +174,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
             for (int k = 0; k < (WIDE ? DS : 1); ++k) part0[k] = part1[k] = 0;
             if (fold_c0) {
 #pragma unroll
-                for (int k = 0; k < DS; ++k) s0a[k] = (uint64_t)L.c0[lane * DS + k] * pm;
+                for (int k = 0; k < DS; ++k) s0a[k] = (uint64_t)L.c0[padw(lane * DS) + k] * pm;
             } else {
 #pragma unroll
                 for (int k = 0; k < DS; ++k) s0a[k] = 0;
@@ -210,7 +219,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
                     ld16((const uint32_t*)A.ka[r] + d * A.key_digit_stride + X.trow + s0, a);
                 }
                 uint32_t x[DS];
-                if (d < MAXD) ld16(L.D[d] + lane * DS, x);
+                if (d < MAXD) ld16(L.D[d] + padw(lane * DS), x);
                 else ld16(X.dptr(d) + s0, x);
 #pragma unroll
                 for (int k = 0; k < DS; ++k) {
@@ -233,7 +242,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
             uint32_t r0[DS], r1[DS];
 #pragma unroll
             for (int k = 0; k < DS; ++k) {
-                const uint64_t e = W.ex[lane * DS + k];
+                const uint64_t e = W.ex[k * DBX + lane];
                 if (WIDE) {
                     r0[k] = addm(part0[k], red(s0a[k]), p);
                     r1[k] = addm(addm(part1[k], red(s1a[k]), p), red(e), p);
@@ -245,7 +254,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
             if ((pc0 && !fold_c0) || m0 == 2) {
 #pragma unroll
                 for (int k = 0; k < DS; ++k) {
-                    const uint32_t cz = L.c0[lane * DS + k];
+                    const uint32_t cz = L.c0[padw(lane * DS) + k];
                     r0[k] = addm(r0[k], m0 == 2 ? cz : shoup(cz, pm, pms, p), p);
                 }
             }
@@ -304,11 +313,6 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
 // a time; each owner adds D_d a_d of its redrawn words into its slots there, after the scatter write of s1. A wave
 // needs 8 KB of LDS, so three workgroups fit on a CU.
 constexpr int FQCAP = DCH;  // queue entries per wave
-
-// D and c0 rows are staged with 4 words of padding after every 16 (a lane's 16 words start 20 words after its
-// neighbour's), so the lanes' 16-byte LDS reads fall on distinct banks.
-constexpr int PADW = DCH + DCH / 4;
-__device__ __forceinline__ int padw(int i) { return i + (i >> 4) * 4; }
 
 struct FastWave {
     uint32_t buf[DCH];  // scatter buffer

@@ -100,7 +100,7 @@ struct JobLds {
     double rb[MAX_REG_SRC];
     uint32_t bmod[MAXT];
     uint32_t lazy[MAXT];   // 1: ns (max source prime - 1) (p_t - 1) < 2^64, the sum needs no carry count
-    uint32_t maxs;         // the job's largest source prime
+    uint32_t sp[MAX_REG_SRC];  // the sources' primes
 };
 
 __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
@@ -212,12 +212,8 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             const int t = e / MAX_REG_SRC, i = e % MAX_REG_SRC;
             S.mt[t][i] = (t < ntl && i < P.ns) ? P.m(i, t0 + t) : 0;
         }
-        if (threadIdx.x == 0) {
-            uint32_t mx = 0;
-            for (int i = 0; i < P.ns; ++i) mx = max(mx, (uint32_t)A.pr[P.src_prime(i)].p);
-            S.maxs = mx;
-        }
-        __syncthreads();
+        // every table load of the set-up is issued by its own thread: one round trip to the pool, one to the primes
+        if (threadIdx.x < P.ns) S.sp[threadIdx.x] = (uint32_t)A.pr[P.src_prime(threadIdx.x)].p;
         for (int t = threadIdx.x; t < ntl; t += BX) {
             const PrimeConst& q = A.pr[P.tgt_prime(t0 + t)];
             S.trow[t] = P.tgt_row(t0 + t);
@@ -225,16 +221,21 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             S.tc[t][1] = (uint32_t)q.split;
             S.tc[t][2] = (uint32_t)(q.split >> 32);
             S.tc[t][3] = (uint32_t)(q.mu_lo >> 32);
-            // sources are reduced below their prime, M's entries below the target's: ns products of at most
-            // (maxs - 1) (p_t - 1) each
-            const uint64_t b = (uint64_t)(S.maxs - 1) * (uint64_t)((uint32_t)q.p - 1);
-            S.lazy[t] = b <= ~0ull / (uint64_t)P.ns;
         }
         if (j.exact) {
             const double* rb = exact_rb((const uint32_t*)A.pool, j);
             const uint32_t* bmod = (const uint32_t*)(rb + j.nsrc);
             for (int i = threadIdx.x; i < P.ns; i += BX) S.rb[i] = rb[i];
             for (int t = threadIdx.x; t < ntl; t += BX) S.bmod[t] = bmod[t0 + t];
+        }
+        __syncthreads();
+        for (int t = threadIdx.x; t < ntl; t += BX) {
+            // sources are reduced below their prime, M's entries below the target's: ns products of at most
+            // (max source prime - 1) (p_t - 1) each
+            uint32_t mx = 0;
+            for (int i = 0; i < P.ns; ++i) mx = max(mx, S.sp[i]);
+            const uint64_t b = (uint64_t)(mx - 1) * (uint64_t)(S.tc[t][0] - 1);
+            S.lazy[t] = b <= ~0ull / (uint64_t)P.ns;
         }
         __syncthreads();
         if (c0 < (1u << logn)) job_lds(A, j, P, S, src, dst, c0, logn, ntl);

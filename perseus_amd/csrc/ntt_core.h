@@ -33,19 +33,39 @@ struct Geo {
 };
 
 // ------------------------------------------------------------------------------------------------ butterflies
-// H: Harvey (every prime < 2^30). p2 = 2p.
+// Two VALU instructions the compiler does not form from this arithmetic by itself:
+// v_sad_u32: a - b + c in one instruction, for b <= a < 2^31 (d = |a - b| + c);
+// v_mad_u64_u32: a b + c mod 2^64; only the low word is used below, so c's high word is free and the Shoup product's
+// subtraction of floor(a ws / 2^32) p folds into a multiply-add by 2^32 - p.
+__device__ __forceinline__ uint32_t sub_add(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t d;
+    asm("v_sad_u32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+// Shoup product a w mod p in [0, 2p) (as shoup_lz) in three instructions: a w as a 64-bit product, the quotient
+// estimate, then a w + q (2^32 - p) mod 2^32
+__device__ __forceinline__ uint32_t shoup3(uint32_t a, uint32_t w, uint32_t ws, uint32_t p) {
+    uint64_t aw, r, c0, c1;
+    asm("v_mad_u64_u32 %0, %1, %2, %3, 0" : "=v"(aw), "=s"(c0) : "v"(a), "v"(w));
+    const uint32_t q = __umulhi(a, ws);
+    asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=v"(r), "=s"(c1) : "v"(q), "v"(0u - p), "v"(aw));
+    return (uint32_t)r;
+}
+
+// H: Harvey (every prime < 2^30). p2 = 2p. Forward: a in [0, 2p) ([0, 4p) for H), b any word; outputs in [0, 2p)
+// ([0, 4p)). Inverse: canonical in and out ([0, 2p) for H).
 template <bool H>
 __device__ __forceinline__ void ct(uint32_t& a, uint32_t& b, uint32_t w, uint32_t ws, uint32_t p, uint32_t p2) {
-    uint32_t t = shoup_lz(b, w, ws, p);  // [0, 2p)
+    uint32_t t = shoup3(b, w, ws, p);  // [0, 2p)
     if (H) {
         const uint32_t u = min(a, a - p2);  // [0, 4p) -> [0, 2p)
         a = u + t;
-        b = u - t + p2;
+        b = sub_add(p2, t, u);  // u - t + 2p
     } else {
         const uint32_t u = min(a, a - p);  // [0, 2p) -> [0, p)
         t = min(t, t - p);
         a = u + t;
-        b = u - t + p;
+        b = sub_add(p, t, u);  // u - t + p
     }
 }
 template <bool H>
@@ -54,10 +74,11 @@ __device__ __forceinline__ void gs(uint32_t& a, uint32_t& b, uint32_t w, uint32_
     if (H) {  // [0, 2p) in and out
         const uint32_t s = u + v;
         a = min(s, s - p2);
-        b = shoup_lz(u - v + p2, w, ws, p);
+        b = shoup3(sub_add(p2, v, u), w, ws, p);
     } else {  // canonical in and out
-        a = addm(u, v, p);
-        const uint32_t d = shoup_lz(u - v + p, w, ws, p);
+        const uint32_t s = u + v;
+        a = min(s, s - p);
+        const uint32_t d = shoup3(sub_add(p, v, u), w, ws, p);
         b = min(d, d - p);
     }
 }

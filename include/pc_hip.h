@@ -868,6 +868,13 @@ int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const voi
  * NULL: out = the sum alone). No key of the sum may be the identity (-1). */
 int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
                    const void* onto, pc_stream_t s);
+/* out = onto + sum_j rot(cts[j], key idx[j]): the giant-step sum of a BSGS linear transform over n distinct ciphertexts
+ * (crates/pc-gpu/src/bts/cts.rs:958-971, the Horner sums kept in the extended basis; rotate.rs:692-776 for the sum's
+ * ModDown): a ModUp of each input, its key dot added onto one extended sum (KS_ACC after the first), then ONE ModDown
+ * whose epilogue adds onto `onto` (onto == out: in place; NULL: the sum alone). cts: a HOST array of n device
+ * ciphertexts. No key may be the identity (-1). */
+int pcx_rotate_many(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top, void* out,
+                    const void* onto, pc_stream_t s);
 /* The rotate-and-sum ladder (crates/pc-gpu/src/rotate.rs:924-992): out = the sum of x over its rotations by every
  * multiple of start below stop (start < 0: the negative steps), rung by rung (out += rot(out, gap), gap doubling), or
  * radix_bits >= 2 rungs at a time through pcx_rotate_sum when the group holds every step of the rung. tmp: a scratch

@@ -983,6 +983,41 @@ int or_rotate_sum(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const
     return 0;
 }
 
+// The giant-step sum over distinct inputs (crates/pc-gpu/src/bts/cts.rs:958-971, the sums kept in the extended basis;
+// rotate.rs:692-776 for the single ModDown): ModUp of each ct[j], its extended rotation by key j added word by word,
+// one ModDown, the result added onto `onto` (Q rows 0..top)
+int or_rotate_many(const or_ctx* c, const uint32_t* const* cts, int top, int nkeys, const uint32_t* seeds,
+                   const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, uint32_t* out) {
+    check_top(c, top);
+    const uint32_t n = c->n;
+    const int R = c->rows();
+    const size_t ctw = (size_t)2 * R * n;
+    if (nkeys < 1) return -1;
+    for (int r = 0; r < nkeys; ++r)
+        if (gs[r] % (2ull * n) == 1) return -1;
+    std::vector<uint32_t> digits((size_t)c->dnum * R * n, 0), ext(ctw, 0), sum(ctw, 0), res(ctw, 0);
+    for (int r = 0; r < nkeys; ++r) {
+        or_modup(c, cts[r] + (size_t)R * n, top, digits.data());
+        or_ks_dot(c, cts[r], digits.data(), top, seeds + 8 * r, bs[r], (uint32_t)or_galois_inverse(gs[r], n),
+                  ext.data());
+        for (int part = 0; part < 2; ++part)
+            for (int t = 0; t < R; ++t) {
+                if (t > top && t < c->nq) continue;
+                const uint32_t p = (uint32_t)c->primes[t];
+                const size_t o = ((size_t)part * R + t) * n;
+                for (uint32_t i = 0; i < n; ++i) sum[o + i] = addm(sum[o + i], ext[o + i], p);
+            }
+    }
+    or_moddown(c, sum.data(), top, res.data());
+    for (int part = 0; part < 2; ++part)
+        for (int t = 0; t <= top; ++t) {
+            const uint32_t p = (uint32_t)c->primes[t];
+            const size_t o = ((size_t)part * R + t) * n;
+            for (uint32_t i = 0; i < n; ++i) out[o + i] = onto ? addm(onto[o + i], res[o + i], p) : res[o + i];
+        }
+    return 0;
+}
+
 // crates/pc-gpu/src/rotate.rs:924-992 (rotate_and_sum): gaps start, 2 start, ... below stop; radix rungs through
 // or_rotate_sum onto out when the keys hold every step of the rung, else rung by rung: tmp = rot(out or x), out += tmp
 int or_rotate_and_sum(const or_ctx* c, const uint32_t* x, int top, int64_t start, int64_t stop, int radix_bits,

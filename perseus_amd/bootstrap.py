@@ -485,7 +485,9 @@ class Bootstrap:
             ops.pt_dot(res, rots, top, pts, B, G)
         else:
             ops.cts(res, x.h, top, pts, B, G)
-        acc = None
+        # the giant steps: the rotated results' key dots summed in the extended basis, one ModDown onto the
+        # unrotated result
+        base, ys, gs = None, [], []
         for j in range(G):
             g = plan.giant[j] % self.par.n
             y = ops.item(res, j)
@@ -494,15 +496,19 @@ class Bootstrap:
                 ops.moddown(t, y, top)
                 y = t
             if g:
-                t = ops.alloc()
-                ops.rotate(t, y, top, g)
-                y = t
-            if acc is None:
-                acc = y
+                ys.append(y)
+                gs.append(g)
+            elif base is None:
+                base = y
             else:
-                s = ops.alloc()
-                ops.add(s, acc, y, top, False)
-                acc = s
+                t = ops.alloc()
+                ops.add(t, base, y, top, False)
+                base = t
+        if ys:
+            acc = ops.alloc()
+            ops.rotate_many(acc, ys, top, gs, base)
+        else:
+            acc = base
         out = ops.alloc()
         ops.rescale2(out, acc, top)
         ops.level_done()
@@ -775,6 +781,10 @@ class GpuOps:
         else:
             r = self.levels[self.level_i][1][step]
         self.ctx.rotate(self.keys, r, x, top, out, self.st)
+
+    def rotate_many(self, out, xs, top, steps, onto):
+        r = [self.levels[self.level_i][1][g] for g in steps]
+        self.ctx.rotate_many(self.keys, r, xs, top, out, self.st, onto=onto)
 
     def hoisted(self, outs, x, top, steps):
         babies = self.levels[self.level_i][0]

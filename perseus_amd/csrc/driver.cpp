@@ -1310,6 +1310,20 @@ int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* c
     return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
 }
 
+int pcx_rotate_many(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top, void* out,
+                    const void* onto, pc_stream_t s) {
+    if (!c || !k || k->c != c || n < 1 || !idx || !cts || !out || !level(c, top)) return -1;
+    for (int j = 0; j < n; ++j)
+        if (!cts[j] || idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
+    // one ModUp per input (each its own c1), its dot written (the first) or added onto the extended sum, c0 folded in
+    // as P sigma(c0); then one ModDown of the sum onto `onto`
+    for (int j = 0; j < n; ++j) {
+        if (int e = modup(c, cts[j], top, s)) return e;
+        if (int e = dot(c, k, idx[j], 1, cts[j], top, c->ext, s, 0, j ? 1 | PC_KS_ACC : 1)) return e;
+    }
+    return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
+}
+
 int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
                        void* out, void* tmp, pc_stream_t s) {
     if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top)) return -1;

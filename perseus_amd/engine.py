@@ -214,6 +214,14 @@ class Context:
         check(LIB.pcx_rotate_sum(self.h, keys.h, arr, len(idx), ct.addr(), top, out.addr(),
                                  None if onto is None else onto.addr(), stream.h), "rotate_sum")
 
+    def rotate_many(self, keys, idx, cts, top, out, stream, onto=None):
+        """out = onto + sum_j rot(cts[j], key idx[j]): a ModUp and a key dot per input, the dots summed in the
+        extended basis, one ModDown (pcx_rotate_many)."""
+        arr = (C.c_int * len(idx))(*idx)
+        ptrs = (C.c_void_p * len(cts))(*[x.addr() for x in cts])
+        check(LIB.pcx_rotate_many(self.h, keys.h, arr, len(idx), ptrs, top, out.addr(),
+                                  None if onto is None else onto.addr(), stream.h), "rotate_many")
+
     def rotate_and_sum(self, keys, x, top, start, stop, out, tmp, stream, radix_bits=1):
         """The rotate-and-sum ladder: out = sum of x over its rotations by the multiples of start below stop."""
         check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(), tmp.addr(),

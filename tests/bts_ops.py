@@ -102,6 +102,11 @@ class OracleOps:
         r = self.conj_key if step == "conj" else self.levels[self.level_i][1][step]
         self.get(out)[:] = self.oc.rotate(self.get(x), top, self.seeds[r], self.bs[r], self.gal[r])
 
+    def rotate_many(self, out, xs, top, steps, onto):
+        r = [self.levels[self.level_i][1][g] for g in steps]
+        self.get(out)[:] = self.oc.rotate_many([self.get(x) for x in xs], top, self.seeds[r], [self.bs[i] for i in r],
+                                               [self.gal[i] for i in r], onto=None if onto is None else self.get(onto))
+
     def hoisted(self, outs, x, top, steps):
         babies = self.levels[self.level_i][0]
         res = self.oc.rotate_hoisted(self.get(x), top, self.seeds[babies], [self.bs[r] for r in babies],

@@ -323,6 +323,41 @@ def test_rotate_sum(stream, name, idx, mode):
     assert (got[:, : top + 1] == want[:, : top + 1]).all()
 
 
+@pytest.mark.parametrize("name,idx,mode", [("small", [0, 1, 2], "onto"), ("small", [2, 0], "plain"),
+                                           ("small", [3, 1], "in_place"), ("small", [1, 2, 3], "table_only"),
+                                           ("c3", [0, 1, 2, 3], "onto")])
+def test_rotate_many(stream, name, idx, mode):
+    """out = onto + ModDown(sum over j of the extended rotation of ct_j by key idx[j]): a ModUp per input, the dots
+    added onto one extended sum (KS_ACC after the first), one ModDown with the add-onto epilogue."""
+    say(f"[rotate_many] {name} keys={idx} {mode}")
+    ch, ctx, oc = contexts(name, k_rot=4)
+    twin.set_threads(16)
+    steps = [1, 3, 2, 7]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=29)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1 if name == "c3" else 5
+    cts = [random_ct(ch, top, 31 + j) for j in range(len(idx))]
+    base = random_ct(ch, top, 30)
+    devs = [pa.DevBuf.from_array(x) for x in cts]
+    onto = pa.DevBuf.from_array(base)
+    if mode == "table_only":
+        ctx.table_only(True)
+    try:
+        if mode == "in_place":
+            ctx.rotate_many(keys, idx, devs, top, devs[0], stream, onto=devs[0])
+            out = devs[0]
+        else:
+            out = ctx.ct_buf()
+            ctx.rotate_many(keys, idx, devs, top, out, stream, onto=None if mode == "plain" else onto)
+        stream.sync()
+    finally:
+        ctx.table_only(False)
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.rotate_many(cts, top, seeds[idx], [bs[i] for i in idx], [gals[i] for i in idx],
+                          onto={"plain": None, "in_place": cts[0]}.get(mode, base))
+    assert (got[:, : top + 1] == want[:, : top + 1]).all()
+
+
 @pytest.mark.parametrize("name,radix", [("small", 1), ("small", 2), ("c3", 2)])
 def test_rotate_and_sum(stream, name, radix):
     say(f"[rotate_and_sum] {name} start=1 stop=16 radix_bits={radix}")

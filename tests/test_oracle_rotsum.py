@@ -120,3 +120,33 @@ def test_sum_is_one_moddown_of_the_summed_dots():
     for r, x in enumerate(gals):
         separate = add_q(ctx, separate, ctx.rotate(ct, top, seeds[r], bs[r], x), top)
     assert not (got[:, : top + 1] == separate[:, : top + 1]).all()
+
+
+def test_rotate_many_pins():
+    """The giant-step sum over distinct inputs: with every input the same ciphertext it is the summed rotation (one
+    ModUp reused there, one per input here: the same digits); with one input, the single rotation; with distinct
+    inputs it decrypts to the sum of their rotated messages up to one small error shared by every limb."""
+    ctx = small_chain()
+    n, top = ctx.n, 5
+    g = twin.Prng([1, 6, 1, 8, 0, 3, 3, 9], 0)
+    s_eval = ctx.secret_eval(g.sparse_ternary(n, 64))
+    rng = np.random.default_rng(7)
+    ms = [rng.integers(-(1 << 22), 1 << 22, n) for _ in range(3)]
+    enc = [encrypt(ctx, s_eval, m, rng, top) for m in ms]
+    cts = [c for c, _ in enc]
+    gals, seeds, bs = keys_for(ctx, g, s_eval, [1, 2, 5])
+    same = ctx.rotate_many([cts[0]] * 3, top, seeds, bs, gals, onto=cts[1])
+    want = ctx.rotate_sum(cts[0], top, seeds, bs, gals, onto=cts[1])
+    assert (same[:, : top + 1] == want[:, : top + 1]).all()
+    one = ctx.rotate_many([cts[2]], top, seeds[1:2], bs[1:2], gals[1:2])
+    assert (one[:, : top + 1] == ctx.rotate(cts[2], top, seeds[1], bs[1], gals[1])[:, : top + 1]).all()
+    out = ctx.rotate_many(cts, top, seeds, bs, gals, onto=cts[0])
+    dec = decrypt(ctx, s_eval, out, top)
+    me = [e for _, e in enc]
+    want = me[0] + sum(coeff_automorph(e, x, n) for e, x in zip(me, gals))
+    errs = [centred((dec[t].astype(np.int64) - want) % ctx.primes[t], ctx.primes[t]) for t in range(top + 1)]
+    for e in errs[1:]:
+        assert (e == errs[0]).all()
+    assert np.abs(errs[0]).max() < (1 << 20)
+    with pytest.raises(ValueError):
+        ctx.rotate_many(cts[:1], top, seeds[:1], bs[:1], [1])

@@ -79,6 +79,7 @@ def _load():
         "or_secret_eval": (None, [C.c_void_p, i8p, u32p]),
         "or_automorph_rows": (None, [C.c_void_p, u32p, C.c_uint32, C.c_int, u32p]),
         "or_rotate_sum": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p, u32p]),
+        "or_rotate_many": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p, u32p]),
         "or_rotate_and_sum": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int64, C.c_int64, C.c_int, C.c_int, u32p,
                                         C.c_void_p, u64p, u32p]),
         "or_cts_fused": (None, [C.c_void_p, C.c_int, u32p, u32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
@@ -298,6 +299,18 @@ class Ctx:
                                np.asarray(gs, np.uint64), None if on is None else on.ctypes.data, out)
         if rc:
             raise ValueError("rotate_sum: an identity key or no keys")
+        return out
+
+    def rotate_many(self, cts, top, seeds, bs, gs, onto=None):
+        """onto + ModDown(sum of the extended rotations of cts[j] by key j): a ModUp each, one ModDown."""
+        out = self.ct_zeros()
+        xs = [np.ascontiguousarray(x, np.uint32) for x in cts]
+        bs = [np.ascontiguousarray(b, np.uint32) for b in bs]
+        on = None if onto is None else np.ascontiguousarray(onto, np.uint32)
+        rc = LIB.or_rotate_many(self.h, ptr_array(xs), top, len(gs), np.ascontiguousarray(seeds, np.uint32).reshape(-1),
+                                ptr_array(bs), np.asarray(gs, np.uint64), None if on is None else on.ctypes.data, out)
+        if rc:
+            raise ValueError("rotate_many: an identity key or no keys")
         return out
 
     def rotate_and_sum(self, x, top, start, stop, seeds, bs, gs, radix_bits=1):

@@ -70,3 +70,32 @@ def test_bootstrap_gpu_matches_the_oracle(lanes, fused):
     st.sync()
     got2 = out2.h.buf.download((2, ctx.rows, ctx.n), offset=out2.h.off, words=ctx.ct_words)
     assert (got2[:, : out.top + 1] == got[:, : out.top + 1]).all(), "the rerun gives the same words"
+
+
+@pytest.mark.parametrize("lanes", [1, 2])
+def test_bootstrap_graph_replay(lanes):
+    """The whole bootstrap captured into one HIP graph (the composite's operations never allocate, synchronise or read
+    device data on the host once a first run has filled the buffer pool and the constants) and replayed three times,
+    with the output cleared and eager work on the same buffers between the replays: every replay equals the eager run
+    word for word."""
+    say(f"[bootstrap graph] N=2^12, {lanes} EvalMod lane(s): capture, 3 replays vs the eager run")
+    S = setup_oracle(fused=False)
+    rng = np.random.default_rng(11)
+    z, ct, me = input_ct(S, rng)
+    ctx, keys, relin, st, ops, boot = gpu_boot(S, lanes)
+    x = pa.DevBuf.from_array(ct)
+    out = boot.run(B.View(x))
+    st.sync()
+    want = out.h.buf.download((2, ctx.rows, ctx.n), offset=out.h.off, words=ctx.ct_words)
+    graph = pa.Graph(st, lambda: boot.run(B.View(x)))
+    zeros = np.zeros(ctx.ct_words, np.uint32)
+    for rep in range(3):
+        out.h.buf.upload(zeros, offset=out.h.off)
+        other = ctx.ct_buf()
+        ctx.rotate(keys, 0, x, boot.T, other, st)  # eager work through the same context's workspace
+        st.sync()
+        graph.launch(st)
+        st.sync()
+        got = out.h.buf.download((2, ctx.rows, ctx.n), offset=out.h.off, words=ctx.ct_words)
+        say(f"[bootstrap graph] replay {rep}")
+        assert (got[:, : out.top + 1] == want[:, : out.top + 1]).all(), f"replay {rep} == eager"

@@ -875,6 +875,11 @@ int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* c
  * ciphertexts. No key may be the identity (-1). */
 int pcx_rotate_many(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top, void* out,
                     const void* onto, pc_stream_t s);
+/* pcx_rotate_many then the two-prime rescale, fused into its ModDown (B = P q_top q_{top-1}, the exact conversion of
+ * crates/pc-gpu/src/bts/cts.rs:740-751, LtEnd::FusedRescale, applied to the extended sum + P onto): out's Q rows
+ * 0..top - 2 = round((P onto + sum) / B). top >= 2; onto NULL or a ciphertext at top (may alias out). */
+int pcx_rotate_many_rescale(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top,
+                            void* out, const void* onto, pc_stream_t s);
 /* The rotate-and-sum ladder (crates/pc-gpu/src/rotate.rs:924-992): out = the sum of x over its rotations by every
  * multiple of start below stop (start < 0: the negative steps), rung by rung (out += rot(out, gap), gap doubling), or
  * radix_bits >= 2 rungs at a time through pcx_rotate_sum when the group holds every step of the rung. tmp: a scratch
@@ -913,6 +918,10 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
  * by key 0 of k (the relinearization key: galois 1) and added: out = (c0, c1) + ModDown(dot(ModUp(d2))) on Q rows
  * 0..top (degree 2, rescale pending). out may be a or b. */
 int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);
+/* pcx_mul_relin then the two-prime rescale, fused into one ModDown by B = P q_top q_{top-1} (the exact conversion of
+ * crates/pc-gpu/src/bts/cts.rs:740-751, LtEnd::FusedRescale, applied to x + P (d0, d1)): out's Q rows 0..top - 2 =
+ * round((P (d0, d1) + KS(d2)) / B). top >= 2. out may alias a or b. */
+int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
  * form rows by prime id (rows 0..top read). out may be ct. */
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);

@@ -818,6 +818,83 @@ void or_moddown(const or_ctx* c, const uint32_t* ext, int top, uint32_t* out) {
     });
 }
 
+// The ModDown and two-prime rescale fused into one exact ModDown (crates/pc-gpu/src/bts/cts.rs:740-751, LtEnd::
+// FusedRescale; the exact conversion of crates/pc-gpu/src/bconv.rs:105-132 and crates/pc-kernels/kernels/bconv.cuh):
+// x = ext + P onto (onto NULL: 0) in the extended basis at top, B = P q_{top-1} q_top, sources in that order;
+// out's Q rows 0..top - 2 = (x - conv_B(x)) B^-1 with conv exact (u = floor(sum_k y_k (1 / b_k) + 0.5) in doubles, the
+// products by fma in source order), computed as (ext - conv) B^-1 + onto (q_top q_{top-1})^-1.
+void or_moddown_rescale(const or_ctx* c, const uint32_t* ext, int top, const uint32_t* onto, uint32_t* out) {
+    check_top(c, top);
+    if (top < 2) throw std::runtime_error("the fused ModDown-rescale needs top >= 2");
+    const uint32_t n = c->n;
+    const int R = c->rows(), kp = c->kp, ns = kp + 2, nt = top - 1;
+    std::vector<int32_t> sid, tid;
+    for (int j = 0; j < kp; ++j) sid.push_back(c->nq + j);
+    sid.push_back(top - 1);
+    sid.push_back(top);
+    for (int t = 0; t < nt; ++t) tid.push_back(t);
+    std::vector<uint32_t> pre, M;
+    bconv_tables(c, sid.data(), ns, tid.data(), nt, pre, M);
+    std::vector<uint32_t> bmod(nt), binv(nt), s2(nt);
+    std::vector<double> rb(ns);
+    for (int k = 0; k < ns; ++k) rb[k] = 1.0 / (double)c->primes[sid[k]];
+    for (int t = 0; t < nt; ++t) {
+        const uint64_t q = c->primes[t];
+        uint64_t b = 1;
+        for (int k = 0; k < ns; ++k) b = mulmod(b, c->primes[sid[k]] % q, q);
+        bmod[t] = (uint32_t)b;
+        binv[t] = (uint32_t)invmod(b, q);
+        s2[t] = (uint32_t)invmod(mulmod(c->primes[top] % q, c->primes[top - 1] % q, q), q);
+    }
+    // the sources in coefficient form, pre folded into the inverse's scale
+    std::vector<uint32_t> y((size_t)2 * ns * n);
+    parallel_for(2 * ns, [&](long e) {
+        const int part = (int)(e / ns), k = (int)(e % ns), id = sid[k];
+        const uint32_t p = (uint32_t)c->primes[id];
+        uint32_t* r = &y[(size_t)e * n];
+        memcpy(r, ext + ((size_t)part * R + id) * n, 4ull * n);
+        if (onto && id < c->nq) {
+            const uint32_t pm = c->pmodq[id];
+            const uint32_t* o = onto + ((size_t)part * R + id) * n;
+            for (uint32_t i = 0; i < n; ++i) r[i] = addm(r[i], (uint32_t)mulmod(o[i], pm, p), p);
+        }
+        const uint32_t es = (uint32_t)mulmod(c->ninv[id], pre[k], p);
+        ntt_inv_row(c, r, id, es, shoup_c(es, p));
+    });
+    std::vector<uint32_t> conv((size_t)2 * nt * n);
+    const uint32_t blk = 2048, nb = (n + blk - 1) / blk;
+    parallel_for(2 * nb, [&](long e) {
+        const int part = (int)(e / nb);
+        const uint32_t lo = (uint32_t)(e % nb) * blk, hi = std::min(n, lo + blk);
+        for (uint32_t i = lo; i < hi; ++i) {
+            double v = 0.0;
+            for (int k = 0; k < ns; ++k) v = std::fma((double)y[((size_t)part * ns + k) * n + i], rb[k], v);
+            const uint64_t u = (uint64_t)std::floor(v + 0.5);
+            for (int t = 0; t < nt; ++t) {
+                const uint64_t q = c->primes[t];
+                u128 acc = 0;
+                for (int k = 0; k < ns; ++k) acc += (uint64_t)y[((size_t)part * ns + k) * n + i] * M[(size_t)k * nt + t];
+                const uint32_t r = (uint32_t)(acc % q);
+                conv[((size_t)part * nt + t) * n + i] = subm(r, (uint32_t)mulmod(u % q, bmod[t], q), (uint32_t)q);
+            }
+        }
+    });
+    parallel_for(2 * nt, [&](long e) {
+        const int part = (int)(e / nt), t = (int)(e % nt);
+        const uint32_t p = (uint32_t)c->primes[t];
+        uint32_t* cv = &conv[(size_t)e * n];
+        ntt_fwd_row(c, cv, t);
+        const uint32_t* x = ext + ((size_t)part * R + t) * n;
+        const uint32_t* d = onto ? onto + ((size_t)part * R + t) * n : nullptr;
+        uint32_t* o = out + ((size_t)part * R + t) * n;
+        for (uint32_t i = 0; i < n; ++i) {
+            uint32_t v = (uint32_t)mulmod(subm(x[i], cv[i], p), binv[t], p);
+            if (d) v = addm(v, (uint32_t)mulmod(d[i], s2[t], p), p);
+            o[i] = v;
+        }
+    });
+}
+
 void or_rotate(const or_ctx* c, const uint32_t* ct, int top, const uint32_t seed[8], const uint32_t* b, uint64_t g,
                uint32_t* out) {
     const uint32_t* ptr[1] = {b};
@@ -987,8 +1064,9 @@ int or_rotate_sum(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const
 // rotate.rs:692-776 for the single ModDown): ModUp of each ct[j], its extended rotation by key j added word by word,
 // one ModDown, the result added onto `onto` (Q rows 0..top)
 int or_rotate_many(const or_ctx* c, const uint32_t* const* cts, int top, int nkeys, const uint32_t* seeds,
-                   const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, uint32_t* out) {
+                   const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, int rescale, uint32_t* out) {
     check_top(c, top);
+    if (rescale && top < 2) return -1;
     const uint32_t n = c->n;
     const int R = c->rows();
     const size_t ctw = (size_t)2 * R * n;
@@ -1007,6 +1085,12 @@ int or_rotate_many(const or_ctx* c, const uint32_t* const* cts, int top, int nke
                 const size_t o = ((size_t)part * R + t) * n;
                 for (uint32_t i = 0; i < n; ++i) sum[o + i] = addm(sum[o + i], ext[o + i], p);
             }
+    }
+    if (rescale) {
+        or_moddown_rescale(c, sum.data(), top, onto, res.data());
+        for (int part = 0; part < 2; ++part)
+            memcpy(out + (size_t)part * R * n, res.data() + (size_t)part * R * n, 4ull * (top - 1) * n);
+        return 0;
     }
     or_moddown(c, sum.data(), top, res.data());
     for (int part = 0; part < 2; ++part)

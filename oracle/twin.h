@@ -113,9 +113,13 @@ void or_rotate_hoisted(const or_ctx* c, const uint32_t* ct, int top, int nkeys, 
 int or_rotate_sum(const or_ctx* c, const uint32_t* ct, int top, int nkeys, const uint32_t* seeds,
                   const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, uint32_t* out);
 /* the giant-step sum over distinct inputs (crates/pc-gpu/src/bts/cts.rs:958-971): out (Q rows 0..top) = onto + ModDown
- * of the sum of the extended rotations of cts[j] by key j (a ModUp each). -1 for an identity key or no keys. */
+ * of the sum of the extended rotations of cts[j] by key j (a ModUp each); rescale: the ModDown fused with the
+ * two-prime rescale (or_moddown_rescale, out at top - 2). -1 for an identity key or no keys. */
 int or_rotate_many(const or_ctx* c, const uint32_t* const* cts, int top, int nkeys, const uint32_t* seeds,
-                   const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, uint32_t* out);
+                   const uint32_t* const* bs, const uint64_t* gs, const uint32_t* onto, int rescale, uint32_t* out);
+/* the ModDown and two-prime rescale as one exact ModDown by B = P q_{top-1} q_top (crates/pc-gpu/src/bts/cts.rs:
+ * 740-751): out's Q rows 0..top - 2 = round((ext + P onto) / B) (onto may be NULL); top >= 2 */
+void or_moddown_rescale(const or_ctx* c, const uint32_t* ext, int top, const uint32_t* onto, uint32_t* out);
 /* the rotate-and-sum ladder (crates/pc-gpu/src/rotate.rs:924-992) over the keys (seeds, bs, gs): out = the sum of x
  * over its rotations by every multiple of start below stop; radix_bits >= 2 rungs through or_rotate_sum. -1 when a
  * step's key is missing. */

@@ -78,6 +78,8 @@ _SIGS = {
     "pcx_keys_relin": (vp, [vp, C.POINTER(C.c_int8), u32p, C.POINTER(C.c_int64), C.c_int, C.POINTER(C.c_int)]),
     "pcx_rescale": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
     "pcx_mul_relin": (C.c_int, [vp, vp, vp, vp, C.c_int, vp, vp]),
+    "pcx_mul_relin_rescale": (C.c_int, [vp, vp, vp, vp, C.c_int, vp, vp]),
+    "pcx_rotate_many_rescale": (C.c_int, [vp, vp, C.POINTER(C.c_int), C.c_int, C.POINTER(vp), C.c_int, vp, vp, vp]),
     "pcx_mul_plain": (C.c_int, [vp, vp, vp, C.c_int, vp, vp]),
     "pcx_modup": (C.c_int, [vp, vp, C.c_int, vp]),
     "pcx_modup_digits": (vp, [vp]),

@@ -313,8 +313,7 @@ class Evaluator:
     def mul(self, a, b):
         t = min(a.top, b.top)
         out = self.ops.alloc()
-        self.ops.mul_relin(out, a.h, b.h, t)
-        self.ops.rescale2(out, out, t)
+        self.ops.mul_relin_rescale(out, a.h, b.h, t)
         return Ct(out, t - 2, a.scale * b.scale / self.qq(t))
 
     def mul_to(self, a, c, scale, top):
@@ -504,13 +503,12 @@ class Bootstrap:
                 t = ops.alloc()
                 ops.add(t, base, y, top, False)
                 base = t
-        if ys:
-            acc = ops.alloc()
-            ops.rotate_many(acc, ys, top, gs, base)
-        else:
-            acc = base
         out = ops.alloc()
-        ops.rescale2(out, acc, top)
+        if ys:
+            # the rescale by the two top primes fused into the sum's ModDown
+            ops.rotate_many_rescale(out, ys, top, gs, base)
+        else:
+            ops.rescale2(out, base, top)
         ops.level_done()
         return Ct(out, top - 2, x.scale * f)
 
@@ -786,6 +784,10 @@ class GpuOps:
         r = [self.levels[self.level_i][1][g] for g in steps]
         self.ctx.rotate_many(self.keys, r, xs, top, out, self.st, onto=onto)
 
+    def rotate_many_rescale(self, out, xs, top, steps, onto):
+        r = [self.levels[self.level_i][1][g] for g in steps]
+        self.ctx.rotate_many_rescale(self.keys, r, xs, top, out, self.st, onto=onto)
+
     def hoisted(self, outs, x, top, steps):
         babies = self.levels[self.level_i][0]
         assert len(babies) == len(steps)
@@ -810,6 +812,9 @@ class GpuOps:
 
     def mul_relin(self, out, a, b, top):
         self.ctx.mul_relin(self.relin, a, b, top, out, self.st)
+
+    def mul_relin_rescale(self, out, a, b, top):
+        self.ctx.mul_relin_rescale(self.relin, a, b, top, out, self.st)
 
     def rescale2(self, out, x, top):
         self.ctx.rescale(x, top, 2, out, self.st)

@@ -14,8 +14,8 @@
 namespace pch {
 namespace bconv {
 
-constexpr int BX = 256, V = 2, PER_WG = BX * V;
-constexpr int MAX_REG_SRC = 16;
+constexpr int BX = 256;
+constexpr int MAX_REG_SRC = 20;  // the fused ModDown-rescale's kp + 2 sources at 16 special primes
 constexpr int TPG = 8;  // targets per workgroup when BconvArgs.max_tgt gives the grid its target groups
 
 struct Pool {
@@ -49,8 +49,8 @@ __device__ __forceinline__ uint64_t exact_u(const BconvJob& j, const double* rb,
     return (uint64_t)floor(v + 0.5);
 }
 
-// One workgroup = one job x 512 coefficients (2 per thread). A job's record lives in device memory, so its size is
-// read here: jobs of at most 16 sources keep the sources of their 2 coefficients in registers and the job's tables in
+// One workgroup = one job x 256 V coefficients (V per thread). A job's record lives in device memory, so its size is
+// read here: jobs of at most 20 sources keep the sources of their V coefficients in registers and the job's tables in
 // LDS; wider jobs (bconv_wide, up to 48 sources at u32 words) re-read their sources per target (L1/L2 resident).
 __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, const Pool& P, const uint32_t* src,
                                          uint32_t* dst, uint32_t c, int logn, int t0, int t1) {
@@ -90,8 +90,8 @@ __device__ __forceinline__ void job_wide(const BconvArgs& A, const BconvJob& j, 
     }
 }
 
-// The job's tables in LDS (jobs of at most 16 sources and MAXT targets): M transposed and zero-padded to 16 sources,
-// so a target's column is 4 broadcast 16-byte reads; each target's reduction constants; the sources' rows and pre.
+// The job's tables in LDS (jobs of at most 20 sources and MAXT targets): M transposed and zero-padded to 20 sources,
+// so a target's column is broadcast 16-byte reads; each target's reduction constants; the sources' rows and pre.
 constexpr int MAXT = 64;
 struct JobLds {
     uint32_t mt[MAXT][MAX_REG_SRC];
@@ -103,14 +103,32 @@ struct JobLds {
     uint32_t sp[MAX_REG_SRC];  // the sources' primes
 };
 
+// V consecutive words at p (V = 2 or 4: one 8- or 16-byte access)
+template <int V>
+__device__ __forceinline__ void ldv(const uint32_t* p, uint32_t (&v)[V]) {
+    if constexpr (V == 4) {
+        const uint4 x = *(const uint4*)p;
+        v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+    } else {
+        const uint2 x = *(const uint2*)p;
+        v[0] = x.x, v[1] = x.y;
+    }
+}
+template <int V>
+__device__ __forceinline__ void stv(uint32_t* p, const uint32_t (&v)[V]) {
+    if constexpr (V == 4) *(uint4*)p = make_uint4(v[0], v[1], v[2], v[3]);
+    else *(uint2*)p = make_uint2(v[0], v[1]);
+}
+
+template <int V>
 __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
                                         const uint32_t* src, uint32_t* dst, uint32_t c0, int logn, int ntl) {
     uint32_t y[MAX_REG_SRC * V];
 #pragma unroll
     for (int i = 0; i < MAX_REG_SRC; ++i) {
         if (i < P.ns) {
-            const uint2 x = *(const uint2*)(src + ((size_t)P.src_row(i) << logn) + c0);
-            uint32_t v[V] = {x.x, x.y};
+            uint32_t v[V];
+            ldv<V>(src + ((size_t)P.src_row(i) << logn) + c0, v);
             if (!j.prescaled) {
                 const Red red(A.pr[P.src_prime(i)]);
                 const uint32_t pre = P.pre(i);
@@ -124,7 +142,7 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
             for (int k = 0; k < V; ++k) y[i * V + k] = 0;
         }
     }
-    uint64_t u[V] = {0, 0};
+    uint64_t u[V] = {};
     if (j.exact) {
 #pragma unroll
         for (int k = 0; k < V; ++k) {
@@ -143,7 +161,7 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
     const int ng = (P.ns + 3) >> 2;  // groups of 4 sources (M zero-padded)
     for (int t = 0; t < ntl; ++t) {
         const Red red(S.tc[t][0], S.tc[t][1], S.tc[t][2], S.tc[t][3]);
-        uint64_t acc[V] = {0, 0};
+        uint64_t acc[V] = {};
         uint32_t r[V];
         if (S.lazy[t]) {
             // every partial sum stays below 2^64: one multiply-add per product
@@ -164,13 +182,13 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
         } else {
             // four products of words below 2^31 stay below 2^64: each group of four is summed by multiply-adds, and
             // only the group sums carry into the 96-bit total
-            uint32_t wraps[V] = {0, 0};
+            uint32_t wraps[V] = {};
 #pragma unroll
             for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
                 if (g < ng) {
                     const uint4 m4 = *(const uint4*)&S.mt[t][4 * g];
                     const uint32_t mv[4] = {m4.x, m4.y, m4.z, m4.w};
-                    uint64_t cs[V] = {0, 0};
+                    uint64_t cs[V] = {};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
 #pragma unroll
@@ -190,15 +208,16 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
         for (int k = 0; k < V; ++k) {
             if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * S.bmod[t]), red.p);
         }
-        *(uint2*)(dst + ((size_t)S.trow[t] << logn) + c0) = make_uint2(r[0], r[1]);
+        stv<V>(dst + ((size_t)S.trow[t] << logn) + c0, r);
     }
 }
 
+template <int V>
 __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
     __shared__ JobLds S;
     const BconvJob j = A.jobs[blockIdx.y];
     const Pool P{(const uint32_t*)A.pool + j.pool_off, (int)j.nsrc, (int)j.ntgt};
-    const uint32_t c0 = blockIdx.x * PER_WG + threadIdx.x * V;
+    const uint32_t c0 = blockIdx.x * (BX * V) + threadIdx.x * V;
     if (P.ns < 1) return;
     // this workgroup's targets [t0, t0 + ntl): the job's targets split evenly over the grid's target groups
     const int tpg = (P.nt + (int)gridDim.z - 1) / (int)gridDim.z;
@@ -208,7 +227,7 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
     const uint32_t* src = (const uint32_t*)A.src + ((size_t)j.src_off << logn);
     uint32_t* dst = (uint32_t*)A.dst + ((size_t)j.dst_off << logn);
     if (P.ns <= MAX_REG_SRC && ntl <= MAXT) {
-        for (int e = threadIdx.x; e < MAXT * MAX_REG_SRC; e += BX) {
+        for (int e = threadIdx.x; e < ntl * MAX_REG_SRC; e += BX) {
             const int t = e / MAX_REG_SRC, i = e % MAX_REG_SRC;
             S.mt[t][i] = (t < ntl && i < P.ns) ? P.m(i, t0 + t) : 0;
         }
@@ -238,7 +257,7 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             S.lazy[t] = b <= ~0ull / (uint64_t)P.ns;
         }
         __syncthreads();
-        if (c0 < (1u << logn)) job_lds(A, j, P, S, src, dst, c0, logn, ntl);
+        if (c0 < (1u << logn)) job_lds<V>(A, j, P, S, src, dst, c0, logn, ntl);
     } else if (c0 < (1u << logn)) {
         for (int k = 0; k < V; ++k) job_wide(A, j, P, src, dst, c0 + k, logn, t0, t0 + ntl);
     }
@@ -253,10 +272,13 @@ template <int LOGN>
 int launch(const BconvArgs* a, pc_stream_t s) {
     if (int rc = check(a)) return rc;
     if (a->njobs == 0) return 0;
-    const int gx = ((1 << LOGN) + PER_WG - 1) / PER_WG;
-    // target groups: every job's targets fit max_tgt (the plan's widest job; 0: one group)
+    // target groups: every job's targets fit max_tgt (the plan's widest job; 0: one group). Two coefficients per thread
+    // and 8 targets per group measured best overall on the bootstrap's ModUps and ModDowns (tops 16 to 46, 16 special
+    // primes) against 4 coefficients or 16 to 64 targets.
+    constexpr int V = 2;
+    const int gx = ((1 << LOGN) + BX * V - 1) / (BX * V);
     const int gz = a->max_tgt > TPG ? std::min((a->max_tgt + TPG - 1) / TPG, 256) : 1;
-    hipLaunchKernelGGL(bconv_k, dim3(gx, a->njobs, gz), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    hipLaunchKernelGGL(bconv_k<V>, dim3(gx, a->njobs, gz), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
     return launch_rc();
 }
 

@@ -139,6 +139,7 @@ struct Dev {
 struct JobSpec {
     uint32_t src_off, dst_off;
     std::vector<uint32_t> src, tgt;  // rows == prime ids
+    bool exact = false;              // the exact conversion (the fast one corrected by u = round(sum y_i / b_i))
 };
 struct Bconv {
     BconvJob* jobs = nullptr;
@@ -156,7 +157,7 @@ struct Bconv {
             r.nsrc = ns;
             r.ntgt = nt;
             r.pool_off = (uint32_t)pool_h.size();
-            r.exact = 0;
+            r.exact = j.exact ? 1 : 0;
             r.prescaled = 1;
             r.split = 0;
             std::vector<uint64_t> bp;
@@ -174,6 +175,28 @@ struct Bconv {
                     pool_h.push_back((uint32_t)v);
                 }
             if (pool_h.size() & 1) pool_h.push_back(0);
+            if (j.exact) {
+                // rb_i = 1 / b_i as doubles (8-byte aligned: the pool's words are even here), B mod t per target, then
+                // floor(2^59 / b_i) as u64 (bconv.rs:105-132)
+                for (uint64_t b : bp) {
+                    const double rb = 1.0 / (double)b;
+                    uint64_t bits;
+                    memcpy(&bits, &rb, 8);
+                    pool_h.push_back((uint32_t)bits);
+                    pool_h.push_back((uint32_t)(bits >> 32));
+                }
+                for (uint32_t t : j.tgt) {
+                    uint64_t tp = primes[t], m = 1;
+                    for (uint64_t b : bp) m = mulmod(m, b % tp, tp);
+                    pool_h.push_back((uint32_t)m);
+                }
+                if (pool_h.size() & 1) pool_h.push_back(0);
+                for (uint64_t b : bp) {
+                    const uint64_t cq = (1ull << 59) / b;
+                    pool_h.push_back((uint32_t)cq);
+                    pool_h.push_back((uint32_t)(cq >> 32));
+                }
+            }
             jobs_h.push_back(r);
             max_tgt = std::max(max_tgt, (int)nt);
         }
@@ -212,6 +235,15 @@ struct Level {
         uint32_t* k = nullptr;
         uint64_t qinv_ab = 0, C_ab = 0;
     } rs[2];
+    // ModDown by B = P q_top q_{top-1} at once, the rescale by the two top primes fused in (crates/pc-gpu/src/bts/
+    // cts.rs:740-751, LtEnd::FusedRescale): INTT of the sources (P rows, then rows top - 1, top; both parts; es =
+    // N^-1 pre_j for B), the exact conversion to rows 0..top - 2, their NTT with the epilogue (x - conv) B^-1 (es);
+    // k: per row [s2 | s2 Shoup | P mod q | its Shoup] (rows words each), s2 = (q_top q_{top-1})^-1 mod q_i
+    struct MdRescale {
+        Rows intt, ntt;
+        Bconv conv;
+        uint32_t* k = nullptr;
+    } mdr;
 };
 
 }  // namespace
@@ -474,6 +506,66 @@ int build_level(pcx_ctx* c, int top, Level& L) {
         if (int e = fill_rows(c->dev, Z.intt, roff, rp, nullptr, nullptr)) return e;
         if (int e = fill_rows(c->dev, Z.ntt, roff2, rp2, nullptr, nullptr)) return e;
     }
+    if (top >= 2) {
+        const int R = c->rows;
+        std::vector<uint32_t> src;
+        for (int k = 0; k < c->kp; ++k) src.push_back((uint32_t)(c->nq + k));
+        src.push_back((uint32_t)(top - 1));
+        src.push_back((uint32_t)top);
+        std::vector<uint64_t> bp;
+        for (uint32_t id : src) bp.push_back(c->primes[id]);
+        const std::vector<uint32_t> pre = pre_factors(bp);
+        std::vector<uint32_t> roff, es, roff2, bi;
+        std::vector<int32_t> rp, rp2;
+        for (size_t j = 0; j < src.size(); ++j) {
+            const uint64_t p = bp[j];
+            const uint32_t sc = (uint32_t)mulmod(invmod(n % p, p), pre[j], p);
+            for (int part = 0; part < 2; ++part) {
+                roff.push_back((uint32_t)(part * R) + src[j]);
+                rp.push_back((int32_t)src[j]);
+                es.push_back(sc);
+            }
+        }
+        std::vector<JobSpec> specs;
+        for (int part = 0; part < 2; ++part) {
+            JobSpec j;
+            j.src_off = j.dst_off = (uint32_t)(part * R);
+            j.src = src;
+            for (int t = 0; t + 2 <= top; ++t) j.tgt.push_back((uint32_t)t);
+            j.exact = true;
+            specs.push_back(j);
+        }
+        // the epilogue's B^-1 by prime id (rows of other ids unused)
+        std::vector<uint32_t> binv(R, 0), k((size_t)4 * R, 0);
+        for (int t = 0; t + 2 <= top; ++t) {
+            const uint64_t q = c->primes[t];
+            uint64_t b = 1;
+            for (uint64_t x : bp) b = mulmod(b, x % q, q);
+            binv[t] = (uint32_t)invmod(b, q);
+            const uint32_t s2 = (uint32_t)invmod(mulmod(c->primes[top] % q, c->primes[top - 1] % q, q), q);
+            k[t] = s2;
+            k[R + t] = shoup_c(s2, (uint32_t)q);
+            for (int part = 0; part < 2; ++part) {
+                roff2.push_back((uint32_t)(part * R + t));
+                rp2.push_back(t);
+            }
+        }
+        for (int t = top - 1; t <= top; ++t) {
+            const uint64_t q = c->primes[t];
+            uint64_t pm = 1;
+            for (int j = 0; j < c->kp; ++j) pm = mulmod(pm, c->primes[c->nq + j] % q, q);
+            k[2 * R + t] = (uint32_t)pm;
+            k[3 * R + t] = shoup_c((uint32_t)pm, (uint32_t)q);
+        }
+        std::vector<uint32_t> est = scale_table(c->primes, rp, es);
+        std::vector<int32_t> ids(R);
+        for (int i = 0; i < R; ++i) ids[i] = i;
+        std::vector<uint32_t> bt = scale_table(c->primes, ids, binv);
+        if (int e = fill_rows(c->dev, L.mdr.intt, roff, rp, nullptr, &est)) return e;
+        if (int e = fill_rows(c->dev, L.mdr.ntt, roff2, rp2, nullptr, &bt)) return e;
+        L.mdr.conv.build(c->dev, c->primes, specs);
+        L.mdr.k = c->dev.upload(k);
+    }
     return c->dev.err;
 }
 
@@ -505,6 +597,48 @@ const Level* level(const pcx_ctx* c, int top) {
 
 // ModUp (crates/pc-gpu/src/ks.rs:958-1040): INTT of c1 rows 0..top (out of place, N^-1 pre_t), conversion of every
 // live digit, NTT of the targets
+// ModDown and the two-prime rescale at once (the level's mdr plan): out (Q rows 0..top - 2) = the exact
+// (x + P onto - conv_B) / B with B = P q_top q_{top-1}, x = ext (one extended ciphertext), onto NULL or a ciphertext at
+// top (may alias out)
+int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto, pc_stream_t s) {
+    const Level* L = level(c, top);
+    if (!L || top < 2 || !L->mdr.k) return -1;
+    const Level::MdRescale& M = L->mdr;
+    if (onto) {
+        Stage st(c, 9, s);
+        if (int e = pch::mdr_prep((int)c->logn, ext, onto, out, M.k, c->pr, c->rows, top, s)) return e;
+    }
+    NttArgs a = ntt_args(c, ext, M.intt, M.intt.n);
+    a.es = M.intt.es;
+    a.ess = M.intt.es + M.intt.n;
+    {
+        Stage st(c, 4, s);
+        if (int e = c->tab->ntt_inv(&a, s)) return e;
+    }
+    BconvArgs b;
+    memset(&b, 0, sizeof b);
+    b.src = ext;
+    b.dst = c->conv;
+    b.jobs = M.conv.jobs;
+    b.pool = M.conv.pool;
+    b.pr = c->pr;
+    b.njobs = M.conv.njobs;
+    b.max_tgt = M.conv.max_tgt;
+    {
+        Stage st(c, 5, s);
+        if (int e = c->tab->bconv(&b, s)) return e;
+    }
+    NttArgs f = ntt_args(c, c->conv, M.ntt, M.ntt.n);
+    f.epi = onto ? 2 : 1;
+    f.ed = nullptr;  // the epilogue adds onto out's rows, which hold onto s2
+    f.eout = out;
+    f.ex = ext;
+    f.xnum = 1;
+    f.es = M.ntt.es;
+    f.ess = M.ntt.es + c->rows;
+    Stage st(c, 6, s);
+    return c->tab->ntt_fwd(&f, s);
+}
 int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
     const Level* L = level(c, top);
     if (!L) return -1;
@@ -1310,18 +1444,32 @@ int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* c
     return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
 }
 
-int pcx_rotate_many(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top, void* out,
-                    const void* onto, pc_stream_t s) {
-    if (!c || !k || k->c != c || n < 1 || !idx || !cts || !out || !level(c, top)) return -1;
+// the extended sum of pcx_rotate_many in c->ext: one ModUp per input (each its own c1), its dot written (the first)
+// or added onto the sum, c0 folded in as P sigma(c0)
+static int rotate_many_ext(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top,
+                           pc_stream_t s) {
+    if (!c || !k || k->c != c || n < 1 || !idx || !cts || !level(c, top)) return -1;
     for (int j = 0; j < n; ++j)
         if (!cts[j] || idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
-    // one ModUp per input (each its own c1), its dot written (the first) or added onto the extended sum, c0 folded in
-    // as P sigma(c0); then one ModDown of the sum onto `onto`
     for (int j = 0; j < n; ++j) {
         if (int e = modup(c, cts[j], top, s)) return e;
         if (int e = dot(c, k, idx[j], 1, cts[j], top, c->ext, s, 0, j ? 1 | PC_KS_ACC : 1)) return e;
     }
+    return 0;
+}
+
+int pcx_rotate_many(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top, void* out,
+                    const void* onto, pc_stream_t s) {
+    if (!out) return -1;
+    if (int e = rotate_many_ext(c, k, idx, n, cts, top, s)) return e;
     return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
+}
+
+int pcx_rotate_many_rescale(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top,
+                            void* out, const void* onto, pc_stream_t s) {
+    if (!out || top < 2) return -1;
+    if (int e = rotate_many_ext(c, k, idx, n, cts, top, s)) return e;
+    return moddown_rescale(c, c->ext, top, out, onto, s);
 }
 
 int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
@@ -1438,7 +1586,8 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
 // tensor kernel (d2 into part 1 of the context's tmp ciphertext), ModUp(d2), the key inner product with the
 // relinearization key (no c0 term, no automorphism), and the ModDown added onto (c0, c1): out = (c0, c1) +
 // (ext - conv) P^-1 on Q rows 0..top. out may be a or b.
-int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
+// the product's (d0, d1) into out and the key switch of d2 into c->ext (before ModDown)
+static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
     if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
     const uint64_t part = (uint64_t)c->rows * c->n;
     TensorArgs t;
@@ -1456,8 +1605,17 @@ int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top
         if (int e = c->tab->tensor(&t, s)) return e;
     }
     if (int e = modup(c, c->tmp, top, s)) return e;
-    if (int e = dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, 0)) return e;
+    return dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, 0);
+}
+int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
+    if (int e = relin_ext(c, k, a, b, top, out, s)) return e;
     return moddown(c, c->ext, c->conv, 1, top, out, s, out);
+}
+int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out,
+                          pc_stream_t s) {
+    if (top < 2) return -1;
+    if (int e = relin_ext(c, k, a, b, top, out, s)) return e;
+    return moddown_rescale(c, c->ext, top, out, out, s);
 }
 
 // The plaintext product (crates/pc-gpu/src/ops.rs:927-951 mult_pt, the table's mul_table, em.cuh:508-515): out = ct pt

@@ -222,6 +222,13 @@ class Context:
         check(LIB.pcx_rotate_many(self.h, keys.h, arr, len(idx), ptrs, top, out.addr(),
                                   None if onto is None else onto.addr(), stream.h), "rotate_many")
 
+    def rotate_many_rescale(self, keys, idx, cts, top, out, stream, onto=None):
+        """rotate_many with the two-prime rescale fused into its ModDown: out at top - 2 (pcx_rotate_many_rescale)."""
+        arr = (C.c_int * len(idx))(*idx)
+        ptrs = (C.c_void_p * len(cts))(*[x.addr() for x in cts])
+        check(LIB.pcx_rotate_many_rescale(self.h, keys.h, arr, len(idx), ptrs, top, out.addr(),
+                                          None if onto is None else onto.addr(), stream.h), "rotate_many_rescale")
+
     def rotate_and_sum(self, keys, x, top, start, stop, out, tmp, stream, radix_bits=1):
         """The rotate-and-sum ladder: out = sum of x over its rotations by the multiples of start below stop."""
         check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(), tmp.addr(),
@@ -238,6 +245,11 @@ class Context:
     def mul_relin(self, keys, a, b, top, out, stream):
         """out = a b relinearized by key 0 of keys (pcx_mul_relin)."""
         check(LIB.pcx_mul_relin(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h), "mul_relin")
+
+    def mul_relin_rescale(self, keys, a, b, top, out, stream):
+        """out (top - 2) = a b relinearized and rescaled by the two top primes in one ModDown (pcx_mul_relin_rescale)."""
+        check(LIB.pcx_mul_relin_rescale(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h),
+              "mul_relin_rescale")
 
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}

@@ -107,6 +107,12 @@ class OracleOps:
         self.get(out)[:] = self.oc.rotate_many([self.get(x) for x in xs], top, self.seeds[r], [self.bs[i] for i in r],
                                                [self.gal[i] for i in r], onto=None if onto is None else self.get(onto))
 
+    def rotate_many_rescale(self, out, xs, top, steps, onto):
+        r = [self.levels[self.level_i][1][g] for g in steps]
+        self.get(out)[:] = self.oc.rotate_many([self.get(x) for x in xs], top, self.seeds[r], [self.bs[i] for i in r],
+                                               [self.gal[i] for i in r], onto=None if onto is None else self.get(onto),
+                                               rescale=True)
+
     def hoisted(self, outs, x, top, steps):
         babies = self.levels[self.level_i][0]
         res = self.oc.rotate_hoisted(self.get(x), top, self.seeds[babies], [self.bs[r] for r in babies],
@@ -125,6 +131,9 @@ class OracleOps:
 
     def mul_relin(self, out, a, b, top):
         self.get(out)[:] = self.oc.mul_relin(self.get(a), self.get(b), top, self.relin_seed, self.relin_b)
+
+    def mul_relin_rescale(self, out, a, b, top):
+        self.get(out)[:] = self.oc.mul_relin_rescale(self.get(a), self.get(b), top, self.relin_seed, self.relin_b)
 
     def rescale2(self, out, x, top):
         self.get(out)[:] = self.oc.rescale(self.get(x).copy(), top, 2)

@@ -135,3 +135,22 @@ def test_mul_relin_rescale_decrypts(stream):
     div = int(ch.primes[top]) * int(ch.primes[top - 1])
     prod = negacyclic(ma, mb)
     assert max(abs(x - round(y / div)) for x, y in zip(got, prod)) < 1 << 8
+
+
+@pytest.mark.parametrize("name,top,alias", [("small", 5, False), ("small", 3, True), ("small31", 5, False),
+                                            ("c3", 29, False), ("c5", 46, True), ("c5", 20, False)])
+def test_mul_relin_rescale(stream, name, top, alias):
+    """The relinearized product and the two-prime rescale as one exact ModDown by P q_top q_{top-1}
+    (pcx_mul_relin_rescale) against the oracle's composition, word for word on rows 0..top - 2."""
+    say(f"[mul_relin_rescale] {name} top={top} out=a:{alias}")
+    ch, ctx, oc = contexts(name)
+    keys, _, seed, _ = relin_key(name)
+    rng = np.random.default_rng(top * 11 + alias)
+    a, b = random_ct(ch, top, rng), random_ct(ch, top, rng)
+    want = oc.mul_relin_rescale(a, b, top, seed, keys.download_b(0))
+    ba, bb = pa.DevBuf.from_array(a), pa.DevBuf.from_array(b)
+    out = ba if alias else ctx.ct_buf(1)
+    ctx.mul_relin_rescale(keys, ba, bb, top, out, stream)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    assert (got[:, : top - 1] == want[:, : top - 1]).all()

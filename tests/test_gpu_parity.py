@@ -358,6 +358,34 @@ def test_rotate_many(stream, name, idx, mode):
     assert (got[:, : top + 1] == want[:, : top + 1]).all()
 
 
+@pytest.mark.parametrize("name,idx,mode", [("small", [0, 1, 2], "onto"), ("small", [2, 0], "plain"),
+                                           ("small", [3, 1], "in_place"), ("c3", [0, 1, 2, 3], "onto")])
+def test_rotate_many_rescale(stream, name, idx, mode):
+    """pcx_rotate_many with the two-prime rescale fused into its ModDown (one exact ModDown by P q_top q_{top-1}):
+    word for word with the oracle on rows 0..top - 2."""
+    say(f"[rotate_many_rescale] {name} keys={idx} {mode}")
+    ch, ctx, oc = contexts(name, k_rot=4)
+    twin.set_threads(16)
+    gals, seeds, bs = oracle_keys(oc, ch, [1, 3, 2, 7], seed=37)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1 if name == "c3" else 5
+    cts = [random_ct(ch, top, 41 + j) for j in range(len(idx))]
+    base = random_ct(ch, top, 40)
+    devs = [pa.DevBuf.from_array(x) for x in cts]
+    onto = pa.DevBuf.from_array(base)
+    if mode == "in_place":
+        ctx.rotate_many_rescale(keys, idx, devs, top, devs[0], stream, onto=devs[0])
+        out = devs[0]
+    else:
+        out = ctx.ct_buf()
+        ctx.rotate_many_rescale(keys, idx, devs, top, out, stream, onto=None if mode == "plain" else onto)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.rotate_many(cts, top, seeds[idx], [bs[i] for i in idx], [gals[i] for i in idx],
+                          onto={"plain": None, "in_place": cts[0]}.get(mode, base), rescale=True)
+    assert (got[:, : top - 1] == want[:, : top - 1]).all()
+
+
 @pytest.mark.parametrize("name,radix", [("small", 1), ("small", 2), ("c3", 2)])
 def test_rotate_and_sum(stream, name, radix):
     say(f"[rotate_and_sum] {name} start=1 stop=16 radix_bits={radix}")

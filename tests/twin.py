@@ -79,7 +79,9 @@ def _load():
         "or_secret_eval": (None, [C.c_void_p, i8p, u32p]),
         "or_automorph_rows": (None, [C.c_void_p, u32p, C.c_uint32, C.c_int, u32p]),
         "or_rotate_sum": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p, u32p]),
-        "or_rotate_many": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p, u32p]),
+        "or_rotate_many": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, u32p, C.c_void_p, u64p, C.c_void_p,
+                                     C.c_int, u32p]),
+        "or_moddown_rescale": (None, [C.c_void_p, u32p, C.c_int, C.c_void_p, u32p]),
         "or_rotate_and_sum": (C.c_int, [C.c_void_p, u32p, C.c_int, C.c_int64, C.c_int64, C.c_int, C.c_int, u32p,
                                         C.c_void_p, u64p, u32p]),
         "or_cts_fused": (None, [C.c_void_p, C.c_int, u32p, u32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
@@ -268,6 +270,28 @@ class Ctx:
         out[1, :n] = ((c1[0].astype(np.uint64) + md[1, :n]) % q).astype(np.uint32)
         return out
 
+    def moddown_rescale(self, ext, top, onto=None):
+        """Q rows 0..top - 2 of round((ext + P onto) / (P q_top q_{top-1})): the ModDown and the two-prime rescale as
+        one exact ModDown."""
+        out = self.ct_zeros()
+        on = None if onto is None else np.ascontiguousarray(onto, np.uint32)
+        LIB.or_moddown_rescale(self.h, np.ascontiguousarray(ext, np.uint32), top,
+                               None if on is None else on.ctypes.data, out)
+        return out
+
+    def mul_relin_rescale(self, a, b, top, seed, bkey):
+        """The relinearized product rescaled by the two top primes in one exact ModDown: the tensor, ModUp(d2), the key
+        dot, then moddown_rescale with (d0, d1) as onto."""
+        from oracle import em
+        n = top + 1
+        c0, c1, d2 = em.tensor(self.primes, [(a[None, :, :n], b[None, :, :n])])
+        tmp = self.ct_zeros()
+        tmp[1, :n] = d2[0]
+        ext = self.ks_dot(tmp, self.modup(tmp[1], top), top, seed, bkey, 1)
+        d = self.ct_zeros()
+        d[0, :n], d[1, :n] = c0[0], c1[0]
+        return self.moddown_rescale(ext, top, d)
+
     def rescale(self, x, top, ndrop):
         """Rows 0..top - ndrop of the rescale of one ciphertext x [2][rows][N] (oracle/em.py rescale)."""
         from oracle import em
@@ -301,14 +325,16 @@ class Ctx:
             raise ValueError("rotate_sum: an identity key or no keys")
         return out
 
-    def rotate_many(self, cts, top, seeds, bs, gs, onto=None):
-        """onto + ModDown(sum of the extended rotations of cts[j] by key j): a ModUp each, one ModDown."""
+    def rotate_many(self, cts, top, seeds, bs, gs, onto=None, rescale=False):
+        """onto + ModDown(sum of the extended rotations of cts[j] by key j): a ModUp each, one ModDown (rescale: the
+        ModDown by P q_top q_{top-1}, the result at top - 2)."""
         out = self.ct_zeros()
         xs = [np.ascontiguousarray(x, np.uint32) for x in cts]
         bs = [np.ascontiguousarray(b, np.uint32) for b in bs]
         on = None if onto is None else np.ascontiguousarray(onto, np.uint32)
         rc = LIB.or_rotate_many(self.h, ptr_array(xs), top, len(gs), np.ascontiguousarray(seeds, np.uint32).reshape(-1),
-                                ptr_array(bs), np.asarray(gs, np.uint64), None if on is None else on.ctypes.data, out)
+                                ptr_array(bs), np.asarray(gs, np.uint64), None if on is None else on.ctypes.data,
+                                int(rescale), out)
         if rc:
             raise ValueError("rotate_many: an identity key or no keys")
         return out

@@ -99,7 +99,6 @@ struct JobLds {
     uint32_t tc[MAXT][4];  // p, 2^32 mod p, its Shoup companion, floor(2^32 / p)
     double rb[MAX_REG_SRC];
     uint32_t bmod[MAXT];
-    uint32_t lazy[MAXT];   // 1: ns (max source prime - 1) (p_t - 1) < 2^64, the sum needs no carry count
     uint32_t sp[MAX_REG_SRC];  // the sources' primes
 };
 
@@ -120,28 +119,38 @@ __device__ __forceinline__ void stv(uint32_t* p, const uint32_t (&v)[V]) {
     else *(uint2*)p = make_uint2(v[0], v[1]);
 }
 
+// the V source words of each source at c0, as stored (zero past the job's sources)
 template <int V>
-__device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
-                                        const uint32_t* src, uint32_t* dst, uint32_t c0, int logn, int ntl) {
-    uint32_t y[MAX_REG_SRC * V];
+__device__ __forceinline__ void load_sources(const Pool& P, const uint32_t* src, uint32_t c0, int logn,
+                                             uint32_t (&y)[MAX_REG_SRC * V]) {
 #pragma unroll
     for (int i = 0; i < MAX_REG_SRC; ++i) {
-        if (i < P.ns) {
-            uint32_t v[V];
-            ldv<V>(src + ((size_t)P.src_row(i) << logn) + c0, v);
-            if (!j.prescaled) {
+        uint32_t v[V] = {};
+        if (i < P.ns) ldv<V>(src + ((size_t)P.src_row(i) << logn) + c0, v);
+#pragma unroll
+        for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
+    }
+}
+
+template <int V>
+__device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, const Pool& P, const JobLds& S,
+                                        uint32_t (&y)[MAX_REG_SRC * V], uint32_t* dst, uint32_t c0, int logn, int ntl) {
+    if (!j.prescaled) {
+#pragma unroll
+        for (int i = 0; i < MAX_REG_SRC; ++i) {
+            if (i < P.ns) {
                 const Red red(A.pr[P.src_prime(i)]);
                 const uint32_t pre = P.pre(i);
 #pragma unroll
-                for (int k = 0; k < V; ++k) v[k] = red.mul(v[k], pre);
+                for (int k = 0; k < V; ++k) y[i * V + k] = red.mul(y[i * V + k], pre);
             }
-#pragma unroll
-            for (int k = 0; k < V; ++k) y[i * V + k] = v[k];
-        } else {
-#pragma unroll
-            for (int k = 0; k < V; ++k) y[i * V + k] = 0;
         }
     }
+    // sources are reduced below their prime, M's entries below the target's: ns products of at most
+    // (max source prime - 1) (p_t - 1) each
+    uint32_t mx = 0;
+    for (int i = 0; i < P.ns; ++i) mx = max(mx, S.sp[i]);
+    const uint64_t lazy_bound = ~0ull / (uint64_t)P.ns;
     uint64_t u[V] = {};
     if (j.exact) {
 #pragma unroll
@@ -163,7 +172,7 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
         const Red red(S.tc[t][0], S.tc[t][1], S.tc[t][2], S.tc[t][3]);
         uint64_t acc[V] = {};
         uint32_t r[V];
-        if (S.lazy[t]) {
+        if ((uint64_t)(mx - 1) * (uint64_t)(red.p - 1) <= lazy_bound) {
             // every partial sum stays below 2^64: one multiply-add per product
 #pragma unroll
             for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
@@ -227,6 +236,9 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
     const uint32_t* src = (const uint32_t*)A.src + ((size_t)j.src_off << logn);
     uint32_t* dst = (uint32_t*)A.dst + ((size_t)j.dst_off << logn);
     if (P.ns <= MAX_REG_SRC && ntl <= MAXT) {
+        // the sources' loads first: their round trips (row ids, then words) overlap the tables' (ids, then primes)
+        uint32_t y[MAX_REG_SRC * V];
+        if (c0 < (1u << logn)) load_sources<V>(P, src, c0, logn, y);
         for (int e = threadIdx.x; e < ntl * MAX_REG_SRC; e += BX) {
             const int t = e / MAX_REG_SRC, i = e % MAX_REG_SRC;
             S.mt[t][i] = (t < ntl && i < P.ns) ? P.m(i, t0 + t) : 0;
@@ -248,16 +260,7 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             for (int t = threadIdx.x; t < ntl; t += BX) S.bmod[t] = bmod[t0 + t];
         }
         __syncthreads();
-        for (int t = threadIdx.x; t < ntl; t += BX) {
-            // sources are reduced below their prime, M's entries below the target's: ns products of at most
-            // (max source prime - 1) (p_t - 1) each
-            uint32_t mx = 0;
-            for (int i = 0; i < P.ns; ++i) mx = max(mx, S.sp[i]);
-            const uint64_t b = (uint64_t)(mx - 1) * (uint64_t)(S.tc[t][0] - 1);
-            S.lazy[t] = b <= ~0ull / (uint64_t)P.ns;
-        }
-        __syncthreads();
-        if (c0 < (1u << logn)) job_lds<V>(A, j, P, S, src, dst, c0, logn, ntl);
+        if (c0 < (1u << logn)) job_lds<V>(A, j, P, S, y, dst, c0, logn, ntl);
     } else if (c0 < (1u << logn)) {
         for (int k = 0; k < V; ++k) job_wide(A, j, P, src, dst, c0 + k, logn, t0, t0 + ntl);
     }

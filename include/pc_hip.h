@@ -827,6 +827,10 @@ size_t pcx_ctx_workspace_bytes(const pcx_ctx* c);
  * group's retry-value table unused); off: the driver's fused forms. Returns the previous setting, -1 on NULL. */
 int pcx_ctx_table_only(pcx_ctx* c, int on);
 
+/* No counterpart in the reference: a tuning switch. Launches of N = 2^16 with at least `rows` rows take the one-pass
+ * transform (one workgroup per row) instead of the two-pass one; 0 (the default, or PCX_NTT1_MIN) never. Returns the
+ * previous threshold. The words are the same either way. */
+int pcx_ntt_one_pass_min(int rows);
 /* Batched NTT of nrows rows of one buffer: row i at base + roff[i]*N (prime id ids[i]); host row tables are uploaded
  * into a device row list made once (crates/pc-gpu/src/ntt.rs:293-326 transform_rows over a RowList). dir: 1 forward,
  * -1 inverse (scaled by N^-1). */

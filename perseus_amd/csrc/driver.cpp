@@ -1128,6 +1128,8 @@ pcx_rows* pcx_rows_new(pcx_ctx* c, const uint32_t* roff, const int32_t* ids, int
 }
 void pcx_rows_free(pcx_rows* r) { delete r; }
 
+int pcx_ntt_one_pass_min(int rows) { return pch::ntt_one_pass_min(rows); }
+
 int pcx_ntt(pcx_ctx* c, int dir, void* base, const pcx_rows* rows, pc_stream_t s) {
     if (!c || !rows || (dir != 1 && dir != -1)) return -1;
     NttArgs a = ntt_args(c, base, rows->r, rows->r.n);

@@ -65,6 +65,8 @@ void ntt1_inv(const NttArgs& a, int r0, int n, pc_stream_t st);
 // The forward NTT of dense rows: row i of a at base + i N with prime id i mod a->xnum (a->roff, a->rprime unused), no
 // epilogue and no out-of-place source; the non-lazy butterflies (legal for every prime below 2^31)
 int ntt_fwd_dense(int logn, const NttArgs* a, pc_stream_t s);
+// the row count from which launches of N = 2^16 take the one-pass transform (0: never); returns the previous one
+int ntt_one_pass_min(int rows);
 
 // ks_dot_key's summed rotations (c0_mode | KS_SUM): out = sum_r sigma_r(dot_r), gathered in output order
 int ks_dot_key_sum(int logn, const KsKeyArgs* g, pc_stream_t s);

@@ -296,6 +296,139 @@ __device__ __forceinline__ void a_to_b(uint32_t (&x)[E], uint32_t* l, int tau) {
     wave_sync();
 }
 
+// ------------------------------------------------------------------------------------------------ row pass, C = 256
+// A 256-word block held by its 16 threads t in one of two layouts:
+//  D: register 4 k + m holds word e = 64 k + 4 t + m (k, m < 4). For each k the block's 16 threads read or write 256
+//     contiguous bytes with one 16-byte access each, so every global access of the pass moves whole cache lines (the
+//     B layout's 64 contiguous bytes per thread put each 16-byte access of a wave on a different line: four times
+//     the requests for the same bytes);
+//  E: thread t = 4 k + m, register j holds word e = 64 k + 4 j + m.
+// Stages h = 128, 64 (word bits 7, 6 = k) and h = 2, 1 (bits 1, 0 = m) run in D, h = 32 .. 4 (bits 5..2 = j) in E. The
+// transposes D <-> E go through the block's LDS with one padding word per 16: both sides conflict-free.
+__device__ __forceinline__ uint32_t dpos(uint32_t e) { return e + (e >> 4); }
+__device__ __forceinline__ void ld_d(const uint32_t* q, uint32_t (&v)[E]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint4 a = *(const uint4*)(q + 64 * k);
+        v[4 * k] = a.x, v[4 * k + 1] = a.y, v[4 * k + 2] = a.z, v[4 * k + 3] = a.w;
+    }
+}
+__device__ __forceinline__ void st_d(uint32_t* q, const uint32_t (&v)[E]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) *(uint4*)(q + 64 * k) = make_uint4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+}
+__device__ __forceinline__ void d_to_e(uint32_t (&x)[E], uint32_t* l, int t) {
+#pragma unroll
+    for (int r = 0; r < E; ++r) l[dpos(64 * (r >> 2) + 4 * t + (r & 3))] = x[r];
+    wave_sync();
+    const int k = t >> 2, m = t & 3;
+#pragma unroll
+    for (int j = 0; j < E; ++j) x[j] = l[dpos(64 * k + 4 * j + m)];
+    wave_sync();
+}
+__device__ __forceinline__ void e_to_d(uint32_t (&x)[E], uint32_t* l, int t) {
+    const int k = t >> 2, m = t & 3;
+#pragma unroll
+    for (int j = 0; j < E; ++j) l[dpos(64 * k + 4 * j + m)] = x[j];
+    wave_sync();
+#pragma unroll
+    for (int r = 0; r < E; ++r) x[r] = l[dpos(64 * (r >> 2) + 4 * t + (r & 3))];
+    wave_sync();
+}
+// the E layout's twiddles of stages h = 4 2^K (K = 3..0): NG = 8 >> K consecutive entries from base(h) + k NG, stage
+// K's at offset NG - 1 (the phase_a_t order)
+template <class Base>
+__device__ __forceinline__ void load_tw_e(Tw& tw, const uint32_t* w, const uint32_t* ws, Base base, int k) {
+#define PCH_LE(K)                                                                      \
+    {                                                                                  \
+        const uint32_t b0 = base(4 << K) + (uint32_t)k * (8 >> K);                     \
+        ldtw_at<(8 >> K)>(w + b0, tw.w + ((8 >> K) - 1));                              \
+        ldtw_at<(8 >> K)>(ws + b0, tw.s + ((8 >> K) - 1));                             \
+    }
+    PCH_LE(3) PCH_LE(2) PCH_LE(1) PCH_LE(0)
+#undef PCH_LE
+}
+// stages h = 128 then 64 (FWD) or 64 then 128 in the D layout: h = 128 pairs registers (r, r + 8), r < 8, one twiddle
+// base(128); h = 64 pairs (r, r + 4) for k in {0, 2}, twiddle base(64) + k / 2
+template <bool FWD, bool H, class Base>
+__device__ __forceinline__ void stages_hi_d(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, Base base,
+                                            uint32_t p, uint32_t p2) {
+    const uint32_t a0 = w[base(128)], s0 = ws[base(128)];
+    const uint2 a1 = *(const uint2*)(w + base(64)), s1 = *(const uint2*)(ws + base(64));
+    auto h128 = [&] {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            if (FWD) ct<H>(x[r], x[r + 8], a0, s0, p, p2);
+            else gs<H>(x[r], x[r + 8], a0, s0, p, p2);
+        }
+    };
+    auto h64 = [&] {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (FWD) {
+                ct<H>(x[r], x[r + 4], a1.x, s1.x, p, p2);
+                ct<H>(x[r + 8], x[r + 12], a1.y, s1.y, p, p2);
+            } else {
+                gs<H>(x[r], x[r + 4], a1.x, s1.x, p, p2);
+                gs<H>(x[r + 8], x[r + 12], a1.y, s1.y, p, p2);
+            }
+        }
+    };
+    if (FWD) {
+        h128();
+        h64();
+    } else {
+        h64();
+        h128();
+    }
+}
+// stages h = 2 then 1 (FWD) or 1 then 2 in the D layout: h = 2 pairs (4k + m, 4k + m + 2), m < 2, twiddle
+// base(2) + 16 k + t; h = 1 pairs (4k + m, 4k + m + 1), m in {0, 2}, twiddle base(1) + 32 k + 2 t + m / 2
+template <bool FWD, bool H, class Base>
+__device__ __forceinline__ void stages_lo_d(uint32_t (&x)[E], const uint32_t* w, const uint32_t* ws, Base base, int t,
+                                            uint32_t p, uint32_t p2) {
+    uint32_t a2[4], s2[4];
+    uint2 a1[4], s1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        a2[k] = w[base(2) + 16 * k + t];
+        s2[k] = ws[base(2) + 16 * k + t];
+        a1[k] = *(const uint2*)(w + base(1) + 32 * k + 2 * t);
+        s1[k] = *(const uint2*)(ws + base(1) + 32 * k + 2 * t);
+    }
+    auto h2 = [&] {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (FWD) {
+                ct<H>(x[4 * k], x[4 * k + 2], a2[k], s2[k], p, p2);
+                ct<H>(x[4 * k + 1], x[4 * k + 3], a2[k], s2[k], p, p2);
+            } else {
+                gs<H>(x[4 * k], x[4 * k + 2], a2[k], s2[k], p, p2);
+                gs<H>(x[4 * k + 1], x[4 * k + 3], a2[k], s2[k], p, p2);
+            }
+        }
+    };
+    auto h1 = [&] {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (FWD) {
+                ct<H>(x[4 * k], x[4 * k + 1], a1[k].x, s1[k].x, p, p2);
+                ct<H>(x[4 * k + 2], x[4 * k + 3], a1[k].y, s1[k].y, p, p2);
+            } else {
+                gs<H>(x[4 * k], x[4 * k + 1], a1[k].x, s1[k].x, p, p2);
+                gs<H>(x[4 * k + 2], x[4 * k + 3], a1[k].y, s1[k].y, p, p2);
+            }
+        }
+    };
+    if (FWD) {
+        h2();
+        h1();
+    } else {
+        h1();
+        h2();
+    }
+}
+
 // Row i's prime id and offset (in rows of N words). Dense launches (roff and rprime both null; internal launchers
 // only, the table entries reject them) take row i at i N with prime id i mod xnum.
 __device__ __forceinline__ int row_prime(const NttArgs& A, int i) { return A.rprime ? A.rprime[i] : i % A.xnum; }
@@ -322,6 +455,17 @@ __device__ __forceinline__ void ld16_src(const RowSrc& s, size_t off, uint32_t p
     for (int k = 1; k < s.n; ++k) {
         uint32_t y[E];
         ld16(s.p0 + off + k * s.stride, y);
+#pragma unroll
+        for (int j = 0; j < E; ++j) x[j] = addm(x[j], y[j], p);
+    }
+}
+
+// ld16_src in the D layout: the words of registers 4k + m at off + 64 k + m, summed over the source's rows
+__device__ __forceinline__ void ld_d_src(const RowSrc& s, size_t off, uint32_t p, uint32_t (&x)[E]) {
+    ld_d(s.p0 + off, x);
+    for (int k = 1; k < s.n; ++k) {
+        uint32_t y[E];
+        ld_d(s.p0 + off + k * s.stride, y);
 #pragma unroll
         for (int j = 0; j < E; ++j) x[j] = addm(x[j], y[j], p);
     }

@@ -18,6 +18,12 @@ def device_count():
     return n.value if rc == 0 else 0
 
 
+def ntt_one_pass_min(rows):
+    """Launches of N = 2^16 with at least `rows` rows take the one-pass transform (0: never); returns the previous
+    threshold (pcx_ntt_one_pass_min)."""
+    return int(LIB.pcx_ntt_one_pass_min(int(rows)))
+
+
 class Stream:
     def __init__(self):
         self.h = C.c_void_p()

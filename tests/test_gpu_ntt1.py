@@ -1,4 +1,5 @@
-"""The one-pass transforms of N = 2^16 (one workgroup per row, taken by launches of 1024 rows or more) through the
+"""The one-pass transforms of N = 2^16 (one workgroup per row, taken by launches of 1024 rows or more once
+pcx_ntt_one_pass_min turns them on) through the
 table's ntt_fwd / ntt_inv entries: bit-exact against the oracle's transforms and against the two-pass transforms of
 the same launch split into chunks of 128 rows (NttArgs.chunk), with 30-bit (lazy) and 31-bit primes, rows addressed
 out of order, the forward epilogues 1-3, summed out-of-place sources and per-row inverse scales. Each test prints its
@@ -27,7 +28,10 @@ def say(*a):
 @pytest.fixture(scope="module")
 def stream():
     assert pa.device_count() >= 1, "no GPU visible"
-    return pa.Stream()
+    # the one-pass transform is off by default: this module turns it on from NR rows, and back off at its end
+    prev = pa.ntt_one_pass_min(NR)
+    yield pa.Stream()
+    pa.ntt_one_pass_min(prev)
 
 
 _CTX = {}

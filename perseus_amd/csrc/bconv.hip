@@ -275,12 +275,16 @@ template <int LOGN>
 int launch(const BconvArgs* a, pc_stream_t s) {
     if (int rc = check(a)) return rc;
     if (a->njobs == 0) return 0;
-    // target groups: every job's targets fit max_tgt (the plan's widest job; 0: one group). Two coefficients per thread
-    // and 8 targets per group measured best overall on the bootstrap's ModUps and ModDowns (tops 16 to 46, 16 special
-    // primes) against 4 coefficients or 16 to 64 targets.
+    // target groups: every job's targets fit max_tgt (the plan's widest job; 0: one group). Each group re-reads the
+    // job's sources, so a launch splits its targets only as far as it needs workgroups: about 2048 in all, with at
+    // least TPG targets per group (two coefficients per thread and 8 targets per group measured best on the
+    // bootstrap's one-ciphertext ModUps and ModDowns against 4 coefficients or 16 to 64 targets; a ModDown of 7
+    // ciphertexts then takes 2 groups instead of 6).
     constexpr int V = 2;
     const int gx = ((1 << LOGN) + BX * V - 1) / (BX * V);
-    const int gz = a->max_tgt > TPG ? std::min((a->max_tgt + TPG - 1) / TPG, 256) : 1;
+    const int gmax = a->max_tgt > TPG ? std::min((a->max_tgt + TPG - 1) / TPG, 256) : 1;
+    const long base = (long)gx * a->njobs;
+    const int gz = (int)std::max(1L, std::min((long)gmax, (2048 + base - 1) / base));
     hipLaunchKernelGGL(bconv_k<V>, dim3(gx, a->njobs, gz), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
     return launch_rc();
 }

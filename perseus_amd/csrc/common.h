@@ -188,8 +188,15 @@ __device__ __forceinline__ void st16(uint32_t* p, const uint32_t (&v)[16]) {
 // accesses past `bytes` read 0 and write nothing.
 struct Buf {
     __amdgpu_buffer_rsrc_t r;
+    // the base must be the same in every lane (a row of the workgroup); read through the first lane, so the compiler
+    // keeps the resource in scalar registers instead of looping over lanes
+    __device__ __forceinline__ static void* uniform(const void* p) {
+        const uint64_t v = (uint64_t)p;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+        return (void*)(((uint64_t)hi << 32) | lo);
+    }
     __device__ __forceinline__ Buf(const void* base, uint32_t bytes)
-        : r(__builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, 0x00020000)) {}
+        : r(__builtin_amdgcn_make_buffer_rsrc(uniform(base), 0, (int)bytes, 0x00020000)) {}
     __device__ __forceinline__ uint32_t ld(uint32_t voff, uint32_t soff) const {
         return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
     }

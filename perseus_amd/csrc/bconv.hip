@@ -2,9 +2,9 @@
 //   y_i = x_i pre_i mod s_i (prescaled jobs: y_i = x_i as stored), out_t = sum_i y_i M[i][t] mod t;
 //   exact jobs: v = sum_i y_i rb_i (double FMA in source order), u = floor(v + 0.5) (centred: the lift's mean),
 //   out_t -= u (B mod t).
-// One launch for every job of a plan: grid (N / 512, njobs, target groups), 256 threads of 2 consecutive
-// coefficients; the job's targets are split over ceil(max_tgt / TPG) groups (each re-reads the job's sources, from
-// L2), so that a few wide jobs still put several waves on every SIMD.
+// One launch for every job of a plan: grid (N / (256 V), njobs, target groups), 256 threads of V consecutive
+// coefficients (V = 1); the job's targets are split over up to ceil(max_tgt / TPG) groups (each re-reads the job's
+// sources, from L2), so that a few wide jobs still put several waves on every SIMD.
 //
 // 31-bit primes break the reference's lazy bound nsrc (p - 1)^2 < 2^64 past 4 sources, so the sum of products is
 // carried in 96 bits (a 64-bit sum and a count of its wraps) and reduced once: the exact integer formula, whatever
@@ -105,7 +105,9 @@ struct JobLds {
 // V consecutive words at p (V = 2 or 4: one 8- or 16-byte access)
 template <int V>
 __device__ __forceinline__ void ldv(const uint32_t* p, uint32_t (&v)[V]) {
-    if constexpr (V == 4) {
+    if constexpr (V == 1) {
+        v[0] = *p;
+    } else if constexpr (V == 4) {
         const uint4 x = *(const uint4*)p;
         v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
     } else {
@@ -115,7 +117,8 @@ __device__ __forceinline__ void ldv(const uint32_t* p, uint32_t (&v)[V]) {
 }
 template <int V>
 __device__ __forceinline__ void stv(uint32_t* p, const uint32_t (&v)[V]) {
-    if constexpr (V == 4) *(uint4*)p = make_uint4(v[0], v[1], v[2], v[3]);
+    if constexpr (V == 1) *p = v[0];
+    else if constexpr (V == 4) *(uint4*)p = make_uint4(v[0], v[1], v[2], v[3]);
     else *(uint2*)p = make_uint2(v[0], v[1]);
 }
 
@@ -277,10 +280,10 @@ int launch(const BconvArgs* a, pc_stream_t s) {
     if (a->njobs == 0) return 0;
     // target groups: every job's targets fit max_tgt (the plan's widest job; 0: one group). Each group re-reads the
     // job's sources, so a launch splits its targets only as far as it needs workgroups: about 2048 in all, with at
-    // least TPG targets per group (two coefficients per thread and 8 targets per group measured best on the
-    // bootstrap's one-ciphertext ModUps and ModDowns against 4 coefficients or 16 to 64 targets; a ModDown of 7
-    // ciphertexts then takes 2 groups instead of 6).
-    constexpr int V = 2;
+    // least TPG targets per group (a ModDown of 7 ciphertexts takes 2 groups instead of 6). One coefficient per thread
+    // measured best on the bootstrap (14.97 ms against 15.25 at two, same box; 4 coefficients, 4 or 16 to 64 targets
+    // per group and 4096 workgroups were no better) and equal on the C3 batch.
+    constexpr int V = 1;
     const int gx = ((1 << LOGN) + BX * V - 1) / (BX * V);
     const int gmax = a->max_tgt > TPG ? std::min((a->max_tgt + TPG - 1) / TPG, 256) : 1;
     const long base = (long)gx * a->njobs;

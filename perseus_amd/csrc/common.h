@@ -192,7 +192,8 @@ struct Buf {
     // keeps the resource in scalar registers instead of looping over lanes
     __device__ __forceinline__ static void* uniform(const void* p) {
         const uint64_t v = (uint64_t)p;
-        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
         return (void*)(((uint64_t)hi << 32) | lo);
     }
     __device__ __forceinline__ Buf(const void* base, uint32_t bytes)

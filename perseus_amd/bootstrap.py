@@ -286,6 +286,31 @@ def encode_rows(z, N, scale, primes):
     return residues(encode(z, N, scale), primes)
 
 
+def compact_shift(rows, cap=12):
+    """The largest s <= cap with every nonzero coefficient of the residue rows at an index divisible by 2^s
+    (crates/pc-gpu/src/bts/cts.rs:277-289). Such a polynomial is one in X^(2^s): its evaluation rows, in the
+    transforms' bit-reversed order, are constant on aligned blocks of 2^s words, so a diagonal is kept at width
+    N / 2^s and read at index i >> s."""
+    nz = np.flatnonzero(np.any(np.asarray(rows) != 0, axis=0))
+    if nz.size == 0:
+        return cap
+    g = int(np.bitwise_or.reduce(nz))
+    return cap if g == 0 else min(cap, (g & -g).bit_length() - 1)
+
+
+def compact_rows(rows, s):
+    """evaluation rows [n][N] constant on aligned blocks of 2^s words -> their [n][N >> s] block values; raises if a
+    block is not constant"""
+    rows = np.asarray(rows)
+    if s == 0:
+        return rows
+    n, N = rows.shape
+    blk = rows.reshape(n, N >> s, 1 << s)
+    if not (blk == blk[:, :, :1]).all():
+        raise ValueError(f"evaluation rows not constant on blocks of 2^{s} words")
+    return np.ascontiguousarray(blk[:, :, 0])
+
+
 def int_rows(k, primes):
     """An integer constant (any size, any sign) as residues per prime (Python ints)."""
     return [int(k) % int(p) for p in primes]
@@ -446,23 +471,29 @@ class Bootstrap:
     def prepare(self):
         """encode every level's diagonals (at the level's input top, scale q_a q_b f) and the i monomial"""
         ops, N = self.ops, self.par.N
-        self.pts = []
+        self.pts, self.pt_s = [], []
         top = self.T
         for plans, f in ((self.cts, self.cts_f), (self.stc, 1.0)):
             for p in plans:
                 sc = self.ev.qq(top) * f
                 prim = self.q[: top + 1] + (self.p or [])
+                coef = [[None if d is None else encode_rows(d, N, sc, prim) for d in p.pts[j]] for j in range(p.G)]
+                # the plaintext dot reads a level's diagonals at one compact width (the fused stage at full width)
+                s = 0
+                if self.p is None:
+                    s = min((compact_shift(c) for r in coef for c in r if c is not None), default=0)
                 row = []
                 for j in range(p.G):
                     for i in range(p.B):
-                        d = p.pts[j][i]
-                        if d is None:
+                        c = coef[j][i]
+                        if c is None:
                             row.append(None)
                         elif self.p is None:
-                            row.append(ops.plaintext(encode_rows(d, N, sc, prim), top))
+                            row.append(ops.plaintext(c, top, s))
                         else:
-                            row.append(ops.plaintext_ext(encode_rows(d, N, sc, prim), top))
+                            row.append(ops.plaintext_ext(c, top))
                 self.pts.append(row)
+                self.pt_s.append(s)
                 top -= 2
                 if plans is self.cts and p is self.cts[-1]:
                     top -= 2 * (7 + self.par.r)
@@ -473,7 +504,8 @@ class Bootstrap:
         mono_m[:, N // 2] = [p - 1 for p in self.q]  # -X^(N/2): -i
         self.mono_mi = ops.plaintext(mono_m, self.T)
 
-    def lt(self, x, plan, pts, f):
+    def lt(self, x, plan, pts, f, s=0):
+        """one BSGS level: pts its diagonals (None where zero), s their compact shift (rows of width N >> s)"""
         ops, top = self.ops, x.top
         B, G = plan.B, plan.G
         res = ops.alloc(G)
@@ -481,7 +513,7 @@ class Bootstrap:
             rots = ops.alloc(B)
             ops.copy(ops.item(rots, 0), x.h, top)
             ops.hoisted(ops.item(rots, 1), x.h, top, [b % self.par.n for b in plan.baby[1:]])
-            ops.pt_dot(res, rots, top, pts, B, G)
+            ops.pt_dot(res, rots, top, pts, B, G, s)
         else:
             ops.cts(res, x.h, top, pts, B, G)
         # the giant steps: the rotated results' key dots summed in the extended basis, one ModDown onto the
@@ -535,7 +567,7 @@ class Bootstrap:
         x = Ct(raised, self.T, self.raise_scale)
         k = 0
         for p in self.cts:
-            x = self.lt(x, p, self.pts[k], self.cts_f)
+            x = self.lt(x, p, self.pts[k], self.cts_f, self.pt_s[k])
             k += 1
         cj = ops.alloc()
         ops.rotate(cj, x.h, x.top, "conj")
@@ -557,7 +589,7 @@ class Bootstrap:
         ops.mul_pt(ii, im.h, im.top, self.mono_i)
         w = ev.add(re, Ct(ii, im.top, im.scale))
         for p in self.stc:
-            w = self.lt(w, p, self.pts[k], 1.0)
+            w = self.lt(w, p, self.pts[k], 1.0, self.pt_s[k])
             k += 1
         # the slot values are now (2 pi / q0) times the message's at the input's scale: relabel
         w.scale = w.scale * 2.0 * math.pi * par.delta_in / self.q0
@@ -719,11 +751,14 @@ class GpuOps:
             self.cache[key] = self.eng.Rows(self.ctx, roff, ids)
         return self.cache[key]
 
-    def plaintext(self, coef_rows, top):
-        """coefficient residue rows 0..top -> a device plaintext [top + 1][N] in evaluation form"""
+    def plaintext(self, coef_rows, top, s=0):
+        """coefficient residue rows 0..top -> a device plaintext [top + 1][N] in evaluation form; with s > 0 (a
+        polynomial in X^(2^s)) its compact form [top + 1][N >> s], one word per block of 2^s equal ones"""
         buf = self.eng.DevBuf.from_array(np.ascontiguousarray(coef_rows[: top + 1], np.uint32))
         self._rows(list(range(top + 1)), list(range(top + 1))).ntt(buf, 1, self.st)
         self.st.sync()
+        if s:
+            buf = self.eng.DevBuf.from_array(compact_rows(buf.download((top + 1, self.N), self.st), s))
         return buf
 
     def plaintext_ext(self, coef_rows, top):
@@ -755,7 +790,7 @@ class GpuOps:
     def moddown(self, out, ext, top):
         self.ctx.moddown(ext, top, out, self.st)
 
-    def pt_dot(self, res, rots, top, pts, B, G):
+    def pt_dot(self, res, rots, top, pts, B, G, s=0):
         key = ("ptr", tuple(id(p) for p in pts))
         if key not in self.cache:
             if any(p is None for p in pts) and self.zero_pt is None:
@@ -769,7 +804,9 @@ class GpuOps:
         a.rot_stride, a.res_stride = self.cw, self.cw
         a.pts, a.pr = self.cache[key].ptr.value, self.pr
         a.rs = self.abi.RowSet(top + 1, 0, self.nq, 0)
-        a.npts, a.bstep, a.gstep, a.K, a.ptw, a.pt_prow, a.enc = B * G, B, G, 1, self.N, top + 1, 0xFFFFFFFF
+        a.npts, a.bstep, a.gstep, a.K, a.pt_prow = B * G, B, G, 1, top + 1
+        # compact diagonals: word i of a row read at i >> s (a zero diagonal reads the full-width zero rows)
+        a.ptw, a.enc = self.N >> s, (0x7F000000 | s) if s else 0xFFFFFFFF
         self._call("pt_dot", a)
 
     # -- key switches

@@ -40,6 +40,18 @@ struct Acc {
     }
     __device__ __forceinline__ uint32_t red(const Red& r) const { return r.red96(lo, hi); }
 };
+// The same sum in two instructions per product: the 64-bit product-sum a b + lo, then its carry-out added into hi
+struct Acc2 {
+    uint64_t lo = 0;
+    uint32_t hi = 0;
+    __device__ __forceinline__ void mad(uint32_t a, uint32_t b) {
+        uint64_t s, c, c2;
+        asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=v"(s), "=s"(c) : "v"(a), "v"(b), "v"(lo));
+        asm("v_addc_co_u32 %0, %1, %2, 0, %3" : "=v"(hi), "=s"(c2) : "v"(hi), "s"(c));
+        lo = s;
+    }
+    __device__ __forceinline__ uint32_t red(const Red& r) const { return r.red96(lo, hi); }
+};
 
 // ------------------------------------------------------------------------------------------------ tensor
 // (c0, c1, d2) = sum_j (a_j0 b_j0, a_j0 b_j1 + a_j1 b_j0, a_j1 b_j1) over the pairs (the operands of pair j: A[j], B[j])
@@ -290,7 +302,92 @@ __global__ void __launch_bounds__(BX) submul_many_k(SubMulManyArgs A, int logn) 
 // res[c][j] = sum_{b < bstep} rot[c][b] pt_{bstep j + b}[prow][ptidx(i, enc)] on the row set's rows (args.cuh:184-198;
 // elem.cuh:83-118): rotations and results by PolyRef plus the per-rotation / per-result strides, diagonals >= npts
 // skipped; prow = y on Q rows, pt_prow + (y - nq) on special rows. 4 consecutive slots per thread, one ciphertext at a
-// time (the diagonals' words come again from L2), the sums exact.
+// time, the sums exact.
+//
+// The register form (bstep <= BM): a thread's words of the bstep rotations stay in registers across the giant steps,
+// so each rotation word is read from HBM once (re-reading them per giant step cost bstep x 2 rows per giant step), and
+// each giant step issues all its diagonal loads before the first product. The diagonal pointers are loaded through the
+// scalar cache and the words as global (not flat) loads, so no wait on one serialises the others. MODE 0: full-width
+// diagonals (words i .. i + 3 in one 16-byte load); 1: compact by a shift s >= 2 (the thread's 4 words share one
+// diagonal word); 2: any other index form (a load per word).
+template <int BM, int MODE>
+__global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
+    typedef const __attribute__((address_space(4))) uint64_t* ConstTab;
+    typedef const __attribute__((address_space(1))) uint32_t* GPtr;
+    typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+    const int y = blockIdx.y;
+    const int row = y < A.rs.nq ? y : A.rs.qmax + (y - A.rs.nq);
+    const int prow = y < A.rs.nq ? y : A.pt_prow + (y - A.rs.nq);
+    const Red red(A.pr[row]);
+    const uint32_t i = lane_word();
+    uint32_t pi[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pi[w] = ptidx(i + w, A.enc);
+    const size_t roff = ((size_t)row << logn) + i;
+    // the rotations read: b < bstep and b < npts (npts >= 1); the loads past them re-read rotation 0, never used
+    const int nb = min(A.bstep, A.npts);
+    const ConstTab tab = (ConstTab)A.pts;
+    for (int c = 0; c < A.K; ++c) {
+        W4 x0[BM], x1[BM];
+#pragma unroll
+        for (int b = 0; b < BM; ++b) {
+            const uint32_t* r =
+                (const uint32_t*)A.rot.base + c * A.rot.ct_stride + (b < nb ? b : 0) * A.rot_stride + roff;
+            x0[b] = ld4(r);
+            x1[b] = ld4(r + A.rot.part_stride);
+        }
+        for (int j = 0; j < A.gstep; ++j) {
+            // a missing diagonal (b >= nb or d >= npts) reads diagonal 0 and weighs 0
+            uint64_t pp[BM];
+#pragma unroll
+            for (int b = 0; b < BM; ++b) {
+                const int d = A.bstep * j + b;
+                pp[b] = tab[b < nb && d < A.npts ? d : 0];
+            }
+            W4 pw[BM];
+#pragma unroll
+            for (int b = 0; b < BM; ++b) {
+                const int d = A.bstep * j + b;
+                const bool ok = b < nb && d < A.npts;
+                const GPtr pt = (GPtr)pp[b] + (size_t)prow * A.ptw;
+                if constexpr (MODE == 0) {
+                    const U4 u = *(const __attribute__((address_space(1))) U4*)(pt + i);
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) pw[b].v[w] = u[w];
+                } else if constexpr (MODE == 1) {
+                    const uint32_t v = pt[pi[0]];
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) pw[b].v[w] = v;
+                } else {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) pw[b].v[w] = pt[pi[w]];
+                }
+#pragma unroll
+                for (int w = 0; w < 4; ++w) pw[b].v[w] = ok ? pw[b].v[w] : 0u;
+            }
+            Acc2 s0[4], s1[4];
+#pragma unroll
+            for (int b = 0; b < BM; ++b) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    s0[w].mad(x0[b].v[w], pw[b].v[w]);
+                    s1[w].mad(x1[b].v[w], pw[b].v[w]);
+                }
+            }
+            W4 r0, r1;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                r0.v[w] = s0[w].red(red);
+                r1.v[w] = s1[w].red(red);
+            }
+            uint32_t* o = (uint32_t*)A.res.base + c * A.res.ct_stride + j * A.res_stride + roff;
+            st4(o, r0);
+            st4(o + A.res.part_stride, r1);
+        }
+    }
+}
+
+// more baby steps, or no diagonals: the rotations re-read per giant step
 __global__ void __launch_bounds__(BX) pt_dot_k(PtDotArgs A, int logn) {
     const int y = blockIdx.y;
     const int row = y < A.rs.nq ? y : A.rs.qmax + (y - A.rs.nq);
@@ -332,7 +429,8 @@ __global__ void __launch_bounds__(BX) pt_dot_k(PtDotArgs A, int logn) {
 
 // ------------------------------------------------------------------------------------------------ launchers
 // The reference's launchers check only the counts below (em.cuh:580-692); these also refuse null operands that the
-// kernel would read (-1) and return 0 without a launch when there is no work.
+// kernel would read (-1), pt_dot's diagonal indices outside its rows of ptw words (-1), and return 0 without a launch
+// when there is no work.
 template <int LOGN>
 dim3 grid(int rows, int z) {
     return dim3((1u << LOGN) / (BX * 4), (unsigned)rows, (unsigned)z);
@@ -618,6 +716,28 @@ int pt_dot(const PtDotArgs* a, pc_stream_t s) {
     if (!a->rot.base || !a->res.base || !a->pts || !a->pr || a->K < 0 || a->bstep < 0 || a->gstep < 0) return -1;
     const int rows = a->rs.nq + a->rs.np;
     if (rows <= 0 || a->K == 0 || a->gstep == 0) return 0;
+    // every diagonal index inside the row of ptw words
+    const uint32_t n = 1u << LOGN;
+    if (a->ptw < 1 || (a->enc == 0xFFFFFFFFu ? (uint32_t)a->ptw < n
+                       : (a->enc >> 24) == 0x7Fu ? (a->enc & 0xFFu) > 31 || (uint32_t)a->ptw < (n >> (a->enc & 0xFFu))
+                                                 : (uint64_t)a->ptw <= ((n - 1) & a->enc)))
+        return -1;
+    // up to 8 baby steps: the register form; its diagonal loads by index form (full rows of whole 16-byte groups,
+    // compact by a shift of at least 2, anything else)
+    if (a->bstep >= 1 && a->bstep <= 8 && a->npts >= 1) {
+        const int mode = a->enc == 0xFFFFFFFFu && (a->ptw & 3) == 0                ? 0
+                         : (a->enc >> 24) == 0x7Fu && (a->enc & 0xFFu) >= 2 ? 1
+                                                                              : 2;
+        const dim3 g = grid<LOGN>(rows, 1);
+        if (a->bstep <= 4) {
+            if (mode == 0) PCH_LAUNCH((pt_dot_reg_k<4, 0>), g, *a, LOGN);
+            if (mode == 1) PCH_LAUNCH((pt_dot_reg_k<4, 1>), g, *a, LOGN);
+            PCH_LAUNCH((pt_dot_reg_k<4, 2>), g, *a, LOGN);
+        }
+        if (mode == 0) PCH_LAUNCH((pt_dot_reg_k<8, 0>), g, *a, LOGN);
+        if (mode == 1) PCH_LAUNCH((pt_dot_reg_k<8, 1>), g, *a, LOGN);
+        PCH_LAUNCH((pt_dot_reg_k<8, 2>), g, *a, LOGN);
+    }
     PCH_LAUNCH(pt_dot_k, grid<LOGN>(rows, 1), *a, LOGN);
 }
 #undef PCH_LAUNCH

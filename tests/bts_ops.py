@@ -8,6 +8,7 @@ import numpy as np
 from oracle import bts as ob
 from oracle import em
 from perseus_amd import bts
+from perseus_amd.bootstrap import compact_rows
 
 
 class OracleOps:
@@ -68,9 +69,9 @@ class OracleOps:
         self.get(out)[:, : top + 1] = (self.get(x)[:, : top + 1].astype(np.uint64) *
                                        pt[None, : top + 1].astype(np.uint64) % self._qq(top)).astype(np.uint32)
 
-    def plaintext(self, coef_rows, top):
+    def plaintext(self, coef_rows, top, s=0):
         ids = list(range(top + 1))
-        return self.oc.ntt_fwd(np.ascontiguousarray(coef_rows[: top + 1], np.uint32).copy(), ids)
+        return compact_rows(self.oc.ntt_fwd(np.ascontiguousarray(coef_rows[: top + 1], np.uint32).copy(), ids), s)
 
     def plaintext_ext(self, coef_rows, top):
         kp = self.R - len(self.q)
@@ -91,11 +92,12 @@ class OracleOps:
     def moddown(self, out, ext, top):
         self.get(out)[:] = self.oc.moddown(self.get(ext).copy(), top)
 
-    def pt_dot(self, res, rots, top, pts, B, G):
-        zero = np.zeros((top + 1, self.N), np.uint32)
+    def pt_dot(self, res, rots, top, pts, B, G, s=0):
+        zero = np.zeros((top + 1, self.N >> s), np.uint32)
         full = [zero if p is None else p for p in pts]
         rot = rots[0][rots[1]: rots[1] + B][None, :, :, : top + 1]
-        out = em.pt_dot(self.q[: top + 1], rot, full, B, G, B * G, 0xFFFFFFFF, list(range(top + 1)))
+        enc = (0x7F000000 | s) if s else 0xFFFFFFFF
+        out = em.pt_dot(self.q[: top + 1], rot, full, B, G, B * G, enc, list(range(top + 1)))
         res[0][res[1]: res[1] + G, :, : top + 1] = out[0]
 
     def rotate(self, out, x, top, step):

@@ -170,6 +170,15 @@ def test_em_launchers_reject_out_of_range_arguments():
     assert abi.call("wsum", w, log_n=12) == -1                              # more than 8 sources
     t = abi.TensorArgs()
     assert abi.call("tensor", t, log_n=12) == -1                            # null outputs
+    # pt_dot: diagonal indices outside the rows of ptw words (fake, never dereferenced operand addresses)
+    for enc, ptw in ((0xFFFFFFFF, 4095), (0x7F000004, 255), (0x3FF, 1023), (0x7F000020, 1 << 12), (0xFFFFFFFF, 0)):
+        p = abi.PtDotArgs()
+        p.rot = abi.PolyRef(64, 0, 0)
+        p.res = abi.PolyRef(64, 0, 0)
+        p.pts, p.pr = 64, 64
+        p.rs = abi.RowSet(1, 0, 1, 0)
+        p.npts, p.bstep, p.gstep, p.K, p.ptw, p.enc = 1, 1, 1, 1, ptw, enc
+        assert abi.call("pt_dot", p, log_n=12) == -1
 
 
 def test_raise_launchers_reject_out_of_range_arguments():

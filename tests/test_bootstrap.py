@@ -152,3 +152,35 @@ def test_bootstrap_on_the_oracle(fused):
     err = np.abs(got - ref).max()
     print(f"bootstrap error vs the input's decryption: {err:.3g} (vs the plaintext: {np.abs(got - z).max():.3g})")
     assert err < 1e-3
+
+
+def test_compact_diagonals():
+    """A polynomial in X^(2^s) has evaluation rows constant on aligned blocks of 2^s words (the transforms'
+    bit-reversed order: slot i evaluates at psi^(2 brev(i) + 1), and the low s bits of i only move that exponent by
+    multiples of 2N / 2^s after the power 2^s), so the plaintext dot on its compact rows at index i >> s gives the
+    full rows' words; one odd coefficient makes the shift 0 and the rows no longer compact."""
+    from oracle import em
+
+    logn, N = 10, 1 << 10
+    q = [int(p) for p in twin.descending_primes(30, 2 << logn, 3)]
+    oc = twin.Ctx(logn, q, [int(p) for p in twin.descending_primes(31, 2 << logn, 1)], 1)
+    rng = np.random.default_rng(3)
+    for s in (0, 1, 4, 7):
+        coef = np.zeros((3, N), np.uint32)
+        coef[:, :: 1 << s] = rng.integers(0, 1 << 20, (1, N >> s))
+        coef %= np.array(q, np.uint32)[:, None]
+        assert B.compact_shift(coef) == s
+        ev = oc.ntt_fwd(coef.copy(), [0, 1, 2])
+        c = B.compact_rows(ev, s)
+        assert c.shape == (3, N >> s)
+        assert (np.repeat(c, 1 << s, axis=1) == ev).all()
+        rot = rng.integers(0, q[-1], (1, 2, 2, 3, N)).astype(np.uint32)
+        full = em.pt_dot(q, rot, [ev, ev], 2, 1, 2, 0xFFFFFFFF, [0, 1, 2])
+        enc = (0x7F000000 | s) if s else 0xFFFFFFFF
+        assert (em.pt_dot(q, rot, [c, c], 2, 1, 2, enc, [0, 1, 2]) == full).all()
+        if s:
+            coef[:, 1] = 1
+            assert B.compact_shift(coef) == 0
+            with pytest.raises(ValueError):
+                B.compact_rows(oc.ntt_fwd(coef.copy(), [0, 1, 2]), s)
+    assert B.compact_shift(np.zeros((2, N), np.uint32)) == 12

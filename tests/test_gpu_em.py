@@ -476,13 +476,16 @@ def test_encrypt(stream, name, with_m, with_c1, alias_e):
 
 
 # ----------------------------------------------------------------------------------------------- BSGS plaintext dot
-@pytest.mark.parametrize("name,enc,K", [("small31", 0xFFFFFFFF, 2), ("small31", 0x7F000003, 3), ("small", 0x3FF, 1),
-                                        ("c3", 0xFFFFFFFF, 1)])
-def test_pt_dot(stream, name, enc, K):
-    say(f"[pt_dot] {name} enc={enc:#x} K={K}")
+# baby steps up to 4 and up to 8 take the register form (full, compact and masked diagonal indices, a last giant step
+# short of diagonals), 9 the re-reading one
+@pytest.mark.parametrize("name,enc,K,B,G,npts", [("small31", 0xFFFFFFFF, 2, 3, 2, 5), ("small31", 0x7F000003, 3, 3, 2, 5),
+                                                ("small", 0x3FF, 1, 3, 2, 5), ("c3", 0xFFFFFFFF, 1, 3, 2, 5),
+                                                ("small31", 0x7F000004, 2, 8, 3, 21), ("small31", 0xFFFFFFFF, 1, 7, 2, 14),
+                                                ("small", 0x7F000001, 1, 6, 2, 9), ("small31", 0x7F000002, 1, 9, 2, 11)])
+def test_pt_dot(stream, name, enc, K, B, G, npts):
+    say(f"[pt_dot] {name} enc={enc:#x} K={K} B={B} G={G} npts={npts}")
     ch, ctx, _ = contexts(name)
-    rng = np.random.default_rng(enc % 1000 + K)
-    B, G, npts = 3, 2, 5
+    rng = np.random.default_rng(enc % 1000 + K + B)
     top = len(ch.q) - 1 if name == "c3" else len(ch.q) - 2
     rows = list(range(top + 1)) + [len(ch.q) + j for j in range(len(ch.p))]
     n, R = len(rows), ch.rows
@@ -490,7 +493,7 @@ def test_pt_dot(stream, name, enc, K):
     rot = np.zeros((K, B, 2, R, ch.n), np.uint32)
     for t in rows:
         rot[:, :, :, t] = rng.integers(0, ch.primes[t], (K, B, 2, ch.n))
-    ptw = ch.n if enc == 0xFFFFFFFF else (ch.n >> 3 if enc >> 24 == 0x7F else enc + 1)
+    ptw = ch.n if enc == 0xFFFFFFFF else (ch.n >> (enc & 0xFF) if enc >> 24 == 0x7F else enc + 1)
     pt_prow = top + 1  # the special rows' diagonal rows follow the Q rows
     pts = [np.stack([rng.integers(0, ch.primes[t], ptw) for t in rows]).astype(np.uint32) for _ in range(npts)]
     pbufs = [pa.DevBuf.from_array(p) for p in pts]

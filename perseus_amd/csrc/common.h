@@ -166,6 +166,24 @@ struct Expander {
 };
 
 // ------------------------------------------------------------------------------------------------ vector access
+// A pointer read from a table in memory (a key's rows, a seed), unlike one passed as a kernel argument, is generic to
+// the compiler: loads through it become flat loads, which also count against the LDS / scalar-load counter, so the next
+// wait for an LDS access waits for them too. These views make such loads global loads.
+typedef const __attribute__((address_space(1))) uint32_t* gptr;
+typedef uint32_t gu4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gu4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ gptr as_global(const void* p) { return (gptr)p; }
+__device__ __forceinline__ void ld16(gptr p, uint32_t (&v)[16]) {
+    const __attribute__((address_space(1))) gu4* q = (const __attribute__((address_space(1))) gu4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const gu4 x = q[i];
+        v[4 * i] = x.x;
+        v[4 * i + 1] = x.y;
+        v[4 * i + 2] = x.z;
+        v[4 * i + 3] = x.w;
+    }
+}
 __device__ __forceinline__ void ld16(const uint32_t* p, uint32_t (&v)[16]) {
     const uint4* q = (const uint4*)p;
 #pragma unroll

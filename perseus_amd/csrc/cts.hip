@@ -62,6 +62,11 @@ __device__ __forceinline__ void ld8(const uint32_t* p, uint32_t (&v)[CS]) {
     const uint4 a = ((const uint4*)p)[0], b = ((const uint4*)p)[1];
     v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
 }
+__device__ __forceinline__ void ld8(gptr p, uint32_t (&v)[CS]) {
+    const __attribute__((address_space(1))) gu4* q = (const __attribute__((address_space(1))) gu4*)p;
+    const gu4 a = q[0], b = q[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
 __device__ __forceinline__ void st8(uint32_t* p, const uint32_t (&v)[CS]) {
     ((uint4*)p)[0] = make_uint4(v[0], v[1], v[2], v[3]);
     ((uint4*)p)[1] = make_uint4(v[4], v[5], v[6], v[7]);
@@ -118,12 +123,12 @@ struct Row {
 // A key's rows at row t: b of digit d at kb + d bstride (dense: plus the slot; packed: bits per value, rows of bwords
 // words), resident a of digit d >= nreg at ka + d astride, the seed of the regenerated digits.
 struct KeyRow {
-    const uint32_t* kb;
+    gptr kb;
     uint64_t bstride, bwords;
     int bits;
-    const uint32_t* ka;
+    gptr ka;
     uint64_t astride;
-    const uint32_t* seed;
+    gptr seed;
 };
 
 __device__ __forceinline__ Row make_row(const PrimeConst& q, int logn, uint32_t* lds, int nreg) {
@@ -139,7 +144,7 @@ __device__ __forceinline__ Row make_row(const PrimeConst& q, int logn, uint32_t*
 }
 
 // 1. The KSKA words of digits d < nreg at the source chunk [sc, sc + 512) into la[d][apad(s - sc)].
-__device__ __forceinline__ void stage_a(const Row& R, const uint32_t* sp, uint32_t sc, int lane) {
+__device__ __forceinline__ void stage_a(const Row& R, gptr sp, uint32_t sc, int lane) {
     uint32_t seed[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) seed[k] = sp[k];
@@ -206,7 +211,7 @@ __device__ __forceinline__ void products(const Row& R, const KeyRow& K, uint32_t
             ld8(K.ka + d * K.astride + s0, a);
         }
         if (K.bits == 0) ld8(K.kb + d * K.bstride + s0, b);
-        else ld_packed(K.kb + d * K.bstride, K.bwords, s0, K.bits, b);
+        else ld_packed((const uint32_t*)(K.kb + d * K.bstride), K.bwords, s0, K.bits, b);
         ld8(R.drow(d) + s0, x);
 #pragma unroll
         for (int k = 0; k < CS; ++k) {
@@ -335,19 +340,19 @@ __global__ void __launch_bounds__(CW, 3) cts_k(CtsRegenArgs RA, int logn, int j0
             const uint32_t g = A.kinv[i - 1];
             KeyRow K;
             if (REGEN) {
-                K.kb = (const uint32_t*)T.kb[i - 1] + (size_t)slot * T.row_words;
+                K.kb = as_global(T.kb[i - 1]) + (size_t)slot * T.row_words;
                 K.bstride = (uint64_t)T.srows * T.row_words;
                 K.bwords = T.row_words;
                 K.bits = T.bits;
-                K.seed = R.nreg > 0 ? T.seed[i - 1] : K.kb;  // (K.kb: never read)
+                K.seed = R.nreg > 0 ? as_global(T.seed[i - 1]) : K.kb;  // (K.kb: never read)
             } else {
-                K.kb = (const uint32_t*)A.kb[i - 1] + roff;
+                K.kb = as_global(A.kb[i - 1]) + roff;
                 K.bstride = A.key_digit_stride;
                 K.bwords = 0;
                 K.bits = 0;
                 K.seed = K.kb;  // no regenerated digit: never read
             }
-            K.ka = R.nreg < A.ndig ? (const uint32_t*)A.ka[i - 1] + roff : K.kb;  // (K.kb: never read)
+            K.ka = R.nreg < A.ndig ? as_global(A.ka[i - 1]) + roff : K.kb;  // (K.kb: never read)
             K.astride = A.key_digit_stride;
             rotation<WIDE>(R, K, g, inv_odd(g) & R.mask2n, oc0, lane, w0, w1);
         }
@@ -360,7 +365,7 @@ __global__ void __launch_bounds__(CW, 3) cts_k(CtsRegenArgs RA, int logn, int j0
             const uint32_t* pt = (const uint32_t*)A.pts[dg] + (size_t)prow * A.ptw;
             uint32_t w[CS];
             if (pt8 && ((uintptr_t)pt & 15) == 0) {
-                ld8(pt + o0, w);
+                ld8(as_global(pt) + o0, w);
             } else {
                 const Buf bp(pt, (uint32_t)A.ptw * 4);
 #pragma unroll
@@ -480,12 +485,12 @@ __global__ void __launch_bounds__(CW, 3) ksum_k(KsKeyArgs G, int logn) {
     for (int k = 0; k < CS; ++k) acc0[k] = acc1[k] = 0;
     for (int r = 0; r < A.R; ++r) {
         KeyRow K;
-        K.kb = (const uint32_t*)T.kb[r] + (size_t)slot * T.row_words;
+        K.kb = as_global(T.kb[r]) + (size_t)slot * T.row_words;
         K.bstride = (uint64_t)T.srows * T.row_words;
         K.bwords = T.row_words;
         K.bits = T.bits;
-        K.seed = R.nreg > 0 ? T.seed[r] : K.kb;                              // (K.kb: never read)
-        K.ka = R.nreg < A.ndig ? (const uint32_t*)A.ka[r] + roff : K.kb;    // (K.kb: never read)
+        K.seed = R.nreg > 0 ? as_global(T.seed[r]) : K.kb;                 // (K.kb: never read)
+        K.ka = R.nreg < A.ndig ? as_global(A.ka[r]) + roff : K.kb;         // (K.kb: never read)
         K.astride = A.key_digit_stride;
         const uint32_t kx = A.autok[r] & R.mask2n;  // the scatter exponent; its inverse gathers
         uint32_t w0[CS], w1[CS];
@@ -535,21 +540,21 @@ __global__ void __launch_bounds__(CW, 3) regen_k(KsRegenArgs G, int logn) {
     R.pm = R.pms = 0;
     KeyRow K;
     if (T.kb) {
-        K.kb = (const uint32_t*)T.kb[0] + (size_t)slot_of(T, t, A.nq) * T.row_words;
+        K.kb = as_global(T.kb[0]) + (size_t)slot_of(T, t, A.nq) * T.row_words;
         K.bstride = (uint64_t)T.srows * T.row_words;
         K.bwords = T.row_words;
         K.bits = T.bits;
     } else {
-        K.kb = (const uint32_t*)A.kb[0] + roff;
+        K.kb = as_global(A.kb[0]) + roff;
         K.bstride = A.key_digit_stride;
         K.bwords = 0;
         K.bits = 0;
     }
     K.ka = K.kb;  // every digit regenerates: never read
     K.astride = 0;
-    K.seed = G.seed;
+    K.seed = as_global(G.seed);
     const uint32_t s0 = blockIdx.x * CCH + lane * CS;  // no automorphism: source and output slots coincide
-    if (R.nreg > 0) stage_a(R, G.seed, blockIdx.x * CCH, lane);
+    if (R.nreg > 0) stage_a(R, as_global(G.seed), blockIdx.x * CCH, lane);
     for (int c = 0; c < A.K; ++c) {
         R.c1 = (const uint32_t*)A.c1 + c * A.ct_stride + roff;
         R.mu = (const uint32_t*)A.modup + c * A.mu_ct_stride + roff;

@@ -160,7 +160,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
         for (int r = r_lo + wv; r < r_hi; r += KW) {
             uint32_t seed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             if (mode == 1 && T.nregen > 0) {
-                const uint32_t* sp = T.seed[r];
+                const gptr sp = as_global(T.seed[r]);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) seed[i] = sp[i];
             }
@@ -184,12 +184,12 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
             for (int d = 0; d < ndig; ++d) {
                 uint32_t b[DS], a[DS];
                 if (mode == 0) {
-                    ld16((const uint32_t*)A.kb[r] + d * A.key_digit_stride + X.trow + s0, b);
+                    ld16(as_global(A.kb[r]) + d * A.key_digit_stride + X.trow + s0, b);
                 } else if (T.bits == 0) {
-                    ld16((const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words + s0, b);
+                    ld16(as_global(T.kb[r]) + (size_t)(d * T.srows + slot) * T.row_words + s0, b);
                 } else {
                     // packed b: the lane's 16 values sit in words [bit0 / 32, bit0 / 32 + 16] of the row's stream
-                    const uint32_t* row = (const uint32_t*)T.kb[r] + (size_t)(d * T.srows + slot) * T.row_words;
+                    const gptr row = as_global(T.kb[r]) + (size_t)(d * T.srows + slot) * T.row_words;
                     const uint32_t bit0 = s0 * (uint32_t)T.bits;
                     const uint32_t msk = T.bits == 32 ? 0xFFFFFFFFu : (1u << T.bits) - 1u;
 #pragma unroll
@@ -216,7 +216,7 @@ __global__ void __launch_bounds__(KBX) dot_k(KsArgs A, KeyTab T, int logn, int m
 #pragma unroll
                     for (int j = 0; j < 16; ++j) a[j] = (rej >> j) & 1 ? 0 : ex.red(a[j]);
                 } else {
-                    ld16((const uint32_t*)A.ka[r] + d * A.key_digit_stride + X.trow + s0, a);
+                    ld16(as_global(A.ka[r]) + d * A.key_digit_stride + X.trow + s0, a);
                 }
                 uint32_t x[DS];
                 if (d < MAXD) ld16(L.D[d] + padw(lane * DS), x);
@@ -365,15 +365,14 @@ __device__ __forceinline__ uint32_t lane_prefix(uint32_t cnt, int lane) {
 // and one word (the row's guard word keeps w0 + 16 inside the row). With s0 a multiple of 16 the first value starts
 // at bit 0 of w0 (even BITS) or at bit 0 or 16 (odd BITS, by the lane's parity): the window is realigned by that shift
 // once, so every value's position is a compile-time constant.
-typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 template <int BITS>
-__device__ __forceinline__ void ldpk16(const uint32_t* row, uint32_t s0, uint32_t (&out)[DS]) {
+__device__ __forceinline__ void ldpk16(gptr row, uint32_t s0, uint32_t (&out)[DS]) {
     const uint32_t bit0 = s0 * BITS;
-    const uint32_t* p = row + (bit0 >> 5);
+    const gptr p = row + (bit0 >> 5);
     uint32_t w[17];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const u32x4a4 v = *(const u32x4a4*)(p + 4 * i);
+        const gu4a4 v = *(const __attribute__((address_space(1))) gu4a4*)(p + 4 * i);
         w[4 * i] = v.x, w[4 * i + 1] = v.y, w[4 * i + 2] = v.z, w[4 * i + 3] = v.w;
     }
     w[16] = p[16];
@@ -401,10 +400,10 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     FastWave& W = *C.W;
     const int lane = C.lane, lp = C.lp;
     const uint32_t p = C.p, s0 = C.s0;
-    const uint32_t* kb = (const uint32_t*)T.kb[r] + (size_t)C.slot * T.row_words + (PK ? 0 : s0);
+    const gptr kb = as_global(T.kb[r]) + (size_t)C.slot * T.row_words + (PK ? 0 : s0);
     const size_t dstride = (size_t)T.srows * T.row_words;
     uint32_t seed[8];
-    const uint32_t* sp = T.seed[r];
+    const gptr sp = as_global(T.seed[r]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) seed[i] = sp[i];
     if (lane == 0) W.qn = 0;

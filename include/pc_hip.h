@@ -815,6 +815,10 @@ int pc_hip_last_error(void);
  * a workspace for up to k_rot extended ciphertexts per hoisted chunk. Errors: NULL, with *err set. */
 typedef struct pcx_ctx pcx_ctx;
 pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int* err);
+/* pcx_ctx_new with plans and workspace for K-ciphertext products and rescales, K <= k_max <= 4 (the reference's
+ * k_max, crates/pc-gpu/src/ops.rs:1554-1595: K ciphertexts per launch); pcx_ctx_new is k_max 1. */
+pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int k_max,
+                       int* err);
 void pcx_ctx_free(pcx_ctx* c);
 const KernelTable* pcx_ctx_table(const pcx_ctx* c);
 const PrimeConst* pcx_ctx_primes(const pcx_ctx* c); /* device table by prime id */
@@ -918,6 +922,9 @@ pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed,
  * the primes one at a time; out's rows above are scratch. Two primes run the table's rescale_fwd (the corrections
  * generated in the forward NTT), one prime rescale_coef and the NTT. out may be ct. */
 int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_stream_t s);
+/* pcx_rescale of K <= k_max consecutive ciphertexts (ct_words apart) in the same launches; each ciphertext's words
+ * are those of pcx_rescale on it alone. */
+int pcx_rescale_k(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, int K, pc_stream_t s);
 /* The relinearized product (crates/pc-gpu/src/relin.rs:213-235 mult): the tensor (c0, c1, d2), then d2 key-switched
  * by key 0 of k (the relinearization key: galois 1) and added: out = (c0, c1) + ModDown(dot(ModUp(d2))) on Q rows
  * 0..top (degree 2, rescale pending). out may be a or b. */
@@ -926,6 +933,11 @@ int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top
  * crates/pc-gpu/src/bts/cts.rs:740-751, LtEnd::FusedRescale, applied to x + P (d0, d1)): out's Q rows 0..top - 2 =
  * round((P (d0, d1) + KS(d2)) / B). top >= 2. out may alias a or b. */
 int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);
+/* pcx_mul_relin_rescale of K <= k_max pairs: a, b and out each K consecutive ciphertexts (ct_words apart), product k
+ * = a_k b_k, every stage one launch for the K (the tensor, ModUp, key dot and fused ModDown-rescale of
+ * crates/pc-gpu/src/relin.rs:213-235 at K ciphertexts); each product's words are those of the K = 1 call. */
+int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, int K,
+                            pc_stream_t s);
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
  * form rows by prime id (rows 0..top read). out may be ct. */
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);

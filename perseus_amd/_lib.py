@@ -51,6 +51,8 @@ _SIGS = {
     "pc_hip_error_string": (C.c_char_p, [C.c_int]),
     "pc_hip_last_error": (C.c_int, []),
     "pcx_ctx_new": (vp, [C.c_uint32, C.POINTER(C.c_uint64), C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
+    "pcx_ctx_new_k": (vp, [C.c_uint32, C.POINTER(C.c_uint64), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                           C.POINTER(C.c_int)]),
     "pcx_ctx_free": (None, [vp]),
     "pcx_ctx_table": (vp, [vp]),
     "pcx_ctx_primes": (vp, [vp]),
@@ -78,8 +80,10 @@ _SIGS = {
                                 vp]),
     "pcx_keys_relin": (vp, [vp, C.POINTER(C.c_int8), u32p, C.POINTER(C.c_int64), C.c_int, C.POINTER(C.c_int)]),
     "pcx_rescale": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
+    "pcx_rescale_k": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, C.c_int, vp]),
     "pcx_mul_relin": (C.c_int, [vp, vp, vp, vp, C.c_int, vp, vp]),
     "pcx_mul_relin_rescale": (C.c_int, [vp, vp, vp, vp, C.c_int, vp, vp]),
+    "pcx_mul_relin_rescale_k": (C.c_int, [vp, vp, vp, vp, C.c_int, vp, C.c_int, vp]),
     "pcx_rotate_many_rescale": (C.c_int, [vp, vp, C.POINTER(C.c_int), C.c_int, C.POINTER(vp), C.c_int, vp, vp, vp]),
     "pcx_mul_plain": (C.c_int, [vp, vp, vp, C.c_int, vp, vp]),
     "pcx_modup": (C.c_int, [vp, vp, C.c_int, vp]),

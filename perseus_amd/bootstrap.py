@@ -436,8 +436,13 @@ class Bootstrap:
     an operations object. `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
     scale par.delta_in. Plaintexts (the levels' diagonals, the i monomial) are encoded once by `prepare`."""
 
-    def __init__(self, ops, par, primes, ops2=None, special=None):
+    def __init__(self, ops, par, primes, ops2=None, special=None, pair=None):
         self.ops, self.par, self.ops2 = ops, par, ops2
+        # pair: the two EvalMod chains batched (K = 2) on ops, which must take two ciphertexts per product; by default
+        # whenever ops can and no second lane is given
+        can = getattr(getattr(ops, "ctx", None), "k_max", 1) >= 2
+        self.pair = (ops2 is None and can) if pair is None else bool(pair)
+        assert not (self.pair and (ops2 is not None or not can)), "pairing needs one lane on a k_max >= 2 context"
         self.q = [int(p) for p in primes]
         # special primes given: the levels' babies run fused in the extended basis (cts: one ModUp, the products of
         # the key-switched babies before any ModDown, one ModDown per giant step), the diagonals encoded over Q and P
@@ -571,13 +576,18 @@ class Bootstrap:
             k += 1
         cj = ops.alloc()
         ops.rotate(cj, x.h, x.top, "conj")
-        re = Ct(ops.alloc(), x.top, x.scale)
+        pair = ops.alloc(2) if self.pair else None
+        re = Ct(ops.item(pair, 0) if self.pair else ops.alloc(), x.top, x.scale)
         ops.add(re.h, x.h, cj, x.top, False)
         d = ops.alloc()
         ops.add(d, x.h, cj, x.top, True)
-        im = Ct(ops.alloc(), x.top, x.scale)
+        im = Ct(ops.item(pair, 1) if self.pair else ops.alloc(), x.top, x.scale)
         ops.mul_pt(im.h, d, x.top, self.mono_mi)
-        if self.ops2 is None:
+        if self.pair:
+            # both chains in the same launches: the pair's ciphertext 0 is the real part's, 1 the imaginary part's
+            h = self.evalmod(Ct(pair, x.top, x.scale), Evaluator(PairOps(ops), self.q))
+            re, im = Ct(ops.item(h.h, 0), h.top, h.scale), Ct(ops.item(h.h, 1), h.top, h.scale)
+        elif self.ops2 is None:
             re, im = self.evalmod(re), self.evalmod(im)
         else:
             # the imaginary part's chain on the second lane (its own workspace and stream), beside the real part's
@@ -635,6 +645,36 @@ def key_plan(boot):
     return gal, levels, len(gal) - 1
 
 
+class PairOps:
+    """The real and imaginary parts' EvalMod chains side by side: every handle is two consecutive ciphertexts of one
+    GpuOps buffer, every operation one launch sequence for both (K = 2). Both chains take the same steps with the same
+    constants, so each part's words are those of its chain run alone."""
+
+    def __init__(self, ops):
+        self.o = ops
+
+    def alloc(self):
+        return self.o.alloc(2)
+
+    def add(self, out, a, b, top, sub):
+        self.o.add(out, a, b, top, sub, K=2)
+
+    def mul_const(self, out, x, top, k):
+        self.o.mul_const(out, x, top, k, K=2)
+
+    def add_const(self, x, top, k):
+        self.o.add_const(x, top, k, K=2)
+
+    def wsum(self, out, srcs, top, ks, k0):
+        self.o.wsum(out, srcs, top, ks, k0, K=2)
+
+    def mul_relin_rescale(self, out, a, b, top):
+        self.o.mul_relin_rescale(out, a, b, top, K=2)
+
+    def rescale2(self, out, x, top):
+        self.o.rescale2(out, x, top, K=2)
+
+
 class GpuOps:
     """The composite's operations on the device: the engine's key switches, rescale and products, the kernel table's
     element-wise entries (ew_add, ew_scale, ew_copy, add_const, mul_table, pt_dot, mod_raise). Buffers come from a
@@ -687,7 +727,7 @@ class GpuOps:
         if rc != 0:
             raise self.eng.HipError(f"{name} returned {rc}")
 
-    def _ew(self, name, out, a, b, top, sub=0, sc=None):
+    def _ew(self, name, out, a, b, top, sub=0, sc=None, K=1):
         e = self.abi.EwArgs()
         e.out, e.a = self._ref(out), self._ref(a)
         if b is not None:
@@ -695,15 +735,15 @@ class GpuOps:
         e.rs = self.abi.RowSet(top + 1, 0, self.nq, 0)
         if sc is not None:
             e.sc, e.scs = sc[0].ptr.value, sc[1].ptr.value
-        e.pr, e.K, e.nparts, e.sub = self.pr, 1, 2, sub
+        e.pr, e.K, e.nparts, e.sub = self.pr, K, 2, sub
         self._call(name, e)
 
     # -- element-wise
     def copy(self, dst, src, top):
         self._ew("ew_copy", dst, src, None, top)
 
-    def add(self, out, a, b, top, sub):
-        self._ew("ew_add", out, a, b, top, 1 if sub else 0)
+    def add(self, out, a, b, top, sub, K=1):
+        self._ew("ew_add", out, a, b, top, 1 if sub else 0, K=K)
 
     def _const_rows(self, k):
         key = ("k", k)
@@ -713,16 +753,16 @@ class GpuOps:
             self.cache[key] = (self.eng.DevBuf.from_array(r), self.eng.DevBuf.from_array(rs))
         return self.cache[key]
 
-    def mul_const(self, out, x, top, k):
-        self._ew("ew_scale", out, x, None, top, sc=self._const_rows(int(k)))
+    def mul_const(self, out, x, top, k, K=1):
+        self._ew("ew_scale", out, x, None, top, sc=self._const_rows(int(k)), K=K)
 
-    def add_const(self, x, top, k):
+    def add_const(self, x, top, k, K=1):
         r, _ = self._const_rows(int(k))
         a = self.abi.AddConstArgs()
-        a.x, a.k, a.pr, a.n, a.K = self._ref(x), r.ptr.value, self.pr, top + 1, 1
+        a.x, a.k, a.pr, a.n, a.K = self._ref(x), r.ptr.value, self.pr, top + 1, K
         self._call("add_const", a)
 
-    def wsum(self, out, srcs, top, ks, k0):
+    def wsum(self, out, srcs, top, ks, k0, K=1):
         key = ("w", tuple(ks), k0)
         if key not in self.cache:
             w = np.array([[k % p for p in self.primes] for k in ks], np.uint32)
@@ -735,7 +775,7 @@ class GpuOps:
         for j, x in enumerate(srcs):
             a.w.src[j] = self._ref(x)
         a.w.w, a.w.ws, a.w.pr = bw.ptr.value, bws.ptr.value, self.pr
-        a.w.nsrc, a.w.rowstride, a.w.n, a.w.K = len(srcs), self.R, top + 1, 1
+        a.w.nsrc, a.w.rowstride, a.w.n, a.w.K = len(srcs), self.R, top + 1, K
         a.k = bk.ptr.value
         self._call("wsum_k", a)
 
@@ -850,11 +890,11 @@ class GpuOps:
     def mul_relin(self, out, a, b, top):
         self.ctx.mul_relin(self.relin, a, b, top, out, self.st)
 
-    def mul_relin_rescale(self, out, a, b, top):
-        self.ctx.mul_relin_rescale(self.relin, a, b, top, out, self.st)
+    def mul_relin_rescale(self, out, a, b, top, K=1):
+        self.ctx.mul_relin_rescale(self.relin, a, b, top, out, self.st, K=K)
 
-    def rescale2(self, out, x, top):
-        self.ctx.rescale(x, top, 2, out, self.st)
+    def rescale2(self, out, x, top, K=1):
+        self.ctx.rescale(x, top, 2, out, self.st, K=K)
 
     # -- ModRaise
     def mod_raise(self, out, x, top):

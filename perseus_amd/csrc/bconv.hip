@@ -97,8 +97,9 @@ struct JobLds {
     uint32_t mt[MAXT][MAX_REG_SRC];
     uint32_t trow[MAXT];
     uint32_t tc[MAXT][4];  // p, 2^32 mod p, its Shoup companion, floor(2^32 / p)
+    uint32_t r64[MAXT];    // 2^64 mod p
     double rb[MAX_REG_SRC];
-    uint32_t bmod[MAXT];
+    uint32_t bmod[MAXT][2];  // B mod p and its Shoup companion
     uint32_t sp[MAX_REG_SRC];  // the sources' primes
 };
 
@@ -173,9 +174,11 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
     const int ng = (P.ns + 3) >> 2;  // groups of 4 sources (M zero-padded)
     for (int t = 0; t < ntl; ++t) {
         const Red red(S.tc[t][0], S.tc[t][1], S.tc[t][2], S.tc[t][3]);
+        const uint32_t r64 = S.r64[t];
+        const uint64_t pm = (uint64_t)(mx - 1) * (uint64_t)(red.p - 1);  // the largest product
         uint64_t acc[V] = {};
         uint32_t r[V];
-        if ((uint64_t)(mx - 1) * (uint64_t)(red.p - 1) <= lazy_bound) {
+        if (pm <= lazy_bound) {
             // every partial sum stays below 2^64: one multiply-add per product
 #pragma unroll
             for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
@@ -191,9 +194,34 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
             }
 #pragma unroll
             for (int k = 0; k < V; ++k) r[k] = red(acc[k]);
+        } else if (pm <= ~0ull / 16) {
+            // 16 products fit a 64-bit sum (30-bit primes): sources 0..15 in one, the rest in a second; their sum's
+            // carry is folded in as 2^64 mod p
+            uint64_t acc2[V] = {};
+#pragma unroll
+            for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
+                if (g < ng) {
+                    const uint4 m4 = *(const uint4*)&S.mt[t][4 * g];
+                    const uint32_t mv[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                        for (int k = 0; k < V; ++k) {
+                            const uint64_t pr = (uint64_t)y[(4 * g + e) * V + k] * mv[e];
+                            if (g < 4) acc[k] += pr;
+                            else acc2[k] += pr;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const uint64_t s2 = acc[k] + acc2[k];
+                r[k] = addm(red(s2), s2 < acc[k] ? r64 : 0u, red.p);
+            }
         } else {
             // four products of words below 2^31 stay below 2^64: each group of four is summed by multiply-adds, and
-            // only the group sums carry into the 96-bit total
+            // only the group sums carry into the 96-bit total (at most 5 wraps: wraps r64 < 2^34)
             uint32_t wraps[V] = {};
 #pragma unroll
             for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
@@ -214,11 +242,12 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
                 }
             }
 #pragma unroll
-            for (int k = 0; k < V; ++k) r[k] = red.red96(acc[k], wraps[k]);
+            for (int k = 0; k < V; ++k) r[k] = addm(red(acc[k]), red((uint64_t)wraps[k] * r64), red.p);
         }
+        // exact jobs: u <= nsrc, so u B mod p is one Shoup product
 #pragma unroll
         for (int k = 0; k < V; ++k) {
-            if (j.exact) r[k] = subm(r[k], red((uint64_t)u[k] * S.bmod[t]), red.p);
+            if (j.exact) r[k] = subm(r[k], shoup((uint32_t)u[k], S.bmod[t][0], S.bmod[t][1], red.p), red.p);
         }
         stv<V>(dst + ((size_t)S.trow[t] << logn) + c0, r);
     }
@@ -251,16 +280,22 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
         for (int t = threadIdx.x; t < ntl; t += BX) {
             const PrimeConst& q = A.pr[P.tgt_prime(t0 + t)];
             S.trow[t] = P.tgt_row(t0 + t);
-            S.tc[t][0] = (uint32_t)q.p;
-            S.tc[t][1] = (uint32_t)q.split;
-            S.tc[t][2] = (uint32_t)(q.split >> 32);
+            const uint32_t qp = (uint32_t)q.p, r32 = (uint32_t)q.split, r32s = (uint32_t)(q.split >> 32);
+            S.tc[t][0] = qp;
+            S.tc[t][1] = r32;
+            S.tc[t][2] = r32s;
             S.tc[t][3] = (uint32_t)(q.mu_lo >> 32);
+            S.r64[t] = shoup(r32, r32, r32s, qp);
         }
         if (j.exact) {
             const double* rb = exact_rb((const uint32_t*)A.pool, j);
             const uint32_t* bmod = (const uint32_t*)(rb + j.nsrc);
             for (int i = threadIdx.x; i < P.ns; i += BX) S.rb[i] = rb[i];
-            for (int t = threadIdx.x; t < ntl; t += BX) S.bmod[t] = bmod[t0 + t];
+            for (int t = threadIdx.x; t < ntl; t += BX) {
+                const uint32_t b = bmod[t0 + t], qp = (uint32_t)A.pr[P.tgt_prime(t0 + t)].p;
+                S.bmod[t][0] = b;
+                S.bmod[t][1] = (uint32_t)(((uint64_t)b << 32) / qp);
+            }
         }
         __syncthreads();
         if (c0 < (1u << logn)) job_lds<V>(A, j, P, S, y, dst, c0, logn, ntl);

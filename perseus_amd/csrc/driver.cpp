@@ -256,6 +256,7 @@ struct pcx_rows {
 struct pcx_ctx {
     uint32_t logn = 0, n = 0;
     int nq = 0, kp = 0, dnum = 0, alpha = 0, k_rot = 1, rows = 0;
+    int k_max = 1;  // ciphertexts per batched product / rescale (the per-level plans hold k_max copies)
     int lazy = 0;   // NttArgs.lazy: 1 when every prime is below 2^30 (Harvey butterflies)
     int chunk = 0;  // NttArgs.chunk of the batched transforms: rows per pass pair (0 = all)
     std::vector<uint64_t> primes, roots;
@@ -347,8 +348,31 @@ std::vector<uint32_t> digit_limbs(const pcx_ctx* c, int d, int top) {
     return v;
 }
 
+// The batched plans: ciphertext k's rows follow ciphertext 0's, shifted by k stride rows, so that the plan of K <= k_max
+// ciphertexts is the first K / k_max of the rows (and of the conversion jobs)
+template <class T>
+void rep_rows(std::vector<T>& v, int kmax, int64_t stride) {
+    const size_t n1 = v.size();
+    for (int k = 1; k < kmax; ++k)
+        for (size_t i = 0; i < n1; ++i) v.push_back((T)((int64_t)v[i] + k * stride));
+}
+void rep_jobs(std::vector<JobSpec>& v, int kmax, uint32_t src_stride, uint32_t dst_stride) {
+    const size_t n1 = v.size();
+    for (int k = 1; k < kmax; ++k)
+        for (size_t i = 0; i < n1; ++i) {
+            JobSpec j = v[i];
+            j.src_off += (uint32_t)k * src_stride;
+            j.dst_off += (uint32_t)k * dst_stride;
+            v.push_back(j);
+        }
+}
+// rows / jobs of the first K ciphertexts of a batched plan
+int k_rows(const pcx_ctx* c, const Rows& r, int K) { return r.n / c->k_max * K; }
+int k_jobs(const pcx_ctx* c, const Bconv& b, int K) { return b.njobs / c->k_max * K; }
+
 int build_level(pcx_ctx* c, int top, Level& L) {
     const uint32_t n = c->n;
+    const int KM = c->k_max, RR = c->rows;
     L.top = top;
     std::vector<std::vector<uint32_t>> digs;
     for (int d = 0; d < c->dnum; ++d) {
@@ -374,6 +398,11 @@ int build_level(pcx_ctx* c, int top, Level& L) {
             uint64_t p = c->primes[t];
             es.push_back((uint32_t)mulmod(invmod(n % p, p), pre_of[t], p));
         }
+        // ciphertext k: coefficient rows k R + t, c1 rows k 2R + t from ciphertext 0's c1
+        rep_rows(roff, KM, RR);
+        rep_rows(soff, KM, 2 * RR);
+        rep_rows(rp, KM, 0);
+        rep_rows(es, KM, 0);
         std::vector<uint32_t> est = scale_table(c->primes, rp, es);
         if (int e = fill_rows(c->dev, L.mu_intt, roff, rp, &soff, &est)) return e;
     }
@@ -399,6 +428,10 @@ int build_level(pcx_ctx* c, int top, Level& L) {
                     roff.push_back(specs[d].dst_off + t);
                     rp.push_back(t);
                 }
+        // ciphertext k: coefficient rows from k R, digit rows from k dnum R
+        rep_jobs(specs, KM, (uint32_t)RR, (uint32_t)(c->dnum * RR));
+        rep_rows(roff, KM, c->dnum * RR);
+        rep_rows(rp, KM, 0);
         L.mu_bconv.build(c->dev, c->primes, specs);
         if (int e = fill_rows(c->dev, L.mu_ntt, roff, rp, nullptr, nullptr)) return e;
     }
@@ -503,6 +536,11 @@ int build_level(pcx_ctx* c, int top, Level& L) {
                 roff2.push_back((uint32_t)(part * R + t));
                 rp2.push_back(t);
             }
+        // ciphertext k (and its correction rows in tmp) at k 2R rows
+        rep_rows(roff, KM, 2 * R);
+        rep_rows(rp, KM, 0);
+        rep_rows(roff2, KM, 2 * R);
+        rep_rows(rp2, KM, 0);
         if (int e = fill_rows(c->dev, Z.intt, roff, rp, nullptr, nullptr)) return e;
         if (int e = fill_rows(c->dev, Z.ntt, roff2, rp2, nullptr, nullptr)) return e;
     }
@@ -557,6 +595,13 @@ int build_level(pcx_ctx* c, int top, Level& L) {
             k[2 * R + t] = (uint32_t)pm;
             k[3 * R + t] = shoup_c((uint32_t)pm, (uint32_t)q);
         }
+        // ciphertext k's extended rows, conversion rows and output rows at k 2R
+        rep_rows(roff, KM, 2 * R);
+        rep_rows(rp, KM, 0);
+        rep_rows(es, KM, 0);
+        rep_rows(roff2, KM, 2 * R);
+        rep_rows(rp2, KM, 0);
+        rep_jobs(specs, KM, (uint32_t)(2 * R), (uint32_t)(2 * R));
         std::vector<uint32_t> est = scale_table(c->primes, rp, es);
         std::vector<int32_t> ids(R);
         for (int i = 0; i < R; ++i) ids[i] = i;
@@ -600,15 +645,16 @@ const Level* level(const pcx_ctx* c, int top) {
 // ModDown and the two-prime rescale at once (the level's mdr plan): out (Q rows 0..top - 2) = the exact
 // (x + P onto - conv_B) / B with B = P q_top q_{top-1}, x = ext (one extended ciphertext), onto NULL or a ciphertext at
 // top (may alias out)
-int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto, pc_stream_t s) {
+// K <= k_max ciphertexts at once: ext, out and onto each K consecutive ciphertexts (ct_words apart)
+int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto, pc_stream_t s, int K = 1) {
     const Level* L = level(c, top);
-    if (!L || top < 2 || !L->mdr.k) return -1;
+    if (!L || top < 2 || !L->mdr.k || K < 1 || K > c->k_max) return -1;
     const Level::MdRescale& M = L->mdr;
     if (onto) {
         Stage st(c, 9, s);
-        if (int e = pch::mdr_prep((int)c->logn, ext, onto, out, M.k, c->pr, c->rows, top, s)) return e;
+        if (int e = pch::mdr_prep((int)c->logn, ext, onto, out, M.k, c->pr, c->rows, top, K, s)) return e;
     }
-    NttArgs a = ntt_args(c, ext, M.intt, M.intt.n);
+    NttArgs a = ntt_args(c, ext, M.intt, k_rows(c, M.intt, K));
     a.es = M.intt.es;
     a.ess = M.intt.es + M.intt.n;
     {
@@ -622,13 +668,13 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     b.jobs = M.conv.jobs;
     b.pool = M.conv.pool;
     b.pr = c->pr;
-    b.njobs = M.conv.njobs;
+    b.njobs = k_jobs(c, M.conv, K);
     b.max_tgt = M.conv.max_tgt;
     {
         Stage st(c, 5, s);
         if (int e = c->tab->bconv(&b, s)) return e;
     }
-    NttArgs f = ntt_args(c, c->conv, M.ntt, M.ntt.n);
+    NttArgs f = ntt_args(c, c->conv, M.ntt, k_rows(c, M.ntt, K));
     f.epi = onto ? 2 : 1;
     f.ed = nullptr;  // the epilogue adds onto out's rows, which hold onto s2
     f.eout = out;
@@ -639,10 +685,11 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     Stage st(c, 6, s);
     return c->tab->ntt_fwd(&f, s);
 }
-int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
+// K <= k_max consecutive ciphertexts (ct_words apart): digits of ciphertext k at digits + k dnum rows N
+int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s, int K = 1) {
     const Level* L = level(c, top);
-    if (!L) return -1;
-    NttArgs a = ntt_args(c, c->coef, L->mu_intt, L->mu_intt.n);
+    if (!L || K < 1 || K > c->k_max) return -1;
+    NttArgs a = ntt_args(c, c->coef, L->mu_intt, k_rows(c, L->mu_intt, K));
     a.src = (const uint32_t*)ct + (size_t)c->rows * c->n;  // c1
     a.soff = L->mu_intt.soff;
     a.snum = 1;
@@ -659,23 +706,25 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s) {
     b.jobs = L->mu_bconv.jobs;
     b.pool = L->mu_bconv.pool;
     b.pr = c->pr;
-    b.njobs = L->mu_bconv.njobs;
+    b.njobs = k_jobs(c, L->mu_bconv, K);
     b.max_tgt = L->mu_bconv.max_tgt;
     {
         Stage st(c, 1, s);
         if (int e = c->tab->bconv(&b, s)) return e;
     }
-    NttArgs f = ntt_args(c, c->digits, L->mu_ntt, L->mu_ntt.n);
+    NttArgs f = ntt_args(c, c->digits, L->mu_ntt, k_rows(c, L->mu_ntt, K));
     Stage st(c, 2, s);
     return c->tab->ntt_fwd(&f, s);
 }
 
 // the dot of keys [r0, r0 + m) of k into m extended ciphertexts at ext (crates/pc-gpu/src/ks.rs:1225-1308 dot_key);
 // sum: 1 sums the m rotations into ext's first ciphertext (KS_SUM), 2 adds that sum onto it (KS_SUM | KS_ACC)
+// K consecutive ciphertexts (ct_words apart, their digits dnum rows N apart) against the same keys: extended
+// ciphertext (k, r) at ext + (k m + r) ct_words
 int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0,
-        int c0_mode = 1) {
+        int c0_mode = 1, int K = 1) {
     const Level* L = level(c, top);
-    if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys) return -1;
+    if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || K < 1 || K > c->k_max || (sum && K > 1)) return -1;
     KsKeyArgs g;
     memset(&g, 0, sizeof g);
     KsArgs& a = g.ks;
@@ -695,10 +744,10 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     a.ct_stride = c->ct_words();
     a.mu_ct_stride = (uint64_t)c->dnum * c->rows * c->n;
     a.mu_digit_stride = (uint64_t)c->rows * c->n;
-    a.out_ct_stride = c->ct_words();
+    a.out_ct_stride = (uint64_t)m * c->ct_words();
     a.out_rot_stride = c->ct_words();
     a.key_digit_stride = 0;
-    a.K = 1;
+    a.K = K;
     a.R = m;
     a.ndig = L->ndig;
     a.c0_mode = c0_mode | (sum ? PC_KS_SUM : 0) | (sum == 2 ? PC_KS_ACC : 0);
@@ -804,15 +853,15 @@ int add_q(pcx_ctx* c, const void* a, const void* b, int top, void* out, pc_strea
 }
 
 // the identity rotation: Q rows 0..top of both parts, one launch of the table's ew_copy
-int copy_q(pcx_ctx* c, const void* ct, int top, void* out, pc_stream_t s) {
+int copy_q(pcx_ctx* c, const void* ct, int top, void* out, pc_stream_t s, int K = 1) {
     const uint64_t part = (uint64_t)c->rows * c->n;
     EwArgs a;
     memset(&a, 0, sizeof a);
-    a.out = PolyRef{out, 0, part};
-    a.a = PolyRef{const_cast<void*>(ct), 0, part};
+    a.out = PolyRef{out, 2 * part, part};
+    a.a = PolyRef{const_cast<void*>(ct), 2 * part, part};
     a.rs = RowSet{top + 1, 0, 0, 0};
     a.pr = c->pr;
-    a.K = 1;
+    a.K = K;
     a.nparts = 2;
     return c->tab->ew_copy(&a, s);
 }
@@ -910,11 +959,15 @@ int build_patches(pcx_ctx* c, pcx_keys* k) {
 extern "C" {
 
 pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int* err) {
+    return pcx_ctx_new_k(log_n, primes, nq, kp, dnum, k_rot, 1, err);
+}
+pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int k_max,
+                       int* err) {
     int dummy;
     if (!err) err = &dummy;
     *err = 0;
     const KernelTable* tab = pc_table_u32_logn(log_n);
-    if (!tab || nq < 1 || kp < 1 || dnum < 1 || dnum > nq || k_rot < 1 || !primes) {
+    if (!tab || nq < 1 || kp < 1 || dnum < 1 || dnum > nq || k_rot < 1 || k_max < 1 || k_max > 4 || !primes) {
         *err = -1;
         return nullptr;
     }
@@ -943,6 +996,7 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
     c->dnum = dnum;
     c->alpha = (nq + dnum - 1) / dnum;
     c->k_rot = k_rot;
+    c->k_max = k_max;
     c->rows = nq + kp;
     c->tab = tab;
     c->primes.assign(primes, primes + nq + kp);
@@ -1026,20 +1080,22 @@ pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int
             delete c;
             return nullptr;
         }
-    // workspace: coefficient rows, ModUp digits, k_rot extended ciphertexts and their conversions
-    const size_t rw = (size_t)n * 4;
-    c->coef = (uint32_t*)c->dev.alloc(nq * rw);
-    c->digits = (uint32_t*)c->dev.alloc((size_t)dnum * R * rw);
-    c->ext = (uint32_t*)c->dev.alloc((size_t)k_rot * 2 * R * rw);
-    c->conv = (uint32_t*)c->dev.alloc((size_t)k_rot * 2 * R * rw);
-    c->tmp = (uint32_t*)c->dev.alloc((size_t)2 * R * rw);
-    c->ws_bytes = nq * rw + (size_t)dnum * R * rw + 2 * (size_t)k_rot * 2 * R * rw + (size_t)2 * R * rw;
+    // workspace: coefficient rows and ModUp digits of k_max ciphertexts, max(k_rot, k_max) extended ciphertexts and
+    // their conversions, k_max ciphertexts of products' d2 and rescale corrections
+    const size_t rw = (size_t)n * 4, next = (size_t)std::max(k_rot, k_max);
+    const size_t coef_rows = k_max == 1 ? (size_t)nq : (size_t)k_max * R;
+    c->coef = (uint32_t*)c->dev.alloc(coef_rows * rw);
+    c->digits = (uint32_t*)c->dev.alloc((size_t)k_max * dnum * R * rw);
+    c->ext = (uint32_t*)c->dev.alloc(next * 2 * R * rw);
+    c->conv = (uint32_t*)c->dev.alloc(next * 2 * R * rw);
+    c->tmp = (uint32_t*)c->dev.alloc((size_t)k_max * 2 * R * rw);
+    c->ws_bytes = (coef_rows + (size_t)k_max * dnum * R + 2 * next * 2 * R + (size_t)k_max * 2 * R) * rw;
     if (c->dev.err) {
         *err = c->dev.err;
         delete c;
         return nullptr;
     }
-    if (hipMemset(c->digits, 0, (size_t)dnum * R * rw) != hipSuccess) c->dev.err = -1;
+    if (hipMemset(c->digits, 0, (size_t)k_max * dnum * R * rw) != hipSuccess) c->dev.err = -1;
     if (hipDeviceSynchronize() != hipSuccess) {
         *err = -1;
         delete c;
@@ -1539,14 +1595,15 @@ int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t 
 // the rescale of ct's rows 0..top (both parts, eval form); out's rows above are left as scratch. Two primes: INTT of
 // the tops, rescale_fwd (the corrections generated in the forward NTT's column pass, out = alpha out + NTT(tmp) in its
 // epilogue); one prime: INTT of the top, rescale_coef, the NTT of the corrections with the same epilogue.
-int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_stream_t s) {
-    if (!c || !ct || !out || (ndrop != 1 && ndrop != 2) || top < ndrop || top >= c->nq) return -1;
+int pcx_rescale_k(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, int K, pc_stream_t s) {
+    if (!c || !ct || !out || (ndrop != 1 && ndrop != 2) || top < ndrop || top >= c->nq || K < 1 || K > c->k_max)
+        return -1;
     const Level::Rescale& Z = c->levels[top].rs[ndrop - 1];
     const int R = c->rows;
     Stage st(c, 9, s);
     if (ct != out)
-        if (int e = copy_q(c, ct, top, out, s)) return e;
-    NttArgs in = ntt_args(c, out, Z.intt, Z.intt.n);
+        if (int e = copy_q(c, ct, top, out, s, K)) return e;
+    NttArgs in = ntt_args(c, out, Z.intt, k_rows(c, Z.intt, K));
     if (int e = c->tab->ntt_inv(&in, s)) return e;
     RescaleArgs r;
     memset(&r, 0, sizeof r);
@@ -1565,9 +1622,9 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
     r.ca = r.cb = 1;
     r.top = top;
     r.nrows = top + 1 - ndrop;
-    r.K = 1;
+    r.K = K;
     r.ndrop = ndrop;
-    NttArgs f = ntt_args(c, c->tmp, Z.ntt, Z.ntt.n);
+    NttArgs f = ntt_args(c, c->tmp, Z.ntt, k_rows(c, Z.ntt, K));
     f.epi = 3;
     f.eout = out;
     f.ex = out;
@@ -1583,14 +1640,19 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
     if (int e = c->tab->rescale_coef(&r, s)) return e;
     return c->tab->ntt_fwd(&f, s);
 }
+int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_stream_t s) {
+    return pcx_rescale_k(c, ct, top, ndrop, out, 1, s);
+}
 
 // The relinearized product (crates/pc-gpu/src/relin.rs:213-235 mult, Cached-key form :119-128): (c0, c1, d2) by the
 // tensor kernel (d2 into part 1 of the context's tmp ciphertext), ModUp(d2), the key inner product with the
 // relinearization key (no c0 term, no automorphism), and the ModDown added onto (c0, c1): out = (c0, c1) +
 // (ext - conv) P^-1 on Q rows 0..top. out may be a or b.
 // the product's (d0, d1) into out and the key switch of d2 into c->ext (before ModDown)
-static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
+static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s,
+                     int K = 1) {
     if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
+    if (K < 1 || K > c->k_max) return -1;
     const uint64_t part = (uint64_t)c->rows * c->n;
     TensorArgs t;
     memset(&t, 0, sizeof t);
@@ -1601,13 +1663,13 @@ static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int 
     t.pr = c->pr;
     t.npairs = 1;
     t.n = top + 1;
-    t.K = 1;
+    t.K = K;
     {
         Stage st(c, 8, s);
         if (int e = c->tab->tensor(&t, s)) return e;
     }
-    if (int e = modup(c, c->tmp, top, s)) return e;
-    return dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, 0);
+    if (int e = modup(c, c->tmp, top, s, K)) return e;
+    return dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, 0, K);
 }
 int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
     if (int e = relin_ext(c, k, a, b, top, out, s)) return e;
@@ -1615,9 +1677,13 @@ int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top
 }
 int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out,
                           pc_stream_t s) {
+    return pcx_mul_relin_rescale_k(c, k, a, b, top, out, 1, s);
+}
+int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, int K,
+                            pc_stream_t s) {
     if (top < 2) return -1;
-    if (int e = relin_ext(c, k, a, b, top, out, s)) return e;
-    return moddown_rescale(c, c->ext, top, out, out, s);
+    if (int e = relin_ext(c, k, a, b, top, out, s, K)) return e;
+    return moddown_rescale(c, c->ext, top, out, out, s, K);
 }
 
 // The plaintext product (crates/pc-gpu/src/ops.rs:927-951 mult_pt, the table's mul_table, em.cuh:508-515): out = ct pt

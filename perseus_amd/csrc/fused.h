@@ -28,9 +28,10 @@ constexpr int MDC_MAX_NTG = 8;
 // error
 int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s);
 // The fused ModDown-rescale's preparation (moddown.hip mdr_prep_k): x rows top - 1, top += P onto; out rows
-// 0..top - 2 = onto s2 (k: [s2 | Shoup | P mod q | Shoup] by prime id, rows words each); both parts of one ciphertext
+// 0..top - 2 = onto s2 (k: [s2 | Shoup | P mod q | Shoup] by prime id, rows words each); both parts of K consecutive
+// ciphertexts (2 rows rows each)
 int mdr_prep(int logn, void* x, const void* onto, void* out, const uint32_t* k, const PrimeConst* pr, int rows,
-             int top, pc_stream_t s);
+             int top, int K, pc_stream_t s);
 
 // The forward transform's row pass alone (grid of every row of a), epilogue a->epi included: completes a forward NTT
 // whose column pass was done by md_conv_cols.

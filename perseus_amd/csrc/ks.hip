@@ -347,6 +347,7 @@ struct FastCtx {
     FastWave* W;
     int lane, lp, slot, logn, m0;
     bool acc_out, pc0;
+    size_t oct;  // this workgroup's ciphertext's output offset (words)
     uint32_t p, pm, n16, mask2n, chunk0, s0, bs0, rb;
     size_t trow;
 };
@@ -516,8 +517,8 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         W.q[i] = ex.red(v);
     }
     const uint32_t kexp = A.autok[r];
-    uint32_t* o0 = (uint32_t*)A.out0 + r * A.out_rot_stride + C.trow;
-    uint32_t* o1 = (uint32_t*)A.out1 + r * A.out_rot_stride + C.trow;
+    uint32_t* o0 = (uint32_t*)A.out0 + C.oct + r * A.out_rot_stride + C.trow;
+    uint32_t* o1 = (uint32_t*)A.out1 + C.oct + r * A.out_rot_stride + C.trow;
     // W_k = top 10 bits of (cb + brev4(k) step) mod 2N; step's low logn - 3 bits are zero, so the sum's top bits are
     // (cb >> sh) + brev4(k) (step >> sh) modulo 1024
     const int sh = C.logn - 9;
@@ -616,10 +617,13 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
     C.trow = (size_t)t << logn;
     const Red red(q);
     const Expander ex(C.p);
-    const int kpg = (A.R + (int)gridDim.z - 1) / (int)gridDim.z;
-    const int r_lo = blockIdx.z * kpg, r_hi = min(A.R, r_lo + kpg);
-    DotCtx X{&A, 0, t < A.nq ? A.digit_of[t] : -1, t, C.trow, C.chunk0};
-    const uint32_t* c0row = (const uint32_t*)A.c0 + C.trow + C.chunk0;
+    // grid z: K ciphertexts x key groups
+    const int ng = (int)gridDim.z / A.K, cix = (int)blockIdx.z / ng, kg = (int)blockIdx.z % ng;
+    const int kpg = (A.R + ng - 1) / ng;
+    const int r_lo = kg * kpg, r_hi = min(A.R, r_lo + kpg);
+    C.oct = (size_t)cix * A.out_ct_stride;
+    DotCtx X{&A, cix, t < A.nq ? A.digit_of[t] : -1, t, C.trow, C.chunk0};
+    const uint32_t* c0row = (const uint32_t*)A.c0 + (size_t)cix * A.ct_stride + C.trow + C.chunk0;
     if constexpr (NW == KW) {
         C.lp = padw(lane * DS);  // this lane's 16 words in the padded rows
 #pragma unroll
@@ -651,7 +655,7 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
 template <int NDIG, bool PATCH, int PK = 0>
 void dot_fast_launch(dim3 grid, const KsArgs& a, const KeyTab& key, const PatchTab& P, int logn, hipStream_t st) {
     if (a.R < KW) {
-        grid.z = a.R;
+        grid.z = a.R * a.K;
         hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1, PK>), grid, dim3(DBX), 0, st, a, key, P, logn);
     } else {
         hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW, PK>), grid, dim3(KBX), 0, st, a, key, P, logn);
@@ -682,11 +686,15 @@ int dot_launch(const KsArgs& a, const KeyTab& key, int mode, pc_stream_t s) {
     while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
     dim3 grid(chunks, a.nrows, groups);
     const bool pk_fast = key.bits == 0 || key.bits == 30 || key.bits == 31;
-    const bool fast = mode == 1 && a.K == 1 && pk_fast && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
+    const bool fast = mode == 1 && a.K <= 4 && pk_fast && key.nregen >= a.ndig && a.ndig >= 1 && a.ndig <= 3;
     if (fast) {
-        if (key.bits == 0) dot_fast_pk<0>(a.ndig, grid, a, key, LOGN, (hipStream_t)s);
-        if (key.bits == 30) dot_fast_pk<30>(a.ndig, grid, a, key, LOGN, (hipStream_t)s);
-        if (key.bits == 31) dot_fast_pk<31>(a.ndig, grid, a, key, LOGN, (hipStream_t)s);
+        // the fast dot takes the K ciphertexts through grid z (K x its key groups)
+        int gf = 1;
+        while (gf < a.R && (long)chunks * a.nrows * gf * a.K < 2048) ++gf;
+        const dim3 g(chunks, a.nrows, gf * a.K);
+        if (key.bits == 0) dot_fast_pk<0>(a.ndig, g, a, key, LOGN, (hipStream_t)s);
+        if (key.bits == 30) dot_fast_pk<30>(a.ndig, g, a, key, LOGN, (hipStream_t)s);
+        if (key.bits == 31) dot_fast_pk<31>(a.ndig, g, a, key, LOGN, (hipStream_t)s);
     } else if (a.ndig > 4) hipLaunchKernelGGL(dot_k<true>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     else hipLaunchKernelGGL(dot_k<false>, grid, dim3(KBX), 0, (hipStream_t)s, a, key, LOGN, mode);
     return launch_rc();
@@ -698,7 +706,7 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     if (!g || !P || !P->idx || !P->val) return -1;
     const KsArgs& a = g->ks;
     const KeyTab& key = g->key;
-    if (a.K != 1 || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 || (a.c0_mode & 3) == 3 ||
+    if (a.K < 1 || a.K > 4 || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 || (a.c0_mode & 3) == 3 ||
         a.ndig > P->ndig || key.q_top >= 0 || key.srows != P->rows)
         return -2;
     if (a.nrows < 0 || a.R < 0) return -1;
@@ -709,8 +717,8 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     if (!key.kb || !key.seed) return -1;
     const int chunks = (1 << LOGN) / DCH;
     int groups = 1;
-    while (groups < a.R && (long)chunks * a.nrows * groups < 2048) ++groups;
-    const dim3 grid(chunks, a.nrows, groups);
+    while (groups < a.R && (long)chunks * a.nrows * groups * a.K < 2048) ++groups;
+    const dim3 grid(chunks, a.nrows, groups * a.K);
     hipStream_t st = (hipStream_t)s;
     if (a.ndig == 1) dot_fast_launch<1, true>(grid, a, key, *P, LOGN, st);
     if (a.ndig == 2) dot_fast_launch<2, true>(grid, a, key, *P, LOGN, st);

@@ -114,15 +114,15 @@ int mdc(const MdcArgs* a, pc_stream_t s) {
     return launch_rc();
 }
 
-// The fused ModDown-rescale's preparation on one ciphertext (both parts, rows 0..top): rows top - 1 and top of x take
-// P onto (the conversion's Q sources then hold x + P onto); rows i <= top - 2 of out become onto s2_i (s2 =
-// (q_top q_{top-1})^-1 mod q_i), onto which the NTT's epilogue adds (x - conv) B^-1. k: [s2 | s2' | P mod q | its
-// Shoup companion] by prime id, rows words each. 4 words per thread.
+// The fused ModDown-rescale's preparation (both parts, rows 0..top; ciphertext blockIdx.z of K, 2 rows rows apart):
+// rows top - 1 and top of x take P onto (the conversion's Q sources then hold x + P onto); rows i <= top - 2 of out
+// become onto s2_i (s2 = (q_top q_{top-1})^-1 mod q_i), onto which the NTT's epilogue adds (x - conv) B^-1. k: [s2 |
+// s2' | P mod q | its Shoup companion] by prime id, rows words each. 4 words per thread.
 __global__ void __launch_bounds__(256) mdr_prep_k(uint32_t* x, const uint32_t* onto, uint32_t* out,
                                                   const uint32_t* k, const PrimeConst* pr, int rows, int top, int logn) {
     const int part = blockIdx.y / (top + 1), i = blockIdx.y % (top + 1);
     const uint32_t p = (uint32_t)pr[i].p;
-    const size_t off = ((size_t)(part * rows + i) << logn) + (blockIdx.x * 256 + threadIdx.x) * 4;
+    const size_t off = ((size_t)((2 * blockIdx.z + part) * rows + i) << logn) + (blockIdx.x * 256 + threadIdx.x) * 4;
     const uint4 v = *(const uint4*)(onto + off);
     if (i >= top - 1) {
         const uint32_t w = k[2 * rows + i], ws = k[3 * rows + i];
@@ -142,9 +142,9 @@ __global__ void __launch_bounds__(256) mdr_prep_k(uint32_t* x, const uint32_t* o
 }  // namespace ntt
 
 int mdr_prep(int logn, void* x, const void* onto, void* out, const uint32_t* k, const PrimeConst* pr, int rows,
-             int top, pc_stream_t s) {
-    if (!x || !onto || !out || !k || !pr || top < 2 || top >= rows || logn < 12 || logn > 16) return -1;
-    const dim3 grid((1u << logn) / 1024, 2 * (top + 1));
+             int top, int K, pc_stream_t s) {
+    if (!x || !onto || !out || !k || !pr || top < 2 || top >= rows || logn < 12 || logn > 16 || K < 1) return -1;
+    const dim3 grid((1u << logn) / 1024, 2 * (top + 1), K);
     hipLaunchKernelGGL(ntt::mdr_prep_k, grid, dim3(256), 0, (hipStream_t)s, (uint32_t*)x, (const uint32_t*)onto,
                        (uint32_t*)out, k, pr, rows, top, logn);
     return launch_rc();

@@ -145,19 +145,21 @@ def _u64(xs):
 
 
 class Context:
-    """One chain on the device: tables, per-top plans and a workspace for k_rot extended ciphertexts."""
+    """One chain on the device: tables, per-top plans and a workspace for k_rot extended ciphertexts; k_max: the
+    ciphertexts a batched product or rescale takes (pcx_ctx_new_k)."""
 
-    def __init__(self, chain: Chain, k_rot=1):
+    def __init__(self, chain: Chain, k_rot=1, k_max=1):
         self.chain = chain
         self.n, self.logn = chain.n, chain.logn
         self.nq, self.kp, self.dnum, self.rows = len(chain.q), len(chain.p), chain.dnum, chain.rows
         if self.kp < 1:
             raise ValueError("a key-switching context needs at least one special prime")
         err = C.c_int(0)
-        self.h = LIB.pcx_ctx_new(chain.logn, _u64(chain.primes), self.nq, self.kp, chain.dnum, k_rot, C.byref(err))
+        self.h = LIB.pcx_ctx_new_k(chain.logn, _u64(chain.primes), self.nq, self.kp, chain.dnum, k_rot, k_max,
+                                   C.byref(err))
         if not self.h:
-            raise HipError(f"pcx_ctx_new failed: {err.value}")
-        self.k_rot = k_rot
+            raise HipError(f"pcx_ctx_new_k failed: {err.value}")
+        self.k_rot, self.k_max = k_rot, k_max
         self.ct_words = 2 * self.rows * self.n
 
     def __del__(self):
@@ -240,9 +242,13 @@ class Context:
         check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(), tmp.addr(),
                                      stream.h), "rotate_and_sum")
 
-    def rescale(self, ct, top, ndrop, out, stream):
-        """out's rows 0..top - ndrop = the rescale of ct by its top ndrop (1 or 2) primes (pcx_rescale)."""
-        check(LIB.pcx_rescale(self.h, ct.addr(), top, ndrop, out.addr(), stream.h), "rescale")
+    def rescale(self, ct, top, ndrop, out, stream, K=1):
+        """out's rows 0..top - ndrop = the rescale of ct by its top ndrop (1 or 2) primes (pcx_rescale); K > 1: K
+        consecutive ciphertexts in the same launches (pcx_rescale_k)."""
+        if K == 1:
+            check(LIB.pcx_rescale(self.h, ct.addr(), top, ndrop, out.addr(), stream.h), "rescale")
+        else:
+            check(LIB.pcx_rescale_k(self.h, ct.addr(), top, ndrop, out.addr(), K, stream.h), "rescale_k")
 
     def mul_plain(self, ct, pt, top, out, stream):
         """out = ct pt on Q rows 0..top (pcx_mul_plain); pt a DevBuf of evaluation-form rows by prime id."""
@@ -252,10 +258,15 @@ class Context:
         """out = a b relinearized by key 0 of keys (pcx_mul_relin)."""
         check(LIB.pcx_mul_relin(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h), "mul_relin")
 
-    def mul_relin_rescale(self, keys, a, b, top, out, stream):
-        """out (top - 2) = a b relinearized and rescaled by the two top primes in one ModDown (pcx_mul_relin_rescale)."""
-        check(LIB.pcx_mul_relin_rescale(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h),
-              "mul_relin_rescale")
+    def mul_relin_rescale(self, keys, a, b, top, out, stream, K=1):
+        """out (top - 2) = a b relinearized and rescaled by the two top primes in one ModDown (pcx_mul_relin_rescale);
+        K > 1: K consecutive pairs in the same launches (pcx_mul_relin_rescale_k)."""
+        if K == 1:
+            check(LIB.pcx_mul_relin_rescale(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h),
+                  "mul_relin_rescale")
+        else:
+            check(LIB.pcx_mul_relin_rescale_k(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), K, stream.h),
+                  "mul_relin_rescale_k")
 
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}

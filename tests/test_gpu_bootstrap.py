@@ -22,9 +22,11 @@ def say(*a):
 
 
 def gpu_boot(S, lanes=1):
+    """lanes 1: one stream; 2: the imaginary part's EvalMod on a second context and stream; "pair": both EvalMod
+    chains batched (K = 2) on a k_max 2 context"""
     par, q, oc = S["par"], S["q"], S["oc"]
     ch = pa.Chain("bts12", par.logn, q, [int(p) for p in oc.primes[len(q):]], oc.dnum)
-    ctx = pa.Context(ch, k_rot=8)
+    ctx = pa.Context(ch, k_rot=8, k_max=2 if lanes == "pair" else 1)
     keys = pa.Keys(ctx, S["gal"], seeds=S["seeds"], b=S["bs"])
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()
@@ -37,11 +39,12 @@ def gpu_boot(S, lanes=1):
         ops2 = B.GpuOps(ctx2, None, relin2, S["levels"], S["conj"], pa.Stream())
         ops2.keep = (ctx2, relin2)
     boot = B.Bootstrap(ops, par, q, ops2, special=S["p"] if S["fused"] else None)
+    assert boot.pair == (lanes == "pair")
     boot.prepare()
     return ctx, keys, relin, st, ops, boot
 
 
-@pytest.mark.parametrize("lanes,fused", [(1, False), (2, True), (1, True)])
+@pytest.mark.parametrize("lanes,fused", [(1, False), (2, True), (1, True), ("pair", False), ("pair", True)])
 def test_bootstrap_gpu_matches_the_oracle(lanes, fused):
     say(f"[bootstrap] N=2^12, {lanes} EvalMod lane(s), fused babies {fused}: GPU composite vs the oracle composite, "
         "decryption, rerun")
@@ -72,7 +75,7 @@ def test_bootstrap_gpu_matches_the_oracle(lanes, fused):
     assert (got2[:, : out.top + 1] == got[:, : out.top + 1]).all(), "the rerun gives the same words"
 
 
-@pytest.mark.parametrize("lanes", [1, 2])
+@pytest.mark.parametrize("lanes", [1, 2, "pair"])
 def test_bootstrap_graph_replay(lanes):
     """The whole bootstrap captured into one HIP graph (the composite's operations never allocate, synchronise or read
     device data on the host once a first run has filled the buffer pool and the constants) and replayed three times,

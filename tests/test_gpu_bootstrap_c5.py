@@ -35,8 +35,8 @@ def say(*a):
 
 @pytest.mark.timeout(1200)
 def test_bootstrap_c5_matches_the_oracle():
-    say("[bootstrap c5] N=2^16, 2^15 slots, 47 Q + 16 special primes, dnum 3, 1 -> 13 limbs, two EvalMod lanes: "
-        "oracle keys")
+    say("[bootstrap c5] N=2^16, 2^15 slots, 47 Q + 16 special primes, dnum 3, 1 -> 13 limbs, the two EvalMod chains "
+        "batched (K = 2): oracle keys")
     twin.set_threads(min(16, os.cpu_count() or 1))
     ch = pa.preset("c5")
     t0 = time.time()
@@ -49,15 +49,13 @@ def test_bootstrap_c5_matches_the_oracle():
     ct, me = encrypt(S["oc"], S["s_eval"], m, rng, 0)
     # the GPU composite: the oracle's keys uploaded, the relinearization key generated on the device from the same
     # secret, seed and errors (device key generation equals the oracle's, tests/test_gpu_parity.py)
-    ctx = pa.Context(ch, k_rot=8)
+    ctx = pa.Context(ch, k_rot=8, k_max=2)
     keys = pa.Keys(ctx, S["gal"], seeds=S["seeds"], b=S["bs"])
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()
     ops = B.GpuOps(ctx, keys, relin, S["levels"], S["conj"], st)
-    ctx2 = pa.Context(ch, k_rot=1)
-    relin2 = pa.Keys(ctx2, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
-    ops2 = B.GpuOps(ctx2, None, relin2, S["levels"], S["conj"], pa.Stream())
-    boot = B.Bootstrap(ops, par, ch.q, ops2)
+    boot = B.Bootstrap(ops, par, ch.q)
+    assert boot.pair
     boot.prepare()
     x = pa.DevBuf.from_array(ct)
     say("[bootstrap c5] GPU run")
@@ -65,7 +63,7 @@ def test_bootstrap_c5_matches_the_oracle():
     st.sync()
     got = out.h.buf.download((2, ctx.rows, ctx.n), offset=out.h.off, words=ctx.ct_words)
     say(f"[bootstrap c5] GPU output at top {out.top}, scale 2^{math.log2(out.scale):.2f}; oracle run")
-    del boot, ops, ops2, keys, relin, relin2, ctx, ctx2
+    del boot, ops, keys, relin, ctx
     t0 = time.time()
     S["boot"].prepare()
     want = S["boot"].run((ct[None], 0))

@@ -154,3 +154,63 @@ def test_mul_relin_rescale(stream, name, top, alias):
     stream.sync()
     got = out.download((2, ch.rows, ch.n))
     assert (got[:, : top - 1] == want[:, : top - 1]).all()
+
+
+_CTX2 = {}
+
+
+def batched(name):
+    """a k_max 2 context of the preset and its relinearization key (the same secret, seed and errors as relin_key's)"""
+    if name not in _CTX2:
+        ch, _, _ = contexts(name)
+        ctx2 = pa.Context(ch, k_rot=1, k_max=2)
+        _, s, seed, errs = relin_key(name)
+        _CTX2[name] = (ctx2, pa.Keys(ctx2, [1], seeds=seed[None], secret=s, errors=errs[None], relin=True))
+    return _CTX2[name]
+
+
+@pytest.mark.parametrize("name,top,alias", [("small", 5, False), ("small31", 4, True), ("c3", 29, True),
+                                            ("c5", 30, False)])
+def test_batched_product_and_rescale(stream, name, top, alias):
+    """Two pairs in one launch sequence (pcx_mul_relin_rescale_k, K = 2, on a k_max 2 context): each product's words
+    equal the K = 1 call's on a k_max 1 context (itself pinned to the oracle by test_mul_relin_rescale); the same for
+    the two-prime rescale of two ciphertexts (pcx_rescale_k); K above k_max is refused."""
+    say(f"[batched product / rescale] {name} top={top} K=2 out=a:{alias}")
+    ch, ctx, _ = contexts(name)
+    keys, _, _, _ = relin_key(name)
+    ctx2, keys2 = batched(name)
+    rng = np.random.default_rng(top * 7 + alias)
+    a = np.stack([random_ct(ch, top, rng) for _ in range(2)])
+    b = np.stack([random_ct(ch, top, rng) for _ in range(2)])
+    want = []
+    for k in range(2):
+        ba, bb, o = pa.DevBuf.from_array(a[k]), pa.DevBuf.from_array(b[k]), ctx.ct_buf(1)
+        ctx.mul_relin_rescale(keys, ba, bb, top, o, stream)
+        stream.sync()
+        want.append(o.download((2, ch.rows, ch.n)))
+    ba, bb = pa.DevBuf.from_array(a), pa.DevBuf.from_array(b)
+    out = ba if alias else ctx2.ct_buf(2)
+    ctx2.mul_relin_rescale(keys2, ba, bb, top, out, stream, K=2)
+    stream.sync()
+    got = out.download((2, 2, ch.rows, ch.n))
+    for k in range(2):
+        assert (got[k][:, : top - 1] == want[k][:, : top - 1]).all(), f"product {k}"
+    # the rescale: two ciphertexts at once against one at a time
+    x = np.stack([random_ct(ch, top, rng) for _ in range(2)])
+    wr = []
+    for k in range(2):
+        bx = pa.DevBuf.from_array(x[k])
+        ctx.rescale(bx, top, 2, bx, stream)
+        stream.sync()
+        wr.append(bx.download((2, ch.rows, ch.n)))
+    bx = pa.DevBuf.from_array(x)
+    ro = ctx2.ct_buf(2)
+    ctx2.rescale(bx, top, 2, ro, stream, K=2)
+    stream.sync()
+    gr = ro.download((2, 2, ch.rows, ch.n))
+    for k in range(2):
+        assert (gr[k][:, : top - 1] == wr[k][:, : top - 1]).all(), f"rescale {k}"
+    with pytest.raises(pa.HipError):
+        ctx2.rescale(bx, top, 2, ro, stream, K=3)
+    with pytest.raises(pa.HipError):
+        ctx.mul_relin_rescale(keys, ba, bb, top, out, stream, K=2)

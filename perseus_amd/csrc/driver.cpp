@@ -722,14 +722,14 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s, int K = 1) {
 // K consecutive ciphertexts (ct_words apart, their digits dnum rows N apart) against the same keys: extended
 // ciphertext (k, r) at ext + (k m + r) ct_words
 int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0,
-        int c0_mode = 1, int K = 1) {
+        int c0_mode = 1, int K = 1, const uint32_t* digits = nullptr) {
     const Level* L = level(c, top);
     if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || K < 1 || K > c->k_max || (sum && K > 1)) return -1;
     KsKeyArgs g;
     memset(&g, 0, sizeof g);
     KsArgs& a = g.ks;
     a.c1 = (const uint32_t*)ct + (size_t)c->rows * c->n;
-    a.modup = c->digits;
+    a.modup = digits ? digits : c->digits;
     a.c0 = ct;
     a.out0 = ext;
     a.out1 = (uint32_t*)ext + (size_t)c->rows * c->n;
@@ -1509,9 +1509,18 @@ static int rotate_many_ext(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const
     if (!c || !k || k->c != c || n < 1 || !idx || !cts || !level(c, top)) return -1;
     for (int j = 0; j < n; ++j)
         if (!cts[j] || idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
-    for (int j = 0; j < n; ++j) {
-        if (int e = modup(c, cts[j], top, s)) return e;
-        if (int e = dot(c, k, idx[j], 1, cts[j], top, c->ext, s, 0, j ? 1 | PC_KS_ACC : 1)) return e;
+    // runs of up to k_max inputs laid out ct_words apart share one ModUp launch sequence; each input's dot then reads
+    // its own digits
+    const size_t cw = c->ct_words(), dw = (size_t)c->dnum * c->rows * c->n;
+    for (int j0 = 0; j0 < n;) {
+        int m = 1;
+        while (j0 + m < n && m < c->k_max && cts[j0 + m] == (const void*)((const uint32_t*)cts[j0] + m * cw)) ++m;
+        if (int e = modup(c, cts[j0], top, s, m)) return e;
+        for (int j = j0; j < j0 + m; ++j)
+            if (int e = dot(c, k, idx[j], 1, cts[j], top, c->ext, s, 0, j ? 1 | PC_KS_ACC : 1, 1,
+                            c->digits + (size_t)(j - j0) * dw))
+                return e;
+        j0 += m;
     }
     return 0;
 }

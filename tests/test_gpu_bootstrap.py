@@ -23,10 +23,10 @@ def say(*a):
 
 def gpu_boot(S, lanes=1):
     """lanes 1: one stream; 2: the imaginary part's EvalMod on a second context and stream; "pair": both EvalMod
-    chains batched (K = 2) on a k_max 2 context"""
+    chains batched (K = 2) on a k_max 4 context (giant steps batched too)"""
     par, q, oc = S["par"], S["q"], S["oc"]
     ch = pa.Chain("bts12", par.logn, q, [int(p) for p in oc.primes[len(q):]], oc.dnum)
-    ctx = pa.Context(ch, k_rot=8, k_max=2 if lanes == "pair" else 1)
+    ctx = pa.Context(ch, k_rot=8, k_max=4 if lanes == "pair" else 1)
     keys = pa.Keys(ctx, S["gal"], seeds=S["seeds"], b=S["bs"])
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import perseus_amd as pa
+from perseus_amd import bootstrap as B
 from tests import twin
 
 pytestmark = pytest.mark.gpu
@@ -28,11 +29,11 @@ def stream():
 _CTX = {}
 
 
-def contexts(name, k_rot=4):
-    key = (name, k_rot)
+def contexts(name, k_rot=4, k_max=1):
+    key = (name, k_rot, k_max)
     if key not in _CTX:
         ch = pa.preset(name)
-        _CTX[key] = (ch, pa.Context(ch, k_rot=k_rot), twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum))
+        _CTX[key] = (ch, pa.Context(ch, k_rot=k_rot, k_max=k_max), twin.Ctx(ch.logn, ch.q, ch.p, ch.dnum))
     return _CTX[key]
 
 
@@ -383,6 +384,35 @@ def test_rotate_many_rescale(stream, name, idx, mode):
     got = out.download((2, ch.rows, ch.n))
     want = oc.rotate_many(cts, top, seeds[idx], [bs[i] for i in idx], [gals[i] for i in idx],
                           onto={"plain": None, "in_place": cts[0]}.get(mode, base), rescale=True)
+    assert (got[:, : top - 1] == want[:, : top - 1]).all()
+
+
+@pytest.mark.parametrize("name,k_max,layout", [("small", 4, [0, 1, 2, 3]), ("small", 2, [0, 1, 2, 4]),
+                                                ("small31", 3, [1, 2, 3, 0]), ("c3", 4, [0, 1, 2])])
+def test_rotate_many_batched(stream, name, k_max, layout):
+    """On a k_max > 1 context, inputs laid out ct_words apart share one ModUp launch sequence (runs of up to k_max;
+    layout[j]: input j's slot in one buffer, so a gap or a backward step ends a run): the words equal the oracle's
+    rotate_many with the rescale, as the one-ModUp-per-input path does."""
+    say(f"[rotate_many batched] {name} k_max={k_max} slots={layout}")
+    ch, ctx, oc = contexts(name, k_rot=1, k_max=k_max)
+    twin.set_threads(16)
+    idx = [0, 1, 2, 3][: len(layout)]
+    gals, seeds, bs = oracle_keys(oc, ch, [1, 3, 2, 7], seed=43)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1 if name == "c3" else 5
+    cts = [random_ct(ch, top, 51 + j) for j in range(len(layout))]
+    buf = pa.DevBuf((max(layout) + 1) * ctx.ct_words)
+    for j, sl in enumerate(layout):
+        buf.upload(cts[j], offset=sl * ctx.ct_words)
+    views = [B.View(buf, sl * ctx.ct_words) for sl in layout]
+    base = random_ct(ch, top, 50)
+    onto = pa.DevBuf.from_array(base)
+    out = ctx.ct_buf()
+    ctx.rotate_many_rescale(keys, idx, views, top, out, stream, onto=onto)
+    stream.sync()
+    got = out.download((2, ch.rows, ch.n))
+    want = oc.rotate_many(cts, top, seeds[idx], [bs[i] for i in idx], [gals[i] for i in idx], onto=base,
+                          rescale=True)
     assert (got[:, : top - 1] == want[:, : top - 1]).all()
 
 

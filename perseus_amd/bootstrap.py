@@ -363,6 +363,40 @@ class Evaluator:
         self.ops.rescale2(out, out, tc)
         return Ct(out, top, scale)
 
+    def lincombs(self, specs):
+        """lincomb of each (terms, c0, top, scale), up to three of them per weighted-sum launch over one source list
+        when the operations have wsum_multi (a source a term does not use weighs 0): the same words as one lincomb
+        at a time"""
+        if not hasattr(self.ops, "wsum_multi"):
+            return [self.lincomb(*sp) for sp in specs]
+        out = []
+        for g0 in range(0, len(specs), 3):
+            grp = specs[g0:g0 + 3]
+            srcs = []
+            for terms, _, _, _ in grp:
+                for a, _ in terms:
+                    if not any(x.h is a.h for x in srcs):
+                        srcs.append(a)
+            if len(srcs) > 8:
+                out += [self.lincomb(*sp) for sp in grp]
+                continue
+            outs, tcs, ks, k0s = [], [], [], []
+            for terms, c0, top, scale in grp:
+                tc = top + 2
+                qq = self.qq(tc)
+                for a, _ in terms:
+                    assert a.top >= tc, (a.top, tc)
+                w = {id(a.h): int(round(c * scale * qq / a.scale)) for a, c in terms}
+                ks.append([w.get(id(x.h), 0) for x in srcs])
+                k0s.append(int(round(c0 * scale * qq)))
+                outs.append(self.ops.alloc())
+                tcs.append(tc)
+            self.ops.wsum_multi(outs, [x.h for x in srcs], tcs, ks, k0s)
+            for o, tc, (_, _, top, scale) in zip(outs, tcs, grp):
+                self.ops.rescale2(o, o, tc)
+                out.append(Ct(o, top, scale))
+        return out
+
     def add(self, a, b, sub=False):
         assert abs(a.scale / b.scale - 1.0) < 1e-9, (a.scale, b.scale)
         t = min(a.top, b.top)
@@ -412,20 +446,30 @@ class ChebEval:
         """the top the series lands on: the leaves need a product below T_7's top, and three giant products follow"""
         return self.T[7].top - 2 - 6
 
-    def eval(self, c, top, scale):
+    def _walk(self, c, top, scale, leaf):
+        """the split recursion: leaf(terms, c0, top, scale) for a leaf, else Q T_g + R with Q and R walked first"""
         c = np.trim_zeros(np.asarray(c, np.float64), "b")
         ev, T = self.ev, self.T
         if len(c) <= self.BABY:
             terms = [(T[k], float(c[k])) for k in range(1, len(c)) if c[k] != 0.0]
             assert terms, "a leaf with no term of degree >= 1"
-            return ev.lincomb(terms, float(c[0]), top, scale)
+            return leaf(terms, float(c[0]), top, scale)
         g = max(x for x in self.GIANTS if x < len(c))
         q, r = cheb_split(c, g)
         G = T[g]
         assert G.top >= top + 2
-        Q = self.eval(q, top + 2, scale * ev.qq(top + 2) / G.scale)
-        P = ev.mul(Q, Ct(G.h, top + 2, G.scale))
-        return ev.add(P, self.eval(r, top, scale))
+        Q = self._walk(q, top + 2, scale * ev.qq(top + 2) / G.scale, leaf)
+        R = self._walk(r, top, scale, leaf)
+        if Q is None:
+            return None
+        return ev.add(ev.mul(Q, Ct(G.h, top + 2, G.scale)), R)
+
+    def eval(self, c, top, scale):
+        """every leaf first (their weighted sums grouped over the shared T_k), then the products and sums"""
+        specs = []
+        self._walk(c, top, scale, lambda *sp: specs.append(sp))
+        vals = iter(self.ev.lincombs(specs))
+        return self._walk(c, top, scale, lambda *sp: next(vals))
 
 
 # ----------------------------------------------------------------------------------------------- the composite
@@ -668,6 +712,9 @@ class PairOps:
     def wsum(self, out, srcs, top, ks, k0):
         self.o.wsum(out, srcs, top, ks, k0, K=2)
 
+    def wsum_multi(self, outs, srcs, tops, ks, k0s):
+        self.o.wsum_multi(outs, srcs, tops, ks, k0s, K=2)
+
     def mul_relin_rescale(self, out, a, b, top):
         self.o.mul_relin_rescale(out, a, b, top, K=2)
 
@@ -778,6 +825,30 @@ class GpuOps:
         a.w.nsrc, a.w.rowstride, a.w.n, a.w.K = len(srcs), self.R, top + 1, K
         a.k = bk.ptr.value
         self._call("wsum_k", a)
+
+    def wsum_multi(self, outs, srcs, tops, ks, k0s, K=1):
+        """up to 3 weighted sums of one source list in one launch (the table's wsum_multi): outs[m] = sum_j ks[m][j]
+        srcs[j] + k0s[m] on rows 0..tops[m]"""
+        key = ("wm", tuple(tuple(k) for k in ks), tuple(k0s))
+        if key not in self.cache:
+            bufs = []
+            for km, k0 in zip(ks, k0s):
+                w = np.array([[k % p for p in self.primes] for k in km], np.uint32)
+                ws = np.array([[(int(v) << 32) // p for v, p in zip(r, self.primes)] for r in w], np.uint64)
+                kr = np.array([k0 % p for p in self.primes], np.uint32)
+                bufs.append(tuple(self.eng.DevBuf.from_array(v) for v in (w, ws.astype(np.uint32), kr)))
+            self.cache[key] = bufs
+        bufs = self.cache[key]
+        a = self.abi.WsumMultiArgs()
+        for m, o in enumerate(outs):
+            a.out[m] = self._ref(o)
+            a.w[m], a.ws[m], a.k[m] = (b.ptr.value for b in bufs[m])
+            a.n[m] = tops[m] + 1
+        for j, x in enumerate(srcs):
+            a.src[j] = self._ref(x)
+        a.pr, a.nout, a.nsrc, a.rowstride, a.K = self.pr, len(outs), len(srcs), self.R, K
+        a.nmax = max(t + 1 for t in tops)
+        self._call("wsum_multi", a)
 
     def mul_pt(self, out, x, top, pt):
         a = self.abi.MulTableArgs()

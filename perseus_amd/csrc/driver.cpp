@@ -1174,8 +1174,17 @@ pcx_rows* pcx_rows_new(pcx_ctx* c, const uint32_t* roff, const int32_t* ids, int
         if (ids[i] < 0 || ids[i] >= c->rows) return nullptr;
     pcx_rows* r = new (std::nothrow) pcx_rows;
     if (!r) return nullptr;
-    std::vector<uint32_t> ro(roff, roff + nrows);
-    std::vector<int32_t> rp(ids, ids + nrows);
+    // prime-major (a stable sort by prime id): the rows are independent, and neighbouring workgroups then read one
+    // prime's twiddle tables from L2 instead of each row's from further out
+    std::vector<int> ord(nrows);
+    for (int i = 0; i < nrows; ++i) ord[i] = i;
+    std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return ids[a] < ids[b]; });
+    std::vector<uint32_t> ro(nrows);
+    std::vector<int32_t> rp(nrows);
+    for (int i = 0; i < nrows; ++i) {
+        ro[i] = roff[ord[i]];
+        rp[i] = ids[ord[i]];
+    }
     if (fill_rows(r->dev, r->r, ro, rp, nullptr, nullptr)) {
         delete r;
         return nullptr;

@@ -935,9 +935,10 @@ int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top
 int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s);
 /* pcx_mul_relin_rescale of K <= k_max pairs: a, b and out each K consecutive ciphertexts (ct_words apart), product k
  * = a_k b_k, every stage one launch for the K (the tensor, ModUp, key dot and fused ModDown-rescale of
- * crates/pc-gpu/src/relin.rs:213-235 at K ciphertexts); each product's words are those of the K = 1 call. */
+ * crates/pc-gpu/src/relin.rs:213-235 at K ciphertexts); each product's words are those of the K = 1 call. twice
+ * nonzero: the tensor's outputs doubled (its dbl, args.cuh TensorArgs), the words of the product of 2a and b. */
 int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, int K,
-                            pc_stream_t s);
+                            int twice, pc_stream_t s);
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
  * form rows by prime id (rows 0..top read). out may be ct. */
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);

@@ -335,10 +335,11 @@ class Evaluator:
         """the two primes the rescale from `top` drops"""
         return float(self.q[top]) * float(self.q[top - 1])
 
-    def mul(self, a, b):
+    def mul(self, a, b, twice=False):
+        """a b, or 2 a b (twice: the doubling folded into the product, the words of mul(double(a), b))"""
         t = min(a.top, b.top)
         out = self.ops.alloc()
-        self.ops.mul_relin_rescale(out, a.h, b.h, t)
+        self.ops.mul_relin_rescale(out, a.h, b.h, t, twice)
         return Ct(out, t - 2, a.scale * b.scale / self.qq(t))
 
     def mul_to(self, a, c, scale, top):
@@ -431,7 +432,7 @@ class ChebEval:
         T = {1: u}
 
         def make(a, b):
-            P = ev.mul(ev.double(T[a]), T[b])
+            P = ev.mul(T[a], T[b], twice=True)
             if a == b:
                 return ev.add_const(P, -1.0)
             return ev.add(P, ev.mul_to(T[a - b], 1.0, P.scale, P.top), sub=True)
@@ -600,7 +601,7 @@ class Bootstrap:
         top = ce.out_top()
         h = ce.eval(self.em.c, top, ev.qq(top))
         for _ in range(self.par.r):
-            h = ev.add_const(ev.mul(ev.double(h), h), -1.0)
+            h = ev.add_const(ev.mul(h, h, twice=True), -1.0)
         return h
 
     def run(self, x_h):
@@ -715,8 +716,8 @@ class PairOps:
     def wsum_multi(self, outs, srcs, tops, ks, k0s):
         self.o.wsum_multi(outs, srcs, tops, ks, k0s, K=2)
 
-    def mul_relin_rescale(self, out, a, b, top):
-        self.o.mul_relin_rescale(out, a, b, top, K=2)
+    def mul_relin_rescale(self, out, a, b, top, twice=False):
+        self.o.mul_relin_rescale(out, a, b, top, K=2, twice=twice)
 
     def rescale2(self, out, x, top):
         self.o.rescale2(out, x, top, K=2)
@@ -961,8 +962,8 @@ class GpuOps:
     def mul_relin(self, out, a, b, top):
         self.ctx.mul_relin(self.relin, a, b, top, out, self.st)
 
-    def mul_relin_rescale(self, out, a, b, top, K=1):
-        self.ctx.mul_relin_rescale(self.relin, a, b, top, out, self.st, K=K)
+    def mul_relin_rescale(self, out, a, b, top, twice=False, K=1):
+        self.ctx.mul_relin_rescale(self.relin, a, b, top, out, self.st, K=K, twice=twice)
 
     def rescale2(self, out, x, top, K=1):
         self.ctx.rescale(x, top, 2, out, self.st, K=K)

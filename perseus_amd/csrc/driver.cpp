@@ -1668,7 +1668,7 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
 // (ext - conv) P^-1 on Q rows 0..top. out may be a or b.
 // the product's (d0, d1) into out and the key switch of d2 into c->ext (before ModDown)
 static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s,
-                     int K = 1) {
+                     int K = 1, int twice = 0) {
     if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
     if (K < 1 || K > c->k_max) return -1;
     const uint64_t part = (uint64_t)c->rows * c->n;
@@ -1682,6 +1682,7 @@ static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int 
     t.npairs = 1;
     t.n = top + 1;
     t.K = K;
+    t.dbl = twice ? 1 : 0;  // 2 (a b): the same residues as the product of 2a and b
     {
         Stage st(c, 8, s);
         if (int e = c->tab->tensor(&t, s)) return e;
@@ -1695,12 +1696,12 @@ int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top
 }
 int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out,
                           pc_stream_t s) {
-    return pcx_mul_relin_rescale_k(c, k, a, b, top, out, 1, s);
+    return pcx_mul_relin_rescale_k(c, k, a, b, top, out, 1, 0, s);
 }
 int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, int K,
-                            pc_stream_t s) {
+                            int twice, pc_stream_t s) {
     if (top < 2) return -1;
-    if (int e = relin_ext(c, k, a, b, top, out, s, K)) return e;
+    if (int e = relin_ext(c, k, a, b, top, out, s, K, twice)) return e;
     return moddown_rescale(c, c->ext, top, out, out, s, K);
 }
 

@@ -258,15 +258,15 @@ class Context:
         """out = a b relinearized by key 0 of keys (pcx_mul_relin)."""
         check(LIB.pcx_mul_relin(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h), "mul_relin")
 
-    def mul_relin_rescale(self, keys, a, b, top, out, stream, K=1):
+    def mul_relin_rescale(self, keys, a, b, top, out, stream, K=1, twice=False):
         """out (top - 2) = a b relinearized and rescaled by the two top primes in one ModDown (pcx_mul_relin_rescale);
-        K > 1: K consecutive pairs in the same launches (pcx_mul_relin_rescale_k)."""
-        if K == 1:
+        K > 1: K consecutive pairs in the same launches, twice: 2 a b (pcx_mul_relin_rescale_k)."""
+        if K == 1 and not twice:
             check(LIB.pcx_mul_relin_rescale(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h),
                   "mul_relin_rescale")
         else:
-            check(LIB.pcx_mul_relin_rescale_k(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), K, stream.h),
-                  "mul_relin_rescale_k")
+            check(LIB.pcx_mul_relin_rescale_k(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), K, int(twice),
+                                              stream.h), "mul_relin_rescale_k")
 
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}

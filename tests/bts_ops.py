@@ -134,8 +134,12 @@ class OracleOps:
     def mul_relin(self, out, a, b, top):
         self.get(out)[:] = self.oc.mul_relin(self.get(a), self.get(b), top, self.relin_seed, self.relin_b)
 
-    def mul_relin_rescale(self, out, a, b, top):
-        self.get(out)[:] = self.oc.mul_relin_rescale(self.get(a), self.get(b), top, self.relin_seed, self.relin_b)
+    def mul_relin_rescale(self, out, a, b, top, twice=False):
+        x = self.get(a)
+        if twice:  # the doubling as the composite's add(a, a) would make it, then the product
+            x = x.copy()
+            self.add((x[None], 0), (x[None], 0), (x[None], 0), top, False)
+        self.get(out)[:] = self.oc.mul_relin_rescale(x, self.get(b), top, self.relin_seed, self.relin_b)
 
     def rescale2(self, out, x, top):
         self.get(out)[:] = self.oc.rescale(self.get(x).copy(), top, 2)

@@ -214,3 +214,26 @@ def test_batched_product_and_rescale(stream, name, top, alias):
         ctx2.rescale(bx, top, 2, ro, stream, K=3)
     with pytest.raises(pa.HipError):
         ctx.mul_relin_rescale(keys, ba, bb, top, out, stream, K=2)
+
+
+@pytest.mark.parametrize("name,top,K", [("small", 5, 1), ("small31", 4, 2), ("c5", 24, 2)])
+def test_product_twice(stream, name, top, K):
+    """The doubling folded into the product (pcx_mul_relin_rescale_k with twice: the tensor's outputs doubled): the
+    words of the oracle's product of 2a (mod q) and b, for each of K pairs."""
+    say(f"[product twice] {name} top={top} K={K}")
+    ch, _, oc = contexts(name)
+    ctx2, keys2 = batched(name)
+    _, _, seed, _ = relin_key(name)
+    rng = np.random.default_rng(top + 17 * K)
+    a = np.stack([random_ct(ch, top, rng) for _ in range(K)])
+    b = np.stack([random_ct(ch, top, rng) for _ in range(K)])
+    ba, bb, out = pa.DevBuf.from_array(a), pa.DevBuf.from_array(b), ctx2.ct_buf(K)
+    ctx2.mul_relin_rescale(keys2, ba, bb, top, out, stream, K=K, twice=True)
+    stream.sync()
+    got = out.download((K, 2, ch.rows, ch.n))
+    q = np.array(ch.primes[: top + 1], np.uint64)[None, :, None]
+    for k in range(K):
+        a2 = a[k].copy()
+        a2[:, : top + 1] = (2 * a[k][:, : top + 1].astype(np.uint64) % q).astype(np.uint32)
+        want = oc.mul_relin_rescale(a2, b[k], top, seed, keys2.download_b(0))
+        assert (got[k][:, : top - 1] == want[:, : top - 1]).all(), f"pair {k}"

@@ -815,8 +815,9 @@ int pc_hip_last_error(void);
  * a workspace for up to k_rot extended ciphertexts per hoisted chunk. Errors: NULL, with *err set. */
 typedef struct pcx_ctx pcx_ctx;
 pcx_ctx* pcx_ctx_new(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int* err);
-/* pcx_ctx_new with plans and workspace for K-ciphertext products and rescales, K <= k_max <= 4 (the reference's
- * k_max, crates/pc-gpu/src/ops.rs:1554-1595: K ciphertexts per launch); pcx_ctx_new is k_max 1. */
+/* pcx_ctx_new with plans and workspace for K-ciphertext ModUps, products and rescales, K <= k_max <= 8 (the
+ * reference's k_max, crates/pc-gpu/src/ops.rs:1554-1595: K ciphertexts per launch; a product's key dot takes at most
+ * 4); pcx_ctx_new is k_max 1. */
 pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, int dnum, int k_rot, int k_max,
                        int* err);
 void pcx_ctx_free(pcx_ctx* c);
@@ -894,6 +895,13 @@ int pcx_rotate_many_rescale(pcx_ctx* c, pcx_keys* k, const int* idx, int n, cons
  * ciphertext. The group must hold the key of every step the ladder takes (-1 otherwise). */
 int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
                        void* out, void* tmp, pc_stream_t s);
+/* pcx_rotate_and_sum of K consecutive ciphertexts (x, out and tmp each K ciphertexts, ct_words apart; K <= the
+ * context's k_max and k_rot): when every rung is a radix rung (2 to 8 bits) whose steps the group holds, the K go
+ * rung by rung together, each rung one ModUp launch sequence and one ModDown for the K (the reference's K-ciphertext
+ * launches, crates/pc-gpu/src/ops.rs:1554-1595); otherwise each takes pcx_rotate_and_sum. Each output's words are
+ * those of the one-ciphertext ladder. */
+int pcx_rotate_and_sum_k(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop,
+                         int radix_bits, void* out, void* tmp, int K, pc_stream_t s);
 /* No counterpart in the reference: pcx_rotate_and_sum for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation). The scratch ciphertext is a file-scope device
  * array of PCX_NOALLOC_SCRATCH_WORDS u32 words (32 MiB per device, held until the process ends) instead of tmp; the

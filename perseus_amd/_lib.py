@@ -75,6 +75,7 @@ _SIGS = {
     "pcx_ntt_one_pass_min": (C.c_int, [C.c_int]),
     "pcx_rotate_many": (C.c_int, [vp, vp, C.POINTER(C.c_int), C.c_int, C.POINTER(vp), C.c_int, vp, vp, vp]),
     "pcx_rotate_and_sum": (C.c_int, [vp, vp, vp, C.c_int, C.c_int64, C.c_int64, C.c_int, vp, vp, vp]),
+    "pcx_rotate_and_sum_k": (C.c_int, [vp, vp, vp, C.c_int, C.c_int64, C.c_int64, C.c_int, vp, vp, C.c_int, vp]),
     "pcx_rotate_and_sum_noalloc": (C.c_int, [vp, vp, vp, C.c_int, C.c_int64, C.c_int64, C.c_int, vp, vp]),
     "pcx_cts_stage": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_uint32, vp, C.c_int, vp,
                                 vp]),

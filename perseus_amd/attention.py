@@ -87,6 +87,21 @@ def score(ctx, keys, ct, pt, top, out, tmp, stream, radix_bits=RADIX_BITS):
     ctx.rotate_and_sum(keys, out, top - 2, 1, BLOCK, out, tmp, stream, radix_bits=radix_bits)
 
 
+def score_batch(ctx, keys, cts, pts, top, outs, tmp, stream, radix_bits=RADIX_BITS):
+    """Every ciphertext's scores at once: cts, outs and tmp each K consecutive ciphertexts of one buffer (the ctx's
+    k_max and k_rot at least K), pts the K plaintexts; the plaintext products one per ciphertext, then the two-prime
+    rescale and the ladder as K-ciphertext launches (pcx_rescale_k, pcx_rotate_and_sum_k). The words of score() on
+    each ciphertext."""
+    from .bootstrap import View
+
+    K = len(pts)
+    for j, pt in enumerate(pts):
+        ctx.mul_plain(View(cts.buf, cts.off + j * ctx.ct_words), pt, top, View(outs.buf, outs.off + j * ctx.ct_words),
+                      stream)
+    ctx.rescale(outs, top, 2, outs, stream, K=K)
+    ctx.rotate_and_sum(keys, outs, top - 2, 1, BLOCK, outs, tmp, stream, radix_bits=radix_bits, K=K)
+
+
 def score_streams(lanes, cts, pts, top, outs, main, radix_bits=RADIX_BITS):
     """The scorings of independent ciphertexts side by side: lane i = (context, keys, stream, tmp) takes ciphertexts
     i, i + len(lanes), ...; each lane has its own context (its own workspace), so the lanes' small kernels overlap on

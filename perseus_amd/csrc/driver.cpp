@@ -967,7 +967,7 @@ pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, i
     if (!err) err = &dummy;
     *err = 0;
     const KernelTable* tab = pc_table_u32_logn(log_n);
-    if (!tab || nq < 1 || kp < 1 || dnum < 1 || dnum > nq || k_rot < 1 || k_max < 1 || k_max > 4 || !primes) {
+    if (!tab || nq < 1 || kp < 1 || dnum < 1 || dnum > nq || k_rot < 1 || k_max < 1 || k_max > 8 || !primes) {
         *err = -1;
         return nullptr;
     }
@@ -1548,6 +1548,76 @@ int pcx_rotate_many_rescale(pcx_ctx* c, pcx_keys* k, const int* idx, int n, cons
     return moddown_rescale(c, c->ext, top, out, onto, s);
 }
 
+// pcx_rotate_sum over K <= min(k_max, k_rot) consecutive ciphertexts: one ModUp launch sequence for the K, each
+// ciphertext's summed key dots into its own extended slot (reading its own digits), one ModDown of the K onto onto
+static int rotate_sum_k(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int K, int top, void* out,
+                        const void* onto, pc_stream_t s) {
+    if (K < 1 || K > c->k_max || K > c->k_rot) return -1;
+    for (int j = 0; j < n; ++j)
+        if (idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
+    const size_t cw = c->ct_words(), dw = (size_t)c->dnum * c->rows * c->n;
+    if (int e = modup(c, ct, top, s, K)) return e;
+    for (int kk = 0; kk < K; ++kk) {
+        const void* ck = (const uint32_t*)ct + kk * cw;
+        for (int j = 0; j < n;) {
+            int m = 1;
+            while (j + m < n && idx[j + m] == idx[j] + m) ++m;
+            if (int e = dot(c, k, idx[j], m, ck, top, c->ext + kk * cw, s, j == 0 ? 1 : 2, 1, 1, c->digits + kk * dw))
+                return e;
+            j += m;
+        }
+    }
+    return moddown(c, c->ext, c->conv, K, top, out, s, onto);
+}
+
+int pcx_rotate_and_sum_k(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop,
+                         int radix_bits, void* out, void* tmp, int K, pc_stream_t s) {
+    if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top) || K < 1) return -1;
+    const size_t cw = c->ct_words();
+    if (K == 1) return pcx_rotate_and_sum(c, k, x, top, start, stop, radix_bits, out, tmp, s);
+    if (start == 0 || stop <= 0 || K > c->k_max || K > c->k_rot) return -1;
+    const uint64_t m2 = 2ull * c->n;
+    auto key_of = [&](int64_t st) {
+        const int64_t h = (int64_t)(c->n / 2);
+        const uint64_t r = (uint64_t)(((st % h) + h) % h);
+        const uint64_t g = powmod(5, r, m2);
+        for (int i = 0; i < k->nkeys; ++i)
+            if (k->galois[i] == g) return i;
+        return -1;
+    };
+    const int64_t sign = start > 0 ? 1 : -1, gap = start > 0 ? start : -start;
+    if (gap >= stop) return copy_q(c, x, top, out, s, K);
+    int64_t gaps[64];
+    size_t ng = 0;
+    for (int64_t g = gap; g < stop && ng < 64; g *= 2) gaps[ng++] = g;
+    // every rung a radix rung of at most 8 bits whose steps the group holds: the K ciphertexts go rung by rung
+    // together; otherwise each takes the one-ciphertext ladder
+    const size_t rb = radix_bits >= 2 ? (size_t)radix_bits : 1;
+    bool batched = rb >= 2 && rb <= 8;
+    int keys[64][255];
+    int cnts[64];
+    size_t nr = 0;
+    for (size_t i0 = 0; batched && i0 < ng; ++nr) {
+        const size_t n = std::min(rb, ng - i0);
+        cnts[nr] = (int)(((int64_t)1 << n) - 1);
+        for (int j = 1; j <= cnts[nr] && batched; ++j) batched = (keys[nr][j - 1] = key_of(sign * j * gaps[i0])) >= 0;
+        batched = batched && n > 1;
+        i0 += n;
+    }
+    if (!batched) {
+        for (int kk = 0; kk < K; ++kk)
+            if (int e = pcx_rotate_and_sum(c, k, (const uint32_t*)x + kk * cw, top, start, stop, radix_bits,
+                                           (uint32_t*)out + kk * cw, (uint32_t*)tmp + kk * cw, s))
+                return e;
+        return 0;
+    }
+    if (x != out)
+        if (int e = copy_q(c, x, top, out, s, K)) return e;
+    for (size_t r = 0; r < nr; ++r)
+        if (int e = rotate_sum_k(c, k, keys[r], cnts[r], out, K, top, out, out, s)) return e;
+    return 0;
+}
+
 int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
                        void* out, void* tmp, pc_stream_t s) {
     if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top)) return -1;
@@ -1670,7 +1740,7 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
 static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s,
                      int K = 1, int twice = 0) {
     if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
-    if (K < 1 || K > c->k_max) return -1;
+    if (K < 1 || K > c->k_max || K > 4) return -1;  // the key dot takes at most 4 ciphertexts
     const uint64_t part = (uint64_t)c->rows * c->n;
     TensorArgs t;
     memset(&t, 0, sizeof t);

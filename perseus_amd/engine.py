@@ -237,10 +237,15 @@ class Context:
         check(LIB.pcx_rotate_many_rescale(self.h, keys.h, arr, len(idx), ptrs, top, out.addr(),
                                           None if onto is None else onto.addr(), stream.h), "rotate_many_rescale")
 
-    def rotate_and_sum(self, keys, x, top, start, stop, out, tmp, stream, radix_bits=1):
-        """The rotate-and-sum ladder: out = sum of x over its rotations by the multiples of start below stop."""
-        check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(), tmp.addr(),
-                                     stream.h), "rotate_and_sum")
+    def rotate_and_sum(self, keys, x, top, start, stop, out, tmp, stream, radix_bits=1, K=1):
+        """The rotate-and-sum ladder: out = sum of x over its rotations by the multiples of start below stop; K > 1: K
+        consecutive ciphertexts rung by rung together (pcx_rotate_and_sum_k)."""
+        if K == 1:
+            check(LIB.pcx_rotate_and_sum(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(),
+                                         tmp.addr(), stream.h), "rotate_and_sum")
+        else:
+            check(LIB.pcx_rotate_and_sum_k(self.h, keys.h, x.addr(), top, start, stop, radix_bits, out.addr(),
+                                           tmp.addr(), K, stream.h), "rotate_and_sum_k")
 
     def rescale(self, ct, top, ndrop, out, stream, K=1):
         """out's rows 0..top - ndrop = the rescale of ct by its top ndrop (1 or 2) primes (pcx_rescale); K > 1: K

@@ -416,6 +416,36 @@ def test_rotate_many_batched(stream, name, k_max, layout):
     assert (got[:, : top - 1] == want[:, : top - 1]).all()
 
 
+@pytest.mark.parametrize("name,K,radix", [("small", 3, 2), ("small", 2, 1), ("c3", 4, 2), ("small31", 6, 3)])
+def test_rotate_and_sum_batched(stream, name, K, radix):
+    """The ladder over K consecutive ciphertexts (pcx_rotate_and_sum_k on a k_max = k_rot = K context): each output
+    equals the one-ciphertext ladder's words (radix 1 takes the per-ciphertext fallback)."""
+    say(f"[rotate_and_sum batched] {name} K={K} radix_bits={radix}")
+    ch, ctx, oc = contexts(name, k_rot=4)
+    ch2, ctxk, _ = contexts(name, k_rot=K, k_max=K)
+    twin.set_threads(16)
+    steps = [1, 2, 3, 4, 8, 12] if radix != 3 else [1, 2, 3, 4, 5, 6, 7, 8]
+    gals, seeds, bs = oracle_keys(oc, ch, steps, seed=19)
+    keys = pa.Keys(ctx, gals, seeds=seeds, b=bs, bits=0)
+    keysk = pa.Keys(ctxk, gals, seeds=seeds, b=bs, bits=0)
+    top = len(ch.q) - 1 if name == "c3" else 5
+    cts = [random_ct(ch, top, 60 + j) for j in range(K)]
+    stop = 16 if radix != 3 else 8
+    want = []
+    for x in cts:
+        dev, out, tmp = pa.DevBuf.from_array(x), ctx.ct_buf(), ctx.ct_buf()
+        ctx.rotate_and_sum(keys, dev, top, 1, stop, out, tmp, stream, radix_bits=radix)
+        stream.sync()
+        want.append(out.download((2, ch.rows, ch.n)))
+    xb = pa.DevBuf.from_array(np.stack(cts))
+    ob, tb = ctxk.ct_buf(K), ctxk.ct_buf(K)
+    ctxk.rotate_and_sum(keysk, xb, top, 1, stop, ob, tb, stream, radix_bits=radix, K=K)
+    stream.sync()
+    got = ob.download((K, 2, ch.rows, ch.n))
+    for j in range(K):
+        assert (got[j][:, : top + 1] == want[j][:, : top + 1]).all(), f"ciphertext {j}"
+
+
 @pytest.mark.parametrize("name,radix", [("small", 1), ("small", 2), ("c3", 2)])
 def test_rotate_and_sum(stream, name, radix):
     say(f"[rotate_and_sum] {name} start=1 stop=16 radix_bits={radix}")

@@ -724,7 +724,7 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s, int K = 1) {
 int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0,
         int c0_mode = 1, int K = 1, const uint32_t* digits = nullptr) {
     const Level* L = level(c, top);
-    if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || K < 1 || K > c->k_max || (sum && K > 1)) return -1;
+    if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || K < 1 || K > c->k_max || K > 4) return -1;
     KsKeyArgs g;
     memset(&g, 0, sizeof g);
     KsArgs& a = g.ks;
@@ -744,7 +744,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     a.ct_stride = c->ct_words();
     a.mu_ct_stride = (uint64_t)c->dnum * c->rows * c->n;
     a.mu_digit_stride = (uint64_t)c->rows * c->n;
-    a.out_ct_stride = (uint64_t)m * c->ct_words();
+    a.out_ct_stride = (uint64_t)(sum ? 1 : m) * c->ct_words();  // a sum: one extended ciphertext per ciphertext
     a.out_rot_stride = c->ct_words();
     a.key_digit_stride = 0;
     a.K = K;
@@ -1557,15 +1557,17 @@ static int rotate_sum_k(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const vo
         if (idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
     const size_t cw = c->ct_words(), dw = (size_t)c->dnum * c->rows * c->n;
     if (int e = modup(c, ct, top, s, K)) return e;
-    for (int kk = 0; kk < K; ++kk) {
-        const void* ck = (const uint32_t*)ct + kk * cw;
-        for (int j = 0; j < n;) {
-            int m = 1;
-            while (j + m < n && idx[j + m] == idx[j] + m) ++m;
-            if (int e = dot(c, k, idx[j], m, ck, top, c->ext + kk * cw, s, j == 0 ? 1 : 2, 1, 1, c->digits + kk * dw))
+    // runs of consecutive keys, each one summed dot over up to 4 of the ciphertexts at a time
+    for (int j = 0; j < n;) {
+        int m = 1;
+        while (j + m < n && idx[j + m] == idx[j] + m) ++m;
+        for (int k0 = 0; k0 < K; k0 += 4) {
+            const int kc = std::min(4, K - k0);
+            if (int e = dot(c, k, idx[j], m, (const uint32_t*)ct + k0 * cw, top, c->ext + k0 * cw, s, j == 0 ? 1 : 2, 1,
+                            kc, c->digits + k0 * dw))
                 return e;
-            j += m;
         }
+        j += m;
     }
     return moddown(c, c->ext, c->conv, K, top, out, s, onto);
 }

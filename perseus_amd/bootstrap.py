@@ -554,14 +554,17 @@ class Bootstrap:
         mono_m[:, N // 2] = [p - 1 for p in self.q]  # -X^(N/2): -i
         self.mono_mi = ops.plaintext(mono_m, self.T)
 
-    def lt(self, x, plan, pts, f, s=0):
-        """one BSGS level: pts its diagonals (None where zero), s their compact shift (rows of width N >> s)"""
+    def lt(self, x, plan, pts, f, s=0, rots=None, dest=None):
+        """one BSGS level: pts its diagonals (None where zero), s their compact shift (rows of width N >> s). rots: a
+        buffer of B ciphertexts whose first already holds x (else x is copied into a new one); dest: where the output
+        goes (else a new ciphertext)"""
         ops, top = self.ops, x.top
         B, G = plan.B, plan.G
         res = ops.alloc(G)
         if self.p is None:
-            rots = ops.alloc(B)
-            ops.copy(ops.item(rots, 0), x.h, top)
+            if rots is None:
+                rots = ops.alloc(B)
+                ops.copy(ops.item(rots, 0), x.h, top)
             ops.hoisted(ops.item(rots, 1), x.h, top, [b % self.par.n for b in plan.baby[1:]])
             ops.pt_dot(res, rots, top, pts, B, G, s)
         else:
@@ -585,7 +588,7 @@ class Bootstrap:
                 t = ops.alloc()
                 ops.add(t, base, y, top, False)
                 base = t
-        out = ops.alloc()
+        out = ops.alloc() if dest is None else dest
         if ys:
             # the rescale by the two top primes fused into the sum's ModDown
             ops.rotate_many_rescale(out, ys, top, gs, base)
@@ -611,13 +614,20 @@ class Bootstrap:
         ops.begin()
         if self.ops2 is not None:
             self.ops2.begin()
-        raised = ops.alloc()
+        # each level's input is written straight into the first slot of that level's rotation buffer (the plaintext
+        # dot reads the unrotated input there), so no level copies it
+        hoist = self.p is None
+        nxt = ops.alloc(self.cts[0].B) if hoist else None
+        raised = ops.item(nxt, 0) if hoist else ops.alloc()
         ops.mod_raise(raised, x_h, self.T)
         ops.mul_const(raised, raised, self.T, self.lift)
         x = Ct(raised, self.T, self.raise_scale)
         k = 0
-        for p in self.cts:
-            x = self.lt(x, p, self.pts[k], self.cts_f, self.pt_s[k])
+        for i, p in enumerate(self.cts):
+            rots = nxt
+            nxt = ops.alloc(self.cts[i + 1].B) if hoist and i + 1 < len(self.cts) else None
+            x = self.lt(x, p, self.pts[k], self.cts_f, self.pt_s[k], rots=rots,
+                        dest=ops.item(nxt, 0) if nxt is not None else None)
             k += 1
         cj = ops.alloc()
         ops.rotate(cj, x.h, x.top, "conj")
@@ -642,9 +652,18 @@ class Bootstrap:
             ops.join(self.ops2)
         ii = ops.alloc()
         ops.mul_pt(ii, im.h, im.top, self.mono_i)
-        w = ev.add(re, Ct(ii, im.top, im.scale))
-        for p in self.stc:
-            w = self.lt(w, p, self.pts[k], 1.0, self.pt_s[k])
+        nxt = ops.alloc(self.stc[0].B) if hoist else None
+        if hoist:
+            assert abs(re.scale / im.scale - 1.0) < 1e-9 and re.top == im.top
+            ops.add(ops.item(nxt, 0), re.h, ii, re.top, False)
+            w = Ct(ops.item(nxt, 0), re.top, re.scale)
+        else:
+            w = ev.add(re, Ct(ii, im.top, im.scale))
+        for i, p in enumerate(self.stc):
+            rots = nxt
+            nxt = ops.alloc(self.stc[i + 1].B) if hoist and i + 1 < len(self.stc) else None
+            w = self.lt(w, p, self.pts[k], 1.0, self.pt_s[k], rots=rots,
+                        dest=ops.item(nxt, 0) if nxt is not None else None)
             k += 1
         # the slot values are now (2 pi / q0) times the message's at the input's scale: relabel
         w.scale = w.scale * 2.0 * math.pi * par.delta_in / self.q0

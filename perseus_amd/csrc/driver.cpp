@@ -722,7 +722,7 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s, int K = 1) {
 // K consecutive ciphertexts (ct_words apart, their digits dnum rows N apart) against the same keys: extended
 // ciphertext (k, r) at ext + (k m + r) ct_words
 int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, pc_stream_t s, int sum = 0,
-        int c0_mode = 1, int K = 1, const uint32_t* digits = nullptr) {
+        int c0_mode = 1, int K = 1, const uint32_t* digits = nullptr, const void* c0 = nullptr) {
     const Level* L = level(c, top);
     if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || K < 1 || K > c->k_max || K > 4) return -1;
     KsKeyArgs g;
@@ -730,7 +730,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     KsArgs& a = g.ks;
     a.c1 = (const uint32_t*)ct + (size_t)c->rows * c->n;
     a.modup = digits ? digits : c->digits;
-    a.c0 = ct;
+    a.c0 = c0 ? c0 : ct;
     a.out0 = ext;
     a.out1 = (uint32_t*)ext + (size_t)c->rows * c->n;
     a.kb = nullptr;
@@ -1739,8 +1739,11 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
 // relinearization key (no c0 term, no automorphism), and the ModDown added onto (c0, c1): out = (c0, c1) +
 // (ext - conv) P^-1 on Q rows 0..top. out may be a or b.
 // the product's (d0, d1) into out and the key switch of d2 into c->ext (before ModDown)
+// The tensor (d0, d1 into out, d2 into c->tmp), d2's ModUp and its key dot into c->ext. *folded: the dot also added
+// P (d0, d1) on the Q rows (the fast dot's c0 mode 3), so the ModDown has nothing to add onto; else out keeps (d0, d1)
+// for the ModDown's add-onto step.
 static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s,
-                     int K = 1, int twice = 0) {
+                     bool* folded, int K = 1, int twice = 0) {
     if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
     if (K < 1 || K > c->k_max || K > 4) return -1;  // the key dot takes at most 4 ciphertexts
     const uint64_t part = (uint64_t)c->rows * c->n;
@@ -1760,11 +1763,15 @@ static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int 
         if (int e = c->tab->tensor(&t, s)) return e;
     }
     if (int e = modup(c, c->tmp, top, s, K)) return e;
-    return dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, 0, K);
+    // the fast dot with the retry table takes (d0, d1) as its c0 mode 3
+    const Level* L = level(c, top);
+    *folded = k->pval && !c->table_only && k->bits == 0 && L->ndig >= 1 && L->ndig <= 3;
+    return dot(c, k, 0, 1, c->tmp, top, c->ext, s, 0, *folded ? 3 : 0, K, nullptr, *folded ? out : nullptr);
 }
 int pcx_mul_relin(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s) {
-    if (int e = relin_ext(c, k, a, b, top, out, s)) return e;
-    return moddown(c, c->ext, c->conv, 1, top, out, s, out);
+    bool folded = false;
+    if (int e = relin_ext(c, k, a, b, top, out, s, &folded)) return e;
+    return moddown(c, c->ext, c->conv, 1, top, out, s, folded ? nullptr : out);
 }
 int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out,
                           pc_stream_t s) {
@@ -1773,8 +1780,9 @@ int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b,
 int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, int K,
                             int twice, pc_stream_t s) {
     if (top < 2) return -1;
-    if (int e = relin_ext(c, k, a, b, top, out, s, K, twice)) return e;
-    return moddown_rescale(c, c->ext, top, out, out, s, K);
+    bool folded = false;
+    if (int e = relin_ext(c, k, a, b, top, out, s, &folded, K, twice)) return e;
+    return moddown_rescale(c, c->ext, top, out, folded ? nullptr : out, s, K);
 }
 
 // The plaintext product (crates/pc-gpu/src/ops.rs:927-951 mult_pt, the table's mul_table, em.cuh:508-515): out = ct pt

@@ -51,7 +51,10 @@ int kska_patch_count(int logn, const uint32_t* const* seeds, const PrimeConst* p
                      uint32_t* counts, pc_stream_t s);
 int kska_patch_fill(int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig, int rows,
                     const uint32_t* idx, uint32_t* val, pc_stream_t s);
-// the fast dot with the retry values read from P instead of redrawn; -2 where the fast dot does not apply
+// the fast dot with the retry values read from P instead of redrawn; -2 where the fast dot does not apply. Beside the
+// table entry's c0 modes it takes c0_mode 3 (no counterpart in the reference, which rejects it): both parts of the
+// ciphertext at c0 (the second ct_stride / 2 words after the first) enter the Q rows as P c0 and P c0', so a
+// relinearized product's (d0, d1) is added in the extended basis and its ModDown needs no add-onto step
 int ks_dot_patched(int logn, const KsKeyArgs* g, const PatchTab* P, pc_stream_t s);
 
 // The forward NTT of composite-rescale corrections (rescale_fwd): row i's input generated in the column pass from the

@@ -344,6 +344,7 @@ struct FastCtx {
     const KeyTab* T;
     const uint32_t* D[MAXD];  // the chunk's D_d words (LDS, padded; or memory), this lane's at lp
     const uint32_t* c0;
+    gptr c0b;  // c0 mode 3: the chunk's words of the second part (memory), this lane's at 16 lane
     FastWave* W;
     int lane, lp, slot, logn, m0;
     bool acc_out, pc0;
@@ -392,8 +393,9 @@ __device__ __forceinline__ void ldpk16(gptr row, uint32_t s0, uint32_t (&out)[DS
 }
 
 // PATCH: the retry values come from the key group's table (P) instead of the wave's redraw. PK: key b bit-packed at
-// PK bits (0: dense words)
-template <int NDIG, bool MU2, bool PATCH, int PK>
+// PK bits (0: dense words). F: c0 mode 3 handled (the one-wave form; its second-part words held through the ChaCha
+// blocks)
+template <int NDIG, bool MU2, bool PATCH, int PK, bool F>
 __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, const Expander& ex, int r,
                                              const PatchTab& P) {
     const KsArgs& A = *C.A;
@@ -483,6 +485,13 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 #pragma unroll
         for (int k = 0; k < DS; ++k) asm volatile("" : "+v"(acc[k]));
     }
+    // c0 mode 3 (F): + P c0' (the second part's words, loaded with b, added at s1's reduction): ndig + 1 <= 4 products
+    // of (p - 1)^2 < 2^62
+    uint32_t cw1[F ? DS : 1];
+    const bool f3 = F && C.m0 == 3 && C.pc0;
+    if constexpr (F) {
+        if (f3) ld16(C.c0b + lane * DS, cw1);
+    }
     // the key's b rows: they arrive while the queued words are redrawn and s1 goes out, and are consumed last
     uint32_t b[NDIG][DS];
 #pragma unroll
@@ -545,7 +554,11 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         // s1 first (its registers free before s0's): reduce, scatter, add D_d a_d of this lane's redrawn words
         uint32_t v[DS];
 #pragma unroll
-        for (int k = 0; k < DS; ++k) buf[scat_addr((cbh + brev4(k) * sth) & (DCH - 1))] = red(acc[k]);
+        for (int k = 0; k < DS; ++k) {
+            uint64_t x = acc[k];
+            if constexpr (F) x += f3 ? (uint64_t)cw1[k] * C.pm : 0;
+            buf[scat_addr((cbh + brev4(k) * sth) & (DCH - 1))] = red(x);
+        }
 #pragma unroll
         for (int d = 0; d < NDIG; ++d) {
             uint32_t m = rejd[d], i = based[d];
@@ -605,7 +618,7 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
     C.logn = logn;
     C.m0 = A.c0_mode & 3;
     C.acc_out = (A.c0_mode & PC_KS_ACC) != 0;
-    C.pc0 = C.m0 == 1 && t < A.nq;
+    C.pc0 = (C.m0 == 1 || C.m0 == 3) && t < A.nq;
     C.p = (uint32_t)q.p;
     C.pm = C.pc0 ? ((const uint32_t*)A.pmod)[t] : 0;
     C.n16 = (1u << logn) >> 4;
@@ -624,6 +637,7 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
     C.oct = (size_t)cix * A.out_ct_stride;
     DotCtx X{&A, cix, t < A.nq ? A.digit_of[t] : -1, t, C.trow, C.chunk0};
     const uint32_t* c0row = (const uint32_t*)A.c0 + (size_t)cix * A.ct_stride + C.trow + C.chunk0;
+    C.c0b = C.m0 == 3 ? as_global(c0row + A.ct_stride / 2) : nullptr;
     if constexpr (NW == KW) {
         C.lp = padw(lane * DS);  // this lane's 16 words in the padded rows
 #pragma unroll
@@ -645,9 +659,9 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
         C.c0 = C.m0 ? c0row : nullptr;
     }
     if (ex.mu == 2) {
-        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH, PK>(C, red, ex, r, P);
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH, PK, NW == 1>(C, red, ex, r, P);
     } else {
-        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH, PK>(C, red, ex, r, P);
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH, PK, NW == 1>(C, red, ex, r, P);
     }
 }
 
@@ -706,14 +720,15 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     if (!g || !P || !P->idx || !P->val) return -1;
     const KsArgs& a = g->ks;
     const KeyTab& key = g->key;
-    if (a.K < 1 || a.K > 4 || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 || (a.c0_mode & 3) == 3 ||
-        a.ndig > P->ndig || key.q_top >= 0 || key.srows != P->rows)
+    if (a.K < 1 || a.K > 4 || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 || a.ndig > P->ndig ||
+        key.q_top >= 0 || key.srows != P->rows)
         return -2;
     if (a.nrows < 0 || a.R < 0) return -1;
     if (a.nrows == 0 || a.R == 0) return 0;
     if (!a.rows || !a.pr || !a.c1 || !a.out0 || !a.out1 || !a.autok || !a.digit_of || !a.modup) return -1;
-    if ((a.c0_mode & 3) == 1 && (!a.c0 || !a.pmod || !a.pmods)) return -1;
+    if ((a.c0_mode & 3) != 0 && (a.c0_mode & 3) != 2 && (!a.c0 || !a.pmod || !a.pmods)) return -1;
     if ((a.c0_mode & 3) == 2 && !a.c0) return -1;
+    if ((a.c0_mode & 3) == 3 && ((a.ct_stride & 1) || a.R >= KW)) return -2;  // mode 3: the one-wave form only
     if (!key.kb || !key.seed) return -1;
     const int chunks = (1 << LOGN) / DCH;
     int groups = 1;

@@ -366,37 +366,44 @@ class Evaluator:
 
     def lincombs(self, specs):
         """lincomb of each (terms, c0, top, scale), up to three of them per weighted-sum launch over one source list
-        when the operations have wsum_multi (a source a term does not use weighs 0): the same words as one lincomb
-        at a time"""
+        when the operations have wsum_multi (a source a term does not use weighs 0), the sums landing on one top laid
+        out side by side and rescaled together (up to ops.kmax per launch sequence): the same words as one lincomb at
+        a time"""
         if not hasattr(self.ops, "wsum_multi"):
             return [self.lincomb(*sp) for sp in specs]
-        out = []
+        groups = []
         for g0 in range(0, len(specs), 3):
-            grp = specs[g0:g0 + 3]
             srcs = []
-            for terms, _, _, _ in grp:
+            for terms, _, _, _ in specs[g0:g0 + 3]:
                 for a, _ in terms:
                     if not any(x.h is a.h for x in srcs):
                         srcs.append(a)
             if len(srcs) > 8:
-                out += [self.lincomb(*sp) for sp in grp]
-                continue
-            outs, tcs, ks, k0s = [], [], [], []
-            for terms, c0, top, scale in grp:
-                tc = top + 2
-                qq = self.qq(tc)
+                return [self.lincomb(*sp) for sp in specs]
+            groups.append((g0, srcs))
+        tcs = [top + 2 for _, _, top, _ in specs]
+        blocks = {tc: [self.ops.alloc(tcs.count(tc)), 0] for tc in dict.fromkeys(tcs)}
+        outs = []
+        for tc in tcs:
+            b = blocks[tc]
+            outs.append(self.ops.item(b[0], b[1]))
+            b[1] += 1
+        for g0, srcs in groups:
+            ks, k0s = [], []
+            for terms, c0, top, scale in specs[g0:g0 + 3]:
+                qq = self.qq(top + 2)
                 for a, _ in terms:
-                    assert a.top >= tc, (a.top, tc)
+                    assert a.top >= top + 2, (a.top, top + 2)
                 w = {id(a.h): int(round(c * scale * qq / a.scale)) for a, c in terms}
                 ks.append([w.get(id(x.h), 0) for x in srcs])
                 k0s.append(int(round(c0 * scale * qq)))
-                outs.append(self.ops.alloc())
-                tcs.append(tc)
-            self.ops.wsum_multi(outs, [x.h for x in srcs], tcs, ks, k0s)
-            for o, tc, (_, _, top, scale) in zip(outs, tcs, grp):
-                self.ops.rescale2(o, o, tc)
-                out.append(Ct(o, top, scale))
-        return out
+            self.ops.wsum_multi(outs[g0:g0 + 3], [x.h for x in srcs], tcs[g0:g0 + 3], ks, k0s)
+        kmax = max(1, getattr(self.ops, "kmax", 1))
+        for tc, (buf, n) in blocks.items():
+            for j0 in range(0, n, kmax):
+                h = self.ops.item(buf, j0)
+                self.ops.rescale2(h, h, tc, min(kmax, n - j0))
+        return [Ct(o, top, scale) for o, (_, _, top, scale) in zip(outs, specs)]
 
     def add(self, a, b, sub=False):
         assert abs(a.scale / b.scale - 1.0) < 1e-9, (a.scale, b.scale)
@@ -716,9 +723,13 @@ class PairOps:
 
     def __init__(self, ops):
         self.o = ops
+        self.kmax = max(1, ops.kmax // 2)
 
-    def alloc(self):
-        return self.o.alloc(2)
+    def alloc(self, count=1):
+        return self.o.alloc(2 * count)
+
+    def item(self, h, i):
+        return self.o.item(h, 2 * i)
 
     def add(self, out, a, b, top, sub):
         self.o.add(out, a, b, top, sub, K=2)
@@ -738,8 +749,8 @@ class PairOps:
     def mul_relin_rescale(self, out, a, b, top, twice=False):
         self.o.mul_relin_rescale(out, a, b, top, K=2, twice=twice)
 
-    def rescale2(self, out, x, top):
-        self.o.rescale2(out, x, top, K=2)
+    def rescale2(self, out, x, top, count=1):
+        self.o.rescale2(out, x, top, K=2 * count)
 
 
 class GpuOps:
@@ -757,6 +768,7 @@ class GpuOps:
         self.levels, self.conj_key = levels, conj
         self.N, self.R, self.nq = ctx.n, ctx.rows, ctx.nq
         self.cw = ctx.ct_words
+        self.kmax = ctx.k_max  # ciphertexts per batched rescale
         self.primes = [int(p) for p in ctx.chain.primes]
         self.pr = LIB.pcx_ctx_primes(ctx.h)
         self.pool, self.cur = [], 0

@@ -20,6 +20,7 @@ class OracleOps:
         self.relin_seed, self.relin_b = relin_seed, relin_b
         self.gal = None
         self.level_i = 0
+        self.kmax = 2  # the leaves' batched rescales taken two at a time, one after the other
         self.mr = bts.mod_raise_consts(self.q, 1)
 
     def set_galois(self, gal):
@@ -141,8 +142,9 @@ class OracleOps:
             self.add((x[None], 0), (x[None], 0), (x[None], 0), top, False)
         self.get(out)[:] = self.oc.mul_relin_rescale(x, self.get(b), top, self.relin_seed, self.relin_b)
 
-    def rescale2(self, out, x, top):
-        self.get(out)[:] = self.oc.rescale(self.get(x).copy(), top, 2)
+    def rescale2(self, out, x, top, count=1):
+        for i in range(count):
+            self.get(self.item(out, i))[:] = self.oc.rescale(self.get(self.item(x, i)).copy(), top, 2)
 
     def mod_raise(self, out, x, top):
         o = self.get(out)

@@ -49,7 +49,7 @@ def test_bootstrap_c5_matches_the_oracle():
     ct, me = encrypt(S["oc"], S["s_eval"], m, rng, 0)
     # the GPU composite: the oracle's keys uploaded, the relinearization key generated on the device from the same
     # secret, seed and errors (device key generation equals the oracle's, tests/test_gpu_parity.py)
-    ctx = pa.Context(ch, k_rot=8, k_max=4)
+    ctx = pa.Context(ch, k_rot=8, k_max=8)
     keys = pa.Keys(ctx, S["gal"], seeds=S["seeds"], b=S["bs"])
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()

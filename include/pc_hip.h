@@ -947,6 +947,12 @@ int pcx_mul_relin_rescale(pcx_ctx* c, pcx_keys* k, const void* a, const void* b,
  * nonzero: the tensor's outputs doubled (its dbl, args.cuh TensorArgs), the words of the product of 2a and b. */
 int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, int K,
                             int twice, pc_stream_t s);
+/* pcx_mul_relin_rescale_k over K <= min(k_max, 8) pairs at their own addresses: product j = a[j] b[j] (each a
+ * ciphertext at top), out K consecutive ciphertexts; one tensor launch for the K pairs, then the ModUp, key dots (four
+ * ciphertexts per launch) and ModDown-rescale of pcx_mul_relin_rescale_k. No counterpart in the reference: independent
+ * products of one level (a Chebyshev basis's T_{a+b} = 2 T_a T_b) batched without gathering their operands first. */
+int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b, int K, int top,
+                               void* out, int twice, pc_stream_t s);
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
  * form rows by prime id (rows 0..top read). out may be ct. */
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);

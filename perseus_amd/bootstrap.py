@@ -342,6 +342,22 @@ class Evaluator:
         self.ops.mul_relin_rescale(out, a.h, b.h, t, twice)
         return Ct(out, t - 2, a.scale * b.scale / self.qq(t))
 
+    def mul_many(self, pairs, twice=False):
+        """[mul(a, b, twice) for (a, b) in pairs]: pairs whose products land on one top as batched products (up to
+        ops.kmax per call) when the operations have mul_list; the same words"""
+        tops = {min(a.top, b.top) for a, b in pairs}
+        if len(pairs) == 1 or len(tops) != 1 or not hasattr(self.ops, "mul_list"):
+            return [self.mul(a, b, twice) for a, b in pairs]
+        t = tops.pop()
+        kmax = max(1, getattr(self.ops, "kmax", 1))
+        out = []
+        for j0 in range(0, len(pairs), kmax):
+            grp = pairs[j0:j0 + kmax]
+            buf = self.ops.alloc(len(grp))
+            self.ops.mul_list(buf, [a.h for a, _ in grp], [b.h for _, b in grp], t, twice)
+            out += [Ct(self.ops.item(buf, j), t - 2, a.scale * b.scale / self.qq(t)) for j, (a, b) in enumerate(grp)]
+        return out
+
     def mul_to(self, a, c, scale, top):
         """c a landing exactly at (top, scale): a times the integer round(c scale q_a q_b / a.scale), rescaled"""
         assert a.top - 2 >= top, (a.top, top)
@@ -434,19 +450,20 @@ class ChebEval:
     def __init__(self, ev):
         self.ev = ev
 
+    # T_k = 2 T_a T_b - T_{a-b}, by rounds of independent products (one batched product per round)
+    ROUNDS = (((2, 1, 1),), ((3, 2, 1), (4, 2, 2)), ((5, 3, 2), (6, 3, 3), (7, 4, 3), (8, 4, 4)), ((16, 8, 8),),
+              ((32, 16, 16),))
+
     def basis(self, u):
         ev = self.ev
         T = {1: u}
-
-        def make(a, b):
-            P = ev.mul(T[a], T[b], twice=True)
-            if a == b:
-                return ev.add_const(P, -1.0)
-            return ev.add(P, ev.mul_to(T[a - b], 1.0, P.scale, P.top), sub=True)
-
-        for k, (a, b) in ((2, (1, 1)), (3, (2, 1)), (4, (2, 2)), (5, (3, 2)), (6, (3, 3)), (7, (4, 3)), (8, (4, 4)),
-                          (16, (8, 8)), (32, (16, 16))):
-            T[k] = make(a, b)
+        for rnd in self.ROUNDS:
+            Ps = ev.mul_many([(T[a], T[b]) for _, a, b in rnd], twice=True)
+            for (k, a, b), P in zip(rnd, Ps):
+                if a == b:
+                    T[k] = ev.add_const(P, -1.0)
+                else:
+                    T[k] = ev.add(P, ev.mul_to(T[a - b], 1.0, P.scale, P.top), sub=True)
         self.T = T
         return T
 
@@ -752,6 +769,10 @@ class PairOps:
     def rescale2(self, out, x, top, count=1):
         self.o.rescale2(out, x, top, K=2 * count)
 
+    def mul_list(self, out, a, b, top, twice=False):
+        ex = lambda hs: [self.o.item(h, i) for h in hs for i in (0, 1)]
+        self.o.mul_list(out, ex(a), ex(b), top, twice)
+
 
 class GpuOps:
     """The composite's operations on the device: the engine's key switches, rescale and products, the kernel table's
@@ -998,6 +1019,11 @@ class GpuOps:
 
     def rescale2(self, out, x, top, K=1):
         self.ctx.rescale(x, top, 2, out, self.st, K=K)
+
+    def mul_list(self, out, a, b, top, twice=False):
+        """out's len(a) consecutive ciphertexts = a[j] b[j], relinearized and rescaled (the pairs at their own
+        addresses)"""
+        self.ctx.mul_relin_rescale_list(self.relin, a, b, top, out, self.st, twice=twice)
 
     # -- ModRaise
     def mod_raise(self, out, x, top):

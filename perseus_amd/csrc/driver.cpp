@@ -1785,6 +1785,44 @@ int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* 
     return moddown_rescale(c, c->ext, top, out, folded ? nullptr : out, s, K);
 }
 
+int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b, int K, int top,
+                               void* out, int twice, pc_stream_t s) {
+    if (!c || !k || !a || !b || !out || top < 2 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
+    if (K < 1 || K > c->k_max || K > pch::TLIST_MAX) return -1;
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    pch::TensorListArgs t;
+    memset(&t, 0, sizeof t);
+    for (int j = 0; j < K; ++j) {
+        if (!a[j] || !b[j]) return -1;
+        t.a[j] = (const uint32_t*)a[j];
+        t.b[j] = (const uint32_t*)b[j];
+    }
+    t.out = (uint32_t*)out;
+    t.d2 = c->tmp;
+    t.part = part;
+    t.ct_stride = 2 * part;
+    t.pr = c->pr;
+    t.n = top + 1;
+    t.K = K;
+    t.dbl = twice ? 1 : 0;
+    {
+        Stage st(c, 8, s);
+        if (int e = pch::tensor_list((int)c->logn, &t, s)) return e;
+    }
+    if (int e = modup(c, c->tmp, top, s, K)) return e;
+    // the key dots four ciphertexts at a time, (d0, d1) folded in as in relin_ext
+    const Level* L = level(c, top);
+    const bool folded = k->pval && !c->table_only && k->bits == 0 && L->ndig >= 1 && L->ndig <= 3;
+    const size_t cw = c->ct_words(), dw = (size_t)c->dnum * c->rows * c->n;
+    for (int j0 = 0; j0 < K; j0 += 4) {
+        const int m = std::min(4, K - j0);
+        if (int e = dot(c, k, 0, 1, c->tmp + j0 * cw, top, c->ext + j0 * cw, s, 0, folded ? 3 : 0, m,
+                        c->digits + j0 * dw, folded ? (const uint32_t*)out + j0 * cw : nullptr))
+            return e;
+    }
+    return moddown_rescale(c, c->ext, top, out, folded ? nullptr : out, s, K);
+}
+
 // The plaintext product (crates/pc-gpu/src/ops.rs:927-951 mult_pt, the table's mul_table, em.cuh:508-515): out = ct pt
 // on Q rows 0..top of both parts, pt one plaintext of evaluation-form rows by prime id. out may be ct.
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s) {

@@ -137,6 +137,20 @@ __global__ void __launch_bounds__(BX) tensor_k(TensorArgs A, TensorYArgs B, int 
                 Y ? ((const uint32_t*)B.cs)[row] : 0u, Y && B.sub != 0, coef);
 }
 
+// the tensor of K pairs at their own addresses: ciphertext c = blockIdx.z reads a[c], b[c]
+__global__ void __launch_bounds__(BX) tensor_list_k(TensorListArgs A, int logn) {
+    const int row = blockIdx.y, c = blockIdx.z;
+    const uint32_t i = lane_word();
+    const Red red(A.pr[row]);
+    const size_t ro = ((size_t)row << logn) + i;
+    const uint32_t *a = A.a[c] + ro, *b = A.b[c] + ro;
+    Tacc s;
+    s.mac(ld4(a), ld4(a + A.part), ld4(b), ld4(b + A.part));
+    uint32_t* o = A.out + c * A.ct_stride + ro;
+    tensor_tail(s, red, o, o + A.part, A.d2 + c * A.ct_stride + A.part + ro, false, false, A.dbl != 0, nullptr,
+                nullptr, 0u, 0u, false, nullptr);
+}
+
 __global__ void __launch_bounds__(BX) tensor_sum_k(TensorSumArgs A, int logn) {
     const int row = blockIdx.y, c = blockIdx.z;
     const uint32_t i = lane_word();
@@ -450,6 +464,14 @@ int tensor(const TensorArgs* a, pc_stream_t s) {
     if (a->npairs >= 2 && (!ref_ok(a->a1) || !ref_ok(a->b1))) return -1;
     if (a->n == 0 || a->K == 0) return 0;
     PCH_LAUNCH(tensor_k<false>, grid<LOGN>(a->n, a->K), *a, TensorYArgs{}, LOGN);
+}
+template <int LOGN>
+int tensor_list(const TensorListArgs* a, pc_stream_t s) {
+    if (!a || !a->pr || !a->out || !a->d2 || a->n < 0 || a->K < 0 || a->K > TLIST_MAX) return -1;
+    for (int c = 0; c < a->K; ++c)
+        if (!a->a[c] || !a->b[c]) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(tensor_list_k, grid<LOGN>(a->n, a->K), *a, LOGN);
 }
 template <int LOGN>
 int tensor_y(const TensorYArgs* a, pc_stream_t s) {
@@ -771,5 +793,16 @@ PCH_EM_INST(13)
 PCH_EM_INST(14)
 PCH_EM_INST(15)
 PCH_EM_INST(16)
+
+int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s) {
+    switch (logn) {
+        case 12: return em::tensor_list<12>(a, s);
+        case 13: return em::tensor_list<13>(a, s);
+        case 14: return em::tensor_list<14>(a, s);
+        case 15: return em::tensor_list<15>(a, s);
+        case 16: return em::tensor_list<16>(a, s);
+        default: return -2;
+    }
+}
 
 }  // namespace pch

@@ -72,6 +72,22 @@ int ntt_fwd_dense(int logn, const NttArgs* a, pc_stream_t s);
 // the row count from which launches of N = 2^16 take the one-pass transform (0: never); returns the previous one
 int ntt_one_pass_min(int rows);
 
+// The tensor of K ciphertext pairs at their own addresses (driver-internal, no counterpart in the reference, whose
+// tensor takes K consecutive ciphertexts): out ciphertext c = (a[c] b[c])'s (d0, d1), part 1 of d2 ciphertext c its
+// d2, doubled when dbl; rows 0..n-1; a[c] / b[c] hold part 0, part 1 `part` words later; out and d2 are K consecutive
+// ciphertexts (ct_stride apart)
+constexpr int TLIST_MAX = 8;
+struct TensorListArgs {
+    const uint32_t* a[TLIST_MAX];
+    const uint32_t* b[TLIST_MAX];
+    uint32_t* out;
+    uint32_t* d2;
+    uint64_t part, ct_stride;
+    const PrimeConst* pr;
+    int n, K, dbl;
+};
+int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s);
+
 // ks_dot_key's summed rotations (c0_mode | KS_SUM): out = sum_r sigma_r(dot_r), gathered in output order
 int ks_dot_key_sum(int logn, const KsKeyArgs* g, pc_stream_t s);
 

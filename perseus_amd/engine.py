@@ -273,6 +273,15 @@ class Context:
             check(LIB.pcx_mul_relin_rescale_k(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), K, int(twice),
                                               stream.h), "mul_relin_rescale_k")
 
+    def mul_relin_rescale_list(self, keys, a, b, top, out, stream, twice=False):
+        """out's len(a) consecutive ciphertexts (top - 2) = a[j] b[j] relinearized and rescaled, the pairs at their own
+        addresses: one tensor launch for all, then the batched ModUp, dots and ModDown (pcx_mul_relin_rescale_list)."""
+        assert len(a) == len(b) >= 1
+        pa = (C.c_void_p * len(a))(*[x.addr() for x in a])
+        pb = (C.c_void_p * len(b))(*[x.addr() for x in b])
+        check(LIB.pcx_mul_relin_rescale_list(self.h, keys.h, pa, pb, len(a), top, out.addr(), int(twice), stream.h),
+              "mul_relin_rescale_list")
+
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}
         in the extended basis, babies i >= 1 by keys r0 + i - 1. pts: a DevBuf holding npts device pointers (uint64)

@@ -142,6 +142,10 @@ class OracleOps:
             self.add((x[None], 0), (x[None], 0), (x[None], 0), top, False)
         self.get(out)[:] = self.oc.mul_relin_rescale(x, self.get(b), top, self.relin_seed, self.relin_b)
 
+    def mul_list(self, out, a, b, top, twice=False):
+        for j in range(len(a)):
+            self.mul_relin_rescale(self.item(out, j), a[j], b[j], top, twice)
+
     def rescale2(self, out, x, top, count=1):
         for i in range(count):
             self.get(self.item(out, i))[:] = self.oc.rescale(self.get(self.item(x, i)).copy(), top, 2)

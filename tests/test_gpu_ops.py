@@ -159,14 +159,46 @@ def test_mul_relin_rescale(stream, name, top, alias):
 _CTX2 = {}
 
 
-def batched(name):
-    """a k_max 2 context of the preset and its relinearization key (the same secret, seed and errors as relin_key's)"""
-    if name not in _CTX2:
+def batched(name, k_max=2):
+    """a k_max context of the preset and its relinearization key (the same secret, seed and errors as relin_key's)"""
+    if (name, k_max) not in _CTX2:
         ch, _, _ = contexts(name)
-        ctx2 = pa.Context(ch, k_rot=1, k_max=2)
+        ctx2 = pa.Context(ch, k_rot=1, k_max=k_max)
         _, s, seed, errs = relin_key(name)
-        _CTX2[name] = (ctx2, pa.Keys(ctx2, [1], seeds=seed[None], secret=s, errors=errs[None], relin=True))
-    return _CTX2[name]
+        _CTX2[name, k_max] = (ctx2, pa.Keys(ctx2, [1], seeds=seed[None], secret=s, errors=errs[None], relin=True))
+    return _CTX2[name, k_max]
+
+
+@pytest.mark.parametrize("name,top,K,twice", [("small", 5, 3, False), ("small31", 4, 6, True), ("c3", 29, 5, True)])
+def test_product_list(stream, name, top, K, twice):
+    """pcx_mul_relin_rescale_list on a k_max 6 context: K pairs at their own addresses (operands drawn with repeats
+    from four ciphertexts of one buffer), one tensor launch and the batched key switch (key dots four ciphertexts at a
+    time): each product's words equal the K = 1 call's; more pairs than k_max are refused."""
+    say(f"[product list] {name} top={top} K={K} twice={twice}")
+    from perseus_amd import bootstrap as B
+
+    ch, ctx, _ = contexts(name)
+    keys, _, _, _ = relin_key(name)
+    ctxk, keysk = batched(name, 6)
+    rng = np.random.default_rng(top * 11 + K)
+    pool = np.stack([random_ct(ch, top, rng) for _ in range(4)])
+    ia, ib = rng.integers(0, 4, K), rng.integers(0, 4, K)
+    want = []
+    for j in range(K):
+        ba, bb, o = pa.DevBuf.from_array(pool[ia[j]]), pa.DevBuf.from_array(pool[ib[j]]), ctx.ct_buf(1)
+        ctx.mul_relin_rescale(keys, ba, bb, top, o, stream, K=1, twice=twice)
+        stream.sync()
+        want.append(o.download((2, ch.rows, ch.n)))
+    buf = pa.DevBuf.from_array(pool)
+    views = lambda idx: [B.View(buf, int(i) * ctxk.ct_words) for i in idx]
+    out = ctxk.ct_buf(K)
+    ctxk.mul_relin_rescale_list(keysk, views(ia), views(ib), top, out, stream, twice=twice)
+    stream.sync()
+    got = out.download((K, 2, ch.rows, ch.n))
+    for j in range(K):
+        assert (got[j][:, : top - 1] == want[j][:, : top - 1]).all(), f"product {j} ({ia[j]} x {ib[j]})"
+    with pytest.raises(pa.HipError):
+        ctxk.mul_relin_rescale_list(keysk, views([0] * 7), views([1] * 7), top, ctxk.ct_buf(7), stream)
 
 
 @pytest.mark.parametrize("name,top,alias", [("small", 5, False), ("small31", 4, True), ("c3", 29, True),

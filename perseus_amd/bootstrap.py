@@ -358,6 +358,31 @@ class Evaluator:
             out += [Ct(self.ops.item(buf, j), t - 2, a.scale * b.scale / self.qq(t)) for j, (a, b) in enumerate(grp)]
         return out
 
+    def prod_meta(self, a, b):
+        """(top, scale) of mul(a, b): the product lands two primes below the lower operand's top"""
+        t = min(a.top, b.top)
+        return t - 2, a.scale * b.scale / self.qq(t)
+
+    def mul_to_many(self, specs):
+        """[mul_to(a, c, scale, top) for each spec]: specs whose sources sit at one top as integer products side by
+        side and one batched rescale (up to ops.kmax at once); the same words"""
+        tops = {sp[0].top for sp in specs}
+        if len(specs) == 1 or len(tops) != 1:
+            return [self.mul_to(*sp) for sp in specs]
+        at = tops.pop()
+        buf = self.ops.alloc(len(specs))
+        out = []
+        for j, (a, c, scale, top) in enumerate(specs):
+            assert a.top - 2 >= top, (a.top, top)
+            h = self.ops.item(buf, j)
+            self.ops.mul_const(h, a.h, a.top, int(round(c * scale * self.qq(a.top) / a.scale)))
+            out.append(Ct(h, top, scale))
+        kmax = max(1, getattr(self.ops, "kmax", 1))
+        for j0 in range(0, len(specs), kmax):
+            h = self.ops.item(buf, j0)
+            self.ops.rescale2(h, h, at, min(kmax, len(specs) - j0))
+        return out
+
     def mul_to(self, a, c, scale, top):
         """c a landing exactly at (top, scale): a times the integer round(c scale q_a q_b / a.scale), rescaled"""
         assert a.top - 2 >= top, (a.top, top)
@@ -455,15 +480,24 @@ class ChebEval:
               ((32, 16, 16),))
 
     def basis(self, u):
+        """T_1..T_8, T_16, T_32. A round that needs corrections T_{a-b} brought to its products' (top, scale) forms
+        them together with every later round's whose products' (top, scale) are already known (they follow from the
+        operands' alone): one batched rescale for T_3's, T_5's and T_7's"""
         ev = self.ev
-        T = {1: u}
-        for rnd in self.ROUNDS:
-            Ps = ev.mul_many([(T[a], T[b]) for _, a, b in rnd], twice=True)
-            for (k, a, b), P in zip(rnd, Ps):
-                if a == b:
-                    T[k] = ev.add_const(P, -1.0)
-                else:
-                    T[k] = ev.add(P, ev.mul_to(T[a - b], 1.0, P.scale, P.top), sub=True)
+        T, corr = {1: u}, {}
+        for i, rnd in enumerate(self.ROUNDS):
+            P = dict(zip([k for k, _, _ in rnd], ev.mul_many([(T[a], T[b]) for _, a, b in rnd], twice=True)))
+            known = {**T, **P}
+            if any(a != b and k not in corr for k, a, b in rnd):
+                todo = [(k, a, b) for r in self.ROUNDS[i:] for k, a, b in r
+                        if a != b and k not in corr and a in known and b in known]
+                specs = []
+                for k, a, b in todo:
+                    top, scale = ev.prod_meta(known[a], known[b])
+                    specs.append((T[a - b], 1.0, scale, top))
+                corr.update(zip([k for k, _, _ in todo], ev.mul_to_many(specs)))
+            for k, a, b in rnd:
+                T[k] = ev.add_const(P[k], -1.0) if a == b else ev.add(P[k], corr[k], sub=True)
         self.T = T
         return T
 

@@ -646,9 +646,12 @@ const Level* level(const pcx_ctx* c, int top) {
 // (x + P onto - conv_B) / B with B = P q_top q_{top-1}, x = ext (one extended ciphertext), onto NULL or a ciphertext at
 // top (may alias out)
 // K <= k_max ciphertexts at once: ext, out and onto each K consecutive ciphertexts (ct_words apart)
-int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto, pc_stream_t s, int K = 1) {
+// nsum > 1 (K = 1): x is the sum of nsum extended ciphertexts ct_words apart (the INTT's first pass and the epilogue
+// read the sum; onto's P multiple goes into the first)
+int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto, pc_stream_t s, int K = 1,
+                    int nsum = 1) {
     const Level* L = level(c, top);
-    if (!L || top < 2 || !L->mdr.k || K < 1 || K > c->k_max) return -1;
+    if (!L || top < 2 || !L->mdr.k || K < 1 || K > c->k_max || nsum < 1 || (nsum > 1 && K != 1)) return -1;
     const Level::MdRescale& M = L->mdr;
     if (onto) {
         Stage st(c, 9, s);
@@ -657,6 +660,12 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     NttArgs a = ntt_args(c, ext, M.intt, k_rows(c, M.intt, K));
     a.es = M.intt.es;
     a.ess = M.intt.es + M.intt.n;
+    if (nsum > 1) {
+        a.src = ext;
+        a.soff = M.intt.roff;
+        a.snum = nsum;
+        a.sstride = c->ct_words();
+    }
     {
         Stage st(c, 4, s);
         if (int e = c->tab->ntt_inv(&a, s)) return e;
@@ -679,7 +688,8 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     f.ed = nullptr;  // the epilogue adds onto out's rows, which hold onto s2
     f.eout = out;
     f.ex = ext;
-    f.xnum = 1;
+    f.xnum = nsum;
+    f.xstride = c->ct_words();
     f.es = M.ntt.es;
     f.ess = M.ntt.es + c->rows;
     Stage st(c, 6, s);
@@ -776,14 +786,68 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
 // ModDown of m extended ciphertexts at ext into m ciphertexts at out (crates/pc-gpu/src/ks.rs:1620-1649): INTT of the
 // P rows (N^-1 pre_j), conversion P -> Q rows 0..top into conv, NTT of conv with the epilogue (ext - conv) P^-1;
 // onto non-null: onto + (ext - conv) P^-1 (onto == out: added in place; crates/pc-gpu/src/ks.rs:1675-1710 MdOut)
-int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc_stream_t s,
-            const void* onto = nullptr) {
+// the dots of m consecutive inputs (ct_words apart, their digits at digits, dnum rows N apart), input j under key
+// r0 + j alone, into m extended ciphertexts at ext (ct_words apart), each c0 folded in as P sigma_j(c0_j): one launch
+// of the fast dot's diagonal form (the key group's retry table); -2 where that form does not apply
+int dot_diag(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* ext, const uint32_t* digits,
+             pc_stream_t s) {
     const Level* L = level(c, top);
-    if (!L || m < 1 || m > c->k_rot) return -1;
+    if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || m > c->k_max) return -1;
+    if (!k->pval || c->table_only) return -2;
+    KsKeyArgs g;
+    memset(&g, 0, sizeof g);
+    KsArgs& a = g.ks;
+    a.c1 = (const uint32_t*)ct + (size_t)c->rows * c->n;
+    a.modup = digits;
+    a.c0 = ct;
+    a.out0 = ext;
+    a.out1 = (uint32_t*)ext + (size_t)c->rows * c->n;
+    a.autok = k->autok + r0;
+    a.rows = L->ks_rows;
+    a.digit_of = c->digit_of;
+    a.pmod = c->pmod;
+    a.pmods = c->pmod + (c->nq + c->kp);
+    a.pr = c->pr;
+    a.ct_stride = c->ct_words();
+    a.mu_ct_stride = (uint64_t)c->dnum * c->rows * c->n;
+    a.mu_digit_stride = (uint64_t)c->rows * c->n;
+    a.out_ct_stride = c->ct_words();
+    a.out_rot_stride = 0;
+    a.K = m;
+    a.R = m;
+    a.ndig = L->ndig;
+    a.c0_mode = 1;
+    a.nq = c->nq;
+    a.nrows = L->nks;
+    KeyTab& t = g.key;
+    t.kb = k->kb + r0;
+    t.seed = k->seed + r0;
+    t.row_words = k->row_words;
+    t.bits = k->bits;
+    t.q_top = -1;
+    t.srows = c->rows;
+    t.nregen = c->dnum;
+    Stage st(c, 3, s);
+    const size_t per_key = (size_t)c->dnum * c->rows * (c->n / 1024);
+    const pch::PatchTab P = {k->pidx + (size_t)r0 * per_key, k->pval, c->dnum, c->rows, 1};
+    return pch::ks_dot_patched((int)c->logn, &g, &P, s);
+}
+
+// nsum > 1 (m = 1): ext holds nsum extended ciphertexts ct_words apart, the ModDown of their sum
+int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc_stream_t s,
+            const void* onto = nullptr, int nsum = 1) {
+    const Level* L = level(c, top);
+    if (!L || m < 1 || m > c->k_rot || nsum < 1 || (nsum > 1 && m != 1)) return -1;
     const Rows& ri = L->md_intt[m - 1];
     NttArgs a = ntt_args(c, ext, ri, ri.n);
     a.es = ri.es;
     a.ess = ri.es + ri.n;
+    if (nsum > 1) {
+        a.src = ext;
+        a.soff = ri.roff;
+        a.snum = nsum;
+        a.sstride = c->ct_words();
+    }
     {
         Stage st(c, 4, s);
         if (int e = c->tab->ntt_inv(&a, s)) return e;
@@ -794,7 +858,8 @@ int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc
     f.ed = onto == out ? nullptr : onto;
     f.eout = out;
     f.ex = ext;
-    f.xnum = 1;
+    f.xnum = nsum;
+    f.xstride = c->ct_words();
     f.es = c->pinv;
     f.ess = c->pinv + (c->nq + c->kp);
     if (c->md_fused) {
@@ -1511,20 +1576,38 @@ int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* c
     return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
 }
 
-// the extended sum of pcx_rotate_many in c->ext: one ModUp per input (each its own c1), its dot written (the first)
-// or added onto the sum, c0 folded in as P sigma(c0)
+// the extended sum of pcx_rotate_many in c->ext: one ModUp per input (each its own c1), c0 folded in as P sigma(c0).
+// When every run's keys are consecutive and the n dots fit c->ext: each run's dots as one diagonal launch, input j's
+// into extended slot j (*nsum = n: the ModDown reads their sum); else each dot written (the first) or added onto one
+// sum (*nsum = 1).
 static int rotate_many_ext(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top,
-                           pc_stream_t s) {
+                           pc_stream_t s, int* nsum) {
     if (!c || !k || k->c != c || n < 1 || !idx || !cts || !level(c, top)) return -1;
     for (int j = 0; j < n; ++j)
         if (!cts[j] || idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
     // runs of up to k_max inputs laid out ct_words apart share one ModUp launch sequence; each input's dot then reads
     // its own digits
     const size_t cw = c->ct_words(), dw = (size_t)c->dnum * c->rows * c->n;
+    bool diag = n > 1 && n <= std::max(c->k_rot, c->k_max) && k->pval && !c->table_only;
+    for (int j0 = 0, m = 1; j0 < n && diag; j0 += m, m = 1) {
+        while (j0 + m < n && m < c->k_max && cts[j0 + m] == (const void*)((const uint32_t*)cts[j0] + m * cw)) ++m;
+        for (int j = j0 + 1; j < j0 + m; ++j) diag = diag && idx[j] == idx[j0] + (j - j0);
+    }
+    *nsum = 1;
     for (int j0 = 0; j0 < n;) {
         int m = 1;
         while (j0 + m < n && m < c->k_max && cts[j0 + m] == (const void*)((const uint32_t*)cts[j0] + m * cw)) ++m;
         if (int e = modup(c, cts[j0], top, s, m)) return e;
+        if (diag) {
+            const int e = dot_diag(c, k, idx[j0], m, cts[j0], top, c->ext + (size_t)j0 * cw, c->digits, s);
+            if (e == 0) {
+                *nsum = j0 + m;
+                j0 += m;
+                continue;
+            }
+            if (e != -2 || j0 > 0) return e;
+            diag = false;  // the diagonal form does not apply: every dot onto one sum
+        }
         for (int j = j0; j < j0 + m; ++j)
             if (int e = dot(c, k, idx[j], 1, cts[j], top, c->ext, s, 0, j ? 1 | PC_KS_ACC : 1, 1,
                             c->digits + (size_t)(j - j0) * dw))
@@ -1537,15 +1620,17 @@ static int rotate_many_ext(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const
 int pcx_rotate_many(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top, void* out,
                     const void* onto, pc_stream_t s) {
     if (!out) return -1;
-    if (int e = rotate_many_ext(c, k, idx, n, cts, top, s)) return e;
-    return moddown(c, c->ext, c->conv, 1, top, out, s, onto);
+    int nsum = 1;
+    if (int e = rotate_many_ext(c, k, idx, n, cts, top, s, &nsum)) return e;
+    return moddown(c, c->ext, c->conv, 1, top, out, s, onto, nsum);
 }
 
 int pcx_rotate_many_rescale(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top,
                             void* out, const void* onto, pc_stream_t s) {
     if (!out || top < 2) return -1;
-    if (int e = rotate_many_ext(c, k, idx, n, cts, top, s)) return e;
-    return moddown_rescale(c, c->ext, top, out, onto, s);
+    int nsum = 1;
+    if (int e = rotate_many_ext(c, k, idx, n, cts, top, s, &nsum)) return e;
+    return moddown_rescale(c, c->ext, top, out, onto, s, 1, nsum);
 }
 
 // pcx_rotate_sum over K <= min(k_max, k_rot) consecutive ciphertexts: one ModUp launch sequence for the K, each

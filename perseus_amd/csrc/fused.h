@@ -45,6 +45,7 @@ struct PatchTab {
     const uint32_t* idx;
     const uint32_t* val;
     int ndig, rows;
+    int diag;  // nonzero: K = R, ciphertext c under key c alone (grid z = K); the table entries pass zero
 };
 // counts[((r ndig + d) rows + t) chunks + c] for the nkeys seeds (device array of seed pointers) and the context's primes
 int kska_patch_count(int logn, const uint32_t* const* seeds, const PrimeConst* pr, int nkeys, int ndig, int rows,

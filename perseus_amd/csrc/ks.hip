@@ -633,7 +633,8 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
     // grid z: K ciphertexts x key groups
     const int ng = (int)gridDim.z / A.K, cix = (int)blockIdx.z / ng, kg = (int)blockIdx.z % ng;
     const int kpg = (A.R + ng - 1) / ng;
-    const int r_lo = kg * kpg, r_hi = min(A.R, r_lo + kpg);
+    int r_lo = kg * kpg, r_hi = min(A.R, r_lo + kpg);
+    if (P.diag) r_lo = cix, r_hi = cix + 1;  // ciphertext cix under key cix alone
     C.oct = (size_t)cix * A.out_ct_stride;
     DotCtx X{&A, cix, t < A.nq ? A.digit_of[t] : -1, t, C.trow, C.chunk0};
     const uint32_t* c0row = (const uint32_t*)A.c0 + (size_t)cix * A.ct_stride + C.trow + C.chunk0;
@@ -668,8 +669,8 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
 // the fast dot's launch: one-wave direct workgroups when the launch has fewer keys than a staged workgroup's waves
 template <int NDIG, bool PATCH, int PK = 0>
 void dot_fast_launch(dim3 grid, const KsArgs& a, const KeyTab& key, const PatchTab& P, int logn, hipStream_t st) {
-    if (a.R < KW) {
-        grid.z = a.R * a.K;
+    if (P.diag || a.R < KW) {
+        grid.z = P.diag ? a.K : a.R * a.K;
         hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1, PK>), grid, dim3(DBX), 0, st, a, key, P, logn);
     } else {
         hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW, PK>), grid, dim3(KBX), 0, st, a, key, P, logn);
@@ -720,8 +721,8 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     if (!g || !P || !P->idx || !P->val) return -1;
     const KsArgs& a = g->ks;
     const KeyTab& key = g->key;
-    if (a.K < 1 || a.K > 4 || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 || a.ndig > P->ndig ||
-        key.q_top >= 0 || key.srows != P->rows)
+    if (a.K < 1 || a.K > (P->diag ? 8 : 4) || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 ||
+        a.ndig > P->ndig || key.q_top >= 0 || key.srows != P->rows || (P->diag && (a.R != a.K || (a.c0_mode & 3) == 3)))
         return -2;
     if (a.nrows < 0 || a.R < 0) return -1;
     if (a.nrows == 0 || a.R == 0) return 0;

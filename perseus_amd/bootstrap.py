@@ -506,7 +506,8 @@ class ChebEval:
         return self.T[7].top - 2 - 6
 
     def _walk(self, c, top, scale, leaf):
-        """the split recursion: leaf(terms, c0, top, scale) for a leaf, else Q T_g + R with Q and R walked first"""
+        """the split recursion: leaf(terms, c0, top, scale) for a leaf, else the split [T_g at top + 2, Q, R] (the
+        value Q T_g + R) with Q and R walked first"""
         c = np.trim_zeros(np.asarray(c, np.float64), "b")
         ev, T = self.ev, self.T
         if len(c) <= self.BABY:
@@ -519,16 +520,44 @@ class ChebEval:
         assert G.top >= top + 2
         Q = self._walk(q, top + 2, scale * ev.qq(top + 2) / G.scale, leaf)
         R = self._walk(r, top, scale, leaf)
-        if Q is None:
-            return None
-        return ev.add(ev.mul(Q, Ct(G.h, top + 2, G.scale)), R)
+        return [Ct(G.h, top + 2, G.scale), Q, R]
 
     def eval(self, c, top, scale):
-        """every leaf first (their weighted sums grouped over the shared T_k), then the products and sums"""
+        """every leaf first (their weighted sums grouped over the shared T_k), then the splits round by round: each
+        round's splits whose Q and R are formed take their products Q T_g together where they land on one top"""
         specs = []
         self._walk(c, top, scale, lambda *sp: specs.append(sp))
         vals = iter(self.ev.lincombs(specs))
-        return self._walk(c, top, scale, lambda *sp: next(vals))
+        tree = self._walk(c, top, scale, lambda *sp: next(vals))
+        while not isinstance(tree, Ct):
+            ready = []
+
+            def visit(n):
+                if isinstance(n, Ct):
+                    return
+                if isinstance(n[1], Ct) and isinstance(n[2], Ct):
+                    ready.append(n)
+                else:
+                    visit(n[1])
+                    visit(n[2])
+
+            visit(tree)
+            for t in dict.fromkeys(n[0].top for n in ready):
+                grp = [n for n in ready if n[0].top == t]
+                for n, P in zip(grp, self.ev.mul_many([(n[1], n[0]) for n in grp])):
+                    n.append(self.ev.add(P, n[2]))
+            tree = self._resolve(tree)
+        return tree
+
+    @staticmethod
+    def _resolve(n):
+        """a split whose sum is formed (its fourth entry) becomes that value"""
+        if isinstance(n, Ct):
+            return n
+        if len(n) == 4:
+            return n[3]
+        n[1], n[2] = ChebEval._resolve(n[1]), ChebEval._resolve(n[2])
+        return n
 
 
 # ----------------------------------------------------------------------------------------------- the composite

@@ -921,6 +921,15 @@ int pcx_rotate_and_sum_noalloc(pcx_ctx* c, pcx_keys* k, const void* x, int top, 
  * res + j ct_words. */
 int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
                   uint32_t enc, const void* ct, int top, void* res, pc_stream_t s);
+/* pcx_cts_stage's words by the hoisted route (no counterpart in the reference, whose stage fuses the babies' key
+ * products with the diagonal products): rot_0 = P ct (the table's ew_scale, special rows zeroed), one ModUp and one
+ * key-dot launch for the B - 1 babies (each key regenerated once) into rot's extended ciphertexts 1..B-1, then the
+ * table's pt_dot over Q rows 0..top and the special rows. rot: B extended ciphertexts of workspace (ct_words apart). */
+int pcx_cts_stage_hoisted(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
+                          uint32_t enc, const void* ct, int top, void* rot, void* res, pc_stream_t s);
+/* pcx_moddown of m <= k_rot extended ciphertexts (ct_words apart) into m ciphertexts in one launch sequence (no
+ * counterpart in the reference beyond its k_max batching of ModDown). */
+int pcx_moddown_k(pcx_ctx* c, void* ext, int top, void* out, int m, pc_stream_t s);
 /* The relinearization key s^2 -> s (crates/pc-gpu/src/keygen.rs:225-226): one key of galois 1 generated as
  * pcx_keys_generate's, its old secret squared in the kernel (KskGenArgs.sq). */
 pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed, const int64_t* errors, int bits,

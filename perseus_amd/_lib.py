@@ -79,6 +79,9 @@ _SIGS = {
     "pcx_rotate_and_sum_noalloc": (C.c_int, [vp, vp, vp, C.c_int, C.c_int64, C.c_int64, C.c_int, vp, vp]),
     "pcx_cts_stage": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_uint32, vp, C.c_int, vp,
                                 vp]),
+    "pcx_cts_stage_hoisted": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_uint32, vp,
+                                        C.c_int, vp, vp, vp]),
+    "pcx_moddown_k": (C.c_int, [vp, vp, C.c_int, vp, C.c_int, vp]),
     "pcx_keys_relin": (vp, [vp, C.POINTER(C.c_int8), u32p, C.POINTER(C.c_int64), C.c_int, C.POINTER(C.c_int)]),
     "pcx_rescale": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
     "pcx_rescale_k": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, C.c_int, vp]),

@@ -568,7 +568,7 @@ class Bootstrap:
     an operations object. `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
     scale par.delta_in. Plaintexts (the levels' diagonals, the i monomial) are encoded once by `prepare`."""
 
-    def __init__(self, ops, par, primes, ops2=None, special=None, pair=None):
+    def __init__(self, ops, par, primes, ops2=None, special=None, pair=None, fuse_stc=True):
         self.ops, self.par, self.ops2 = ops, par, ops2
         # pair: the two EvalMod chains batched (K = 2) on ops, which must take two ciphertexts per product; by default
         # whenever ops can and no second lane is given
@@ -583,6 +583,11 @@ class Bootstrap:
         n = par.n
         self.cts = [BsgsPlan(lv, n) for lv in cts_levels(n, par.cts)]
         self.stc = [BsgsPlan(lv, n) for lv in stc_levels(n, par.stc)]
+        # per level (CtS, then StC): fused in the extended basis, else hoisted babies and the plaintext dot over Q. The
+        # fused form takes a ModDown per giant step instead of one per baby, so it pays where a level has fewer giant
+        # steps than babies (CtS); fuse_stc False keeps the StC levels hoisted
+        fz = self.p is not None
+        self.fuse = [fz] * len(self.cts) + [fz and fuse_stc] * len(self.stc)
         self.em = EvalModPlan(par.K, par.deg, par.r)
         self.ev = Evaluator(ops, self.q)
         self.q0 = float(self.q[0])
@@ -612,23 +617,22 @@ class Bootstrap:
         top = self.T
         for plans, f in ((self.cts, self.cts_f), (self.stc, 1.0)):
             for p in plans:
+                fused = self.fuse[len(self.pts)]
                 sc = self.ev.qq(top) * f
-                prim = self.q[: top + 1] + (self.p or [])
+                prim = self.q[: top + 1] + (self.p if fused else [])
                 coef = [[None if d is None else encode_rows(d, N, sc, prim) for d in p.pts[j]] for j in range(p.G)]
-                # the plaintext dot reads a level's diagonals at one compact width (the fused stage at full width)
-                s = 0
-                if self.p is None:
-                    s = min((compact_shift(c) for r in coef for c in r if c is not None), default=0)
+                # the plaintext dot (and the fused stage) reads a level's diagonals at one compact width
+                s = min((compact_shift(c) for r in coef for c in r if c is not None), default=0)
                 row = []
                 for j in range(p.G):
                     for i in range(p.B):
                         c = coef[j][i]
                         if c is None:
                             row.append(None)
-                        elif self.p is None:
+                        elif not fused:
                             row.append(ops.plaintext(c, top, s))
                         else:
-                            row.append(ops.plaintext_ext(c, top))
+                            row.append(ops.plaintext_ext(c, top, s))
                 self.pts.append(row)
                 self.pt_s.append(s)
                 top -= 2
@@ -641,31 +645,36 @@ class Bootstrap:
         mono_m[:, N // 2] = [p - 1 for p in self.q]  # -X^(N/2): -i
         self.mono_mi = ops.plaintext(mono_m, self.T)
 
-    def lt(self, x, plan, pts, f, s=0, rots=None, dest=None):
+    def lt(self, x, plan, pts, f, s=0, rots=None, dest=None, fused=False):
         """one BSGS level: pts its diagonals (None where zero), s their compact shift (rows of width N >> s). rots: a
         buffer of B ciphertexts whose first already holds x (else x is copied into a new one); dest: where the output
-        goes (else a new ciphertext)"""
+        goes (else a new ciphertext); fused: the babies in the extended basis (pts encoded over Q and P)"""
         ops, top = self.ops, x.top
         B, G = plan.B, plan.G
         res = ops.alloc(G)
-        if self.p is None:
+        if not fused:
             if rots is None:
                 rots = ops.alloc(B)
                 ops.copy(ops.item(rots, 0), x.h, top)
             ops.hoisted(ops.item(rots, 1), x.h, top, [b % self.par.n for b in plan.baby[1:]])
             ops.pt_dot(res, rots, top, pts, B, G, s)
         else:
-            ops.cts(res, x.h, top, pts, B, G)
+            ops.cts(res, x.h, top, pts, B, G, s)
         # the giant steps: the rotated results' key dots summed in the extended basis, one ModDown onto the
         # unrotated result
+        if fused:
+            # the fused stage's G extended results brought down to Q, one batched ModDown where the operations have it
+            q = ops.alloc(G)
+            if hasattr(ops, "moddown_k"):
+                ops.moddown_k(q, res, top, G)
+            else:
+                for j in range(G):
+                    ops.moddown(ops.item(q, j), ops.item(res, j), top)
+            res = q
         base, ys, gs = None, [], []
         for j in range(G):
             g = plan.giant[j] % self.par.n
             y = ops.item(res, j)
-            if self.p is not None:
-                t = ops.alloc()
-                ops.moddown(t, y, top)
-                y = t
             if g:
                 ys.append(y)
                 gs.append(g)
@@ -703,18 +712,19 @@ class Bootstrap:
             self.ops2.begin()
         # each level's input is written straight into the first slot of that level's rotation buffer (the plaintext
         # dot reads the unrotated input there), so no level copies it
-        hoist = self.p is None
-        nxt = ops.alloc(self.cts[0].B) if hoist else None
-        raised = ops.item(nxt, 0) if hoist else ops.alloc()
+        plans = self.cts + self.stc
+        hoist = [not fz for fz in self.fuse]
+        nxt = ops.alloc(plans[0].B) if hoist[0] else None
+        raised = ops.item(nxt, 0) if hoist[0] else ops.alloc()
         ops.mod_raise(raised, x_h, self.T)
         ops.mul_const(raised, raised, self.T, self.lift)
         x = Ct(raised, self.T, self.raise_scale)
         k = 0
         for i, p in enumerate(self.cts):
             rots = nxt
-            nxt = ops.alloc(self.cts[i + 1].B) if hoist and i + 1 < len(self.cts) else None
+            nxt = ops.alloc(plans[k + 1].B) if hoist[k + 1] and i + 1 < len(self.cts) else None
             x = self.lt(x, p, self.pts[k], self.cts_f, self.pt_s[k], rots=rots,
-                        dest=ops.item(nxt, 0) if nxt is not None else None)
+                        dest=ops.item(nxt, 0) if nxt is not None else None, fused=self.fuse[k])
             k += 1
         cj = ops.alloc()
         ops.rotate(cj, x.h, x.top, "conj")
@@ -739,8 +749,8 @@ class Bootstrap:
             ops.join(self.ops2)
         ii = ops.alloc()
         ops.mul_pt(ii, im.h, im.top, self.mono_i)
-        nxt = ops.alloc(self.stc[0].B) if hoist else None
-        if hoist:
+        nxt = ops.alloc(self.stc[0].B) if hoist[k] else None
+        if hoist[k]:
             assert abs(re.scale / im.scale - 1.0) < 1e-9 and re.top == im.top
             ops.add(ops.item(nxt, 0), re.h, ii, re.top, False)
             w = Ct(ops.item(nxt, 0), re.top, re.scale)
@@ -748,9 +758,9 @@ class Bootstrap:
             w = ev.add(re, Ct(ii, im.top, im.scale))
         for i, p in enumerate(self.stc):
             rots = nxt
-            nxt = ops.alloc(self.stc[i + 1].B) if hoist and i + 1 < len(self.stc) else None
+            nxt = ops.alloc(plans[k + 1].B) if i + 1 < len(self.stc) and hoist[k + 1] else None
             w = self.lt(w, p, self.pts[k], 1.0, self.pt_s[k], rots=rots,
-                        dest=ops.item(nxt, 0) if nxt is not None else None)
+                        dest=ops.item(nxt, 0) if nxt is not None else None, fused=self.fuse[k])
             k += 1
         # the slot values are now (2 pi / q0) times the message's at the input's scale: relabel
         w.scale = w.scale * 2.0 * math.pi * par.delta_in / self.q0
@@ -853,6 +863,8 @@ class GpuOps:
         self.N, self.R, self.nq = ctx.n, ctx.rows, ctx.nq
         self.cw = ctx.ct_words
         self.kmax = ctx.k_max  # ciphertexts per batched rescale
+        # the fused stage's words by the hoisted route (babies' keys regenerated once per level) instead of cts_k
+        self.cts_hoisted = True
         self.primes = [int(p) for p in ctx.chain.primes]
         self.pr = LIB.pcx_ctx_primes(ctx.h)
         self.pool, self.cur = [], 0
@@ -988,20 +1000,24 @@ class GpuOps:
             buf = self.eng.DevBuf.from_array(compact_rows(buf.download((top + 1, self.N), self.st), s))
         return buf
 
-    def plaintext_ext(self, coef_rows, top):
+    def plaintext_ext(self, coef_rows, top, s=0):
         """coefficient residue rows over Q 0..top then the special primes -> a device plaintext [top + 1 + kp][N] in
-        evaluation form (the extended basis of the fused stage)"""
+        evaluation form (the extended basis of the fused stage); compact [top + 1 + kp][N >> s] as plaintext's"""
         kp = self.R - self.nq
         rows = top + 1 + kp
         buf = self.eng.DevBuf.from_array(np.ascontiguousarray(coef_rows[:rows], np.uint32))
         ids = list(range(top + 1)) + [self.nq + j for j in range(kp)]
         self._rows(list(range(rows)), ids).ntt(buf, 1, self.st)
         self.st.sync()
+        if s:
+            buf = self.eng.DevBuf.from_array(compact_rows(buf.download((rows, self.N), self.st), s))
         return buf
 
-    def cts(self, res, x, top, pts, B, G):
+    def cts(self, res, x, top, pts, B, G, s=0):
         """res_j = sum_i rot_i(x) pt_{B j + i} in the extended basis (pcx_cts_stage: one ModUp, the babies' key
-        switches before ModDown, keys regenerated in the kernel)"""
+        switches before ModDown, keys regenerated in the kernel; or its hoisted route); s: the diagonals' compact
+        shift"""
+        ptw, enc = self.N >> s, (0x7F000000 | s) if s else 0xFFFFFFFF
         key = ("cptr", tuple(id(p) for p in pts))
         if key not in self.cache:
             if any(p is None for p in pts) and "zero_ext" not in self.cache:
@@ -1011,8 +1027,16 @@ class GpuOps:
             ptrs = np.array([(self.cache["zero_ext"] if p is None else p).ptr.value for p in pts], np.uint64)
             self.cache[key] = self.eng.DevBuf.from_array(ptrs.view(np.uint32))
         babies = self.levels[self.level_i][0]
-        self.ctx.cts_stage(self.keys, babies[0] if babies else 0, B, G, self.cache[key], B * G, self.N, 0xFFFFFFFF, x,
-                           top, res, self.st)
+        if self.cts_hoisted:
+            rot = self.alloc(B)
+            self.ctx.cts_stage_hoisted(self.keys, babies[0] if babies else 0, B, G, self.cache[key], B * G, ptw, enc,
+                                       x, top, rot, res, self.st)
+        else:
+            self.ctx.cts_stage(self.keys, babies[0] if babies else 0, B, G, self.cache[key], B * G, ptw, enc, x, top,
+                               res, self.st)
+
+    def moddown_k(self, out, ext, top, m):
+        self.ctx.moddown_k(ext, top, out, m, self.st)
 
     def moddown(self, out, ext, top):
         self.ctx.moddown(ext, top, out, self.st)

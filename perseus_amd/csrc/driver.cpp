@@ -1475,6 +1475,55 @@ int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ou
     return moddown(c, c->ext, c->conv, 1, top, out, s);
 }
 
+int pcx_cts_stage_hoisted(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
+                          uint32_t enc, const void* ct, int top, void* rot, void* res, pc_stream_t s) {
+    const Level* L = c ? level(c, top) : nullptr;
+    if (!L || !k || k->c != c || B < 1 || G < 1 || npts < 0 || !pts || !ct || !rot || !res) return -1;
+    if (B > 1 && (r0 < 0 || r0 + B - 1 > k->nkeys)) return -1;
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    // rot_0 = P ct on Q rows 0..top, zero on the special rows
+    EwArgs e;
+    memset(&e, 0, sizeof e);
+    e.out = PolyRef{rot, 2 * part, part};
+    e.a = PolyRef{const_cast<void*>(ct), 2 * part, part};
+    e.rs = RowSet{top + 1, c->kp, c->nq, 0};
+    e.sc = c->pmod;
+    e.scs = c->pmod + (c->nq + c->kp);
+    e.pr = c->pr;
+    e.K = 1;
+    e.nparts = 2;
+    e.zero_p = 1;
+    if (int er = c->tab->ew_scale(&e, s)) return er;
+    // rot_i (i >= 1): the babies' key switches before ModDown, one ModUp and one dot launch for the B - 1 keys
+    if (B > 1) {
+        if (int er = modup(c, ct, top, s)) return er;
+        if (int er = dot(c, k, r0, B - 1, ct, top, (uint32_t*)rot + c->ct_words(), s)) return er;
+    }
+    PtDotArgs a;
+    memset(&a, 0, sizeof a);
+    a.rot = PolyRef{rot, (uint64_t)B * c->ct_words(), part};
+    a.res = PolyRef{res, (uint64_t)G * c->ct_words(), part};
+    a.rot_stride = c->ct_words();
+    a.res_stride = c->ct_words();
+    a.pts = pts;
+    a.pr = c->pr;
+    a.rs = RowSet{top + 1, c->kp, c->nq, 0};
+    a.npts = npts;
+    a.bstep = B;
+    a.gstep = G;
+    a.K = 1;
+    a.ptw = ptw;
+    a.pt_prow = top + 1;
+    a.enc = enc;
+    Stage st(c, 7, s);
+    return c->tab->pt_dot(&a, s);
+}
+
+int pcx_moddown_k(pcx_ctx* c, void* ext, int top, void* out, int m, pc_stream_t s) {
+    if (!c || !ext || !out || m < 1 || m > c->k_rot || !level(c, top)) return -1;
+    return moddown(c, ext, c->conv, m, top, out, s);
+}
+
 int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* const* pts, int npts, int ptw,
                   uint32_t enc, const void* ct, int top, void* res, pc_stream_t s) {
     const Level* L = c ? level(c, top) : nullptr;

@@ -289,6 +289,16 @@ class Context:
         check(LIB.pcx_cts_stage(self.h, keys.h, r0, B, G, pts.addr(), npts, ptw, enc, ct.addr(), top, res.addr(),
                                 stream.h), "cts_stage")
 
+    def cts_stage_hoisted(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, rot, res, stream):
+        """cts_stage's words by the hoisted route (pcx_cts_stage_hoisted): rot_0 = P ct, one ModUp and one key-dot
+        launch for the babies into rot's B extended ciphertexts, then the plaintext dot over the extended rows."""
+        check(LIB.pcx_cts_stage_hoisted(self.h, keys.h, r0, B, G, pts.addr(), npts, ptw, enc, ct.addr(), top,
+                                        rot.addr(), res.addr(), stream.h), "cts_stage_hoisted")
+
+    def moddown_k(self, ext, top, out, m, stream):
+        """ModDown of m extended ciphertexts into m ciphertexts, one launch sequence (pcx_moddown_k)"""
+        check(LIB.pcx_moddown_k(self.h, ext.addr(), top, out.addr(), m, stream.h), "moddown_k")
+
 
 class Keys:
     """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed. relin:

@@ -74,12 +74,12 @@ class OracleOps:
         ids = list(range(top + 1))
         return compact_rows(self.oc.ntt_fwd(np.ascontiguousarray(coef_rows[: top + 1], np.uint32).copy(), ids), s)
 
-    def plaintext_ext(self, coef_rows, top):
+    def plaintext_ext(self, coef_rows, top, s=0):  # full rows: the compact form is the GPU's storage of the same values
         kp = self.R - len(self.q)
         ids = list(range(top + 1)) + [len(self.q) + j for j in range(kp)]
         return self.oc.ntt_fwd(np.ascontiguousarray(coef_rows[: top + 1 + kp], np.uint32).copy(), ids)
 
-    def cts(self, res, x, top, pts, B, G):
+    def cts(self, res, x, top, pts, B, G, s=0):
         kp = self.R - len(self.q)
         zero = np.zeros((top + 1 + kp, self.N), np.uint32)
         full = [zero if p is None else p for p in pts]

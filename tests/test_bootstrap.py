@@ -87,7 +87,7 @@ def test_simulated_bootstrap():
 
 def setup_oracle(logn=12, seed=5, fused=True, chain=None):
     """a chain with the bootstrap's levels plus one spare (three limbs out), or the given chain (q, p, dnum), oracle
-    keys, the composite (fused: the levels' babies in the extended basis)"""
+    keys, the composite (fused: the levels' babies in the extended basis; "cts": the CtS levels' only)"""
     par = B.Params(logn)
     if chain is None:
         nq = 1 + 2 * par.levels_used() + 2
@@ -101,7 +101,7 @@ def setup_oracle(logn=12, seed=5, fused=True, chain=None):
     g = twin.Prng([seed, 2, 7, 1, 8, 2, 8, 1], 0)
     s = g.sparse_ternary(1 << logn, 192)
     s_eval = oc.secret_eval(s)
-    boot = B.Bootstrap(None, par, q, special=p if fused else None)
+    boot = B.Bootstrap(None, par, q, special=p if fused else None, fuse_stc=fused != "cts")
     gal, levels, conj = B.key_plan(boot)
     keys = [oc.rotation_key(g, s_eval, x) for x in gal]
     seeds = np.stack([k[0] for k in keys])
@@ -138,7 +138,7 @@ def decrypt_slots(S, ct, top, scale):
     return decode(coef, S["par"].N, scale)
 
 
-@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("fused", [True, False, "cts"])
 def test_bootstrap_on_the_oracle(fused):
     S = setup_oracle(fused=fused)
     boot, ops = S["boot"], S["ops"]

@@ -38,13 +38,14 @@ def gpu_boot(S, lanes=1):
                          relin=True)
         ops2 = B.GpuOps(ctx2, None, relin2, S["levels"], S["conj"], pa.Stream())
         ops2.keep = (ctx2, relin2)
-    boot = B.Bootstrap(ops, par, q, ops2, special=S["p"] if S["fused"] else None)
+    boot = B.Bootstrap(ops, par, q, ops2, special=S["p"] if S["fused"] else None, fuse_stc=S["fused"] != "cts")
     assert boot.pair == (lanes == "pair")
     boot.prepare()
     return ctx, keys, relin, st, ops, boot
 
 
-@pytest.mark.parametrize("lanes,fused", [(1, False), (2, True), (1, True), ("pair", False), ("pair", True)])
+@pytest.mark.parametrize("lanes,fused", [(1, False), (2, True), (1, True), ("pair", False), ("pair", True),
+                                         ("pair", "cts")])
 def test_bootstrap_gpu_matches_the_oracle(lanes, fused):
     say(f"[bootstrap] N=2^12, {lanes} EvalMod lane(s), fused babies {fused}: GPU composite vs the oracle composite, "
         "decryption, rerun")

@@ -40,7 +40,7 @@ def test_bootstrap_c5_matches_the_oracle():
     twin.set_threads(min(16, os.cpu_count() or 1))
     ch = pa.preset("c5")
     t0 = time.time()
-    S = setup_oracle(logn=ch.logn, seed=55, fused=False, chain=(ch.q, ch.p, ch.dnum))
+    S = setup_oracle(logn=ch.logn, seed=55, fused="cts", chain=(ch.q, ch.p, ch.dnum))
     par = S["par"]
     say(f"[bootstrap c5] {len(S['gal'])} rotation keys from the oracle in {time.time() - t0:.1f} s")
     rng = np.random.default_rng(505)
@@ -54,7 +54,7 @@ def test_bootstrap_c5_matches_the_oracle():
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()
     ops = B.GpuOps(ctx, keys, relin, S["levels"], S["conj"], st)
-    boot = B.Bootstrap(ops, par, ch.q)
+    boot = B.Bootstrap(ops, par, ch.q, special=ch.p, fuse_stc=False)
     assert boot.pair
     boot.prepare()
     x = pa.DevBuf.from_array(ct)

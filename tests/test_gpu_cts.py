@@ -86,8 +86,12 @@ def oracle_keys(oc, ch, steps, seed):
     ("rej", 4, 2, 8, FULL, 5, 0),             # a third of the KSKA words rejected: the wave's redraw queue
     ("small28", 9, 4, 33, FULL, 5, 28),       # 28-bit primes, more than 8 baby steps: the reference's own regime
 ])
-def test_cts_stage(stream, name, B, G, npts, enc, top, bits):
-    say(f"[cts stage] {name} B={B} G={G} npts={npts} enc={enc:#x} top={top} bits={bits}")
+@pytest.mark.parametrize("route", ["fused", "hoisted"])
+def test_cts_stage(stream, name, B, G, npts, enc, top, bits, route):
+    """pcx_cts_stage (fused: the cts_fused_regen kernel) and pcx_cts_stage_hoisted (P ct, the babies' dots into a
+    workspace of extended ciphertexts, pt_dot over the extended rows) against the oracle's fused stage; the hoisted
+    route's results then through pcx_moddown_k (all G in one launch sequence) against the oracle's ModDown of each."""
+    say(f"[cts stage] {route} {name} B={B} G={G} npts={npts} enc={enc:#x} top={top} bits={bits}")
     ch, ctx, oc = contexts(name)
     twin.set_threads(16)
     rng = np.random.default_rng(B * 31 + G)
@@ -101,7 +105,11 @@ def test_cts_stage(stream, name, B, G, npts, enc, top, bits):
     ptrs = dev_ptrs(pbufs)
     dev = pa.DevBuf.from_array(ct)
     res = ctx.ct_buf(G)
-    ctx.cts_stage(keys, 0, B, G, ptrs, npts, ptw, enc, dev, top, res, stream)
+    if route == "fused":
+        ctx.cts_stage(keys, 0, B, G, ptrs, npts, ptw, enc, dev, top, res, stream)
+    else:
+        rot = ctx.ct_buf(B)
+        ctx.cts_stage_hoisted(keys, 0, B, G, ptrs, npts, ptw, enc, dev, top, rot, res, stream)
     stream.sync()
     got = res.download((G, 2, ch.rows, ch.n))
     digits = oc.modup(ct[1], top)
@@ -109,6 +117,14 @@ def test_cts_stage(stream, name, B, G, npts, enc, top, bits):
     rs = ext_rows(ch, top)
     for j in range(G):
         assert (got[j][:, rs] == want[j][:, rs]).all(), j
+    if route == "hoisted":
+        out = ctx.ct_buf(G)
+        ctx.moddown_k(res, top, out, G, stream)
+        stream.sync()
+        gq = out.download((G, 2, ch.rows, ch.n))
+        for j in range(G):
+            wq = oc.moddown(want[j].copy(), top)
+            assert (gq[j][:, : top + 1] == wq[:, : top + 1]).all(), f"moddown {j}"
 
 
 # ----------------------------------------------------------------------------------------------- table entries

@@ -965,6 +965,10 @@ int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, co
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
  * form rows by prime id (rows 0..top read). out may be ct. */
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);
+/* pcx_mul_plain of K <= 8 ciphertexts (ct and out each K consecutive ciphertexts), ciphertext j by its own plaintext
+ * pts[j], in one launch. No counterpart in the reference, whose mul_table multiplies its K ciphertexts by one table:
+ * for a batch of independent scorings (one plaintext query per ciphertext). */
+int pcx_mul_plain_k(pcx_ctx* c, const void* ct, const void* const* pts, int K, int top, void* out, pc_stream_t s);
 /* the stages alone, for tests and profiles: ModUp of ct's c1 into the context's digit workspace; the dot of key r
  * into ext (one extended ciphertext); ModDown of ext into out */
 int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);

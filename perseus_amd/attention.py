@@ -89,15 +89,11 @@ def score(ctx, keys, ct, pt, top, out, tmp, stream, radix_bits=RADIX_BITS):
 
 def score_batch(ctx, keys, cts, pts, top, outs, tmp, stream, radix_bits=RADIX_BITS):
     """Every ciphertext's scores at once: cts, outs and tmp each K consecutive ciphertexts of one buffer (the ctx's
-    k_max and k_rot at least K), pts the K plaintexts; the plaintext products one per ciphertext, then the two-prime
-    rescale and the ladder as K-ciphertext launches (pcx_rescale_k, pcx_rotate_and_sum_k). The words of score() on
-    each ciphertext."""
-    from .bootstrap import View
-
+    k_max and k_rot at least K), pts the K plaintexts; the plaintext products (each ciphertext by its own plaintext),
+    the two-prime rescale and the ladder as K-ciphertext launches (pcx_mul_plain_k, pcx_rescale_k,
+    pcx_rotate_and_sum_k). The words of score() on each ciphertext."""
     K = len(pts)
-    for j, pt in enumerate(pts):
-        ctx.mul_plain(View(cts.buf, cts.off + j * ctx.ct_words), pt, top, View(outs.buf, outs.off + j * ctx.ct_words),
-                      stream)
+    ctx.mul_plain_k(cts, pts, top, outs, stream)
     ctx.rescale(outs, top, 2, outs, stream, K=K)
     ctx.rotate_and_sum(keys, outs, top - 2, 1, BLOCK, outs, tmp, stream, radix_bits=radix_bits, K=K)
 

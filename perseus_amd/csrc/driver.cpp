@@ -1957,6 +1957,24 @@ int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, co
     return moddown_rescale(c, c->ext, top, out, folded ? nullptr : out, s, K);
 }
 
+int pcx_mul_plain_k(pcx_ctx* c, const void* ct, const void* const* pts, int K, int top, void* out, pc_stream_t s) {
+    if (!c || !ct || !pts || !out || top < 0 || top >= c->nq || K < 1 || K > pch::TLIST_MAX) return -1;
+    pch::MulPtListArgs m;
+    memset(&m, 0, sizeof m);
+    for (int j = 0; j < K; ++j) {
+        if (!pts[j]) return -1;
+        m.t[j] = (const uint32_t*)pts[j];
+    }
+    m.in = (const uint32_t*)ct;
+    m.out = (uint32_t*)out;
+    m.part = (uint64_t)c->rows * c->n;
+    m.ct_stride = c->ct_words();
+    m.pr = c->pr;
+    m.n = top + 1;
+    m.K = K;
+    return pch::mul_pt_list((int)c->logn, &m, s);
+}
+
 // The plaintext product (crates/pc-gpu/src/ops.rs:927-951 mult_pt, the table's mul_table, em.cuh:508-515): out = ct pt
 // on Q rows 0..top of both parts, pt one plaintext of evaluation-form rows by prime id. out may be ct.
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s) {

@@ -267,6 +267,19 @@ __global__ void __launch_bounds__(BX) mul_k(MulAddNArgs A, int logn) {
     st4(at(A.out, c, part, row, logn) + i, r);
 }
 
+// out[c] = in[c] t[c] on both parts (ciphertext c = blockIdx.z >> 1, its own plaintext)
+__global__ void __launch_bounds__(BX) mul_pt_list_k(MulPtListArgs A, int logn) {
+    const int row = blockIdx.y, part = blockIdx.z & 1, c = blockIdx.z >> 1;
+    const size_t ro = ((size_t)row << logn) + lane_word();
+    const Red red(A.pr[row]);
+    const W4 x = ld4(A.in + c * A.ct_stride + part * A.part + ro);
+    const W4 t = ld4(A.t[c] + ro);
+    W4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r.v[w] = red((uint64_t)x.v[w] * t.v[w]);
+    st4(A.out + c * A.ct_stride + part * A.part + ro, r);
+}
+
 // x_i = alpha_i x_i + tmp_i (rescale_combine), or out_i = alpha_i x_i + tmp_i (rescale_combine_to)
 __global__ void __launch_bounds__(BX) combine_k(RescaleCombineToArgs R, int logn) {
     const RescaleCombineArgs& A = R.a;
@@ -472,6 +485,14 @@ int tensor_list(const TensorListArgs* a, pc_stream_t s) {
         if (!a->a[c] || !a->b[c]) return -1;
     if (a->n == 0 || a->K == 0) return 0;
     PCH_LAUNCH(tensor_list_k, grid<LOGN>(a->n, a->K), *a, LOGN);
+}
+template <int LOGN>
+int mul_pt_list(const MulPtListArgs* a, pc_stream_t s) {
+    if (!a || !a->pr || !a->in || !a->out || a->n < 0 || a->K < 0 || a->K > TLIST_MAX) return -1;
+    for (int c = 0; c < a->K; ++c)
+        if (!a->t[c]) return -1;
+    if (a->n == 0 || a->K == 0) return 0;
+    PCH_LAUNCH(mul_pt_list_k, grid<LOGN>(a->n, 2 * a->K), *a, LOGN);
 }
 template <int LOGN>
 int tensor_y(const TensorYArgs* a, pc_stream_t s) {
@@ -793,6 +814,17 @@ PCH_EM_INST(13)
 PCH_EM_INST(14)
 PCH_EM_INST(15)
 PCH_EM_INST(16)
+
+int mul_pt_list(int logn, const MulPtListArgs* a, pc_stream_t s) {
+    switch (logn) {
+        case 12: return em::mul_pt_list<12>(a, s);
+        case 13: return em::mul_pt_list<13>(a, s);
+        case 14: return em::mul_pt_list<14>(a, s);
+        case 15: return em::mul_pt_list<15>(a, s);
+        case 16: return em::mul_pt_list<16>(a, s);
+        default: return -2;
+    }
+}
 
 int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s) {
     switch (logn) {

@@ -88,6 +88,18 @@ struct TensorListArgs {
     int n, K, dbl;
 };
 int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s);
+// The plaintext products of K ciphertexts (K consecutive, ct_stride apart; out likewise), ciphertext c by its own
+// plaintext t[c] (evaluation-form rows by prime id): rows 0..n-1 of both parts (driver-internal: the reference's
+// mul_table takes one plaintext for its K ciphertexts)
+struct MulPtListArgs {
+    const uint32_t* in;
+    uint32_t* out;
+    const uint32_t* t[TLIST_MAX];
+    uint64_t part, ct_stride;
+    const PrimeConst* pr;
+    int n, K;
+};
+int mul_pt_list(int logn, const MulPtListArgs* a, pc_stream_t s);
 
 // ks_dot_key's summed rotations (c0_mode | KS_SUM): out = sum_r sigma_r(dot_r), gathered in output order
 int ks_dot_key_sum(int logn, const KsKeyArgs* g, pc_stream_t s);

@@ -259,6 +259,11 @@ class Context:
         """out = ct pt on Q rows 0..top (pcx_mul_plain); pt a DevBuf of evaluation-form rows by prime id."""
         check(LIB.pcx_mul_plain(self.h, ct.addr(), pt.addr(), top, out.addr(), stream.h), "mul_plain")
 
+    def mul_plain_k(self, ct, pts, top, out, stream):
+        """ct and out each len(pts) consecutive ciphertexts: out_j = ct_j pts[j] in one launch (pcx_mul_plain_k)."""
+        arr = (C.c_void_p * len(pts))(*[p.addr() for p in pts])
+        check(LIB.pcx_mul_plain_k(self.h, ct.addr(), arr, len(pts), top, out.addr(), stream.h), "mul_plain_k")
+
     def mul_relin(self, keys, a, b, top, out, stream):
         """out = a b relinearized by key 0 of keys (pcx_mul_relin)."""
         check(LIB.pcx_mul_relin(self.h, keys.h, a.addr(), b.addr(), top, out.addr(), stream.h), "mul_relin")

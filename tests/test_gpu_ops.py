@@ -269,3 +269,30 @@ def test_product_twice(stream, name, top, K):
         a2[:, : top + 1] = (2 * a[k][:, : top + 1].astype(np.uint64) % q).astype(np.uint32)
         want = oc.mul_relin_rescale(a2, b[k], top, seed, keys2.download_b(0))
         assert (got[k][:, : top - 1] == want[:, : top - 1]).all(), f"pair {k}"
+
+
+@pytest.mark.parametrize("name,top,K", [("small", 5, 3), ("c3", 29, 6)])
+def test_mul_plain_k(stream, name, top, K):
+    """pcx_mul_plain_k: K consecutive ciphertexts, each by its own plaintext, in one launch (also in place): each
+    output equals pcx_mul_plain's (the table's mul_table) on that ciphertext."""
+    say(f"[mul_plain_k] {name} top={top} K={K}")
+    ch, ctx, _ = contexts(name)
+    rng = np.random.default_rng(top + K)
+    x = np.stack([random_ct(ch, top, rng) for _ in range(K)])
+    pts = [np.stack([rng.integers(0, p, ch.n) for p in ch.primes]).astype(np.uint32) for _ in range(K)]
+    bpts = [pa.DevBuf.from_array(p) for p in pts]
+    want = []
+    for j in range(K):
+        bx, o = pa.DevBuf.from_array(x[j]), ctx.ct_buf(1)
+        ctx.mul_plain(bx, bpts[j], top, o, stream)
+        stream.sync()
+        want.append(o.download((2, ch.rows, ch.n)))
+    bx = pa.DevBuf.from_array(x)
+    out = ctx.ct_buf(K)
+    ctx.mul_plain_k(bx, bpts, top, out, stream)
+    ctx.mul_plain_k(bx, bpts, top, bx, stream)  # in place
+    stream.sync()
+    got, got2 = out.download((K, 2, ch.rows, ch.n)), bx.download((K, 2, ch.rows, ch.n))
+    for j in range(K):
+        assert (got[j][:, : top + 1] == want[j][:, : top + 1]).all(), j
+        assert (got2[j][:, : top + 1] == want[j][:, : top + 1]).all(), j

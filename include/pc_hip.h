@@ -778,6 +778,25 @@ const KernelTable* pc_table_u32_logn(uint32_t log_n);
 int pc_hip_device_count(int* n);
 int pc_hip_set_device(int dev);
 int pc_hip_device_name(int dev, char* out, int len);
+/* cudaRuntimeGetVersion / cudaDriverGetVersion (crates/pc-cuda/src/device.rs:83-84, Device::open): HIP's numbers */
+int pc_hip_runtime_version(int* v);
+int pc_hip_driver_version(int* v);
+/* cudaDeviceGetAttribute (device.rs:115 sm_count, :126 clusters). attr takes the cudaDeviceAttr numbers the reference
+ * passes (16: compute units; 75 / 76: the gfx major / minor HIP reports, 9 / 5 on gfx950), PC_HIP_ATTR_CLUSTERS (0:
+ * CDNA has no thread-block clusters, the value Device::clusters should read) and PC_HIP_ATTR_GFX_ARCH (the gfx code as
+ * hexadecimal digits, 0x950). Any other attr: hipErrorInvalidValue. */
+#define PC_HIP_ATTR_CU_COUNT 16
+#define PC_HIP_ATTR_CC_MAJOR 75
+#define PC_HIP_ATTR_CC_MINOR 76
+#define PC_HIP_ATTR_CLUSTERS 0x10000
+#define PC_HIP_ATTR_GFX_ARCH 0x10001
+int pc_hip_device_attribute(int* v, int attr, int dev);
+/* cudaMemGetInfo (device.rs:137 mem_info, :188 mem_info_current): free and total bytes of the current device */
+int pc_hip_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+/* cudaProfilerStart / cudaProfilerStop (device.rs:151-158 profiler): synchronise the device, then ask a running
+ * rocprofv3 to resume / pause collection (roctx, its --selected-regions mode); a no-op without a profiler */
+int pc_hip_profiler_start(void);
+int pc_hip_profiler_stop(void);
 int pc_hip_malloc(void** p, size_t bytes);
 int pc_hip_free(void* p);
 int pc_hip_malloc_host(void** p, size_t bytes);
@@ -789,11 +808,20 @@ int pc_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, pc_stream_t s);
  * enqueued on s as a fill kernel (so a captured replay holds no memset node) */
 int pc_hip_memset(void* dst, int value, size_t bytes, pc_stream_t s);
 int pc_hip_stream_create(pc_stream_t* s);
+/* cudaDeviceGetStreamPriorityRange / cudaStreamCreateWithPriority (stream.rs:33-44, Stream::high_priority): every
+ * stream of this library runs at the default priority (mixed-priority streams have been seen to stall on MI355X), so
+ * the range reads (0, 0) and the priority argument is accepted and not applied */
+int pc_hip_stream_priority_range(int* least, int* greatest);
+int pc_hip_stream_create_with_priority(pc_stream_t* s, int priority);
 int pc_hip_stream_destroy(pc_stream_t s);
 int pc_hip_stream_sync(pc_stream_t s);
 int pc_hip_stream_wait_event(pc_stream_t s, void* ev);
 int pc_hip_device_sync(void);
 int pc_hip_event_create(void** ev);
+/* cudaEventCreateWithFlags (stream.rs:146): flags 0 (a timing event, Event::timing) or PC_HIP_EVENT_DISABLE_TIMING
+ * (ordering only, Event::new); other bits: hipErrorInvalidValue */
+#define PC_HIP_EVENT_DISABLE_TIMING 2
+int pc_hip_event_create_flags(void** ev, unsigned flags);
 int pc_hip_event_destroy(void* ev);
 int pc_hip_event_record(void* ev, pc_stream_t s);
 int pc_hip_event_sync(void* ev);
@@ -805,6 +833,8 @@ int pc_hip_graph_launch(void* exec, pc_stream_t s);
 int pc_hip_graph_destroy(void* graph);
 int pc_hip_graph_exec_destroy(void* exec);
 const char* pc_hip_error_string(int code);
+/* cudaGetErrorName (crates/pc-cuda/src/error.rs:29-32): the code's symbolic name */
+const char* pc_hip_error_name(int code);
 /* the last launch error of the calling thread (hipGetLastError), 0 if none */
 int pc_hip_last_error(void);
 
@@ -959,7 +989,9 @@ int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* 
 /* pcx_mul_relin_rescale_k over K <= min(k_max, 8) pairs at their own addresses: product j = a[j] b[j] (each a
  * ciphertext at top), out K consecutive ciphertexts; one tensor launch for the K pairs, then the ModUp, key dots (four
  * ciphertexts per launch) and ModDown-rescale of pcx_mul_relin_rescale_k. No counterpart in the reference: independent
- * products of one level (a Chebyshev basis's T_{a+b} = 2 T_a T_b) batched without gathering their operands first. */
+ * products of one level (a Chebyshev basis's T_{a+b} = 2 T_a T_b) batched without gathering their operands first.
+ * Aliasing: out's slot j may be a[j] or b[j] exactly (in place); a slot overlapping any other pair's operand, or
+ * overlapping its own partly, is refused with -1 (the one tensor launch stores every slot while it reads every pair). */
 int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b, int K, int top,
                                void* out, int twice, pc_stream_t s);
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
@@ -975,6 +1007,19 @@ int pcx_modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s);
 const void* pcx_modup_digits(const pcx_ctx* c); /* [dnum][nq + kp][N] */
 int pcx_dot(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* ext, pc_stream_t s);
 int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s);
+
+/* Decryption on the device (crates/pc-gpu/src/decrypt.rs:27-117, Decryptor): c0 + c1 s over the bottom d rows through
+ * the tensor kernel with the key pair (s, 1), then the inverse NTT. pcx_decryptor_new carves its buffers (the key
+ * pairs and k_max outputs of 2 d rows); load_secret takes the secret's evaluation-form rows 0..d-1 from the host
+ * ([nwhich][d][N]: dense, then sparse when nwhich is 2; each word below its prime) and synchronises s;
+ * pcx_decrypt_rows writes the coefficient rows [K][d][N] of K consecutive ciphertexts at top >= d - 1 into out
+ * (device), enqueued on s (the reference's decrypt_rows also downloads them). which: 0 dense, 1 sparse. Returns -1 on
+ * arguments out of range (K > k_max, top < d - 1, a secret not loaded). */
+typedef struct pcx_decryptor pcx_decryptor;
+pcx_decryptor* pcx_decryptor_new(pcx_ctx* c, int d, int k_max, int* err);
+void pcx_decryptor_free(pcx_decryptor* x);
+int pcx_decryptor_load_secret(pcx_decryptor* x, const uint32_t* s_rows, int nwhich, pc_stream_t s);
+int pcx_decrypt_rows(pcx_decryptor* x, const void* ct, int K, int top, int which, void* out, pc_stream_t s);
 
 /* Stage timing, for measurement: while on, the driver records a HIP event pair on the launch stream around each
  * stage it enqueues (0 ModUp INTT, 1 ModUp conversion, 2 ModUp NTT, 3 key dot, 4 ModDown INTT, 5 ModDown conversion,

@@ -24,6 +24,16 @@ _SIGS = {
     "pc_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "pc_hip_set_device": (C.c_int, [C.c_int]),
     "pc_hip_device_name": (C.c_int, [C.c_int, C.c_char_p, C.c_int]),
+    "pc_hip_runtime_version": (C.c_int, [C.POINTER(C.c_int)]),
+    "pc_hip_driver_version": (C.c_int, [C.POINTER(C.c_int)]),
+    "pc_hip_device_attribute": (C.c_int, [C.POINTER(C.c_int), C.c_int, C.c_int]),
+    "pc_hip_mem_get_info": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "pc_hip_profiler_start": (C.c_int, []),
+    "pc_hip_profiler_stop": (C.c_int, []),
+    "pc_hip_stream_priority_range": (C.c_int, [C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "pc_hip_stream_create_with_priority": (C.c_int, [C.POINTER(vp), C.c_int]),
+    "pc_hip_event_create_flags": (C.c_int, [C.POINTER(vp), C.c_uint]),
+    "pc_hip_error_name": (C.c_char_p, [C.c_int]),
     "pc_hip_malloc": (C.c_int, [C.POINTER(vp), C.c_size_t]),
     "pc_hip_free": (C.c_int, [vp]),
     "pc_hip_malloc_host": (C.c_int, [C.POINTER(vp), C.c_size_t]),
@@ -100,6 +110,10 @@ _SIGS = {
     "pcx_timing_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
     "pcx_copy_probe": (C.c_int, [vp, vp, C.c_size_t, vp]),
     "pcx_keys_patch_bytes": (C.c_size_t, [vp]),
+    "pcx_decryptor_new": (vp, [vp, C.c_int, C.c_int, C.POINTER(C.c_int)]),
+    "pcx_decryptor_free": (None, [vp]),
+    "pcx_decryptor_load_secret": (C.c_int, [vp, u32p, C.c_int, vp]),
+    "pcx_decrypt_rows": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(LIB, _name)

@@ -267,6 +267,7 @@ struct pcx_ctx {
     uint32_t *pmod = nullptr, *pinv = nullptr;  // values then Shoup companions, by prime id
     uint32_t* mdt = nullptr;  // ModDown conversion matrix M[j][t] = [P / p_j]_{q_t}, j < kp, t < nq
     int md_fused = 1;         // ModDown conversion inside the NTT column pass (kp <= MDC_MAX_KP)
+    int md_fused_init = 1;    // md_fused as chosen at creation (PCX_MD_FUSED included), restored by table_only(0)
     int table_only = 0;       // every launch through the kernel table (pcx_ctx_table_only)
     int md_ntg = 5;           // its target rows per workgroup
     int32_t* digit_of = nullptr;
@@ -1071,6 +1072,7 @@ pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, i
     if (const char* e = getenv("PCX_NTT_CHUNK")) c->chunk = atoi(e);
     c->md_fused = kp <= pch::MDC_MAX_KP ? 1 : 0;
     if (const char* e = getenv("PCX_MD_FUSED")) c->md_fused = c->md_fused && atoi(e) != 0;
+    c->md_fused_init = c->md_fused;
     if (const char* e = getenv("PCX_MD_NTG")) c->md_ntg = std::max(1, std::min(pch::MDC_MAX_NTG, atoi(e)));
     const int R = c->rows;
     // prime constants and twiddles (crates/pc-gpu/src/context.rs:186-230)
@@ -1166,6 +1168,9 @@ pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, i
         delete c;
         return nullptr;
     }
+    // the no-allocation ladder's scratch address on this device, taken now, outside any capture (a failure here is
+    // retried by that entry point's first call)
+    (void)pch::noalloc_prepare();
     return c;
 }
 
@@ -1228,7 +1233,7 @@ int pcx_ctx_table_only(pcx_ctx* c, int on) {
     if (!c) return -1;
     const int prev = c->table_only;
     c->table_only = on ? 1 : 0;
-    c->md_fused = on ? 0 : (c->kp <= pch::MDC_MAX_KP ? 1 : 0);
+    c->md_fused = on ? 0 : c->md_fused_init;
     return prev;
 }
 size_t pcx_ct_words(const pcx_ctx* c) { return c->ct_words(); }
@@ -1926,10 +1931,20 @@ int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, co
     const uint64_t part = (uint64_t)c->rows * c->n;
     pch::TensorListArgs t;
     memset(&t, 0, sizeof t);
+    // out slot i may be an operand of pair i itself (the tensor reads each word before storing it, in one thread),
+    // but must not overlap any other pair's operands: the launch stores slot i while other workgroups read them
+    const uintptr_t cwb = (uintptr_t)c->ct_words() * sizeof(uint32_t);
     for (int j = 0; j < K; ++j) {
         if (!a[j] || !b[j]) return -1;
         t.a[j] = (const uint32_t*)a[j];
         t.b[j] = (const uint32_t*)b[j];
+        for (int i = 0; i < K; ++i) {
+            const uintptr_t o = (uintptr_t)out + i * cwb;
+            for (const void* x : {a[j], b[j]}) {
+                const uintptr_t xv = (uintptr_t)x;
+                if (xv < o + cwb && o < xv + cwb && !(i == j && xv == o)) return -1;
+            }
+        }
     }
     t.out = (uint32_t*)out;
     t.d2 = c->tmp;
@@ -1989,6 +2004,106 @@ int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out
     m.n = top + 1;
     m.K = 1;
     return c->tab->mul_table(&m, s);
+}
+
+// Decryption on the device (crates/pc-gpu/src/decrypt.rs:27-117 Decryptor): c0 + c1 s over the bottom d rows of each
+// ciphertext through the tensor kernel with the key pair (s, 1) (its middle term x0 c1 + x1 c0; the other two terms
+// land in part 0 and are discarded), then the inverse NTT of those rows. Its own buffers: the key pairs
+// [which][part][d][N] and k_max outputs [c][part][d][N]; the INTT row lists for 1..k_max ciphertexts.
+struct pcx_decryptor {
+    pcx_ctx* c = nullptr;
+    int d = 0, k_max = 0;
+    int loaded[2] = {0, 0};
+    Dev dev;
+    uint32_t *key = nullptr, *out = nullptr;
+    std::vector<Rows> lists;
+};
+
+pcx_decryptor* pcx_decryptor_new(pcx_ctx* c, int d, int k_max, int* err) {
+    auto fail = [&](int e) -> pcx_decryptor* {
+        if (err) *err = e;
+        return nullptr;
+    };
+    if (!c || d < 1 || d > c->nq || k_max < 1) return fail(-1);
+    pcx_decryptor* x = new (std::nothrow) pcx_decryptor;
+    if (!x) return fail(-1);
+    x->c = c;
+    x->d = d;
+    x->k_max = k_max;
+    const size_t n = c->n;
+    x->key = (uint32_t*)x->dev.alloc(4 * d * n * sizeof(uint32_t));
+    x->out = (uint32_t*)x->dev.alloc((size_t)k_max * 2 * d * n * sizeof(uint32_t));
+    x->lists.resize(k_max);
+    for (int k = 1; k <= k_max && !x->dev.err; ++k) {
+        std::vector<uint32_t> ro;
+        std::vector<int32_t> rp;
+        for (int r = 0; r < d; ++r)  // prime-major
+            for (int cc = 0; cc < k; ++cc) {
+                ro.push_back((uint32_t)(cc * 2 * d + d + r));
+                rp.push_back(r);
+            }
+        if (fill_rows(x->dev, x->lists[k - 1], ro, rp, nullptr, nullptr)) break;
+    }
+    if (x->dev.err || !x->key || !x->out) {
+        const int e = x->dev.err ? x->dev.err : -1;
+        delete x;
+        return fail(e);
+    }
+    if (err) *err = 0;
+    return x;
+}
+void pcx_decryptor_free(pcx_decryptor* x) { delete x; }
+
+// The secret's evaluation-form rows 0..d-1 ([nwhich][d][N], host): dense, then sparse when nwhich is 2
+// (decrypt.rs:65-77 load_secret). Synchronises s.
+int pcx_decryptor_load_secret(pcx_decryptor* x, const uint32_t* s_rows, int nwhich, pc_stream_t s) {
+    if (!x || !s_rows || nwhich < 1 || nwhich > 2) return -1;
+    const size_t n = x->c->n, dn = (size_t)x->d * n;
+    std::vector<uint32_t> host(4 * dn, 0);
+    for (int w = 0; w < nwhich; ++w) {
+        for (int r = 0; r < x->d; ++r)
+            for (size_t i = 0; i < n; ++i)
+                if (s_rows[w * dn + r * n + i] >= x->c->primes[r]) return -1;
+        memcpy(&host[w * 2 * dn], s_rows + w * dn, dn * sizeof(uint32_t));
+        std::fill(host.begin() + w * 2 * dn + dn, host.begin() + (w + 1) * 2 * dn, 1u);
+    }
+    hipError_t e = hipMemcpyAsync(x->key, host.data(), host.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                                  (hipStream_t)s);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)s);
+    if (e != hipSuccess) return (int)e;
+    x->loaded[0] = 1;
+    x->loaded[1] = nwhich == 2;
+    return 0;
+}
+
+// Coefficient rows of c0 + c1 s on rows 0..d-1 of K ciphertexts (ct: K consecutive ciphertexts of the context's
+// layout, top >= d - 1) into out [K][d][N] (device), enqueued on s (decrypt.rs:79-117 decrypt_rows, without its
+// download: the caller reads out). which: 0 dense secret, 1 sparse.
+int pcx_decrypt_rows(pcx_decryptor* x, const void* ct, int K, int top, int which, void* out, pc_stream_t s) {
+    if (!x || !ct || !out || K < 1 || K > x->k_max || which < 0 || which > 1 || !x->loaded[which]) return -1;
+    pcx_ctx* c = x->c;
+    if (top < x->d - 1 || top >= c->nq) return -1;
+    const uint64_t n = c->n, dn = (uint64_t)x->d * n, part = (uint64_t)c->rows * n;
+    TensorArgs t;
+    memset(&t, 0, sizeof t);
+    t.out = PolyRef{x->out, 2 * dn, dn};
+    t.d2 = PolyRef{x->out, 2 * dn, 0};  // part 1 of d2 is part 0 of out
+    t.a0 = PolyRef{x->key + which * 2 * dn, 0, dn};
+    t.b0 = PolyRef{const_cast<void*>(ct), 2 * part, part};
+    t.pr = c->pr;
+    t.npairs = 1;
+    t.n = x->d;
+    t.K = K;
+    if (int e = c->tab->tensor(&t, s)) return e;
+    const Rows& r = x->lists[K - 1];
+    NttArgs a = ntt_args(c, x->out, r, r.n);
+    if (int e = c->tab->ntt_inv(&a, s)) return e;
+    for (int cc = 0; cc < K; ++cc) {
+        hipError_t e = hipMemcpyAsync((uint32_t*)out + cc * dn, x->out + cc * 2 * dn + dn, dn * sizeof(uint32_t),
+                                      hipMemcpyDeviceToDevice, (hipStream_t)s);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
 }
 
 }  // extern "C"

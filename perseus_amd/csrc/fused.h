@@ -73,6 +73,9 @@ int ntt_fwd_dense(int logn, const NttArgs* a, pc_stream_t s);
 // the row count from which launches of N = 2^16 take the one-pass transform (0: never); returns the previous one
 int ntt_one_pass_min(int rows);
 
+// noalloc.hip: looks up the no-allocation ladder's scratch address on the current device (0 or the HIP error)
+int noalloc_prepare();
+
 // The tensor of K ciphertext pairs at their own addresses (driver-internal, no counterpart in the reference, whose
 // tensor takes K consecutive ciphertexts): out ciphertext c = (a[c] b[c])'s (d0, d1), part 1 of d2 ciphertext c its
 // d2, doubled when dbl; rows 0..n-1; a[c] / b[c] hold part 0, part 1 `part` words later; out and d2 are K consecutive

@@ -4,7 +4,8 @@
 // ciphertext of 2 parts x 64 rows x 2^16 words) on every device the library runs on, until the process ends.
 //
 // Host code never passes the array's name to a kernel: each device's address comes from hipGetSymbolAddress, taken
-// once per device with that device current, and only that address reaches the launches.
+// once per device with that device current (at context creation, pcx_ctx_new_k), and only that address reaches the
+// launches.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -40,6 +41,16 @@ void* scratch_ptr(int* rc) {
 }
 
 }  // namespace
+
+namespace pch {
+// Called by pcx_ctx_new_k with the context's device current: the address is looked up at set-up, outside any stream
+// capture a caller may later run the entry point under (a first lookup can load the code object, which a capture may
+// refuse). Returns 0 or the lookup's error; the entry point retries a failed lookup on its first call.
+int noalloc_prepare() {
+    int rc = 0;
+    return scratch_ptr(&rc) ? 0 : rc;
+}
+}  // namespace pch
 
 extern "C" int pcx_rotate_and_sum_noalloc(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start,
                                           int64_t stop, int radix_bits, void* out, pc_stream_t s) {

@@ -1,6 +1,7 @@
 // The HIP runtime FFI: the MI355X replacement of crates/pc-cuda's hand-written cudart bindings (ffi.rs:18-50,
 // mem.rs:19-24). Thin wrappers so a C / Rust / Python caller needs no HIP headers; each returns 0 or the HIP error.
 #include <hip/hip_runtime.h>
+#include <rocprofiler-sdk-roctx/roctx.h>
 #include <string.h>
 
 #include "pc_hip.h"
@@ -21,6 +22,62 @@ int pc_hip_device_name(int dev, char* out, int len) {
     if (e != hipSuccess) return rc(e);
     strncpy(out, p.gcnArchName, len > 0 ? (size_t)len - 1 : 0);
     if (len > 0) out[len - 1] = 0;
+    return 0;
+}
+// cudaRuntimeGetVersion / cudaDriverGetVersion (crates/pc-cuda/src/device.rs:83-84): HIP's own version numbers
+int pc_hip_runtime_version(int* v) { return rc(hipRuntimeGetVersion(v)); }
+int pc_hip_driver_version(int* v) { return rc(hipDriverGetVersion(v)); }
+// cudaDeviceGetAttribute (device.rs:115, :126) for the attribute numbers the reference passes, plus the gfx code
+int pc_hip_device_attribute(int* v, int attr, int dev) {
+    if (!v) return (int)hipErrorInvalidValue;
+    switch (attr) {
+    case PC_HIP_ATTR_CU_COUNT:
+        return rc(hipDeviceGetAttribute(v, hipDeviceAttributeMultiprocessorCount, dev));
+    case PC_HIP_ATTR_CC_MAJOR:
+        return rc(hipDeviceGetAttribute(v, hipDeviceAttributeComputeCapabilityMajor, dev));
+    case PC_HIP_ATTR_CC_MINOR:
+        return rc(hipDeviceGetAttribute(v, hipDeviceAttributeComputeCapabilityMinor, dev));
+    case PC_HIP_ATTR_CLUSTERS: {
+        // CDNA has no thread-block clusters: 0 for every valid device
+        int cus = 0;
+        if (int e = rc(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev))) return e;
+        *v = 0;
+        return 0;
+    }
+    case PC_HIP_ATTR_GFX_ARCH: {
+        // "gfx950" -> 0x950: the hexadecimal digits after "gfx", up to the first ':'
+        hipDeviceProp_t p;
+        hipError_t e = hipGetDeviceProperties(&p, dev);
+        if (e != hipSuccess) return rc(e);
+        const char* a = p.gcnArchName;
+        if (strncmp(a, "gfx", 3) != 0) return (int)hipErrorInvalidValue;
+        int code = 0;
+        for (a += 3; *a && *a != ':'; ++a) {
+            const char ch = *a;
+            const int d = ch >= '0' && ch <= '9' ? ch - '0' : ch >= 'a' && ch <= 'f' ? ch - 'a' + 10 : -1;
+            if (d < 0) return (int)hipErrorInvalidValue;
+            code = code * 16 + d;
+        }
+        *v = code;
+        return 0;
+    }
+    default:
+        return (int)hipErrorInvalidValue;
+    }
+}
+// cudaMemGetInfo (device.rs:137, :188): free and total bytes of the current device
+int pc_hip_mem_get_info(size_t* free_bytes, size_t* total_bytes) { return rc(hipMemGetInfo(free_bytes, total_bytes)); }
+// cudaProfilerStart / cudaProfilerStop (device.rs:151-158): the device is synchronised first, as the reference does,
+// then a running rocprofv3 is asked to resume or pause collection (its --selected-regions mode). With no profiling
+// tool attached the request is a no-op, as cudaProfilerStart is without a profiler.
+int pc_hip_profiler_start(void) {
+    if (int e = rc(hipDeviceSynchronize())) return e;
+    (void)roctxProfilerResume(0);
+    return 0;
+}
+int pc_hip_profiler_stop(void) {
+    if (int e = rc(hipDeviceSynchronize())) return e;
+    (void)roctxProfilerPause(0);
     return 0;
 }
 int pc_hip_malloc(void** p, size_t bytes) { return rc(hipMalloc(p, bytes)); }
@@ -45,6 +102,19 @@ int pc_hip_stream_create(pc_stream_t* s) {
     *s = (pc_stream_t)h;
     return rc(e);
 }
+// cudaDeviceGetStreamPriorityRange / cudaStreamCreateWithPriority (stream.rs:33-44, Stream::high_priority). Every
+// stream of this library runs at the default priority: streams of different priorities sharing an MI355X have been
+// seen to stop making progress. The range reads (0, 0), and the priority argument is accepted and not applied.
+int pc_hip_stream_priority_range(int* least, int* greatest) {
+    if (!least || !greatest) return (int)hipErrorInvalidValue;
+    *least = 0;
+    *greatest = 0;
+    return 0;
+}
+int pc_hip_stream_create_with_priority(pc_stream_t* s, int priority) {
+    (void)priority;
+    return pc_hip_stream_create(s);
+}
 int pc_hip_stream_destroy(pc_stream_t s) { return rc(hipStreamDestroy(S(s))); }
 int pc_hip_stream_sync(pc_stream_t s) { return rc(hipStreamSynchronize(S(s))); }
 int pc_hip_stream_wait_event(pc_stream_t s, void* ev) { return rc(hipStreamWaitEvent(S(s), (hipEvent_t)ev, 0)); }
@@ -52,6 +122,15 @@ int pc_hip_device_sync(void) { return rc(hipDeviceSynchronize()); }
 int pc_hip_event_create(void** ev) {
     hipEvent_t e;
     hipError_t r = hipEventCreate(&e);
+    *ev = (void*)e;
+    return rc(r);
+}
+// cudaEventCreateWithFlags (stream.rs:146): PC_HIP_EVENT_DISABLE_TIMING (2, the value of both runtimes' flag) makes
+// an ordering-only event (Event::new); 0 a timing event (Event::timing)
+int pc_hip_event_create_flags(void** ev, unsigned flags) {
+    if (!ev || (flags & ~(unsigned)PC_HIP_EVENT_DISABLE_TIMING)) return (int)hipErrorInvalidValue;
+    hipEvent_t e;
+    hipError_t r = hipEventCreateWithFlags(&e, flags ? hipEventDisableTiming : hipEventDefault);
     *ev = (void*)e;
     return rc(r);
 }
@@ -82,6 +161,12 @@ const char* pc_hip_error_string(int code) {
     if (code == -2) return "launch argument outside the kernel's range (-2)";
     if (code == -3) return "launch mode not supported by this kernel (-3)";
     return hipGetErrorString((hipError_t)code);
+}
+// cudaGetErrorName (crates/pc-cuda/src/error.rs:29-32)
+const char* pc_hip_error_name(int code) {
+    if (code == -1 || code == -2) return "PC_LAUNCH_ARGS";
+    if (code == -3) return "PC_LAUNCH_MODE";
+    return hipGetErrorName((hipError_t)code);
 }
 int pc_hip_last_error(void) { return rc(hipGetLastError()); }
 }

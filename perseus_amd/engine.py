@@ -376,3 +376,34 @@ class Rows:
         if getattr(self, "h", None):
             LIB.pcx_rows_free(self.h)
             self.h = None
+
+
+class Decryptor:
+    """Decryption on the device (pcx_decryptor, crates/pc-gpu/src/decrypt.rs): c0 + c1 s over the bottom d rows of
+    each ciphertext, then the inverse NTT; coefficient rows out."""
+
+    def __init__(self, ctx, d, k_max=1):
+        self.ctx, self.d, self.k_max = ctx, int(d), int(k_max)
+        err = C.c_int(0)
+        self.h = LIB.pcx_decryptor_new(ctx.h, self.d, self.k_max, C.byref(err))
+        if not self.h:
+            raise HipError(f"pcx_decryptor_new: {err.value}")
+        self.out = DevBuf(self.k_max * self.d * ctx.chain.n)
+
+    def load_secret(self, s_rows, stream):
+        """s_rows: the secret's evaluation-form rows [nwhich][d][N] (dense, then sparse)."""
+        s = np.ascontiguousarray(s_rows, np.uint32)
+        s = s.reshape(-1, self.d, self.ctx.chain.n)
+        check(LIB.pcx_decryptor_load_secret(self.h, s.ctypes.data_as(C.POINTER(C.c_uint32)), s.shape[0],
+                                            stream.h), "decryptor_load_secret")
+
+    def decrypt_rows(self, ct, top, stream, K=1, which=0):
+        """[K][d][N] coefficient rows of K consecutive ciphertexts at top (synchronises stream)."""
+        check(LIB.pcx_decrypt_rows(self.h, ct.addr(), K, top, which, self.out.ptr, stream.h), "decrypt_rows")
+        stream.sync()
+        return self.out.download((K, self.d, self.ctx.chain.n), stream=stream, words=K * self.d * self.ctx.chain.n)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pcx_decryptor_free(self.h)
+            self.h = None

@@ -199,6 +199,24 @@ def test_product_list(stream, name, top, K, twice):
         assert (got[j][:, : top - 1] == want[j][:, : top - 1]).all(), f"product {j} ({ia[j]} x {ib[j]})"
     with pytest.raises(pa.HipError):
         ctxk.mul_relin_rescale_list(keysk, views([0] * 7), views([1] * 7), top, ctxk.ct_buf(7), stream)
+    # aliasing: slot j in place over pair j's own operand is allowed (the words of the out-of-place call) ...
+    inplace = pa.DevBuf.from_array(pool[:2])
+    both = [B.View(inplace, j * ctxk.ct_words) for j in range(2)]
+    ctxk.mul_relin_rescale_list(keysk, both, views(ib[:2]), top, both[0], stream, twice=twice)
+    stream.sync()
+    got = inplace.download((2, 2, ch.rows, ch.n))
+    out2 = ctxk.ct_buf(2)
+    ctxk.mul_relin_rescale_list(keysk, views([0, 1]), views(ib[:2]), top, out2, stream, twice=twice)
+    stream.sync()
+    want2 = out2.download((2, 2, ch.rows, ch.n))
+    for j in range(2):
+        assert (got[j][:, : top - 1] == want2[j][:, : top - 1]).all(), f"in place, product {j}"
+    # ... a slot over another pair's operand is refused, before anything is launched
+    shifted = pa.DevBuf.from_array(pool[:3])
+    tri = [B.View(shifted, j * ctxk.ct_words) for j in range(3)]
+    with pytest.raises(pa.HipError):
+        ctxk.mul_relin_rescale_list(keysk, tri[1:], tri[1:], top, tri[0], stream)
+    assert (shifted.download((3, 2, ch.rows, ch.n)) == pool[:3]).all()
 
 
 @pytest.mark.parametrize("name,top,alias", [("small", 5, False), ("small31", 4, True), ("c3", 29, True),

@@ -65,3 +65,63 @@ def test_memset_in_a_captured_graph():
         wb = np.arange(n, dtype=np.uint32)
         wb[2:5] = 0
         assert (b.download() == wb).all(), rep
+
+
+def test_device_queries_of_device_open():
+    """What crates/pc-cuda/src/device.rs:63-158 (Device::open, sm_count, clusters, mem_info, profiler) reads."""
+    say("[runtime] versions, attributes, memory info, profiler range, priority range")
+    rt, dr = C.c_int(0), C.c_int(0)
+    assert LIB.pc_hip_runtime_version(C.byref(rt)) == 0 and rt.value > 0
+    assert LIB.pc_hip_driver_version(C.byref(dr)) == 0 and dr.value > 0
+    v = C.c_int(-1)
+    assert LIB.pc_hip_device_attribute(C.byref(v), 16, 0) == 0
+    assert v.value == 256, v.value  # MI355X: 256 compute units
+    assert LIB.pc_hip_device_attribute(C.byref(v), 75, 0) == 0 and v.value == 9
+    assert LIB.pc_hip_device_attribute(C.byref(v), 76, 0) == 0 and v.value == 5
+    assert LIB.pc_hip_device_attribute(C.byref(v), 0x10000, 0) == 0 and v.value == 0
+    assert LIB.pc_hip_device_attribute(C.byref(v), 0x10001, 0) == 0 and v.value == 0x950
+    assert LIB.pc_hip_device_attribute(C.byref(v), 12345, 0) != 0
+    assert LIB.pc_hip_device_attribute(C.byref(v), 16, 99) != 0  # no such device
+    free, total = C.c_size_t(0), C.c_size_t(0)
+    assert LIB.pc_hip_mem_get_info(C.byref(free), C.byref(total)) == 0
+    assert 0 < free.value <= total.value and total.value > (250 << 30)  # 288 GB of HBM3E
+    buf = pa.DevBuf(1 << 28)  # 1 GiB: free memory drops by about that much
+    free2 = C.c_size_t(0)
+    assert LIB.pc_hip_mem_get_info(C.byref(free2), C.byref(total)) == 0
+    assert free.value - free2.value >= (1 << 30) - (64 << 20), (free.value, free2.value)
+    del buf
+    assert LIB.pc_hip_profiler_start() == 0 and LIB.pc_hip_profiler_stop() == 0
+    lo, hi = C.c_int(-7), C.c_int(-7)
+    assert LIB.pc_hip_stream_priority_range(C.byref(lo), C.byref(hi)) == 0 and (lo.value, hi.value) == (0, 0)
+    assert LIB.pc_hip_error_name(1) and LIB.pc_hip_error_name(-1) == b"PC_LAUNCH_ARGS"
+
+
+def test_events_with_flags_and_a_priority_stream():
+    """Event::new (ordering only: no elapsed time) and Event::timing (crates/pc-cuda/src/stream.rs:133-147) on a
+    stream made by Stream::high_priority's call, ordering a copy between two streams."""
+    say("[runtime] event flags: ordering-only and timing events across two streams")
+    s1, s2 = C.c_void_p(), C.c_void_p()
+    assert LIB.pc_hip_stream_create_with_priority(C.byref(s1), -1) == 0
+    assert LIB.pc_hip_stream_create(C.byref(s2)) == 0
+    ev_order, t0, t1 = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    assert LIB.pc_hip_event_create_flags(C.byref(ev_order), 2) == 0
+    assert LIB.pc_hip_event_create_flags(C.byref(t0), 0) == 0
+    assert LIB.pc_hip_event_create_flags(C.byref(t1), 0) == 0
+    assert LIB.pc_hip_event_create_flags(C.byref(C.c_void_p()), 4) != 0  # unknown flag bits
+    n = 1 << 22
+    src = pa.DevBuf.from_array(np.arange(n, dtype=np.uint32))
+    mid, dst = pa.DevBuf(n), pa.DevBuf(n)
+    assert LIB.pc_hip_event_record(t0, s1) == 0
+    assert LIB.pc_hip_memcpy_dtod(mid.ptr, src.ptr, 4 * n, s1) == 0
+    assert LIB.pc_hip_event_record(ev_order, s1) == 0
+    assert LIB.pc_hip_event_record(t1, s1) == 0
+    assert LIB.pc_hip_stream_wait_event(s2, ev_order) == 0
+    assert LIB.pc_hip_memcpy_dtod(dst.ptr, mid.ptr, 4 * n, s2) == 0
+    assert LIB.pc_hip_stream_sync(s2) == 0 and LIB.pc_hip_event_sync(t1) == 0
+    assert (dst.download() == np.arange(n, dtype=np.uint32)).all()
+    ms = C.c_float(-1)
+    assert LIB.pc_hip_event_elapsed_ms(C.byref(ms), t0, t1) == 0 and ms.value >= 0
+    for e in (ev_order, t0, t1):
+        assert LIB.pc_hip_event_destroy(e) == 0
+    for s in (s1, s2):
+        assert LIB.pc_hip_stream_destroy(s) == 0

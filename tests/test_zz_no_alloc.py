@@ -73,3 +73,37 @@ def test_noalloc_ladder_equals_the_ladder():
     say("[noalloc] a rung of 9 bits is refused (-2), before any GPU work")
     x = ctxs.ct_buf()
     assert LIB.pcx_rotate_and_sum_noalloc(ctxs.h, keys_s.h, x.addr(), 5, 1, 1 << 10, 9, x.addr(), st.h) == -2
+
+
+def test_noalloc_ladder_in_a_captured_graph():
+    """The entry point under stream capture (its scratch address taken at context creation): the ladder captured into
+    one HIP graph, replayed three times with a new input uploaded and eager work between the replays; every replay
+    equals pcx_rotate_and_sum run eagerly on the same input."""
+    assert pa.device_count() >= 1, "no GPU visible"
+    st = pa.Stream()
+    ch = pa.preset("small")
+    ctx = pa.Context(ch, k_rot=4)
+    keys = keys_for(ch, ctx, [1, 2, 3, 4, 8, 12], 73)
+    top = 5
+    x, got_buf = ctx.ct_buf(), ctx.ct_buf()
+    say("[noalloc] small ring top 5: the ladder (1..16, radix 4) captured into a graph")
+
+    def work():
+        assert LIB.pcx_rotate_and_sum_noalloc(ctx.h, keys.h, x.addr(), top, 1, 16, 2, got_buf.addr(), st.h) == 0
+
+    x.upload(random_ct(ch, top, 90), st)
+    g = pa.Graph(st, work)
+    want_buf, tmp = ctx.ct_buf(), ctx.ct_buf()
+    for rep in range(3):
+        say(f"[noalloc] graph replay {rep}")
+        ct = random_ct(ch, top, 91 + rep)
+        x.upload(ct, st)
+        got_buf.zero()
+        g.launch(st)
+        st.sync()
+        got = got_buf.download((2, ch.rows, ch.n))
+        assert LIB.pcx_rotate_and_sum(ctx.h, keys.h, x.addr(), top, 1, 16, 2, want_buf.addr(), tmp.addr(),
+                                      st.h) == 0
+        st.sync()
+        want = want_buf.download((2, ch.rows, ch.n))
+        assert (got[:, : top + 1] == want[:, : top + 1]).all(), rep

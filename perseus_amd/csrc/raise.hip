@@ -7,9 +7,9 @@
 // All in coefficient form, u32 words, source primes below 2^31.
 //
 // mod_raise streams 4 consecutive coefficients per thread over one target row per workgroup row (the d source rows
-// stay in L2 across the target rows). small_int and small_int1 give one coefficient per thread: its multi-word
-// integer lives in registers (fixed trip counts over the table's maxima), and every source word of a coefficient is
-// read before its first output word is written, so the outputs may overwrite the sources.
+// stay in L2 across the target rows). small_int gives one coefficient per thread, its multi-word integer in registers
+// (fixed trip counts over the table's maxima); small_int1 four. Every source word of a coefficient is read before its
+// first output word is written, by the same thread, so the outputs may overwrite the sources.
 #include "common.h"
 
 namespace pch {
@@ -46,150 +46,222 @@ __global__ void __launch_bounds__(BX) mod_raise_k(ModRaiseArgs A, int logn) {
 }
 
 // ------------------------------------------------------------------------------------------------ small_int
+// CRT by the sum form with a floating-point quotient, not mixed radix: X = S - u Q with S = sum_a y_a M_a,
+// M_a = Q / q_a, y_a = [x_a (M_a^-1 mod q_a)]_{q_a} and u = floor(S / Q) = floor(sum_a y_a / q_a). The quotient is
+// estimated in double (its error stays below 2^-48, so the estimate is u or u +- 1) and fixed with one exact multi-word
+// comparison. The per-prime constants are derived in LDS at the start of each workgroup from the table's primes and
+// Q_k alone (M_a by long division of Q_k, the inverse by Fermat), so the table's Garner constants (qinv) and its
+// powers of 2^32 (pow32) are not read: the outputs are reduced by Horner's rule in 2^32 with the prime's own
+// (2^32 mod p) Shoup pair from PrimeConst.
+struct SiConst {
+    uint32_t q[PC_SI_MAXK], qm[PC_SI_MAXK], c[PC_SI_MAXK], cs[PC_SI_MAXK];
+    uint32_t M[PC_SI_MAXK][PC_SI_MAXW];
+    double inv[PC_SI_MAXK];
+};
+
+__device__ uint32_t powmod32(uint32_t b, uint32_t e, uint32_t q) {
+    uint64_t r = 1, x = b % q;
+    for (; e; e >>= 1) {
+        if (e & 1) r = r * x % q;
+        x = x * x % q;
+    }
+    return (uint32_t)r;
+}
+
+// lane a < k: M_a = Q_k / q_a (exact long division from the top word), M_a^-1 mod q_a, 1 / q_a
+__device__ void si_prologue(const SmallIntTab& T, int k, int nw, SiConst& L) {
+    const int a = threadIdx.x;
+    if (a >= k) return;
+    const uint32_t q = T.q[a];
+    uint64_t rem = 0;
+    for (int w = PC_SI_MAXW - 1; w >= 0; --w) {
+        const uint64_t cur = (rem << 32) | (w < nw ? T.Qk[w] : 0u);
+        L.M[a][w] = (uint32_t)(cur / q);
+        rem = cur % q;
+    }
+    uint64_t mr = 0;  // M_a mod q_a
+    for (int w = PC_SI_MAXW - 1; w >= 0; --w) mr = ((mr << 32) | L.M[a][w]) % q;
+    const uint32_t c = powmod32((uint32_t)mr, q - 2, q);
+    L.q[a] = q;
+    L.qm[a] = m32(q);
+    L.c[a] = c;
+    L.cs[a] = (uint32_t)(((uint64_t)c << 32) / q);
+    L.inv[a] = 1.0 / (double)q;
+}
+
+// a 96-bit column accumulator of 64-bit products
+struct Col {
+    uint64_t lo = 0;
+    uint32_t hi = 0;
+    __device__ __forceinline__ void add(uint64_t v) {
+        lo += v;
+        hi += lo < v;
+    }
+    __device__ __forceinline__ uint32_t take() {  // the low word out, the rest shifted down
+        const uint32_t w = (uint32_t)lo;
+        lo = (lo >> 32) | ((uint64_t)hi << 32);
+        hi = 0;
+        return w;
+    }
+};
+
 __global__ void __launch_bounds__(BX) small_int_k(SmallIntArgs A, int logn) {
     const SmallIntTab& T = *A.tab;
-    __shared__ uint32_t sq[PC_SI_MAXK], sm[PC_SI_MAXK], sw[PC_SI_MAXK][PC_SI_MAXK], sws[PC_SI_MAXK][PC_SI_MAXK];
-    const int k = T.k < PC_SI_MAXK ? T.k : PC_SI_MAXK;
-    const int nw = T.nw < PC_SI_MAXW ? T.nw : PC_SI_MAXW;
-    const int nr = T.nr < PC_SI_MAXR ? T.nr : PC_SI_MAXR;
-    const int nout = T.nout < PC_SI_MAXOUT ? T.nout : PC_SI_MAXOUT;
-    if (threadIdx.x < PC_SI_MAXK * PC_SI_MAXK) {
-        // the Garner constants q_j^-1 mod q_i with their Shoup companions, once per workgroup
-        const int a = threadIdx.x / PC_SI_MAXK, b = threadIdx.x % PC_SI_MAXK;
-        if (a < k) {
-            const uint32_t q = T.q[a];
-            if (b == 0) {
-                sq[a] = q;
-                sm[a] = m32(q);
-            }
-            if (b < a) {
-                const uint32_t w = T.qinv[a][b];
-                sw[a][b] = w;
-                sws[a][b] = (uint32_t)(((uint64_t)w << 32) / q);
-            }
-        }
-    }
+    const int k = min(T.k, PC_SI_MAXK), nw = min(T.nw, PC_SI_MAXW), nr = min(T.nr, PC_SI_MAXR);
+    const int nout = min(T.nout, PC_SI_MAXOUT);
+    __shared__ SiConst L;
+    si_prologue(T, k, nw, L);
     __syncthreads();
     const int part = blockIdx.y, c = blockIdx.z;
-    const uint32_t idx = blockIdx.x * BX + threadIdx.x;
-    const uint32_t* src = (const uint32_t*)A.src + c * A.src_ct_stride + part * A.src_part_stride;
-    // Garner digits: X = v0 + v1 q0 + v2 q0 q1 + v3 q0 q1 q2
-    uint32_t v[PC_SI_MAXK];
+    const size_t idx = (size_t)blockIdx.x * BX + threadIdx.x;
+    const uint32_t* src = (const uint32_t*)A.src + c * A.src_ct_stride + part * A.src_part_stride + idx;
+    // y_a and the quotient estimate; every source word is read here, before any output is written
+    uint32_t y[PC_SI_MAXK];
+    double f = 0.0;
 #pragma unroll
     for (int a = 0; a < PC_SI_MAXK; ++a) {
-        v[a] = 0;
+        y[a] = 0;
         if (a < k) {
-            const uint32_t q = sq[a], m = sm[a];
-            uint32_t d = red32(src[((size_t)a << logn) + idx], q, m);
-#pragma unroll
-            for (int b = 0; b < a; ++b) d = shoup(subm(d, red32(v[b], q, m), q), sw[a][b], sws[a][b], q);
-            v[a] = d;
+            y[a] = shoup(red32(src[(size_t)a << logn], L.q[a], L.qm[a]), L.c[a], L.cs[a], L.q[a]);
+            f += (double)y[a] * L.inv[a];
         }
     }
-    // the digits to 32-bit words, Horner from the top digit
+    // S = sum_a y_a M_a, column by column
     uint32_t x[XW];
+    {
+        Col acc;
 #pragma unroll
-    for (int w = 0; w < XW; ++w) x[w] = 0;
+        for (int w = 0; w < PC_SI_MAXW; ++w) {
 #pragma unroll
-    for (int a = PC_SI_MAXK - 1; a >= 0; --a) {
-        if (a < k) {
-            const uint32_t q = a == k - 1 ? 0u : sq[a];
-            uint64_t carry = v[a];
+            for (int a = 0; a < PC_SI_MAXK; ++a) acc.add((uint64_t)y[a] * L.M[a][w]);
+            x[w] = acc.take();
+        }
 #pragma unroll
-            for (int w = 0; w < PC_SI_MAXK + 1; ++w) {
-                const uint64_t s = (uint64_t)x[w] * q + carry;
-                x[w] = (uint32_t)s;
-                carry = s >> 32;
+        for (int w = PC_SI_MAXW; w < XW; ++w) x[w] = 0;
+    }
+    // X = S - u Q, then the one correction: + Q when negative, - Q when >= Q
+    {
+        const uint32_t u = (uint32_t)f;
+        int64_t carry = 0;
+#pragma unroll
+        for (int w = 0; w < PC_SI_MAXW; ++w) {
+            const int64_t d = (int64_t)x[w] - (int64_t)((uint64_t)u * T.Qk[w]) + carry;
+            x[w] = (uint32_t)d;
+            carry = d >> 32;
+        }
+        if (carry < 0) {
+            uint64_t cy = 0;
+#pragma unroll
+            for (int w = 0; w < PC_SI_MAXW; ++w) {
+                cy += (uint64_t)x[w] + T.Qk[w];
+                x[w] = (uint32_t)cy;
+                cy >>= 32;
+            }
+        } else {
+            bool ge = true;  // X >= Q, decided from the top word down
+            bool tie = true;
+#pragma unroll
+            for (int w = PC_SI_MAXW - 1; w >= 0; --w)
+                if (tie && x[w] != T.Qk[w]) {
+                    ge = x[w] > T.Qk[w];
+                    tie = false;
+                }
+            if (ge) {
+                int64_t b = 0;
+#pragma unroll
+                for (int w = 0; w < PC_SI_MAXW; ++w) {
+                    const int64_t d = (int64_t)x[w] - T.Qk[w] + b;
+                    x[w] = (uint32_t)d;
+                    b = d >> 32;
+                }
             }
         }
     }
-    // centre: X > Q_k / 2 -> the magnitude Q_k - X, negative
-    int cmp = 0;
+    // the centred lift: X > floor(Q / 2) stands for X - Q, kept as its magnitude and a sign
+    bool neg = false;
+    {
+        bool tie = true;
 #pragma unroll
-    for (int w = PC_SI_MAXW - 1; w >= 0; --w)
-        if (w < nw && cmp == 0 && x[w] != T.Qkh[w]) cmp = x[w] > T.Qkh[w] ? 1 : -1;
-    const bool neg = cmp > 0;
-    if (neg) {
-        uint32_t borrow = 0;
+        for (int w = PC_SI_MAXW - 1; w >= 0; --w)
+            if (tie && x[w] != T.Qkh[w]) {
+                neg = x[w] > T.Qkh[w];
+                tie = false;
+            }
+        if (neg) {
+            int64_t b = 0;
 #pragma unroll
-        for (int w = 0; w < PC_SI_MAXW; ++w) {
-            const uint64_t s = (uint64_t)(w < nw ? T.Qk[w] : 0u) - x[w] - borrow;
-            x[w] = (uint32_t)s;
-            borrow = (uint32_t)(s >> 63);
+            for (int w = 0; w < PC_SI_MAXW; ++w) {
+                const int64_t d = (int64_t)T.Qk[w] - x[w] + b;
+                x[w] = (uint32_t)d;
+                b = d >> 32;
+            }
         }
     }
     int nq = nw;
     if (T.divide) {
-        // floor((|X| R + 2^191) / 2^192): the product, the half, the top words
-        uint32_t pr[XW];
-#pragma unroll
-        for (int w = 0; w < XW; ++w) pr[w] = 0;
-#pragma unroll
-        for (int a = 0; a < PC_SI_MAXW; ++a) {
-            uint64_t carry = 0;
-#pragma unroll
-            for (int b = 0; b < PC_SI_MAXR; ++b) {
-                const uint64_t s = (uint64_t)x[a] * (b < nr ? T.R[b] : 0u) + pr[a + b] + carry;
-                pr[a + b] = (uint32_t)s;
-                carry = s >> 32;
-            }
-#pragma unroll
-            for (int b = a + PC_SI_MAXR; b < XW; ++b) {
-                const uint64_t s = (uint64_t)pr[b] + carry;
-                pr[b] = (uint32_t)s;
-                carry = s >> 32;
-            }
-        }
-        uint64_t carry = 1ull << 31;  // 2^191 = 2^31 in word 5
-#pragma unroll
-        for (int w = 5; w < XW; ++w) {
-            const uint64_t s = (uint64_t)pr[w] + carry;
-            pr[w] = (uint32_t)s;
-            carry = s >> 32;
-        }
+        // floor((|X| R + 2^191) / 2^192) by product scanning: column j sums x_a R_(j-a); 2^191 joins column 5 and
+        // columns from 6 on are the quotient's words
         constexpr int DW = PC_SI_SHIFT / 32;
-        nq = nw + nr - DW;
-        nq = nq < 1 ? 1 : nq;
+        uint32_t qw[XW];
+        Col acc;
 #pragma unroll
-        for (int w = 0; w < XW; ++w) x[w] = (w < nq && w + DW < XW) ? pr[w + DW] : 0u;
+        for (int j = 0; j < XW; ++j) {
+#pragma unroll
+            for (int a = 0; a < PC_SI_MAXW; ++a)
+                if (j - a >= 0 && j - a < PC_SI_MAXR) acc.add((uint64_t)x[a] * T.R[j - a]);
+            if (j == DW - 1) acc.add(1ull << 31);
+            const uint32_t w = acc.take();
+            if (j >= DW) qw[j - DW] = w;
+        }
+#pragma unroll
+        for (int j = XW - DW; j < XW; ++j) qw[j] = 0;
+        nq = max(1, nw + nr - DW);
+#pragma unroll
+        for (int w = 0; w < XW; ++w) x[w] = w < nq ? qw[w] : 0u;
     }
-    uint32_t* out = (uint32_t*)A.out + c * A.ct_stride + part * A.part_stride;
+    // sign(X) q mod p for every output row: Horner in 2^32 from the top word
+    uint32_t* out = (uint32_t*)A.out + c * A.ct_stride + part * A.part_stride + idx;
     for (int o = 0; o < nout; ++o) {
         const int row = T.orow[o];
         const Red r(A.pr[row]);
-        uint64_t lo = 0;
-        uint32_t hi = 0;
+        uint32_t h = 0;
 #pragma unroll
-        for (int w = 0; w < XW; ++w) {
-            if (w < nq) {
-                const uint64_t s = (uint64_t)x[w] * T.pow32[o][w];
-                lo += s;
-                hi += lo < s;
-            }
-        }
-        uint32_t y = r.red96(lo, hi);
-        if (neg && y) y = r.p - y;
-        out[((size_t)row << logn) + idx] = y;
+        for (int w = XW - 1; w >= 0; --w)
+            if (w < nq) h = r(((uint64_t)h << 32) | x[w]);
+        out[(size_t)row << logn] = neg && h ? r.p - h : h;
     }
 }
 
 // ------------------------------------------------------------------------------------------------ small_int1
+// Four coefficients per thread with 16-byte accesses: row 0 is read whole first (the outputs overwrite it), each
+// magnitude scaled to q = floor((|x| mc + 2^(sh-1)) / 2^sh) in 128-bit arithmetic, then every output row is written
+// four words at a time with the sign restored.
 __global__ void __launch_bounds__(BX) small_int1_k(SmallInt1Args A, int logn) {
     const int part = blockIdx.y, c = blockIdx.z;
-    const uint32_t idx = blockIdx.x * BX + threadIdx.x;
-    uint32_t* x = (uint32_t*)A.x + c * A.ct_stride + part * A.part_stride;
-    const uint32_t q0 = (uint32_t)A.pr[0].p;
-    const uint32_t v = x[idx];
-    const bool neg = v > (q0 >> 1);
-    const uint32_t mag = neg ? q0 - v : v;
-    // |x| mc + 2^(sh - 1) as a 128-bit integer, shifted down by sh
-    unsigned __int128 s = (unsigned __int128)mag * A.mc + ((unsigned __int128)1 << (A.sh - 1));
-    const uint64_t q = (uint64_t)(s >> A.sh);
+    const size_t idx = ((size_t)blockIdx.x * BX + threadIdx.x) * 4;
+    uint32_t* x = (uint32_t*)A.x + c * A.ct_stride + part * A.part_stride + idx;
+    const uint32_t q0 = (uint32_t)A.pr[0].p, half = q0 >> 1;
+    const uint4 v4 = *(const uint4*)x;
+    const uint32_t v[4] = {v4.x, v4.y, v4.z, v4.w};
+    const unsigned __int128 rnd = (unsigned __int128)1 << (A.sh - 1);
+    uint64_t q[4];
+    uint32_t neg = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool n = v[j] > half;
+        neg |= (uint32_t)n << j;
+        const uint32_t mag = n ? q0 - v[j] : v[j];
+        q[j] = (uint64_t)(((unsigned __int128)mag * A.mc + rnd) >> A.sh);
+    }
     for (int t = 0; t < A.nrows; ++t) {
         const Red r(A.pr[t]);
-        uint32_t y = r(q);
-        if (neg && y) y = r.p - y;
-        x[((size_t)t << logn) + idx] = y;
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t h = r(q[j]);
+            o[j] = (neg >> j & 1) && h ? r.p - h : h;
+        }
+        *(uint4*)(x + ((size_t)t << logn)) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -217,7 +289,8 @@ int small_int1(const SmallInt1Args* a, pc_stream_t s) {
     if (!a || a->sh < 1 || a->sh > 127 || a->nrows < 1 || a->nrows > 64 || a->K < 1 || a->nparts < 1 || a->nparts > 2)
         return -1;
     if (!a->x || !a->pr) return -1;
-    hipLaunchKernelGGL(small_int1_k, dim3((1u << LOGN) / BX, a->nparts, a->K), dim3(BX), 0, (hipStream_t)s, *a, LOGN);
+    hipLaunchKernelGGL(small_int1_k, dim3((1u << LOGN) / (BX * 4), a->nparts, a->K), dim3(BX), 0, (hipStream_t)s, *a,
+                       LOGN);
     return launch_rc();
 }
 

@@ -6,7 +6,13 @@
 
 #include "pc_hip.h"
 
-static inline int rc(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
+// A failed call's error is returned here and then cleared from the thread's last-error slot, so that the next kernel
+// launch's check (hipGetLastError after the launch) does not report it a second time as its own.
+static inline int rc(hipError_t e) {
+    if (e == hipSuccess) return 0;
+    (void)hipGetLastError();
+    return (int)e;
+}
 
 namespace pch {
 int fill_bytes(void* dst, int value, size_t bytes, pc_stream_t s);  // elem.hip: a fill kernel
@@ -168,5 +174,8 @@ const char* pc_hip_error_name(int code) {
     if (code == -3) return "PC_LAUNCH_MODE";
     return hipGetErrorName((hipError_t)code);
 }
-int pc_hip_last_error(void) { return rc(hipGetLastError()); }
+int pc_hip_last_error(void) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : (int)e;
+}
 }

@@ -110,6 +110,54 @@ def test_small_int(stream, name, k, c, inplace):
             assert (got[cc, part] == want).all(), (cc, part)
 
 
+def boundary_values(q_src, n, rng):
+    """N integers in [0, Q): the ones where the CRT quotient sum_a y_a / q_a sits next to an integer (X near 0 and
+    near Q), the centring boundary floor(Q / 2) and its neighbours, the CRT basis elements Q / q_a and their
+    neighbours, thirds of Q; the rest uniform."""
+    Q = 1
+    for p in q_src:
+        Q *= int(p)
+    h = Q // 2
+    vals = [0, 1, 2, 3, 1000, Q - 1, Q - 2, Q - 3, Q - 1000, h - 2, h - 1, h, h + 1, h + 2, Q // 3, 2 * Q // 3]
+    for p in q_src:
+        m = Q // int(p)
+        vals += [m - 1, m, m + 1, Q - m, Q - m + 1]
+    vals = [v % Q for v in vals]
+    rest = [int(rng.integers(0, 1 << 62)) * (1 << 62) % Q + int(rng.integers(0, 1 << 62)) for _ in range(n - len(vals))]
+    return vals + [v % Q for v in rest]
+
+
+@pytest.mark.parametrize("k,c", [(1, None), (2, None), (3, 1.0 / 3), (4, None), (4, 7.1e-12)])
+def test_small_int_boundaries(stream, k, c):
+    """small_int on integers chosen where a CRT or centring step can go wrong (next to 0 and Q, at floor(Q / 2), at
+    the basis elements Q / q_a), against the oracle's Garner reconstruction."""
+    name = "small31"
+    say(f"[small_int boundaries] {name} k={k} c={c}")
+    ch, ctx = context(name)
+    rng = np.random.default_rng(100 + k)
+    X = boundary_values(ch.primes[:k], ch.n, rng)
+    src = np.zeros((1, 2, ch.rows, ch.n), np.uint32)
+    for a in range(k):
+        src[0, 0, a] = [x % int(ch.primes[a]) for x in X]
+        src[0, 1, a] = [(int(ch.primes[a]) - 1 - x) % int(ch.primes[a]) for x in X]
+    out_rows = list(range(ch.rows))
+    tab = bts.small_int_tab(ch.primes[:k], out_rows, [ch.primes[r] for r in out_rows], c)
+    tb = tab_buf(tab)
+    sbuf = pa.DevBuf.from_array(src)
+    obuf = pa.DevBuf(src.size)
+    a = abi.SmallIntArgs()
+    a.src, a.out, a.tab, a.pr = sbuf.ptr.value, obuf.ptr.value, tb.ptr.value, LIB.pcx_ctx_primes(ctx.h)
+    a.src_ct_stride = a.ct_stride = 2 * ch.rows * ch.n
+    a.src_part_stride = a.part_stride = ch.rows * ch.n
+    a.K, a.nparts = 1, 2
+    run("small_int", a, stream, ch.logn)
+    got = obuf.download(src.shape)
+    for part in range(2):
+        want = ob.small_int(ch.primes[:k], src[0, part, :k], ch.primes, None if c is None else list(tab.R))
+        bad = np.nonzero((got[0, part] != want).any(axis=0))[0]
+        assert bad.size == 0, (part, bad[:8], [X[i] for i in bad[:4]])
+
+
 @pytest.mark.parametrize("c,nparts", [(0.25, 2), (2.3167161361161844e-07 * 4096.0, 1), (3.0e-5, 2)])
 def test_small_int1(stream, c, nparts):
     name = "small31"

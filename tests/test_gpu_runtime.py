@@ -82,6 +82,8 @@ def test_device_queries_of_device_open():
     assert LIB.pc_hip_device_attribute(C.byref(v), 0x10001, 0) == 0 and v.value == 0x950
     assert LIB.pc_hip_device_attribute(C.byref(v), 12345, 0) != 0
     assert LIB.pc_hip_device_attribute(C.byref(v), 16, 99) != 0  # no such device
+    # the failure is reported once, by its return code: the thread's last error is clear for the next launch's check
+    assert LIB.pc_hip_last_error() == 0
     free, total = C.c_size_t(0), C.c_size_t(0)
     assert LIB.pc_hip_mem_get_info(C.byref(free), C.byref(total)) == 0
     assert 0 < free.value <= total.value and total.value > (250 << 30)  # 288 GB of HBM3E

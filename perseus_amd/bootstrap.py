@@ -20,139 +20,34 @@ import math
 
 import numpy as np
 
-# ----------------------------------------------------------------------------------------------- special FFT layers
+from . import bts_setup as S
+
+# ----------------------------------------------------------------------------------------------- linear transforms
 
 
-def rot_group(n):
-    """5^j mod 4n, j < n: slot j sits at the root zeta^(5^j), zeta = exp(2 pi i / 4n)."""
-    g = np.empty(n, np.int64)
-    v = 1
-    for j in range(n):
-        g[j] = v
-        v = v * 5 % (4 * n)
-    return g
+class LtPlan:
+    """One linear-transform stage as the route evaluates it: a collapsed-FFT stage of the reference's factors in
+    FIDESlib's layout (bts_setup.FidesStage): y = sum_j rot(sum_i pts[j][i] rot(x, baby[i]), giant[j]) with
+    baby = rot_in (baby[0] = 0: the unrotated input), giant = rot_out, pts[j][i] the plaintext slot vector of diagonal
+    B j + i (None past the stage's diagonals or where it is zero)."""
 
-
-def _layer_w(n, ln):
-    """The twiddles of the butterfly layer of blocks of 2^ln slots, per slot of the first half of each block."""
-    m, length = 4 * n, 1 << ln
-    lenh, lenq = length >> 1, length << 2
-    k = np.arange(n)
-    pos = k % length
-    first = pos < lenh
-    j = np.where(first, pos, pos - lenh)
-    idx = (rot_group(n)[j] % lenq) * (m // lenq)
-    return first, np.exp(2j * np.pi * idx / m), lenh
-
-
-def layer(n, ln):
-    """Decoding layer (blocks of 2^ln): u, v -> u + w v, u - w v, as diagonals {offset: vector} over n slots
-    (y[k] = sum_d D_d[k] x[(k + d) mod n])."""
-    first, w, lenh = _layer_w(n, ln)
-    return {0: np.where(first, 1.0, -w).astype(complex), lenh: np.where(first, w, 0).astype(complex),
-            -lenh: np.where(first, 0, 1).astype(complex)}
-
-
-def layer_inv(n, ln):
-    """Inverse of `layer`: y_top, y_bot -> (y_top + y_bot) / 2, (y_top - y_bot) / (2 w)."""
-    first, w, lenh = _layer_w(n, ln)
-    iw = 1.0 / (2.0 * w)
-    return {0: np.where(first, 0.5, -iw).astype(complex), lenh: np.where(first, 0.5, 0).astype(complex),
-            -lenh: np.where(first, 0, iw).astype(complex)}
-
-
-def _norm(d, n):
-    d %= n
-    return d - n if d > n // 2 else d
-
-
-def compose(a, b, n):
-    """Diagonals of A o B (B applied first)."""
-    out = {}
-    for da, va in a.items():
-        for db, vb in b.items():
-            d = _norm(da + db, n)
-            t = va * np.roll(vb, -da)
-            out[d] = out[d] + t if d in out else t
-    return out
-
-
-def apply_diags(diags, x):
-    """y = sum_d D_d * rot(x, d) on plain slot vectors (rot(x, d)[k] = x[k + d])."""
-    y = np.zeros_like(x, dtype=complex)
-    for d, v in diags.items():
-        y += v * np.roll(x, -d)
-    return y
-
-
-def bitrev(n):
-    b = n.bit_length() - 1
-    return np.array([int(format(i, f"0{b}b")[::-1], 2) for i in range(n)], np.int64)
-
-
-def cts_levels(n, sizes):
-    """The CoeffToSlot levels: the inverse layers applied from blocks of n down to blocks of 2, grouped `sizes` (sum =
-    log2 n) in order of application; the product of all is the inverse decoding map up to the bit reversal
-    (slots come out bit-reversed)."""
-    assert sum(sizes) == n.bit_length() - 1
-    lns = list(range(n.bit_length() - 1, 0, -1))
-    out, i = [], 0
-    for s in sizes:
-        acc = None
-        for ln in lns[i:i + s]:
-            L = layer_inv(n, ln)
-            acc = L if acc is None else compose(L, acc, n)
-        out.append(acc)
-        i += s
-    return out
-
-
-def stc_levels(n, sizes):
-    """The SlotToCoeff levels: the decoding layers applied from blocks of 2 up to blocks of n, grouped `sizes`; their
-    product takes bit-reversed slots to the decoding of the coefficients."""
-    assert sum(sizes) == n.bit_length() - 1
-    lns = list(range(1, n.bit_length()))
-    out, i = [], 0
-    for s in sizes:
-        acc = None
-        for ln in lns[i:i + s]:
-            L = layer(n, ln)
-            acc = L if acc is None else compose(L, acc, n)
-        out.append(acc)
-        i += s
-    return out
-
-
-class BsgsPlan:
-    """A level y = sum_d D_d rot(x, d), offsets d = k s with k in [k0, k1] (each offset reduced into (-n/2, n/2]), as
-    baby-step giant-step: k - k0 = B j + i, y = sum_j rot(sum_i D'_{j,i} rot(x, i s), g_j s), g_j = B j + k0,
-    D'_{j,i} = rot(D_{(g_j + i) s}, -g_j s)."""
-
-    def __init__(self, diags, n, B=None):
-        offs = [d for d, v in diags.items() if np.abs(v).max() > 0]
-        s = 0
-        for d in offs:
-            s = math.gcd(s, abs(d))
-        s = s or 1
-        ks = sorted(d // s for d in offs)
-        k0, k1 = ks[0], ks[-1]
-        self.n, self.s, self.k0, self.k1 = n, s, k0, k1
-        width = k1 - k0 + 1
-        self.B = B or (1 << max(1, (width.bit_length() + 1) // 2))
-        self.G = -(-width // self.B)
-        self.baby = [i * s for i in range(self.B)]
-        self.giant = [(self.B * j + k0) * s for j in range(self.G)]
-        self.pts = []  # [j][i] the pre-rotated diagonal or None
+    def __init__(self, st, n):
+        self.n = n
+        self.B, self.G = st.b_step, st.g_step
+        self.baby = [int(x) for x in st.rot_in]
+        self.giant = [int(x) for x in st.rot_out]
+        assert self.baby[0] == 0, "the first baby step is the unrotated input"
+        self.pts = []
         for j in range(self.G):
             row = []
             for i in range(self.B):
-                k = self.B * j + k0 + i
-                v = diags.get(k * s) if k <= k1 else None
-                row.append(None if v is None or np.abs(v).max() == 0 else np.roll(v, self.giant[j]))
+                d = self.B * j + i
+                v = st.pts[d] if d < st.num_diags else None
+                row.append(None if v is None or not np.any(v) else np.asarray(v, np.complex128))
             self.pts.append(row)
 
     def apply(self, x):
-        """plain evaluation in BSGS order (the check of the decomposition)"""
+        """plain evaluation in the stage's BSGS order (the check of the layout)"""
         rots = [np.roll(x, -b) for b in self.baby]
         y = np.zeros(self.n, complex)
         for j in range(self.G):
@@ -164,7 +59,7 @@ class BsgsPlan:
         return y
 
     def steps(self):
-        """the rotation steps the level takes (babies, then giants), reduced to (0, n)"""
+        """the rotation steps the stage takes (babies, then giants), reduced to (0, n)"""
         out = []
         for r in self.baby[1:] + self.giant:
             r %= self.n
@@ -173,12 +68,19 @@ class BsgsPlan:
         return out
 
 
+def lt_plans(N, budget):
+    """The CoeffToSlot and SlotToCoeff stages of the full-slot bootstrap at ring degree N: the reference's factors
+    (bts_setup.cts_stc_factors with scale_enc = scale_dec = 1, its dense route's call, crates/pc-gpu/src/bts/
+    dense.rs:83) in FIDESlib's layout, CtS in evaluation order. Returns (cts plans, stc plans, the CtS stages' total
+    gain). The CtS stages compose to n brev(U0^-1) (OpenFHE's unnormalised inverse: each stage carries 2^layers), the
+    StC stages to U0 brev, the decoding map, exactly."""
+    n = N // 2
+    f = S.cts_stc_factors(N, n, list(budget), [0, 0], 1.0, 1.0)
+    cts, stc, _acc = f.fides_layout()
+    return [LtPlan(st, n) for st in cts], [LtPlan(st, n) for st in stc], float(n)
+
+
 # ----------------------------------------------------------------------------------------------- Chebyshev series
-
-
-def cheb_coeffs(f, deg):
-    """Chebyshev interpolant of f on [-1, 1] at the deg + 1 Chebyshev nodes: p(u) = sum_k c_k T_k(u)."""
-    return np.polynomial.chebyshev.chebinterpolate(f, deg)
 
 
 def cheb_split(c, g):
@@ -201,17 +103,23 @@ def cheb_eval(c, u):
 
 
 class EvalModPlan:
-    """y -> sin(2 pi y) / (2 pi)... as cos(2 pi (y - 1/4) / 2^r) on |y| <= K, a Chebyshev series in u = y / K of degree
-    `deg`, then r double angles (cos 2t = 2 cos^2 t - 1): the output is cos(2 pi (y - 1/4)) = sin(2 pi y)."""
+    """The reference's EvalMod series (bts_setup.evalmod_k32_low: K = 32, degree 59, 3 double angles, the prefactor
+    (2 pi)^(-1/8)) with its double-angle constants (bts_setup.double_angle_scalar): on u = y / K, the series
+    a cos(2 pi (K u - 1/4) / 8), then x -> 2 x^2 - (2 pi)^(-2^(j - 3)) three times, reads sin(2 pi K u) / (2 pi).
+    c holds the series with c0 halved: the reference's tables keep the evaluator convention (c0 / 2 + sum c_k T_k),
+    this module's Chebyshev evaluation the plain sum; halving is exact."""
 
-    def __init__(self, K=32, deg=63, r=3):
-        self.K, self.deg, self.r = K, deg, r
-        self.c = cheb_coeffs(lambda u: np.cos(2 * np.pi * (K * u - 0.25) / (1 << r)), deg)
+    def __init__(self):
+        self.K, self.r = S.EVALMOD_K32, S.EVALMOD_K32_LOW_DA_ITS
+        self.table = S.evalmod_k32_low()
+        self.c = np.array([self.table[0] / 2.0] + list(self.table[1:]))
+        self.deg = len(self.c) - 1
+        self.scalars = [S.double_angle_scalar(j, self.r) for j in range(1, self.r + 1)]
 
     def plain(self, u):
         h = cheb_eval(self.c, u)
-        for _ in range(self.r):
-            h = 2 * h * h - 1
+        for sc in self.scalars:
+            h = 2 * h * h + sc
         return h
 
 
@@ -219,45 +127,37 @@ class EvalModPlan:
 
 
 class Params:
-    """Bootstrap shape: slots n = N/2; CtS / StC level sizes (layers per level); EvalMod's K, degree, double angles;
-    the input's message scale; the output scale is whatever the chain leaves (reported)."""
+    """Bootstrap shape: slots n = N/2; the CtS / StC level budgets (OpenFHE's levelBudget: the collapsed FFT's stage
+    counts, [4, 3] in the reference's dense route); the input's message scale and the EvalMod input's target scale.
+    EvalMod is the reference's K = 32 series (EvalModPlan); the output scale is whatever the chain leaves."""
 
-    def __init__(self, logn, cts=None, stc=None, K=32, deg=63, r=3, delta_in=2.0 ** 25, target=2.0 ** 60):
+    def __init__(self, logn, budget=(4, 3), delta_in=2.0 ** 25, target=2.0 ** 60):
         self.logn, self.N, self.n = logn, 1 << logn, 1 << (logn - 1)
-        L = logn - 1
-        self.cts = cts or _split(L, 4)
-        self.stc = stc or _split(L, 3)
-        self.K, self.deg, self.r = K, deg, r
+        self.budget = (min(budget[0], logn - 1), min(budget[1], logn - 1))
+        self.K, self.r = S.EVALMOD_K32, S.EVALMOD_K32_LOW_DA_ITS
         self.delta_in, self.target = delta_in, target
 
     def levels_used(self):
         """composite (two-prime) levels the bootstrap consumes after ModRaise"""
-        return len(self.cts) + 7 + self.r + len(self.stc)
-
-
-def _split(L, k):
-    base, extra = divmod(L, k)
-    return [base + (1 if i < extra else 0) for i in range(k)]
+        return self.budget[0] + 7 + self.r + self.budget[1]
 
 
 def simulate(P, par, em=None):
     """Plain float simulation of the bootstrap's algorithm on an integer coefficient vector P (= m + q0 I after the raise,
-    here given directly) whose decoding the ciphertext holds: returns the output slot values (the decoding of
-    q0 / (2 pi) sin(2 pi P / q0), i.e. of m when |m| << q0) -- the check that the factors, the BSGS split and the
-    EvalMod series compose to the bootstrap. q0 is taken as 1 (P given as P / q0)."""
-    n = par.n
-    em = em or EvalModPlan(par.K, par.deg, par.r)
+    here given directly as P / q0): the reference's stages in FIDESlib's layout, the EvalMod series on the real and
+    imaginary parts, the StC stages; returns the output slot values, the decoding of sin(2 pi P / q0) / (2 pi), i.e. of
+    m / q0 when |m| << q0 -- the check that the factors, the layout and the EvalMod series compose to the bootstrap."""
     from .encoding import decode
 
-    z = decode(P, par.N, 1.0)  # slots of P / q0
-    x = z / (2.0 * par.K)
-    for lv in cts_levels(n, par.cts):
-        x = BsgsPlan(lv, n).apply(x)
+    em = em or EvalModPlan()
+    cts, stc, gain = lt_plans(par.N, par.budget)
+    x = decode(P, par.N, 1.0) / (2.0 * par.K * gain)
+    for p in cts:
+        x = p.apply(x)
     re, im = x + np.conj(x), -1j * (x - np.conj(x))
-    s_re, s_im = em.plain(re.real), em.plain(im.real)
-    w = (s_re + 1j * s_im) / (2 * np.pi)
-    for lv in stc_levels(n, par.stc):
-        w = BsgsPlan(lv, n).apply(w)
+    w = em.plain(re.real) + 1j * em.plain(im.real)
+    for p in stc:
+        w = p.apply(w)
     return w
 
 
@@ -564,8 +464,9 @@ class ChebEval:
 
 
 class Bootstrap:
-    """ModRaise -> CtS (len(par.cts) levels) -> EvalMod (real and imaginary parts) -> StC (len(par.stc) levels) on
-    an operations object. `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
+    """ModRaise -> CtS (par.budget[0] stages) -> EvalMod (real and imaginary parts) -> StC (par.budget[1] stages) on
+    an operations object, with the reference's constants: the collapsed-FFT factors in FIDESlib's layout (lt_plans)
+    and the K = 32 EvalMod series with its double angles (EvalModPlan). `primes`: the chain's Q primes (q0 = primes[0], the input's only limb); the input's message
     scale par.delta_in. Plaintexts (the levels' diagonals, the i monomial) are encoded once by `prepare`."""
 
     def __init__(self, ops, par, primes, ops2=None, special=None, pair=None, fuse_stc=True):
@@ -580,23 +481,23 @@ class Bootstrap:
         # the key-switched babies before any ModDown, one ModDown per giant step), the diagonals encoded over Q and P
         self.p = None if special is None else [int(x) for x in special]
         self.T = len(self.q) - 1
-        n = par.n
-        self.cts = [BsgsPlan(lv, n) for lv in cts_levels(n, par.cts)]
-        self.stc = [BsgsPlan(lv, n) for lv in stc_levels(n, par.stc)]
+        self.cts, self.stc, cts_gain = lt_plans(par.N, par.budget)
         # per level (CtS, then StC): fused in the extended basis, else hoisted babies and the plaintext dot over Q. The
         # fused form takes a ModDown per giant step instead of one per baby, so it pays where a level has fewer giant
         # steps than babies (CtS); fuse_stc False keeps the StC levels hoisted
         fz = self.p is not None
         self.fuse = [fz] * len(self.cts) + [fz and fuse_stc] * len(self.stc)
-        self.em = EvalModPlan(par.K, par.deg, par.r)
+        self.em = EvalModPlan()
         self.ev = Evaluator(ops, self.q)
         self.q0 = float(self.q[0])
-        # CtS: the raised ciphertext (values decode(P) / (2 q0 K), P = m + q0 I) is first multiplied by the integer
-        # c = 2^e that lifts its label 2 q0 K near par.target: the baby rotations' key-switch noise is added to
-        # integers that large, not to the raw P (about 2 q0 K); each level then multiplies the label by f so that the
-        # EvalMod input sits at par.target exactly
+        # CtS: the raised ciphertext (P = m + q0 I) is first multiplied by the integer c = 2^e that lifts 2 q0 K near
+        # par.target: the baby rotations' key-switch noise is added to integers that large, not to the raw P (about
+        # 2 q0 K). Its label carries 2 q0 K c times the CtS stages' gain n (OpenFHE's unnormalised inverse), so that
+        # after the stages the values are brev(U0^-1 decode(P)) / (2 q0 K), the EvalMod input; each stage multiplies
+        # the label by f so that this input sits at par.target exactly (the reference rides the same 1 / (K n) on its
+        # post-raise constant, crates/pc-gpu/src/bts/dense.rs)
         self.lift = 1 << max(0, int(math.floor(math.log2(par.target / (2.0 * self.q0 * par.K)))))
-        self.raise_scale = 2.0 * self.q0 * par.K * self.lift
+        self.raise_scale = 2.0 * self.q0 * par.K * self.lift * cts_gain
         self.cts_f = (par.target / self.raise_scale) ** (1.0 / len(self.cts))
         self.top_out = self.T - 2 * (len(self.cts) + 7 + par.r + len(self.stc))
         assert self.top_out >= 0, "the chain is too short for the bootstrap"
@@ -699,8 +600,8 @@ class Bootstrap:
         ce.basis(u)
         top = ce.out_top()
         h = ce.eval(self.em.c, top, ev.qq(top))
-        for _ in range(self.par.r):
-            h = ev.add_const(ev.mul(h, h, twice=True), -1.0)
+        for sc in self.em.scalars:
+            h = ev.add_const(ev.mul(h, h, twice=True), sc)
         return h
 
     def run(self, x_h):
@@ -762,8 +663,9 @@ class Bootstrap:
             w = self.lt(w, p, self.pts[k], 1.0, self.pt_s[k], rots=rots,
                         dest=ops.item(nxt, 0) if nxt is not None else None, fused=self.fuse[k])
             k += 1
-        # the slot values are now (2 pi / q0) times the message's at the input's scale: relabel
-        w.scale = w.scale * 2.0 * math.pi * par.delta_in / self.q0
+        # the slot values are now sin(2 pi P / q0) / (2 pi) ~ m / q0: 1 / q0 times the message's at the input's
+        # scale: relabel
+        w.scale = w.scale * par.delta_in / self.q0
         return w
 
     def precision_bits(self, err):

@@ -1,68 +1,38 @@
-"""The bootstrap composite (perseus_amd/bootstrap.py) on the CPU: its host constants against what the mathematics
-fixes (the special-FFT layers against the direct Vandermonde sums of the canonical embedding, the CoeffToSlot /
-SlotToCoeff levels and their baby-step giant-step split against the plain maps, the Chebyshev division identity, the
-EvalMod series against sin(2 pi y)), the float simulation of the whole algorithm, and the homomorphic composite run on
-the oracle's operations at N = 2^12: the decrypted output equals the input's message.
+"""The bootstrap composite (perseus_amd/bootstrap.py) on the CPU: the route's stage plans (the reference's factors,
+pinned in tests/test_bts_setup.py) composing to the CoeffToSlot / SlotToCoeff maps, the float simulation of the whole
+algorithm, and the homomorphic composite run on the oracle's operations at N = 2^12: the decrypted output equals the
+input's message.
 """
 import numpy as np
 import pytest
 
 from perseus_amd import bootstrap as B
 from perseus_amd.encoding import decode, encode
+from tests import special_fft as SF
 from tests import twin
 from tests.bts_ops import OracleOps
 from tests.test_oracle_ks import decrypt, encrypt
 
 
-def test_layers_compose_to_the_canonical_embedding():
-    logn = 7
-    N, n = 1 << logn, 1 << (logn - 1)
-    rng = np.random.default_rng(1)
-    w = rng.normal(size=n) + 1j * rng.normal(size=n)
-    x = w[B.bitrev(n)]
-    for ln in range(1, logn):
-        x = B.apply_diags(B.layer(n, ln), x)
-    zeta = np.exp(2j * np.pi / (4 * n))
-    g = B.rot_group(n)
-    direct = np.array([np.sum(w * zeta ** ((g[j] * np.arange(n)) % (4 * n))) for j in range(n)])
-    assert np.abs(x - direct).max() < 1e-10
-    # a real coefficient vector m decodes to V (m_lo + i m_hi)
-    m = rng.normal(size=N)
-    want = np.array([np.sum((m[:n] + 1j * m[n:]) * zeta ** ((g[j] * np.arange(n)) % (4 * n))) for j in range(n)])
-    assert np.abs(decode(m, N, 1.0) - want).max() < 1e-10
-
-
-@pytest.mark.parametrize("logn", [6, 9])
-def test_levels_and_bsgs(logn):
-    N, n = 1 << logn, 1 << (logn - 1)
-    par = B.Params(logn)
-    rng = np.random.default_rng(logn)
-    m = rng.normal(size=N)
-    z = decode(m, N, 1.0)
-    y = z
-    for lv in B.cts_levels(n, par.cts):
-        p = B.BsgsPlan(lv, n)
-        y2 = B.apply_diags(lv, y)
-        assert np.abs(p.apply(y) - y2).max() < 1e-9
-        y = y2
-    assert np.abs(y - (m[:n] + 1j * m[n:])[B.bitrev(n)]).max() < 1e-9, "CtS gives the bit-reversed coefficients"
-    for lv in B.stc_levels(n, par.stc):
-        p = B.BsgsPlan(lv, n)
-        y2 = B.apply_diags(lv, y)
-        assert np.abs(p.apply(y) - y2).max() < 1e-9
-        y = y2
-    assert np.abs(y - z).max() < 1e-9, "StC undoes CtS"
-
-
-def test_cheb_split_and_evalmod():
-    em = B.EvalModPlan(32, 63, 3)
-    u = np.linspace(-1, 1, 4001)
-    assert np.abs(em.plain(u) - np.sin(2 * np.pi * 32 * u)).max() < 1e-9
-    for g in (8, 16, 32):
-        c = em.c[: 2 * g]
-        q, r = B.cheb_split(c, g)
-        Tg = np.polynomial.chebyshev.chebval(u, np.eye(g + 1)[g])
-        assert np.abs(B.cheb_eval(q, u) * Tg + B.cheb_eval(r, u) - B.cheb_eval(c, u)).max() < 1e-12
+def test_route_stages_compose_to_the_transforms():
+    """the route's stage plans (the reference's factors in FIDESlib's layout): the CtS stages take the decoding of a
+    coefficient vector to n times its bit-reversed coefficients up to the layout's rotation, and the StC stages after
+    them give n times the input back (the accumulated rotation paid by the last StC stage)"""
+    for logn in (6, 9):
+        N, n = 1 << logn, 1 << (logn - 1)
+        cts, stc, gain = B.lt_plans(N, B.Params(logn).budget)
+        assert gain == n
+        rng = np.random.default_rng(logn)
+        m = rng.normal(size=N)
+        z = decode(m, N, 1.0)
+        y = z
+        for p in cts:
+            y = p.apply(y)
+        coeffs = (m[:n] + 1j * m[n:])[SF.bitrev(n)] * n
+        assert min(np.abs(np.roll(y, r) - coeffs).max() for r in range(n)) < 1e-8, "CtS: rotated coefficients"
+        for p in stc:
+            y = p.apply(y)
+        assert np.abs(y - n * z).max() < 1e-8 * n, "StC undoes CtS"
 
 
 def test_residues_exact():

@@ -880,16 +880,27 @@ int pcx_ntt(pcx_ctx* c, int dir, void* base, const pcx_rows* rows, pc_stream_t s
 typedef struct pcx_keys pcx_keys;
 pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
                        const uint32_t* const* b_host, int bits, int* err);
+/* A banded key group (crates/pc-gpu/src/keys.rs:81-103 KskShape::banded, :351-376 KeySetSpec::with_band): every key
+ * stores digits 0..ndig (each digit whose first prime id is <= q_top, ndig = q_top / ceil(nq / dnum) + 1), each the Q
+ * rows 0..=q_top then the kp special rows: host b [ndig][q_top + 1 + kp][N] per key. Its `a` is the full key's (the
+ * KSKA words depend on the seed, digit and prime only), so the band is the full key's rows restricted. The group
+ * serves ciphertexts at top <= q_top; an operation at a higher top returns -1. Its dots go through the kernel
+ * table's in-place reads of the stored slots (KeyTab.q_top, srows); no retry-value table is built. q_top = nq - 1 is
+ * pcx_keys_new. Special primes: all kp of the chain (chains with fewer special primes at low tops are not built). */
+pcx_keys* pcx_keys_new_banded(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
+                              const uint32_t* const* b_host, int bits, int q_top, int* err);
+/* the highest ciphertext top the group serves (nq - 1 for full keys), -1 on NULL */
+int pcx_keys_q_top(const pcx_keys* k);
 /* Keys generated on the device (crates/pc-gpu/src/keygen.rs:172-262): secret s (ternary coefficients), per key the
  * seed of a and the Gaussian errors e[dnum][N] (signed coefficients, the same error on every limb of a digit). */
 pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret,
                             const uint32_t* seeds, const int64_t* errors, int bits, int* err);
 void pcx_keys_free(pcx_keys* k);
-/* download key r's stored b as dense [dnum][nq + kp][N] words */
 /* bytes of the group's KSKA retry-value table (dense keys: the accepted redraws of the rejected ChaCha words, built
  * when the keys are made and read by the dot instead of redrawing them; about 1-2% of b at 31-bit primes); 0 if none.
  * No counterpart in the reference, whose dot redraws in the kernel (as the table entry ks_dot_key does here). */
 size_t pcx_keys_patch_bytes(const pcx_keys* k);
+/* download key r's stored b as dense words [ndig][srows][N] (full keys: [dnum][nq + kp][N]) */
 int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host);
 
 /* Ciphertexts are device buffers in the context layout [part][row = prime id over Q u P][N] words (2 (nq+kp) N words;

@@ -110,6 +110,9 @@ _SIGS = {
     "pcx_timing_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
     "pcx_copy_probe": (C.c_int, [vp, vp, C.c_size_t, vp]),
     "pcx_keys_patch_bytes": (C.c_size_t, [vp]),
+    "pcx_keys_new_banded": (vp, [vp, C.c_int, C.POINTER(C.c_uint64), u32p, C.POINTER(vp), C.c_int, C.c_int,
+                                 C.POINTER(C.c_int)]),
+    "pcx_keys_q_top": (C.c_int, [vp]),
     "pcx_decryptor_new": (vp, [vp, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "pcx_decryptor_free": (None, [vp]),
     "pcx_decryptor_load_secret": (C.c_int, [vp, u32p, C.c_int, vp]),

@@ -289,6 +289,9 @@ struct pcx_ctx {
 struct pcx_keys {
     pcx_ctx* c = nullptr;
     int nkeys = 0, bits = 0;
+    // the rows every key stores (crates/pc-gpu/src/keys.rs:81-103 KskShape): digits 0..ndig, each the Q rows
+    // 0..=q_top then the kp special rows (srows per digit); q_top = -1: the full layout (slot = prime id)
+    int q_top = -1, ndig = 0, srows = 0;
     uint64_t row_words = 0;
     std::vector<uint64_t> galois;
     std::vector<uint32_t> autok_h;
@@ -736,6 +739,7 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
         int c0_mode = 1, int K = 1, const uint32_t* digits = nullptr, const void* c0 = nullptr) {
     const Level* L = level(c, top);
     if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || K < 1 || K > c->k_max || K > 4) return -1;
+    if (k->q_top >= 0 && top > k->q_top) return -1;  // above the keys' band
     KsKeyArgs g;
     memset(&g, 0, sizeof g);
     KsArgs& a = g.ks;
@@ -769,9 +773,9 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     t.seed = k->seed + r0;
     t.row_words = k->row_words;
     t.bits = k->bits;
-    t.q_top = -1;
-    t.srows = c->rows;
-    t.nregen = c->dnum;
+    t.q_top = k->q_top;
+    t.srows = k->srows;
+    t.nregen = k->ndig;
     Stage st(c, 3, s);
     if (k->pval && !sum && !c->table_only) {
         // the retry values from the key group's table (no redraw in the dot)
@@ -794,7 +798,7 @@ int dot_diag(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, vo
              pc_stream_t s) {
     const Level* L = level(c, top);
     if (!L || r0 < 0 || m < 1 || r0 + m > k->nkeys || m > c->k_max) return -1;
-    if (!k->pval || c->table_only) return -2;
+    if (!k->pval || c->table_only || k->q_top >= 0) return -2;
     KsKeyArgs g;
     memset(&g, 0, sizeof g);
     KsArgs& a = g.ks;
@@ -966,6 +970,8 @@ pcx_keys* keys_shell(pcx_ctx* c, int nkeys, const uint64_t* galois, int bits, in
     k->c = c;
     k->nkeys = nkeys;
     k->bits = bits;
+    k->ndig = c->dnum;
+    k->srows = c->rows;
     k->row_words = bits ? packed_row_words(c->n, bits) : c->n;
     const uint64_t m = 2ull * c->n;
     for (int r = 0; r < nkeys; ++r) {
@@ -1271,15 +1277,26 @@ int pcx_ntt(pcx_ctx* c, int dir, void* base, const pcx_rows* rows, pc_stream_t s
     return dir == 1 ? c->tab->ntt_fwd(&a, s) : c->tab->ntt_inv(&a, s);
 }
 
-pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
-                       const uint32_t* const* b_host, int bits, int* err) {
+// A key group from host b ([ndig][srows][N] per key, dense words) and seeds, banded at q_top (nq - 1: full rows)
+static pcx_keys* keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
+                          const uint32_t* const* b_host, int bits, int q_top, int* err) {
     int dummy;
     if (!err) err = &dummy;
     *err = 0;
+    if (!c || !galois || !seeds || !b_host || q_top < 0 || q_top >= c->nq) {
+        *err = -1;
+        return nullptr;
+    }
     pcx_keys* k = keys_shell(c, nkeys, galois, bits, err);
     if (!k) return nullptr;
+    if (q_top < c->nq - 1) {
+        // crates/pc-gpu/src/keys.rs:86-92 KskShape::banded: every digit whose first prime is <= q_top
+        k->q_top = q_top;
+        k->ndig = q_top / c->alpha + 1;
+        k->srows = q_top + 1 + c->kp;
+    }
     const uint32_t n = c->n;
-    const size_t nrow = (size_t)c->dnum * c->rows;
+    const size_t nrow = (size_t)k->ndig * k->srows;
     std::vector<const void*> kb;
     std::vector<const uint32_t*> sd;
     for (int r = 0; r < nkeys; ++r) {
@@ -1298,7 +1315,8 @@ pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint
     }
     k->kb = (const void**)k->dev.upload(kb);
     k->seed = (const uint32_t**)k->dev.upload(sd);
-    if (!k->dev.err) {
+    if (!k->dev.err && k->q_top < 0) {
+        // the retry-value table is indexed by prime id: full-layout groups only (a band redraws in the dot)
         if (int e = build_patches(c, k)) k->dev.err = e;
     }
     if (k->dev.err) {
@@ -1308,6 +1326,16 @@ pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint
     }
     return k;
 }
+
+pcx_keys* pcx_keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
+                       const uint32_t* const* b_host, int bits, int* err) {
+    return keys_new(c, nkeys, galois, seeds, b_host, bits, c ? c->nq - 1 : 0, err);
+}
+pcx_keys* pcx_keys_new_banded(pcx_ctx* c, int nkeys, const uint64_t* galois, const uint32_t* seeds,
+                              const uint32_t* const* b_host, int bits, int q_top, int* err) {
+    return keys_new(c, nkeys, galois, seeds, b_host, bits, q_top, err);
+}
+int pcx_keys_q_top(const pcx_keys* k) { return k ? (k->q_top < 0 ? k->c->nq - 1 : k->q_top) : -1; }
 
 // crates/pc-gpu/src/keygen.rs:172-262: the secret's eval rows, per key the Gaussian errors NTT'd, s_new =
 // sigma_{g^-1}(s) by the automorph kernel, then ksk_gen (b dense or packed); sq: the old secret squared in the kernel
@@ -1443,7 +1471,7 @@ size_t pcx_keys_patch_bytes(const pcx_keys* k) { return k ? k->patch_words * 4 :
 int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host) {
     if (!k || r < 0 || r >= k->nkeys) return -1;
     pcx_ctx* c = k->c;
-    const size_t nrow = (size_t)c->dnum * c->rows;
+    const size_t nrow = (size_t)k->ndig * k->srows;
     std::vector<uint32_t> st(nrow * k->row_words);
     if (hipMemcpy(st.data(), k->b_ptr[r], st.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
     for (size_t q = 0; q < nrow; ++q) {
@@ -1567,9 +1595,9 @@ int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* con
     t.seed = k->seed + (B > 1 ? r0 : 0);
     t.row_words = k->row_words;
     t.bits = k->bits;
-    t.q_top = -1;
-    t.srows = c->rows;
-    t.nregen = c->dnum;
+    t.q_top = k->q_top;
+    t.srows = k->srows;
+    t.nregen = k->ndig;
     Stage st(c, 7, s);
     for (int j0 = 0; j0 < G; j0 += 4) {
         // up to four giant steps per launch: the baby keys regenerated once per launch

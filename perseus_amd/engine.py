@@ -305,11 +305,26 @@ class Context:
         check(LIB.pcx_moddown_k(self.h, ext.addr(), top, out.addr(), m, stream.h), "moddown_k")
 
 
+def band_digits(ctx, q_top):
+    """the digits a key banded at q_top stores: every digit whose first prime id is <= q_top"""
+    alpha = -(-ctx.nq // ctx.dnum)
+    return q_top // alpha + 1
+
+
+def band_rows(b, ctx, q_top):
+    """a full key's b [dnum][nq + kp][N] restricted to the band at q_top: digits 0..ndig, rows 0..=q_top then P"""
+    b = np.asarray(b)
+    nd = band_digits(ctx, q_top)
+    return np.ascontiguousarray(np.concatenate([b[:nd, : q_top + 1], b[:nd, ctx.nq:]], axis=1))
+
+
 class Keys:
     """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed. relin:
     the relinearization key s^2 -> s (galois 1, generated from secret / errors)."""
 
-    def __init__(self, ctx: Context, galois, seeds=None, b=None, bits=0, secret=None, errors=None, relin=False):
+    def __init__(self, ctx: Context, galois, seeds=None, b=None, bits=0, secret=None, errors=None, relin=False,
+                 q_top=None):
+        """q_top: a banded group (host b given as [ndig][q_top + 1 + kp][N] per key, pcx_keys_new_banded)"""
         self.ctx = ctx
         self.galois = [int(g) for g in galois]
         n = len(self.galois)
@@ -329,7 +344,11 @@ class Keys:
             bs = [np.ascontiguousarray(x, np.uint32) for x in b]
             self._keep += bs
             ptrs = (C.c_void_p * n)(*[x.ctypes.data for x in bs])
-            self.h = LIB.pcx_keys_new(ctx.h, n, _u64(self.galois), sp, ptrs, bits, C.byref(err))
+            if q_top is None:
+                self.h = LIB.pcx_keys_new(ctx.h, n, _u64(self.galois), sp, ptrs, bits, C.byref(err))
+            else:
+                self.h = LIB.pcx_keys_new_banded(ctx.h, n, _u64(self.galois), sp, ptrs, bits, int(q_top),
+                                                 C.byref(err))
         else:
             s = np.ascontiguousarray(secret, np.int8)
             e = np.ascontiguousarray(errors, np.int64).reshape(n, ctx.dnum, ctx.n)
@@ -345,8 +364,17 @@ class Keys:
         """Bytes of the group's KSKA retry-value table (0 when the dot redraws in the kernel)."""
         return int(LIB.pcx_keys_patch_bytes(self.h))
 
+    def q_top(self):
+        """the highest ciphertext top the group serves"""
+        return int(LIB.pcx_keys_q_top(self.h))
+
     def download_b(self, r):
-        out = np.empty((self.ctx.dnum, self.ctx.rows, self.ctx.n), np.uint32)
+        qt = self.q_top()
+        if qt == self.ctx.nq - 1:
+            shape = (self.ctx.dnum, self.ctx.rows, self.ctx.n)
+        else:
+            shape = (band_digits(self.ctx, qt), qt + 1 + self.ctx.kp, self.ctx.n)
+        out = np.empty(shape, np.uint32)
         check(LIB.pcx_keys_download_b(self.h, r, out.ctypes.data_as(C.POINTER(C.c_uint32))), "download_b")
         return out
 

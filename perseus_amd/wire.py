@@ -191,26 +191,36 @@ def pack_ksk(b, bits, row_words):
 
 def load_keys(reader, ctx, entries=None):
     """Rotation / automorphism keys of a bundle as one engine key group: each entry's b unpacked and stored at the
-    bundle's packing width, `a` regenerated from its seed as the reference's. The keys must be full-shape ones of the
-    context's chain (q_top = nq - 1, every digit, every special prime); banded keys are refused."""
-    from .engine import Keys
+    bundle's packing width, `a` regenerated from its seed as the reference's. The entries must share one shape over
+    the context's chain: full (q_top = nq - 1, every digit) or banded at one q_top (crates/pc-gpu/src/keys.rs:81-103
+    KskShape::banded: the digits whose first prime id is <= q_top, Q rows 0..=q_top, then the special rows); a
+    banded key over fewer special primes than the chain's (a LowP tier) is refused, as is a mix of bands (load each
+    band's entries as its own group)."""
+    from .engine import Keys, band_digits
 
     h = reader.header
     n = int(h["n"])
     idx = [i for i, e in enumerate(h["entries"]) if e["kind"] == "ksk" and galois_of(e, n) is not None] \
         if entries is None else list(entries)
-    gal, seeds, bs = [], [], []
+    gal, seeds, bs, tops = [], [], [], set()
     for i in idx:
         e = h["entries"][i]
         sh = e["shape"]
-        if sh["q_top"] != ctx.nq - 1 or sh["nq"] != ctx.nq or sh["kp"] != ctx.kp or sh["ndig"] != ctx.dnum:
+        qt = int(sh["q_top"])
+        if sh["nq"] != ctx.nq or sh["kp"] != ctx.kp or not 0 <= qt < ctx.nq or sh["ndig"] != band_digits(ctx, qt):
             raise WireError(f"entry {i}: a key of shape {sh} does not fit the context (nq {ctx.nq}, kp {ctx.kp}, "
-                            f"dnum {ctx.dnum})")
+                            f"dnum {ctx.dnum}; a band at q_top {qt} holds {band_digits(ctx, min(max(qt, 0), ctx.nq - 1))}"
+                            f" digits)")
+        tops.add(qt)
         gal.append(galois_of(e, n))
         seeds.append(np.asarray(e["seed"], np.uint32))
         bs.append(reader.ksk_b(i))
+    if len(tops) > 1:
+        raise WireError(f"entries of several bands {sorted(tops)}: load each band as its own group")
     bits = int(h["bits"])
-    return Keys(ctx, gal, seeds=np.stack(seeds), b=bs, bits=0 if bits >= 32 else bits), idx
+    qt = tops.pop() if tops else ctx.nq - 1
+    return Keys(ctx, gal, seeds=np.stack(seeds), b=bs, bits=0 if bits >= 32 else bits,
+                q_top=None if qt == ctx.nq - 1 else qt), idx
 
 
 # ----------------------------------------------------------------------------------------------- ciphertext frame

@@ -308,6 +308,9 @@ struct pcx_keys {
 
 namespace {
 
+// a key group serves a ciphertext at top: every top for full keys, tops up to the band for banded ones
+inline bool serves(const pcx_keys* k, int top) { return k->q_top < 0 || top <= k->q_top; }
+
 // A stage bracket: when timing is on, an event before and after the stage's launches (stream order)
 struct Stage {
     pcx_ctx* c;
@@ -1501,7 +1504,7 @@ int pcx_moddown(pcx_ctx* c, void* ext, int top, void* out, pc_stream_t s) {
 }
 
 int pcx_rotate(pcx_ctx* c, pcx_keys* k, int r, const void* ct, int top, void* out, pc_stream_t s) {
-    if (!c || !k || r < 0 || r >= k->nkeys || !level(c, top)) return -1;
+    if (!c || !k || r < 0 || r >= k->nkeys || !level(c, top) || !serves(k, top)) return -1;
     if (k->galois[r] == 1) return copy_q(c, ct, top, out, s);
     if (int e = modup(c, ct, top, s)) return e;
     if (int e = dot(c, k, r, 1, ct, top, c->ext, s)) return e;
@@ -1512,6 +1515,7 @@ int pcx_cts_stage_hoisted(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const v
                           uint32_t enc, const void* ct, int top, void* rot, void* res, pc_stream_t s) {
     const Level* L = c ? level(c, top) : nullptr;
     if (!L || !k || k->c != c || B < 1 || G < 1 || npts < 0 || !pts || !ct || !rot || !res) return -1;
+    if (!serves(k, top)) return -1;
     if (B > 1 && (r0 < 0 || r0 + B - 1 > k->nkeys)) return -1;
     const uint64_t part = (uint64_t)c->rows * c->n;
     // rot_0 = P ct on Q rows 0..top, zero on the special rows
@@ -1561,6 +1565,7 @@ int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* con
                   uint32_t enc, const void* ct, int top, void* res, pc_stream_t s) {
     const Level* L = c ? level(c, top) : nullptr;
     if (!L || !k || k->c != c || B < 1 || G < 1 || npts < 0 || !pts || !ct || !res) return -1;
+    if (!serves(k, top)) return -1;
     if (B > 1 && (r0 < 0 || r0 + B - 1 > k->nkeys)) return -1;
     if (B > 1)
         if (int e = modup(c, ct, top, s)) return e;
@@ -1612,7 +1617,7 @@ int pcx_cts_stage(pcx_ctx* c, pcx_keys* k, int r0, int B, int G, const void* con
 
 int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
                        pc_stream_t s) {
-    if (!c || !k || n < 1 || !level(c, top)) return -1;
+    if (!c || !k || n < 1 || !level(c, top) || !serves(k, top)) return -1;
     for (int j = 0; j < n; ++j)
         if (idx[j] < 0 || idx[j] >= k->nkeys) return -1;
     const size_t cw = c->ct_words();
@@ -1644,7 +1649,7 @@ int pcx_rotate_hoisted(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const voi
 
 int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* ct, int top, void* out,
                    const void* onto, pc_stream_t s) {
-    if (!c || !k || k->c != c || n < 1 || !idx || !ct || !out || !level(c, top)) return -1;
+    if (!c || !k || k->c != c || n < 1 || !idx || !ct || !out || !level(c, top) || !serves(k, top)) return -1;
     for (int j = 0; j < n; ++j)
         if (idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;  // no step 0 in a sum group
     if (int e = modup(c, ct, top, s)) return e;
@@ -1664,7 +1669,7 @@ int pcx_rotate_sum(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* c
 // sum (*nsum = 1).
 static int rotate_many_ext(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const void* const* cts, int top,
                            pc_stream_t s, int* nsum) {
-    if (!c || !k || k->c != c || n < 1 || !idx || !cts || !level(c, top)) return -1;
+    if (!c || !k || k->c != c || n < 1 || !idx || !cts || !level(c, top) || !serves(k, top)) return -1;
     for (int j = 0; j < n; ++j)
         if (!cts[j] || idx[j] < 0 || idx[j] >= k->nkeys || k->galois[idx[j]] == 1) return -1;
     // runs of up to k_max inputs laid out ct_words apart share one ModUp launch sequence; each input's dot then reads
@@ -1741,7 +1746,7 @@ static int rotate_sum_k(pcx_ctx* c, pcx_keys* k, const int* idx, int n, const vo
 
 int pcx_rotate_and_sum_k(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop,
                          int radix_bits, void* out, void* tmp, int K, pc_stream_t s) {
-    if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top) || K < 1) return -1;
+    if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top) || K < 1 || !serves(k, top)) return -1;
     const size_t cw = c->ct_words();
     if (K == 1) return pcx_rotate_and_sum(c, k, x, top, start, stop, radix_bits, out, tmp, s);
     if (start == 0 || stop <= 0 || K > c->k_max || K > c->k_rot) return -1;
@@ -1789,7 +1794,7 @@ int pcx_rotate_and_sum_k(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_
 
 int pcx_rotate_and_sum(pcx_ctx* c, pcx_keys* k, const void* x, int top, int64_t start, int64_t stop, int radix_bits,
                        void* out, void* tmp, pc_stream_t s) {
-    if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top)) return -1;
+    if (!c || !k || k->c != c || !x || !out || !tmp || !level(c, top) || !serves(k, top)) return -1;
     if (start == 0 || stop <= 0) return -1;
     const uint64_t m2 = 2ull * c->n;
     // the key of a rotation step (g = 5^step mod 2N; negative steps by the inverse), -1 if the group has none
@@ -1912,7 +1917,7 @@ int pcx_rescale(pcx_ctx* c, const void* ct, int top, int ndrop, void* out, pc_st
 static int relin_ext(pcx_ctx* c, pcx_keys* k, const void* a, const void* b, int top, void* out, pc_stream_t s,
                      bool* folded, int K = 1, int twice = 0) {
     if (!c || !k || !a || !b || !out || top < 0 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
-    if (K < 1 || K > c->k_max || K > 4) return -1;  // the key dot takes at most 4 ciphertexts
+    if (K < 1 || K > c->k_max || K > 4 || !serves(k, top)) return -1;  // the key dot takes at most 4 ciphertexts
     const uint64_t part = (uint64_t)c->rows * c->n;
     TensorArgs t;
     memset(&t, 0, sizeof t);
@@ -1955,7 +1960,7 @@ int pcx_mul_relin_rescale_k(pcx_ctx* c, pcx_keys* k, const void* a, const void* 
 int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b, int K, int top,
                                void* out, int twice, pc_stream_t s) {
     if (!c || !k || !a || !b || !out || top < 2 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
-    if (K < 1 || K > c->k_max || K > pch::TLIST_MAX) return -1;
+    if (K < 1 || K > c->k_max || K > pch::TLIST_MAX || !serves(k, top)) return -1;
     const uint64_t part = (uint64_t)c->rows * c->n;
     pch::TensorListArgs t;
     memset(&t, 0, sizeof t);

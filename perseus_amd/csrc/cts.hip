@@ -67,6 +67,13 @@ __device__ __forceinline__ void ld8(gptr p, uint32_t (&v)[CS]) {
     const gu4 a = q[0], b = q[1];
     v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
 }
+// a stream read once per launch (a key's b row, a diagonal): non-temporal, so that it does not push the rows read
+// again out of L2 (the ModUp digits, which every baby of the chunk's row reads at another source chunk)
+__device__ __forceinline__ void ld8_once(gptr p, uint32_t (&v)[CS]) {
+    const __attribute__((address_space(1))) gu4* q = (const __attribute__((address_space(1))) gu4*)p;
+    const gu4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
 __device__ __forceinline__ void st8(uint32_t* p, const uint32_t (&v)[CS]) {
     ((uint4*)p)[0] = make_uint4(v[0], v[1], v[2], v[3]);
     ((uint4*)p)[1] = make_uint4(v[4], v[5], v[6], v[7]);
@@ -210,7 +217,7 @@ __device__ __forceinline__ void products(const Row& R, const KeyRow& K, uint32_t
         } else {
             ld8(K.ka + d * K.astride + s0, a);
         }
-        if (K.bits == 0) ld8(K.kb + d * K.bstride + s0, b);
+        if (K.bits == 0) ld8_once(K.kb + d * K.bstride + s0, b);
         else ld_packed((const uint32_t*)(K.kb + d * K.bstride), K.bwords, s0, K.bits, b);
         ld8(R.drow(d) + s0, x);
 #pragma unroll
@@ -279,6 +286,15 @@ __device__ __forceinline__ void rotation(const Row& R, const KeyRow& K, uint32_t
     to_output(R, kx, sc + lane * CS, lane, v0, v1, w0, w1);
 }
 
+// The block's (chunk, row index) in an XCD-aware order: each XCD takes a contiguous range of the row-major
+// (row, chunk) blocks, so that a row's chunks run on one XCD. A rotation's sources are the automorphism's image of the
+// output chunk, spread over the whole row: kept on one XCD, a row's digit and key words are fetched into that XCD's
+// L2 once instead of once per XCD.
+__device__ __forceinline__ uint2 chunk_row() {
+    const uint32_t l = xcd_block(blockIdx.y * gridDim.x + blockIdx.x, gridDim.x * gridDim.y);
+    return make_uint2(l % gridDim.x, l / gridDim.x);
+}
+
 // ------------------------------------------------------------------------------------------------ CtS stage
 // grid (N / 512 chunks, rows, K ciphertexts); giant steps j0 .. j0 + 3 of the launch. REGEN: keys through the KeyTab
 // (a regenerated for digits < nregen).
@@ -288,7 +304,8 @@ __global__ void __launch_bounds__(CW, 3) cts_k(CtsRegenArgs RA, int logn, int j0
     const CtsArgs& A = RA.cts;
     const KeyTab& T = RA.key;
     const int lane = threadIdx.x, c = blockIdx.z;
-    const int t = (int)A.rows[blockIdx.y];
+    const uint2 cr = chunk_row();
+    const int t = (int)A.rows[cr.y];
     const PrimeConst& q = A.pr[t];
     const bool isq = t < A.nq;
     Row R = make_row(q, logn, lds, REGEN ? min(A.ndig, T.nregen) : 0);
@@ -306,7 +323,7 @@ __global__ void __launch_bounds__(CW, 3) cts_k(CtsRegenArgs RA, int logn, int j0
     R.pms = isq ? ((const uint32_t*)A.pmods)[t] : 0;
     const int prow = isq ? t : A.pt_prow + (t - A.nq);
     const int slot = REGEN ? slot_of(T, t, A.nq) : t;
-    const uint32_t oc0 = blockIdx.x * CCH;
+    const uint32_t oc0 = cr.x * CCH;
     const uint32_t o0 = oc0 + lane * CS;  // the lane's output slots o0 .. o0 + 7
     const int gn = min(GW, A.G - j0);
     const bool pt8 = A.enc == 0xFFFFFFFFu && (A.ptw & 3) == 0;
@@ -365,7 +382,7 @@ __global__ void __launch_bounds__(CW, 3) cts_k(CtsRegenArgs RA, int logn, int j0
             const uint32_t* pt = (const uint32_t*)A.pts[dg] + (size_t)prow * A.ptw;
             uint32_t w[CS];
             if (pt8 && ((uintptr_t)pt & 15) == 0) {
-                ld8(as_global(pt) + o0, w);
+                ld8_once(as_global(pt) + o0, w);
             } else {
                 const Buf bp(pt, (uint32_t)A.ptw * 4);
 #pragma unroll
@@ -462,7 +479,8 @@ __global__ void __launch_bounds__(CW, 3) ksum_k(KsKeyArgs G, int logn) {
     const KsArgs& A = G.ks;
     const KeyTab& T = G.key;
     const int lane = threadIdx.x, c = blockIdx.z;
-    const int t = (int)A.rows[blockIdx.y];
+    const uint2 cr = chunk_row();
+    const int t = (int)A.rows[cr.y];
     const bool isq = t < A.nq;
     Row R = make_row(A.pr[t], logn, lds, max(0, min(A.ndig, T.nregen)));
     const uint32_t p = R.p;
@@ -478,7 +496,7 @@ __global__ void __launch_bounds__(CW, 3) ksum_k(KsKeyArgs G, int logn) {
     R.pm = R.c0m == 1 ? ((const uint32_t*)A.pmod)[t] : 0;
     R.pms = R.c0m == 1 ? ((const uint32_t*)A.pmods)[t] : 0;
     const int slot = slot_of(T, t, A.nq);
-    const uint32_t oc0 = blockIdx.x * CCH;
+    const uint32_t oc0 = cr.x * CCH;
     const uint32_t o0 = oc0 + lane * CS;
     uint32_t acc0[CS], acc1[CS];
 #pragma unroll

@@ -289,7 +289,8 @@ __device__ __forceinline__ void rotation(const Row& R, const KeyRow& K, uint32_t
 // The block's (chunk, row index) in an XCD-aware order: each XCD takes a contiguous range of the row-major
 // (row, chunk) blocks, so that a row's chunks run on one XCD. A rotation's sources are the automorphism's image of the
 // output chunk, spread over the whole row: kept on one XCD, a row's digit and key words are fetched into that XCD's
-// L2 once instead of once per XCD.
+// L2 once instead of once per XCD. (The summed rotations' kernel keeps the plain order: there the K ciphertexts of a
+// launch share each key row, and the plain order measured faster.)
 __device__ __forceinline__ uint2 chunk_row() {
     const uint32_t l = xcd_block(blockIdx.y * gridDim.x + blockIdx.x, gridDim.x * gridDim.y);
     return make_uint2(l % gridDim.x, l / gridDim.x);
@@ -479,8 +480,7 @@ __global__ void __launch_bounds__(CW, 3) ksum_k(KsKeyArgs G, int logn) {
     const KsArgs& A = G.ks;
     const KeyTab& T = G.key;
     const int lane = threadIdx.x, c = blockIdx.z;
-    const uint2 cr = chunk_row();
-    const int t = (int)A.rows[cr.y];
+    const int t = (int)A.rows[blockIdx.y];
     const bool isq = t < A.nq;
     Row R = make_row(A.pr[t], logn, lds, max(0, min(A.ndig, T.nregen)));
     const uint32_t p = R.p;
@@ -496,7 +496,7 @@ __global__ void __launch_bounds__(CW, 3) ksum_k(KsKeyArgs G, int logn) {
     R.pm = R.c0m == 1 ? ((const uint32_t*)A.pmod)[t] : 0;
     R.pms = R.c0m == 1 ? ((const uint32_t*)A.pmods)[t] : 0;
     const int slot = slot_of(T, t, A.nq);
-    const uint32_t oc0 = cr.x * CCH;
+    const uint32_t oc0 = blockIdx.x * CCH;
     const uint32_t o0 = oc0 + lane * CS;
     uint32_t acc0[CS], acc1[CS];
 #pragma unroll

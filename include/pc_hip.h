@@ -558,7 +558,8 @@ PC_STATIC_ASSERT(sizeof(SmallInt1Args) == 56, "SmallInt1Args layout");
  * res[c][j][part] = sum_{i < bstep} rot[c][i][part] pt[bstep j + i] (j < gstep, diagonals >= npts skipped); rot (c, i)
  * at rot.base + c rot.ct_stride + i rot_stride, res (c, j) at res.base + c res.ct_stride + j res_stride; pts[d]: the
  * diagonal's rows (ptw words each; Q rows, then the special rows from pt_prow), read at the compact index (enc as
- * CtsArgs.enc) */
+ * CtsArgs.enc). res must not overlap rot: past 8 baby steps the sums of later groups of rotations are added onto the
+ * results stored by the earlier groups, so a result row written over a rotation not yet read would feed it back. */
 typedef struct PtDotArgs {
     PolyRef rot, res;
     uint64_t rot_stride, res_stride;

@@ -331,9 +331,11 @@ __global__ void __launch_bounds__(BX) submul_many_k(SubMulManyArgs A, int logn) 
 // skipped; prow = y on Q rows, pt_prow + (y - nq) on special rows. 4 consecutive slots per thread, one ciphertext at a
 // time, the sums exact.
 //
-// The register form (bstep <= BM): a thread's words of the bstep rotations stay in registers across the giant steps,
-// so each rotation word is read from HBM once (re-reading them per giant step cost bstep x 2 rows per giant step), and
-// each giant step issues all its diagonal loads before the first product. The diagonal pointers are loaded through the
+// The register form: a thread's words of BM rotations stay in registers across the giant steps, so each rotation word
+// is read from HBM once (re-reading them per giant step cost bstep x 2 rows per giant step), and each giant step
+// issues all its diagonal loads before the first product. More than BM baby steps go in groups of BM: a later group's
+// sums are added onto the results the earlier groups stored (the same thread's words: two result rows per giant step
+// and group, against bstep rotation rows per giant step re-read). The diagonal pointers are loaded through the
 // scalar cache and the words as global (not flat) loads, so no wait on one serialises the others. MODE 0: full-width
 // diagonals (words i .. i + 3 in one 16-byte load); 1: compact by a shift s >= 2 (the thread's 4 words share one
 // diagonal word); 2: any other index form (a load per word).
@@ -354,28 +356,29 @@ __global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
     // the rotations read: b < bstep and b < npts (npts >= 1); the loads past them re-read rotation 0, never used
     const int nb = min(A.bstep, A.npts);
     const ConstTab tab = (ConstTab)A.pts;
-    for (int c = 0; c < A.K; ++c) {
+    for (int c = 0; c < A.K; ++c)
+      for (int b0 = 0; b0 < nb; b0 += BM) {
         W4 x0[BM], x1[BM];
 #pragma unroll
         for (int b = 0; b < BM; ++b) {
-            const uint32_t* r =
-                (const uint32_t*)A.rot.base + c * A.rot.ct_stride + (b < nb ? b : 0) * A.rot_stride + roff;
+            const uint32_t* r = (const uint32_t*)A.rot.base + c * A.rot.ct_stride +
+                                (b0 + b < nb ? b0 + b : 0) * A.rot_stride + roff;
             x0[b] = ld4(r);
             x1[b] = ld4(r + A.rot.part_stride);
         }
         for (int j = 0; j < A.gstep; ++j) {
-            // a missing diagonal (b >= nb or d >= npts) reads diagonal 0 and weighs 0
+            // a missing diagonal (b0 + b >= nb or d >= npts) reads diagonal 0 and weighs 0
             uint64_t pp[BM];
 #pragma unroll
             for (int b = 0; b < BM; ++b) {
-                const int d = A.bstep * j + b;
-                pp[b] = tab[b < nb && d < A.npts ? d : 0];
+                const int d = A.bstep * j + b0 + b;
+                pp[b] = tab[b0 + b < nb && d < A.npts ? d : 0];
             }
             W4 pw[BM];
 #pragma unroll
             for (int b = 0; b < BM; ++b) {
-                const int d = A.bstep * j + b;
-                const bool ok = b < nb && d < A.npts;
+                const int d = A.bstep * j + b0 + b;
+                const bool ok = b0 + b < nb && d < A.npts;
                 const GPtr pt = (GPtr)pp[b] + (size_t)prow * A.ptw;
                 if constexpr (MODE == 0) {
                     const U4 u = *(const __attribute__((address_space(1))) U4*)(pt + i);
@@ -408,13 +411,22 @@ __global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
                 r1.v[w] = s1[w].red(red);
             }
             uint32_t* o = (uint32_t*)A.res.base + c * A.res.ct_stride + j * A.res_stride + roff;
+            if (b0 > 0) {
+                // the earlier groups' sums, stored by this thread
+                const W4 e0 = ld4(o), e1 = ld4(o + A.res.part_stride);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    r0.v[w] = addm(r0.v[w], e0.v[w], red.p);
+                    r1.v[w] = addm(r1.v[w], e1.v[w], red.p);
+                }
+            }
             st4(o, r0);
             st4(o + A.res.part_stride, r1);
         }
-    }
+      }
 }
 
-// more baby steps, or no diagonals: the rotations re-read per giant step
+// no diagonals: the rotations re-read per giant step
 __global__ void __launch_bounds__(BX) pt_dot_k(PtDotArgs A, int logn) {
     const int y = blockIdx.y;
     const int row = y < A.rs.nq ? y : A.rs.qmax + (y - A.rs.nq);
@@ -765,9 +777,9 @@ int pt_dot(const PtDotArgs* a, pc_stream_t s) {
                        : (a->enc >> 24) == 0x7Fu ? (a->enc & 0xFFu) > 31 || (uint32_t)a->ptw < (n >> (a->enc & 0xFFu))
                                                  : (uint64_t)a->ptw <= ((n - 1) & a->enc)))
         return -1;
-    // up to 8 baby steps: the register form; its diagonal loads by index form (full rows of whole 16-byte groups,
-    // compact by a shift of at least 2, anything else)
-    if (a->bstep >= 1 && a->bstep <= 8 && a->npts >= 1) {
+    // the register form (baby steps in groups of 4 or 8); its diagonal loads by index form (full rows of whole 16-byte
+    // groups, compact by a shift of at least 2, anything else)
+    if (a->bstep >= 1 && a->npts >= 1) {
         const int mode = a->enc == 0xFFFFFFFFu && (a->ptw & 3) == 0                ? 0
                          : (a->enc >> 24) == 0x7Fu && (a->enc & 0xFFu) >= 2 ? 1
                                                                               : 2;

@@ -476,12 +476,15 @@ def test_encrypt(stream, name, with_m, with_c1, alias_e):
 
 
 # ----------------------------------------------------------------------------------------------- BSGS plaintext dot
-# baby steps up to 4 and up to 8 take the register form (full, compact and masked diagonal indices, a last giant step
-# short of diagonals), 9 the re-reading one
+# the register form in groups of 4 or 8 baby steps (full, compact and masked diagonal indices, a last giant step
+# short of diagonals): one group up to 8, two or three past it (a short last group; 16 babies x 4 giant steps, a
+# SlotToCoeff stage's shape; K ciphertexts sharing the diagonals)
 @pytest.mark.parametrize("name,enc,K,B,G,npts", [("small31", 0xFFFFFFFF, 2, 3, 2, 5), ("small31", 0x7F000003, 3, 3, 2, 5),
                                                 ("small", 0x3FF, 1, 3, 2, 5), ("c3", 0xFFFFFFFF, 1, 3, 2, 5),
                                                 ("small31", 0x7F000004, 2, 8, 3, 21), ("small31", 0xFFFFFFFF, 1, 7, 2, 14),
-                                                ("small", 0x7F000001, 1, 6, 2, 9), ("small31", 0x7F000002, 1, 9, 2, 11)])
+                                                ("small", 0x7F000001, 1, 6, 2, 9), ("small31", 0x7F000002, 1, 9, 2, 11),
+                                                ("small31", 0xFFFFFFFF, 2, 16, 4, 63), ("small", 0x7F000003, 1, 16, 2, 25),
+                                                ("small31", 0x1FF, 3, 24, 2, 40), ("c3", 0x7F000002, 1, 16, 4, 63)])
 def test_pt_dot(stream, name, enc, K, B, G, npts):
     say(f"[pt_dot] {name} enc={enc:#x} K={K} B={B} G={G} npts={npts}")
     ch, ctx, _ = contexts(name)

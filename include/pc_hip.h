@@ -862,6 +862,12 @@ size_t pcx_ctx_workspace_bytes(const pcx_ctx* c);
  * the ModDown conversion as the table's bconv then ntt_fwd with its epilogue, the key dots as ks_dot_key (a key
  * group's retry-value table unused); off: the driver's fused forms. Returns the previous setting, -1 on NULL. */
 int pcx_ctx_table_only(pcx_ctx* c, int on);
+/* No counterpart in the reference: a tuning switch. Which conversions the driver streams into the forward NTT's
+ * column pass instead of the table's bconv then ntt_fwd: bit 0 the ModUp, bit 1 the ModDown the register-held fused
+ * form does not take (more than 6 special primes), bit 2 the ModDown-rescale (default 3, or PCX_CC_FUSED at context
+ * creation; the table-only mode uses none). mask < 0 reads the setting. Returns the previous mask, -1 on NULL. The
+ * words are the same either way. */
+int pcx_ctx_conv_fusion(pcx_ctx* c, int mask);
 
 /* No counterpart in the reference: a tuning switch. Launches of N = 2^16 with at least `rows` rows take the one-pass
  * transform (one workgroup per row) instead of the two-pass one; 0 (the default, or PCX_NTT1_MIN) never. Returns the

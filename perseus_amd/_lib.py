@@ -70,6 +70,7 @@ _SIGS = {
     "pcx_ctx_root": (C.c_uint64, [vp, C.c_int]),
     "pcx_ctx_workspace_bytes": (C.c_size_t, [vp]),
     "pcx_ctx_table_only": (C.c_int, [vp, C.c_int]),
+    "pcx_ctx_conv_fusion": (C.c_int, [vp, C.c_int]),
     "pcx_rows_new": (vp, [vp, u32p, C.POINTER(C.c_int32), C.c_int]),
     "pcx_rows_free": (None, [vp]),
     "pcx_ntt": (C.c_int, [vp, C.c_int, vp, vp, vp]),

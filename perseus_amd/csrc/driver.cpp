@@ -269,6 +269,14 @@ struct pcx_ctx {
     int md_fused = 1;         // ModDown conversion inside the NTT column pass (kp <= MDC_MAX_KP)
     int md_fused_init = 1;    // md_fused as chosen at creation (PCX_MD_FUSED included), restored by table_only(0)
     int table_only = 0;       // every launch through the kernel table (pcx_ctx_table_only)
+    // conversions streamed into the NTT column pass (pch::conv_cols), by call site: CC_MODUP | CC_MODDOWN | CC_MDR
+    // (ModDown the fused md_conv_cols does not take, the ModDown-rescale); pcx_ctx_conv_fusion, PCX_CC_FUSED. The
+    // default leaves the ModDown-rescale on bconv then ntt_fwd: its exact form carries the doubles of u beside the sums
+    // (2 waves per SIMD) and measured slower on the C5 bootstrap (ModUp + ModDown stages 5.09 ms unfused, 4.91 with
+    // ModUp and ModDown streamed, 5.22 with the rescale's too; same box)
+    int cc_fused = 3;
+    int cc_tpw = 0;  // its targets per workgroup (0: from the launch's size; PCX_CC_TPW)
+    int cc_ntg = 3, cc_ntgx = 2;  // targets per round of a thread's sums: fast, exact jobs (PCX_CC_NTG, PCX_CC_NTGX)
     int md_ntg = 5;           // its target rows per workgroup
     int32_t* digit_of = nullptr;
     std::vector<Level> levels;
@@ -647,6 +655,31 @@ const Level* level(const pcx_ctx* c, int top) {
     return &c->levels[top];
 }
 
+enum { CC_MODUP = 1, CC_MODDOWN = 2, CC_MDR = 4 };
+bool cc_on(const pcx_ctx* c, int site) { return !c->table_only && (c->cc_fused & site); }
+// targets per workgroup of a streamed conversion: CC_NTG, raised while the launch keeps about 2048 workgroups (each
+// target group re-reads its column block's sources from L2)
+int cc_tpw(const pcx_ctx* c, const BconvArgs& b, int ntg) {
+    if (c->cc_tpw > 0) return c->cc_tpw;
+    const long per = (long)(c->n / 4096) * b.njobs;
+    int k = 1;
+    while (k < 4 && per * ((b.max_tgt + ntg * (k + 1) - 1) / (ntg * (k + 1))) >= 2048) ++k;
+    return ntg * k;
+}
+// the conversion b streamed into the column pass of f's rows (exactly b's targets), then f's row pass and epilogue
+// (exact: b's jobs are the exact conversion)
+int conv_then_rows(pcx_ctx* c, const BconvArgs& b, const NttArgs& f, pc_stream_t s, int st_conv, int st_rows,
+                   int exact = 0) {
+    {
+        Stage st(c, st_conv, s);
+        const int ntg = exact ? c->cc_ntgx : c->cc_ntg;
+        if (int e = pch::conv_cols((int)c->logn, &b, c->fw, c->fws, c->lazy, exact, ntg, cc_tpw(c, b, ntg), s))
+            return e;
+    }
+    Stage st(c, st_rows, s);
+    return pch::ntt_fwd_rows_only((int)c->logn, &f, s);
+}
+
 // ModUp (crates/pc-gpu/src/ks.rs:958-1040): INTT of c1 rows 0..top (out of place, N^-1 pre_t), conversion of every
 // live digit, NTT of the targets
 // ModDown and the two-prime rescale at once (the level's mdr plan): out (Q rows 0..top - 2) = the exact
@@ -686,10 +719,6 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     b.pr = c->pr;
     b.njobs = k_jobs(c, M.conv, K);
     b.max_tgt = M.conv.max_tgt;
-    {
-        Stage st(c, 5, s);
-        if (int e = c->tab->bconv(&b, s)) return e;
-    }
     NttArgs f = ntt_args(c, c->conv, M.ntt, k_rows(c, M.ntt, K));
     f.epi = onto ? 2 : 1;
     f.ed = nullptr;  // the epilogue adds onto out's rows, which hold onto s2
@@ -699,6 +728,11 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     f.xstride = c->ct_words();
     f.es = M.ntt.es;
     f.ess = M.ntt.es + c->rows;
+    if (cc_on(c, CC_MDR)) return conv_then_rows(c, b, f, s, 5, 6, 1);
+    {
+        Stage st(c, 5, s);
+        if (int e = c->tab->bconv(&b, s)) return e;
+    }
     Stage st(c, 6, s);
     return c->tab->ntt_fwd(&f, s);
 }
@@ -725,11 +759,12 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s, int K = 1) {
     b.pr = c->pr;
     b.njobs = k_jobs(c, L->mu_bconv, K);
     b.max_tgt = L->mu_bconv.max_tgt;
+    NttArgs f = ntt_args(c, c->digits, L->mu_ntt, k_rows(c, L->mu_ntt, K));
+    if (cc_on(c, CC_MODUP)) return conv_then_rows(c, b, f, s, 1, 2);
     {
         Stage st(c, 1, s);
         if (int e = c->tab->bconv(&b, s)) return e;
     }
-    NttArgs f = ntt_args(c, c->digits, L->mu_ntt, k_rows(c, L->mu_ntt, K));
     Stage st(c, 2, s);
     return c->tab->ntt_fwd(&f, s);
 }
@@ -902,6 +937,7 @@ int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc
     b.pr = c->pr;
     b.njobs = 2 * m;
     b.max_tgt = top + 1;
+    if (cc_on(c, CC_MODDOWN)) return conv_then_rows(c, b, f, s, 5, 6);
     {
         Stage st(c, 5, s);
         if (int e = c->tab->bconv(&b, s)) return e;
@@ -1082,6 +1118,10 @@ pcx_ctx* pcx_ctx_new_k(uint32_t log_n, const uint64_t* primes, int nq, int kp, i
     c->md_fused = kp <= pch::MDC_MAX_KP ? 1 : 0;
     if (const char* e = getenv("PCX_MD_FUSED")) c->md_fused = c->md_fused && atoi(e) != 0;
     c->md_fused_init = c->md_fused;
+    if (const char* e = getenv("PCX_CC_FUSED")) c->cc_fused = atoi(e) & 7;
+    if (const char* e = getenv("PCX_CC_TPW")) c->cc_tpw = std::max(0, atoi(e));
+    if (const char* e = getenv("PCX_CC_NTG")) c->cc_ntg = std::max(1, std::min(3, atoi(e)));
+    if (const char* e = getenv("PCX_CC_NTGX")) c->cc_ntgx = std::max(1, std::min(3, atoi(e)));
     if (const char* e = getenv("PCX_MD_NTG")) c->md_ntg = std::max(1, std::min(pch::MDC_MAX_NTG, atoi(e)));
     const int R = c->rows;
     // prime constants and twiddles (crates/pc-gpu/src/context.rs:186-230)
@@ -1243,6 +1283,12 @@ int pcx_ctx_table_only(pcx_ctx* c, int on) {
     const int prev = c->table_only;
     c->table_only = on ? 1 : 0;
     c->md_fused = on ? 0 : c->md_fused_init;
+    return prev;
+}
+int pcx_ctx_conv_fusion(pcx_ctx* c, int mask) {
+    if (!c) return -1;
+    const int prev = c->cc_fused;
+    if (mask >= 0) c->cc_fused = mask & 7;
     return prev;
 }
 size_t pcx_ct_words(const pcx_ctx* c) { return c->ct_words(); }

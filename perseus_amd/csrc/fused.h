@@ -27,6 +27,14 @@ constexpr int MDC_MAX_NTG = 8;
 // 0, or -1 (bad arguments), -2 (kp outside 1..MDC_MAX_KP, ntg above MDC_MAX_NTG or logn outside 12..16), or a HIP
 // error
 int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s);
+// Any conversion plan (a's jobs: prescaled sources, fast or exact; every job's targets within a->max_tgt) fused into the
+// forward NTT's column pass: job k's target t gets the column pass of conv_t (prime tgt_prime) in dst row
+// dst_off + tgt_row, lazy words as the plain column pass leaves them. ntg (1..3): the targets whose sums a thread
+// carries at once; tpw: targets per workgroup (rounded up to a multiple of ntg); fw / fws: the forward twiddles by prime
+// id; lazy: NttArgs.lazy; exact: every job of a is exact (nonzero) or every job fast (0). 0, -1 (bad arguments), -2
+// (logn outside 12..16) or a HIP error.
+int conv_cols(int logn, const BconvArgs* a, const uint32_t* fw, const uint32_t* fws, int lazy, int exact, int ntg,
+              int tpw, pc_stream_t s);
 // The fused ModDown-rescale's preparation (moddown.hip mdr_prep_k): x rows top - 1, top += P onto; out rows
 // 0..top - 2 = onto s2 (k: [s2 | Shoup | P mod q | Shoup] by prime id, rows words each); both parts of K consecutive
 // ciphertexts (2 rows rows each)

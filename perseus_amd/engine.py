@@ -170,6 +170,11 @@ class Context:
     def ct_buf(self, count=1):
         return DevBuf(count * self.ct_words)
 
+    def conv_fusion(self, mask=-1):
+        """The conversions streamed into the NTT column pass (pcx_ctx_conv_fusion: bit 0 ModUp, 1 ModDown, 2 the
+        ModDown-rescale); mask < 0 only reads. Returns the previous mask."""
+        return int(LIB.pcx_ctx_conv_fusion(self.h, int(mask)))
+
     def table_only(self, on=True):
         """Issue every operation through the kernel table alone (pcx_ctx_table_only); returns the previous setting."""
         return bool(LIB.pcx_ctx_table_only(self.h, int(on)))

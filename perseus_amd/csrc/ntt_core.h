@@ -313,6 +313,15 @@ __device__ __forceinline__ void ld_d(const uint32_t* q, uint32_t (&v)[E]) {
         v[4 * k] = a.x, v[4 * k + 1] = a.y, v[4 * k + 2] = a.z, v[4 * k + 3] = a.w;
     }
 }
+// ld_d of words read once (streamed past the caches)
+__device__ __forceinline__ void ld_d_nt(const uint32_t* q, uint32_t (&v)[E]) {
+    typedef const __attribute__((address_space(1))) gu4* gq;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const gu4 a = __builtin_nontemporal_load((gq)(q + 64 * k));
+        v[4 * k] = a.x, v[4 * k + 1] = a.y, v[4 * k + 2] = a.z, v[4 * k + 3] = a.w;
+    }
+}
 __device__ __forceinline__ void st_d(uint32_t* q, const uint32_t (&v)[E]) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) *(uint4*)(q + 64 * k) = make_uint4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);

@@ -31,7 +31,7 @@ int md_conv_cols(int logn, const MdcArgs* a, pc_stream_t s);
 // forward NTT's column pass: job k's target t gets the column pass of conv_t (prime tgt_prime) in dst row
 // dst_off + tgt_row, lazy words as the plain column pass leaves them. ntg (1..3): the targets whose sums a thread
 // carries at once; tpw: targets per workgroup (rounded up to a multiple of ntg); fw / fws: the forward twiddles by prime
-// id; lazy: NttArgs.lazy; exact: every job of a is exact (nonzero) or every job fast (0). 0, -1 (bad arguments), -2
+// id; lazy: NttArgs.lazy; exact: nonzero when a's jobs include exact ones (0: every job taken as fast). 0, -1 (bad arguments), -2
 // (logn outside 12..16) or a HIP error.
 int conv_cols(int logn, const BconvArgs* a, const uint32_t* fw, const uint32_t* fws, int lazy, int exact, int ntg,
               int tpw, pc_stream_t s);

@@ -157,11 +157,11 @@ __global__ void __launch_bounds__(WG, EX ? (NTG == 1 ? 3 : 2) : (NTG == 3 ? 3 : 
 #pragma unroll
         for (int e = 0; e < E; ++e) y[e] = bs.ld(vy, ((row << LOGN) + (uint32_t)(G::TR * e * G::C)) * 4);
     };
-    // EX: the launch's jobs are exact (u (B mod t) subtracted), else fast
+    // EX: the launch's jobs may be exact (u (B mod t) subtracted where j.exact); without EX every job is taken as fast
     uint32_t u[EX ? E : 1];
     const double* rb = nullptr;
     const uint32_t* bmod = nullptr;
-    if (EX) {
+    if (EX && j.exact) {
         // rb[ns] doubles at the first 8-byte aligned word after M, then bmod[nt] (Bconv::build)
         size_t w = (size_t)j.pool_off + 3 * ns + 2 * nt + (size_t)ns * nt;
         if (w & 1) ++w;
@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(WG, EX ? (NTG == 1 ? 3 : 2) : (NTG == 3 ? 3 : 
             uint32_t x[E];
 #pragma unroll
             for (int e = 0; e < E; ++e) x[e] = rd(k)(acc[k][e]);
-            if constexpr (EX) {
+            if (EX && j.exact) {
                 // u <= ns: u (B mod t) as one Shoup product
                 const uint32_t b = bmod[tt + k], bs2 = (uint32_t)(((uint64_t)b << 32) / p);
 #pragma unroll

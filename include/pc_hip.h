@@ -898,6 +898,22 @@ pcx_keys* pcx_keys_new_banded(pcx_ctx* c, int nkeys, const uint64_t* galois, con
                               const uint32_t* const* b_host, int bits, int q_top, int* err);
 /* the highest ciphertext top the group serves (nq - 1 for full keys), -1 on NULL */
 int pcx_keys_q_top(const pcx_keys* k);
+/* The host sampler of key generation (perseus_amd/csrc/drbg.cpp): the DRBG of crates/pc-core/src/keys.rs:113-232
+ * (Prng: ChaCha20, a 64-bit block counter in state words 12..13, word 14 the stream id, word 15 "DRBG"; from_seed,
+ * next_u32, ksk_seed), the sparse ternary secret (keys.rs:245-262 sample_sparse_ternary: -1 when h > n) and the
+ * discrete Gaussian (keys.rs DiscreteGaussian: inversion of the CDF on |x| <= ceil(14 sigma), one uniform double then
+ * a sign word when x != 0; -1 for sigma outside (0, 1e6)). A host object, not thread-safe. */
+typedef struct pcx_drbg pcx_drbg;
+pcx_drbg* pcx_drbg_new(const uint32_t key[8], uint32_t stream);
+void pcx_drbg_free(pcx_drbg* g);
+uint32_t pcx_drbg_u32(pcx_drbg* g);
+int pcx_drbg_ksk_seed(pcx_drbg* g, uint32_t out[8]);
+int pcx_drbg_sparse_ternary(pcx_drbg* g, uint32_t n, uint32_t h, int8_t* out);
+int pcx_drbg_gaussian(pcx_drbg* g, double sigma, uint32_t n, int64_t* out);
+/* The host draws of nkeys switching keys in crates/pc-gpu/src/keygen.rs:193-210 (generate_with) order: per key its seed
+ * (8 words of g), the key of its per-digit error streams (8 more), then digit d's n errors from the stream (that key,
+ * d). seeds[nkeys][8], errors[nkeys][ndig][n]: pcx_keys_generate's inputs. */
+int pcx_keygen_draw(pcx_drbg* g, int nkeys, int ndig, uint32_t n, double sigma, uint32_t* seeds, int64_t* errors);
 /* Keys generated on the device (crates/pc-gpu/src/keygen.rs:172-262): secret s (ternary coefficients), per key the
  * seed of a and the Gaussian errors e[dnum][N] (signed coefficients, the same error on every limb of a digit). */
 pcx_keys* pcx_keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, const int8_t* secret,

@@ -78,6 +78,13 @@ _SIGS = {
     "pcx_keys_generate": (vp, [vp, C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_int8), u32p,
                                C.POINTER(C.c_int64), C.c_int, C.POINTER(C.c_int)]),
     "pcx_keys_free": (None, [vp]),
+    "pcx_drbg_new": (vp, [u32p, C.c_uint32]),
+    "pcx_drbg_free": (None, [vp]),
+    "pcx_drbg_u32": (C.c_uint32, [vp]),
+    "pcx_drbg_ksk_seed": (C.c_int, [vp, u32p]),
+    "pcx_drbg_sparse_ternary": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.POINTER(C.c_int8)]),
+    "pcx_drbg_gaussian": (C.c_int, [vp, C.c_double, C.c_uint32, C.POINTER(C.c_int64)]),
+    "pcx_keygen_draw": (C.c_int, [vp, C.c_int, C.c_int, C.c_uint32, C.c_double, u32p, C.POINTER(C.c_int64)]),
     "pcx_keys_download_b": (C.c_int, [vp, C.c_int, u32p]),
     "pcx_ct_words": (C.c_size_t, [vp]),
     "pcx_rotate": (C.c_int, [vp, vp, C.c_int, vp, C.c_int, vp, vp]),

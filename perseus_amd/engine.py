@@ -323,6 +323,49 @@ def band_rows(b, ctx, q_top):
     return np.ascontiguousarray(np.concatenate([b[:nd, : q_top + 1], b[:nd, ctx.nq:]], axis=1))
 
 
+class Drbg:
+    """The key-generation sampler's DRBG on the host (pcx_drbg_*: crates/pc-core/src/keys.rs:113-325 Prng with its
+    sparse ternary and discrete Gaussian samplers)."""
+
+    def __init__(self, key, stream=0):
+        k = np.ascontiguousarray(key, np.uint32).reshape(8)
+        self.h = LIB.pcx_drbg_new(k.ctypes.data_as(C.POINTER(C.c_uint32)), int(stream))
+        if not self.h:
+            raise HipError("pcx_drbg_new failed")
+
+    def u32(self):
+        return int(LIB.pcx_drbg_u32(self.h))
+
+    def ksk_seed(self):
+        out = np.zeros(8, np.uint32)
+        check(LIB.pcx_drbg_ksk_seed(self.h, out.ctypes.data_as(C.POINTER(C.c_uint32))), "drbg_ksk_seed")
+        return out
+
+    def sparse_ternary(self, n, h):
+        out = np.zeros(n, np.int8)
+        if LIB.pcx_drbg_sparse_ternary(self.h, n, h, out.ctypes.data_as(C.POINTER(C.c_int8))) != 0:
+            raise ValueError(f"sparse ternary: h={h} > n={n}")
+        return out
+
+    def gaussian(self, n, sigma=3.19):
+        out = np.zeros(n, np.int64)
+        check(LIB.pcx_drbg_gaussian(self.h, sigma, n, out.ctypes.data_as(C.POINTER(C.c_int64))), "drbg_gaussian")
+        return out
+
+    def keygen_draw(self, nkeys, ndig, n, sigma=3.19):
+        """(seeds[nkeys][8], errors[nkeys][ndig][n]) in crates/pc-gpu/src/keygen.rs:193-210 order (pcx_keygen_draw)"""
+        seeds = np.zeros((nkeys, 8), np.uint32)
+        errors = np.zeros((nkeys, ndig, n), np.int64)
+        check(LIB.pcx_keygen_draw(self.h, nkeys, ndig, n, sigma, seeds.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                  errors.ctypes.data_as(C.POINTER(C.c_int64))), "keygen_draw")
+        return seeds, errors
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            LIB.pcx_drbg_free(self.h)
+            self.h = None
+
+
 class Keys:
     """A key group: rotation keys by galois element, a regenerated from each seed, b stored dense or packed. relin:
     the relinearization key s^2 -> s (galois 1, generated from secret / errors)."""

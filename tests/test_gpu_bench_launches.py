@@ -36,15 +36,12 @@ def stream():
     return pa.Stream()
 
 
-def bench_keys_material(n, gals, dnum, seed):
-    """the bench's synthetic key material (bench.py main): a weight-192 ternary secret, clipped Gaussian errors,
-    ChaCha seeds"""
+def bench_keys_material(n, gals, dnum, seed, stream):
+    """the bench's key material (bench.py main): the weight-192 ternary secret and each key's seed and Gaussian errors
+    from the bench's DRBG streams (bench.draw_secret, bench.key_draws: the reference's samplers and keygen order)"""
     rng = np.random.default_rng(seed)
-    secret = np.zeros(n, np.int8)
-    pos = rng.choice(n, 192, replace=False)
-    secret[pos] = rng.choice([-1, 1], 192)
-    seeds = rng.integers(0, 1 << 32, (len(gals), 8), dtype=np.uint64).astype(np.uint32)
-    errors = np.clip(np.round(rng.normal(0, 3.19, (len(gals), dnum, n))), -45, 45).astype(np.int64)
+    secret = bench.draw_secret(pa, n)
+    seeds, errors = bench.key_draws(pa, stream, len(gals), dnum, n)
     return secret, seeds, errors, rng
 
 
@@ -57,7 +54,7 @@ def test_c3_hoisted_batch_of_the_bench(stream, layout):
     R = sum(1 for g in gals if g != 1)
     assert R == 26 and len(gals) == 27
     say(f"[bench launches] c3 hoisted batch, {R} key switches + the identity, keys {layout}")
-    secret, seeds, errors, rng = bench_keys_material(n, gals, ch.dnum, 2024)
+    secret, seeds, errors, rng = bench_keys_material(n, gals, ch.dnum, 2024, 1)
     ctx = pa.Context(ch, k_rot=R)
     bits = 0
     if layout != "dense":
@@ -90,7 +87,7 @@ def test_c4_score_batch_of_the_bench(stream):
     gals = [pow(5, r, 2 * n) for r in steps]
     say(f"[bench launches] c4 score_batch: {nc} ciphertexts, ladder radix 2^{attention.RADIX_BITS}, "
         f"{len(gals)} keys")
-    secret, seeds, errors, rng = bench_keys_material(n, gals, ch.dnum, 404)
+    secret, seeds, errors, rng = bench_keys_material(n, gals, ch.dnum, 404, 4)
     ctx = pa.Context(ch, k_rot=nc, k_max=nc)
     keys = pa.Keys(ctx, gals, seeds=seeds, secret=secret, errors=errors)
     cts = np.zeros((nc, 2, ch.rows, n), np.uint32)

@@ -242,6 +242,13 @@ def test_bconv_crt_invariant():
     B = 1
     for i in sid:
         B *= ps[i]
+    # the fast conversion's own value, in Python integers: sum_i [y_i (B / b_i)^-1]_{b_i} (B / b_i) mod t (an exact
+    # conversion, u = 0 everywhere, fails this)
+    for c in range(ctx.n):
+        y = [int(src[k][c]) * pow(B // ps[i], -1, ps[i]) % ps[i] for k, i in enumerate(sid)]
+        for k, t in enumerate(tid):
+            q = ps[t]
+            assert int(out[k][c]) == sum(yi * (B // ps[i]) for yi, i in zip(y, sid)) % q, (c, t)
     for c in range(0, ctx.n, 7):
         X = 0
         for k, i in enumerate(sid):

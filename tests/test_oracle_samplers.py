@@ -169,3 +169,45 @@ def test_sparse_ternary_from_raw_words(n, h):
     assert g.u32() == r.u32()
     if n <= 64 and h == n:
         assert collisions > 0, "a full-weight draw on a small ring collides"
+
+
+def test_rotation_key_draw_order_from_raw_words():
+    """or_rotation_key rebuilt from its parts in the order of crates/pc-gpu/src/keygen.rs:193-262 (generate_with, a
+    rotation key): the key's seed is the caller's DRBG's first 8 words and the per-digit error streams' key the next 8;
+    digit d's errors are the Gaussian draws of the stream (sub, d), reduced per prime and taken to the evaluation form;
+    a = KSKA(seed, d, p); b = e + [P s]_{digit d's own rows} - a sigma_{g^-1}(s). Each part is pinned by its own test
+    (the DRBG words, the Gaussian's draw order, the KSKA expander, the NTT, the automorphism); this pins their order and
+    the relation that joins them (a key drawn with seed and sub swapped, or its errors from one stream, fails)."""
+    logn, nq, kp, dnum = 10, 6, 2, 3
+    n = 1 << logn
+    ps = twin.descending_primes(30, 2 * n, nq + kp)
+    oc = twin.Ctx(logn, ps[:nq], ps[nq:], dnum)
+    key = [11, 22, 33, 44, 55, 66, 77, 88]
+    s = twin.Prng(key, 1).sparse_ternary(n, 64)
+    s_eval = oc.secret_eval(s)
+    gal = twin.rotation_galois(3, n)
+    seed, b = oc.rotation_key(twin.Prng(key, 5), s_eval, gal)
+    g = twin.Prng(key, 5)
+    words = np.array([g.u32() for _ in range(16)], np.uint32)
+    assert (seed == words[:8]).all()
+    sub = words[8:]
+    rows = oc.rows
+    e = np.zeros((dnum, rows, n), np.uint32)
+    for d in range(dnum):
+        ev = twin.Prng(sub, d).gaussian(n, 3.19)
+        assert np.abs(ev).max() < 64
+        for t in range(rows):
+            e[d, t] = np.mod(ev, ps[t]).astype(np.uint32)
+        e[d] = oc.ntt_fwd(e[d], list(range(rows)))
+    s_new = oc.automorph_rows(s_eval, twin.galois_inverse(gal, n))
+    P = 1
+    for x in ps[nq:]:
+        P *= x
+    for d in range(dnum):
+        for t in range(rows):
+            p = ps[t]
+            a = twin.kska_row(seed, d, p, n).astype(object)
+            want = e[d, t].astype(object) - a * s_new[t].astype(object)
+            if t < nq and oc.digit_of(t) == d:
+                want = want + (P % p) * s_eval[t].astype(object)
+            assert (b[d, t].astype(object) == want % p).all(), (d, t)

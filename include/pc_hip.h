@@ -923,6 +923,14 @@ void pcx_keys_free(pcx_keys* k);
  * when the keys are made and read by the dot instead of redrawing them; about 1-2% of b at 31-bit primes); 0 if none.
  * No counterpart in the reference, whose dot redraws in the kernel (as the table entry ks_dot_key does here). */
 size_t pcx_keys_patch_bytes(const pcx_keys* k);
+/* Keys with a resident dense `a` (crates/pc-gpu/src/ks.rs:346-347, 408-411, 1259-1262 set_regen_digits: a group that stores `a` regenerates its
+ * digits below regen_digits and reads the rest, KeyTab.nregen): the first call expands every key's `a` on the device
+ * into [dnum][nq + kp][N] words per key (pcx_keys_resident_bytes); later calls only change regen_digits (>= dnum:
+ * every digit regenerated again). Memory for VALU work: each resident digit trades one ChaCha12 block per 16 slots for
+ * 64 bytes of HBM reads. Full-layout groups only (-1 for a band or a negative count); s: the expansion's stream
+ * (synchronised before returning). */
+int pcx_keys_resident_a(pcx_keys* k, int regen_digits, pc_stream_t s);
+size_t pcx_keys_resident_bytes(const pcx_keys* k);
 /* download key r's stored b as dense words [ndig][srows][N] (full keys: [dnum][nq + kp][N]) */
 int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host);
 

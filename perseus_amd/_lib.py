@@ -78,6 +78,8 @@ _SIGS = {
     "pcx_keys_generate": (vp, [vp, C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_int8), u32p,
                                C.POINTER(C.c_int64), C.c_int, C.POINTER(C.c_int)]),
     "pcx_keys_free": (None, [vp]),
+    "pcx_keys_resident_a": (C.c_int, [vp, C.c_int, vp]),
+    "pcx_keys_resident_bytes": (C.c_size_t, [vp]),
     "pcx_drbg_new": (vp, [u32p, C.c_uint32]),
     "pcx_drbg_free": (None, [vp]),
     "pcx_drbg_u32": (C.c_uint32, [vp]),

@@ -312,6 +312,11 @@ struct pcx_keys {
     // the KSKA retry-value table (dense keys): offsets [key][digit][row][chunk] + 1, values
     uint32_t *pidx = nullptr, *pval = nullptr;
     size_t patch_words = 0;
+    std::vector<const uint32_t*> seed_ptr;  // device seed per key (host copy of `seed`)
+    // resident dense `a` (pcx_keys_resident_a; crates/pc-gpu/src/ks.rs:346-347, 408-411 regen_digits): digits < regen are
+    // regenerated, the rest read from ka[r] [dnum][rows][N] (prime-id rows)
+    const void** ka = nullptr;
+    int regen = 1 << 30;
 };
 
 namespace {
@@ -814,6 +819,12 @@ int dot(pcx_ctx* c, pcx_keys* k, int r0, int m, const void* ct, int top, void* e
     t.q_top = k->q_top;
     t.srows = k->srows;
     t.nregen = k->ndig;
+    if (k->ka && k->regen < L->ndig) {
+        // the keys' resident `a` for digits >= regen
+        t.nregen = k->regen;
+        a.ka = k->ka + r0;
+        a.key_digit_stride = (uint64_t)c->rows * c->n;
+    }
     Stage st(c, 3, s);
     if (k->pval && !sum && !c->table_only) {
         // the retry values from the key group's table (no redraw in the dot)
@@ -1364,6 +1375,7 @@ static pcx_keys* keys_new(pcx_ctx* c, int nkeys, const uint64_t* galois, const u
     }
     k->kb = (const void**)k->dev.upload(kb);
     k->seed = (const uint32_t**)k->dev.upload(sd);
+    k->seed_ptr = sd;
     if (!k->dev.err && k->q_top < 0) {
         // the retry-value table is indexed by prime id: full-layout groups only (a band redraws in the dot)
         if (int e = build_patches(c, k)) k->dev.err = e;
@@ -1490,6 +1502,7 @@ static pcx_keys* keys_generate(pcx_ctx* c, int nkeys, const uint64_t* galois, co
     if (!rc) {
         k->kb = (const void**)k->dev.upload(kb);
         k->seed = (const uint32_t**)k->dev.upload(sd);
+        k->seed_ptr = sd;
         if (k->dev.err) rc = k->dev.err;
     }
     if (!rc) rc = build_patches(c, k);
@@ -1516,6 +1529,42 @@ pcx_keys* pcx_keys_relin(pcx_ctx* c, const int8_t* secret, const uint32_t* seed,
 void pcx_keys_free(pcx_keys* k) { delete k; }
 
 size_t pcx_keys_patch_bytes(const pcx_keys* k) { return k ? k->patch_words * 4 : 0; }
+
+int pcx_keys_resident_a(pcx_keys* k, int regen_digits, pc_stream_t s) {
+    if (!k || regen_digits < 0 || k->q_top >= 0 || (int)k->seed_ptr.size() != k->nkeys) return -1;
+    pcx_ctx* c = k->c;
+    if (!k->ka && regen_digits < c->dnum) {
+        // every key's a expanded once: [dnum][rows][N] words, prime-id rows (the table's ksk_expand)
+        std::vector<int32_t> ids(c->rows);
+        for (int i = 0; i < c->rows; ++i) ids[i] = i;
+        const int32_t* dids = k->dev.upload(ids);
+        std::vector<const void*> ka;
+        for (int r = 0; r < k->nkeys && !k->dev.err; ++r) {
+            void* p = k->dev.alloc((size_t)c->dnum * c->rows * c->n * 4);
+            if (!p) break;
+            KskExpandArgs e;
+            memset(&e, 0, sizeof e);
+            e.out = p;
+            e.seed = k->seed_ptr[r];
+            e.prime_ids = dids;
+            e.pr = c->pr;
+            e.nmod = c->rows;
+            e.dnum = c->dnum;
+            e.d0 = 0;
+            if (int rc = c->tab->ksk_expand(&e, s)) return rc;
+            ka.push_back(p);
+        }
+        if (k->dev.err) return k->dev.err;
+        k->ka = (const void**)k->dev.upload(ka);
+        if (!k->ka) return k->dev.err ? k->dev.err : -1;
+        if (int rc = pc_hip_stream_sync(s)) return rc;
+    }
+    k->regen = regen_digits;
+    return 0;
+}
+size_t pcx_keys_resident_bytes(const pcx_keys* k) {
+    return k && k->ka ? (size_t)k->nkeys * k->c->dnum * k->c->rows * k->c->n * 4 : 0;
+}
 
 int pcx_keys_download_b(pcx_keys* k, int r, uint32_t* b_host) {
     if (!k || r < 0 || r >= k->nkeys) return -1;

@@ -395,7 +395,9 @@ __device__ __forceinline__ void ldpk16(gptr row, uint32_t s0, uint32_t (&out)[DS
 // PATCH: the retry values come from the key group's table (P) instead of the wave's redraw. PK: key b bit-packed at
 // PK bits (0: dense words). F: c0 mode 3 handled (the one-wave form; its second-part words held through the ChaCha
 // blocks)
-template <int NDIG, bool MU2, bool PATCH, int PK, bool F>
+// RES: digits >= KeyTab.nregen read the key's resident dense `a` (KsArgs.ka[r] + d key_digit_stride, prime-id rows:
+// the reference's keys with a stored `a`, crates/pc-gpu/src/ks.rs:1259-1262), the others regenerated
+template <int NDIG, bool MU2, bool PATCH, int PK, bool F, bool RES = false>
 __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, const Expander& ex, int r,
                                              const PatchTab& P) {
     const KsArgs& A = *C.A;
@@ -413,12 +415,18 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     wave_sync();
     // PATCH: this chunk's retry values of each digit, loaded now (two per lane) and stored to the queue after the
     // ChaCha blocks; a digit whose list would overflow the queue redraws in the lane
+    const int nreg = RES ? T.nregen : NDIG;
     uint32_t poff[PATCH ? NDIG : 1], pn[PATCH ? NDIG : 1], pv[PATCH ? NDIG : 1][2];
     if constexpr (PATCH) {
         const uint32_t chunks = (1u << C.logn) / DCH;
         uint32_t tot = 0;
 #pragma unroll
         for (int d = 0; d < NDIG; ++d) {
+            if (RES && d >= nreg) {
+                // a resident digit: no retry values
+                poff[d] = pn[d] = pv[d][0] = pv[d][1] = 0;
+                continue;
+            }
             const size_t ix = (((size_t)r * P.ndig + d) * P.rows + C.slot) * chunks + C.chunk0 / DCH;
             poff[d] = P.idx[ix];
             pn[d] = P.idx[ix + 1] - poff[d];
@@ -438,41 +446,46 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 #pragma unroll
     for (int d = 0; d < NDIG; ++d) {
         uint32_t a[DS];
-        chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
         uint32_t rej = 0;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
         uint32_t base = 0;
-        if (PATCH && pn[d] != 0xFFFFFFFFu) {
-            // the table lists this chunk's rejected words in slot order: this lane's come after the lower lanes'
-            base = pbase + lane_prefix(__builtin_popcount(rej), lane);
-            pbase += pn[d];
-        } else if (rej) {
-            const uint32_t cnt = __builtin_popcount(rej);
-            base = PATCH ? (uint32_t)FQCAP : atomicAdd(&W.qn, cnt);
-            if (!PATCH && base + cnt <= (uint32_t)FQCAP) {
-                uint32_t m = rej, i = base;
-#pragma unroll 1
-                while (m) {
-                    const int j = __builtin_ctz(m);
-                    m &= m - 1;
-                    W.q[i++] = (uint32_t)d << 16 | (lane * DS + j);
-                }
-            } else {
-                // the queue is full (rejection rates far above any prime of this path's): redraw in the lane
-                uint32_t m = rej;
-                while (m) {
-                    const int j = __builtin_ctz(m);
-                    m &= m - 1;
-                    uint32_t v = 0;
-                    for (int tt = 1; tt < KSK_T_MAX; ++tt) {
-                        v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * C.n16, (uint32_t)d, p, TAG_KSKA, j);
-                        if (v < ex.mp) break;
-                    }
+        if (RES && d >= nreg) {
+            // canonical words: kska_value leaves them as they are
+            ld16(as_global(((const void* const*)A.ka)[r]) + (size_t)d * A.key_digit_stride + C.trow + s0, a);
+        } else {
+            chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
 #pragma unroll
-                    for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? v : a[jj];
+            for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
+            if (PATCH && pn[d] != 0xFFFFFFFFu) {
+                // the table lists this chunk's rejected words in slot order: this lane's come after the lower lanes'
+                base = pbase + lane_prefix(__builtin_popcount(rej), lane);
+                pbase += pn[d];
+            } else if (rej) {
+                const uint32_t cnt = __builtin_popcount(rej);
+                base = PATCH ? (uint32_t)FQCAP : atomicAdd(&W.qn, cnt);
+                if (!PATCH && base + cnt <= (uint32_t)FQCAP) {
+                    uint32_t m = rej, i = base;
+#pragma unroll 1
+                    while (m) {
+                        const int j = __builtin_ctz(m);
+                        m &= m - 1;
+                        W.q[i++] = (uint32_t)d << 16 | (lane * DS + j);
+                    }
+                } else {
+                    // the queue is full (rejection rates far above any prime of this path's): redraw in the lane
+                    uint32_t m = rej;
+                    while (m) {
+                        const int j = __builtin_ctz(m);
+                        m &= m - 1;
+                        uint32_t v = 0;
+                        for (int tt = 1; tt < KSK_T_MAX; ++tt) {
+                            v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * C.n16, (uint32_t)d, p, TAG_KSKA, j);
+                            if (v < ex.mp) break;
+                        }
+#pragma unroll
+                        for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? v : a[jj];
+                    }
+                    rej = 0;
                 }
-                rej = 0;
             }
         }
         rejd[d] = rej;
@@ -598,7 +611,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
 }
 
 // NW: waves per workgroup (KW: staged D and c0, one key per wave; 1: read from memory)
-template <int NDIG, bool PATCH, int NW, int PK = 0>
+template <int NDIG, bool PATCH, int NW, int PK = 0, bool RES = false>
 __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, PatchTab P, int logn) {
     static_assert(NDIG >= 1 && NDIG <= MAXD, "digits staged in LDS");
     static_assert(NW == KW || NW == 1, "staged (KW waves) or direct (one wave)");
@@ -660,20 +673,20 @@ __global__ void __launch_bounds__(DBX * NW, 3) dot_fast(KsArgs A, KeyTab T, Patc
         C.c0 = C.m0 ? c0row : nullptr;
     }
     if (ex.mu == 2) {
-        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH, PK, NW == 1>(C, red, ex, r, P);
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, true, PATCH, PK, NW == 1, RES>(C, red, ex, r, P);
     } else {
-        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH, PK, NW == 1>(C, red, ex, r, P);
+        for (int r = r_lo + wv; r < r_hi; r += NW) dot_fast_key<NDIG, false, PATCH, PK, NW == 1, RES>(C, red, ex, r, P);
     }
 }
 
 // the fast dot's launch: one-wave direct workgroups when the launch has fewer keys than a staged workgroup's waves
-template <int NDIG, bool PATCH, int PK = 0>
+template <int NDIG, bool PATCH, int PK = 0, bool RES = false>
 void dot_fast_launch(dim3 grid, const KsArgs& a, const KeyTab& key, const PatchTab& P, int logn, hipStream_t st) {
     if (P.diag || a.R < KW) {
         grid.z = P.diag ? a.K : a.R * a.K;
-        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1, PK>), grid, dim3(DBX), 0, st, a, key, P, logn);
+        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, 1, PK, RES>), grid, dim3(DBX), 0, st, a, key, P, logn);
     } else {
-        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW, PK>), grid, dim3(KBX), 0, st, a, key, P, logn);
+        hipLaunchKernelGGL((dot_fast<NDIG, PATCH, KW, PK, RES>), grid, dim3(KBX), 0, st, a, key, P, logn);
     }
 }
 // the fast dot's packed-b widths (the reference's PackedSeeded keys store b at the widest prime's bits)
@@ -721,8 +734,11 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     if (!g || !P || !P->idx || !P->val) return -1;
     const KsArgs& a = g->ks;
     const KeyTab& key = g->key;
-    if (a.K < 1 || a.K > (P->diag ? 8 : 4) || key.bits != 0 || key.nregen < a.ndig || a.ndig < 1 || a.ndig > 3 ||
-        a.ndig > P->ndig || key.q_top >= 0 || key.srows != P->rows || (P->diag && (a.R != a.K || (a.c0_mode & 3) == 3)))
+    // digits >= nregen: the keys' resident dense `a` (full layout)
+    const bool res = key.nregen < a.ndig;
+    if (a.K < 1 || a.K > (P->diag ? 8 : 4) || key.bits != 0 || key.nregen < 0 || a.ndig < 1 || a.ndig > 3 ||
+        a.ndig > P->ndig || key.q_top >= 0 || key.srows != P->rows || (P->diag && (a.R != a.K || (a.c0_mode & 3) == 3)) ||
+        (res && (!a.ka || a.key_digit_stride < (uint64_t)key.srows << LOGN)))
         return -2;
     if (a.nrows < 0 || a.R < 0) return -1;
     if (a.nrows == 0 || a.R == 0) return 0;
@@ -736,6 +752,12 @@ int dot_patched(const KsKeyArgs* g, const PatchTab* P, pc_stream_t s) {
     while (groups < a.R && (long)chunks * a.nrows * groups * a.K < 2048) ++groups;
     const dim3 grid(chunks, a.nrows, groups * a.K);
     hipStream_t st = (hipStream_t)s;
+    if (res) {
+        if (a.ndig == 1) dot_fast_launch<1, true, 0, true>(grid, a, key, *P, LOGN, st);
+        if (a.ndig == 2) dot_fast_launch<2, true, 0, true>(grid, a, key, *P, LOGN, st);
+        if (a.ndig == 3) dot_fast_launch<3, true, 0, true>(grid, a, key, *P, LOGN, st);
+        return launch_rc();
+    }
     if (a.ndig == 1) dot_fast_launch<1, true>(grid, a, key, *P, LOGN, st);
     if (a.ndig == 2) dot_fast_launch<2, true>(grid, a, key, *P, LOGN, st);
     if (a.ndig == 3) dot_fast_launch<3, true>(grid, a, key, *P, LOGN, st);

@@ -408,6 +408,13 @@ class Keys:
         self._keep = None
         self.bits = bits
 
+    def resident_a(self, regen_digits, stream):
+        """Store every key's `a` on the device and regenerate only digits < regen_digits (pcx_keys_resident_a)."""
+        check(LIB.pcx_keys_resident_a(self.h, int(regen_digits), stream.h), "keys_resident_a")
+
+    def resident_bytes(self):
+        return int(LIB.pcx_keys_resident_bytes(self.h))
+
     def patch_bytes(self):
         """Bytes of the group's KSKA retry-value table (0 when the dot redraws in the kernel)."""
         return int(LIB.pcx_keys_patch_bytes(self.h))

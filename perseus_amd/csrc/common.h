@@ -173,6 +173,12 @@ typedef const __attribute__((address_space(1))) uint32_t* gptr;
 typedef uint32_t gu4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gu4a4 __attribute__((ext_vector_type(4), aligned(4)));
 __device__ __forceinline__ gptr as_global(const void* p) { return (gptr)p; }
+// A read of read-only memory at an address uniform over the wave, through the constant address space: a scalar load
+// (kept by the scalar cache, counted by lgkmcnt, not by the vector memory counter)
+template <class T>
+__device__ __forceinline__ T sload(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
 __device__ __forceinline__ void ld16(gptr p, uint32_t (&v)[16]) {
     const __attribute__((address_space(1))) gu4* q = (const __attribute__((address_space(1))) gu4*)p;
 #pragma unroll

@@ -135,7 +135,7 @@ struct KeyRow {
     int bits;
     gptr ka;
     uint64_t astride;
-    gptr seed;
+    const uint32_t* seed;  // read with scalar loads (uniform, read-only)
 };
 
 __device__ __forceinline__ Row make_row(const PrimeConst& q, int logn, uint32_t* lds, int nreg) {
@@ -151,10 +151,10 @@ __device__ __forceinline__ Row make_row(const PrimeConst& q, int logn, uint32_t*
 }
 
 // 1. The KSKA words of digits d < nreg at the source chunk [sc, sc + 512) into la[d][apad(s - sc)].
-__device__ __forceinline__ void stage_a(const Row& R, gptr sp, uint32_t sc, int lane) {
+__device__ __forceinline__ void stage_a(const Row& R, const uint32_t* sp, uint32_t sc, int lane) {
     uint32_t seed[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) seed[k] = sp[k];
+    for (int k = 0; k < 8; ++k) seed[k] = sload(sp + k);
     if (lane == 0) *R.lqn = 0;
     wave_sync();
     // item = digit d, block b (slots sc + 16 b ..), one per lane and round
@@ -355,22 +355,22 @@ __global__ void __launch_bounds__(CW, 3) cts_k(CtsRegenArgs RA, int logn, int j0
             }
         } else {
             // baby i: sources s = automorph_slot(g, o) of the chunk's outputs, scattered back by g^-1
-            const uint32_t g = A.kinv[i - 1];
+            const uint32_t g = sload(A.kinv + (i - 1));
             KeyRow K;
             if (REGEN) {
-                K.kb = as_global(T.kb[i - 1]) + (size_t)slot * T.row_words;
+                K.kb = as_global(sload(T.kb + (i - 1))) + (size_t)slot * T.row_words;
                 K.bstride = (uint64_t)T.srows * T.row_words;
                 K.bwords = T.row_words;
                 K.bits = T.bits;
-                K.seed = R.nreg > 0 ? as_global(T.seed[i - 1]) : K.kb;  // (K.kb: never read)
+                K.seed = R.nreg > 0 ? sload(T.seed + (i - 1)) : nullptr;
             } else {
-                K.kb = as_global(A.kb[i - 1]) + roff;
+                K.kb = as_global(sload(A.kb + (i - 1))) + roff;
                 K.bstride = A.key_digit_stride;
                 K.bwords = 0;
                 K.bits = 0;
-                K.seed = K.kb;  // no regenerated digit: never read
+                K.seed = nullptr;  // no regenerated digit: never read
             }
-            K.ka = R.nreg < A.ndig ? as_global(A.ka[i - 1]) + roff : K.kb;  // (K.kb: never read)
+            K.ka = R.nreg < A.ndig ? as_global(sload(A.ka + (i - 1))) + roff : K.kb;  // (K.kb: never read)
             K.astride = A.key_digit_stride;
             rotation<WIDE>(R, K, g, inv_odd(g) & R.mask2n, oc0, lane, w0, w1);
         }
@@ -503,14 +503,14 @@ __global__ void __launch_bounds__(CW, 3) ksum_k(KsKeyArgs G, int logn) {
     for (int k = 0; k < CS; ++k) acc0[k] = acc1[k] = 0;
     for (int r = 0; r < A.R; ++r) {
         KeyRow K;
-        K.kb = as_global(T.kb[r]) + (size_t)slot * T.row_words;
+        K.kb = as_global(sload(T.kb + r)) + (size_t)slot * T.row_words;
         K.bstride = (uint64_t)T.srows * T.row_words;
         K.bwords = T.row_words;
         K.bits = T.bits;
-        K.seed = R.nreg > 0 ? as_global(T.seed[r]) : K.kb;                 // (K.kb: never read)
-        K.ka = R.nreg < A.ndig ? as_global(A.ka[r]) + roff : K.kb;         // (K.kb: never read)
+        K.seed = R.nreg > 0 ? sload(T.seed + r) : nullptr;
+        K.ka = R.nreg < A.ndig ? as_global(sload(A.ka + r)) + roff : K.kb;  // (K.kb: never read)
         K.astride = A.key_digit_stride;
-        const uint32_t kx = A.autok[r] & R.mask2n;  // the scatter exponent; its inverse gathers
+        const uint32_t kx = sload(A.autok + r) & R.mask2n;  // the scatter exponent; its inverse gathers
         uint32_t w0[CS], w1[CS];
         rotation<WIDE>(R, K, inv_odd(kx) & R.mask2n, kx, oc0, lane, w0, w1);
 #pragma unroll
@@ -570,9 +570,9 @@ __global__ void __launch_bounds__(CW, 3) regen_k(KsRegenArgs G, int logn) {
     }
     K.ka = K.kb;  // every digit regenerates: never read
     K.astride = 0;
-    K.seed = as_global(G.seed);
+    K.seed = G.seed;
     const uint32_t s0 = blockIdx.x * CCH + lane * CS;  // no automorphism: source and output slots coincide
-    if (R.nreg > 0) stage_a(R, as_global(G.seed), blockIdx.x * CCH, lane);
+    if (R.nreg > 0) stage_a(R, G.seed, blockIdx.x * CCH, lane);
     for (int c = 0; c < A.K; ++c) {
         R.c1 = (const uint32_t*)A.c1 + c * A.ct_stride + roff;
         R.mu = (const uint32_t*)A.modup + c * A.mu_ct_stride + roff;

@@ -405,21 +405,31 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
     FastWave& W = *C.W;
     const int lane = C.lane, lp = C.lp;
     const uint32_t p = C.p, s0 = C.s0;
-    const gptr kb = as_global(T.kb[r]) + (size_t)C.slot * T.row_words + (PK ? 0 : s0);
+    // the key's tables (row pointer, seed, automorphism exponent, retry-list offsets) are uniform over the wave and
+    // read-only: scalar loads, whose waits do not include the vector memory counter (the previous key's stores)
+    const gptr kb = as_global(sload(T.kb + r)) + (size_t)C.slot * T.row_words + (PK ? 0 : s0);
     const size_t dstride = (size_t)T.srows * T.row_words;
     uint32_t seed[8];
-    const gptr sp = as_global(T.seed[r]);
+    const uint32_t* sp = sload(T.seed + r);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) seed[i] = sp[i];
+    for (int i = 0; i < 8; ++i) seed[i] = sload(sp + i);
+    const uint32_t kexp = sload(A.autok + r);
     if (lane == 0) W.qn = 0;
     wave_sync();
     // PATCH: this chunk's retry values of each digit, loaded now (two per lane) and stored to the queue after the
-    // ChaCha blocks; a digit whose list would overflow the queue redraws in the lane
+    // ChaCha blocks; a digit whose list would overflow the queue is read from the table when the words are patched
     const int nreg = RES ? T.nregen : NDIG;
     uint32_t poff[PATCH ? NDIG : 1], pn[PATCH ? NDIG : 1], pv[PATCH ? NDIG : 1][2];
     if constexpr (PATCH) {
         const uint32_t chunks = (1u << C.logn) / DCH;
-        uint32_t tot = 0;
+        uint32_t tot = 0, i1[NDIG];
+        // every digit's offsets first (one wait for all)
+#pragma unroll
+        for (int d = 0; d < NDIG; ++d) {
+            const size_t ix = (((size_t)r * P.ndig + d) * P.rows + C.slot) * chunks + C.chunk0 / DCH;
+            poff[d] = sload(P.idx + ix);
+            i1[d] = sload(P.idx + ix + 1);
+        }
 #pragma unroll
         for (int d = 0; d < NDIG; ++d) {
             if (RES && d >= nreg) {
@@ -427,10 +437,8 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
                 poff[d] = pn[d] = pv[d][0] = pv[d][1] = 0;
                 continue;
             }
-            const size_t ix = (((size_t)r * P.ndig + d) * P.rows + C.slot) * chunks + C.chunk0 / DCH;
-            poff[d] = P.idx[ix];
-            pn[d] = P.idx[ix + 1] - poff[d];
-            if (tot + pn[d] > (uint32_t)FQCAP) pn[d] = 0xFFFFFFFFu;  // redrawn in the lane
+            pn[d] = i1[d] - poff[d];
+            if (tot + pn[d] > (uint32_t)FQCAP) pn[d] = 0xFFFFFFFFu;  // read from memory when patched
             else tot += pn[d];
             const bool ok = pn[d] != 0xFFFFFFFFu;
             pv[d][0] = ok && (uint32_t)lane < pn[d] ? P.val[poff[d] + lane] : 0;
@@ -453,16 +461,34 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
             ld16(as_global(((const void* const*)A.ka)[r]) + (size_t)d * A.key_digit_stride + C.trow + s0, a);
         } else {
             chacha12(seed, s0 >> 4, (uint32_t)d, p, TAG_KSKA, a);
+            if constexpr (MU2) {
+                // reduced at once: z = min(v, v - p) is v mod p for v < 2p, and z >= p exactly when v >= 2p (rejected:
+                // 0 here, its bit in rej, built by shifts)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
-            if (PATCH && pn[d] != 0xFFFFFFFFu) {
-                // the table lists this chunk's rejected words in slot order: this lane's come after the lower lanes'
-                base = pbase + lane_prefix(__builtin_popcount(rej), lane);
-                pbase += pn[d];
+                for (int j = 15; j >= 0; --j) {
+                    const uint32_t z = min(a[j], a[j] - p);
+                    const bool bad = z >= p;
+                    rej = rej << 1 | (uint32_t)bad;
+                    a[j] = bad ? 0u : z;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) rej |= (uint32_t)(a[j] >= ex.mp) << j;
+            }
+            if constexpr (PATCH) {
+                // the table lists this chunk's rejected words in slot order: this lane's come after the lower lanes'.
+                // A list that does not fit the queue is read from the table in memory (top bit of base)
+                const uint32_t pre = lane_prefix(__builtin_popcount(rej), lane);
+                if (pn[d] != 0xFFFFFFFFu) {
+                    base = pbase + pre;
+                    pbase += pn[d];
+                } else {
+                    base = poff[d] + pre;
+                }
             } else if (rej) {
                 const uint32_t cnt = __builtin_popcount(rej);
-                base = PATCH ? (uint32_t)FQCAP : atomicAdd(&W.qn, cnt);
-                if (!PATCH && base + cnt <= (uint32_t)FQCAP) {
+                base = atomicAdd(&W.qn, cnt);
+                if (base + cnt <= (uint32_t)FQCAP) {
                     uint32_t m = rej, i = base;
 #pragma unroll 1
                     while (m) {
@@ -481,8 +507,9 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
                             v = chacha12_word(seed, (s0 >> 4) + (uint32_t)tt * C.n16, (uint32_t)d, p, TAG_KSKA, j);
                             if (v < ex.mp) break;
                         }
+                        const uint32_t nv = MU2 ? kska_value<true>(ex, v) : v;
 #pragma unroll
-                        for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? v : a[jj];
+                        for (int jj = 0; jj < 16; ++jj) a[jj] = jj == j ? nv : a[jj];
                     }
                     rej = 0;
                 }
@@ -493,7 +520,7 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         uint32_t x[DS];
         ld16(C.D[d] + lp, x);
 #pragma unroll
-        for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * ((rej >> k) & 1 ? 0 : kska_value<MU2>(ex, a[k]));
+        for (int k = 0; k < DS; ++k) acc[k] += (uint64_t)x[k] * (MU2 ? a[k] : (rej >> k) & 1 ? 0 : ex.red(a[k]));
         // materialise the sums here: this digit's a words die before the next block is computed
 #pragma unroll
         for (int k = 0; k < DS; ++k) asm volatile("" : "+v"(acc[k]));
@@ -538,7 +565,6 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         }
         W.q[i] = ex.red(v);
     }
-    const uint32_t kexp = A.autok[r];
     uint32_t* o0 = (uint32_t*)A.out0 + C.oct + r * A.out_rot_stride + C.trow;
     uint32_t* o1 = (uint32_t*)A.out1 + C.oct + r * A.out_rot_stride + C.trow;
     // W_k = top 10 bits of (cb + brev4(k) step) mod 2N; step's low logn - 3 bits are zero, so the sum's top bits are
@@ -574,15 +600,23 @@ __device__ __forceinline__ void dot_fast_key(const FastCtx& C, const Red& red, c
         }
 #pragma unroll
         for (int d = 0; d < NDIG; ++d) {
-            uint32_t m = rejd[d], i = based[d];
+            // the values from the queue in LDS, or (a list too long for it: uniform over the wave) from the table in
+            // memory; two loops, so that the LDS one waits for no memory load
+            auto patch = [&](auto value) {
+                uint32_t m = rejd[d], i = based[d];
 #pragma unroll 1
-            while (m) {
-                const uint32_t j = __builtin_ctz(m);
-                m &= m - 1;
-                const uint32_t add = red.mul(C.D[d][lp + j], W.q[i++]);
-                const uint32_t o = scat_addr((cbh + brev4(j) * sth) & (DCH - 1));
-                buf[o] = addm(buf[o], add, p);
-            }
+                while (m) {
+                    const uint32_t j = __builtin_ctz(m);
+                    m &= m - 1;
+                    const uint32_t add = red.mul(C.D[d][lp + j], value(i++));
+                    const uint32_t o = scat_addr((cbh + brev4(j) * sth) & (DCH - 1));
+                    buf[o] = addm(buf[o], add, p);
+                }
+            };
+            if (PATCH && __builtin_amdgcn_readfirstlane(pn[PATCH ? d : 0]) == 0xFFFFFFFFu)
+                patch([&](uint32_t i) { return P.val[i]; });
+            else
+                patch([&](uint32_t i) { return W.q[i]; });
         }
         emit(v, o1);
     }

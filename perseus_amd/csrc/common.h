@@ -43,6 +43,8 @@ struct Red {
         : p((uint32_t)c.p), r32((uint32_t)c.split), r32s((uint32_t)(c.split >> 32)), m((uint32_t)(c.mu_lo >> 32)) {}
     __device__ __forceinline__ Red(uint32_t p_, uint32_t r32_, uint32_t r32s_, uint32_t m_)
         : p(p_), r32(r32_), r32s(r32s_), m(m_) {}
+    // the constants of prime table entry i read with scalar loads (i uniform over the wave)
+    __device__ __forceinline__ static Red scalar(const PrimeConst* pr, uint32_t i);
     __device__ __forceinline__ uint32_t operator()(uint64_t x) const {
         const uint32_t hi = (uint32_t)(x >> 32), lo = (uint32_t)x;
         uint32_t a = shoup(hi, r32, r32s, p);
@@ -178,6 +180,10 @@ __device__ __forceinline__ gptr as_global(const void* p) { return (gptr)p; }
 template <class T>
 __device__ __forceinline__ T sload(const T* p) {
     return *(const __attribute__((address_space(4))) T*)p;
+}
+__device__ __forceinline__ Red Red::scalar(const PrimeConst* pr, uint32_t i) {
+    const uint64_t p = sload(&pr[i].p), split = sload(&pr[i].split), mu = sload(&pr[i].mu_lo);
+    return Red((uint32_t)p, (uint32_t)split, (uint32_t)(split >> 32), (uint32_t)(mu >> 32));
 }
 __device__ __forceinline__ void ld16(gptr p, uint32_t (&v)[16]) {
     const __attribute__((address_space(1))) gu4* q = (const __attribute__((address_space(1))) gu4*)p;

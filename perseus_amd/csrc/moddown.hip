@@ -49,12 +49,14 @@ __global__ void __launch_bounds__(WG) md_conv_cols_k(MdcArgs A) {
     __syncthreads();
     auto base = [](int h) { return (uint32_t)(G::R / (2 * h)); };
     for (int t = t0; t < t1; ++t) {
-        const Red red(A.pr[t]);
+        // the target's constants through the scalar cache: a vector load here would wait for the previous target's
+        // stores
+        const Red red = Red::scalar(A.pr, t);
         const uint32_t p = red.p, p2 = 2 * p;
         const uint32_t r64 = shoup(red.r32, red.r32, red.r32s, p);  // 2^64 mod q_t
         uint32_t m[KP];
 #pragma unroll
-        for (int j = 0; j < KP; ++j) m[j] = A.mt[j * A.nq + t];
+        for (int j = 0; j < KP; ++j) m[j] = sload(A.mt + j * A.nq + t);
         // sum_j y_j M[j][t]: products below 2^62, three to a 64-bit sum; two sums add to 65 bits, the carry folded in
         // as 2^64 mod q_t, so one reduction per word
         uint32_t x[E];
@@ -142,7 +144,7 @@ __global__ void __launch_bounds__(WG, EX ? (NTG == 1 ? 3 : 2) : (NTG == 3 ? 3 : 
     uint32_t smax = 0, maxsp = 0;
     for (int i = 0; i < ns; ++i) {
         smax = max(smax, pool[i]);
-        maxsp = max(maxsp, (uint32_t)A.pr[pool[ns + i]].p);
+        maxsp = max(maxsp, (uint32_t)sload(&A.pr[pool[ns + i]].p));
     }
     uint32_t dmax = 0;
     for (int t = t0; t < t1; ++t) dmax = max(dmax, trows[t]);
@@ -186,7 +188,7 @@ __global__ void __launch_bounds__(WG, EX ? (NTG == 1 ? 3 : 2) : (NTG == 3 ? 3 : 
             const int t = k < nk ? tt + k : tt;
             pid[k] = tprimes[t];
             trow[k] = trows[t];
-            maxtp = max(maxtp, (uint32_t)A.pr[pid[k]].p);
+            maxtp = max(maxtp, (uint32_t)sload(&A.pr[pid[k]].p));
         }
         // g products of (max source prime - 1)(max target prime - 1) stay below 2^64, a reduced residue counting as
         // one: a sum is folded to its residue before its (g + 1)-th product
@@ -195,7 +197,7 @@ __global__ void __launch_bounds__(WG, EX ? (NTG == 1 ? 3 : 2) : (NTG == 3 ? 3 : 
         uint32_t rq[NTG][4];  // each target's Red constants
 #pragma unroll
         for (int k = 0; k < NTG; ++k) {
-            const Red r(A.pr[pid[k]]);
+            const Red r = Red::scalar(A.pr, pid[k]);
             rq[k][0] = r.p, rq[k][1] = r.r32, rq[k][2] = r.r32s, rq[k][3] = r.m;
         }
         auto rd = [&](int k) { return Red(rq[k][0], rq[k][1], rq[k][2], rq[k][3]); };

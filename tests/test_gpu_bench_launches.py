@@ -2,7 +2,7 @@
 - the C3 hoisted batch (N = 2^16, 30 limbs of 31-bit primes, dnum 3, 6 special primes) over every step of the bench's
   step set ({1..16} and 32..2^15: 26 key switches and the identity) on a context of k_rot 26, keys generated on the
   device from a ternary secret, Gaussian errors and ChaCha seeds as the bench makes them: the headline's dense keys
-  (the fused dot with the key group's retry-value table, dot_fast<3, true, 4, 0>) and the drop-in path's PackedSeeded
+  (the fused dot with the key group's retry-value table, dot_fast<3, true, 4, 0, false>) and the drop-in path's PackedSeeded
   keys at 31 bits through the kernel table alone; every one of the 27 outputs word for word against the oracle's
   hoisted rotations with the same keys (their b downloaded);
 - the C4 attention scoring as one batch of six ciphertexts (attention.score_batch: pcx_mul_plain_k, pcx_rescale_k and

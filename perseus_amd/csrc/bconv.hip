@@ -98,6 +98,7 @@ struct JobLds {
     uint32_t trow[MAXT];
     uint32_t tc[MAXT][4];  // p, 2^32 mod p, its Shoup companion, floor(2^32 / p)
     uint32_t r64[MAXT];    // 2^64 mod p
+    uint32_t r64k[MAXT][8];  // k 2^64 mod p, k < 8 (the wraps of a 96-bit sum of at most 20 products)
     double rb[MAX_REG_SRC];
     uint32_t bmod[MAXT][2];  // B mod p and its Shoup companion
     uint32_t sp[MAX_REG_SRC];  // the sources' primes
@@ -220,8 +221,9 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
                 r[k] = addm(red(s2), s2 < acc[k] ? r64 : 0u, red.p);
             }
         } else {
-            // four products of words below 2^31 stay below 2^64: each group of four is summed by multiply-adds, and
-            // only the group sums carry into the 96-bit total (at most 5 wraps: wraps r64 < 2^34)
+            // four products of words below 2^31 stay below 2^64: each group of four (the last one as long as the
+            // sources go) is summed by multiply-adds, and only the group sums carry into the 96-bit total; its at most
+            // 4 wraps come back as wraps 2^64 mod p from the table
             uint32_t wraps[V] = {};
 #pragma unroll
             for (int g = 0; g < MAX_REG_SRC / 4; ++g) {
@@ -231,18 +233,24 @@ __device__ __forceinline__ void job_lds(const BconvArgs& A, const BconvJob& j, c
                     uint64_t cs[V] = {};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
+                        if (4 * g + e < P.ns) {
 #pragma unroll
-                        for (int k = 0; k < V; ++k) cs[k] += (uint64_t)y[(4 * g + e) * V + k] * mv[e];
+                            for (int k = 0; k < V; ++k) cs[k] += (uint64_t)y[(4 * g + e) * V + k] * mv[e];
+                        }
                     }
 #pragma unroll
                     for (int k = 0; k < V; ++k) {
-                        acc[k] += cs[k];
-                        wraps[k] += acc[k] < cs[k];
+                        if (g == 0) {
+                            acc[k] = cs[k];
+                        } else {
+                            acc[k] += cs[k];
+                            wraps[k] += acc[k] < cs[k];
+                        }
                     }
                 }
             }
 #pragma unroll
-            for (int k = 0; k < V; ++k) r[k] = addm(red(acc[k]), red((uint64_t)wraps[k] * r64), red.p);
+            for (int k = 0; k < V; ++k) r[k] = addm(red(acc[k]), S.r64k[t][wraps[k]], red.p);
         }
         // exact jobs: u <= nsrc, so u B mod p is one Shoup product
 #pragma unroll
@@ -285,7 +293,10 @@ __global__ void __launch_bounds__(BX) bconv_k(BconvArgs A, int logn) {
             S.tc[t][1] = r32;
             S.tc[t][2] = r32s;
             S.tc[t][3] = (uint32_t)(q.mu_lo >> 32);
-            S.r64[t] = shoup(r32, r32, r32s, qp);
+            const uint32_t r64 = shoup(r32, r32, r32s, qp);
+            S.r64[t] = r64;
+            uint32_t v = 0;
+            for (int k = 0; k < 8; ++k, v = addm(v, r64, qp)) S.r64k[t][k] = v;
         }
         if (j.exact) {
             const double* rb = exact_rb((const uint32_t*)A.pool, j);

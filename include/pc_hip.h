@@ -785,7 +785,9 @@ int pc_hip_driver_version(int* v);
 /* cudaDeviceGetAttribute (device.rs:115 sm_count, :126 clusters). attr takes the cudaDeviceAttr numbers the reference
  * passes (16: compute units; 75 / 76: the gfx major / minor HIP reports, 9 / 5 on gfx950), PC_HIP_ATTR_CLUSTERS (0:
  * CDNA has no thread-block clusters, the value Device::clusters should read) and PC_HIP_ATTR_GFX_ARCH (the gfx code as
- * hexadecimal digits, 0x950). Any other attr: hipErrorInvalidValue. */
+ * hexadecimal digits, 0x950); also 13, the peak shader clock in kHz (cudaDevAttrClockRate's number; the reference
+ * does not read it). Any other attr: hipErrorInvalidValue. */
+#define PC_HIP_ATTR_CLOCK_KHZ 13
 #define PC_HIP_ATTR_CU_COUNT 16
 #define PC_HIP_ATTR_CC_MAJOR 75
 #define PC_HIP_ATTR_CC_MINOR 76
@@ -1077,6 +1079,12 @@ int pcx_timing_read(pcx_ctx* c, int stage, double* total_ms, int* count);
  * state the achievable bandwidth next to the spec figure and to calibrate the FETCH_SIZE / WRITE_SIZE counters. No
  * counterpart in the reference. */
 int pcx_copy_probe(void* dst, const void* src, size_t bytes, pc_stream_t s);
+/* VALU throughput probe: `blocks` workgroups of 256 threads, each thread `iters` rounds of 8 independent chains of one
+ * instruction form (kind 0 v_add_u32, 1 v_xor_b32, 2 v_alignbit_b32, 3 v_min_u32, 4 v_mul_lo_u32, 5 v_mul_hi_u32,
+ * 6 v_mad_u64_u32): 8 iters wave-instructions per wave. `out` holds 1024 words (written only on a value the chains
+ * never reach). States the integer rates the kernels can reach beside the spec figures. No counterpart in the
+ * reference. -1 on a bad kind or size. */
+int pcx_valu_probe(int kind, int blocks, int iters, uint32_t* out, pc_stream_t s);
 
 #ifdef __cplusplus
 }

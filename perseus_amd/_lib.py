@@ -119,6 +119,7 @@ _SIGS = {
     "pcx_timing": (C.c_int, [vp, C.c_int]),
     "pcx_timing_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]),
     "pcx_copy_probe": (C.c_int, [vp, vp, C.c_size_t, vp]),
+    "pcx_valu_probe": (C.c_int, [C.c_int, C.c_int, C.c_int, vp, vp]),
     "pcx_keys_patch_bytes": (C.c_size_t, [vp]),
     "pcx_keys_new_banded": (vp, [vp, C.c_int, C.POINTER(C.c_uint64), u32p, C.POINTER(vp), C.c_int, C.c_int,
                                  C.POINTER(C.c_int)]),

@@ -127,6 +127,63 @@ extern "C" int pcx_copy_probe(void* dst, const void* src, size_t bytes, pc_strea
     return pch::launch_rc();
 }
 
+// ------------------------------------------------------------------------------------------------ VALU probe
+// The throughput of single VALU instruction forms: each thread runs `iters` rounds of 8 independent dependency chains
+// of one form (inline assembly, so that the instruction is the one named), a workgroup of 256 threads; the wave-
+// instructions issued are 8 iters per wave. Timed by the caller, it states what the integer work of the kernels can
+// reach beside the spec figures: the kernels' products (v_mul_lo/hi_u32, v_mad_u64_u32), ChaCha12's add / xor / rotate
+// (v_alignbit_b32) and the conditional subtraction's v_min_u32. Nothing is read; one word per thread is written only
+// when the chains end on a value they never reach (so the work is not removed), inside the caller's 1024 words.
+namespace pch {
+namespace elem {
+template <int K>
+__global__ void __launch_bounds__(BX) valu_probe_k(uint32_t* out, int iters, uint32_t seed) {
+    uint32_t x[8];
+    uint64_t y[8];
+    const uint32_t t = blockIdx.x * BX + threadIdx.x;
+    const uint32_t c = seed | 1u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (t + seed) * (2u * i + 3u) | 1u, y[i] = x[i];
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if constexpr (K == 0) asm volatile("v_add_u32 %0, %0, %1" : "+v"(x[i]) : "v"(c));
+            if constexpr (K == 1) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x[i]) : "v"(c));
+            if constexpr (K == 2) asm volatile("v_alignbit_b32 %0, %0, %0, 16" : "+v"(x[i]));
+            if constexpr (K == 3) asm volatile("v_min_u32 %0, %0, %1" : "+v"(x[i]) : "v"(c));
+            if constexpr (K == 4) asm volatile("v_mul_lo_u32 %0, %0, %1" : "+v"(x[i]) : "v"(c));
+            if constexpr (K == 5) asm volatile("v_mul_hi_u32 %0, %0, %1" : "+v"(x[i]) : "v"(c));
+            if constexpr (K == 6) {
+                uint64_t cc;
+                asm volatile("v_mad_u64_u32 %0, %1, %2, %3, %0" : "+v"(y[i]), "=s"(cc) : "v"(x[i]), "v"(c));
+            }
+        }
+    }
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r ^= x[i] ^ (uint32_t)y[i] ^ (uint32_t)(y[i] >> 32);
+    if (r == 0x9E3779B9u) out[t & 1023] = r;
+}
+}  // namespace elem
+}  // namespace pch
+
+extern "C" int pcx_valu_probe(int kind, int blocks, int iters, uint32_t* out, pc_stream_t s) {
+    if (!out || blocks < 1 || iters < 1) return -1;
+    hipStream_t st = (hipStream_t)s;
+    const dim3 g((unsigned)blocks), b(pch::elem::BX);
+    switch (kind) {
+        case 0: hipLaunchKernelGGL(pch::elem::valu_probe_k<0>, g, b, 0, st, out, iters, 1u); break;
+        case 1: hipLaunchKernelGGL(pch::elem::valu_probe_k<1>, g, b, 0, st, out, iters, 1u); break;
+        case 2: hipLaunchKernelGGL(pch::elem::valu_probe_k<2>, g, b, 0, st, out, iters, 1u); break;
+        case 3: hipLaunchKernelGGL(pch::elem::valu_probe_k<3>, g, b, 0, st, out, iters, 1u); break;
+        case 4: hipLaunchKernelGGL(pch::elem::valu_probe_k<4>, g, b, 0, st, out, iters, 1u); break;
+        case 5: hipLaunchKernelGGL(pch::elem::valu_probe_k<5>, g, b, 0, st, out, iters, 1u); break;
+        case 6: hipLaunchKernelGGL(pch::elem::valu_probe_k<6>, g, b, 0, st, out, iters, 1u); break;
+        default: return -1;
+    }
+    return pch::launch_rc();
+}
+
 // ------------------------------------------------------------------------------------------------ byte fill
 // cudaMemsetAsync's replacement (crates/pc-cuda/src/mem.rs:305-331, DBuf::zero / zero_range) as an ordinary kernel, so
 // that a replay captured into a HIP graph holds a kernel node and no memset node. The body between the first and

@@ -43,6 +43,8 @@ int pc_hip_device_attribute(int* v, int attr, int dev) {
         return rc(hipDeviceGetAttribute(v, hipDeviceAttributeComputeCapabilityMajor, dev));
     case PC_HIP_ATTR_CC_MINOR:
         return rc(hipDeviceGetAttribute(v, hipDeviceAttributeComputeCapabilityMinor, dev));
+    case PC_HIP_ATTR_CLOCK_KHZ:
+        return rc(hipDeviceGetAttribute(v, hipDeviceAttributeClockRate, dev));
     case PC_HIP_ATTR_CLUSTERS: {
         // CDNA has no thread-block clusters: 0 for every valid device
         int cus = 0;

@@ -80,6 +80,7 @@ def test_device_queries_of_device_open():
     assert LIB.pc_hip_device_attribute(C.byref(v), 76, 0) == 0 and v.value == 5
     assert LIB.pc_hip_device_attribute(C.byref(v), 0x10000, 0) == 0 and v.value == 0
     assert LIB.pc_hip_device_attribute(C.byref(v), 0x10001, 0) == 0 and v.value == 0x950
+    assert LIB.pc_hip_device_attribute(C.byref(v), 13, 0) == 0 and 1_000_000 <= v.value <= 4_000_000  # kHz
     assert LIB.pc_hip_device_attribute(C.byref(v), 12345, 0) != 0
     assert LIB.pc_hip_device_attribute(C.byref(v), 16, 99) != 0  # no such device
     # the failure is reported once, by its return code: the thread's last error is clear for the next launch's check
@@ -127,3 +128,16 @@ def test_events_with_flags_and_a_priority_stream():
         assert LIB.pc_hip_event_destroy(e) == 0
     for s in (s1, s2):
         assert LIB.pc_hip_stream_destroy(s) == 0
+
+
+def test_valu_probe_runs_and_rejects_bad_arguments():
+    """pcx_valu_probe: every instruction form runs to completion on a small grid; a bad kind or size is refused"""
+    out = pa.DevBuf(1024)
+    st = pa.Stream()
+    for kind in range(7):
+        assert LIB.pcx_valu_probe(kind, 4, 8, out.ptr, st.h) == 0
+    st.sync()
+    assert LIB.pcx_valu_probe(7, 4, 8, out.ptr, st.h) == -1
+    assert LIB.pcx_valu_probe(0, 0, 8, out.ptr, st.h) == -1
+    assert LIB.pcx_valu_probe(0, 4, 0, out.ptr, st.h) == -1
+    assert LIB.pcx_valu_probe(0, 4, 8, None, st.h) == -1

@@ -662,24 +662,35 @@ const Level* level(const pcx_ctx* c, int top) {
 
 enum { CC_MODUP = 1, CC_MODDOWN = 2, CC_MDR = 4 };
 bool cc_on(const pcx_ctx* c, int site) { return !c->table_only && (c->cc_fused & site); }
-// targets per workgroup of a streamed conversion: CC_NTG, raised while the launch keeps about 2048 workgroups (each
-// target group re-reads its column block's sources from L2)
-int cc_tpw(const pcx_ctx* c, const BconvArgs& b, int ntg) {
-    if (c->cc_tpw > 0) return c->cc_tpw;
+// targets per round (returned) and per workgroup (tpw) of a streamed conversion of jobs of at most nsrc sources:
+// ntg0 targets per round, fewer (down to 1) for jobs of at most 8 sources when one round per workgroup leaves the
+// launch under about 2048 workgroups (a small launch then spreads its targets over more CUs: a C1 rotation 0.0592 ->
+// 0.0548 ms beside the ModDown's own fewer rows per workgroup, while the bootstrap's 16-source jobs lost more to
+// re-reading their sources than they gained),
+// then rounds per workgroup raised while the launch keeps about 2048 workgroups (each target group re-reads its
+// column block's sources from L2)
+int cc_shape(const pcx_ctx* c, const BconvArgs& b, int ntg0, int nsrc, int* tpw) {
+    if (c->cc_tpw > 0) {
+        *tpw = c->cc_tpw;
+        return ntg0;
+    }
     const long per = (long)(c->n / 4096) * b.njobs;
+    int ntg = ntg0;
+    while (nsrc <= 8 && ntg > 1 && per * ((b.max_tgt + ntg - 1) / ntg) < 2048) --ntg;
     int k = 1;
     while (k < 4 && per * ((b.max_tgt + ntg * (k + 1) - 1) / (ntg * (k + 1))) >= 2048) ++k;
-    return ntg * k;
+    *tpw = ntg * k;
+    return ntg;
 }
 // the conversion b streamed into the column pass of f's rows (exactly b's targets), then f's row pass and epilogue
 // (exact: b's jobs are the exact conversion)
 int conv_then_rows(pcx_ctx* c, const BconvArgs& b, const NttArgs& f, pc_stream_t s, int st_conv, int st_rows,
-                   int exact = 0) {
+                   int nsrc, int exact = 0) {
     {
         Stage st(c, st_conv, s);
-        const int ntg = exact ? c->cc_ntgx : c->cc_ntg;
-        if (int e = pch::conv_cols((int)c->logn, &b, c->fw, c->fws, c->lazy, exact, ntg, cc_tpw(c, b, ntg), s))
-            return e;
+        int tpw = 0;
+        const int ntg = cc_shape(c, b, exact ? c->cc_ntgx : c->cc_ntg, nsrc, &tpw);
+        if (int e = pch::conv_cols((int)c->logn, &b, c->fw, c->fws, c->lazy, exact, ntg, tpw, s)) return e;
     }
     Stage st(c, st_rows, s);
     return pch::ntt_fwd_rows_only((int)c->logn, &f, s);
@@ -733,7 +744,7 @@ int moddown_rescale(pcx_ctx* c, void* ext, int top, void* out, const void* onto,
     f.xstride = c->ct_words();
     f.es = M.ntt.es;
     f.ess = M.ntt.es + c->rows;
-    if (cc_on(c, CC_MDR)) return conv_then_rows(c, b, f, s, 5, 6, 1);
+    if (cc_on(c, CC_MDR)) return conv_then_rows(c, b, f, s, 5, 6, c->kp + 2, 1);
     {
         Stage st(c, 5, s);
         if (int e = c->tab->bconv(&b, s)) return e;
@@ -765,7 +776,7 @@ int modup(pcx_ctx* c, const void* ct, int top, pc_stream_t s, int K = 1) {
     b.njobs = k_jobs(c, L->mu_bconv, K);
     b.max_tgt = L->mu_bconv.max_tgt;
     NttArgs f = ntt_args(c, c->digits, L->mu_ntt, k_rows(c, L->mu_ntt, K));
-    if (cc_on(c, CC_MODUP)) return conv_then_rows(c, b, f, s, 1, 2);
+    if (cc_on(c, CC_MODUP)) return conv_then_rows(c, b, f, s, 1, 2, c->alpha);
     {
         Stage st(c, 1, s);
         if (int e = c->tab->bconv(&b, s)) return e;
@@ -948,7 +959,7 @@ int moddown(pcx_ctx* c, void* ext, uint32_t* conv, int m, int top, void* out, pc
     b.pr = c->pr;
     b.njobs = 2 * m;
     b.max_tgt = top + 1;
-    if (cc_on(c, CC_MODDOWN)) return conv_then_rows(c, b, f, s, 5, 6);
+    if (cc_on(c, CC_MODDOWN)) return conv_then_rows(c, b, f, s, 5, 6, c->kp);
     {
         Stage st(c, 5, s);
         if (int e = c->tab->bconv(&b, s)) return e;

@@ -109,10 +109,16 @@ void mdc_launch(const MdcArgs& a, hipStream_t st) {
     }
 }
 
+// a.ntg target rows per workgroup, fewer (down to 1) when the launch would have under 2048 workgroups: a small
+// ModDown (a C1 rotation's 2 x 12 rows at N = 2^14: 24 workgroups at 5 rows each) then spreads its targets over
+// more CUs, each workgroup re-reading its column block's sources from L2
 template <int LOGN>
 int mdc(const MdcArgs* a, pc_stream_t s) {
-    if (a->lazy) mdc_launch<LOGN, true>(*a, (hipStream_t)s);
-    else mdc_launch<LOGN, false>(*a, (hipStream_t)s);
+    using G = Geo<LOGN>;
+    MdcArgs b = *a;
+    while (b.ntg > 1 && (long)G::COL_WGS * ((b.top + b.ntg) / b.ntg) * 2 * b.m < 2048) --b.ntg;
+    if (b.lazy) mdc_launch<LOGN, true>(b, (hipStream_t)s);
+    else mdc_launch<LOGN, false>(b, (hipStream_t)s);
     return launch_rc();
 }
 

@@ -1,7 +1,7 @@
 """The full-slot bootstrap at its workload shape, N = 2^16 with 2^15 complex slots: ModRaise of a 1-limb ciphertext to
 47 limbs, CoeffToSlot (4 BSGS levels), EvalMod on the real and imaginary parts (two lanes, as the benchmark runs it),
-SlotToCoeff (3 levels), 13 limbs out, on the chain of 47 Q + 16 special 30-bit primes with dnum 3 and 80 rotation
-keys plus the relinearization key.
+SlotToCoeff (3 levels), every level's babies in the extended basis (one ModDown per giant step), 13 limbs out, on the
+chain of 47 Q + 16 special 30-bit primes with dnum 3 and 80 rotation keys plus the relinearization key.
 
 Every output residue of the GPU composite equals the same composite run on the oracle's operations (tests/bts_ops.py)
 with the same keys, word for word; the output decrypts to the input's message within 2^-16, and to the plaintext slots
@@ -40,7 +40,7 @@ def test_bootstrap_c5_matches_the_oracle():
     twin.set_threads(min(16, os.cpu_count() or 1))
     ch = pa.preset("c5")
     t0 = time.time()
-    S = setup_oracle(logn=ch.logn, seed=55, fused="cts", chain=(ch.q, ch.p, ch.dnum))
+    S = setup_oracle(logn=ch.logn, seed=55, fused=True, chain=(ch.q, ch.p, ch.dnum))
     par = S["par"]
     say(f"[bootstrap c5] {len(S['gal'])} rotation keys from the oracle in {time.time() - t0:.1f} s")
     rng = np.random.default_rng(505)
@@ -54,7 +54,7 @@ def test_bootstrap_c5_matches_the_oracle():
     relin = pa.Keys(ctx, [1], seeds=S["rseed"][None], secret=S["s"], errors=np.stack(S["errs"])[None], relin=True)
     st = pa.Stream()
     ops = B.GpuOps(ctx, keys, relin, S["levels"], S["conj"], st)
-    boot = B.Bootstrap(ops, par, ch.q, special=ch.p, fuse_stc=False)
+    boot = B.Bootstrap(ops, par, ch.q, special=ch.p, fuse_stc=True)
     assert boot.pair
     boot.prepare()
     x = pa.DevBuf.from_array(ct)

@@ -53,6 +53,18 @@ struct Acc2 {
     __device__ __forceinline__ uint32_t red(const Red& r) const { return r.red96(lo, hi); }
 };
 
+// Acc2, or (NARROW: the row's prime below 2^30, so that up to 8 products of (p - 1)^2 < 2^60 stay below 2^63) a plain
+// 64-bit sum, one multiply-add per product and no carry
+template <bool NARROW>
+struct AccN {
+    Acc2 a;
+    __device__ __forceinline__ void mad(uint32_t x, uint32_t y) {
+        if constexpr (NARROW) a.lo += (uint64_t)x * y;
+        else a.mad(x, y);
+    }
+    __device__ __forceinline__ uint32_t red(const Red& r) const { return NARROW ? r(a.lo) : a.red(r); }
+};
+
 // ------------------------------------------------------------------------------------------------ tensor
 // (c0, c1, d2) = sum_j (a_j0 b_j0, a_j0 b_j1 + a_j1 b_j0, a_j1 b_j1) over the pairs (the operands of pair j: A[j], B[j])
 struct Tacc {
@@ -339,8 +351,8 @@ __global__ void __launch_bounds__(BX) submul_many_k(SubMulManyArgs A, int logn) 
 // scalar cache and the words as global (not flat) loads, so no wait on one serialises the others. MODE 0: full-width
 // diagonals (words i .. i + 3 in one 16-byte load); 1: compact by a shift s >= 2 (the thread's 4 words share one
 // diagonal word); 2: any other index form (a load per word).
-template <int BM, int MODE>
-__global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
+template <int BM, int MODE, bool NARROW>
+__device__ __forceinline__ void pt_dot_reg_body(const PtDotArgs& A, int logn) {
     typedef const __attribute__((address_space(4))) uint64_t* ConstTab;
     typedef const __attribute__((address_space(1))) uint32_t* GPtr;
     typedef uint32_t U4 __attribute__((ext_vector_type(4)));
@@ -395,7 +407,7 @@ __global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
 #pragma unroll
                 for (int w = 0; w < 4; ++w) pw[b].v[w] = ok ? pw[b].v[w] : 0u;
             }
-            Acc2 s0[4], s1[4];
+            AccN<NARROW> s0[4], s1[4];
 #pragma unroll
             for (int b = 0; b < BM; ++b) {
 #pragma unroll
@@ -424,6 +436,14 @@ __global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
             st4(o + A.res.part_stride, r1);
         }
       }
+}
+template <int BM, int MODE>
+__global__ void __launch_bounds__(BX) pt_dot_reg_k(PtDotArgs A, int logn) {
+    const int y = blockIdx.y;
+    const int row = y < A.rs.nq ? y : A.rs.qmax + (y - A.rs.nq);
+    // the branch is uniform over the workgroup (one row per grid row)
+    if ((uint32_t)A.pr[row].p < (1u << 30)) pt_dot_reg_body<BM, MODE, true>(A, logn);
+    else pt_dot_reg_body<BM, MODE, false>(A, logn);
 }
 
 // no diagonals: the rotations re-read per giant step

@@ -258,6 +258,33 @@ class Evaluator:
             out += [Ct(self.ops.item(buf, j), t - 2, a.scale * b.scale / self.qq(t)) for j, (a, b) in enumerate(grp)]
         return out
 
+    def mul_sums(self, groups):
+        """[sum of a b over the pairs (a, b) of g for g in groups], each sum relinearized and rescaled once (the
+        operations' mul_sum_list): every pair of every group at one top and the pairs of a group at one product scale.
+        Groups go up to ops.kmax per call and up to ops.sum_pairs pairs per call."""
+        tops = {min(a.top, b.top) for g in groups for a, b in g}
+        assert len(tops) == 1, tops
+        t = tops.pop()
+        scales = []
+        for g in groups:
+            s0 = g[0][0].scale * g[0][1].scale
+            assert all(abs(a.scale * b.scale / s0 - 1.0) < 1e-9 for a, b in g), [a.scale * b.scale for a, b in g]
+            scales.append(s0 / self.qq(t))
+        kmax = max(1, getattr(self.ops, "kmax", 1))
+        pmax = max(1, getattr(self.ops, "sum_pairs", 8))
+        out, j0 = [], 0
+        while j0 < len(groups):
+            j1, npairs = j0, 0
+            while j1 < len(groups) and j1 - j0 < kmax and npairs + len(groups[j1]) <= pmax:
+                npairs += len(groups[j1])
+                j1 += 1
+            assert j1 > j0, "a group with more pairs than one call takes"
+            buf = self.ops.alloc(j1 - j0)
+            self.ops.mul_sum_list(buf, [[(a.h, b.h) for a, b in g] for g in groups[j0:j1]], t)
+            out += [Ct(self.ops.item(buf, j - j0), t - 2, scales[j]) for j in range(j0, j1)]
+            j0 = j1
+        return out
+
     def prod_meta(self, a, b):
         """(top, scale) of mul(a, b): the product lands two primes below the lower operand's top"""
         t = min(a.top, b.top)
@@ -372,8 +399,9 @@ class ChebEval:
 
     BABY, GIANTS = 8, (8, 16, 32)
 
-    def __init__(self, ev):
+    def __init__(self, ev, fuse=True):
         self.ev = ev
+        self.fuse = fuse  # the chains of remainders in one relinearization each (eval)
 
     # T_k = 2 T_a T_b - T_{a-b}, by rounds of independent products (one batched product per round)
     ROUNDS = (((2, 1, 1),), ((3, 2, 1), (4, 2, 2)), ((5, 3, 2), (6, 3, 3), (7, 4, 3), (8, 4, 4)), ((16, 8, 8),),
@@ -422,13 +450,29 @@ class ChebEval:
         R = self._walk(r, top, scale, leaf)
         return [Ct(G.h, top + 2, G.scale), Q, R]
 
+    @staticmethod
+    def _chain(n):
+        """a split's products and its last remainder: Q T_g + R with R = Q' T_g' + R' ... down to a leaf, as the pairs
+        [(Q, T_g), (Q', T_g'), ...] and that leaf. Every pair lands on the split's (top, scale): R is walked at the
+        split's own (top, scale), and a split's product sits two primes above it at scale times their product"""
+        pairs, r = [(n[1], n[0])], n[2]
+        while not isinstance(r, Ct):
+            pairs.append((r[1], r[0]))
+            r = r[2]
+        return pairs, r
+
     def eval(self, c, top, scale):
         """every leaf first (their weighted sums grouped over the shared T_k), then the splits round by round: each
-        round's splits whose Q and R are formed take their products Q T_g together where they land on one top"""
+        round's splits whose Q and R are formed take their products Q T_g together where they land on one top. With
+        the operations' mul_sum_list, a split whose remainder R is itself a split takes R's products into its own sum
+        (one relinearization and rescale for the chain of remainders, their tensors summed); only the root and the
+        splits that are some split's Q are formed on their own"""
         specs = []
         self._walk(c, top, scale, lambda *sp: specs.append(sp))
         vals = iter(self.ev.lincombs(specs))
         tree = self._walk(c, top, scale, lambda *sp: next(vals))
+        if self.fuse and hasattr(self.ev.ops, "mul_sum_list"):
+            return self._eval_chains(tree)
         while not isinstance(tree, Ct):
             ready = []
 
@@ -446,6 +490,27 @@ class ChebEval:
                 grp = [n for n in ready if n[0].top == t]
                 for n, P in zip(grp, self.ev.mul_many([(n[1], n[0]) for n in grp])):
                     n.append(self.ev.add(P, n[2]))
+            tree = self._resolve(tree)
+        return tree
+
+    def _eval_chains(self, tree):
+        while not isinstance(tree, Ct):
+            ready = []
+
+            def visit(n):
+                pairs, leaf = self._chain(n)
+                if all(isinstance(q, Ct) for q, _ in pairs):
+                    ready.append((n, pairs, leaf))
+                else:
+                    for q, _ in pairs:
+                        if not isinstance(q, Ct):
+                            visit(q)
+
+            visit(tree)
+            for t in dict.fromkeys(min(pairs[0][0].top, pairs[0][1].top) for _, pairs, _ in ready):
+                grp = [r for r in ready if min(r[1][0][0].top, r[1][0][1].top) == t]
+                for (n, _, leaf), P in zip(grp, self.ev.mul_sums([pairs for _, pairs, _ in grp])):
+                    n.append(self.ev.add(P, leaf))
             tree = self._resolve(tree)
         return tree
 
@@ -748,6 +813,14 @@ class PairOps:
         ex = lambda hs: [self.o.item(h, i) for h in hs for i in (0, 1)]
         self.o.mul_list(out, ex(a), ex(b), top, twice)
 
+    @property
+    def sum_pairs(self):
+        return max(1, getattr(self.o, "sum_pairs", 8) // 2)
+
+    def mul_sum_list(self, out, groups, top):
+        self.o.mul_sum_list(out, [[(self.o.item(a, i), self.o.item(b, i)) for a, b in g] for g in groups
+                                  for i in (0, 1)], top)
+
 
 class GpuOps:
     """The composite's operations on the device: the engine's key switches, rescale and products, the kernel table's
@@ -1013,6 +1086,13 @@ class GpuOps:
         """out's len(a) consecutive ciphertexts = a[j] b[j], relinearized and rescaled (the pairs at their own
         addresses)"""
         self.ctx.mul_relin_rescale_list(self.relin, a, b, top, out, self.st, twice=twice)
+
+    sum_pairs = 8  # pairs per pcx_mul_sum_relin_rescale_list call
+
+    def mul_sum_list(self, out, groups, top):
+        """out's len(groups) consecutive ciphertexts: product j = the sum of a b over the pairs of groups[j],
+        relinearized and rescaled once"""
+        self.ctx.mul_sum_relin_rescale_list(self.relin, groups, top, out, self.st)
 
     # -- ModRaise
     def mod_raise(self, out, x, top):

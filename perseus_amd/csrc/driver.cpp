@@ -2111,6 +2111,52 @@ int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, co
     return moddown_rescale(c, c->ext, top, out, folded ? nullptr : out, s, K);
 }
 
+int pcx_mul_sum_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b,
+                                   const int* off, int K, int top, void* out, pc_stream_t s) {
+    if (!c || !k || !a || !b || !off || !out || top < 2 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
+    if (K < 1 || K > c->k_max || !serves(k, top) || off[0] != 0) return -1;
+    for (int j = 0; j < K; ++j)
+        if (off[j + 1] <= off[j] || off[j + 1] > pch::TLIST_MAX) return -1;
+    const uint64_t part = (uint64_t)c->rows * c->n;
+    pch::TensorListArgs t;
+    memset(&t, 0, sizeof t);
+    // no out slot may overlap any operand: the one tensor launch stores every slot while it reads every pair
+    const uintptr_t cwb = (uintptr_t)c->ct_words() * sizeof(uint32_t);
+    for (int j = 0; j < off[K]; ++j) {
+        if (!a[j] || !b[j]) return -1;
+        t.a[j] = (const uint32_t*)a[j];
+        t.b[j] = (const uint32_t*)b[j];
+        for (const void* x : {a[j], b[j]}) {
+            const uintptr_t xv = (uintptr_t)x, o = (uintptr_t)out;
+            if (xv < o + K * cwb && o < xv + cwb) return -1;
+        }
+    }
+    t.sum = 1;
+    for (int j = 0; j <= K; ++j) t.off[j] = off[j];
+    t.out = (uint32_t*)out;
+    t.d2 = c->tmp;
+    t.part = part;
+    t.ct_stride = 2 * part;
+    t.pr = c->pr;
+    t.n = top + 1;
+    t.K = K;
+    {
+        Stage st(c, 8, s);
+        if (int e = pch::tensor_list((int)c->logn, &t, s)) return e;
+    }
+    if (int e = modup(c, c->tmp, top, s, K)) return e;
+    const Level* L = level(c, top);
+    const bool folded = k->pval && !c->table_only && k->bits == 0 && L->ndig >= 1 && L->ndig <= 3;
+    const size_t cw = c->ct_words(), dw = (size_t)c->dnum * c->rows * c->n;
+    for (int j0 = 0; j0 < K; j0 += 4) {
+        const int m = std::min(4, K - j0);
+        if (int e = dot(c, k, 0, 1, c->tmp + j0 * cw, top, c->ext + j0 * cw, s, 0, folded ? 3 : 0, m,
+                        c->digits + j0 * dw, folded ? (const uint32_t*)out + j0 * cw : nullptr))
+            return e;
+    }
+    return moddown_rescale(c, c->ext, top, out, folded ? nullptr : out, s, K);
+}
+
 int pcx_mul_plain_k(pcx_ctx* c, const void* ct, const void* const* pts, int K, int top, void* out, pc_stream_t s) {
     if (!c || !ct || !pts || !out || top < 0 || top >= c->nq || K < 1 || K > pch::TLIST_MAX) return -1;
     pch::MulPtListArgs m;

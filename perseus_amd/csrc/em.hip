@@ -155,9 +155,13 @@ __global__ void __launch_bounds__(BX) tensor_list_k(TensorListArgs A, int logn) 
     const uint32_t i = lane_word();
     const Red red(A.pr[row]);
     const size_t ro = ((size_t)row << logn) + i;
-    const uint32_t *a = A.a[c] + ro, *b = A.b[c] + ro;
+    // product c's pairs (one, or a summed range): the sums exact over any number of pairs
+    const int j0 = A.sum ? A.off[c] : c, j1 = A.sum ? A.off[c + 1] : c + 1;
     Tacc s;
-    s.mac(ld4(a), ld4(a + A.part), ld4(b), ld4(b + A.part));
+    for (int j = j0; j < j1; ++j) {
+        const uint32_t *a = A.a[j] + ro, *b = A.b[j] + ro;
+        s.mac(ld4(a), ld4(a + A.part), ld4(b), ld4(b + A.part));
+    }
     uint32_t* o = A.out + c * A.ct_stride + ro;
     tensor_tail(s, red, o, o + A.part, A.d2 + c * A.ct_stride + A.part + ro, false, false, A.dbl != 0, nullptr,
                 nullptr, 0u, 0u, false, nullptr);
@@ -513,7 +517,13 @@ int tensor(const TensorArgs* a, pc_stream_t s) {
 template <int LOGN>
 int tensor_list(const TensorListArgs* a, pc_stream_t s) {
     if (!a || !a->pr || !a->out || !a->d2 || a->n < 0 || a->K < 0 || a->K > TLIST_MAX) return -1;
-    for (int c = 0; c < a->K; ++c)
+    const int np = a->sum ? a->off[a->K] : a->K;
+    if (a->sum) {
+        if (a->off[0] != 0) return -1;
+        for (int c = 0; c < a->K; ++c)
+            if (a->off[c + 1] <= a->off[c] || a->off[c + 1] > TLIST_MAX) return -1;
+    }
+    for (int c = 0; c < np; ++c)
         if (!a->a[c] || !a->b[c]) return -1;
     if (a->n == 0 || a->K == 0) return 0;
     PCH_LAUNCH(tensor_list_k, grid<LOGN>(a->n, a->K), *a, LOGN);

@@ -89,6 +89,7 @@ int noalloc_prepare();
 // d2, doubled when dbl; rows 0..n-1; a[c] / b[c] hold part 0, part 1 `part` words later; out and d2 are K consecutive
 // ciphertexts (ct_stride apart)
 constexpr int TLIST_MAX = 8;
+// sum != 0: product c is the sum of pairs off[c] .. off[c + 1] - 1 (off[K] <= TLIST_MAX pairs in all); else pair c
 struct TensorListArgs {
     const uint32_t* a[TLIST_MAX];
     const uint32_t* b[TLIST_MAX];
@@ -97,6 +98,8 @@ struct TensorListArgs {
     uint64_t part, ct_stride;
     const PrimeConst* pr;
     int n, K, dbl;
+    int sum;
+    int off[TLIST_MAX + 1];
 };
 int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s);
 // The plaintext products of K ciphertexts (K consecutive, ct_stride apart; out likewise), ciphertext c by its own

@@ -292,6 +292,20 @@ class Context:
         check(LIB.pcx_mul_relin_rescale_list(self.h, keys.h, pa, pb, len(a), top, out.addr(), int(twice), stream.h),
               "mul_relin_rescale_list")
 
+    def mul_sum_relin_rescale_list(self, keys, groups, top, out, stream):
+        """out's len(groups) consecutive ciphertexts (top - 2): product j = the sum of a b over the pairs (a, b) of
+        groups[j], relinearized and rescaled once (pcx_mul_sum_relin_rescale_list)."""
+        pairs = [p for g in groups for p in g]
+        assert groups and all(groups)
+        off = [0]
+        for g in groups:
+            off.append(off[-1] + len(g))
+        pa = (C.c_void_p * len(pairs))(*[x.addr() for x, _ in pairs])
+        pb = (C.c_void_p * len(pairs))(*[y.addr() for _, y in pairs])
+        po = (C.c_int * len(off))(*off)
+        check(LIB.pcx_mul_sum_relin_rescale_list(self.h, keys.h, pa, pb, po, len(groups), top, out.addr(), stream.h),
+              "mul_sum_relin_rescale_list")
+
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}
         in the extended basis, babies i >= 1 by keys r0 + i - 1. pts: a DevBuf holding npts device pointers (uint64)

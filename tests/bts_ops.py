@@ -146,6 +146,13 @@ class OracleOps:
         for j in range(len(a)):
             self.mul_relin_rescale(self.item(out, j), a[j], b[j], top, twice)
 
+    sum_pairs = 8
+
+    def mul_sum_list(self, out, groups, top):
+        for j, g in enumerate(groups):
+            self.get(self.item(out, j))[:] = self.oc.mul_sum_relin_rescale(
+                [(self.get(a), self.get(b)) for a, b in g], top, self.relin_seed, self.relin_b)
+
     def rescale2(self, out, x, top, count=1):
         for i in range(count):
             self.get(self.item(out, i))[:] = self.oc.rescale(self.get(self.item(x, i)).copy(), top, 2)

@@ -219,6 +219,43 @@ def test_product_list(stream, name, top, K, twice):
     assert (shifted.download((3, 2, ch.rows, ch.n)) == pool[:3]).all()
 
 
+@pytest.mark.parametrize("name,top,sizes", [("small", 5, (1, 2, 3)), ("small31", 4, (3, 1)), ("c3", 29, (2, 2, 1)),
+                                            ("c5", 30, (4, 4))])
+def test_product_sums(stream, name, top, sizes):
+    """pcx_mul_sum_relin_rescale_list on a k_max 6 context: product j the sum of sizes[j] pairs (operands drawn
+    with repeats from four ciphertexts of one buffer), its tensors summed and relinearized and rescaled once: each
+    product's words equal the oracle's (the tensor of all its pairs, ModUp of d2, the key dot, the exact ModDown by
+    P q_top q_top-1 with (d0, d1) onto it); more than 8 pairs, an empty group and an out slot over an operand are
+    refused before anything is launched."""
+    say(f"[product sums] {name} top={top} sizes={sizes}")
+    from perseus_amd import bootstrap as B
+
+    ch, _, oc = contexts(name)
+    _, _, seed, _ = relin_key(name)
+    ctxk, keysk = batched(name, 6)
+    rng = np.random.default_rng(top * 7 + len(sizes))
+    pool = np.stack([random_ct(ch, top, rng) for _ in range(4)])
+    groups = [[(int(rng.integers(0, 4)), int(rng.integers(0, 4))) for _ in range(m)] for m in sizes]
+    buf = pa.DevBuf.from_array(pool)
+    view = lambda i: B.View(buf, i * ctxk.ct_words)
+    out = ctxk.ct_buf(len(sizes))
+    ctxk.mul_sum_relin_rescale_list(keysk, [[(view(i), view(j)) for i, j in g] for g in groups], top, out, stream)
+    stream.sync()
+    got = out.download((len(sizes), 2, ch.rows, ch.n))
+    bkey = keysk.download_b(0)
+    for j, g in enumerate(groups):
+        want = oc.mul_sum_relin_rescale([(pool[a], pool[b]) for a, b in g], top, seed, bkey)
+        assert (got[j][:, : top - 1] == want[:, : top - 1]).all(), f"product {j} ({g})"
+    with pytest.raises(pa.HipError):
+        ctxk.mul_sum_relin_rescale_list(keysk, [[(view(0), view(1))] * 5, [(view(2), view(3))] * 4], top,
+                                        ctxk.ct_buf(2), stream)
+    with pytest.raises((pa.HipError, AssertionError)):
+        ctxk.mul_sum_relin_rescale_list(keysk, [[(view(0), view(1))], []], top, ctxk.ct_buf(2), stream)
+    with pytest.raises(pa.HipError):
+        ctxk.mul_sum_relin_rescale_list(keysk, [[(view(1), view(2))]], top, view(1), stream)
+    assert (buf.download((4, 2, ch.rows, ch.n)) == pool).all()
+
+
 @pytest.mark.parametrize("name,top,alias", [("small", 5, False), ("small31", 4, True), ("c3", 29, True),
                                             ("c5", 30, False)])
 def test_batched_product_and_rescale(stream, name, top, alias):

@@ -292,6 +292,19 @@ class Ctx:
         d[0, :n], d[1, :n] = c0[0], c1[0]
         return self.moddown_rescale(ext, top, d)
 
+    def mul_sum_relin_rescale(self, pairs, top, seed, bkey):
+        """The sum of the pairs' tensors (a b over every pair, summed exactly mod each prime), relinearized and
+        rescaled once as mul_relin_rescale does one tensor."""
+        from oracle import em
+        n = top + 1
+        c0, c1, d2 = em.tensor(self.primes, [(a[None, :, :n], b[None, :, :n]) for a, b in pairs])
+        tmp = self.ct_zeros()
+        tmp[1, :n] = d2[0]
+        ext = self.ks_dot(tmp, self.modup(tmp[1], top), top, seed, bkey, 1)
+        d = self.ct_zeros()
+        d[0, :n], d[1, :n] = c0[0], c1[0]
+        return self.moddown_rescale(ext, top, d)
+
     def rescale(self, x, top, ndrop):
         """Rows 0..top - ndrop of the rescale of one ciphertext x [2][rows][N] (oracle/em.py rescale)."""
         from oracle import em

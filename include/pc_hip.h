@@ -683,7 +683,8 @@ typedef struct SpruScatterArgs {
 } SpruScatterArgs;
 PC_STATIC_ASSERT(sizeof(SpruScatterArgs) == 56, "SpruScatterArgs layout");
 
-/* Argument structs of the table entries this build does not implement (their launchers return -1): declared only. */
+/* Argument structs of the table entries this library does not implement (their launchers return -1): declared
+ * only. */
 /* args.cuh:595-611 (encode): N/2 complex slots v (re, im doubles) -> coefficient-form rows out[l][N], l < nl
  * (prime id l): slot j at zeta^(5^j) and its conjugate, an N-point DFT in double, c_k = scale Re(Y_k zeta^-k) / N and
  * max |c_k|, OpenFHE's 2^61 split, residues times deg_factor[l] (round(scale)^(deg - 1) mod p_l) and 2^split.

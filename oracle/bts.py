@@ -2,7 +2,7 @@
 repository's tests.
 
 Test infrastructure only. Nothing in the product library (perseus_amd/) imports this module; only tests/,
-__graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the checker.
+__graft_entry__.smoke() and bench.py's cpu_baseline leg use it, to check the GPU's results against.
 
 Semantics: crates/pc-kernels/kernels/args.cuh ModRaiseArgs / SmallIntArgs / SmallInt1Args :665-709, :890-907, and the
 host twins crates/pc-gpu/src/bts/raise.rs:159-215 (small_int_host), :279-292 (small_int1_host). The multi-word

@@ -2,7 +2,7 @@
 ORACLE of this repository's tests.
 
 Test infrastructure only. Nothing in the product library (perseus_amd/) imports this module; only tests/,
-__graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the checker.
+__graft_entry__.smoke() and bench.py's cpu_baseline leg use it, to check the GPU's results against.
 
 Each function states one kernel of the reference's table over canonical residues with numpy uint64 arithmetic (every
 product is reduced before it is summed, so any number of terms is exact). Arrays are ciphertext slices

@@ -1,7 +1,8 @@
 /* CPU twin of the CKKS key-switch / NTT path: the ORACLE of this repository's tests.
  *
  * Test infrastructure only. Nothing in the product library (perseus_amd/) links, loads or calls this code; only
- * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the checker and as the host-CPU baseline.
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, to check the GPU's results against and as the
+ * host-CPU baseline.
  *
  * It restates the reference's CPU twin (crates/pc-host) and the math it rests on (crates/pc-core), and the launch
  * sequences of crates/pc-gpu (ks.rs, rotate.rs, keygen.rs) as whole functions, in plain loops over canonical

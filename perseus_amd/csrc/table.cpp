@@ -1,5 +1,5 @@
 // The kernel tables (crates/pc-kernels/kernels/inst/instantiate.inc:32-91): one constant-initialised KernelTable per
-// ring degree, u32 words, Barrett64 (mm 0). Entries this build does not implement return -1 (argument outside the
+// ring degree, u32 words, Barrett64 (mm 0). Entries this library does not implement return -1 (argument outside the
 // kernel's range), as the reference's table does for an entry a build leaves out.
 #include "pc_hip.h"
 

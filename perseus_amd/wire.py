@@ -81,7 +81,7 @@ def _read_header(f, magic):
         raise WireError(f"magic {m!r}, expected {magic!r}")
     ver, ln = struct.unpack("<IQ", f.read(12))
     if ver != VERSION:
-        raise WireError(f"version {ver}; this build reads version {VERSION}")
+        raise WireError(f"version {ver}; this library reads version {VERSION}")
     if ln > 1 << 30:
         raise WireError(f"header of {ln} bytes")
     h = f.read(ln)

@@ -1,4 +1,4 @@
-"""ctypes bindings of the CPU twin (oracle/libtwin.so): the checker of every parity test.
+"""ctypes bindings of the CPU twin (oracle/libtwin.so): the oracle of every parity test.
 
 Test infrastructure only: the product package (perseus_amd) never imports this module.
 """

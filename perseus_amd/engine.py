@@ -5,6 +5,7 @@ rotate_hoisted, crates/pc-gpu/src/ntt.rs transform_rows, crates/pc-gpu/src/keyge
 the work itself runs in libpchip.so (the driver and the gfx950 kernels).
 """
 import ctypes as C
+import gc
 
 import numpy as np
 
@@ -71,11 +72,22 @@ class Graph:
 
     def __init__(self, stream, fn):
         self.graph, self.exe = C.c_void_p(), C.c_void_p()
-        check(LIB.pc_hip_graph_begin_capture(stream.h), "graph_begin_capture")
+        # no device memory may be freed while the stream is captured (a free invalidates the capture): a DevBuf whose
+        # last reference sits in a reference cycle (a buffer pool's replaced buffer held by an earlier run's closures)
+        # is freed by the cyclic collector whenever it runs, so collect now and hold the collector off until the
+        # capture has ended
+        gc.collect()
+        was = gc.isenabled()
+        gc.disable()
         try:
-            fn()
+            check(LIB.pc_hip_graph_begin_capture(stream.h), "graph_begin_capture")
+            try:
+                fn()
+            finally:
+                rc = LIB.pc_hip_graph_end_capture(stream.h, C.byref(self.graph))
         finally:
-            rc = LIB.pc_hip_graph_end_capture(stream.h, C.byref(self.graph))
+            if was:
+                gc.enable()
         check(rc, "graph_end_capture")
         check(LIB.pc_hip_graph_instantiate(C.byref(self.exe), self.graph), "graph_instantiate")
 

@@ -67,6 +67,32 @@ def test_memset_in_a_captured_graph():
         assert (b.download() == wb).all(), rep
 
 
+def test_capture_beside_cyclic_garbage_holding_device_buffers():
+    """Device buffers whose last references sit in reference cycles are freed by Python's cyclic collector whenever it
+    runs, and a free inside a stream capture would invalidate it: pa.Graph collects before it begins and holds the
+    collector off until the capture ends. The captured work allocates far past the collector's thresholds; the graph
+    is built and its replay copies the words."""
+    say("[graph] capture beside cyclic garbage that holds device buffers")
+    st = pa.Stream()
+    n = 1 << 16
+    src = pa.DevBuf.from_array(np.arange(n, dtype=np.uint32))
+    dst = pa.DevBuf(n)
+    for _ in range(8):
+        cyc = [pa.DevBuf(1024)]
+        cyc.append(cyc)  # a cycle: only the collector frees its buffer
+    del cyc
+
+    def work():
+        junk = [[i] for i in range(200000)]
+        assert LIB.pc_hip_memcpy_dtod(dst.ptr, src.ptr, 4 * n, st.h) == 0
+        del junk
+
+    g = pa.Graph(st, work)
+    g.launch(st)
+    st.sync()
+    assert (dst.download() == np.arange(n, dtype=np.uint32)).all()
+
+
 def test_device_queries_of_device_open():
     """What crates/pc-cuda/src/device.rs:63-158 (Device::open, sm_count, clusters, mem_info, profiler) reads."""
     say("[runtime] versions, attributes, memory info, profiler range, priority range")

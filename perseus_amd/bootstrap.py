@@ -258,17 +258,21 @@ class Evaluator:
             out += [Ct(self.ops.item(buf, j), t - 2, a.scale * b.scale / self.qq(t)) for j, (a, b) in enumerate(grp)]
         return out
 
-    def mul_sums(self, groups):
-        """[sum of a b over the pairs (a, b) of g for g in groups], each sum relinearized and rescaled once (the
-        operations' mul_sum_list): every pair of every group at one top and the pairs of a group at one product scale.
-        Groups go up to ops.kmax per call and up to ops.sum_pairs pairs per call."""
+    def mul_sums(self, groups, adds=None):
+        """[sum of a b over the pairs (a, b) of g, plus adds[j] for g = groups[j]], each sum relinearized and rescaled
+        once (the operations' mul_sum_list): every pair of every group at one top t, the pairs of a group at one
+        product scale, and an addend (None: none) at that scale and at top t or above, so that it is rescaled with
+        the products. Groups go up to ops.kmax per call and up to ops.sum_pairs pairs per call."""
         tops = {min(a.top, b.top) for g in groups for a, b in g}
         assert len(tops) == 1, tops
         t = tops.pop()
+        adds = [None] * len(groups) if adds is None else adds
+        assert len(adds) == len(groups)
         scales = []
-        for g in groups:
+        for g, y in zip(groups, adds):
             s0 = g[0][0].scale * g[0][1].scale
             assert all(abs(a.scale * b.scale / s0 - 1.0) < 1e-9 for a, b in g), [a.scale * b.scale for a, b in g]
+            assert y is None or (y.top >= t and abs(y.scale / s0 - 1.0) < 1e-9), (y.top, y.scale, t, s0)
             scales.append(s0 / self.qq(t))
         kmax = max(1, getattr(self.ops, "kmax", 1))
         pmax = max(1, getattr(self.ops, "sum_pairs", 8))
@@ -280,7 +284,9 @@ class Evaluator:
                 j1 += 1
             assert j1 > j0, "a group with more pairs than one call takes"
             buf = self.ops.alloc(j1 - j0)
-            self.ops.mul_sum_list(buf, [[(a.h, b.h) for a, b in g] for g in groups[j0:j1]], t)
+            ys = adds[j0:j1]
+            self.ops.mul_sum_list(buf, [[(a.h, b.h) for a, b in g] for g in groups[j0:j1]], t,
+                                  None if all(y is None for y in ys) else [None if y is None else y.h for y in ys])
             out += [Ct(self.ops.item(buf, j - j0), t - 2, scales[j]) for j in range(j0, j1)]
             j0 = j1
         return out
@@ -319,9 +325,10 @@ class Evaluator:
         self.ops.rescale2(out, out, a.top)
         return Ct(out, top, scale)
 
-    def lincomb(self, terms, c0, top, scale):
+    def lincomb(self, terms, c0, top, scale, rescale=True):
         """c0 + sum c_j a_j landing exactly at (top, scale): each a_j (dropped to top + 2) times the integer
-        round(c_j scale q_a q_b / a_j.scale) in one weighted sum with the constant, then one rescale"""
+        round(c_j scale q_a q_b / a_j.scale) in one weighted sum with the constant, then one rescale (rescale False:
+        the sum before it, at (top + 2, scale q_a q_b))"""
         tc = top + 2
         qq = self.qq(tc)
         for a, _ in terms:
@@ -329,16 +336,19 @@ class Evaluator:
         ks = [int(round(c * scale * qq / a.scale)) for a, c in terms]
         out = self.ops.alloc()
         self.ops.wsum(out, [a.h for a, _ in terms], tc, ks, int(round(c0 * scale * qq)))
+        if not rescale:
+            return Ct(out, tc, scale * qq)
         self.ops.rescale2(out, out, tc)
         return Ct(out, top, scale)
 
-    def lincombs(self, specs):
+    def lincombs(self, specs, raw=()):
         """lincomb of each (terms, c0, top, scale), up to three of them per weighted-sum launch over one source list
         when the operations have wsum_multi (a source a term does not use weighs 0), the sums landing on one top laid
         out side by side and rescaled together (up to ops.kmax per launch sequence): the same words as one lincomb at
-        a time"""
+        a time. The specs whose index is in raw are left before their rescale: the weighted sum at (top + 2, scale
+        q_{top+2} q_{top+1}), for a product to rescale with itself (mul_sums' addend)"""
         if not hasattr(self.ops, "wsum_multi"):
-            return [self.lincomb(*sp) for sp in specs]
+            return [self.lincomb(*sp, rescale=i not in raw) for i, sp in enumerate(specs)]
         groups = []
         for g0 in range(0, len(specs), 3):
             srcs = []
@@ -347,13 +357,18 @@ class Evaluator:
                     if not any(x.h is a.h for x in srcs):
                         srcs.append(a)
             if len(srcs) > 8:
-                return [self.lincomb(*sp) for sp in specs]
+                return [self.lincomb(*sp, rescale=i not in raw) for i, sp in enumerate(specs)]
             groups.append((g0, srcs))
         tcs = [top + 2 for _, _, top, _ in specs]
-        blocks = {tc: [self.ops.alloc(tcs.count(tc)), 0] for tc in dict.fromkeys(tcs)}
+        # the blocks of one top (rescaled together) hold the specs not in raw; each raw one its own buffer
+        keys = [(tc, i in raw) for i, tc in enumerate(tcs)]
+        blocks = {k: [self.ops.alloc(keys.count(k)), 0] for k in dict.fromkeys(keys) if not k[1]}
         outs = []
-        for tc in tcs:
-            b = blocks[tc]
+        for k in keys:
+            if k[1]:
+                outs.append(self.ops.alloc())
+                continue
+            b = blocks[k]
             outs.append(self.ops.item(b[0], b[1]))
             b[1] += 1
         for g0, srcs in groups:
@@ -367,11 +382,12 @@ class Evaluator:
                 k0s.append(int(round(c0 * scale * qq)))
             self.ops.wsum_multi(outs[g0:g0 + 3], [x.h for x in srcs], tcs[g0:g0 + 3], ks, k0s)
         kmax = max(1, getattr(self.ops, "kmax", 1))
-        for tc, (buf, n) in blocks.items():
+        for (tc, _), (buf, n) in blocks.items():
             for j0 in range(0, n, kmax):
                 h = self.ops.item(buf, j0)
                 self.ops.rescale2(h, h, tc, min(kmax, n - j0))
-        return [Ct(o, top, scale) for o, (_, _, top, scale) in zip(outs, specs)]
+        return [Ct(o, top + 2, scale * self.qq(top + 2)) if i in raw else Ct(o, top, scale)
+                for i, (o, (_, _, top, scale)) in enumerate(zip(outs, specs))]
 
     def add(self, a, b, sub=False):
         assert abs(a.scale / b.scale - 1.0) < 1e-9, (a.scale, b.scale)
@@ -399,9 +415,11 @@ class ChebEval:
 
     BABY, GIANTS = 8, (8, 16, 32)
 
-    def __init__(self, ev, fuse=True):
+    def __init__(self, ev, fuse=True, fold_ends=True):
         self.ev = ev
         self.fuse = fuse  # the chains of remainders in one relinearization each (eval)
+        # with fuse: each chain's last leaf added, unrescaled, into the chain's summed product (rescaled with it)
+        self.fold_ends = fold_ends
 
     # T_k = 2 T_a T_b - T_{a-b}, by rounds of independent products (one batched product per round)
     ROUNDS = (((2, 1, 1),), ((3, 2, 1), (4, 2, 2)), ((5, 3, 2), (6, 3, 3), (7, 4, 3), (8, 4, 4)), ((16, 8, 8),),
@@ -468,11 +486,20 @@ class ChebEval:
         (one relinearization and rescale for the chain of remainders, their tensors summed); only the root and the
         splits that are some split's Q are formed on their own"""
         specs = []
-        self._walk(c, top, scale, lambda *sp: specs.append(sp))
-        vals = iter(self.ev.lincombs(specs))
-        tree = self._walk(c, top, scale, lambda *sp: next(vals))
-        if self.fuse and hasattr(self.ev.ops, "mul_sum_list"):
-            return self._eval_chains(tree)
+
+        def spec(*sp):
+            specs.append(sp)
+            return len(specs) - 1
+
+        shape = self._walk(c, top, scale, spec)
+        fused = self.fuse and hasattr(self.ev.ops, "mul_sum_list")
+        # fused: the leaf that ends each chain of remainders stays unrescaled, the chain's addend
+        raw = self._chain_ends(shape) if fused and self.fold_ends else set()
+        vals = self.ev.lincombs(specs, raw)
+        it = iter(vals)
+        tree = self._walk(c, top, scale, lambda *sp: next(it))
+        if fused:
+            return self._eval_chains(tree, {id(vals[i]) for i in raw})
         while not isinstance(tree, Ct):
             ready = []
 
@@ -493,7 +520,28 @@ class ChebEval:
             tree = self._resolve(tree)
         return tree
 
-    def _eval_chains(self, tree):
+    @staticmethod
+    def _chain_ends(n):
+        """the leaves (walk indices) that end a chain of remainders: the root's chain's and each chain's whose head is
+        some split's Q"""
+        ends = set()
+
+        def head(x):
+            # x a split: its chain is x, x's R, R's R ... down to a leaf; every Q on the way that is a split heads a
+            # chain of its own (a Q that is a leaf is a product's operand)
+            while isinstance(x, list):
+                if isinstance(x[1], list):
+                    head(x[1])
+                x = x[2]
+            ends.add(x)
+
+        if isinstance(n, list):
+            head(n)
+        return ends
+
+    def _eval_chains(self, tree, raw=frozenset()):
+        """raw: ids of the unrescaled chain-end leaves, each added into its chain's summed product (mul_sums' addend)
+        instead of after it"""
         while not isinstance(tree, Ct):
             ready = []
 
@@ -509,8 +557,9 @@ class ChebEval:
             visit(tree)
             for t in dict.fromkeys(min(pairs[0][0].top, pairs[0][1].top) for _, pairs, _ in ready):
                 grp = [r for r in ready if min(r[1][0][0].top, r[1][0][1].top) == t]
-                for (n, _, leaf), P in zip(grp, self.ev.mul_sums([pairs for _, pairs, _ in grp])):
-                    n.append(self.ev.add(P, leaf))
+                adds = [leaf if id(leaf) in raw else None for _, _, leaf in grp]
+                for (n, _, leaf), y, P in zip(grp, adds, self.ev.mul_sums([pairs for _, pairs, _ in grp], adds)):
+                    n.append(P if y is not None else self.ev.add(P, leaf))
             tree = self._resolve(tree)
         return tree
 
@@ -817,9 +866,10 @@ class PairOps:
     def sum_pairs(self):
         return max(1, getattr(self.o, "sum_pairs", 8) // 2)
 
-    def mul_sum_list(self, out, groups, top):
+    def mul_sum_list(self, out, groups, top, adds=None):
+        ys = None if adds is None else [None if y is None else self.o.item(y, i) for y in adds for i in (0, 1)]
         self.o.mul_sum_list(out, [[(self.o.item(a, i), self.o.item(b, i)) for a, b in g] for g in groups
-                                  for i in (0, 1)], top)
+                                  for i in (0, 1)], top, ys)
 
 
 class GpuOps:
@@ -1089,10 +1139,10 @@ class GpuOps:
 
     sum_pairs = 8  # pairs per pcx_mul_sum_relin_rescale_list call
 
-    def mul_sum_list(self, out, groups, top):
-        """out's len(groups) consecutive ciphertexts: product j = the sum of a b over the pairs of groups[j],
-        relinearized and rescaled once"""
-        self.ctx.mul_sum_relin_rescale_list(self.relin, groups, top, out, self.st)
+    def mul_sum_list(self, out, groups, top, adds=None):
+        """out's len(groups) consecutive ciphertexts: product j = the sum of a b over the pairs of groups[j] plus
+        adds[j] (None: nothing), relinearized and rescaled once"""
+        self.ctx.mul_sum_relin_rescale_list(self.relin, groups, top, out, self.st, adds)
 
     # -- ModRaise
     def mod_raise(self, out, x, top):

@@ -100,6 +100,10 @@ struct TensorListArgs {
     int n, K, dbl;
     int sum;
     int off[TLIST_MAX + 1];
+    // product c's addend y[c] (a ciphertext: two parts part apart, rows by prime id; null: none), added to (d0, d1),
+    // subtracted where bit c of ysub is set
+    const uint32_t* y[TLIST_MAX];
+    uint32_t ysub;
 };
 int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s);
 // The plaintext products of K ciphertexts (K consecutive, ct_stride apart; out likewise), ciphertext c by its own

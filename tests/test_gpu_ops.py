@@ -226,7 +226,8 @@ def test_product_sums(stream, name, top, sizes):
     with repeats from four ciphertexts of one buffer), its tensors summed and relinearized and rescaled once: each
     product's words equal the oracle's (the tensor of all its pairs, ModUp of d2, the key dot, the exact ModDown by
     P q_top q_top-1 with (d0, d1) onto it); more than 8 pairs, an empty group and an out slot over an operand are
-    refused before anything is launched."""
+    refused before anything is launched. The same products with addends (one added, one subtracted, one without)
+    equal the oracle's with the addend folded into (d0, d1) before the key switch."""
     say(f"[product sums] {name} top={top} sizes={sizes}")
     from perseus_amd import bootstrap as B
 
@@ -246,6 +247,23 @@ def test_product_sums(stream, name, top, sizes):
     for j, g in enumerate(groups):
         want = oc.mul_sum_relin_rescale([(pool[a], pool[b]) for a, b in g], top, seed, bkey)
         assert (got[j][:, : top - 1] == want[:, : top - 1]).all(), f"product {j} ({g})"
+    # addends: product 0 plus the pool's ciphertext 3, product 1 minus ciphertext 2, the last with none; against the
+    # oracle's addend folded into (d0, d1) before the key switch
+    adds = [3, 2] + [None] * (len(sizes) - 2)
+    out2 = ctxk.ct_buf(len(sizes))
+    ctxk.mul_sum_relin_rescale_list(keysk, [[(view(i), view(j)) for i, j in g] for g in groups], top, out2, stream,
+                                    adds=[None if y is None else view(y) for y in adds], sub=0b10)
+    stream.sync()
+    got2 = out2.download((len(sizes), 2, ch.rows, ch.n))
+    for j, g in enumerate(groups):
+        y = None if adds[j] is None else pool[adds[j]]
+        want = oc.mul_sum_relin_rescale([(pool[a], pool[b]) for a, b in g], top, seed, bkey, y, j == 1)
+        assert (got2[j][:, : top - 1] == want[:, : top - 1]).all(), f"product {j} ({g}) with addend {adds[j]}"
+        if adds[j] is None:
+            assert (got2[j][:, : top - 1] == got[j][:, : top - 1]).all()
+    o1 = ctxk.ct_buf(1)
+    with pytest.raises(pa.HipError):  # an addend over the out slot
+        ctxk.mul_sum_relin_rescale_list(keysk, [[(view(0), view(2))]], top, o1, stream, adds=[o1])
     with pytest.raises(pa.HipError):
         ctxk.mul_sum_relin_rescale_list(keysk, [[(view(0), view(1))] * 5, [(view(2), view(3))] * 4], top,
                                         ctxk.ct_buf(2), stream)

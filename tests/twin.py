@@ -292,9 +292,10 @@ class Ctx:
         d[0, :n], d[1, :n] = c0[0], c1[0]
         return self.moddown_rescale(ext, top, d)
 
-    def mul_sum_relin_rescale(self, pairs, top, seed, bkey):
+    def mul_sum_relin_rescale(self, pairs, top, seed, bkey, add=None, sub=False):
         """The sum of the pairs' tensors (a b over every pair, summed exactly mod each prime), relinearized and
-        rescaled once as mul_relin_rescale does one tensor."""
+        rescaled once as mul_relin_rescale does one tensor; add (a ciphertext, or None) is added to the tensor's
+        (d0, d1) first (subtracted with sub), so it is rescaled with the product."""
         from oracle import em
         n = top + 1
         c0, c1, d2 = em.tensor(self.primes, [(a[None, :, :n], b[None, :, :n]) for a, b in pairs])
@@ -303,6 +304,11 @@ class Ctx:
         ext = self.ks_dot(tmp, self.modup(tmp[1], top), top, seed, bkey, 1)
         d = self.ct_zeros()
         d[0, :n], d[1, :n] = c0[0], c1[0]
+        if add is not None:
+            ps = np.array(self.primes[:n], np.uint64)[:, None]
+            for part in range(2):
+                x, y = d[part, :n].astype(np.uint64), add[part, :n].astype(np.uint64)
+                d[part, :n] = ((x + ps - y) if sub else (x + y)) % ps
         return self.moddown_rescale(ext, top, d)
 
     def rescale(self, x, top, ndrop):

@@ -1041,15 +1041,17 @@ int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, co
                                void* out, int twice, pc_stream_t s);
 /* pcx_mul_relin_rescale_list with each product a sum of pairs: product j = sum of a[i] b[i] over i in off[j] ..
  * off[j + 1] - 1 (off[0] = 0, each range non-empty, off[K] <= 8 pairs in all), relinearized and rescaled once: the
- * words of relinearizing and rescaling the summed tensor (d0, d1, d2). y (NULL, or K pointers, each NULL or a
- * ciphertext at top or above): y[j] is added to product j's (d0, d1) before the key switch (subtracted where bit j of
- * ysub is set), so it is rescaled with the product: a term at the product's scale and top rides along for free.
+ * words of relinearizing and rescaling the summed tensor (d0, d1, d2); twice: the tensor doubled. y (NULL, or K
+ * pointers, each NULL or a ciphertext at top or above): y[j] times its multiplier is added to product j's (d0, d1)
+ * before the key switch (subtracted where bit j of ysub is set), so it is rescaled with the product: a term at the
+ * product's scale and top rides along for free. yk (NULL, or K pointers, each NULL for 1): y[j]'s multiplier, device
+ * rows of the context's row count of words, k mod q by prime id, then their Shoup companions floor(k 2^32 / q).
  * K <= k_max. No out slot may overlap any operand or addend (-1). No counterpart in the reference: a Chebyshev split's
  * product, its remainder's own products and the last remainder, which land on one (top, scale), share one
  * relinearization and one rescale. */
 int pcx_mul_sum_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b,
-                                   const int* off, int K, int top, const void* const* y, unsigned ysub, void* out,
-                                   pc_stream_t s);
+                                   const int* off, int K, int top, const void* const* y, const void* const* yk,
+                                   unsigned ysub, int twice, void* out, pc_stream_t s);
 /* The plaintext product (mult_pt; the table's mul_table): out = ct pt on Q rows 0..top of both parts, pt evaluation-
  * form rows by prime id (rows 0..top read). out may be ct. */
 int pcx_mul_plain(pcx_ctx* c, const void* ct, const void* pt, int top, void* out, pc_stream_t s);

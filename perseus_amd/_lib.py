@@ -110,7 +110,7 @@ _SIGS = {
     "pcx_mul_relin_rescale_k": (C.c_int, [vp, vp, vp, vp, C.c_int, vp, C.c_int, C.c_int, vp]),
     "pcx_mul_relin_rescale_list": (C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(vp), C.c_int, C.c_int, vp, C.c_int, vp]),
     "pcx_mul_sum_relin_rescale_list": (C.c_int, [vp, vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int), C.c_int,
-                                                 C.c_int, C.POINTER(vp), C.c_uint, vp, vp]),
+                                                 C.c_int, C.POINTER(vp), C.POINTER(vp), C.c_uint, C.c_int, vp, vp]),
     "pcx_rotate_many_rescale": (C.c_int, [vp, vp, C.POINTER(C.c_int), C.c_int, C.POINTER(vp), C.c_int, vp, vp, vp]),
     "pcx_mul_plain": (C.c_int, [vp, vp, vp, C.c_int, vp, vp]),
     "pcx_mul_plain_k": (C.c_int, [vp, vp, C.POINTER(vp), C.c_int, C.c_int, vp, vp]),

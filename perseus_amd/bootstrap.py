@@ -258,21 +258,25 @@ class Evaluator:
             out += [Ct(self.ops.item(buf, j), t - 2, a.scale * b.scale / self.qq(t)) for j, (a, b) in enumerate(grp)]
         return out
 
-    def mul_sums(self, groups, adds=None):
-        """[sum of a b over the pairs (a, b) of g, plus adds[j] for g = groups[j]], each sum relinearized and rescaled
-        once (the operations' mul_sum_list): every pair of every group at one top t, the pairs of a group at one
-        product scale, and an addend (None: none) at that scale and at top t or above, so that it is rescaled with
-        the products. Groups go up to ops.kmax per call and up to ops.sum_pairs pairs per call."""
+    def mul_sums(self, groups, adds=None, twice=False):
+        """[sum of a b over the pairs (a, b) of g (doubled with twice), plus adds[j] for g = groups[j]], each sum
+        relinearized and rescaled once (the operations' mul_sum_list): every pair of every group at one top t, the
+        pairs of a group at one product scale, and an addend (None: none; a Ct; or (Ct, k, sub): k times it, subtracted
+        with sub) whose multiple sits at that scale, at top t or above, so that it is rescaled with the products.
+        Groups go up to ops.kmax per call and up to ops.sum_pairs pairs per call."""
         tops = {min(a.top, b.top) for g in groups for a, b in g}
         assert len(tops) == 1, tops
         t = tops.pop()
         adds = [None] * len(groups) if adds is None else adds
         assert len(adds) == len(groups)
+        adds = [None if y is None else y if isinstance(y, tuple) else (y, None, False) for y in adds]
         scales = []
         for g, y in zip(groups, adds):
             s0 = g[0][0].scale * g[0][1].scale
             assert all(abs(a.scale * b.scale / s0 - 1.0) < 1e-9 for a, b in g), [a.scale * b.scale for a, b in g]
-            assert y is None or (y.top >= t and abs(y.scale / s0 - 1.0) < 1e-9), (y.top, y.scale, t, s0)
+            if y is not None:
+                ys = y[0].scale * (1 if y[1] is None else y[1])
+                assert y[0].top >= t and abs(ys / s0 - 1.0) < 1e-9, (y[0].top, ys, t, s0)
             scales.append(s0 / self.qq(t))
         kmax = max(1, getattr(self.ops, "kmax", 1))
         pmax = max(1, getattr(self.ops, "sum_pairs", 8))
@@ -285,8 +289,13 @@ class Evaluator:
             assert j1 > j0, "a group with more pairs than one call takes"
             buf = self.ops.alloc(j1 - j0)
             ys = adds[j0:j1]
-            self.ops.mul_sum_list(buf, [[(a.h, b.h) for a, b in g] for g in groups[j0:j1]], t,
-                                  None if all(y is None for y in ys) else [None if y is None else y.h for y in ys])
+            gh = [[(a.h, b.h) for a, b in g] for g in groups[j0:j1]]
+            if all(y is None for y in ys) and not twice:
+                self.ops.mul_sum_list(buf, gh, t)
+            else:
+                self.ops.mul_sum_list(buf, gh, t, [None if y is None else y[0].h for y in ys],
+                                      sum(1 << j for j, y in enumerate(ys) if y is not None and y[2]),
+                                      [None if y is None else y[1] for y in ys], twice)
             out += [Ct(self.ops.item(buf, j - j0), t - 2, scales[j]) for j in range(j0, j1)]
             j0 = j1
         return out
@@ -415,11 +424,13 @@ class ChebEval:
 
     BABY, GIANTS = 8, (8, 16, 32)
 
-    def __init__(self, ev, fuse=True, fold_ends=True):
+    def __init__(self, ev, fuse=True, fold_ends=True, fold_corr=True):
         self.ev = ev
         self.fuse = fuse  # the chains of remainders in one relinearization each (eval)
         # with fuse: each chain's last leaf added, unrescaled, into the chain's summed product (rescaled with it)
         self.fold_ends = fold_ends
+        # with fuse: the basis's corrections T_{a-b} as integer multiples inside their products' sums (basis)
+        self.fold_corr = fold_corr
 
     # T_k = 2 T_a T_b - T_{a-b}, by rounds of independent products (one batched product per round)
     ROUNDS = (((2, 1, 1),), ((3, 2, 1), (4, 2, 2)), ((5, 3, 2), (6, 3, 3), (7, 4, 3), (8, 4, 4)), ((16, 8, 8),),
@@ -431,6 +442,19 @@ class ChebEval:
         operands' alone): one batched rescale for T_3's, T_5's and T_7's"""
         ev = self.ev
         T, corr = {1: u}, {}
+        if self.fuse and self.fold_corr and hasattr(ev.ops, "mul_sum_list"):
+            # T_k = 2 T_a T_b - T_{a-b}: the correction, times the integer that puts it at the product's scale, is
+            # subtracted inside the doubled product's tensor and rescaled with it
+            for rnd in self.ROUNDS:
+                for t in dict.fromkeys(min(T[a].top, T[b].top) for _, a, b in rnd):
+                    sub_r = [(k, a, b) for k, a, b in rnd if min(T[a].top, T[b].top) == t]
+                    adds = [None if a == b else (T[a - b], int(round(T[a].scale * T[b].scale / T[a - b].scale)), True)
+                            for _, a, b in sub_r]
+                    P = ev.mul_sums([[(T[a], T[b])] for _, a, b in sub_r], adds, twice=True)
+                    for (k, a, b), p in zip(sub_r, P):
+                        T[k] = ev.add_const(p, -1.0) if a == b else p
+            self.T = T
+            return T
         for i, rnd in enumerate(self.ROUNDS):
             P = dict(zip([k for k, _, _ in rnd], ev.mul_many([(T[a], T[b]) for _, a, b in rnd], twice=True)))
             known = {**T, **P}
@@ -866,10 +890,12 @@ class PairOps:
     def sum_pairs(self):
         return max(1, getattr(self.o, "sum_pairs", 8) // 2)
 
-    def mul_sum_list(self, out, groups, top, adds=None):
+    def mul_sum_list(self, out, groups, top, adds=None, sub=0, kmuls=None, twice=False):
         ys = None if adds is None else [None if y is None else self.o.item(y, i) for y in adds for i in (0, 1)]
+        sub2 = sum(3 << 2 * j for j in range(len(groups)) if (sub >> j) & 1)
+        ks = None if kmuls is None else [k for k in kmuls for _ in (0, 1)]
         self.o.mul_sum_list(out, [[(self.o.item(a, i), self.o.item(b, i)) for a, b in g] for g in groups
-                                  for i in (0, 1)], top, ys)
+                                  for i in (0, 1)], top, ys, sub2, ks, twice)
 
 
 class GpuOps:
@@ -1139,10 +1165,21 @@ class GpuOps:
 
     sum_pairs = 8  # pairs per pcx_mul_sum_relin_rescale_list call
 
-    def mul_sum_list(self, out, groups, top, adds=None):
-        """out's len(groups) consecutive ciphertexts: product j = the sum of a b over the pairs of groups[j] plus
-        adds[j] (None: nothing), relinearized and rescaled once"""
-        self.ctx.mul_sum_relin_rescale_list(self.relin, groups, top, out, self.st, adds)
+    def mul_sum_list(self, out, groups, top, adds=None, sub=0, kmuls=None, twice=False):
+        """out's len(groups) consecutive ciphertexts: product j = the sum of a b over the pairs of groups[j] (doubled
+        with twice) plus kmuls[j] adds[j] (None: nothing; a multiplier None: 1; subtracted where bit j of sub is set),
+        relinearized and rescaled once"""
+        kb = None if kmuls is None else [None if k is None else self._krows(int(k)) for k in kmuls]
+        self.ctx.mul_sum_relin_rescale_list(self.relin, groups, top, out, self.st, adds, sub, kb, twice)
+
+    def _krows(self, k):
+        """the integer k as device rows: k mod q by prime id, then their Shoup companions (one buffer, cached)"""
+        key = ("kr", k)
+        if key not in self.cache:
+            r = np.array([k % p for p in self.primes], np.uint32)
+            rs = np.array([(int(v) << 32) // p for v, p in zip(r, self.primes)], np.uint64).astype(np.uint32)
+            self.cache[key] = self.eng.DevBuf.from_array(np.concatenate([r, rs]))
+        return self.cache[key]
 
     # -- ModRaise
     def mod_raise(self, out, x, top):

@@ -2112,8 +2112,8 @@ int pcx_mul_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, co
 }
 
 int pcx_mul_sum_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a, const void* const* b,
-                                   const int* off, int K, int top, const void* const* y, unsigned ysub, void* out,
-                                   pc_stream_t s) {
+                                   const int* off, int K, int top, const void* const* y, const void* const* yk,
+                                   unsigned ysub, int twice, void* out, pc_stream_t s) {
     if (!c || !k || !a || !b || !off || !out || top < 2 || top >= c->nq || k->nkeys < 1 || k->galois[0] != 1) return -1;
     if (K < 1 || K > c->k_max || !serves(k, top) || off[0] != 0) return -1;
     for (int j = 0; j < K; ++j)
@@ -2137,8 +2137,11 @@ int pcx_mul_sum_relin_rescale_list(pcx_ctx* c, pcx_keys* k, const void* const* a
         const uintptr_t yv = (uintptr_t)y[j], o = (uintptr_t)out;
         if (yv < o + K * cwb && o < yv + cwb) return -1;
         t.y[j] = (const uint32_t*)y[j];
+        t.yk[j] = yk ? (const uint32_t*)yk[j] : nullptr;
         t.ysub |= ((ysub >> j) & 1u) << j;
     }
+    t.krows = c->rows;
+    t.dbl = twice ? 1 : 0;
     t.sum = 1;
     for (int j = 0; j <= K; ++j) t.off[j] = off[j];
     t.out = (uint32_t*)out;

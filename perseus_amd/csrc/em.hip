@@ -163,10 +163,13 @@ __global__ void __launch_bounds__(BX) tensor_list_k(TensorListArgs A, int logn) 
         s.mac(ld4(a), ld4(a + A.part), ld4(b), ld4(b + A.part));
     }
     uint32_t* o = A.out + c * A.ct_stride + ro;
-    // the addend's words by a Shoup product with 1 (companion 0): each canonical word unchanged
+    // the addend's words times its row's multiplier (a Shoup product; none: 1 with companion 0, each canonical word
+    // unchanged)
     const uint32_t* y = A.y[c];
+    const uint32_t* yk = A.yk[c];
+    const uint32_t ym = yk ? yk[row] : 1u, yms = yk ? yk[A.krows + row] : 0u;
     tensor_tail(s, red, o, o + A.part, A.d2 + c * A.ct_stride + A.part + ro, false, false, A.dbl != 0,
-                y ? y + ro : nullptr, y ? y + A.part + ro : nullptr, 1u, 0u, (A.ysub >> c) & 1u, nullptr);
+                y ? y + ro : nullptr, y ? y + A.part + ro : nullptr, ym, yms, (A.ysub >> c) & 1u, nullptr);
 }
 
 __global__ void __launch_bounds__(BX) tensor_sum_k(TensorSumArgs A, int logn) {

@@ -104,6 +104,9 @@ struct TensorListArgs {
     // subtracted where bit c of ysub is set
     const uint32_t* y[TLIST_MAX];
     uint32_t ysub;
+    // y[c]'s multiplier (null: 1): krows words k mod q by prime id, then their Shoup companions
+    const uint32_t* yk[TLIST_MAX];
+    int krows;
 };
 int tensor_list(int logn, const TensorListArgs* a, pc_stream_t s);
 // The plaintext products of K ciphertexts (K consecutive, ct_stride apart; out likewise), ciphertext c by its own

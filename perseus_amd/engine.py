@@ -304,10 +304,12 @@ class Context:
         check(LIB.pcx_mul_relin_rescale_list(self.h, keys.h, pa, pb, len(a), top, out.addr(), int(twice), stream.h),
               "mul_relin_rescale_list")
 
-    def mul_sum_relin_rescale_list(self, keys, groups, top, out, stream, adds=None, sub=0):
+    def mul_sum_relin_rescale_list(self, keys, groups, top, out, stream, adds=None, sub=0, kmuls=None, twice=False):
         """out's len(groups) consecutive ciphertexts (top - 2): product j = the sum of a b over the pairs (a, b) of
-        groups[j] plus adds[j] (a ciphertext at top or above at the products' scale, or None; subtracted where bit j
-        of sub is set), relinearized and rescaled once (pcx_mul_sum_relin_rescale_list)."""
+        groups[j] (doubled with twice) plus adds[j] times kmuls[j] (a ciphertext at top or above whose multiple sits
+        at the products' scale, or None; the multiplier a DevBuf of the rows' k mod q then Shoup companions, or None
+        for 1; subtracted where bit j of sub is set), relinearized and rescaled once
+        (pcx_mul_sum_relin_rescale_list)."""
         pairs = [p for g in groups for p in g]
         assert groups and all(groups)
         assert adds is None or len(adds) == len(groups)
@@ -318,8 +320,9 @@ class Context:
         pb = (C.c_void_p * len(pairs))(*[y.addr() for _, y in pairs])
         po = (C.c_int * len(off))(*off)
         py = None if adds is None else (C.c_void_p * len(adds))(*[None if y is None else y.addr() for y in adds])
-        check(LIB.pcx_mul_sum_relin_rescale_list(self.h, keys.h, pa, pb, po, len(groups), top, py, int(sub),
-                                                 out.addr(), stream.h), "mul_sum_relin_rescale_list")
+        pk = None if kmuls is None else (C.c_void_p * len(kmuls))(*[None if k is None else k.addr() for k in kmuls])
+        check(LIB.pcx_mul_sum_relin_rescale_list(self.h, keys.h, pa, pb, po, len(groups), top, py, pk, int(sub),
+                                                 1 if twice else 0, out.addr(), stream.h), "mul_sum_relin_rescale_list")
 
     def cts_stage(self, keys, r0, B, G, pts, npts, ptw, enc, ct, top, res, stream):
         """One CtS / StC stage's baby steps and plaintext products (pcx_cts_stage): res_j = sum_i rot_i(ct) pt_{Bj+i}

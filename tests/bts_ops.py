@@ -148,11 +148,13 @@ class OracleOps:
 
     sum_pairs = 8
 
-    def mul_sum_list(self, out, groups, top, adds=None, sub=0):
+    def mul_sum_list(self, out, groups, top, adds=None, sub=0, kmuls=None, twice=False):
         for j, g in enumerate(groups):
             y = None if adds is None or adds[j] is None else self.get(adds[j])
+            k = None if kmuls is None else kmuls[j]
             self.get(self.item(out, j))[:] = self.oc.mul_sum_relin_rescale(
-                [(self.get(a), self.get(b)) for a, b in g], top, self.relin_seed, self.relin_b, y, (sub >> j) & 1)
+                [(self.get(a), self.get(b)) for a, b in g], top, self.relin_seed, self.relin_b, y, (sub >> j) & 1, k,
+                twice)
 
     def rescale2(self, out, x, top, count=1):
         for i in range(count):

@@ -226,8 +226,9 @@ def test_product_sums(stream, name, top, sizes):
     with repeats from four ciphertexts of one buffer), its tensors summed and relinearized and rescaled once: each
     product's words equal the oracle's (the tensor of all its pairs, ModUp of d2, the key dot, the exact ModDown by
     P q_top q_top-1 with (d0, d1) onto it); more than 8 pairs, an empty group and an out slot over an operand are
-    refused before anything is launched. The same products with addends (one added, one subtracted, one without)
-    equal the oracle's with the addend folded into (d0, d1) before the key switch."""
+    refused before anything is launched. The same products with addends (one added, one subtracted, one without),
+    then doubled with an addend times a multiplier, equal the oracle's with the addend folded into (d0, d1) before
+    the key switch."""
     say(f"[product sums] {name} top={top} sizes={sizes}")
     from perseus_amd import bootstrap as B
 
@@ -261,6 +262,21 @@ def test_product_sums(stream, name, top, sizes):
         assert (got2[j][:, : top - 1] == want[:, : top - 1]).all(), f"product {j} ({g}) with addend {adds[j]}"
         if adds[j] is None:
             assert (got2[j][:, : top - 1] == got[j][:, : top - 1]).all()
+    # doubled tensors, addend 3 times an integer beyond every prime subtracted from product 0, addend 2 plain on 1
+    k0 = (1 << 75) + 12345
+    kr = np.array([k0 % int(p) for p in ch.primes], np.uint64)
+    krows = pa.DevBuf.from_array(np.concatenate([kr, (kr << 32) // np.array(ch.primes, np.uint64)]).astype(np.uint32))
+    out3 = ctxk.ct_buf(len(sizes))
+    ctxk.mul_sum_relin_rescale_list(keysk, [[(view(i), view(j)) for i, j in g] for g in groups], top, out3, stream,
+                                    adds=[None if y is None else view(y) for y in adds], sub=0b01,
+                                    kmuls=[krows] + [None] * (len(sizes) - 1), twice=True)
+    stream.sync()
+    got3 = out3.download((len(sizes), 2, ch.rows, ch.n))
+    for j, g in enumerate(groups):
+        y = None if adds[j] is None else pool[adds[j]]
+        want = oc.mul_sum_relin_rescale([(pool[a], pool[b]) for a, b in g], top, seed, bkey, y, j == 0,
+                                        k0 if j == 0 else None, True)
+        assert (got3[j][:, : top - 1] == want[:, : top - 1]).all(), f"doubled product {j} ({g}), addend {adds[j]}"
     o1 = ctxk.ct_buf(1)
     with pytest.raises(pa.HipError):  # an addend over the out slot
         ctxk.mul_sum_relin_rescale_list(keysk, [[(view(0), view(2))]], top, o1, stream, adds=[o1])

@@ -292,12 +292,16 @@ class Ctx:
         d[0, :n], d[1, :n] = c0[0], c1[0]
         return self.moddown_rescale(ext, top, d)
 
-    def mul_sum_relin_rescale(self, pairs, top, seed, bkey, add=None, sub=False):
-        """The sum of the pairs' tensors (a b over every pair, summed exactly mod each prime), relinearized and
-        rescaled once as mul_relin_rescale does one tensor; add (a ciphertext, or None) is added to the tensor's
-        (d0, d1) first (subtracted with sub), so it is rescaled with the product."""
+    def mul_sum_relin_rescale(self, pairs, top, seed, bkey, add=None, sub=False, kmul=None, twice=False):
+        """The sum of the pairs' tensors (a b over every pair, summed exactly mod each prime; twice: 2a b),
+        relinearized and rescaled once as mul_relin_rescale does one tensor; add (a ciphertext, or None) times the
+        integer kmul (None: 1) is added to the tensor's (d0, d1) first (subtracted with sub), so it is rescaled with
+        the product."""
         from oracle import em
         n = top + 1
+        ps = np.array(self.primes[:n], np.uint64)[:, None]
+        if twice:
+            pairs = [(((a[:, :n].astype(np.uint64) * 2) % ps).astype(np.uint32), b) for a, b in pairs]
         c0, c1, d2 = em.tensor(self.primes, [(a[None, :, :n], b[None, :, :n]) for a, b in pairs])
         tmp = self.ct_zeros()
         tmp[1, :n] = d2[0]
@@ -305,9 +309,9 @@ class Ctx:
         d = self.ct_zeros()
         d[0, :n], d[1, :n] = c0[0], c1[0]
         if add is not None:
-            ps = np.array(self.primes[:n], np.uint64)[:, None]
+            km = np.array([1 if kmul is None else int(kmul) % int(p) for p in self.primes[:n]], np.uint64)[:, None]
             for part in range(2):
-                x, y = d[part, :n].astype(np.uint64), add[part, :n].astype(np.uint64)
+                x, y = d[part, :n].astype(np.uint64), add[part, :n].astype(np.uint64) * km % ps
                 d[part, :n] = ((x + ps - y) if sub else (x + y)) % ps
         return self.moddown_rescale(ext, top, d)
 
